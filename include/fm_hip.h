@@ -1,0 +1,212 @@
+/* fm_hip.h -- C ABI of libfm_hip.so, the MI355X (gfx950) kernels behind the
+ * fp8_flow_moe operator path.
+ *
+ * The reference exposes this path only as Python names re-exported by
+ * nanopsyche (reference fp8/__init__.py:8-24, fp8/flow_moe.py:3-15,
+ * fp8/recipes.py:3-7) from the absent `fp8_flow_moe` package, and as the
+ * object call made by MoEBase (reference model/moe.py:1313-1332 construct,
+ * :1516-1517 and :1557-1558 call).  Each entry point below names the
+ * reference function or op sequence it replaces.
+ *
+ * Conventions
+ *   - Plain device pointers, element counts and pitches (in elements), and a
+ *     hipStream_t passed as void*.  No allocation, no host synchronisation:
+ *     every call only enqueues work on `stream`.
+ *   - Return 0 on success; nonzero on a rejected argument or launch failure,
+ *     with the message available from fm_last_error_string() (thread-local).
+ *   - bf16 is passed as raw 16-bit words, e4m3 (OCP e4m3fn) and e8m0 as bytes.
+ *   - Block-scale spec: scale = max(amax, 1e-12) / 448 in fp32 (power-of-two
+ *     kinds round it up to 2^ceil(log2)); q = e4m3(clamp(x / scale, +-448)).
+ *     MX: code = clamp(exponent(amax) - 8, 0, 254), q = sat_e4m3(x * 2^(127-code)).
+ */
+#ifndef FM_HIP_H_
+#define FM_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define FM_DTYPE_BF16 0
+#define FM_DTYPE_F32 1
+
+/* quantisation kinds (payload + scale format) */
+#define FM_QUANT_BF16 0   /* no quantisation: bf16 payload, no scales          */
+#define FM_QUANT_BLOCK 1  /* e4m3, fp32 scale per 128 block                     */
+#define FM_QUANT_POW2 2   /* e4m3, power-of-two fp32 scale per 128 block        */
+#define FM_QUANT_MX 3     /* e4m3, e8m0 scale per 32 block (OCP MXFP8)          */
+
+/* grouped GEMM arithmetic kinds */
+#define FM_GEMM_BF16 0
+#define FM_GEMM_FP8_F32 1  /* fp32 block scales, promoted per 128-deep K block */
+#define FM_GEMM_FP8_POW2 2 /* power-of-two scales through the scaled MFMA      */
+#define FM_GEMM_FP8_MX 3   /* e8m0 per-32 scales through the scaled MFMA       */
+
+/* gating functions (reference model/moe.py:44-46 GatingFunction) */
+#define FM_GATING_SOFTMAX 0
+#define FM_GATING_SIGMOID 1
+
+/* ------------------------------------------------------------ library ---- */
+const char* fm_last_error_string(void);
+const char* fm_version(void);
+/* Host-side codec (no GPU): the same f32 -> e4m3 routine the kernels use,
+ * exported so tests can check it against other implementations. */
+void fm_host_encode_e4m3(const float* in, uint8_t* out, int64_t n);
+void fm_host_decode_e4m3(const uint8_t* in, float* out, int64_t n);
+
+/* ------------------------------------------------------- quantisation ---- */
+/* Replaces fp8_flow_moe.quantize_to_fp8 for activations (1x128 / MX 1x32 row
+ * blocks), fused with the 128x1 / 32x1 column-block quantisation of the
+ * transpose when qt != NULL (reference fp8/__init__.py:14; "no double
+ * quantisation", train/README.md:99-100).  x [rows, cols] bf16 or fp32.
+ * Row output q [rows, cols] + s [rows, cols/128] fp32 (or [rows, cols/32] e8m0);
+ * transposed output qt [cols, rows] + st [rows/128, cols] (or [rows/32, cols]).
+ * kind FM_QUANT_POW2: the transposed output is the scaling-aware transpose
+ * of the row output.  FM_QUANT_BF16: plain bf16 copy / transpose. */
+int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int kind,
+                void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st,
+                int64_t ld_st, void* stream);
+
+/* Replaces quantize_to_fp8 for expert weights (128x128 blocks), batched over
+ * `groups` matrices [rows, cols] of w (pitch ld_w, group stride gs_w), writing
+ * into row offset q_row_off of q (and column offset qt_col_off of the
+ * transposed payload qt, same blocks), so w1 and w3 can be packed into one
+ * [E, 2H, D] operand.  kind: FM_QUANT_BF16 / BLOCK / POW2. */
+int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows, int64_t cols,
+                       int64_t ld_w, int64_t gs_w, int kind, void* q, int64_t ld_q, int64_t gs_q,
+                       int64_t q_row_off, float* s, int64_t ld_s, int64_t gs_s, void* qt,
+                       int64_t ld_qt, int64_t gs_qt, int64_t qt_col_off, float* st, int64_t ld_st,
+                       int64_t gs_st, void* stream);
+
+/* Replaces fp8_flow_moe.dequantize_from_fp8 (reference fp8/__init__.py:15).
+ * out[r][c] = decode(q[r][c]) * S, S = s[(r >> row_shift) * s_row_stride +
+ * (c >> col_shift) * s_col_stride] (fp32, or e8m0 when s_e8m0). */
+int fm_dequantize(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const void* s,
+                  int s_e8m0, int row_shift, int col_shift, int64_t s_row_stride,
+                  int64_t s_col_stride, void* out, int out_dtype, int64_t ld_out, void* stream);
+
+/* Replaces fp8_flow_moe.scaling_aware_transpose (reference fp8/__init__.py:16):
+ * row-quantised q [rows, cols] + s [rows, cols/128] -> column-quantised
+ * transpose qt [cols, rows] + st [rows/128, cols] without the bf16 source.
+ * st = largest row scale in the 128x128 tile; exact for power-of-two scales
+ * outside the e4m3 subnormal range. */
+int fm_scaling_aware_transpose(const void* q, int64_t rows, int64_t cols, int64_t ld_q,
+                               const float* s, int64_t ld_s, void* qt, int64_t ld_qt, float* st,
+                               int64_t ld_st, void* stream);
+
+/* ------------------------------------------------------------ routing ---- */
+/* Replaces MoERouter._softmax_gating / _sigmoid_gating (reference
+ * model/moe.py:249-265): per token, top-K of the logits (softmax, weights =
+ * softmax over the K selected logits) or of sigmoid(logits) (weights / (sum +
+ * 1e-8)); ties go to the lower expert index.  E <= 256, K <= min(E, 64).
+ * If prob_partial != NULL it receives [n_waves, E] per-wave sums of the full
+ * softmax for fm_aux_loss.  n_waves: positive multiple of 4 (grid size). */
+int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating,
+                   float* weights, void* indices, int indices_i64, float* prob_partial,
+                   int64_t n_waves, void* stream);
+
+/* Replaces MoERouter._load_balancing_loss (reference model/moe.py:267-281):
+ * loss[0] = E * sum_e (counts[e] / T) * (sum_w prob_partial[w][e] / T). */
+int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
+                float* loss, void* stream);
+
+/* Sizes for fm_route_sort: padded-buffer row bound, and workspace bytes. */
+int64_t fm_route_rows_max(int64_t assignments, int E);
+int64_t fm_route_workspace_bytes(int64_t assignments, int E);
+
+/* Replaces the per-expert `(indices == e).any(-1).nonzero()` token lists of
+ * MoEBase._compute_experts_padded_bmm (reference model/moe.py:1565-1567) and
+ * the routing half of fp8_flow_moe.fused_permute_pad (fp8/__init__.py:19):
+ * stable counting sort of the T*K assignments a = t*K + k by expert.
+ * counts [E], offsets [E+1] (padded to multiples of 128), row_of [T*K]
+ * (-1 for indices outside [0, E), which the reference loop also ignores),
+ * assign_of_row [rows_max] (-1 on pad rows), tile_expert [rows_max/128]
+ * (-1 past the last group), use_fp8 [E] (counts[e] >= threshold; may be NULL). */
+int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
+                  int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
+                  int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
+                  int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces fp8_flow_moe.fused_permute_pad (reference fp8/__init__.py:19) and
+ * the gather + pad of model/moe.py:1571,1577-1580: row r of the padded buffer
+ * is x[assign_of_row[r] / K] (times weights[assign_of_row[r]] if weights !=
+ * NULL), zeros on pad rows, written as `kind` with optional transposed output
+ * (same layout rules as fm_quantize). */
+int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,
+               int64_t rows, int K, const float* weights, int kind, void* q, int64_t ld_q, void* s,
+               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream);
+
+/* Replaces fp8_flow_moe.fused_unpermute_unpad (reference fp8/__init__.py:20)
+ * and the weighted scatter-add of model/moe.py:1594:
+ * out[t] = sum_k weights[t*K+k] * y[row_of[t*K+k]] (weights NULL -> 1),
+ * fp32 sum in slot order, one rounding to out_dtype. */
+int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
+                 int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
+                 void* stream);
+
+/* Gradient of the combine with respect to the router weights (autograd of
+ * model/moe.py:1594 in the reference): dw[a] = <dout[a/K], y[row_of[a]]>. */
+int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_t ld_y,
+                          const int32_t* row_of, int64_t T, int K, int64_t D, float* dw,
+                          void* stream);
+
+/* ------------------------------------------------------------- SwiGLU ---- */
+/* Replaces fp8_flow_moe.fused_swiglu_quantize / fused_silu_multiply_quantize
+ * (reference fp8/__init__.py:17-18; math of model/moe.py:1590, 1181-1183):
+ * h = silu(g) * u from bf16 g, u, emitted as `kind` (fm_quantize layouts). */
+int fm_swiglu_quantize(const void* g, int64_t ld_g, const void* u, int64_t ld_u, int64_t rows,
+                       int64_t H, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt,
+                       int64_t ld_qt, void* st, int64_t ld_st, void* stream);
+
+/* Backward of SwiGLU (autograd of model/moe.py:1590 in the reference):
+ * [dg | du] with dg = dh*u*s*(1+g*(1-s)), du = dh*g*s, s = sigmoid(g), as a
+ * [rows, 2H] operand emitted as `kind`. */
+int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u, const void* dh,
+                       int64_t ld_dh, int64_t rows, int64_t H, int kind, void* q, int64_t ld_q,
+                       void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
+                       void* stream);
+
+/* ------------------------------------------------------- grouped GEMM ---- */
+/* One operand of the grouped GEMM: K-contiguous rows.  Scale of (row, kb) is
+ * scale[g*scale_group_stride + (row >> scale_row_shift)*scale_row_stride +
+ * kb*scale_kb_stride], kb counting 128-blocks (fp32 / pow2) or 32-blocks (MX). */
+typedef struct FmGemmOperand {
+  const void* data;
+  int64_t ld;            /* row pitch, elements */
+  int64_t group_stride;  /* elements between experts (weights), else 0 */
+  const void* scale;     /* fp32, or e8m0 bytes for FM_GEMM_FP8_MX; NULL for bf16 */
+  int64_t scale_row_stride;
+  int64_t scale_kb_stride;
+  int64_t scale_group_stride;
+  int scale_row_shift;   /* 7 for 128x128 weight blocks, 0 otherwise */
+} FmGemmOperand;
+
+/* Replaces fp8_flow_moe.fp8_grouped_gemm (reference fp8/__init__.py:21) and
+ * the per-expert torch.bmm calls of model/moe.py:1588-1591 (forward and
+ * dgrad): out[r][n] = sum_k tokens[r][k] * weights_e[n][k] for every 128-row
+ * tile r of the padded buffer, e = tile_expert[r/128] (tiles with e < 0, or
+ * expert_mask[e] != mask_want when expert_mask != NULL, are skipped -- the
+ * fp8_gemm_threshold switch of model/moe.py:1215-1216).  N, K multiples of 128. */
+int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
+                             int64_t m_tiles, const int32_t* tile_expert, int E, int64_t N,
+                             int64_t K, const int32_t* expert_mask, int mask_want, void* out,
+                             int out_dtype, int64_t ld_out, void* stream);
+
+/* Weight-gradient grouped GEMM (autograd of model/moe.py:1588-1591 with
+ * respect to w1/w2/w3): out_e[m][n] = sum over the tokens t of expert e
+ * (columns offsets[e]..offsets[e+1] of a_t and b_t) of a_t[m][t] * b_t[n][t].
+ * Rows m >= split_rows go to out2 (row m - split_rows), so dW1|dW3 land in two
+ * tensors.  Experts with no tokens get zeros. */
+int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                             const int32_t* offsets, int E, int64_t M, int64_t N,
+                             const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
+                             void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
+                             int64_t ld_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FM_HIP_H_ */

@@ -1,0 +1,132 @@
+"""ctypes binding of libfm_hip.so (declared in include/fm_hip.h).
+
+The library is built in-tree by ``nanopysche_amd.build``.  There is no CPU
+fallback anywhere in the package: if the library is missing, or no ROCm
+device is present when a kernel is requested, the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libfm_hip.so"
+
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+QUANT_BF16 = 0
+QUANT_BLOCK = 1
+QUANT_POW2 = 2
+QUANT_MX = 3
+
+GEMM_BF16 = 0
+GEMM_FP8_F32 = 1
+GEMM_FP8_POW2 = 2
+GEMM_FP8_MX = 3
+
+GATING_SOFTMAX = 0
+GATING_SIGMOID = 1
+
+
+class FmGemmOperand(C.Structure):
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("ld", C.c_int64),
+        ("group_stride", C.c_int64),
+        ("scale", C.c_void_p),
+        ("scale_row_stride", C.c_int64),
+        ("scale_kb_stride", C.c_int64),
+        ("scale_group_stride", C.c_int64),
+        ("scale_row_shift", C.c_int),
+    ]
+
+
+_vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int
+_OPND = C.POINTER(FmGemmOperand)
+
+# name -> (restype, argtypes); must match include/fm_hip.h
+SIGNATURES = {
+    "fm_last_error_string": (C.c_char_p, []),
+    "fm_version": (C.c_char_p, []),
+    "fm_host_encode_e4m3": (None, [_vp, _vp, _i64]),
+    "fm_host_decode_e4m3": (None, [_vp, _vp, _i64]),
+    "fm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,
+                           _vp, _i64, _vp]),
+    "fm_quantize_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _i64,
+                                  _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                                  _vp]),
+    "fm_dequantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _i64, _i64, _vp, _i32,
+                             _i64, _vp]),
+    "fm_scaling_aware_transpose": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
+                                          _vp]),
+    "fm_topk_gating": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp, _i64, _vp]),
+    "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "fm_route_rows_max": (_i64, [_i64, _i32]),
+    "fm_route_workspace_bytes": (_i64, [_i64, _i32]),
+    "fm_route_sort": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                             _vp, _i64, _vp]),
+    "fm_permute": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _vp, _i64, _vp, _i64,
+                          _vp, _i64, _vp, _i64, _vp]),
+    "fm_unpermute": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i32, _i64, _vp]),
+    "fm_router_weight_grad": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _vp, _vp]),
+    "fm_swiglu_quantize": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp,
+                                  _i64, _vp, _i64, _vp]),
+    "fm_swiglu_backward": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp,
+                                  _i64, _vp, _i64, _vp, _i64, _vp]),
+    "fm_grouped_gemm_ragged_m": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _i32, _i64, _i64, _vp, _i32,
+                                        _vp, _i32, _i64, _vp]),
+    "fm_grouped_gemm_ragged_k": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,
+                                        _i64, _vp, _i64, _i64, _i32, _i64, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> C.CDLL:
+    """Load libfm_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m nanopysche_amd.build` "
+                    "(there is no CPU fallback)")
+            lib = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = load().fm_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"libfm_hip {what} failed (code {rc}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)
+
+
+def require_device(t: torch.Tensor, name: str = "tensor") -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{name} must be on a ROCm device: the fp8_flow_moe kernels run only on the GPU "
+            "(there is no CPU fallback)")
+
+
+def stream_of(t: torch.Tensor) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t) -> C.c_void_p:
+    return C.c_void_p(0 if t is None else t.data_ptr())

@@ -1,0 +1,124 @@
+// Device helpers shared by the fp8_flow_moe HIP kernels (gfx950 / CDNA4).
+//
+// Number formats:
+//   bf16   -- stored as uint16_t; widened by a 16-bit shift, narrowed with
+//             round-to-nearest-even.
+//   e4m3   -- OCP e4m3fn (bias 7, max 448, 0x7F/0xFF NaN, no infinities).
+//             f32 -> e4m3 is an integer round-to-nearest-even routine; it is
+//             __host__ __device__ so the host test build can check it against
+//             torch's cast exhaustively.
+//   e8m0   -- OCP MX shared exponent, value 2^(code-127).
+//
+// Block-scale spec (blockwise recipes):
+//   amax  = max |x| over the block (fp32)
+//   scale = max(amax, 1e-12f) / 448.0f             (IEEE fp32 division)
+//   pow2 recipe: scale = 2^ceil(log2(scale))       (exponent-field round up)
+//   q     = e4m3(clamp(x / scale, -448, 448))
+// MX spec (1x32): code = clamp(biased_exp(amax) - 8, 0, 254),
+//   q = e4m3_saturate(x * 2^(127-code)).
+#pragma once
+
+#include <stdint.h>
+#include <hip/hip_runtime.h>
+
+#define FM_HD __host__ __device__ __forceinline__
+
+namespace fm {
+
+constexpr float kE4M3Max = 448.0f;
+constexpr float kAmaxFloor = 1e-12f;
+constexpr int kBlock = 128;
+constexpr int kMxBlock = 32;
+
+FM_HD uint32_t f2u(float f) { union { float f; uint32_t u; } v; v.f = f; return v.u; }
+FM_HD float u2f(uint32_t u) { union { float f; uint32_t u; } v; v.u = u; return v.f; }
+
+FM_HD float bf16_to_f32(uint16_t b) { return u2f(uint32_t(b) << 16); }
+
+FM_HD uint16_t f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// f32 -> e4m3fn, round-to-nearest-even, non-saturating (|x| > 464 -> NaN).
+// Callers clamp to +-448 first, so the NaN branch only sees NaN inputs.
+FM_HD uint8_t f32_to_e4m3(float x) {
+  uint32_t u = f2u(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x43e80000u) return uint8_t(sign | 0x7fu);   // > 464 or NaN / inf
+  if (a < 0x3c800000u) {                               // < 2^-6: e4m3 subnormal
+    // value = m * 2^-9, m = RNE(|x| * 2^9) in [0, 8]; 8 is the smallest normal
+    float s = u2f(a) * 512.0f;                         // exact (power of two)
+    uint32_t m = uint32_t(s);                          // truncate
+    float frac = s - float(m);
+    if (frac > 0.5f || (frac == 0.5f && (m & 1u))) m += 1u;
+    return uint8_t(sign | m);
+  }
+  // normal: keep 3 mantissa bits, round the dropped 20 bits to nearest-even;
+  // a carry out of the mantissa bumps the exponent, which is the right answer.
+  uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  uint32_t code = (r >> 20) - (120u << 3);             // rebias 127 -> 7
+  if (code > 0x7eu) code = 0x7eu;                      // 448 < x <= 464 -> 448
+  return uint8_t(sign | code);
+}
+
+FM_HD float e4m3_to_f32(uint8_t c) {
+  uint32_t sign = uint32_t(c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+  if ((c & 0x7fu) == 0x7fu) return u2f(sign | 0x7fc00000u);
+  if (e == 0) return u2f(sign | f2u(float(m) * 0.001953125f));  // m * 2^-9
+  return u2f(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+FM_HD float clamp448(float v) { return fminf(fmaxf(v, -kE4M3Max), kE4M3Max); }
+
+// Blockwise scale from the block's amax.
+FM_HD float block_scale(float amax, bool pow2) {
+  float s = fmaxf(amax, kAmaxFloor) / kE4M3Max;
+  if (pow2) {
+    uint32_t u = f2u(s);
+    uint32_t e = (u >> 23) & 0xffu;
+    if (u & 0x7fffffu) e += 1u;
+    s = u2f(e << 23);
+  }
+  return s;
+}
+
+FM_HD uint8_t quant_e4m3(float x, float scale) { return f32_to_e4m3(clamp448(x / scale)); }
+
+// MX shared-exponent code of a block with this amax.
+FM_HD uint32_t mx_code(float amax) {
+  int e = int((f2u(amax) >> 23) & 0xffu) - 8;
+  e = e < 0 ? 0 : (e > 254 ? 254 : e);
+  return uint32_t(e);
+}
+// 2^(127 - code) as a float (code in [0, 254] -> exponent field 254 - code).
+FM_HD float mx_inv_scale(uint32_t code) {
+  uint32_t f = 254u - code;
+  return f == 0u ? u2f(0x00400000u) : u2f(f << 23);
+}
+FM_HD float e8m0_to_f32(uint32_t code) {
+  return code == 0u ? u2f(0x00400000u) : u2f(code << 23);
+}
+FM_HD uint8_t quant_mx(float x, float inv_scale) { return f32_to_e4m3(clamp448(x * inv_scale)); }
+
+}  // namespace fm
+
+// ----------------------------------------------------------- error plumbing ----
+// Every C-ABI entry point returns 0 on success or a nonzero code; the message
+// of the last failure on the calling thread is kept for fm_last_error_string.
+namespace fm {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace fm
+
+#define FM_REQUIRE(cond, ...)            \
+  do {                                   \
+    if (!(cond)) {                       \
+      fm::set_error(__VA_ARGS__);        \
+      return 1;                          \
+    }                                    \
+  } while (0)

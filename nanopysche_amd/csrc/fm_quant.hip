@@ -1,0 +1,345 @@
+// Blockwise e4m3 quantisation kernels and their C-ABI entry points:
+//   fm_quantize            -- 1x128 / 1x32 row blocks, optional fused 128x1 /
+//                             32x1 transposed output (one read of the source)
+//   fm_quantize_weight     -- 128x128 blocks, batched over expert groups, with
+//                             optional transposed payload (same blocks)
+//   fm_dequantize          -- any block layout -> bf16 / fp32
+//   fm_scaling_aware_transpose -- row-quantised e4m3 -> column-quantised e4m3
+//                             of the transpose, without the bf16 source
+#include "fm_tile.h"
+#include "../../include/fm_hip.h"
+
+namespace fm {
+
+// ------------------------------------------------------------------ sources ----
+template <typename T>
+struct DenseSrc {
+  const T* p;
+  int64_t ld;
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const;
+};
+
+template <>
+__device__ __forceinline__ void DenseSrc<uint16_t>::load8(int64_t row, int64_t col, float v[8]) const {
+  const uint4 pk = *reinterpret_cast<const uint4*>(p + row * ld + col);
+  const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = u2f(w[i] << 16);
+    v[2 * i + 1] = u2f(w[i] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col, float v[8]) const {
+  const float4 a = *reinterpret_cast<const float4*>(p + row * ld + col);
+  const float4 b = *reinterpret_cast<const float4*>(p + row * ld + col + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// ------------------------------------------------------- 128x128 weight blocks ----
+struct WeightQuantArgs {
+  const void* w;       // [G][R][C] source, pitch ld_w, group stride gs_w (elements)
+  int src_f32;
+  int64_t ld_w, gs_w;
+  int kind;            // QK_BF16 / QK_BLOCK / QK_POW2
+  uint8_t* q;          // [G][.][C] e4m3 (or bf16 if kind == QK_BF16), rows offset q_row_off
+  int64_t ld_q, gs_q, q_row_off;
+  float* s;            // [G][./128][C/128]
+  int64_t ld_s, gs_s;
+  uint8_t* qt;         // [G][C][.] transposed payload, columns offset qt_col_off
+  int64_t ld_qt, gs_qt, qt_col_off;
+  float* st;           // [G][C/128][./128]
+  int64_t ld_st, gs_st;
+};
+
+// grid (C/128, R/128, G); 256 threads.  Thread t loads rows rr + 16*i
+// (rr = t/16, i < 8), columns [8*(t%16), +8) of the tile; the whole tile
+// shares one scale.  The transposed payload is staged through LDS so each
+// thread writes whole 16-byte pieces of a transposed row.
+template <typename T>
+__global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
+  __shared__ float red[256];
+  __shared__ uint32_t tile[128][65];  // [row][col/2] (bf16 pairs) or [row][col/4] (e4m3 quads)
+  const int tid = threadIdx.x;
+  const int64_t g = blockIdx.z;
+  const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
+  const int cc = (tid & 15) * 8;
+  const int rr = tid >> 4;
+  const DenseSrc<T> src{static_cast<const T*>(a.w) + g * a.gs_w, a.ld_w};
+  float v[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) src.load8(r0 + rr + 16 * i, c0 + cc, v[i]);
+  float am = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(v[i][j]));
+  const int c = tid & 127, h = tid >> 7;  // transposed-store role
+  if (a.kind == QK_BF16) {
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(a.q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = rr + 16 * i;
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = uint32_t(f32_to_bf16(v[i][2 * j])) | (uint32_t(f32_to_bf16(v[i][2 * j + 1])) << 16);
+      if (q16)
+        *reinterpret_cast<uint4*>(q16 + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tile[row][(cc >> 1) + j] = w[j];
+    }
+    if (!a.qt) return;
+    __syncthreads();
+    uint16_t* dst = reinterpret_cast<uint16_t*>(a.qt) + g * a.gs_qt + (c0 + c) * a.ld_qt +
+                    a.qt_col_off + r0 + 64 * h;
+    for (int r8 = 0; r8 < 64; r8 += 8) {
+      uint32_t w4[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int row = 64 * h + r8 + 2 * k;
+        const uint32_t lo = (tile[row][c >> 1] >> (16 * (c & 1))) & 0xffffu;
+        const uint32_t hi = (tile[row + 1][c >> 1] >> (16 * (c & 1))) & 0xffffu;
+        w4[k] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + r8) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+    return;
+  }
+  red[tid] = am;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float s = block_scale(red[0], a.kind == QK_POW2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = rr + 16 * i;
+    uint8_t qb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qb[j] = quant_e4m3(v[i][j], s);
+    if (a.q)
+      *reinterpret_cast<uint64_t*>(a.q + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
+          pack8_e4m3(qb);
+    tile[row][(cc >> 2)] = uint32_t(qb[0]) | (uint32_t(qb[1]) << 8) | (uint32_t(qb[2]) << 16) |
+                           (uint32_t(qb[3]) << 24);
+    tile[row][(cc >> 2) + 1] = uint32_t(qb[4]) | (uint32_t(qb[5]) << 8) |
+                               (uint32_t(qb[6]) << 16) | (uint32_t(qb[7]) << 24);
+  }
+  if (a.q && tid == 0) a.s[g * a.gs_s + ((r0 + a.q_row_off) >> 7) * a.ld_s + (c0 >> 7)] = s;
+  if (!a.qt) return;
+  __syncthreads();
+  uint8_t* dst = a.qt + g * a.gs_qt + (c0 + c) * a.ld_qt + a.qt_col_off + r0 + 64 * h;
+  for (int r16 = 0; r16 < 64; r16 += 16) {
+    uint32_t w4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int row = 64 * h + r16 + 4 * k + b;
+        word |= ((tile[row][c >> 2] >> (8 * (c & 3))) & 0xffu) << (8 * b);
+      }
+      w4[k] = word;
+    }
+    *reinterpret_cast<uint4*>(dst + r16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
+  if (tid == 0) a.st[g * a.gs_st + (c0 >> 7) * a.ld_st + ((r0 + a.qt_col_off) >> 7)] = s;
+}
+
+// ------------------------------------------------------------- dequantise ----
+struct DequantArgs {
+  const uint8_t* q;
+  int64_t rows, cols, ld_q;
+  const void* s;        // fp32 or e8m0
+  int s_e8m0;
+  int row_shift, col_shift;
+  int64_t s_row_stride, s_col_stride;
+  void* out;            // bf16 or fp32
+  int out_f32;
+  int64_t ld_out;
+};
+
+__global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
+  const int64_t chunks_per_row = a.cols / 8;
+  const int64_t n = a.rows * chunks_per_row;
+  for (int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x; idx < n;
+       idx += int64_t(gridDim.x) * 256) {
+    const int64_t r = idx / chunks_per_row;
+    const int64_t c = (idx % chunks_per_row) * 8;
+    const uint64_t pk = *reinterpret_cast<const uint64_t*>(a.q + r * a.ld_q + c);
+    const int64_t si = (r >> a.row_shift) * a.s_row_stride + (c >> a.col_shift) * a.s_col_stride;
+    const float sc = a.s_e8m0 ? e8m0_to_f32(static_cast<const uint8_t*>(a.s)[si])
+                              : static_cast<const float*>(a.s)[si];
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32(uint8_t(pk >> (8 * i))) * sc;
+    if (a.out_f32) {
+      float* o = static_cast<float*>(a.out) + r * a.ld_out + c;
+      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      uint16_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = f32_to_bf16(v[i]);
+      uint4 w;
+      w.x = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
+      w.y = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
+      w.z = uint32_t(b[4]) | (uint32_t(b[5]) << 16);
+      w.w = uint32_t(b[6]) | (uint32_t(b[7]) << 16);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + r * a.ld_out + c) = w;
+    }
+  }
+}
+
+// --------------------------------------------------- scaling-aware transpose ----
+// grid (C/128, R/128).  Column-block scale = largest row scale of the tile;
+// qt[c][r] = e4m3(clamp(fp32(decode(q[r][c]) * s[r][c/128]) / st)).
+__global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q, const float* s,
+                                                  int64_t ld_s, uint8_t* qt, int64_t ld_qt,
+                                                  float* st, int64_t ld_st) {
+  __shared__ uint32_t tile[128][33];
+  __shared__ float rs[128];
+  __shared__ float smax;
+  const int tid = threadIdx.x;
+  const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
+  // load 128x128 bytes: thread -> 16 bytes x 4 rows
+  const int cc = (tid & 7) * 16;
+  const int rr = tid >> 3;  // rows rr + 32*i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = rr + 32 * i;
+    const uint4 pk = *reinterpret_cast<const uint4*>(q + (r0 + row) * ld_q + c0 + cc);
+    tile[row][(cc >> 2) + 0] = pk.x;
+    tile[row][(cc >> 2) + 1] = pk.y;
+    tile[row][(cc >> 2) + 2] = pk.z;
+    tile[row][(cc >> 2) + 3] = pk.w;
+  }
+  if (tid < 128) rs[tid] = s[(r0 + tid) * ld_s + (c0 >> 7)];
+  __syncthreads();
+  if (tid < 64) {
+    float m = fmaxf(rs[tid], rs[tid + 64]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (tid == 0) smax = m;
+  }
+  __syncthreads();
+  const float sc = smax;
+  const int c = tid & 127, h = tid >> 7;
+  uint8_t* dst = qt + (c0 + c) * ld_qt + r0 + 64 * h;
+  for (int r16 = 0; r16 < 64; r16 += 16) {
+    uint32_t w4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int row = 64 * h + r16 + 4 * k + b;
+        const uint8_t code = uint8_t((tile[row][c >> 2] >> (8 * (c & 3))) & 0xffu);
+        const float v = e4m3_to_f32(code) * rs[row];
+        word |= uint32_t(quant_e4m3(v, sc)) << (8 * b);
+      }
+      w4[k] = word;
+    }
+    *reinterpret_cast<uint4*>(dst + r16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
+  if (tid < 128) st[(r0 >> 7) * ld_st + c0 + tid] = sc;
+}
+
+}  // namespace fm
+
+using namespace fm;
+
+extern "C" {
+
+int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int kind,
+                void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st,
+                int64_t ld_st, void* stream) {
+  FM_REQUIRE(x != nullptr, "fm_quantize: null input");
+  FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_quantize: bad input dtype %d",
+             x_dtype);
+  FM_REQUIRE(ld_x >= cols && ld_x % 8 == 0, "fm_quantize: input pitch must be >= cols and a multiple of 8");
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  if (x_dtype == FM_DTYPE_BF16)
+    return launch_tile_producer(DenseSrc<uint16_t>{static_cast<const uint16_t*>(x), ld_x}, o, rows,
+                                cols, sm, "fm_quantize");
+  return launch_tile_producer(DenseSrc<float>{static_cast<const float*>(x), ld_x}, o, rows, cols,
+                              sm, "fm_quantize");
+}
+
+int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows, int64_t cols,
+                       int64_t ld_w, int64_t gs_w, int kind, void* q, int64_t ld_q, int64_t gs_q,
+                       int64_t q_row_off, float* s, int64_t ld_s, int64_t gs_s, void* qt,
+                       int64_t ld_qt, int64_t gs_qt, int64_t qt_col_off, float* st, int64_t ld_st,
+                       int64_t gs_st, void* stream) {
+  FM_REQUIRE(w != nullptr, "fm_quantize_weight: null input");
+  FM_REQUIRE(w_dtype == FM_DTYPE_BF16 || w_dtype == FM_DTYPE_F32, "fm_quantize_weight: bad dtype");
+  FM_REQUIRE(kind == QK_BF16 || kind == QK_BLOCK || kind == QK_POW2,
+             "fm_quantize_weight: kind must be bf16, block or pow2 (MX weights use fm_quantize)");
+  FM_REQUIRE(rows > 0 && cols > 0 && rows % 128 == 0 && cols % 128 == 0,
+             "fm_quantize_weight: rows and cols must be positive multiples of 128 (got %lld x %lld)",
+             (long long)rows, (long long)cols);
+  FM_REQUIRE(groups > 0, "fm_quantize_weight: groups must be positive");
+  FM_REQUIRE(q != nullptr || qt != nullptr, "fm_quantize_weight: no output requested");
+  FM_REQUIRE(q_row_off % 128 == 0 && qt_col_off % 128 == 0, "fm_quantize_weight: offsets must be multiples of 128");
+  if (kind != QK_BF16) {
+    FM_REQUIRE(q == nullptr || s != nullptr, "fm_quantize_weight: scale output missing");
+    FM_REQUIRE(qt == nullptr || st != nullptr, "fm_quantize_weight: transposed scale output missing");
+    FM_REQUIRE(q == nullptr || ld_q % 8 == 0, "fm_quantize_weight: fp8 pitch must be a multiple of 8");
+    FM_REQUIRE(qt == nullptr || ld_qt % 16 == 0, "fm_quantize_weight: transposed pitch must be a multiple of 16");
+  }
+  WeightQuantArgs a{w, w_dtype == FM_DTYPE_F32, ld_w, gs_w, kind,
+                    static_cast<uint8_t*>(q), ld_q, gs_q, q_row_off, s, ld_s, gs_s,
+                    static_cast<uint8_t*>(qt), ld_qt, gs_qt, qt_col_off, st, ld_st, gs_st};
+  FM_REQUIRE(ld_w % 8 == 0 && gs_w % 8 == 0, "fm_quantize_weight: source pitch must be a multiple of 8");
+  dim3 grid(unsigned(cols / 128), unsigned(rows / 128), unsigned(groups));
+  if (w_dtype == FM_DTYPE_F32)
+    hipLaunchKernelGGL(weight_quant_kernel<float>, grid, dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(weight_quant_kernel<uint16_t>, grid, dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  return check_launch("fm_quantize_weight");
+}
+
+int fm_dequantize(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const void* s,
+                  int s_e8m0, int row_shift, int col_shift, int64_t s_row_stride,
+                  int64_t s_col_stride, void* out, int out_dtype, int64_t ld_out, void* stream) {
+  FM_REQUIRE(q != nullptr && s != nullptr && out != nullptr, "fm_dequantize: null pointer");
+  FM_REQUIRE(cols % 8 == 0 && ld_q % 8 == 0 && ld_out % 8 == 0,
+             "fm_dequantize: cols and pitches must be multiples of 8");
+  FM_REQUIRE(col_shift >= 3 && col_shift <= 16 && row_shift >= 0 && row_shift <= 16,
+             "fm_dequantize: block shifts out of range");
+  FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_dequantize: bad out dtype");
+  if (rows == 0 || cols == 0) return 0;
+  DequantArgs a{static_cast<const uint8_t*>(q), rows, cols, ld_q, s, s_e8m0, row_shift, col_shift,
+                s_row_stride, s_col_stride, out, out_dtype == FM_DTYPE_F32, ld_out};
+  const int64_t chunks = rows * (cols / 8);
+  const unsigned blocks = unsigned(chunks / 256 + 1 < 8192 ? chunks / 256 + 1 : 8192);
+  hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("fm_dequantize");
+}
+
+int fm_scaling_aware_transpose(const void* q, int64_t rows, int64_t cols, int64_t ld_q,
+                               const float* s, int64_t ld_s, void* qt, int64_t ld_qt, float* st,
+                               int64_t ld_st, void* stream) {
+  FM_REQUIRE(q && s && qt && st, "fm_scaling_aware_transpose: null pointer");
+  FM_REQUIRE(rows % 128 == 0 && cols % 128 == 0,
+             "fm_scaling_aware_transpose: rows and cols must be multiples of 128 (got %lld x %lld)",
+             (long long)rows, (long long)cols);
+  FM_REQUIRE(ld_q % 16 == 0 && ld_qt % 16 == 0 && ld_q >= cols && ld_qt >= rows,
+             "fm_scaling_aware_transpose: pitches must be multiples of 16 and cover the matrix");
+  FM_REQUIRE(ld_s >= cols / 128 && ld_st >= cols, "fm_scaling_aware_transpose: scale pitch too small");
+  if (rows == 0 || cols == 0) return 0;
+  dim3 grid(unsigned(cols / 128), unsigned(rows / 128));
+  hipLaunchKernelGGL(sat_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(q), ld_q, s, ld_s, static_cast<uint8_t*>(qt), ld_qt,
+                     st, ld_st);
+  return check_launch("fm_scaling_aware_transpose");
+}
+
+}  // extern "C"

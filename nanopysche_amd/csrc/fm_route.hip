@@ -1,0 +1,510 @@
+// Token routing for the expert block:
+//   fm_topk_gating      -- softmax / sigmoid top-k over E experts, one wave64 per
+//                          token, plus deterministic per-wave sums of the full
+//                          softmax for the load-balancing loss
+//   fm_aux_loss         -- E * sum_i f_i P_i from the counts and those sums
+//   fm_route_sort       -- stable counting sort of the T*K (token, slot)
+//                          assignments by expert: LDS histograms, one-block scan,
+//                          wave-ballot ranks; padded group offsets (multiples of
+//                          128), row maps, and the m-tile -> expert table
+//   fm_permute          -- gather x rows into the padded expert-contiguous
+//                          buffer, optionally scaled by the router weight, fused
+//                          with bf16 / e4m3 row and transposed outputs
+//   fm_unpermute        -- out[t] = sum_k w[t,k] * y[row(t,k)], fp32 sum, one
+//                          rounding
+//   fm_router_weight_grad -- dw[t,k] = <dout[t], y[row(t,k)]>
+#include "fm_tile.h"
+#include "../../include/fm_hip.h"
+
+namespace fm {
+
+// ---------------------------------------------------------------- top-k ----
+struct TopkArgs {
+  const float* logits;   // [T, E] row pitch ld
+  int64_t T, ld;
+  int E, K;
+  int sigmoid;
+  float* w;              // [T, K]
+  void* idx;             // [T, K] int64 or int32
+  int idx_i64;
+  float* prob_partial;   // [n_waves, E] or null: per-wave sums of softmax(logits)
+};
+
+constexpr int kTopkMaxPerLane = 4;  // E <= 256
+
+__global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t n_waves = int64_t(gridDim.x) * 4;
+  float psum[kTopkMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kTopkMaxPerLane; ++j) psum[j] = 0.f;
+  for (int64_t t = wave; t < a.T; t += n_waves) {
+    float v[kTopkMaxPerLane];   // logits of experts lane + 64*j
+    float sc[kTopkMaxPerLane];  // selection scores
+#pragma unroll
+    for (int j = 0; j < kTopkMaxPerLane; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < a.E ? a.logits[t * a.ld + e] : -INFINITY;
+      sc[j] = a.sigmoid ? (e < a.E ? 1.f / (1.f + expf(-v[j])) : -INFINITY) : v[j];
+    }
+    if (a.prob_partial) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kTopkMaxPerLane; ++j) m = fmaxf(m, v[j]);
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      float ex[kTopkMaxPerLane], s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kTopkMaxPerLane; ++j) {
+        ex[j] = (lane + 64 * j) < a.E ? expf(v[j] - m) : 0.f;
+        s += ex[j];
+      }
+      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+#pragma unroll
+      for (int j = 0; j < kTopkMaxPerLane; ++j) psum[j] += ex[j] / s;
+    }
+    // K rounds of wave arg-max; ties -> lower expert index
+    float top_first = 0.f;
+    float wsum = 0.f;
+    float my_w = 0.f;
+    int my_i = 0;
+    for (int k = 0; k < a.K; ++k) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < kTopkMaxPerLane; ++j) {
+        const int e = lane + 64 * j;
+        if (e < a.E && (sc[j] > bv || (sc[j] == bv && e < bi))) { bv = sc[j]; bi = e; }
+      }
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      // remove the winner from its owner lane
+      if ((bi & 63) == lane) {
+#pragma unroll
+        for (int j = 0; j < kTopkMaxPerLane; ++j)
+          if (lane + 64 * j == bi) sc[j] = -INFINITY;
+      }
+      float lg = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kTopkMaxPerLane; ++j)
+        if (lane + 64 * j == bi) lg = v[j];
+      for (int off = 32; off > 0; off >>= 1) lg = fmaxf(lg, __shfl_xor(lg, off));
+      if (k == 0) top_first = lg;
+      // lane k keeps slot k
+      float wk;
+      if (a.sigmoid) {
+        wk = bv;  // sigmoid score
+      } else {
+        wk = expf(lg - top_first);  // top_first is the max of the selected logits
+      }
+      wsum += wk;
+      if (lane == k) { my_w = wk; my_i = bi; }
+    }
+    if (lane < a.K) {
+      const float wn = a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum;
+      a.w[t * a.K + lane] = wn;
+      if (a.idx_i64) static_cast<int64_t*>(a.idx)[t * a.K + lane] = my_i;
+      else static_cast<int32_t*>(a.idx)[t * a.K + lane] = my_i;
+    }
+  }
+  if (a.prob_partial) {
+#pragma unroll
+    for (int j = 0; j < kTopkMaxPerLane; ++j) {
+      const int e = lane + 64 * j;
+      if (e < a.E) a.prob_partial[wave * a.E + e] = psum[j];
+    }
+  }
+}
+
+// one block: P_e = sum over waves (fixed order) / T; loss = E * sum_e f_e P_e
+__global__ __launch_bounds__(256) void aux_loss_kernel(const float* prob_partial, int64_t n_waves,
+                                                       const int32_t* counts, int E, int64_t T,
+                                                       float* loss) {
+  __shared__ float red[256];
+  float acc = 0.f;
+  for (int e = threadIdx.x; e < E; e += 256) {
+    float p = 0.f;
+    for (int64_t w = 0; w < n_waves; ++w) p += prob_partial[w * E + e];
+    acc += (float(counts[e]) / float(T)) * (p / float(T));
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = float(E) * red[0];
+}
+
+// ----------------------------------------------------------------- sort ----
+constexpr int kSortBlock = 4096;     // assignments per workgroup
+constexpr int kSortMaxExperts = 1024;
+
+template <typename I>
+__device__ __forceinline__ int load_expert(const I* idx, int64_t a, int E) {
+  const int64_t e = int64_t(idx[a]);
+  return (e >= 0 && e < E) ? int(e) : -1;
+}
+
+template <typename I>
+__global__ __launch_bounds__(256) void sort_hist_kernel(const I* idx, int64_t A, int E,
+                                                        int32_t* block_hist) {
+  __shared__ int32_t hist[kSortMaxExperts];
+  for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
+  __syncthreads();
+  const int64_t base = int64_t(blockIdx.x) * kSortBlock;
+  for (int i = threadIdx.x; i < kSortBlock; i += 256) {
+    const int64_t a = base + i;
+    if (a < A) {
+      const int e = load_expert(idx, a, E);
+      if (e >= 0) atomicAdd(&hist[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) block_hist[int64_t(blockIdx.x) * E + e] = hist[e];
+}
+
+// One block of 1024 threads.  block_hist[b][e] becomes the exclusive prefix
+// over blocks; counts, padded offsets, the m-tile -> expert map and the
+// per-expert FP8/BF16 flag are written; assign_of_row is reset to -1.
+__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* block_hist, int64_t n_blocks,
+                                                         int E, int32_t* counts, int32_t* offsets,
+                                                         int32_t* tile_expert, int64_t n_tiles_max,
+                                                         int32_t* assign_of_row, int64_t rows_max,
+                                                         int32_t* use_fp8, int64_t threshold) {
+  __shared__ int32_t padded[kSortMaxExperts];
+  __shared__ int32_t scan[kSortMaxExperts + 1];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) {
+    int32_t run = 0;
+    for (int64_t b = 0; b < n_blocks; ++b) {
+      const int32_t h = block_hist[b * E + e];
+      block_hist[b * E + e] = run;
+      run += h;
+    }
+    counts[e] = run;
+    padded[e] = (run + 127) / 128 * 128;
+    if (use_fp8) use_fp8[e] = int64_t(run) >= threshold ? 1 : 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t s = 0;
+    for (int e = 0; e < E; ++e) { scan[e] = s; s += padded[e]; }
+    scan[E] = s;
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += 1024) offsets[e] = scan[e];
+  const int64_t used_tiles = scan[E] / 128;
+  for (int64_t m = tid; m < n_tiles_max; m += 1024) {
+    int32_t ex = -1;
+    if (m < used_tiles) {
+      // binary search: last e with scan[e] <= 128*m
+      int lo = 0, hi = E - 1;
+      const int32_t r = int32_t(m * 128);
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (scan[mid] <= r) lo = mid; else hi = mid - 1;
+      }
+      ex = lo;
+    }
+    tile_expert[m] = ex;
+  }
+  for (int64_t r = tid; r < rows_max; r += 1024) assign_of_row[r] = -1;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Each wave owns a contiguous quarter (1024 assignments) of the block and
+// walks it 64 at a time; peers with the same expert are found with one ballot
+// per expert-id bit, so ranks follow assignment order (stable).
+template <typename I>
+__global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t A, int E,
+                                                           const int32_t* block_prefix,
+                                                           const int32_t* offsets,
+                                                           int32_t* row_of,
+                                                           int32_t* assign_of_row) {
+  __shared__ int32_t base[4][kSortMaxExperts];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < 4 * E; i += 256) base[i / E][i % E] = 0;
+  __syncthreads();
+  const int64_t q0 = int64_t(blockIdx.x) * kSortBlock + int64_t(wave) * (kSortBlock / 4);
+  for (int i = lane; i < kSortBlock / 4; i += 64) {
+    const int64_t a = q0 + i;
+    if (a < A) {
+      const int e = load_expert(idx, a, E);
+      if (e >= 0) atomicAdd(&base[wave][e], 1);
+    }
+  }
+  __syncthreads();
+  // exclusive prefix over the 4 waves, plus the block prefix and group offset
+  for (int e = threadIdx.x; e < E; e += 256) {
+    int32_t run = offsets[e] + block_prefix[int64_t(blockIdx.x) * E + e];
+    for (int w = 0; w < 4; ++w) {
+      const int32_t c = base[w][e];
+      base[w][e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
+    const int64_t a = q0 + i0 + lane;
+    const int e = a < A ? load_expert(idx, a, E) : -1;
+    uint64_t peers = __ballot(e >= 0);
+#pragma unroll 1
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t ones = __ballot(e >= 0 && ((e >> b) & 1));
+      peers &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    int32_t my_base = 0;
+    if (e >= 0) my_base = base[wave][e];
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) {
+      const int32_t row = my_base + __popcll(peers & lanemask_lt());
+      row_of[a] = row;
+      assign_of_row[row] = int32_t(a);
+      // lowest lane of the peer group advances the counter
+      if ((peers & lanemask_lt()) == 0) base[wave][e] = my_base + __popcll(peers);
+    } else if (a < A) {
+      row_of[a] = -1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// -------------------------------------------------------------- permute ----
+// Row r of the padded buffer is x[assign_of_row[r] / K] (times the router
+// weight of that assignment when `w` is set), zeros for pad rows.
+struct GatherSrc {
+  const uint16_t* x;  // bf16 [T, D]
+  int64_t ld;
+  const int32_t* assign_of_row;
+  int K;
+  const float* w;     // [T*K] or null
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const {
+    const int32_t a = assign_of_row[row];
+    if (a < 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+      return;
+    }
+    const uint4 pk = *reinterpret_cast<const uint4*>(x + int64_t(a / K) * ld + col);
+    const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = u2f(q[i] << 16);
+      v[2 * i + 1] = u2f(q[i] & 0xffff0000u);
+    }
+    if (w) {
+      const float s = w[a];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(s, v[i]);
+    }
+  }
+};
+
+// ------------------------------------------------------------ unpermute ----
+// grid-stride over (token, 8-column chunk); K rows summed in slot order
+// with separately rounded multiply and add (no fused multiply-add), one
+// rounding to the output dtype at the end.
+__global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64_t ld_y,
+                                                        const int32_t* row_of, const float* w,
+                                                        int64_t T, int K, int64_t D,
+                                                        void* out, int out_f32, int64_t ld_out) {
+  const int64_t chunks = D / 8;
+  const int64_t n = T * chunks;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    const int64_t t = i / chunks, c = (i % chunks) * 8;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int32_t r = row_of[t * K + k];
+      if (r < 0) continue;
+      const float s = w ? w[t * K + k] : 1.f;
+      const uint4 pk = *reinterpret_cast<const uint4*>(y + int64_t(r) * ld_y + c);
+      const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = __fadd_rn(acc[2 * j], __fmul_rn(s, u2f(q[j] << 16)));
+        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], __fmul_rn(s, u2f(q[j] & 0xffff0000u)));
+      }
+    }
+    if (out_f32) {
+      float* o = static_cast<float*>(out) + t * ld_out + c;
+      *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    } else {
+      uint4 pk;
+      pk.x = uint32_t(f32_to_bf16(acc[0])) | (uint32_t(f32_to_bf16(acc[1])) << 16);
+      pk.y = uint32_t(f32_to_bf16(acc[2])) | (uint32_t(f32_to_bf16(acc[3])) << 16);
+      pk.z = uint32_t(f32_to_bf16(acc[4])) | (uint32_t(f32_to_bf16(acc[5])) << 16);
+      pk.w = uint32_t(f32_to_bf16(acc[6])) | (uint32_t(f32_to_bf16(acc[7])) << 16);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + t * ld_out + c) = pk;
+    }
+  }
+}
+
+// one wave per assignment: dw[a] = sum_d dout[t][d] * y[row_of[a]][d]
+__global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* dout, int64_t ld_do,
+                                                          const uint16_t* y, int64_t ld_y,
+                                                          const int32_t* row_of, int64_t A, int K,
+                                                          int64_t D, float* dw) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t a = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); a < A;
+       a += int64_t(gridDim.x) * 4) {
+    const int32_t r = row_of[a];
+    float acc = 0.f;
+    if (r >= 0) {
+      const uint16_t* g = dout + (a / K) * ld_do;
+      const uint16_t* yy = y + int64_t(r) * ld_y;
+      for (int64_t c = int64_t(lane) * 8; c < D; c += 512) {
+        const uint4 p = *reinterpret_cast<const uint4*>(g + c);
+        const uint4 q = *reinterpret_cast<const uint4*>(yy + c);
+        const uint32_t pw[4] = {p.x, p.y, p.z, p.w}, qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc += u2f(pw[j] << 16) * u2f(qw[j] << 16);
+          acc += u2f(pw[j] & 0xffff0000u) * u2f(qw[j] & 0xffff0000u);
+        }
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) dw[a] = acc;
+  }
+}
+
+}  // namespace fm
+
+using namespace fm;
+
+extern "C" {
+
+int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating,
+                   float* weights, void* indices, int indices_i64, float* prob_partial,
+                   int64_t n_waves, void* stream) {
+  FM_REQUIRE(logits && weights && indices, "fm_topk_gating: null pointer");
+  FM_REQUIRE(E >= 1 && E <= 64 * kTopkMaxPerLane, "fm_topk_gating: E must be in [1, %d] (got %d)",
+             64 * kTopkMaxPerLane, E);
+  FM_REQUIRE(K >= 1 && K <= E && K <= 64, "fm_topk_gating: K must be in [1, min(E, 64)] (got %d)", K);
+  FM_REQUIRE(gating == FM_GATING_SOFTMAX || gating == FM_GATING_SIGMOID, "fm_topk_gating: bad gating");
+  FM_REQUIRE(ld >= E, "fm_topk_gating: pitch < E");
+  FM_REQUIRE(n_waves >= 4 && n_waves % 4 == 0, "fm_topk_gating: n_waves must be a positive multiple of 4");
+  if (T == 0) return 0;
+  TopkArgs a{logits, T, ld, E, K, gating == FM_GATING_SIGMOID, weights, indices, indices_i64,
+             prob_partial};
+  hipLaunchKernelGGL(topk_kernel, dim3(unsigned(n_waves / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("fm_topk_gating");
+}
+
+int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
+                float* loss, void* stream) {
+  FM_REQUIRE(prob_partial && counts && loss, "fm_aux_loss: null pointer");
+  FM_REQUIRE(T > 0 && E > 0, "fm_aux_loss: T and E must be positive");
+  hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     prob_partial, n_waves, counts, E, T, loss);
+  return check_launch("fm_aux_loss");
+}
+
+int64_t fm_route_rows_max(int64_t assignments, int E) {
+  return (assignments + int64_t(E) * 127 + 127) / 128 * 128;
+}
+
+int64_t fm_route_workspace_bytes(int64_t assignments, int E) {
+  const int64_t nb = (assignments + kSortBlock - 1) / kSortBlock;
+  return (nb > 0 ? nb : 1) * E * int64_t(sizeof(int32_t));
+}
+
+int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
+                  int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
+                  int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
+                  int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int64_t A = T * K;
+  FM_REQUIRE(indices || A == 0, "fm_route_sort: null indices");
+  FM_REQUIRE(E >= 1 && E <= kSortMaxExperts, "fm_route_sort: E must be in [1, %d]", kSortMaxExperts);
+  FM_REQUIRE(counts && offsets && assign_of_row && tile_expert && workspace,
+             "fm_route_sort: null output");
+  FM_REQUIRE(rows_max >= fm_route_rows_max(A, E) && rows_max % 128 == 0,
+             "fm_route_sort: rows_max must be >= fm_route_rows_max() and a multiple of 128");
+  FM_REQUIRE(workspace_bytes >= fm_route_workspace_bytes(A, E), "fm_route_sort: workspace too small");
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  const int64_t nb = (A + kSortBlock - 1) / kSortBlock;
+  int32_t* bh = static_cast<int32_t*>(workspace);
+  if (nb > 0) {
+    if (indices_i64)
+      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int64_t*>(indices), A, E, bh);
+    else
+      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int32_t*>(indices), A, E, bh);
+    if (int rc = check_launch("fm_route_sort/hist")) return rc;
+  }
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
+                     tile_expert, rows_max / 128, assign_of_row, rows_max, use_fp8, threshold);
+  if (int rc = check_launch("fm_route_sort/scan")) return rc;
+  if (nb > 0) {
+    if (indices_i64)
+      hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int64_t*>(indices), A, E, bh, offsets, row_of,
+                         assign_of_row);
+    else
+      hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int32_t*>(indices), A, E, bh, offsets, row_of,
+                         assign_of_row);
+    if (int rc = check_launch("fm_route_sort/scatter")) return rc;
+  }
+  return 0;
+}
+
+int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,
+               int64_t rows, int K, const float* weights, int kind, void* q, int64_t ld_q, void* s,
+               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream) {
+  FM_REQUIRE(x || T == 0, "fm_permute: null input");
+  FM_REQUIRE(assign_of_row, "fm_permute: null assign_of_row");
+  FM_REQUIRE(ld_x >= D && ld_x % 8 == 0, "fm_permute: input pitch must be >= D and a multiple of 8");
+  FM_REQUIRE(K >= 1, "fm_permute: K must be >= 1");
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  GatherSrc src{static_cast<const uint16_t*>(x), ld_x, assign_of_row, K, weights};
+  return launch_tile_producer(src, o, rows, D, static_cast<hipStream_t>(stream), "fm_permute");
+}
+
+int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
+                 int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
+                 void* stream) {
+  FM_REQUIRE((y && row_of && out) || T == 0, "fm_unpermute: null pointer");
+  FM_REQUIRE(D % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0,
+             "fm_unpermute: D and pitches must be multiples of 8");
+  FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_unpermute: bad out dtype");
+  if (T == 0) return 0;
+  const int64_t n = T * (D / 8);
+  const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
+  hipLaunchKernelGGL(unpermute_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
+                     out_dtype == FM_DTYPE_F32, ld_out);
+  return check_launch("fm_unpermute");
+}
+
+int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_t ld_y,
+                          const int32_t* row_of, int64_t T, int K, int64_t D, float* dw,
+                          void* stream) {
+  FM_REQUIRE((dout && y && row_of && dw) || T == 0, "fm_router_weight_grad: null pointer");
+  FM_REQUIRE(D % 8 == 0 && ld_do % 8 == 0 && ld_y % 8 == 0,
+             "fm_router_weight_grad: D and pitches must be multiples of 8");
+  if (T == 0) return 0;
+  const int64_t A = T * K;
+  const unsigned blocks = unsigned(A / 4 + 1 < 16384 ? A / 4 + 1 : 16384);
+  hipLaunchKernelGGL(router_grad_kernel, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(dout), ld_do,
+                     static_cast<const uint16_t*>(y), ld_y, row_of, A, K, D, dw);
+  return check_launch("fm_router_weight_grad");
+}
+
+}  // extern "C"

@@ -1,0 +1,712 @@
+"""fp8_flow_moe operator path on MI355X: the functions and the expert-block
+object that nanopsyche imports from ``fp8_flow_moe`` (reference
+``fp8/__init__.py:8-24``, ``fp8/flow_moe.py:3-15``) and calls from
+``MoEBase`` (reference ``model/moe.py:1313-1332`` construction,
+``:1516-1517`` / ``:1557-1558`` call, ``:1716-1754`` post-hoc install).
+
+Every function here enqueues hand-written HIP kernels from libfm_hip.so on the
+current stream.  Nothing falls back to torch math: tensors must live on a
+ROCm device and the library must be built.
+
+The absent reference package's free-function signatures are not recoverable
+(only their names are), so the signatures below are this build's own; the
+object API (``FP8FlowMoECompute(cfg, d_model, hidden, E,
+fp8_gemm_threshold=...)``, ``set_weights``, ``__call__(x, weights, indices,
+expert_offset, num_local_experts)``) is the reference's.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .recipes import BlockScalingGranularity, FP8RecipeConfig, FP8RecipeType
+from .routing import PAD_ROWS, RoutingPlan, route_tokens
+
+FP8_BLOCK_SIZE = 128
+MX_BLOCK_SIZE = 32
+
+G = BlockScalingGranularity
+
+
+# ======================================================================= tensors ====
+@dataclass
+class FP8Tensor:
+    """e4m3 payload with its block scales.
+
+    granularity ROW_1x128 / MX_1x32:  data [R, C], scale [R, C/128] fp32 / [R, C/32] e8m0
+    granularity COL_128x1 / MX_32x1:  data [C, R] holds the transpose of a source
+                                      [R, C]; scale [R/128, C] fp32 / [R/32, C] e8m0
+    granularity BLOCK_128x128:        data [R, C], scale [R/128, C/128] fp32
+    """
+
+    data: torch.Tensor
+    scale: torch.Tensor
+    granularity: BlockScalingGranularity
+    pow2: bool = False
+
+    @property
+    def shape(self):
+        return self.data.shape
+
+    def dequantize(self, out_dtype=torch.bfloat16) -> torch.Tensor:
+        return dequantize_from_fp8(self, out_dtype=out_dtype)
+
+
+def _as_2d(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() < 2:
+        raise ValueError("expected a tensor with at least 2 dimensions")
+    x = x.reshape(-1, x.shape[-1])
+    return x if x.stride(-1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
+
+
+def _src_dtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if x.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise TypeError(f"expected bfloat16 or float32 input, got {x.dtype}")
+
+
+def _alloc_quant(rows: int, cols: int, kind: int, row: bool, col: bool, dev):
+    """Payload / scale buffers for a [rows, cols] source quantised as `kind`."""
+    u8, f32, bf = torch.uint8, torch.float32, torch.bfloat16
+    q = s = qt = st = None
+    pay = bf if kind == _lib.QUANT_BF16 else u8
+    if row:
+        q = torch.empty(rows, cols, dtype=pay, device=dev)
+        if kind in (_lib.QUANT_BLOCK, _lib.QUANT_POW2):
+            s = torch.empty(rows, cols // FP8_BLOCK_SIZE, dtype=f32, device=dev)
+        elif kind == _lib.QUANT_MX:
+            s = torch.empty(rows, cols // MX_BLOCK_SIZE, dtype=u8, device=dev)
+    if col:
+        qt = torch.empty(cols, rows, dtype=pay, device=dev)
+        if kind in (_lib.QUANT_BLOCK, _lib.QUANT_POW2):
+            st = torch.empty(rows // FP8_BLOCK_SIZE, cols, dtype=f32, device=dev)
+        elif kind == _lib.QUANT_MX:
+            st = torch.empty(rows // MX_BLOCK_SIZE, cols, dtype=u8, device=dev)
+    return q, s, qt, st
+
+
+def _ld(t):
+    return 0 if t is None else t.stride(0)
+
+
+def _tile_args(q, s, qt, st):
+    return (_lib.ptr(q), _ld(q), _lib.ptr(s), _ld(s), _lib.ptr(qt), _ld(qt), _lib.ptr(st), _ld(st))
+
+
+def _wrap(q, s, qt, st, kind):
+    if kind == _lib.QUANT_BF16:
+        return q, qt
+    pow2 = kind == _lib.QUANT_POW2
+    row_g = G.MX_1x32 if kind == _lib.QUANT_MX else G.ROW_1x128
+    col_g = G.MX_32x1 if kind == _lib.QUANT_MX else G.COL_128x1
+    row = FP8Tensor(q, s, row_g, pow2) if q is not None else None
+    col = FP8Tensor(qt, st, col_g, pow2) if qt is not None else None
+    return row, col
+
+
+# ================================================================== quantisation ====
+def quantize_to_fp8(x: torch.Tensor,
+                    granularity: BlockScalingGranularity = G.ROW_1x128,
+                    *, pow2_scale: bool = False, return_transpose: bool = False):
+    """Blockwise e4m3 quantisation of a bf16 / fp32 tensor (last dim = columns).
+
+    ROW_1x128 / MX_1x32:  row blocks; with ``return_transpose`` also the
+        column-block (128x1 / 32x1) quantisation of the transpose from the
+        same read, returned as a second FP8Tensor (no double quantisation;
+        with ``pow2_scale`` the transposed output is the scaling-aware
+        transpose of the row output).
+    COL_128x1 / MX_32x1:  only the column-block quantisation of the transpose.
+    BLOCK_128x128:        weight blocks.
+    """
+    granularity = BlockScalingGranularity(granularity)
+    _lib.require_device(x, "x")
+    x2 = _as_2d(x)
+    R, C = x2.shape
+    if granularity == G.BLOCK_128x128:
+        if R % 128 or C % 128:
+            raise ValueError(f"128x128 quantisation needs both dims % 128 == 0, got {tuple(x2.shape)}")
+        kind = _lib.QUANT_POW2 if pow2_scale else _lib.QUANT_BLOCK
+        q = torch.empty(R, C, dtype=torch.uint8, device=x.device)
+        s = torch.empty(R // 128, C // 128, dtype=torch.float32, device=x.device)
+        _lib.call("fm_quantize_weight", _lib.ptr(x2), _src_dtype(x2), 1, R, C, x2.stride(0), 0, kind,
+                  _lib.ptr(q), C, 0, 0, _lib.ptr(s), C // 128, 0, None, 0, 0, 0, None, 0, 0,
+                  _lib.stream_of(x2))
+        return FP8Tensor(q, s, G.BLOCK_128x128, pow2_scale)
+    mx = granularity in (G.MX_1x32, G.MX_32x1)
+    kind = _lib.QUANT_MX if mx else (_lib.QUANT_POW2 if pow2_scale else _lib.QUANT_BLOCK)
+    want_row = granularity in (G.ROW_1x128, G.MX_1x32)
+    want_col = return_transpose or not want_row
+    if C % 128:
+        raise ValueError(f"columns must be a multiple of 128, got {C}")
+    if want_col and R % 128:
+        raise ValueError(f"column-block quantisation needs rows % 128 == 0, got {R}")
+    q, s, qt, st = _alloc_quant(R, C, kind, want_row, want_col, x.device)
+    _lib.call("fm_quantize", _lib.ptr(x2), _src_dtype(x2), R, C, x2.stride(0), kind,
+              *_tile_args(q, s, qt, st), _lib.stream_of(x2))
+    row, col = _wrap(q, s, qt, st, kind)
+    if want_row and return_transpose:
+        return row, col
+    return row if want_row else col
+
+
+def dequantize_from_fp8(t: FP8Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """decode(q) * scale, rounded once to ``out_dtype`` (bf16 or fp32)."""
+    q, s = t.data, t.scale
+    _lib.require_device(q, "data")
+    R, C = q.shape
+    g = BlockScalingGranularity(t.granularity)
+    e8m0 = g in (G.MX_1x32, G.MX_32x1)
+    if g == G.ROW_1x128:
+        shifts = (0, 7, s.stride(0), 1)
+    elif g == G.MX_1x32:
+        shifts = (0, 5, s.stride(0), 1)
+    elif g == G.BLOCK_128x128:
+        shifts = (7, 7, s.stride(0), 1)
+    elif g in (G.COL_128x1, G.MX_32x1):
+        shifts = (0, 7 if g == G.COL_128x1 else 5, 1, s.stride(0))
+    else:
+        raise ValueError(g)
+    out = torch.empty(R, C, dtype=out_dtype, device=q.device)
+    od = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("out_dtype must be bfloat16 or float32")
+    _lib.call("fm_dequantize", _lib.ptr(q), R, C, q.stride(0), _lib.ptr(s), int(e8m0), shifts[0],
+              shifts[1], shifts[2], shifts[3], _lib.ptr(out), od, out.stride(0), _lib.stream_of(q))
+    return out
+
+
+def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
+    """Row-quantised (1x128) e4m3 -> column-quantised (128x1) e4m3 of the
+    transpose, computed from the e4m3 payload alone: each 128x128 tile's
+    column scale is the largest of its row scales and every element is
+    re-expressed as e4m3(decode(q) * s_row / s_col).  Exact for power-of-two
+    scales (an exponent shift) unless the result is an e4m3 subnormal."""
+    if BlockScalingGranularity(t.granularity) != G.ROW_1x128:
+        raise ValueError("scaling_aware_transpose expects a ROW_1x128 tensor")
+    q, s = t.data, t.scale
+    _lib.require_device(q, "data")
+    R, C = q.shape
+    if R % 128 or C % 128:
+        raise ValueError(f"scaling_aware_transpose needs both dims % 128 == 0, got {tuple(q.shape)}")
+    qt = torch.empty(C, R, dtype=torch.uint8, device=q.device)
+    st = torch.empty(R // 128, C, dtype=torch.float32, device=q.device)
+    _lib.call("fm_scaling_aware_transpose", _lib.ptr(q), R, C, q.stride(0), _lib.ptr(s), s.stride(0),
+              _lib.ptr(qt), qt.stride(0), _lib.ptr(st), st.stride(0), _lib.stream_of(q))
+    return FP8Tensor(qt, st, G.COL_128x1, t.pow2)
+
+
+# ======================================================================= SwiGLU ====
+def _swiglu(g, u, rows, H, kind, row, col, dev):
+    q, s, qt, st = _alloc_quant(rows, H, kind, row, col, dev)
+    _lib.call("fm_swiglu_quantize", _lib.ptr(g), g.stride(0), _lib.ptr(u), u.stride(0), rows, H, kind,
+              *_tile_args(q, s, qt, st), _lib.stream_of(g))
+    return q, s, qt, st
+
+
+def _act_kind(granularity, pow2_scale):
+    if granularity is None:
+        return _lib.QUANT_BF16
+    granularity = BlockScalingGranularity(granularity)
+    if granularity in (G.MX_1x32, G.MX_32x1):
+        return _lib.QUANT_MX
+    return _lib.QUANT_POW2 if pow2_scale else _lib.QUANT_BLOCK
+
+
+def fused_silu_multiply_quantize(gate: torch.Tensor, up: torch.Tensor,
+                                 granularity: Optional[BlockScalingGranularity] = G.ROW_1x128,
+                                 *, pow2_scale: bool = False, return_transpose: bool = False):
+    """h = silu(gate) * up in fp32 from bf16 inputs [M, H], quantised like
+    ``quantize_to_fp8`` (granularity None -> bf16 output)."""
+    _lib.require_device(gate, "gate")
+    if gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+        raise TypeError("gate and up must be bfloat16")
+    if gate.shape != up.shape or gate.dim() != 2:
+        raise ValueError("gate and up must be 2-D tensors of one shape")
+    if gate.stride(1) != 1 or up.stride(1) != 1:
+        raise ValueError("gate and up must have unit column stride")
+    M, H = gate.shape
+    kind = _act_kind(granularity, pow2_scale)
+    want_col = return_transpose
+    q, s, qt, st = _swiglu(gate, up, M, H, kind, True, want_col, gate.device)
+    row, col = _wrap(q, s, qt, st, kind)
+    return (row, col) if return_transpose else row
+
+
+def fused_swiglu_quantize(gate_up: torch.Tensor,
+                          granularity: Optional[BlockScalingGranularity] = G.ROW_1x128,
+                          *, pow2_scale: bool = False, return_transpose: bool = False):
+    """Same as ``fused_silu_multiply_quantize`` for a packed [M, 2H] input
+    whose first H columns are the gate and last H the up projection."""
+    H = gate_up.shape[-1] // 2
+    return fused_silu_multiply_quantize(gate_up[:, :H], gate_up[:, H:], granularity,
+                                        pow2_scale=pow2_scale, return_transpose=return_transpose)
+
+
+# ======================================================== permute / unpermute ====
+@dataclass
+class PermutedTokens:
+    """Expert-contiguous, per-expert padded copy of the tokens plus its plan."""
+
+    plan: RoutingPlan
+    rows: object            # FP8Tensor (row blocks) or bf16 tensor [rows_max, D]
+    rows_t: object = None   # FP8Tensor (column blocks) or bf16 tensor [D, rows_max]
+
+
+def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
+                      granularity: Optional[BlockScalingGranularity] = G.ROW_1x128,
+                      pow2_scale: bool = False, return_transpose: bool = False,
+                      weights: Optional[torch.Tensor] = None,
+                      fp8_gemm_threshold: int = 0) -> PermutedTokens:
+    """Gather the rows of ``x`` [T, D] (bf16) into expert order, each expert's
+    group padded to 128 rows (zeros), and quantise them in the same pass.
+
+    ``indices`` is the router's [T, K] expert indices or a RoutingPlan from an
+    earlier call.  ``weights`` [T, K] (optional) scales each gathered row by
+    its router weight.  granularity None keeps bf16."""
+    _lib.require_device(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("x must be bfloat16")
+    x2 = _as_2d(x)
+    T, D = x2.shape
+    plan = indices if isinstance(indices, RoutingPlan) else route_tokens(indices, num_experts,
+                                                                         fp8_gemm_threshold)
+    if plan.num_tokens != T:
+        raise ValueError(f"plan is for {plan.num_tokens} tokens, x has {T}")
+    kind = _act_kind(granularity, pow2_scale)
+    q, s, qt, st = _alloc_quant(plan.rows_max, D, kind, True, return_transpose, x.device)
+    w = None
+    if weights is not None:
+        w = weights.reshape(-1).to(torch.float32).contiguous()
+    _lib.call("fm_permute", _lib.ptr(x2), T, D, x2.stride(0), _lib.ptr(plan.assign_of_row),
+              plan.rows_max, plan.top_k, _lib.ptr(w), kind, *_tile_args(q, s, qt, st),
+              _lib.stream_of(x2))
+    row, col = _wrap(q, s, qt, st, kind)
+    return PermutedTokens(plan, row, col)
+
+
+def fused_unpermute_unpad(y: torch.Tensor, plan: RoutingPlan,
+                          weights: Optional[torch.Tensor] = None,
+                          out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """out[t] = sum_k weights[t, k] * y[row(t, k)] (weights None -> 1), summed
+    in fp32 in slot order and rounded once.  y is bf16 [rows_max, D]."""
+    _lib.require_device(y, "y")
+    if y.dtype != torch.bfloat16:
+        raise TypeError("y must be bfloat16")
+    D = y.shape[1]
+    T, K = plan.num_tokens, plan.top_k
+    out = torch.empty(T, D, dtype=out_dtype, device=y.device)
+    w = None if weights is None else weights.reshape(-1).to(torch.float32).contiguous()
+    od = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    _lib.call("fm_unpermute", _lib.ptr(y), y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(w), T, K, D,
+              _lib.ptr(out), od, out.stride(0), _lib.stream_of(y))
+    return out
+
+
+# ================================================================ grouped GEMM ====
+def _operand(data, scale=None, *, ld=None, gs=0, s_row=0, s_kb=0, s_gs=0, shift=0):
+    o = _lib.FmGemmOperand()
+    o.data = data.data_ptr()
+    o.ld = data.stride(0) if ld is None else ld
+    o.group_stride = gs
+    o.scale = None if scale is None else scale.data_ptr()
+    o.scale_row_stride = s_row
+    o.scale_kb_stride = s_kb
+    o.scale_group_stride = s_gs
+    o.scale_row_shift = shift
+    return o
+
+
+def _token_operand(t, kind):
+    """Row-major activations [rows, K] (FP8Tensor or bf16 tensor)."""
+    if kind == _lib.QUANT_BF16:
+        return _operand(t)
+    return _operand(t.data, t.scale, s_row=t.scale.stride(0), s_kb=1)
+
+
+def _col_operand(t, kind):
+    """Column-quantised transposed activations [C, rows] with scales [rows/blk, C]."""
+    if kind == _lib.QUANT_BF16:
+        return _operand(t)
+    return _operand(t.data, t.scale, s_row=1, s_kb=t.scale.stride(0))
+
+
+@dataclass
+class ExpertWeightOperand:
+    """One expert-weight GEMM operand: E matrices [N, K] (K contiguous)."""
+
+    data: torch.Tensor
+    scale: Optional[torch.Tensor]
+    ld: int
+    gs: int
+    s_row: int = 0
+    s_kb: int = 0
+    s_gs: int = 0
+    shift: int = 0
+    N: int = 0
+    K: int = 0
+
+    def operand(self):
+        return _operand(self.data, self.scale, ld=self.ld, gs=self.gs, s_row=self.s_row,
+                        s_kb=self.s_kb, s_gs=self.s_gs, shift=self.shift)
+
+
+def _gemm_kind(kind):
+    return {_lib.QUANT_BF16: _lib.GEMM_BF16, _lib.QUANT_BLOCK: _lib.GEMM_FP8_F32,
+            _lib.QUANT_POW2: _lib.GEMM_FP8_POW2, _lib.QUANT_MX: _lib.GEMM_FP8_MX}[kind]
+
+
+# Optional per-launch timer (bench.py sets it): called as
+# GEMM_TIMER(name, algorithmic_flops, launch_fn) around each grouped GEMM.
+GEMM_TIMER = None
+_KIND_NAME = {_lib.QUANT_BF16: "bf16", _lib.QUANT_BLOCK: "fp8_f32", _lib.QUANT_POW2: "fp8_pow2",
+              _lib.QUANT_MX: "fp8_mx"}
+
+
+def _timed(name, flops, fn):
+    if GEMM_TIMER is None:
+        fn()
+    else:
+        GEMM_TIMER(name, flops, fn)
+
+
+def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=None, want=1):
+    def launch():
+        _lib.call("fm_grouped_gemm_ragged_m", _gemm_kind(kind), _token_operand(tokens, kind),
+                  w.operand(), plan.m_tiles, _lib.ptr(plan.tile_expert), plan.num_experts, w.N, w.K,
+                  _lib.ptr(mask), want, _lib.ptr(out), _dt(out), out.stride(0), _lib.stream_of(out))
+
+    _timed(f"grouped_gemm_ragged_m/{_KIND_NAME[kind]}",
+           2.0 * plan.num_tokens * plan.top_k * w.N * w.K, launch)
+
+
+def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out2_gs=0, split=None,
+            mask=None, want=1):
+    def launch():
+        _lib.call("fm_grouped_gemm_ragged_k", _gemm_kind(kind), _col_operand(a_t, kind),
+                  _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
+                  _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
+                  M if split is None else split, _dt(out), N, _lib.stream_of(out))
+
+    _timed(f"grouped_gemm_ragged_k/{_KIND_NAME[kind]}",
+           2.0 * plan.num_tokens * plan.top_k * M * N, launch)
+
+
+def _dt(t):
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    raise TypeError(f"unsupported output dtype {t.dtype}")
+
+
+def fp8_grouped_gemm(tokens, weights: ExpertWeightOperand, plan: RoutingPlan,
+                     out_dtype: torch.dtype = torch.bfloat16,
+                     expert_mask: Optional[torch.Tensor] = None, mask_want: int = 1,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-expert out[r] = tokens[r] @ W_e^T over the padded expert buffer.
+
+    ``tokens`` is a row-quantised FP8Tensor (or a bf16 tensor for the BF16
+    path) of [plan.rows_max, K]; ``weights`` an ExpertWeightOperand from
+    ``ExpertWeights``.  Tiles of experts with ``expert_mask[e] != mask_want``
+    are skipped (the fp8_gemm_threshold switch)."""
+    if isinstance(tokens, FP8Tensor):
+        g = BlockScalingGranularity(tokens.granularity)
+        kind = _lib.QUANT_MX if g == G.MX_1x32 else (_lib.QUANT_POW2 if tokens.pow2 else _lib.QUANT_BLOCK)
+        rows = tokens.data.shape[0]
+        dev = tokens.data.device
+    else:
+        kind = _lib.QUANT_BF16
+        rows = tokens.shape[0]
+        dev = tokens.device
+    if out is None:
+        out = torch.empty(rows, weights.N, dtype=out_dtype, device=dev)
+    _gemm_m(kind, tokens, weights, plan, out, expert_mask, mask_want)
+    return out
+
+
+# ============================================================== expert weights ====
+class ExpertWeights:
+    """GEMM operands of the expert weights for one recipe, rebuilt only when
+    the parameters change (their ``_version`` counters or storage move).
+
+    w13   [E][2H, D]  forward gate|up          (rows of w1 then w3 per expert)
+    w2t   [E][D, H]   forward down             (w2_e transposed)
+    w2    [E][H, D]   dgrad dH = dY w2_e^T
+    w13t  [E][D, 2H]  dgrad dX = [dg|du] [w1_e; w3_e]
+    """
+
+    def __init__(self, kind: int):
+        self.kind = kind
+        self.key = None
+        self.w13 = self.w2t = self.w2 = self.w13t = None
+
+    def refresh(self, w1, w2, w3, E: int) -> "ExpertWeights":
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in (w1, w2, w3))
+        if key != self.key:
+            self._build(w1.detach(), w2.detach(), w3.detach(), E)
+            self.key = key
+        return self
+
+    def _build(self, w1, w2, w3, E):
+        EH, D = w1.shape
+        H = EH // E
+        dev = w1.device
+        kind = self.kind
+        if kind == _lib.QUANT_MX:
+            self._build_mx(w1, w2, w3, E, H, D)
+            return
+        pay = torch.bfloat16 if kind == _lib.QUANT_BF16 else torch.uint8
+        f32 = torch.float32
+        W13 = torch.empty(E, 2 * H, D, dtype=pay, device=dev)
+        W13t = torch.empty(E, D, 2 * H, dtype=pay, device=dev)
+        W2 = torch.empty(E, H, D, dtype=pay, device=dev)
+        W2t = torch.empty(E, D, H, dtype=pay, device=dev)
+        fp8 = kind != _lib.QUANT_BF16
+        S13 = torch.empty(E, 2 * H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
+        S13t = torch.empty(E, D // 128, 2 * H // 128, dtype=f32, device=dev) if fp8 else None
+        S2 = torch.empty(E, H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
+        S2t = torch.empty(E, D // 128, H // 128, dtype=f32, device=dev) if fp8 else None
+        stream = _lib.stream_of(w1)
+
+        def q(src, dst, s, dst_t, s_t, row_off, col_off, rows_out, s_rows_out):
+            src = src.contiguous()
+            _lib.call("fm_quantize_weight", _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind,
+                      _lib.ptr(dst), D, rows_out * D, row_off,
+                      _lib.ptr(s), D // 128, (s_rows_out // 128) * (D // 128),
+                      _lib.ptr(dst_t), rows_out, D * rows_out, col_off,
+                      _lib.ptr(s_t), s_rows_out // 128, (D // 128) * (s_rows_out // 128), stream)
+
+        q(w1, W13, S13, W13t, S13t, 0, 0, 2 * H, 2 * H)
+        q(w3, W13, S13, W13t, S13t, H, H, 2 * H, 2 * H)
+        q(w2, W2, S2, W2t, S2t, 0, 0, H, H)
+        sh = 7
+        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, (2 * H // 128) * (D // 128), sh, 2 * H, D)
+        self.w13t = ExpertWeightOperand(W13t, S13t, 2 * H, D * 2 * H, 2 * H // 128, 1, (D // 128) * (2 * H // 128), sh, D, 2 * H)
+        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, (H // 128) * (D // 128), sh, H, D)
+        self.w2t = ExpertWeightOperand(W2t, S2t, H, D * H, H // 128, 1, (D // 128) * (H // 128), sh, D, H)
+
+    def _build_mx(self, w1, w2, w3, E, H, D):
+        dev = w1.device
+        W13src = torch.cat([w1.reshape(E, H, D), w3.reshape(E, H, D)], dim=1).reshape(E * 2 * H, D)
+        W13src = W13src.to(torch.bfloat16).contiguous()
+        W2src = w2.to(torch.bfloat16).contiguous()
+        stream = _lib.stream_of(w1)
+
+        def q(src, rows):
+            qq, s, qt, st = _alloc_quant(rows, D, _lib.QUANT_MX, True, True, dev)
+            _lib.call("fm_quantize", _lib.ptr(src), _lib.DTYPE_BF16, rows, D, D, _lib.QUANT_MX,
+                      *_tile_args(qq, s, qt, st), stream)
+            return qq, s, qt, st
+
+        W13, S13, W13t, S13t = q(W13src, E * 2 * H)
+        W2, S2, W2t, S2t = q(W2src, E * H)
+        self._keep = (W13src, W2src)
+        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 32, 1, 2 * H * D // 32, 0, 2 * H, D)
+        self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H)
+        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D)
+        self.w2t = ExpertWeightOperand(W2t, S2t, E * H, H, 1, D, (H // 32) * D, 0, D, H)
+
+
+# ================================================================ expert block ====
+@dataclass
+class FP8FlowMoEConfig:
+    enabled: bool = False
+    fp8_recipe: FP8RecipeConfig = field(default_factory=FP8RecipeConfig)
+
+
+class _FlowMoEFunction(torch.autograd.Function):
+    """Forward + backward of the expert block; see FP8FlowMoECompute."""
+
+    @staticmethod
+    def forward(ctx, x, weights, w1, w2, w3, indices, compute):
+        return compute._forward(ctx, x, weights, w1, w2, w3, indices)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        return ctx.compute._backward(ctx, grad_out)
+
+
+class FP8FlowMoECompute:
+    """The expert block behind ``MoEBase._fp8_flow_moe`` (reference
+    ``model/moe.py:1313-1332``).
+
+    ``__call__(x [N, D], weights [N, K] fp32, indices [N, K] int, expert_offset,
+    num_local_experts) -> [N, D]`` returns sum_k weights[n, k] *
+    expert_{indices[n, k]}(x[n]) with SwiGLU experts
+    ``(silu(x w1_e^T) * (x w3_e^T)) w2_e`` (reference ``model/moe.py:1164-1183``),
+    differentiable with respect to x, weights, w1, w2, w3.
+
+    Dataflow (all on the GPU, no host synchronisation):
+      route (stable counting sort, groups padded to 128 rows)
+      -> permute + quantise x (row blocks; column blocks kept for dW13)
+      -> grouped GEMM gate|up -> SwiGLU + quantise -> grouped GEMM down
+      -> weighted unpermute.
+    ``fp8_gemm_threshold``: experts with at least that many assignments use
+    the FP8 GEMMs, the others BF16 (0 forces FP8 for all).  The object owns no
+    parameters and adds no state_dict keys; weights are borrowed via
+    ``set_weights``.
+    """
+
+    def __init__(self, config: FP8FlowMoEConfig, d_model: int, hidden_size: int,
+                 num_experts: int, fp8_gemm_threshold: int = 1000000):
+        if d_model % 128 or hidden_size % 128:
+            raise ValueError(f"d_model ({d_model}) and hidden_size ({hidden_size}) must be "
+                             "multiples of 128")
+        self.config = config
+        self.d_model = d_model
+        self.hidden_size = hidden_size
+        self.num_experts = num_experts
+        self.fp8_gemm_threshold = int(fp8_gemm_threshold)
+        recipe = config.fp8_recipe if config.enabled else FP8RecipeConfig()
+        self.recipe = recipe
+        self.fp8_kind = recipe.act_kind
+        if self.fp8_kind == _lib.QUANT_BF16:
+            self.fp8_gemm_threshold = 1 << 62  # no FP8 recipe: every expert on BF16
+        self._w = None
+        self._cache = {}
+
+    def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
+        for w in (w1, w2, w3):
+            if tuple(w.shape) != (self.num_experts * self.hidden_size, self.d_model):
+                raise ValueError(f"expert weights must be [E*H, D] = "
+                                 f"[{self.num_experts * self.hidden_size}, {self.d_model}], got {tuple(w.shape)}")
+        self._w = (w1, w2, w3)
+
+    def _weights(self, kind: int) -> ExpertWeights:
+        ew = self._cache.get(kind)
+        if ew is None:
+            ew = self._cache[kind] = ExpertWeights(kind)
+        return ew.refresh(*self._w, self.num_experts)
+
+    def modes(self, num_assignments: int):
+        """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
+        the host from the threshold alone (no read of the device counts)."""
+        if self.fp8_kind == _lib.QUANT_BF16:
+            return None, True
+        if self.fp8_gemm_threshold <= 0:
+            return self.fp8_kind, False
+        if self.fp8_gemm_threshold > num_assignments:
+            return None, True
+        return self.fp8_kind, True
+
+    def __call__(self, x, weights, indices, expert_offset: int = 0,
+                 num_local_experts: Optional[int] = None):
+        if self._w is None:
+            raise RuntimeError("set_weights() must be called before the expert block runs")
+        E = self.num_experts if num_local_experts is None else int(num_local_experts)
+        if E != self.num_experts:
+            raise ValueError(f"num_local_experts={E} but the block holds {self.num_experts} experts")
+        _lib.require_device(x, "x")
+        if expert_offset:
+            indices = indices - int(expert_offset)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        K = indices.shape[-1]
+        out = _FlowMoEFunction.apply(x2, weights.reshape(-1, K), *self._w,
+                                     indices.reshape(-1, K), self)
+        return out.reshape(shape)
+
+    # ------------------------------------------------------------------ forward ----
+    def _forward(self, ctx, x, weights, w1, w2, w3, indices):
+        ctx.x_dtype = x.dtype
+        if x.dtype != torch.bfloat16:
+            x = x.to(torch.bfloat16)
+        x = x.contiguous()
+        T, D = x.shape
+        E, H = self.num_experts, self.hidden_size
+        K = indices.shape[1]
+        fp8_kind, use_bf16 = self.modes(T * K)
+        plan = route_tokens(indices, E, self.fp8_gemm_threshold if fp8_kind is not None else 1 << 62)
+        wts = weights.to(torch.float32).contiguous()
+        dev = x.device
+        R = plan.rows_max
+        GU = torch.empty(R, 2 * H, dtype=torch.bfloat16, device=dev)
+        Y = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
+        mask = plan.use_fp8 if (fp8_kind is not None and use_bf16) else None
+        saved = {}
+        for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
+            if kind is None:
+                continue
+            ew = self._weights(kind)
+            pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
+                                   return_transpose=True)
+            _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
+            saved[kind] = (pt.rows_t, ew)
+        for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
+            if kind is None:
+                continue
+            q, s, _, _ = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, False, dev)
+            hrow, _ = _wrap(q, s, None, None, kind)
+            _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
+        out = fused_unpermute_unpad(Y, plan, wts)
+        ctx.compute = self
+        ctx.plan = plan
+        ctx.kinds = (fp8_kind, use_bf16)
+        ctx.saved_cols = {k: v[0] for k, v in saved.items()}
+        ctx.wdtypes = (w1.dtype, w2.dtype, w3.dtype)
+        ctx.save_for_backward(wts, GU, Y)
+        return out
+
+    # ----------------------------------------------------------------- backward ----
+    def _backward(self, ctx, grad_out):
+        wts, GU, Y = ctx.saved_tensors
+        plan = ctx.plan
+        fp8_kind, use_bf16 = ctx.kinds
+        E, H, D = self.num_experts, self.hidden_size, self.d_model
+        T, K = plan.num_tokens, plan.top_k
+        R = plan.rows_max
+        dev = GU.device
+        dO = grad_out.reshape(T, D).to(torch.bfloat16).contiguous()
+        mask = plan.use_fp8 if (fp8_kind is not None and use_bf16) else None
+        # router-weight gradient from the saved expert outputs
+        dw = torch.empty(T * K, dtype=torch.float32, device=dev)
+        _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
+                  _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
+        dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
+        dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
+        w1dt, w2dt, w3dt = ctx.wdtypes
+        dW1 = torch.empty(E * H, D, dtype=w1dt, device=dev)
+        dW2 = torch.empty(E * H, D, dtype=w2dt, device=dev)
+        dW3 = torch.empty(E * H, D, dtype=w3dt, device=dev)
+        if not (w1dt == w3dt and w1dt in (torch.float32, torch.bfloat16) and w2dt in (torch.float32, torch.bfloat16)):
+            raise TypeError("expert weights must be float32 or bfloat16 (w1 and w3 alike)")
+        runs = [(k, w) for k, w in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)) if k is not None]
+        dy = {}
+        for kind, want in runs:
+            ew = self._weights(kind)
+            pt = fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
+                                   return_transpose=True, weights=wts)
+            _gemm_m(kind, pt.rows, ew.w2, plan, dH, mask, want)
+            dy[kind] = pt.rows_t
+        for kind, want in runs:
+            ew = self._weights(kind)
+            gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev)
+            _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
+                      _lib.ptr(dH), dH.stride(0), R, H, kind, *_tile_args(gq, gs, gqt, gst),
+                      _lib.stream_of(GU))
+            dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
+            _, _, hqt, hst = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, False, True, dev)
+            _, h_col = _wrap(None, None, hqt, hst, kind)
+            # weight gradients: contraction over each expert's tokens
+            _gemm_k(kind, h_col, dy[kind], plan, H, D, dW2, H * D, mask=mask, want=want)
+            _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,
+                    mask=mask, want=want)
+            # input gradient
+            _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
+        dx = fused_unpermute_unpad(dXp, plan, None)
+        ctx.saved_cols = None
+        return (dx.to(ctx.x_dtype), dw.reshape(T, K), dW1, dW2, dW3, None, None)
+
+
+def _gran(kind):
+    if kind == _lib.QUANT_BF16:
+        return None
+    if kind == _lib.QUANT_MX:
+        return G.MX_1x32
+    return G.ROW_1x128

@@ -1,0 +1,119 @@
+"""Token routing on the GPU: top-k gating, load-balancing loss and the
+stable counting sort that orders (token, slot) assignments by expert.
+
+Reference behaviour restated by these kernels:
+  ``model/moe.py:249-255``   softmax gating (top-k of logits, softmax over the
+                             K selected logits)
+  ``model/moe.py:257-265``   sigmoid gating (top-k of sigmoid, /(sum + 1e-8))
+  ``model/moe.py:267-281``   load-balancing loss E * sum f_i P_i
+  ``model/moe.py:1565-1567`` per-expert token lists in ascending token order
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+PAD_ROWS = 128  # every expert group is padded to a multiple of this many rows
+
+
+@dataclass
+class RoutingPlan:
+    """Device-resident result of the counting sort (no host synchronisation).
+
+    counts        [E] int32       assignments per expert
+    offsets       [E+1] int32     padded group starts (multiples of 128)
+    row_of        [T*K] int32     padded row of assignment a = t*K + k (-1 if its
+                                  expert index is outside [0, E))
+    assign_of_row [rows_max] int32  assignment held by each row, -1 on padding
+    tile_expert   [rows_max/128] int32  expert of each 128-row tile, -1 past the end
+    use_fp8       [E] int32       counts[e] >= fp8_gemm_threshold
+    """
+
+    num_tokens: int
+    top_k: int
+    num_experts: int
+    rows_max: int
+    counts: torch.Tensor
+    offsets: torch.Tensor
+    row_of: torch.Tensor
+    assign_of_row: torch.Tensor
+    tile_expert: torch.Tensor
+    use_fp8: torch.Tensor
+
+    @property
+    def m_tiles(self) -> int:
+        return self.rows_max // PAD_ROWS
+
+
+def rows_max(num_assignments: int, num_experts: int) -> int:
+    """Upper bound of the padded buffer's rows, known without reading counts."""
+    return int(_lib.load().fm_route_rows_max(num_assignments, num_experts))
+
+
+def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: int = 0) -> RoutingPlan:
+    """Stable counting sort of ``indices`` [T, K] (int64 or int32) by expert."""
+    _lib.require_device(indices, "indices")
+    if indices.dim() != 2:
+        indices = indices.reshape(-1, indices.shape[-1])
+    if indices.dtype not in (torch.int64, torch.int32):
+        raise TypeError(f"indices must be int64 or int32, got {indices.dtype}")
+    indices = indices.contiguous()
+    T, K = indices.shape
+    A = T * K
+    lib = _lib.load()
+    rmax = int(lib.fm_route_rows_max(A, num_experts))
+    dev = indices.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, **i32)
+    offsets = torch.empty(num_experts + 1, **i32)
+    row_of = torch.empty(max(A, 1), **i32)
+    assign_of_row = torch.empty(rmax, **i32)
+    tile_expert = torch.empty(rmax // PAD_ROWS, **i32)
+    use_fp8 = torch.empty(num_experts, **i32)
+    ws_bytes = int(lib.fm_route_workspace_bytes(A, num_experts))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("fm_route_sort", _lib.ptr(indices), int(indices.dtype == torch.int64), T, K,
+              num_experts, int(fp8_gemm_threshold), _lib.ptr(counts), _lib.ptr(offsets),
+              _lib.ptr(row_of), _lib.ptr(assign_of_row), rmax, _lib.ptr(tile_expert),
+              _lib.ptr(use_fp8), _lib.ptr(ws), ws_bytes, _lib.stream_of(indices))
+    return RoutingPlan(T, K, num_experts, rmax, counts, offsets, row_of[:A], assign_of_row,
+                       tile_expert, use_fp8)
+
+
+def topk_gating(logits: torch.Tensor, top_k: int, gating: str = "softmax",
+                return_prob_partial: bool = False):
+    """Top-k gating over the last dimension of fp32 ``logits`` [..., E].
+
+    Returns (weights [..., K] fp32, indices [..., K] int64[, prob_partial])."""
+    _lib.require_device(logits, "logits")
+    if logits.dtype != torch.float32:
+        raise TypeError("logits must be float32 (the router runs the gate in fp32)")
+    E = logits.shape[-1]
+    lead = logits.shape[:-1]
+    lg = logits.reshape(-1, E).contiguous()
+    T = lg.shape[0]
+    w = torch.empty(T, top_k, dtype=torch.float32, device=lg.device)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=lg.device)
+    n_waves = 1024
+    part = torch.empty(n_waves, E, dtype=torch.float32, device=lg.device) if return_prob_partial else None
+    g = {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[str(gating).lower().split(".")[-1]]
+    _lib.call("fm_topk_gating", _lib.ptr(lg), T, E, E, top_k, g, _lib.ptr(w), _lib.ptr(idx), 1,
+              _lib.ptr(part), n_waves, _lib.stream_of(lg))
+    w = w.reshape(*lead, top_k)
+    idx = idx.reshape(*lead, top_k)
+    if return_prob_partial:
+        return w, idx, part
+    return w, idx
+
+
+def load_balancing_loss(prob_partial: torch.Tensor, counts: torch.Tensor, num_tokens: int) -> torch.Tensor:
+    """E * sum_e (counts[e]/T) * mean_t softmax(logits)[t, e] as a 0-d fp32 tensor."""
+    E = counts.numel()
+    loss = torch.empty((), dtype=torch.float32, device=counts.device)
+    _lib.call("fm_aux_loss", _lib.ptr(prob_partial), prob_partial.shape[0], _lib.ptr(counts), E,
+              num_tokens, _lib.ptr(loss), _lib.stream_of(counts))
+    return loss

@@ -1,0 +1,226 @@
+"""CPU restatement of the MoE expert block, forward + backward (test oracle only).
+
+Two oracles:
+
+``moe_bf16_loop``  -- the reference's BF16 expert computation,
+    ``MoEBase._compute_experts_padded_bmm`` (``model/moe.py:1542-1596``) with the
+    SwiGLU convention of ``ExpertMLP.forward`` (``model/moe.py:1181-1183``:
+    gate/up are ``x @ w.T``, down is ``h @ w2`` with ``w2`` un-transposed), in
+    fp32 on CPU from the same bf16 inputs, differentiated by torch autograd.
+    Padding rows to a power of two (``:1577-1580``) is dropped: zero rows change
+    no valid output.  The per-expert bf16 rounding of ``output`` (``:1594``) is
+    replaced by one fp32 sum, well inside the stated tolerance.
+
+``moe_flow_reference`` -- the FP8 flow with the quantisation points the HIP
+    path uses, as dequantise-then-fp32-matmul (the tolerance oracle named for
+    the FP8 path).  Quantised operands come from ``oracle.fp8`` and are
+    bit-identical to the kernels' when the inputs are; GEMM outputs are rounded
+    to bf16 where the HIP path stores bf16.  With ``recipe=None`` it is the
+    BF16 grouped path (bf16 operands, fp32 accumulate).
+
+    The dataflow (which tensor is quantised along which axis) is this build's
+    own: the absent ``fp8_flow_moe`` package's dataflow cannot be read, so it
+    is "parity unpinned" against that package and pinned instead by (i) the
+    BF16 loop above within a looser FP8-vs-exact bound and (ii) torch autograd
+    of the same math for the gradient formulas.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import fp8 as ofp8
+from . import routing as orouting
+
+
+def moe_bf16_loop(x, weights, indices, w1, w2, w3, num_experts, grad_out=None):
+    """model/moe.py:1542-1596 in fp32; returns (out, grads dict or None)."""
+    H = w1.shape[0] // num_experts
+    xs = x.detach().float().requires_grad_(grad_out is not None)
+    ws = weights.detach().float().requires_grad_(grad_out is not None)
+    W1 = w1.detach().float().requires_grad_(grad_out is not None)
+    W2 = w2.detach().float().requires_grad_(grad_out is not None)
+    W3 = w3.detach().float().requires_grad_(grad_out is not None)
+    out = torch.zeros_like(xs)
+    for e in range(num_experts):
+        mask = indices == e
+        token_ids = mask.any(dim=-1).nonzero(as_tuple=True)[0]
+        if token_ids.numel() == 0:
+            continue
+        tx = xs[token_ids]
+        slot = (indices[token_ids] == e).float()
+        tw = (ws[token_ids] * slot).sum(dim=-1)
+        g = tx @ W1[e * H:(e + 1) * H].T
+        u = tx @ W3[e * H:(e + 1) * H].T
+        y = (F.silu(g) * u) @ W2[e * H:(e + 1) * H]
+        out = out.index_add(0, token_ids, tw.unsqueeze(-1) * y)
+    if grad_out is None:
+        return out.detach(), None
+    out.backward(grad_out.float())
+    grads = dict(x=xs.grad, weights=ws.grad, w1=W1.grad, w2=W2.grad, w3=W3.grad)
+    return out.detach(), grads
+
+
+# ------------------------------------------------------------------ FP8 flow ----
+def _np(t):
+    return t.detach().cpu().float().numpy()
+
+
+def _bf16(a):
+    return ofp8.bf16_round(np.asarray(a, dtype=np.float32))
+
+
+def _q_rows(a, recipe):
+    """Row quantise + dequantise: the values the GEMM sees."""
+    if recipe == "mxfp8":
+        q, c = ofp8.quant_mx_1x32(a)
+        return ofp8.dequant_mx_1x32(q, c)
+    q, s = ofp8.quant_1x128(a, pow2=(recipe == "flow_moe"))
+    return ofp8.dequant_1x128(q, s)
+
+
+def _q_cols(a, recipe, rowq_of_a=None):
+    """Column-quantised transpose of a [R, C] -> dequantised [C, R].
+
+    blockwise / mxfp8 quantise the source directly; flow_moe re-expresses the
+    row-quantised tensor with the scaling-aware transpose (exact exponent
+    shifts for power-of-two scales)."""
+    if recipe == "mxfp8":
+        qt, ct = ofp8.quant_mx_32x1(a)
+        return ofp8.dequant_mx_1x32(qt, np.ascontiguousarray(ct.T))
+    if recipe == "flow_moe":
+        q, s = ofp8.quant_1x128(a, pow2=True)
+        qt, st = ofp8.scaling_aware_transpose(q, s)
+        return ofp8.dequant_1x128(qt, np.ascontiguousarray(st.T))
+    qt, st = ofp8.quant_128x1(a, pow2=False)
+    return ofp8.dequant_1x128(qt, np.ascontiguousarray(st.T))
+
+
+def _q_weight(w, recipe):
+    """Weight operand [N, K] as the GEMM sees it (blocks along K for MX)."""
+    if recipe == "mxfp8":
+        q, c = ofp8.quant_mx_1x32(w)
+        return ofp8.dequant_mx_1x32(q, c)
+    q, s = ofp8.quant_128x128(w, pow2=(recipe == "flow_moe"))
+    return ofp8.dequant_128x128(q, s)
+
+
+def _mm(a, b_t):
+    """fp32 a @ b_t.T via torch CPU."""
+    return (torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+            @ torch.from_numpy(np.ascontiguousarray(b_t, dtype=np.float32)).T).numpy()
+
+
+def _silu(g):
+    return (g / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
+
+
+def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=None,
+                       recipe="flow_moe"):
+    """The HIP path's dataflow on CPU.  recipe in {None, 'blockwise', 'flow_moe', 'mxfp8'}.
+
+    Returns (out [T, D] f32 (bf16-valued), grads dict or None)."""
+    E = num_experts
+    T, D = x.shape
+    K = indices.shape[1]
+    H = w1.shape[0] // E
+    xs = _bf16(_np(x))
+    wts = _np(weights).astype(np.float32)
+    rt = orouting.sort_assignments(indices.cpu().numpy(), E)
+    offs = rt["offsets"]
+    Xp = orouting.permute_pad(xs, rt["assign_of_row"], K)
+    W1 = _bf16(_np(w1)).reshape(E, H, D)
+    W2 = _bf16(_np(w2)).reshape(E, H, D)
+    W3 = _bf16(_np(w3)).reshape(E, H, D)
+    Mp = int(offs[-1])
+    fp8 = recipe is not None
+    Xv = _q_rows(Xp, recipe) if fp8 else Xp
+    GU = np.zeros((Mp, 2 * H), np.float32)
+    Y = np.zeros((Mp, D), np.float32)
+    Hv_all = np.zeros((Mp, H), np.float32)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        W13 = np.concatenate([W1[e], W3[e]], axis=0)
+        Bv = _q_weight(W13, recipe) if fp8 else W13
+        GU[r0:r1] = _bf16(_mm(Xv[r0:r1], Bv))
+    g, u = GU[:, :H], GU[:, H:]
+    h = (_silu(g) * u).astype(np.float32)
+    Hv = _q_rows(h, recipe) if fp8 else _bf16(h)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        W2t = np.ascontiguousarray(W2[e].T)
+        Bv = _q_weight(W2t, recipe) if fp8 else W2t
+        Y[r0:r1] = _bf16(_mm(Hv[r0:r1], Bv))
+    out = orouting.unpermute_unpad(Y, rt["row_of"], wts, T, K)
+    out = _bf16(out)
+    if grad_out is None:
+        return out, None
+
+    dO = _bf16(_np(grad_out))
+    a_rows = rt["assign_of_row"]
+    valid = a_rows >= 0
+    dYp = np.zeros((Mp, D), np.float32)
+    dYp[valid] = (wts.reshape(-1)[a_rows[valid], None] * dO[a_rows[valid] // K]).astype(np.float32)
+    dw = np.einsum("td,tkd->tk", dO.astype(np.float64),
+                   Y[rt["row_of"].reshape(T, K)].astype(np.float64)).astype(np.float32)
+    if fp8:
+        dYv = _q_rows(dYp, recipe)
+        dYvT = _q_cols(dYp, recipe)          # [D, Mp]
+    else:
+        dYv = _bf16(dYp)
+        dYvT = dYv.T
+    dH = np.zeros((Mp, H), np.float32)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        Bv = _q_weight(W2[e], recipe) if fp8 else W2[e]      # [H, D]
+        dH[r0:r1] = _bf16(_mm(dYv[r0:r1], Bv))
+    sg = (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
+    dg = (dH * u * sg * (1.0 + g * (1.0 - sg))).astype(np.float32)
+    du = (dH * (g * sg)).astype(np.float32)
+    dGU = np.concatenate([dg, du], axis=1)
+    if fp8:
+        dGUv = _q_rows(dGU, recipe)
+        dGUvT = _q_cols(dGU, recipe)         # [2H, Mp]
+        HvT = _q_cols(h, recipe)             # [H, Mp]
+        XvT = _q_cols(Xp, recipe)            # [D, Mp]
+    else:
+        dGUv = _bf16(dGU)
+        dGUvT = dGUv.T
+        HvT = Hv.T
+        XvT = Xp.T
+    dW1 = np.zeros((E, H, D), np.float32)
+    dW2 = np.zeros((E, H, D), np.float32)
+    dW3 = np.zeros((E, H, D), np.float32)
+    dXp = np.zeros((Mp, D), np.float32)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        dW2[e] = _mm(HvT[:, r0:r1], dYvT[:, r0:r1])
+        dW13 = _mm(dGUvT[:, r0:r1], XvT[:, r0:r1])
+        dW1[e], dW3[e] = dW13[:H], dW13[H:]
+        W13t = np.ascontiguousarray(np.concatenate([W1[e], W3[e]], axis=0).T)  # [D, 2H]
+        Bv = _q_weight(W13t, recipe) if fp8 else W13t
+        dXp[r0:r1] = _bf16(_mm(dGUv[r0:r1], Bv))
+    dx = _bf16(orouting.unpermute_unpad(dXp, rt["row_of"], None, T, K))
+    grads = dict(x=dx, weights=dw, w1=dW1.reshape(E * H, D), w2=dW2.reshape(E * H, D),
+                 w3=dW3.reshape(E * H, D))
+    return out, grads
+
+
+def max_rel_err(y, ref) -> float:
+    """max|y - ref| / max|ref| -- the tolerance metric of the path."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.abs(ref).max()
+    if den == 0:
+        return float(np.abs(y).max())
+    return float(np.abs(y - ref).max() / den)

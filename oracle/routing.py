@@ -1,0 +1,126 @@
+"""Numpy restatement of the routing half of the path (test oracle only).
+
+Follows:
+  ``model/moe.py:249-255``  softmax gating: top-k of the logits, softmax over
+                            the K selected logits only.
+  ``model/moe.py:257-265``  sigmoid gating: top-k of sigmoid(logits),
+                            weights / (sum + 1e-8).
+  ``model/moe.py:267-281``  load-balancing loss E * sum_i f_i * P_i.
+  ``model/moe.py:1565-1567`` per-expert token lists in ascending token order
+                            (``nonzero``), which is the stable sort of the
+                            flat (token, slot) assignments by expert.
+
+Spec choices the absent ``fp8_flow_moe`` package would have fixed:
+  * ties in top-k go to the lower expert index;
+  * each expert's group in the permuted buffer is padded to a multiple of
+    128 rows (``PAD``) so no 128-row quantisation block straddles experts;
+    pad rows hold zeros and map to assignment -1.
+
+Pinning (tests/test_oracle_routing.py): brute-force Python loops over
+tokens/experts on small cases; invariants (counts sum to T*K, every
+assignment appears once, rows ascending within an expert, offsets multiples
+of 128); top-1 softmax weights are exactly 1.0 (``model/moe.py:253-254``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+PAD = 128
+
+
+def topk_lower_index(scores: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest per row, descending, ties -> lower index."""
+    order = np.argsort(-scores, axis=-1, kind="stable")
+    return order[:, :k].astype(np.int64)
+
+
+def softmax_topk(logits: np.ndarray, k: int):
+    """model/moe.py:249-255."""
+    logits = np.asarray(logits, dtype=np.float32)
+    idx = topk_lower_index(logits, k)
+    sel = np.take_along_axis(logits, idx, axis=-1).astype(np.float64)
+    e = np.exp(sel - sel.max(axis=-1, keepdims=True))
+    w = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    return w, idx
+
+
+def sigmoid_topk(logits: np.ndarray, k: int):
+    """model/moe.py:257-265 (score bias, if any, is already inside ``logits``)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    s = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))).astype(np.float32)
+    idx = topk_lower_index(s, k)
+    sel = np.take_along_axis(s, idx, axis=-1).astype(np.float64)
+    w = (sel / (sel.sum(axis=-1, keepdims=True) + 1e-8)).astype(np.float32)
+    return w, idx
+
+
+def load_balancing_loss(logits: np.ndarray, idx: np.ndarray, num_experts: int) -> float:
+    """model/moe.py:267-281: f_i counts every one of the K slots, divided by
+    the number of tokens; P_i is the mean softmax over all E experts."""
+    logits = np.asarray(logits, dtype=np.float64).reshape(-1, num_experts)
+    T = logits.shape[0]
+    counts = np.bincount(np.asarray(idx).reshape(-1), minlength=num_experts).astype(np.float64)
+    f = counts / T
+    p = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    p = p / p.sum(axis=-1, keepdims=True)
+    P = p.mean(axis=0)
+    return float(num_experts * (f * P).sum())
+
+
+def sort_assignments(idx: np.ndarray, num_experts: int, pad: int = PAD):
+    """Stable counting sort of the flat assignments a = t*K + k by expert.
+
+    Returns a dict:
+      counts      [E] int32       assignments per expert
+      offsets     [E+1] int32     padded group starts (multiples of ``pad``)
+      row_of      [T*K] int32     padded row of each assignment
+      assign_of_row [offsets[E]] int32  assignment in each row, -1 for pad
+      perm        [T*K] int64     assignments in sorted order (unpadded)
+    """
+    flat = np.asarray(idx, dtype=np.int64).reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= num_experts):
+        raise ValueError("expert index out of range")
+    counts = np.bincount(flat, minlength=num_experts).astype(np.int64)
+    perm = np.argsort(flat, kind="stable")
+    padded = (counts + pad - 1) // pad * pad
+    offsets = np.zeros(num_experts + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(padded)
+    starts = np.zeros(num_experts + 1, dtype=np.int64)
+    starts[1:] = np.cumsum(counts)
+    row_of = np.empty(flat.size, dtype=np.int64)
+    pos = np.arange(flat.size)
+    e_sorted = flat[perm]
+    row_of[perm] = offsets[e_sorted] + (pos - starts[e_sorted])
+    assign_of_row = np.full(int(offsets[-1]), -1, dtype=np.int64)
+    assign_of_row[row_of] = np.arange(flat.size)
+    return dict(
+        counts=counts.astype(np.int32),
+        offsets=offsets.astype(np.int32),
+        row_of=row_of.astype(np.int32),
+        assign_of_row=assign_of_row.astype(np.int32),
+        perm=perm,
+    )
+
+
+def permute_pad(x: np.ndarray, assign_of_row: np.ndarray, top_k: int) -> np.ndarray:
+    """Row r of the output is x[assign_of_row[r] // K], zeros for pad rows."""
+    x = np.asarray(x)
+    out = np.zeros((assign_of_row.size, x.shape[1]), dtype=x.dtype)
+    valid = assign_of_row >= 0
+    out[valid] = x[assign_of_row[valid] // top_k]
+    return out
+
+
+def unpermute_unpad(y: np.ndarray, row_of: np.ndarray, weights, num_tokens: int, top_k: int):
+    """out[t] = sum_k w[t,k] * y[row_of[t*K+k]], summed in fp32 in k order."""
+    y = np.asarray(y, dtype=np.float32)
+    rows = y[np.asarray(row_of).reshape(num_tokens, top_k)]  # [T, K, D]
+    if weights is None:
+        w = np.ones((num_tokens, top_k), dtype=np.float32)
+    else:
+        w = np.asarray(weights, dtype=np.float32).reshape(num_tokens, top_k)
+    acc = np.zeros((num_tokens, y.shape[1]), dtype=np.float32)
+    for k in range(top_k):
+        acc = (acc + (w[:, k : k + 1] * rows[:, k]).astype(np.float32)).astype(np.float32)
+    return acc

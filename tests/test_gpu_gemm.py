@@ -1,0 +1,148 @@
+"""GPU grouped GEMM vs dequantise-then-fp32-matmul on CPU (FP8) and fp32
+matmul of the bf16 operands (BF16), for ragged-M (forward / dgrad) and
+ragged-K (weight gradient) tiles, with zero-token experts and the expert mask."""
+
+import numpy as np
+import pytest
+import torch
+
+import nanopysche_amd as fm
+from nanopysche_amd import _lib
+from nanopysche_amd.flow_moe import ExpertWeights, _gemm_k
+from oracle import fp8 as ofp8
+from oracle.layer import max_rel_err
+from tests.helpers import randn_bf16, zipf_routing
+
+pytestmark = pytest.mark.gpu
+KINDS = {"bf16": _lib.QUANT_BF16, "block": _lib.QUANT_BLOCK, "pow2": _lib.QUANT_POW2, "mx": _lib.QUANT_MX}
+
+
+def _deq_rows(t, kind):
+    if kind == "bf16":
+        return t.float().cpu().numpy()
+    q, s = t.data.cpu().numpy(), t.scale.cpu().numpy()
+    return ofp8.dequant_mx_1x32(q, s) if kind == "mx" else ofp8.dequant_1x128(q, s)
+
+
+def _deq_cols(t, kind):
+    """Transposed operand [C, R] with k-major scales [R/blk, C]."""
+    if kind == "bf16":
+        return t.float().cpu().numpy()
+    q, s = t.data.cpu().numpy(), np.ascontiguousarray(t.scale.cpu().numpy().T)
+    return ofp8.dequant_mx_1x32(q, s) if kind == "mx" else ofp8.dequant_1x128(q, s)
+
+
+def _weight_values(w, kind):
+    """[E*N, K] weights as the GEMM sees them (N rows of each expert, K contiguous)."""
+    wf = w.float().numpy()
+    if kind == "bf16":
+        return ofp8.bf16_round(wf)
+    if kind == "mx":
+        q, c = ofp8.quant_mx_1x32(wf)
+        return ofp8.dequant_mx_1x32(q, c)
+    E_N, K = wf.shape
+    out = np.empty_like(wf)
+    for r0 in range(0, E_N, 128):
+        q, s = ofp8.quant_128x128(wf[r0:r0 + 128], pow2=kind == "pow2")
+        out[r0:r0 + 128] = ofp8.dequant_128x128(q, s)
+    return out
+
+
+@pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
+@pytest.mark.parametrize("E,T,K,zeros", [(4, 2048, 2, ()), (8, 3000, 2, (2, 5))])
+def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros):
+    D, H = 512, 384
+    k = KINDS[kind]
+    x = randn_bf16((T, D), seed=1)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=s, std=0.02) for s in (2, 3, 4))
+    ew = ExpertWeights(k).refresh(w1.to(dev), w2.to(dev), w3.to(dev), E)
+    gran = {"bf16": None, "block": "1x128", "pow2": "1x128", "mx": "1x32"}[kind]
+    pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2")
+    plan = pt.plan
+    gu = fm.fp8_grouped_gemm(pt.rows, ew.w13, plan, out_dtype=torch.float32)
+    offs = plan.offsets.cpu().numpy()
+    a = _deq_rows(pt.rows, kind)
+    W1v = _weight_values(w1, kind).reshape(E, H, D) if kind != "mx" else None
+    if kind == "mx":
+        W13 = torch.cat([w1.view(E, H, D), w3.view(E, H, D)], 1).reshape(E * 2 * H, D)
+        W13v = _weight_values(W13, kind).reshape(E, 2 * H, D)
+    else:
+        W13v = np.concatenate([W1v, _weight_values(w3, kind).reshape(E, H, D)], axis=1)
+    got = gu.cpu().numpy()
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        ref = a[r0:r1] @ W13v[e].T
+        assert max_rel_err(got[r0:r1], ref) < 1e-3, (kind, e)
+    # down projection: K = H, weights = w2_e^T
+    hq = fm.quantize_to_fp8(gu[:, :H].bfloat16(), gran, pow2_scale=kind == "pow2") if gran else gu[:, :H].bfloat16()
+    y = fm.fp8_grouped_gemm(hq, ew.w2t, plan, out_dtype=torch.float32)
+    hv = _deq_rows(hq, kind)
+    W2 = w2.float().numpy().reshape(E, H, D)
+    got = y.cpu().numpy()
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            continue
+        w2t = np.ascontiguousarray(W2[e].T)
+        if kind == "bf16":
+            wv = ofp8.bf16_round(w2t)
+        elif kind == "mx":
+            q, c = ofp8.quant_mx_1x32(w2t)
+            wv = ofp8.dequant_mx_1x32(q, c)
+        else:
+            q, s = ofp8.quant_128x128(w2t, pow2=kind == "pow2")
+            wv = ofp8.dequant_128x128(q, s)
+        ref = hv[r0:r1] @ wv.T
+        assert max_rel_err(got[r0:r1], ref) < 1e-3, (kind, e)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
+def test_ragged_k_weight_grad(dev, kind):
+    E, T, K, D, H = 6, 2500, 2, 256, 256
+    k = KINDS[kind]
+    x = randn_bf16((T, D), seed=5)
+    g = randn_bf16((T, 2 * H), seed=6)
+    _, idx = zipf_routing(T, E, K, 1.2, seed=3, zero_experts=(4,))
+    gran = {"bf16": None, "block": "1x128", "pow2": "1x128", "mx": "1x32"}[kind]
+    px = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True)
+    pg = fm.fused_permute_pad(g.to(dev), px.plan, E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True)
+    plan = px.plan
+    for out_dtype in (torch.float32, torch.bfloat16):
+        dW1 = torch.full((E * H, D), float("nan"), dtype=out_dtype, device=dev)
+        dW3 = torch.full((E * H, D), float("nan"), dtype=out_dtype, device=dev)
+        _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H)
+        av = _deq_cols(pg.rows_t, kind)  # [2H, R]
+        bv = _deq_cols(px.rows_t, kind)  # [D, R]
+        offs = plan.offsets.cpu().numpy()
+        d1 = dW1.float().cpu().numpy().reshape(E, H, D)
+        d3 = dW3.float().cpu().numpy().reshape(E, H, D)
+        tol = 1e-3 if out_dtype == torch.float32 else 8e-3
+        for e in range(E):
+            r0, r1 = offs[e], offs[e + 1]
+            ref = av[:, r0:r1] @ bv[:, r0:r1].T
+            if r1 == r0:
+                assert np.all(d1[e] == 0) and np.all(d3[e] == 0)
+                continue
+            assert max_rel_err(d1[e], ref[:H]) < tol, (kind, e)
+            assert max_rel_err(d3[e], ref[H:]) < tol, (kind, e)
+
+
+def test_expert_mask_skips_tiles(dev):
+    E, T, K, D, H = 4, 1024, 1, 256, 256
+    x = randn_bf16((T, D), seed=1)
+    _, idx = zipf_routing(T, E, K, 0.0, seed=1)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=s, std=0.02) for s in (2, 3, 4))
+    ew = ExpertWeights(_lib.QUANT_BF16).refresh(w1.to(dev), w2.to(dev), w3.to(dev), E)
+    pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=None)
+    mask = torch.tensor([1, 0, 1, 0], dtype=torch.int32, device=dev)
+    out = torch.full((pt.plan.rows_max, 2 * H), 7.0, dtype=torch.float32, device=dev)
+    fm.fp8_grouped_gemm(pt.rows, ew.w13, pt.plan, expert_mask=mask, mask_want=1, out=out)
+    offs = pt.plan.offsets.cpu().numpy()
+    o = out.cpu().numpy()
+    assert np.all(o[offs[1]:offs[2]] == 7.0) and np.all(o[offs[3]:offs[4]] == 7.0)
+    assert not np.all(o[offs[0]:offs[1]] == 7.0)

@@ -1,0 +1,126 @@
+"""Expert block forward + backward on the GPU against the CPU oracles:
+FP8 recipes within 2e-2 (max|err| / max|ref|) of the dequantise-then-fp32
+flow, BF16 within 1e-2 of the reference's per-expert loop
+(model/moe.py:1542-1596)."""
+
+import pytest
+import torch
+
+import nanopysche_amd as fm
+from oracle import layer as olayer
+from oracle import routing as orouting
+from tests.helpers import randn_bf16, zipf_routing
+
+pytestmark = pytest.mark.gpu
+
+FP8_TOL = 2e-2
+BF16_TOL = 1e-2
+
+
+def _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold, param_dtype=torch.bfloat16):
+    H = w1.shape[0] // E
+    D = x.shape[1]
+    rt = fm.FP8RecipeType(recipe)
+    cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, rt))
+    blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=threshold)
+    p = [t.to(dev).to(param_dtype).requires_grad_(True) for t in (w1, w2, w3)]
+    blk.set_weights(*p)
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    out = blk(xd, wd, idx.to(dev), 0, E)
+    out.backward(go.to(dev))
+    torch.cuda.synchronize()
+    grads = dict(x=xd.grad, weights=wd.grad, w1=p[0].grad, w2=p[1].grad, w3=p[2].grad)
+    return out, grads
+
+
+def _case(T, D, H, E, K, seed, skew=0.0, zeros=()):
+    x = randn_bf16((T, D), seed=seed)
+    w, idx = zipf_routing(T, E, K, skew, seed=seed + 1, zero_experts=zeros)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=seed + s, std=0.02) for s in (2, 3, 4))
+    go = randn_bf16((T, D), seed=seed + 5, std=1e-2)
+    return x, w, idx, w1, w2, w3, go
+
+
+def _check(out, grads, ref_out, ref_grads, tol, label):
+    e = olayer.max_rel_err(out.float().cpu().numpy(), ref_out)
+    assert e <= tol, f"{label}: forward {e}"
+    for name in ("x", "weights", "w1", "w2", "w3"):
+        r = ref_grads[name]
+        r = r.numpy() if torch.is_tensor(r) else r
+        e = olayer.max_rel_err(grads[name].float().cpu().numpy(), r)
+        assert e <= tol, f"{label}: grad {name} {e}"
+
+
+@pytest.mark.parametrize("recipe", ["blockwise", "flow_moe", "mxfp8"])
+@pytest.mark.parametrize("shape", [(512, 256, 256, 4, 2, 0.0, ()), (700, 384, 256, 8, 2, 1.2, (1, 6))])
+def test_fp8_block_matches_flow_oracle(dev, recipe, shape):
+    T, D, H, E, K, skew, zeros = shape
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=T, skew=skew, zeros=zeros)
+    out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold=0)
+    ref_out, ref_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=recipe)
+    _check(out, grads, ref_out, ref_grads, FP8_TOL, recipe)
+
+
+@pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float32])
+def test_bf16_block_matches_reference_loop(dev, param_dtype):
+    T, D, H, E, K = 600, 256, 384, 4, 2
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=3, skew=1.0, zeros=(2,))
+    out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, "none", threshold=0, param_dtype=param_dtype)
+    ref_out, ref_grads = olayer.moe_bf16_loop(x, w, idx, w1, w2, w3, E, go)
+    _check(out, grads, ref_out.numpy(), ref_grads, BF16_TOL, "bf16")
+    assert grads["w1"].dtype == param_dtype
+
+
+def test_threshold_mixed_fp8_and_bf16(dev):
+    """Experts with >= threshold assignments take FP8, the rest BF16."""
+    T, D, H, E, K = 1024, 256, 256, 4, 1
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=9)
+    idx = torch.tensor([0] * 600 + [1] * 300 + [2] * 124, dtype=torch.int64).reshape(T, 1)
+    out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, "flow_moe", threshold=400)
+    f_out, f_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe="flow_moe")
+    b_out, b_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=None)
+    o = out.float().cpu().numpy()
+    fp8_rows = (idx[:, 0] == 0).numpy()
+    assert olayer.max_rel_err(o[fp8_rows], f_out[fp8_rows]) <= FP8_TOL
+    assert olayer.max_rel_err(o[~fp8_rows], b_out[~fp8_rows]) <= BF16_TOL
+    # expert 0 weight grads follow the FP8 flow, expert 1-2 the BF16 flow, expert 3 is zero
+    g1 = grads["w1"].float().cpu().numpy().reshape(E, H, D)
+    assert olayer.max_rel_err(g1[0], f_grads["w1"].reshape(E, H, D)[0]) <= FP8_TOL
+    assert olayer.max_rel_err(g1[1], b_grads["w1"].reshape(E, H, D)[1]) <= BF16_TOL
+    assert (g1[3] == 0).all()
+
+
+def test_drop_in_call_convention(dev):
+    """The reference call: compute(x, weights, indices, 0, E) with [B, S, *] shapes."""
+    B, S, D, H, E, K = 2, 64, 256, 256, 4, 2
+    x = randn_bf16((B, S, D), seed=4)
+    logits = torch.randn(B, S, E, generator=torch.Generator().manual_seed(0))
+    w, idx = orouting.softmax_topk(logits.reshape(-1, E).numpy(), K)
+    w = torch.from_numpy(w).reshape(B, S, K)
+    idx = torch.from_numpy(idx).reshape(B, S, K)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=s, std=0.02) for s in (2, 3, 4))
+    from fp8_flow_moe import FP8FlowMoECompute, FP8FlowMoEConfig, FP8RecipeConfig, FP8RecipeType
+
+    cfg = FP8FlowMoEConfig(enabled=True, fp8_recipe=FP8RecipeConfig(enabled=True, recipe_type=FP8RecipeType("flow_moe")))
+    blk = FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=0)
+    blk.set_weights(w1.to(dev), w2.to(dev), w3.to(dev))
+    out = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
+    assert out.shape == (B, S, D) and out.dtype == torch.bfloat16
+    ref, _ = olayer.moe_flow_reference(x.reshape(-1, D), w.reshape(-1, K), idx.reshape(-1, K), w1, w2, w3, E,
+                                       recipe="flow_moe")
+    assert olayer.max_rel_err(out.reshape(-1, D).float().cpu().numpy(), ref) <= FP8_TOL
+
+
+def test_weight_cache_tracks_parameter_updates(dev):
+    T, D, H, E, K = 256, 256, 256, 2, 1
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=1)
+    cfg = fm.FP8FlowMoEConfig(True, fm.FP8RecipeConfig(True, fm.FP8RecipeType.FLOW_MOE))
+    blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=0)
+    p = [t.to(dev) for t in (w1, w2, w3)]
+    blk.set_weights(*p)
+    a = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
+    with torch.no_grad():
+        p[1].mul_(2.0)  # in-place update bumps _version
+    b = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
+    assert torch.allclose(b.float(), 2 * a.float(), rtol=2e-2, atol=1e-3)

@@ -1,0 +1,150 @@
+"""GPU parity of the quantisation kernels against the CPU oracle: payload
+bytes and scales bit-exact (BASELINE config 2 shapes and edge cases)."""
+
+import numpy as np
+import pytest
+import torch
+
+import nanopysche_amd as fm
+from oracle import fp8 as ofp8
+from tests.helpers import randn_bf16
+
+pytestmark = pytest.mark.gpu
+G = fm.BlockScalingGranularity
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _edge_matrix():
+    """256 x 512 bf16 with zero blocks, ties, saturation-adjacent values, subnormals."""
+    x = randn_bf16((256, 512), seed=11).float()
+    x[0:2, 0:128] = 0.0                      # all-zero 1x128 blocks
+    x[2, 0:128] = 0.0
+    x[2, 5] = 448.0                          # amax exactly 448 -> scale 1
+    x[2, 6] = 464.0 * (448.0 / 448.0) / 2    # an exact half-way value after scaling
+    x[3, 0:128] = 2.0 ** -20                 # tiny block (amax below the 1e-12 floor? no: 9.5e-7)
+    x[4, 0:128] = 1e-13                      # below the amax floor -> payload rounds to 0
+    x[5, 128:256] = torch.linspace(-3, 3, 128)
+    x[6, 256:384] = -7.0                     # constant block
+    x[7, 384:512] = torch.arange(128).float() * 2 ** -12  # e4m3-subnormal range after scaling
+    x[8:128, 0:128] = 0.0                    # a whole 128x128 tile of zeros
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_quant_1x128_config2_bitexact(dev, pow2):
+    x = randn_bf16((8192, 4096), seed=1, outlier_frac=0.001)
+    q = fm.quantize_to_fp8(x.to(dev), G.ROW_1x128, pow2_scale=pow2)
+    rq, rs = ofp8.quant_1x128(x.float().numpy(), pow2=pow2)
+    assert np.array_equal(_np(q.scale), rs)
+    assert np.array_equal(_np(q.data), rq)
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_fused_row_col_bitexact(dev, pow2):
+    x = randn_bf16((2048, 1024), seed=1, outlier_frac=0.001)
+    row, col = fm.quantize_to_fp8(x.to(dev), G.ROW_1x128, pow2_scale=pow2, return_transpose=True)
+    rq, rs = ofp8.quant_1x128(x.float().numpy(), pow2=pow2)
+    assert np.array_equal(_np(row.data), rq) and np.array_equal(_np(row.scale), rs)
+    if pow2:
+        cq, cs = ofp8.scaling_aware_transpose(rq, rs)
+    else:
+        cq, cs = ofp8.quant_128x1(x.float().numpy())
+    assert np.array_equal(_np(col.scale), cs)
+    assert np.array_equal(_np(col.data), cq)
+
+
+def test_edge_blocks_bitexact(dev):
+    x = _edge_matrix()
+    for pow2 in (False, True):
+        row, col = fm.quantize_to_fp8(x.to(dev), pow2_scale=pow2, return_transpose=True)
+        rq, rs = ofp8.quant_1x128(x.float().numpy(), pow2=pow2)
+        assert np.array_equal(_np(row.data), rq) and np.array_equal(_np(row.scale), rs)
+        cq, cs = (ofp8.scaling_aware_transpose(rq, rs) if pow2 else ofp8.quant_128x1(x.float().numpy()))
+        assert np.array_equal(_np(col.data), cq) and np.array_equal(_np(col.scale), cs)
+    mq = fm.quantize_to_fp8(x.to(dev), G.MX_1x32)
+    oq, oc = ofp8.quant_mx_1x32(x.float().numpy())
+    assert np.array_equal(_np(mq.data), oq) and np.array_equal(_np(mq.scale), oc)
+
+
+def test_fp32_input_and_ragged_rows(dev):
+    x = randn_bf16((333, 256), seed=5).float() * 3.7  # rows not a multiple of 128
+    q = fm.quantize_to_fp8(x.to(dev))
+    rq, rs = ofp8.quant_1x128(x.numpy())
+    assert np.array_equal(_np(q.data), rq) and np.array_equal(_np(q.scale), rs)
+    mq = fm.quantize_to_fp8(x.to(dev), G.MX_1x32)
+    oq, oc = ofp8.quant_mx_1x32(x.numpy())
+    assert np.array_equal(_np(mq.data), oq) and np.array_equal(_np(mq.scale), oc)
+
+
+def test_mx_1x32_and_32x1_bitexact(dev):
+    x = randn_bf16((1024, 2048), seed=4, outlier_frac=0.001)
+    row, col = fm.quantize_to_fp8(x.to(dev), G.MX_1x32, return_transpose=True)
+    oq, oc = ofp8.quant_mx_1x32(x.float().numpy())
+    tq, tc = ofp8.quant_mx_32x1(x.float().numpy())
+    assert np.array_equal(_np(row.data), oq) and np.array_equal(_np(row.scale), oc)
+    assert np.array_equal(_np(col.data), tq) and np.array_equal(_np(col.scale), tc)
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_weight_128x128_config2_bitexact(dev, pow2):
+    w = randn_bf16((14336, 4096), seed=1, std=0.02)
+    q = fm.quantize_to_fp8(w.to(dev), G.BLOCK_128x128, pow2_scale=pow2)
+    rq, rs = ofp8.quant_128x128(w.float().numpy(), pow2=pow2)
+    assert np.array_equal(_np(q.scale), rs)
+    assert np.array_equal(_np(q.data), rq)
+
+
+def test_dequantize_bitexact(dev):
+    x = randn_bf16((1024, 1024), seed=3, outlier_frac=0.001)
+    xd = x.to(dev)
+    row, col = fm.quantize_to_fp8(xd, return_transpose=True)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        d = fm.dequantize_from_fp8(row, out_dtype)
+        ref = ofp8.dequant_1x128(_np(row.data), _np(row.scale))
+        if out_dtype == torch.bfloat16:
+            ref = ofp8.bf16_round(ref)
+        assert np.array_equal(d.float().cpu().numpy(), ref)
+        dc = fm.dequantize_from_fp8(col, out_dtype)
+        refc = ofp8.dequant_1x128(_np(col.data), np.ascontiguousarray(_np(col.scale).T))
+        if out_dtype == torch.bfloat16:
+            refc = ofp8.bf16_round(refc)
+        assert np.array_equal(dc.float().cpu().numpy(), refc)
+    w = fm.quantize_to_fp8(xd, G.BLOCK_128x128)
+    assert np.array_equal(fm.dequantize_from_fp8(w, torch.float32).cpu().numpy(),
+                          ofp8.dequant_128x128(_np(w.data), _np(w.scale)))
+    m = fm.quantize_to_fp8(xd, G.MX_1x32)
+    assert np.array_equal(fm.dequantize_from_fp8(m, torch.float32).cpu().numpy(),
+                          ofp8.dequant_mx_1x32(_np(m.data), _np(m.scale)))
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_scaling_aware_transpose_bitexact(dev, pow2):
+    x = randn_bf16((8192, 4096), seed=1, outlier_frac=0.001)
+    row = fm.quantize_to_fp8(x.to(dev), pow2_scale=pow2)
+    t = fm.scaling_aware_transpose(row)
+    cq, cs = ofp8.scaling_aware_transpose(_np(row.data), _np(row.scale))
+    assert np.array_equal(_np(t.scale), cs)
+    assert np.array_equal(_np(t.data), cq)
+
+
+def test_scaling_aware_transpose_exact_for_pow2(dev):
+    """Size-independent property at full size: with power-of-two scales the
+    transpose preserves every dequantised value outside the e4m3 subnormal range."""
+    x = randn_bf16((8192, 4096), seed=1, outlier_frac=0.001).to(dev)
+    row = fm.quantize_to_fp8(x, pow2_scale=True)
+    t = fm.scaling_aware_transpose(row)
+    a = fm.dequantize_from_fp8(row, torch.float32).T
+    b = fm.dequantize_from_fp8(t, torch.float32)
+    q = t.data
+    normal = ((q & 0x7F) >> 3) > 0
+    assert torch.equal(a[normal], b[normal])
+
+
+def test_rejects_bad_shapes(dev):
+    with pytest.raises((RuntimeError, ValueError)):
+        fm.quantize_to_fp8(torch.zeros(128, 100, dtype=torch.bfloat16, device=dev))
+    with pytest.raises((RuntimeError, ValueError)):
+        fm.quantize_to_fp8(torch.zeros(100, 128, dtype=torch.bfloat16, device=dev), return_transpose=True)
