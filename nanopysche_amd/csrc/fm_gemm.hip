@@ -223,12 +223,16 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
+            // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in
+            // bytes 0-15 and K [32+16h, 32+16h+16) in bytes 16-31, so bytes
+            // 0-15 of both halves form the first 32-deep scale block (scale
+            // from lane `row`) and bytes 16-31 the second (lane `row + 32`).
             const int ra = wi * 64 + t * 32 + lrow, rb = wj * 64 + t * 32 + lrow;
-            const int c0 = ks * 4 + lhalf * 2;
+            const int c0 = ks * 4 + lhalf, c1 = c0 + 2;
             const uint4 a0 = *reinterpret_cast<const uint4*>(lq + lds_off(ra, c0));
-            const uint4 a1 = *reinterpret_cast<const uint4*>(lq + lds_off(ra, c0 + 1));
+            const uint4 a1 = *reinterpret_cast<const uint4*>(lq + lds_off(ra, c1));
             const uint4 b0 = *reinterpret_cast<const uint4*>(lp + lds_off(rb, c0));
-            const uint4 b1 = *reinterpret_cast<const uint4*>(lp + lds_off(rb, c0 + 1));
+            const uint4 b1 = *reinterpret_cast<const uint4*>(lp + lds_off(rb, c1));
             fa[ks][t] = v8i{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
             fb[ks][t] = v8i{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
           }

@@ -312,12 +312,13 @@ struct GatherSrc {
 
 // ------------------------------------------------------------ unpermute ----
 // grid-stride over (token, 8-column chunk); K rows summed in slot order
-// with separately rounded multiply and add (no fused multiply-add), one
-// rounding to the output dtype at the end.
+// with separately rounded multiply and add (contraction into FMA is switched
+// off for this kernel), one rounding to the output dtype at the end.
 __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64_t ld_y,
                                                         const int32_t* row_of, const float* w,
                                                         int64_t T, int K, int64_t D,
                                                         void* out, int out_f32, int64_t ld_out) {
+#pragma clang fp contract(off)
   const int64_t chunks = D / 8;
   const int64_t n = T * chunks;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
@@ -333,8 +334,8 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64
       const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        acc[2 * j] = __fadd_rn(acc[2 * j], __fmul_rn(s, u2f(q[j] << 16)));
-        acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], __fmul_rn(s, u2f(q[j] & 0xffff0000u)));
+        acc[2 * j] = acc[2 * j] + s * u2f(q[j] << 16);
+        acc[2 * j + 1] = acc[2 * j + 1] + s * u2f(q[j] & 0xffff0000u);
       }
     }
     if (out_f32) {

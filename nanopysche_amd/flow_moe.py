@@ -570,6 +570,10 @@ class FP8FlowMoECompute:
             self.fp8_gemm_threshold = 1 << 62  # no FP8 recipe: every expert on BF16
         self._w = None
         self._cache = {}
+        # When set to a dict, forward stores the bf16 gate|up GEMM output
+        # ("gate_up") and backward the bf16 dH GEMM output ("dh"), [rows_max, *];
+        # used by parity tests to feed a CPU oracle the device's own GEMM results.
+        self.capture_intermediates = None
 
     def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
         for w in (w1, w2, w3):
@@ -645,6 +649,8 @@ class FP8FlowMoECompute:
             hrow, _ = _wrap(q, s, None, None, kind)
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
         out = fused_unpermute_unpad(Y, plan, wts)
+        if self.capture_intermediates is not None:
+            self.capture_intermediates["gate_up"] = GU.detach().clone()
         ctx.compute = self
         ctx.plan = plan
         ctx.kinds = (fp8_kind, use_bf16)
@@ -684,6 +690,8 @@ class FP8FlowMoECompute:
                                    return_transpose=True, weights=wts)
             _gemm_m(kind, pt.rows, ew.w2, plan, dH, mask, want)
             dy[kind] = pt.rows_t
+        if self.capture_intermediates is not None:
+            self.capture_intermediates["dh"] = dH.detach().clone()
         for kind, want in runs:
             ew = self._weights(kind)
             gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev)

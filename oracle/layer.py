@@ -81,7 +81,7 @@ def _q_rows(a, recipe):
     return ofp8.dequant_1x128(q, s)
 
 
-def _q_cols(a, recipe, rowq_of_a=None):
+def _q_cols(a, recipe):
     """Column-quantised transpose of a [R, C] -> dequantised [C, R].
 
     blockwise / mxfp8 quantise the source directly; flow_moe re-expresses the
@@ -118,8 +118,15 @@ def _silu(g):
 
 
 def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=None,
-                       recipe="flow_moe"):
+                       recipe="flow_moe", taps=None):
     """The HIP path's dataflow on CPU.  recipe in {None, 'blockwise', 'flow_moe', 'mxfp8'}.
+
+    ``taps`` (optional) holds the device's own bf16 GEMM outputs ``gate_up``
+    [rows, 2H] and ``dh`` [rows, H] of the padded buffer; when given they
+    replace the oracle's gate|up and dH products, so every quantiser
+    downstream sees the same input as on the device (stage-synchronised
+    parity: the gfx950 FP8 MFMA sums with ~1e-5 relative error, which
+    otherwise flips block scales of the following quantisation).
 
     Returns (out [T, D] f32 (bf16-valued), grads dict or None)."""
     E = num_experts
@@ -139,7 +146,6 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
     Xv = _q_rows(Xp, recipe) if fp8 else Xp
     GU = np.zeros((Mp, 2 * H), np.float32)
     Y = np.zeros((Mp, D), np.float32)
-    Hv_all = np.zeros((Mp, H), np.float32)
     for e in range(E):
         r0, r1 = offs[e], offs[e + 1]
         if r1 == r0:
@@ -147,6 +153,8 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         W13 = np.concatenate([W1[e], W3[e]], axis=0)
         Bv = _q_weight(W13, recipe) if fp8 else W13
         GU[r0:r1] = _bf16(_mm(Xv[r0:r1], Bv))
+    if taps is not None and "gate_up" in taps:
+        GU = _bf16(np.asarray(taps["gate_up"], dtype=np.float32)[:Mp])
     g, u = GU[:, :H], GU[:, H:]
     h = (_silu(g) * u).astype(np.float32)
     Hv = _q_rows(h, recipe) if fp8 else _bf16(h)
@@ -182,6 +190,8 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
             continue
         Bv = _q_weight(W2[e], recipe) if fp8 else W2[e]      # [H, D]
         dH[r0:r1] = _bf16(_mm(dYv[r0:r1], Bv))
+    if taps is not None and "dh" in taps:
+        dH = _bf16(np.asarray(taps["dh"], dtype=np.float32)[:Mp])
     sg = (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
     dg = (dH * u * sg * (1.0 + g * (1.0 - sg))).astype(np.float32)
     du = (dH * (g * sg)).astype(np.float32)

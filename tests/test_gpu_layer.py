@@ -17,12 +17,14 @@ FP8_TOL = 2e-2
 BF16_TOL = 1e-2
 
 
-def _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold, param_dtype=torch.bfloat16):
+def _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold, param_dtype=torch.bfloat16,
+         taps=None):
     H = w1.shape[0] // E
     D = x.shape[1]
     rt = fm.FP8RecipeType(recipe)
     cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, rt))
     blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=threshold)
+    blk.capture_intermediates = taps
     p = [t.to(dev).to(param_dtype).requires_grad_(True) for t in (w1, w2, w3)]
     blk.set_weights(*p)
     xd = x.to(dev).requires_grad_(True)
@@ -43,7 +45,7 @@ def _case(T, D, H, E, K, seed, skew=0.0, zeros=()):
 
 
 def _check(out, grads, ref_out, ref_grads, tol, label):
-    e = olayer.max_rel_err(out.float().cpu().numpy(), ref_out)
+    e = olayer.max_rel_err(out.detach().float().cpu().numpy(), ref_out)
     assert e <= tol, f"{label}: forward {e}"
     for name in ("x", "weights", "w1", "w2", "w3"):
         r = ref_grads[name]
@@ -55,11 +57,32 @@ def _check(out, grads, ref_out, ref_grads, tol, label):
 @pytest.mark.parametrize("recipe", ["blockwise", "flow_moe", "mxfp8"])
 @pytest.mark.parametrize("shape", [(512, 256, 256, 4, 2, 0.0, ()), (700, 384, 256, 8, 2, 1.2, (1, 6))])
 def test_fp8_block_matches_flow_oracle(dev, recipe, shape):
+    """Stage-synchronised: the oracle takes the device's bf16 gate|up and dH
+    GEMM outputs, so every quantiser sees identical inputs; what remains is the
+    FP8 MFMA's own summation error (~1e-5 relative)."""
     T, D, H, E, K, skew, zeros = shape
     x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=T, skew=skew, zeros=zeros)
+    taps = {}
+    out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold=0, taps=taps)
+    taps = {k: v.float().cpu().numpy() for k, v in taps.items()}
+    ref_out, ref_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=recipe, taps=taps)
+    _check(out, grads, ref_out, ref_grads, FP8_TOL, recipe)
+
+
+@pytest.mark.parametrize("recipe", ["blockwise", "flow_moe", "mxfp8"])
+def test_fp8_block_free_running(dev, recipe):
+    """End-to-end against the independent oracle with no shared intermediates,
+    at >= 1024 assignments per expert: max-rel within 2e-2 and mean relative
+    error within 5e-3 for the output and every gradient."""
+    T, D, H, E, K = 2048, 512, 256, 4, 2
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=17)
     out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold=0)
     ref_out, ref_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=recipe)
     _check(out, grads, ref_out, ref_grads, FP8_TOL, recipe)
+    pairs = [(out.detach(), ref_out)] + [(grads[k], ref_grads[k]) for k in ("x", "weights", "w1", "w2", "w3")]
+    for got, ref in pairs:
+        g = got.float().cpu().numpy()
+        assert abs(g - ref).mean() <= 5e-3 * abs(ref).mean()
 
 
 @pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float32])
@@ -80,7 +103,7 @@ def test_threshold_mixed_fp8_and_bf16(dev):
     out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, "flow_moe", threshold=400)
     f_out, f_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe="flow_moe")
     b_out, b_grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=None)
-    o = out.float().cpu().numpy()
+    o = out.detach().float().cpu().numpy()
     fp8_rows = (idx[:, 0] == 0).numpy()
     assert olayer.max_rel_err(o[fp8_rows], f_out[fp8_rows]) <= FP8_TOL
     assert olayer.max_rel_err(o[~fp8_rows], b_out[~fp8_rows]) <= BF16_TOL
@@ -109,7 +132,7 @@ def test_drop_in_call_convention(dev):
     assert out.shape == (B, S, D) and out.dtype == torch.bfloat16
     ref, _ = olayer.moe_flow_reference(x.reshape(-1, D), w.reshape(-1, K), idx.reshape(-1, K), w1, w2, w3, E,
                                        recipe="flow_moe")
-    assert olayer.max_rel_err(out.reshape(-1, D).float().cpu().numpy(), ref) <= FP8_TOL
+    assert olayer.max_rel_err(out.detach().reshape(-1, D).float().cpu().numpy(), ref) <= FP8_TOL
 
 
 def test_weight_cache_tracks_parameter_updates(dev):

@@ -1,0 +1,127 @@
+"""Pins the routing oracle (oracle/routing.py): against the reference's own
+torch op sequences (model/moe.py:249-281, :1565-1567, :1594) and brute-force
+Python loops on small inputs."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import routing as orouting
+from tests.helpers import zipf_routing
+
+
+def test_softmax_topk_matches_reference_ops():
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(2, 300, 8, generator=g)
+    vals, idx = logits.topk(2, dim=-1)            # model/moe.py:253
+    w = F.softmax(vals, dim=-1)                   # model/moe.py:254
+    ow, oidx = orouting.softmax_topk(logits.reshape(-1, 8).numpy(), 2)
+    assert np.array_equal(oidx, idx.reshape(-1, 2).numpy())
+    assert np.allclose(ow, w.reshape(-1, 2).numpy(), rtol=1e-6, atol=1e-7)
+    w1, _ = orouting.softmax_topk(logits.reshape(-1, 8).numpy(), 1)
+    assert np.all(w1 == 1.0)
+
+
+def test_sigmoid_topk_matches_reference_ops():
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(500, 64, generator=g) * 3
+    s = torch.sigmoid(logits)                     # model/moe.py:260
+    vals, idx = s.topk(6, dim=-1)                 # model/moe.py:261
+    w = vals / (vals.sum(dim=-1, keepdim=True) + 1e-8)  # model/moe.py:263
+    ow, oidx = orouting.sigmoid_topk(logits.numpy(), 6)
+    assert np.array_equal(oidx, idx.numpy())
+    assert np.allclose(ow, w.numpy(), rtol=1e-6, atol=1e-7)
+
+
+def test_load_balancing_loss_matches_reference_ops():
+    g = torch.Generator().manual_seed(2)
+    E, K = 8, 2
+    logits = torch.randn(2, 256, E, generator=g)
+    _, idx = logits.topk(K, dim=-1)
+    # model/moe.py:274-281
+    num_tokens = logits.shape[0] * logits.shape[1]
+    expert_mask = F.one_hot(idx, E).sum(dim=2)
+    f = expert_mask.float().sum(dim=[0, 1]) / num_tokens
+    P = F.softmax(logits, dim=-1).float().mean(dim=[0, 1])
+    ref = float(E * (f * P).sum())
+    got = orouting.load_balancing_loss(logits.numpy(), idx.numpy(), E)
+    assert abs(got - ref) < 1e-6
+
+
+def _brute_force_sort(idx, E, pad=128):
+    T, K = idx.shape
+    counts = [0] * E
+    rows = {}
+    off = 0
+    offsets = []
+    for e in range(E):
+        offsets.append(off)
+        r = off
+        for t in range(T):
+            for k in range(K):
+                if idx[t, k] == e:
+                    rows[t * K + k] = r
+                    r += 1
+                    counts[e] += 1
+        off += -(-counts[e] // pad) * pad
+    offsets.append(off)
+    return counts, offsets, [rows[a] for a in range(T * K)]
+
+
+@pytest.mark.parametrize("T,E,K,s,zeros", [(300, 4, 1, 0.0, ()), (257, 8, 2, 1.1, (3,)),
+                                           (100, 32, 8, 1.2, (0, 1, 31)), (1, 1, 1, 0.0, ())])
+def test_sort_matches_brute_force(T, E, K, s, zeros):
+    _, idx = zipf_routing(T, E, K, s, seed=T, zero_experts=zeros)
+    idx = idx.numpy()
+    r = orouting.sort_assignments(idx, E)
+    counts, offsets, rows = _brute_force_sort(idx, E)
+    assert r["counts"].tolist() == counts
+    assert r["offsets"].tolist() == offsets
+    assert r["row_of"].tolist() == rows
+    aor = r["assign_of_row"]
+    assert sorted(aor[aor >= 0].tolist()) == list(range(T * K))
+    assert (aor[np.asarray(rows)] == np.arange(T * K)).all()
+
+
+def test_sort_order_equals_reference_nonzero():
+    """model/moe.py:1566-1567: the tokens of expert e, ascending."""
+    _, idx = zipf_routing(500, 8, 2, 0.5, seed=3)
+    r = orouting.sort_assignments(idx.numpy(), 8)
+    for e in range(8):
+        ref = (idx == e).any(dim=-1).nonzero(as_tuple=True)[0].numpy()
+        a = r["assign_of_row"][r["offsets"][e]: r["offsets"][e] + r["counts"][e]]
+        assert np.array_equal(a // 2, ref)
+
+
+def test_sort_duplicate_expert_in_one_token():
+    idx = np.array([[1, 1], [0, 1]])
+    r = orouting.sort_assignments(idx, 2)
+    assert r["counts"].tolist() == [1, 3]
+    assert r["row_of"].tolist() == [128, 129, 0, 130]
+
+
+def test_permute_and_unpermute_brute_force():
+    rng = np.random.default_rng(0)
+    T, E, K, D = 50, 4, 2, 16
+    w, idx = zipf_routing(T, E, K, 0.0, seed=5)
+    r = orouting.sort_assignments(idx.numpy(), E)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    p = orouting.permute_pad(x, r["assign_of_row"], K)
+    for row, a in enumerate(r["assign_of_row"]):
+        assert np.array_equal(p[row], x[a // K] if a >= 0 else np.zeros(D, np.float32))
+    y = rng.standard_normal((p.shape[0], D)).astype(np.float32)
+    out = orouting.unpermute_unpad(y, r["row_of"], w.numpy(), T, K)
+    for t in range(T):
+        acc = np.zeros(D, np.float32)
+        for k in range(K):
+            acc = (acc + np.float32(w[t, k]) * y[r["row_of"][t * K + k]]).astype(np.float32)
+        assert np.array_equal(out[t], acc)
+    # the reference's combine: output[token_ids] += w * expert_out, per expert (model/moe.py:1594)
+    ref = torch.zeros(T, D)
+    for e in range(E):
+        tok = (idx == e).any(-1).nonzero(as_tuple=True)[0]
+        pw = (w[tok] * (idx[tok] == e).float()).sum(-1)
+        rows = [r["row_of"][t * K + int((idx[t] == e).nonzero()[0])] for t in tok.tolist()]
+        ref[tok] += pw[:, None] * torch.from_numpy(y[rows])
+    assert np.allclose(out, ref.numpy(), rtol=1e-6, atol=1e-6)
