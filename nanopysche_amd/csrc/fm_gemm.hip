@@ -86,217 +86,344 @@ __device__ __forceinline__ uint32_t scale_e8m0(const Operand& o, int64_t g, int6
   return static_cast<const uint8_t*>(o.s)[g * o.s_gs + (row >> o.s_shift) * o.s_row + kb * o.s_kb];
 }
 
+// LDS-DMA: the 64 lanes' `size`-byte loads land at consecutive LDS addresses
+// starting at `lds` (wave-uniform); `g` is each lane's own global source.
+// Issued from inline assembly so the compiler's wait insertion does not treat
+// them as pending LDS writes (it would wait for every prefetch in flight before
+// each LDS read); the kernel orders them with explicit vmcnt waits instead.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(size_t((__attribute__((address_space(3))) const void*)(p)));
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written here and nowhere else
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits [3:0] and [15:14],
+// expcnt [6:4] left at its maximum, lgkmcnt [11:8]).  Draining lgkmcnt too
+// means this wave's LDS reads of a stage have returned before the barrier that
+// allows the stage to be refilled.
+#define FM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
+
+constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
+constexpr int kBJ = 128;   // workgroup tile along j (tokens / N)
+
+template <int KIND>
+struct GemmSmem {
+  static constexpr bool kScaled = KIND != GK_BF16;
+  static constexpr int kQ = kBI * 128;                 // operand bytes per stage
+  static constexpr int kP = kBJ * 128;
+  static constexpr int kQS = kScaled ? kBI * 4 : 0;   // scale bytes per stage
+  static constexpr int kPS = kScaled ? kBJ * 4 : 0;
+  static constexpr int kStage = kQ + kP + kQS + kPS;
+};
+
+// Per-lane DMA sources of one workgroup tile.
+struct TileSrc {
+  const uint8_t* q[8];   // 8 x 1 KiB of the 256-row operand per wave
+  const uint8_t* p[4];   // 4 x 1 KiB of the 128-row operand per wave
+  const uint8_t* qs;     // scale word of this lane (Q side)
+  const uint8_t* ps;     // scale word of this lane (P side; lanes 0-31)
+  int64_t qs_k, ps_k;    // scale byte advance per K step
+};
+
+template <int KIND>
+__device__ __forceinline__ void gemm_issue(const TileSrc& src, int64_t k, uint8_t* stage, int wave,
+                                           int lane) {
+  using SM = GemmSmem<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const int64_t kb = k * ES;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) dma16(src.q[u] + kb, stage + (wave * 8 + u) * 1024);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16(src.p[u] + kb, stage + SM::kQ + (wave * 4 + u) * 1024);
+  if (SM::kScaled) {
+    const int64_t ks = k / KSTEP;
+    dma4(src.qs + ks * src.qs_k, stage + SM::kQ + SM::kP + wave * 256);
+    if (lane < 32) dma4(src.ps + ks * src.ps_k, stage + SM::kQ + SM::kP + SM::kQS + wave * 128);
+  }
+}
+
+// One 128-byte K step from a stage: 4 x 2 MFMA 32x32 blocks per wave.
+template <int KIND, int MODE>
+__device__ __forceinline__ void gemm_compute(const uint8_t* st, v16f (&acc)[4][2], int wi, int wj,
+                                             int lrow, int lhalf, bool q_mx_k, bool p_mx_k) {
+  using SM = GemmSmem<KIND>;
+  const uint8_t* lq = st;
+  const uint8_t* lp = st + SM::kQ;
+  const float* qs = reinterpret_cast<const float*>(st + SM::kQ + SM::kP);
+  const float* ps = reinterpret_cast<const float*>(st + SM::kQ + SM::kP + SM::kQS);
+  const uint8_t* qs8 = st + SM::kQ + SM::kP;
+  const uint8_t* ps8 = st + SM::kQ + SM::kP + SM::kQS;
+  if (KIND == GK_BF16) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      v8bf fa[4], fb[2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        fa[t] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + t * 32 + lrow, ks * 2 + lhalf)));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        fb[t] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + t * 32 + lrow, ks * 2 + lhalf)));
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    }
+    return;
+  }
+  // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in bytes 0-15 and
+  // K [32+16h, +16) in bytes 16-31, so bytes 0-15 of both halves form the first
+  // 32-deep scale block (scale from lane `row`) and bytes 16-31 the second
+  // (scale from lane `row + 32`).
+  v8i fa[2][4], fb[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c0 = ks * 4 + lhalf, c1 = c0 + 2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = wi * 128 + t * 32 + lrow;
+      const uint4 x0 = *reinterpret_cast<const uint4*>(lq + lds_off(r, c0));
+      const uint4 x1 = *reinterpret_cast<const uint4*>(lq + lds_off(r, c1));
+      fa[ks][t] = v8i{int(x0.x), int(x0.y), int(x0.z), int(x0.w), int(x1.x), int(x1.y), int(x1.z), int(x1.w)};
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wj * 64 + t * 32 + lrow;
+      const uint4 x0 = *reinterpret_cast<const uint4*>(lp + lds_off(r, c0));
+      const uint4 x1 = *reinterpret_cast<const uint4*>(lp + lds_off(r, c1));
+      fb[ks][t] = v8i{int(x0.x), int(x0.y), int(x0.z), int(x0.w), int(x1.x), int(x1.y), int(x1.z), int(x1.w)};
+    }
+  }
+  if (KIND == GK_FP8_F32) {
+    // 128-deep partial sums, promoted with the product of the block scales
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        v16f part;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[r] = 0.f;
+        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[0][a], fb[0][b], part, 0, 0, 0, 127, 0, 127);
+        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[1][a], fb[1][b], part, 0, 0, 0, 127, 0, 127);
+        const float sp = ps[wj * 64 + b * 32 + lrow];
+        if (MODE == GM_RAGGED_M) {
+          const float sc = qs[wi * 128] * sp;  // a wave's 128 rows are one 128x128 weight block
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[a][b][r] += part[r] * sc;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int ii = wi * 128 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+            acc[a][b][r] += part[r] * (qs[ii] * sp);
+          }
+        }
+      }
+    return;
+  }
+  int sa[2][4], sb[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int blk = ks * 2 + lhalf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = wi * 128 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) sa[ks][t] = int((f2u(qs[r]) >> 23) & 0xffu);
+      else sa[ks][t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wj * 64 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) sb[ks][t] = int((f2u(ps[r]) >> 23) & 0xffu);
+      else sb[ks][t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[ks][a], fb[ks][b], acc[a][b], 0, 0,
+                                                                   0, sa[ks][a], 0, sb[ks][b]);
+}
+
 template <int KIND, int MODE>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
+  using SM = GemmSmem<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
-  constexpr int KSTEP = 128 / ES;                     // elements per K step
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][128 * 128];  // [stage][Q,P]
-  __shared__ float s_lds[2][2][128];                  // fp32 / pow2 scales per row
-  __shared__ uint32_t mx_lds[2][2][128];              // 4 e8m0 codes per row per K step
+  constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
+  constexpr bool SCALED = SM::kScaled;
+  constexpr int NLOAD = 12 + (SCALED ? 2 : 0);        // DMA instructions per wave per step
+  // three pipeline stages as separate arrays: the compiler's alias analysis then
+  // knows a DMA into one stage never feeds the LDS reads of another and inserts
+  // no vector-memory wait in front of those reads
+  __shared__ __attribute__((aligned(1024))) uint8_t smem0[SM::kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem1[SM::kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem2[SM::kStage];
 
   // ---------------------------------------------------------- tile decode ----
   const int64_t per_xcd = (p.n_tiles + 7) / 8;
   const int64_t L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (L >= p.n_tiles) return;
   int64_t e, i0, j0, k_lo, k_hi;
-  {
-    const int64_t NI = p.n_i / 128;
-    if (MODE == GM_RAGGED_M) {
-      const int64_t MT = p.m_tiles;
-      const int64_t group = L / (kGroupM * NI);
-      const int64_t first = group * kGroupM;
-      const int64_t gsz = MT - first < kGroupM ? MT - first : kGroupM;
-      const int64_t mt = first + (L % gsz);
-      const int64_t nt = (L % (kGroupM * NI)) / gsz;
-      e = p.tile_expert[mt];
-      if (e < 0) return;
-      j0 = mt * 128;
-      i0 = nt * 128;
-      k_lo = 0;
-      k_hi = p.K;
-    } else {
-      const int64_t NJ = p.n_j / 128;
-      const int64_t per_e = NI * NJ;
-      e = L / per_e;
-      const int64_t Lr = L % per_e;
-      const int64_t group = Lr / (kGroupM * NJ);
-      const int64_t first = group * kGroupM;
-      const int64_t gsz = NI - first < kGroupM ? NI - first : kGroupM;
-      i0 = (first + (Lr % gsz)) * 128;
-      j0 = ((Lr % (kGroupM * NJ)) / gsz) * 128;
-      k_lo = p.offsets[e];
-      k_hi = p.offsets[e + 1];
-    }
+  const int64_t NI = (p.n_i + kBI - 1) / kBI;
+  if (MODE == GM_RAGGED_M) {
+    const int64_t MT = p.m_tiles;
+    const int64_t group = L / (kGroupM * NI);
+    const int64_t first = group * kGroupM;
+    const int64_t gsz = MT - first < kGroupM ? MT - first : kGroupM;
+    const int64_t mt = first + (L % gsz);
+    const int64_t nt = (L % (kGroupM * NI)) / gsz;
+    e = p.tile_expert[mt];
+    if (e < 0) return;
+    j0 = mt * kBJ;
+    i0 = nt * kBI;
+    k_lo = 0;
+    k_hi = p.K;
+  } else {
+    const int64_t NJ = p.n_j / kBJ;
+    const int64_t per_e = NI * NJ;
+    e = L / per_e;
+    const int64_t Lr = L % per_e;
+    const int64_t group = Lr / (kGroupM * NJ);
+    const int64_t first = group * kGroupM;
+    const int64_t gsz = NI - first < kGroupM ? NI - first : kGroupM;
+    i0 = (first + (Lr % gsz)) * kBI;
+    j0 = ((Lr % (kGroupM * NJ)) / gsz) * kBJ;
+    k_lo = p.offsets[e];
+    k_hi = p.offsets[e + 1];
   }
   if (p.mask != nullptr && p.mask[e] != p.mask_want) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wi = wave >> 1, wj = wave & 1;
-
-  // ---------------------------------------------------- global load setup ----
+  const int wi = wave >> 1, wj = wave & 1;   // wave tile: i [128*wi, +128), j [64*wj, +64)
+  const int lrow = lane & 31, lhalf = lane >> 5;
   const int64_t q_group = MODE == GM_RAGGED_M ? e : 0;
-  const uint8_t* qbase = p.Q.p + (q_group * p.Q.gs) * ES;
-  const uint8_t* pbase = p.P.p;
-  uint4 rq[4], rp[4];
-  float sq_reg = 0.f, sp_reg = 0.f;
-  uint32_t mq_reg = 0, mp_reg = 0;
-  const int srow = tid & 127;
-  const bool s_is_q = tid < 128;
+  const int64_t i_last = p.n_i - 1;
 
-  auto gload = [&](int64_t k) {
+  // ------------------------------------------------ per-lane DMA sources ----
+  // Linear LDS chunk c = 64*instr + lane of a tile of 128-byte rows holds row
+  // c/8, swizzled chunk (c%8) ^ (row%8); each lane fetches the global 16 bytes
+  // that belong there.  Rows past the end of Q (an N tail) re-read the last row.
+  TileSrc src;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int id = tid + 256 * u;
-      const int row = id >> 3, c = id & 7;
-      rq[u] = *reinterpret_cast<const uint4*>(qbase + ((i0 + row) * p.Q.ld + k) * ES + c * 16);
-      rp[u] = *reinterpret_cast<const uint4*>(pbase + ((j0 + row) * p.P.ld + k) * ES + c * 16);
-    }
-    if (KIND == GK_FP8_F32 || KIND == GK_FP8_POW2) {
-      const int64_t kb = k >> 7;
-      if (s_is_q) sq_reg = scale_f32(p.Q, q_group, i0 + srow, kb);
-      else sp_reg = scale_f32(p.P, 0, j0 + srow, kb);
-    } else if (KIND == GK_FP8_MX) {
-      const int64_t kb = k >> 5;
-      const Operand& o = s_is_q ? p.Q : p.P;
-      const int64_t g = s_is_q ? q_group : 0;
-      const int64_t row = (s_is_q ? i0 : j0) + srow;
-      uint32_t w = 0;
+  for (int u = 0; u < 8; ++u) {
+    const int c = (wave * 8 + u) * 64 + lane;
+    const int row = c >> 3, ch = (c & 7) ^ (row & 7);
+    int64_t gr = i0 + row;
+    gr = gr < i_last ? gr : i_last;
+    src.q[u] = p.Q.p + (q_group * p.Q.gs + gr * p.Q.ld) * ES + ch * 16;
+  }
 #pragma unroll
-      for (int b = 0; b < 4; ++b) w |= scale_e8m0(o, g, row, kb + b) << (8 * b);
-      if (s_is_q) mq_reg = w; else mp_reg = w;
+  for (int u = 0; u < 4; ++u) {
+    const int c = (wave * 4 + u) * 64 + lane;
+    const int row = c >> 3, ch = (c & 7) ^ (row & 7);
+    src.p[u] = p.P.p + ((j0 + row) * p.P.ld) * ES + ch * 16;
+  }
+  // Scales: Q one row per lane (256 rows), P one row per lane of lanes 0-31
+  // (128 rows).  MX scales in k-major layout pack four consecutive rows of one
+  // 32-block per lane instead ([block][row] bytes in LDS).
+  const bool q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
+  const bool p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
+  src.qs = src.ps = nullptr;
+  src.qs_k = src.ps_k = 0;
+  if (SCALED) {
+    const int qi = wave * 64 + lane;           // 0..255
+    const int pi = wave * 32 + (lane & 31);    // 0..127
+    const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
+    if (q_mx_k) {
+      const int b = (qi * 4) / kBI, row = (qi * 4) % kBI;
+      int64_t gr = i0 + row;
+      gr = gr + 3 <= i_last ? gr : i_last - 3;  // n_i is a multiple of 128
+      src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + gr * p.Q.s_row + b * p.Q.s_kb);
+    } else {
+      int64_t gr = i0 + qi;
+      gr = gr < i_last ? gr : i_last;
+      src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * sbytes;
     }
-  };
-  auto lstore = [&](int st) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int id = tid + 256 * u;
-      const int row = id >> 3, c = id & 7;
-      *reinterpret_cast<uint4*>(&lds[st][0][lds_off(row, c)]) = rq[u];
-      *reinterpret_cast<uint4*>(&lds[st][1][lds_off(row, c)]) = rp[u];
+    if (p_mx_k) {
+      const int b = (pi * 4) / kBJ, row = (pi * 4) % kBJ;
+      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + row) * p.P.s_row + b * p.P.s_kb);
+    } else {
+      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + pi) >> p.P.s_shift) * p.P.s_row * sbytes;
     }
-    if (KIND == GK_FP8_F32 || KIND == GK_FP8_POW2) {
-      if (s_is_q) s_lds[st][0][srow] = sq_reg; else s_lds[st][1][srow] = sp_reg;
-    } else if (KIND == GK_FP8_MX) {
-      if (s_is_q) mx_lds[st][0][srow] = mq_reg; else mx_lds[st][1][srow] = mp_reg;
-    }
-  };
+    // per K step: one 128-block (fp32 / pow2 scales) or four 32-blocks (MX)
+    src.qs_k = (KIND == GK_FP8_MX ? 4 : 1) * p.Q.s_kb * sbytes;
+    src.ps_k = (KIND == GK_FP8_MX ? 4 : 1) * p.P.s_kb * sbytes;
+  }
 
-  v16f acc[2][2];
+  v16f acc[4][2];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  const int lrow = lane & 31, lhalf = lane >> 5;
-  if (k_lo < k_hi) {
-    gload(k_lo);
-    lstore(0);
-    __syncthreads();
-    int st = 0;
-    for (int64_t k = k_lo; k < k_hi; k += KSTEP) {
-      const bool more = k + KSTEP < k_hi;
-      if (more) gload(k + KSTEP);
-      const uint8_t* lq = lds[st][0];
-      const uint8_t* lp = lds[st][1];
-      if (KIND == GK_BF16) {
+  // Pipeline: stage t % 3 is filled two steps ahead.  Readiness of a stage is
+  // this wave's own vmcnt wait (DMA writes land in LDS before the counter
+  // drops) followed by a barrier; a stage is refilled only after every wave has
+  // passed the barrier that follows its last read of it.  The barrier carries
+  // no memory fence, which would wait for the prefetches still in flight.
+  const int64_t nk = (k_hi - k_lo) / KSTEP;
+  if (nk > 0) gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
+  if (nk > 1) gemm_issue<KIND>(src, k_lo + KSTEP, smem1, wave, lane);
+  // Main loop: steps with a successor, whose loads are always in flight here,
+  // so an unconditional vmcnt(NLOAD) retires exactly the current stage's DMA
+  // (the compiler's wait tracking follows it and adds no wait of its own as
+  // long as every body issues the same loads).
+  int64_t t = 0;
+  while (t + 1 < nk) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          v8bf fa[2], fb[2];
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const uint4 xa = *reinterpret_cast<const uint4*>(lq + lds_off(wi * 64 + t * 32 + lrow, ks * 2 + lhalf));
-            const uint4 xb = *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + t * 32 + lrow, ks * 2 + lhalf));
-            fa[t] = __builtin_bit_cast(v8bf, xa);
-            fb[t] = __builtin_bit_cast(v8bf, xb);
-          }
-#pragma unroll
-          for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-        }
-      } else {
-        v8i fa[2][2], fb[2][2];  // [ks][t]
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in
-            // bytes 0-15 and K [32+16h, 32+16h+16) in bytes 16-31, so bytes
-            // 0-15 of both halves form the first 32-deep scale block (scale
-            // from lane `row`) and bytes 16-31 the second (lane `row + 32`).
-            const int ra = wi * 64 + t * 32 + lrow, rb = wj * 64 + t * 32 + lrow;
-            const int c0 = ks * 4 + lhalf, c1 = c0 + 2;
-            const uint4 a0 = *reinterpret_cast<const uint4*>(lq + lds_off(ra, c0));
-            const uint4 a1 = *reinterpret_cast<const uint4*>(lq + lds_off(ra, c1));
-            const uint4 b0 = *reinterpret_cast<const uint4*>(lp + lds_off(rb, c0));
-            const uint4 b1 = *reinterpret_cast<const uint4*>(lp + lds_off(rb, c1));
-            fa[ks][t] = v8i{int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-            fb[ks][t] = v8i{int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-          }
-        if (KIND == GK_FP8_F32) {
-          // partial sums over this 128-deep block, then promote with the scales
-#pragma unroll
-          for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-              v16f part;
-#pragma unroll
-              for (int r = 0; r < 16; ++r) part[r] = 0.f;
-              part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[0][a], fb[0][b], part, 0, 0, 0, 127, 0, 127);
-              part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[1][a], fb[1][b], part, 0, 0, 0, 127, 0, 127);
-              const float sp = s_lds[st][1][wj * 64 + b * 32 + lrow];
-              if (MODE == GM_RAGGED_M) {
-                const float s = s_lds[st][0][0] * sp;  // weight block scale is uniform
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][b][r] += part[r] * s;
-              } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                  const int ii = wi * 64 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                  acc[a][b][r] += part[r] * (s_lds[st][0][ii] * sp);
-                }
-              }
-            }
-        } else {
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-              for (int b = 0; b < 2; ++b) {
-                int sa, sb;
-                if (KIND == GK_FP8_POW2) {
-                  sa = int((f2u(s_lds[st][0][wi * 64 + a * 32 + lrow]) >> 23) & 0xffu);
-                  sb = int((f2u(s_lds[st][1][wj * 64 + b * 32 + lrow]) >> 23) & 0xffu);
-                } else {
-                  const int sh = 8 * (ks * 2 + lhalf);
-                  sa = int((mx_lds[st][0][wi * 64 + a * 32 + lrow] >> sh) & 0xffu);
-                  sb = int((mx_lds[st][1][wj * 64 + b * 32 + lrow] >> sh) & 0xffu);
-                }
-                acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                    fa[ks][a], fb[ks][b], acc[a][b], 0, 0, 0, sa, 0, sb);
-              }
-        }
-      }
-      if (more) lstore(st ^ 1);
-      __syncthreads();
-      st ^= 1;
+    for (int u = 0; u < 3; ++u) {
+      if (t + 1 >= nk) break;
+      FM_WAIT_VMCNT(NLOAD);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      uint8_t* nxt = u == 0 ? smem2 : (u == 1 ? smem0 : smem1);
+      const uint8_t* cur = u == 0 ? smem0 : (u == 1 ? smem1 : smem2);
+      // unconditional (keeps the compiler's wait tracking exact): at t = nk-2
+      // this re-reads step nk-1 into the stage of step nk, which is never read
+      const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
+      gemm_issue<KIND>(src, k_lo + tn * KSTEP, nxt, wave, lane);
+      gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
+      ++t;
     }
+  }
+  if (t < nk) {  // last step: nothing else in flight
+    FM_WAIT_VMCNT(0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const int sidx = int(t % 3);
+    const uint8_t* cur = sidx == 0 ? smem0 : (sidx == 1 ? smem1 : smem2);
+    gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
   }
 
   // -------------------------------------------------------------- epilogue ----
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int64_t j = j0 + wj * 64 + b * 32 + lrow;
       if (MODE == GM_RAGGED_M) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int64_t i = i0 + wi * 64 + a * 32 + 8 * q + 4 * lhalf;
+          const int64_t i = i0 + wi * 128 + a * 32 + 8 * q + 4 * lhalf;
+          if (i >= p.n_i) continue;
           if (p.out_f32) {
             float* dst = static_cast<float*>(p.C) + j * p.ldC + i;
             *reinterpret_cast<float4*>(dst) =
@@ -312,7 +439,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t i = i0 + wi * 64 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          const int64_t i = i0 + wi * 128 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          if (i >= p.n_i) continue;
           const bool second = i >= p.split;
           const int64_t row = second ? i - p.split : i;
           const int64_t off = e * (second ? p.c2_gs : p.c_gs) + row * p.ldC + j;
@@ -392,7 +520,7 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   p.ldC = ld_out;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
   p.split = INT64_MAX;
-  p.n_tiles = m_tiles * (N / 128);
+  p.n_tiles = m_tiles * ((N + kBI - 1) / kBI);
   return dispatch_gemm<GM_RAGGED_M>(kind, p, static_cast<hipStream_t>(stream));
 }
 
@@ -428,7 +556,7 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
   p.c2_gs = out2_gs;
   p.split = split_rows >= M ? INT64_MAX : split_rows;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
-  p.n_tiles = int64_t(E) * (M / 128) * (N / 128);
+  p.n_tiles = int64_t(E) * ((M + kBI - 1) / kBI) * (N / kBJ);
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
 }
 
