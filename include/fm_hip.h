@@ -55,6 +55,12 @@ const char* fm_version(void);
  * exported so tests can check it against other implementations. */
 void fm_host_encode_e4m3(const float* in, uint8_t* out, int64_t n);
 void fm_host_decode_e4m3(const uint8_t* in, float* out, int64_t n);
+/* Device conversion check: x [n] fp32 (n % 4 == 0) encoded to e4m3 (after a
+ * clamp to +-448) and to bf16 by the gfx950 convert instructions (*_hw) and by
+ * the integer routines (*_sw).  The kernels use the hardware path; a GPU test
+ * asserts the two agree bit for bit. */
+int fm_convert_check(const float* x, int64_t n, void* e4m3_hw, void* e4m3_sw, void* bf16_hw,
+                     void* bf16_sw, void* stream);
 
 /* ------------------------------------------------------- quantisation ---- */
 /* Replaces fp8_flow_moe.quantize_to_fp8 for activations (1x128 / MX 1x32 row
@@ -133,10 +139,13 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
  * the gather + pad of model/moe.py:1571,1577-1580: row r of the padded buffer
  * is x[assign_of_row[r] / K] (times weights[assign_of_row[r]] if weights !=
  * NULL), zeros on pad rows, written as `kind` with optional transposed output
- * (same layout rules as fm_quantize). */
+ * (same layout rules as fm_quantize).  tile_valid (optional, e.g. the
+ * tile_expert map of fm_route_sort): 128-row tiles t with tile_valid[t] < 0 are
+ * not written. */
 int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,
                int64_t rows, int K, const float* weights, int kind, void* q, int64_t ld_q, void* s,
-               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream);
+               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
+               const int32_t* tile_valid, void* stream);
 
 /* Replaces fp8_flow_moe.fused_unpermute_unpad (reference fp8/__init__.py:20)
  * and the weighted scatter-add of model/moe.py:1594:
@@ -158,15 +167,17 @@ int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_
  * h = silu(g) * u from bf16 g, u, emitted as `kind` (fm_quantize layouts). */
 int fm_swiglu_quantize(const void* g, int64_t ld_g, const void* u, int64_t ld_u, int64_t rows,
                        int64_t H, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt,
-                       int64_t ld_qt, void* st, int64_t ld_st, void* stream);
+                       int64_t ld_qt, void* st, int64_t ld_st, const int32_t* tile_valid,
+                       void* stream);
 
 /* Backward of SwiGLU (autograd of model/moe.py:1590 in the reference):
  * [dg | du] with dg = dh*u*s*(1+g*(1-s)), du = dh*g*s, s = sigmoid(g), as a
- * [rows, 2H] operand emitted as `kind`. */
+ * [rows, 2H] operand emitted as `kind` (one read of g, u, dh per element).
+ * tile_valid as for fm_permute. */
 int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u, const void* dh,
                        int64_t ld_dh, int64_t rows, int64_t H, int kind, void* q, int64_t ld_q,
                        void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
-                       void* stream);
+                       const int32_t* tile_valid, void* stream);
 
 /* ------------------------------------------------------- grouped GEMM ---- */
 /* One operand of the grouped GEMM: K-contiguous rows.  Scale of (row, kb) is

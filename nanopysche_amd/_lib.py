@@ -54,6 +54,7 @@ SIGNATURES = {
     "fm_version": (C.c_char_p, []),
     "fm_host_encode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_host_decode_e4m3": (None, [_vp, _vp, _i64]),
+    "fm_convert_check": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "fm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,
                            _vp, _i64, _vp]),
     "fm_quantize_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _i64,
@@ -70,13 +71,13 @@ SIGNATURES = {
     "fm_route_sort": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp]),
     "fm_permute": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _vp, _i64, _vp, _i64,
-                          _vp, _i64, _vp, _i64, _vp]),
+                          _vp, _i64, _vp, _i64, _vp, _vp]),
     "fm_unpermute": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i32, _i64, _vp]),
     "fm_router_weight_grad": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _vp, _vp]),
     "fm_swiglu_quantize": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp,
-                                  _i64, _vp, _i64, _vp]),
+                                  _i64, _vp, _i64, _vp, _vp]),
     "fm_swiglu_backward": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp,
-                                  _i64, _vp, _i64, _vp, _i64, _vp]),
+                                  _i64, _vp, _i64, _vp, _i64, _vp, _vp]),
     "fm_grouped_gemm_ragged_m": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _i32, _i64, _i64, _vp, _i32,
                                         _vp, _i32, _i64, _vp]),
     "fm_grouped_gemm_ragged_k": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,

@@ -89,6 +89,22 @@ FM_HD float block_scale(float amax, bool pow2) {
 
 FM_HD uint8_t quant_e4m3(float x, float scale) { return f32_to_e4m3(clamp448(x / scale)); }
 
+// gfx950 v_cvt_pk_fp8_f32 (OCP e4m3fn, round-to-nearest-even) on four values
+// already clamped to +-448; byte i of the result encodes value i.  The GPU test
+// test_gpu_quant.py::test_hw_convert_matches_software checks it against the
+// integer routine above.
+__device__ __forceinline__ uint32_t hw_e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return uint32_t(w);
+}
+// gfx950 v_cvt_pk_bf16_f32 (round-to-nearest-even): low half = a.
+__device__ __forceinline__ uint32_t hw_bf16x2(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // MX shared-exponent code of a block with this amax.
 FM_HD uint32_t mx_code(float amax) {
   int e = int((f2u(amax) >> 23) & 0xffu) - 8;

@@ -24,11 +24,10 @@
 //              promotion.
 //   FP8_MX     e4m3 with e8m0 scales per 32 (OCP MXFP8), same instruction.
 //
-// Tiling: 256 threads = 4 wave64 as 2 (i) x 2 (j); workgroup tile 128 x 128,
-// K step 128 bytes (128 e4m3 / 64 bf16); each wave owns 64 x 64 = 2 x 2 MFMA
-// 32x32 blocks.  Operands are double-buffered in LDS (2 x 2 x 16 KiB), rows of
-// 128 bytes with the 16-byte chunk index XOR-swizzled by (row % 8) so both the
-// 16-byte stores and the MFMA fragment reads are bank-conflict free.
+// Tiling: 256 threads = 4 wave64 as 2 (i) x 2 (j); workgroup tile 256 (i) x
+// 128 (j), each wave 128 x 64 = 4 x 2 MFMA 32x32 blocks; K step 128 bytes
+// (128 e4m3 / 64 bf16).  Operands and scales stream into a 3-stage LDS ring by
+// direct global->LDS loads (see grouped_gemm_kernel).
 // Workgroup ids are remapped so each XCD walks a contiguous range of tiles,
 // grouped 8 m-tiles at a time for L2 reuse of weights and activations.
 #include "fm_common.h"
@@ -37,6 +36,7 @@
 namespace fm {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
@@ -75,8 +75,13 @@ struct GemmParams {
 
 constexpr int kGroupM = 8;
 
+// 16-byte chunk `chunk` of 128-byte row `row` of an operand tile in LDS.  The
+// chunk index is XOR-swizzled with (row / 2) % 8: a ds_read_b128 serves 16
+// lanes per pass from 64 four-byte banks (two 128-byte rows), and the 16 rows
+// those lanes touch then fall on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_swz(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * 128 + ((chunk ^ (row & 7)) << 4);
+  return row * 128 + ((chunk ^ lds_swz(row)) << 4);
 }
 
 __device__ __forceinline__ float scale_f32(const Operand& o, int64_t g, int64_t row, int64_t kb) {
@@ -121,7 +126,7 @@ struct GemmSmem {
   static constexpr int kQ = kBI * 128;                 // operand bytes per stage
   static constexpr int kP = kBJ * 128;
   static constexpr int kQS = kScaled ? kBI * 4 : 0;   // scale bytes per stage
-  static constexpr int kPS = kScaled ? kBJ * 4 : 0;
+  static constexpr int kPS = kScaled ? kBI * 4 : 0;  // 256 slots, the upper 128 unused
   static constexpr int kStage = kQ + kP + kQS + kPS;
 };
 
@@ -130,7 +135,7 @@ struct TileSrc {
   const uint8_t* q[8];   // 8 x 1 KiB of the 256-row operand per wave
   const uint8_t* p[4];   // 4 x 1 KiB of the 128-row operand per wave
   const uint8_t* qs;     // scale word of this lane (Q side)
-  const uint8_t* ps;     // scale word of this lane (P side; lanes 0-31)
+  const uint8_t* ps;     // scale word of this lane (P side; rows past 128 re-read row 127)
   int64_t qs_k, ps_k;    // scale byte advance per K step
 };
 
@@ -148,7 +153,7 @@ __device__ __forceinline__ void gemm_issue(const TileSrc& src, int64_t k, uint8_
   if (SM::kScaled) {
     const int64_t ks = k / KSTEP;
     dma4(src.qs + ks * src.qs_k, stage + SM::kQ + SM::kP + wave * 256);
-    if (lane < 32) dma4(src.ps + ks * src.ps_k, stage + SM::kQ + SM::kP + SM::kQS + wave * 128);
+    dma4(src.ps + ks * src.ps_k, stage + SM::kQ + SM::kP + SM::kQS + wave * 256);
   }
 }
 
@@ -259,6 +264,199 @@ __device__ __forceinline__ void gemm_compute(const uint8_t* st, v16f (&acc)[4][2
                                                                    0, sa[ks][a], 0, sb[ks][b]);
 }
 
+// Register fragments for one half of a 128-byte K step: for e4m3 one 64-deep
+// MFMA K slice (4 A + 2 B fragments of 32 bytes per lane, plus their e8m0
+// scale operands), for bf16 two 16-deep slices.
+template <int KIND>
+struct HalfFrag {
+  v8i a[4], b[2];
+  int sa[4], sb[2];
+};
+template <>
+struct HalfFrag<GK_BF16> {
+  v8bf a[2][4], b[2][2];
+};
+
+// Loads half `half` (0 or 1) of the K step held in stage `st`.
+template <int KIND>
+__device__ __forceinline__ void load_half(const uint8_t* st, int half, HalfFrag<KIND>& f, int wi, int wj,
+                                          int lrow, int lhalf, bool q_mx_k, bool p_mx_k) {
+  using SM = GemmSmem<KIND>;
+  const uint8_t* lq = st;
+  const uint8_t* lp = st + SM::kQ;
+  if constexpr (KIND == GK_BF16) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int ks = half * 2 + s2;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        f.a[s2][t] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + t * 32 + lrow, ks * 2 + lhalf)));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        f.b[s2][t] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + t * 32 + lrow, ks * 2 + lhalf)));
+    }
+  } else {
+    // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in bytes 0-15
+    // and K [32+16h, +16) in bytes 16-31; bytes 0-15 of both halves form the
+    // first 32-deep scale block (scale from lane `row`), bytes 16-31 the second
+    // (scale from lane `row + 32`).
+    const int c0 = half * 4 + lhalf, c1 = c0 + 2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = wi * 128 + t * 32 + lrow;
+      const v4i x0 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c0));
+      const v4i x1 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c1));
+      f.a[t] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wj * 64 + t * 32 + lrow;
+      const v4i x0 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c0));
+      const v4i x1 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c1));
+      f.b[t] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    const float* qs = reinterpret_cast<const float*>(st + SM::kQ + SM::kP);
+    const float* ps = reinterpret_cast<const float*>(st + SM::kQ + SM::kP + SM::kQS);
+    const uint8_t* qs8 = st + SM::kQ + SM::kP;
+    const uint8_t* ps8 = st + SM::kQ + SM::kP + SM::kQS;
+    const int blk = half * 2 + lhalf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = wi * 128 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) f.sa[t] = int((f2u(qs[r]) >> 23) & 0xffu);
+      else f.sa[t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wj * 64 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) f.sb[t] = int((f2u(ps[r]) >> 23) & 0xffu);
+      else f.sb[t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
+    }
+  }
+}
+
+template <int KIND>
+__device__ __forceinline__ void mma_half(const HalfFrag<KIND>& f, v16f (&acc)[4][2]) {
+  if constexpr (KIND == GK_BF16) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][a], f.b[s2][b], acc[a][b], 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[a], f.b[b], acc[a][b], 0, 0, 0,
+                                                                   f.sa[a], 0, f.sb[b]);
+  }
+}
+
+// Phase C/D of the pipelined loop: refills stage `cur` with K step `k` (the 14
+// DMA instructions of gemm_issue) and loads half 0 of the next step from
+// `nxt`, two DMAs per group of fragment reads.  The DMAs are inline assembly
+// with a memory clobber, so they keep this program order relative to the LDS
+// reads, and the MFMA interleave pattern of the caller spreads both between
+// the MFMAs instead of queueing all DMAs ahead of them.
+template <int KIND>
+__device__ __forceinline__ void refill_and_load_half0(const TileSrc& src, int64_t k, uint8_t* cur,
+                                                      const uint8_t* nxt, HalfFrag<KIND>& f, int wave,
+                                                      int lane, int wi, int wj, int lrow, int lhalf,
+                                                      bool q_mx_k, bool p_mx_k) {
+  using SM = GemmSmem<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const int64_t kb = k * ES;
+  const uint8_t* lq = nxt;
+  const uint8_t* lp = nxt + SM::kQ;
+  if constexpr (KIND == GK_BF16) {
+    // half 0 = substeps 0 and 1: A fragments t = 0..3, B fragments t = 0..1
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      dma16(src.q[2 * u] + kb, cur + (wave * 8 + 2 * u) * 1024);
+      dma16(src.q[2 * u + 1] + kb, cur + (wave * 8 + 2 * u + 1) * 1024);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        f.a[s2][u] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + u * 32 + lrow, s2 * 2 + lhalf)));
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma16(src.p[2 * u] + kb, cur + SM::kQ + (wave * 4 + 2 * u) * 1024);
+      dma16(src.p[2 * u + 1] + kb, cur + SM::kQ + (wave * 4 + 2 * u + 1) * 1024);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        f.b[s2][u] = __builtin_bit_cast(
+            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + u * 32 + lrow, s2 * 2 + lhalf)));
+    }
+  } else {
+    const int c0 = lhalf, c1 = c0 + 2;  // half 0
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      dma16(src.q[2 * u] + kb, cur + (wave * 8 + 2 * u) * 1024);
+      dma16(src.q[2 * u + 1] + kb, cur + (wave * 8 + 2 * u + 1) * 1024);
+      const int r = wi * 128 + u * 32 + lrow;
+      const v4i x0 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c0));
+      const v4i x1 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c1));
+      f.a[u] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma16(src.p[2 * u] + kb, cur + SM::kQ + (wave * 4 + 2 * u) * 1024);
+      dma16(src.p[2 * u + 1] + kb, cur + SM::kQ + (wave * 4 + 2 * u + 1) * 1024);
+      const int r = wj * 64 + u * 32 + lrow;
+      const v4i x0 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c0));
+      const v4i x1 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c1));
+      f.b[u] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    const int64_t ks = k / KSTEP;
+    dma4(src.qs + ks * src.qs_k, cur + SM::kQ + SM::kP + wave * 256);
+    dma4(src.ps + ks * src.ps_k, cur + SM::kQ + SM::kP + SM::kQS + wave * 256);
+    const float* qs = reinterpret_cast<const float*>(nxt + SM::kQ + SM::kP);
+    const float* ps = reinterpret_cast<const float*>(nxt + SM::kQ + SM::kP + SM::kQS);
+    const uint8_t* qs8 = nxt + SM::kQ + SM::kP;
+    const uint8_t* ps8 = nxt + SM::kQ + SM::kP + SM::kQS;
+    const int blk = lhalf;  // half 0
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = wi * 128 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) f.sa[t] = int((f2u(qs[r]) >> 23) & 0xffu);
+      else f.sa[t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wj * 64 + t * 32 + lrow;
+      if (KIND == GK_FP8_POW2) f.sb[t] = int((f2u(ps[r]) >> 23) & 0xffu);
+      else f.sb[t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
+    }
+  }
+}
+
+// Scheduling pattern for one half step: each MFMA is followed by LDS reads of
+// the next fragments, so the MFMA pipe never waits for operands and the reads
+// hide behind the MFMAs (8 x 64-cycle e4m3 MFMAs, or 16 x bf16 MFMAs).
+template <int KIND>
+__device__ __forceinline__ void interleave_mfma_lds() {
+  constexpr int kMfma = KIND == GK_BF16 ? 16 : 8;
+  constexpr int kReads = KIND == GK_BF16 ? 1 : 2;
+#pragma unroll
+  for (int i = 0; i < kMfma; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // LDS reads
+  }
+}
+
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int KIND, int MODE>
 __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
   using SM = GemmSmem<KIND>;
@@ -266,12 +464,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
   constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
   constexpr bool SCALED = SM::kScaled;
   constexpr int NLOAD = 12 + (SCALED ? 2 : 0);        // DMA instructions per wave per step
-  // three pipeline stages as separate arrays: the compiler's alias analysis then
-  // knows a DMA into one stage never feeds the LDS reads of another and inserts
-  // no vector-memory wait in front of those reads
-  __shared__ __attribute__((aligned(1024))) uint8_t smem0[SM::kStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t smem1[SM::kStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t smem2[SM::kStage];
+  // three pipeline stages of one K step each (operands + scales)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * SM::kStage];
+  uint8_t* const smem0 = smem;
+  uint8_t* const smem1 = smem + SM::kStage;
+  uint8_t* const smem2 = smem + 2 * SM::kStage;
 
   // ---------------------------------------------------------- tile decode ----
   const int64_t per_xcd = (p.n_tiles + 7) / 8;
@@ -315,13 +512,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
 
   // ------------------------------------------------ per-lane DMA sources ----
   // Linear LDS chunk c = 64*instr + lane of a tile of 128-byte rows holds row
-  // c/8, swizzled chunk (c%8) ^ (row%8); each lane fetches the global 16 bytes
-  // that belong there.  Rows past the end of Q (an N tail) re-read the last row.
+  // c/8, swizzled chunk (c%8) ^ lds_swz(row); each lane fetches the global 16
+  // bytes that belong there.  Rows past the end of Q (an N tail) re-read the last row.
   TileSrc src;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int c = (wave * 8 + u) * 64 + lane;
-    const int row = c >> 3, ch = (c & 7) ^ (row & 7);
+    const int row = c >> 3, ch = (c & 7) ^ lds_swz(row);
     int64_t gr = i0 + row;
     gr = gr < i_last ? gr : i_last;
     src.q[u] = p.Q.p + (q_group * p.Q.gs + gr * p.Q.ld) * ES + ch * 16;
@@ -329,19 +526,20 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int c = (wave * 4 + u) * 64 + lane;
-    const int row = c >> 3, ch = (c & 7) ^ (row & 7);
+    const int row = c >> 3, ch = (c & 7) ^ lds_swz(row);
     src.p[u] = p.P.p + ((j0 + row) * p.P.ld) * ES + ch * 16;
   }
-  // Scales: Q one row per lane (256 rows), P one row per lane of lanes 0-31
-  // (128 rows).  MX scales in k-major layout pack four consecutive rows of one
-  // 32-block per lane instead ([block][row] bytes in LDS).
+  // Scales: one row per lane, Q 256 rows, P 128 rows (lanes for P rows 128-255
+  // re-read row 127 into unused slots, so every wave issues the same loads).
+  // MX scales in k-major layout pack four consecutive rows of one 32-block per
+  // lane instead ([block][row] bytes in LDS).
   const bool q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
   const bool p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
   src.qs = src.ps = nullptr;
   src.qs_k = src.ps_k = 0;
   if (SCALED) {
     const int qi = wave * 64 + lane;           // 0..255
-    const int pi = wave * 32 + (lane & 31);    // 0..127
+    const int pi = wave * 64 + lane;           // 0..255, rows >= 128 clamped below
     const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
     if (q_mx_k) {
       const int b = (qi * 4) / kBI, row = (qi * 4) % kBI;
@@ -354,10 +552,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
       src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * sbytes;
     }
     if (p_mx_k) {
-      const int b = (pi * 4) / kBJ, row = (pi * 4) % kBJ;
+      const int pc = pi < 128 ? pi : 127;      // 4 blocks x 128 rows = 128 lanes of 4 bytes
+      const int b = (pc * 4) / kBJ, row = (pc * 4) % kBJ;
       src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + row) * p.P.s_row + b * p.P.s_kb);
     } else {
-      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + pi) >> p.P.s_shift) * p.P.s_row * sbytes;
+      const int pc = pi < kBJ ? pi : kBJ - 1;
+      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + pc) >> p.P.s_shift) * p.P.s_row * sbytes;
     }
     // per K step: one 128-block (fp32 / pow2 scales) or four 32-blocks (MX)
     src.qs_k = (KIND == GK_FP8_MX ? 4 : 1) * p.Q.s_kb * sbytes;
@@ -378,39 +578,86 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
   // passed the barrier that follows its last read of it.  The barrier carries
   // no memory fence, which would wait for the prefetches still in flight.
   const int64_t nk = (k_hi - k_lo) / KSTEP;
-  if (nk > 0) gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
-  if (nk > 1) gemm_issue<KIND>(src, k_lo + KSTEP, smem1, wave, lane);
-  // Main loop: steps with a successor, whose loads are always in flight here,
-  // so an unconditional vmcnt(NLOAD) retires exactly the current stage's DMA
-  // (the compiler's wait tracking follows it and adds no wait of its own as
-  // long as every body issues the same loads).
-  int64_t t = 0;
-  while (t + 1 < nk) {
-#pragma unroll
-    for (int u = 0; u < 3; ++u) {
-      if (t + 1 >= nk) break;
-      FM_WAIT_VMCNT(NLOAD);
+  if constexpr (KIND == GK_FP8_F32) {
+    // fp32 block scales: each 128-deep partial sum is promoted as a whole, so
+    // this kind keeps the one-barrier-per-step loop over whole K steps.
+    if (nk > 0) gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
+    if (nk > 1) gemm_issue<KIND>(src, k_lo + KSTEP, smem1, wave, lane);
+    // Main loop: steps with a successor, whose loads are always in flight here,
+    // so an unconditional vmcnt(NLOAD) retires exactly the current stage's DMA
+    // (the compiler's wait tracking follows it and adds no wait of its own as
+    // long as every body issues the same loads).
+    int64_t t = 0;
+    while (t + 1 < nk) {
+  #pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (t + 1 >= nk) break;
+        FM_WAIT_VMCNT(NLOAD);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        uint8_t* nxt = u == 0 ? smem2 : (u == 1 ? smem0 : smem1);
+        const uint8_t* cur = u == 0 ? smem0 : (u == 1 ? smem1 : smem2);
+        // unconditional (keeps the compiler's wait tracking exact): at t = nk-2
+        // this re-reads step nk-1 into the stage of step nk, which is never read
+        const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
+        gemm_issue<KIND>(src, k_lo + tn * KSTEP, nxt, wave, lane);
+        gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
+        ++t;
+      }
+    }
+    if (t < nk) {  // last step: nothing else in flight
+      FM_WAIT_VMCNT(0);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      uint8_t* nxt = u == 0 ? smem2 : (u == 1 ? smem0 : smem1);
-      const uint8_t* cur = u == 0 ? smem0 : (u == 1 ? smem1 : smem2);
-      // unconditional (keeps the compiler's wait tracking exact): at t = nk-2
-      // this re-reads step nk-1 into the stage of step nk, which is never read
-      const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
-      gemm_issue<KIND>(src, k_lo + tn * KSTEP, nxt, wave, lane);
+      const int sidx = int(t % 3);
+      const uint8_t* cur = sidx == 0 ? smem0 : (sidx == 1 ? smem1 : smem2);
       gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
-      ++t;
     }
-  }
-  if (t < nk) {  // last step: nothing else in flight
-    FM_WAIT_VMCNT(0);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const int sidx = int(t % 3);
-    const uint8_t* cur = sidx == 0 ? smem0 : (sidx == 1 ? smem1 : smem2);
-    gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
+
+
+  } else {
+    // Register-pipelined loop.  Every K step t is split in two halves; while
+    // the MFMAs of one half run, the fragments of the next half are read:
+    //   A  read half 1 of step t          (stage t % 3)
+    //   B  MFMAs of half 0 of step t      (registers loaded during step t-1)
+    //   C  wait for step t+1's DMA, barrier, refill stage t % 3 with step t+3
+    //   D  read half 0 of step t+1        (stage (t+1) % 3)
+    //   E  MFMAs of half 1 of step t
+    // Each step issues exactly one group of DMA loads (clamped to the last step
+    // at the end; the re-read lands in a stage nobody reads again), so
+    // vmcnt(NLOAD) always retires exactly step t+1's group at C.
+    HalfFrag<KIND> f0, f1;
+    if (nk > 0) {
+      gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
+      gemm_issue<KIND>(src, k_lo + (nk > 1 ? 1 : 0) * KSTEP, smem1, wave, lane);
+      gemm_issue<KIND>(src, k_lo + (nk > 2 ? 2 : nk - 1) * KSTEP, smem2, wave, lane);
+      FM_WAIT_VMCNT(2 * NLOAD);
+      block_barrier();
+      load_half<KIND>(smem0, 0, f0, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
+    }
+    int cur_off = 0;  // byte offset of stage t % 3
+#pragma unroll 1
+    for (int64_t t = 0; t < nk; ++t) {
+      const int nxt_off = cur_off == 2 * SM::kStage ? 0 : cur_off + SM::kStage;
+      uint8_t* cur = smem + cur_off;
+      load_half<KIND>(cur, 1, f1, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);   // A
+      mma_half<KIND>(f0, acc);                                               // B
+      interleave_mfma_lds<KIND>();
+      FM_WAIT_VMCNT(NLOAD);                                                  // C
+      block_barrier();
+      // C+D: refill this stage with step t+3 and read half 0 of step t+1
+      // (unconditional: after the last step it reads a stage holding valid data
+      // that is never used, which keeps the body one basic block)
+      const int64_t tn = t + 3 < nk ? t + 3 : nk - 1;
+      refill_and_load_half0<KIND>(src, k_lo + tn * KSTEP, cur, smem + nxt_off, f0, wave, lane, wi, wj,
+                                  lrow, lhalf, q_mx_k, p_mx_k);
+      mma_half<KIND>(f1, acc);                                               // E
+      interleave_mfma_lds<KIND>();
+      cur_off = nxt_off;
+    }
+    FM_WAIT_VMCNT(0);  // no LDS-DMA may still be in flight when the workgroup exits
   }
 
   // -------------------------------------------------------------- epilogue ----

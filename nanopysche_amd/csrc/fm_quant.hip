@@ -14,28 +14,29 @@ namespace fm {
 // ------------------------------------------------------------------ sources ----
 template <typename T>
 struct DenseSrc {
+  static constexpr int kOut = 1;
   const T* p;
   int64_t ld;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const;
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const;
 };
 
 template <>
-__device__ __forceinline__ void DenseSrc<uint16_t>::load8(int64_t row, int64_t col, float v[8]) const {
+__device__ __forceinline__ void DenseSrc<uint16_t>::load8(int64_t row, int64_t col, float v[][8]) const {
   const uint4 pk = *reinterpret_cast<const uint4*>(p + row * ld + col);
   const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    v[2 * i] = u2f(w[i] << 16);
-    v[2 * i + 1] = u2f(w[i] & 0xffff0000u);
+    v[0][2 * i] = u2f(w[i] << 16);
+    v[0][2 * i + 1] = u2f(w[i] & 0xffff0000u);
   }
 }
 
 template <>
-__device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col, float v[8]) const {
+__device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col, float v[][8]) const {
   const float4 a = *reinterpret_cast<const float4*>(p + row * ld + col);
   const float4 b = *reinterpret_cast<const float4*>(p + row * ld + col + 4);
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  v[0][0] = a.x; v[0][1] = a.y; v[0][2] = a.z; v[0][3] = a.w;
+  v[0][4] = b.x; v[0][5] = b.y; v[0][6] = b.z; v[0][7] = b.w;
 }
 
 // ------------------------------------------------------- 128x128 weight blocks ----
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
   const DenseSrc<T> src{static_cast<const T*>(a.w) + g * a.gs_w, a.ld_w};
   float v[8][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) src.load8(r0 + rr + 16 * i, c0 + cc, v[i]);
+  for (int i = 0; i < 8; ++i) src.load8(r0 + rr + 16 * i, c0 + cc, v + i);
   float am = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -249,11 +250,39 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
   if (tid < 128) st[(r0 >> 7) * ld_st + c0 + tid] = sc;
 }
 
+// Runs both e4m3 and both bf16 conversion paths on the same inputs.
+__global__ __launch_bounds__(256) void convert_check_kernel(const float* x, int64_t n4, uint32_t* e_hw,
+                                                            uint32_t* e_sw, uint32_t* b_hw,
+                                                            uint32_t* b_sw) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+    const float4 v = reinterpret_cast<const float4*>(x)[i];
+    e_hw[i] = enc_e4m3x4<true>(v.x, v.y, v.z, v.w);
+    e_sw[i] = enc_e4m3x4<false>(v.x, v.y, v.z, v.w);
+    b_hw[2 * i] = enc_bf16x2<true>(v.x, v.y);
+    b_hw[2 * i + 1] = enc_bf16x2<true>(v.z, v.w);
+    b_sw[2 * i] = enc_bf16x2<false>(v.x, v.y);
+    b_sw[2 * i + 1] = enc_bf16x2<false>(v.z, v.w);
+  }
+}
+
 }  // namespace fm
 
 using namespace fm;
 
 extern "C" {
+
+int fm_convert_check(const float* x, int64_t n, void* e4m3_hw, void* e4m3_sw, void* bf16_hw,
+                     void* bf16_sw, void* stream) {
+  FM_REQUIRE(x && e4m3_hw && e4m3_sw && bf16_hw && bf16_sw, "fm_convert_check: null pointer");
+  FM_REQUIRE(n % 4 == 0, "fm_convert_check: n must be a multiple of 4");
+  if (n == 0) return 0;
+  const int64_t n4 = n / 4;
+  const unsigned blocks = unsigned(n4 / 256 + 1 < 4096 ? n4 / 256 + 1 : 4096);
+  hipLaunchKernelGGL(convert_check_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, n4, static_cast<uint32_t*>(e4m3_hw), static_cast<uint32_t*>(e4m3_sw),
+                     static_cast<uint32_t*>(bf16_hw), static_cast<uint32_t*>(bf16_sw));
+  return check_launch("fm_convert_check");
+}
 
 int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int kind,
                 void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st,
@@ -262,7 +291,7 @@ int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t 
   FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_quantize: bad input dtype %d",
              x_dtype);
   FM_REQUIRE(ld_x >= cols && ld_x % 8 == 0, "fm_quantize: input pitch must be >= cols and a multiple of 8");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, nullptr};
   hipStream_t sm = static_cast<hipStream_t>(stream);
   if (x_dtype == FM_DTYPE_BF16)
     return launch_tile_producer(DenseSrc<uint16_t>{static_cast<const uint16_t*>(x), ld_x}, o, rows,

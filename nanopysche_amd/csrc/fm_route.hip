@@ -283,29 +283,30 @@ __global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t
 // Row r of the padded buffer is x[assign_of_row[r] / K] (times the router
 // weight of that assignment when `w` is set), zeros for pad rows.
 struct GatherSrc {
+  static constexpr int kOut = 1;
   const uint16_t* x;  // bf16 [T, D]
   int64_t ld;
   const int32_t* assign_of_row;
   int K;
   const float* w;     // [T*K] or null
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const {
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
     const int32_t a = assign_of_row[row];
     if (a < 0) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+      for (int i = 0; i < 8; ++i) v[0][i] = 0.f;
       return;
     }
     const uint4 pk = *reinterpret_cast<const uint4*>(x + int64_t(a / K) * ld + col);
     const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[2 * i] = u2f(q[i] << 16);
-      v[2 * i + 1] = u2f(q[i] & 0xffff0000u);
+      v[0][2 * i] = u2f(q[i] << 16);
+      v[0][2 * i + 1] = u2f(q[i] & 0xffff0000u);
     }
     if (w) {
       const float s = w[a];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(s, v[i]);
+      for (int i = 0; i < 8; ++i) v[0][i] = s * v[0][i];
     }
   }
 };
@@ -467,12 +468,13 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
 
 int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,
                int64_t rows, int K, const float* weights, int kind, void* q, int64_t ld_q, void* s,
-               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream) {
+               int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
+               const int32_t* tile_valid, void* stream) {
   FM_REQUIRE(x || T == 0, "fm_permute: null input");
   FM_REQUIRE(assign_of_row, "fm_permute: null assign_of_row");
   FM_REQUIRE(ld_x >= D && ld_x % 8 == 0, "fm_permute: input pitch must be >= D and a multiple of 8");
   FM_REQUIRE(K >= 1, "fm_permute: K must be >= 1");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, tile_valid};
   GatherSrc src{static_cast<const uint16_t*>(x), ld_x, assign_of_row, K, weights};
   return launch_tile_producer(src, o, rows, D, static_cast<hipStream_t>(stream), "fm_permute");
 }

@@ -2,8 +2,8 @@
 //   fm_swiglu_quantize      -- h = silu(g) * u from bf16 g, u (one [M, 2H]
 //                              buffer or two tensors), emitted as bf16 or e4m3
 //                              with row and/or transposed block scales
-//   fm_swiglu_backward      -- [dg | du] from g, u and dh, emitted the same way
-//                              (the [M, 2H] layout feeds the fused
+//   fm_swiglu_backward      -- [dg | du] from one read of g, u and dh, emitted
+//                              the same way (the [M, 2H] layout feeds the fused
 //                              dx = dg w1 + du w3 GEMM and the dW1|dW3 GEMM)
 // silu(g) = g / (1 + exp(-g)) in fp32; d silu = s (1 + g (1 - s)), s = sigmoid(g).
 #include "fm_tile.h"
@@ -24,41 +24,37 @@ __device__ __forceinline__ void load8_bf16(const uint16_t* p, float v[8]) {
 __device__ __forceinline__ float sigmoidf(float g) { return 1.f / (1.f + expf(-g)); }
 
 struct SwigluSrc {
+  static constexpr int kOut = 1;
   const uint16_t* g;  // [M, H] pitch ld_g
   const uint16_t* u;  // [M, H] pitch ld_u
   int64_t ld_g, ld_u;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const {
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
     float gv[8], uv[8];
     load8_bf16(g + row * ld_g + col, gv);
     load8_bf16(u + row * ld_u + col, uv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (gv[i] / (1.f + expf(-gv[i]))) * uv[i];
+    for (int i = 0; i < 8; ++i) v[0][i] = (gv[i] / (1.f + expf(-gv[i]))) * uv[i];
   }
 };
 
-// logical columns [0, H) are dg, [H, 2H) are du; a 128-column tile never
-// straddles the two halves because H % 128 == 0.
+// Two values per element from one read of g, u, dh: v[0] = dg (output columns
+// [0, H)), v[1] = du (output columns [H, 2H)).
 struct SwigluBwdSrc {
+  static constexpr int kOut = 2;
   const uint16_t* g;
   const uint16_t* u;
   const uint16_t* dh;
-  int64_t ld_g, ld_u, ld_dh, H;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[8]) const {
-    const bool is_up = col >= H;
-    const int64_t c = is_up ? col - H : col;
+  int64_t ld_g, ld_u, ld_dh;
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
     float gv[8], uv[8], dv[8];
-    load8_bf16(g + row * ld_g + c, gv);
-    load8_bf16(dh + row * ld_dh + c, dv);
-    if (is_up) {
+    load8_bf16(g + row * ld_g + col, gv);
+    load8_bf16(u + row * ld_u + col, uv);
+    load8_bf16(dh + row * ld_dh + col, dv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = dv[i] * (gv[i] * sigmoidf(gv[i]));
-    } else {
-      load8_bf16(u + row * ld_u + c, uv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float s = sigmoidf(gv[i]);
-        v[i] = dv[i] * uv[i] * s * (1.f + gv[i] * (1.f - s));
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float s = sigmoidf(gv[i]);
+      v[0][i] = dv[i] * uv[i] * s * (1.f + gv[i] * (1.f - s));
+      v[1][i] = dv[i] * (gv[i] * s);
     }
   }
 };
@@ -71,11 +67,12 @@ extern "C" {
 
 int fm_swiglu_quantize(const void* g, int64_t ld_g, const void* u, int64_t ld_u, int64_t rows,
                        int64_t H, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt,
-                       int64_t ld_qt, void* st, int64_t ld_st, void* stream) {
+                       int64_t ld_qt, void* st, int64_t ld_st, const int32_t* tile_valid,
+                       void* stream) {
   FM_REQUIRE((g && u) || rows == 0, "fm_swiglu_quantize: null input");
   FM_REQUIRE(ld_g % 8 == 0 && ld_u % 8 == 0 && ld_g >= H && ld_u >= H,
              "fm_swiglu_quantize: pitches must be multiples of 8 and >= H");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, tile_valid};
   SwigluSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), ld_g, ld_u};
   return launch_tile_producer(src, o, rows, H, static_cast<hipStream_t>(stream),
                               "fm_swiglu_quantize");
@@ -84,15 +81,15 @@ int fm_swiglu_quantize(const void* g, int64_t ld_g, const void* u, int64_t ld_u,
 int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u, const void* dh,
                        int64_t ld_dh, int64_t rows, int64_t H, int kind, void* q, int64_t ld_q,
                        void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
-                       void* stream) {
+                       const int32_t* tile_valid, void* stream) {
   FM_REQUIRE((g && u && dh) || rows == 0, "fm_swiglu_backward: null input");
   FM_REQUIRE(H % 128 == 0, "fm_swiglu_backward: H must be a multiple of 128");
   FM_REQUIRE(ld_g % 8 == 0 && ld_u % 8 == 0 && ld_dh % 8 == 0,
              "fm_swiglu_backward: pitches must be multiples of 8");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st};
+  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, H}, tile_valid};
   SwigluBwdSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
-                   static_cast<const uint16_t*>(dh), ld_g, ld_u, ld_dh, H};
-  return launch_tile_producer(src, o, rows, 2 * H, static_cast<hipStream_t>(stream),
+                   static_cast<const uint16_t*>(dh), ld_g, ld_u, ld_dh};
+  return launch_tile_producer(src, o, rows, H, static_cast<hipStream_t>(stream),
                               "fm_swiglu_backward");
 }
 

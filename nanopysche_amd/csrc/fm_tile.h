@@ -3,14 +3,26 @@
 // functor -- into
 //   * a row-major output   (bf16, or e4m3 with 1x128 / 1x32 block scales), and/or
 //   * a transposed output  (bf16, or e4m3 with 128x1 / 32x1 block scales),
-// reading the source exactly once.  HBM-bound: 16-byte loads, 8-byte row
-// stores (16 lanes cover one 128-byte row segment), 64-byte transposed stores.
+// reading the source exactly once.  A source may yield NOUT values per
+// element (SwiGLU backward yields dg and du), each with its own column offset
+// in the outputs.  HBM-bound: 16-byte loads, 8-byte row stores (16 lanes cover
+// one 128-byte row segment), 16-byte transposed stores.
 //
-// The transposed values go through LDS as fp32 ([128][129] floats, the odd
-// pitch keeps column walks conflict-free).
+// LDS staging for the transposed output:
+//   QK_POW2  -- e4m3 codes [128][128 + 4 pad] + one row scale per row (17 KiB):
+//               the transposed output is the scaling-aware transpose of the
+//               row output, so the codes are all it needs.
+//   others   -- fp32 values [128][129] (66 KiB).
 #pragma once
 
 #include "fm_common.h"
+
+// e4m3 / bf16 conversion: the gfx950 convert instructions, or the integer
+// routines of fm_common.h.  Both are bit-identical (checked on the GPU by
+// fm_convert_check); the hardware path is the default.
+#ifndef FM_HW_CVT
+#define FM_HW_CVT 1
+#endif
 
 namespace fm {
 
@@ -23,20 +35,38 @@ enum QuantKind : int {
 };
 
 struct TileOut {
-  int kind;              // QuantKind
+  int kind;              // QuantKind (dispatched to a template argument)
   // row-major output (nullptr = not wanted)
-  void* row_q;           // bf16 or e4m3 [rows, cols] with pitch ld_row (elements)
+  void* row_q;           // bf16 or e4m3 [rows, *] with pitch ld_row (elements)
   int64_t ld_row;
-  void* row_s;           // fp32 [rows, cols/128] or e8m0 [rows, cols/32]; pitch ld_row_s
+  void* row_s;           // fp32 [rows, */128] or e8m0 [rows, */32]; pitch ld_row_s
   int64_t ld_row_s;
   // transposed output (nullptr = not wanted); requires rows % 128 == 0
-  void* col_q;           // bf16 or e4m3 [cols, rows] with pitch ld_col (elements)
+  void* col_q;           // bf16 or e4m3 [*, rows] with pitch ld_col (elements)
   int64_t ld_col;
-  void* col_s;           // fp32 [rows/128, cols] or e8m0 [rows/32, cols]; pitch ld_col_s
+  void* col_s;           // fp32 [rows/128, *] or e8m0 [rows/32, *]; pitch ld_col_s
   int64_t ld_col_s;
+  int64_t col_off[2];    // output column offset of source value 0 / 1
+  const int32_t* tile_valid;  // optional: skip 128-row tile t when tile_valid[t] < 0
 };
 
 constexpr int kTileLdsPitch = 129;
+
+// ------------------------------------------------------------- conversions ----
+template <bool HW>
+__device__ __forceinline__ uint32_t enc_e4m3x4(float a, float b, float c, float d) {
+  if constexpr (HW) {
+    return hw_e4m3x4(clamp448(a), clamp448(b), clamp448(c), clamp448(d));
+  } else {
+    return uint32_t(f32_to_e4m3(clamp448(a))) | (uint32_t(f32_to_e4m3(clamp448(b))) << 8) |
+           (uint32_t(f32_to_e4m3(clamp448(c))) << 16) | (uint32_t(f32_to_e4m3(clamp448(d))) << 24);
+  }
+}
+template <bool HW>
+__device__ __forceinline__ uint32_t enc_bf16x2(float a, float b) {
+  if constexpr (HW) return hw_bf16x2(a, b);
+  else return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
+}
 
 __device__ __forceinline__ float group_max16(float v) {
   // max over the 16 consecutive lanes that share a 128-column row block
@@ -60,20 +90,24 @@ __device__ __forceinline__ uint64_t pack8_e4m3(const uint8_t* b) {
 }
 
 // Source functor contract:
-//   __device__ void load8(int64_t row, int64_t col, float v[8]) const;
-// loads columns [col, col+8) of logical row `row` as fp32 (zeros for rows the
-// source treats as padding).  `rows` is the logical row count.
-template <class Src>
-__device__ __forceinline__ void produce_tile(const Src& src, const TileOut& o, int64_t rows,
-                                             int64_t row0, int64_t col0, float* lds,
-                                             float* lds_rowscale) {
+//   static constexpr int kOut;                       // values per element (1 or 2)
+//   __device__ void load8(int64_t row, int64_t col, float v[kOut][8]) const;
+// loads columns [col, col+8) of logical row `row` (zeros for rows the source
+// treats as padding).
+template <class Src, int KIND>
+__global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, int64_t rows) {
+  constexpr int NOUT = Src::kOut;
+  constexpr bool HW = FM_HW_CVT != 0;
+  const int64_t col0 = int64_t(blockIdx.x) * 128;
+  const int64_t row0 = int64_t(blockIdx.y) * 128;
+  if (o.tile_valid != nullptr && o.tile_valid[blockIdx.y] < 0) return;
   const int tid = threadIdx.x;
   const bool want_col = o.col_q != nullptr;
-  const bool rowq = o.kind != QK_BF16;
-  // ---- phase 1: rows.  thread -> (row = tid/16 + 16*it, 8 columns at 8*(tid%16))
+  const bool want_row = o.row_q != nullptr;
+
+  // ---- phase 1: thread -> rows (tid/16) + 16*it, columns [8*(tid%16), +8)
   const int cpos = (tid & 15) * 8;
-  // issue all eight 8-column loads before any store so they overlap in flight
-  float vv[8][8];
+  float vv[8][NOUT][8];
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int64_t grow = row0 + (tid >> 4) + 16 * it;
@@ -81,171 +115,185 @@ __device__ __forceinline__ void produce_tile(const Src& src, const TileOut& o, i
       src.load8(grow, col0 + cpos, vv[it]);
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vv[it][i] = 0.f;
+      for (int q = 0; q < NOUT; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vv[it][q][i] = 0.f;
     }
   }
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int r = (tid >> 4) + 16 * it;
-    const int64_t grow = row0 + r;
-    float* v = vv[it];
-    float am = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-    float keep[8];  // value stored for the transposed pass
-#pragma unroll
-    for (int i = 0; i < 8; ++i) keep[i] = v[i];
-    if (o.kind == QK_BLOCK || o.kind == QK_POW2) {
-      const float bam = group_max16(am);
-      const float s = block_scale(bam, o.kind == QK_POW2);
-      uint8_t q[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = quant_e4m3(v[i], s);
-      if (o.kind == QK_POW2) {
-        // the transposed output re-expresses the row-quantised values
-#pragma unroll
-        for (int i = 0; i < 8; ++i) keep[i] = e4m3_to_f32(q[i]) * s;
-        if ((tid & 15) == 0) lds_rowscale[r] = s;
-      }
-      if (o.row_q != nullptr && grow < rows) {
-        *reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + col0 +
-                                     cpos) = pack8_e4m3(q);
-        if ((tid & 15) == 0)
-          static_cast<float*>(o.row_s)[grow * o.ld_row_s + (col0 >> 7)] = s;
-      }
-    } else if (o.kind == QK_MX) {
-      const float bam = group_max4(am);
-      const uint32_t code = mx_code(bam);
-      const float inv = mx_inv_scale(code);
-      uint8_t q[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = quant_mx(v[i], inv);
-      if (o.row_q != nullptr && grow < rows) {
-        *reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + col0 +
-                                     cpos) = pack8_e4m3(q);
-        if ((tid & 3) == 0)
-          static_cast<uint8_t*>(o.row_s)[grow * o.ld_row_s + ((col0 + cpos) >> 5)] =
-              uint8_t(code);
-      }
-    } else {  // bf16
-      if (o.row_q != nullptr && grow < rows) {
-        uint16_t b[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) b[i] = f32_to_bf16(v[i]);
-        uint4 pk;
-        pk.x = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
-        pk.y = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
-        pk.z = uint32_t(b[4]) | (uint32_t(b[5]) << 16);
-        pk.w = uint32_t(b[6]) | (uint32_t(b[7]) << 16);
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(o.row_q) + grow * o.ld_row + col0 +
-                                  cpos) = pk;
-      }
-    }
-    (void)rowq;
-    if (want_col) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lds[r * kTileLdsPitch + cpos + i] = keep[i];
-    }
-  }
-  if (!want_col) return;
-  __syncthreads();
-  // ---- phase 2: columns.  thread -> column c = tid % 128, rows [64*h, 64*h+64)
-  const int c = tid & 127;
-  const int h = tid >> 7;
-  float* colmax = lds_rowscale + 128;  // [2][128]
-  float am = 0.f;
-  if (o.kind == QK_BLOCK) {
-    for (int r = 0; r < 64; ++r) am = fmaxf(am, fabsf(lds[(64 * h + r) * kTileLdsPitch + c]));
-    colmax[h * 128 + c] = am;
-  }
-  __syncthreads();
-  const int64_t gcol = col0 + c;
-  uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
-  if (o.kind == QK_BLOCK || o.kind == QK_POW2) {
-    float s;
-    if (o.kind == QK_BLOCK) {
-      s = block_scale(fmaxf(colmax[c], colmax[128 + c]), false);
-    } else {
-      s = 0.f;  // largest row scale of the tile (uniform over its columns)
-      for (int r = 0; r < 128; ++r) s = fmaxf(s, lds_rowscale[r]);
-    }
-    for (int r16 = 0; r16 < 64; r16 += 16) {
-      uint8_t q[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        q[i] = quant_e4m3(lds[(64 * h + r16 + i) * kTileLdsPitch + c], s);
-      uint4 pk;
-      pk.x = uint32_t(q[0]) | (uint32_t(q[1]) << 8) | (uint32_t(q[2]) << 16) | (uint32_t(q[3]) << 24);
-      pk.y = uint32_t(q[4]) | (uint32_t(q[5]) << 8) | (uint32_t(q[6]) << 16) | (uint32_t(q[7]) << 24);
-      pk.z = uint32_t(q[8]) | (uint32_t(q[9]) << 8) | (uint32_t(q[10]) << 16) | (uint32_t(q[11]) << 24);
-      pk.w = uint32_t(q[12]) | (uint32_t(q[13]) << 8) | (uint32_t(q[14]) << 16) | (uint32_t(q[15]) << 24);
-      *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = pk;
-    }
-    if (h == 0) static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + gcol] = s;
-  } else if (o.kind == QK_MX) {
-    for (int b = 0; b < 2; ++b) {  // two 32-row MX blocks per thread
-      const int rb = 64 * h + 32 * b;
-      float m = 0.f;
-      for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(lds[(rb + i) * kTileLdsPitch + c]));
-      const uint32_t code = mx_code(m);
-      const float inv = mx_inv_scale(code);
-      for (int r16 = 0; r16 < 32; r16 += 16) {
-        uint8_t q[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) q[i] = quant_mx(lds[(rb + r16 + i) * kTileLdsPitch + c], inv);
-        uint4 pk;
-        pk.x = uint32_t(q[0]) | (uint32_t(q[1]) << 8) | (uint32_t(q[2]) << 16) | (uint32_t(q[3]) << 24);
-        pk.y = uint32_t(q[4]) | (uint32_t(q[5]) << 8) | (uint32_t(q[6]) << 16) | (uint32_t(q[7]) << 24);
-        pk.z = uint32_t(q[8]) | (uint32_t(q[9]) << 8) | (uint32_t(q[10]) << 16) | (uint32_t(q[11]) << 24);
-        pk.w = uint32_t(q[12]) | (uint32_t(q[13]) << 8) | (uint32_t(q[14]) << 16) | (uint32_t(q[15]) << 24);
-        *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + rb + r16) = pk;
-      }
-      static_cast<uint8_t*>(o.col_s)[((row0 + rb) >> 5) * o.ld_col_s + gcol] = uint8_t(code);
-    }
-  } else {  // bf16 transpose
-    uint16_t* qt16 = static_cast<uint16_t*>(o.col_q);
-    for (int r8 = 0; r8 < 64; r8 += 8) {
-      uint16_t b[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) b[i] = f32_to_bf16(lds[(64 * h + r8 + i) * kTileLdsPitch + c]);
-      uint4 pk;
-      pk.x = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
-      pk.y = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
-      pk.z = uint32_t(b[4]) | (uint32_t(b[5]) << 16);
-      pk.w = uint32_t(b[6]) | (uint32_t(b[7]) << 16);
-      *reinterpret_cast<uint4*>(qt16 + gcol * o.ld_col + row0 + 64 * h + r8) = pk;
-    }
-  }
-}
 
-// Kernel wrapper: grid (cols/128, ceil(rows/128)).  Dynamic LDS is not used;
-// the tile buffer is a static array of 128*129 floats + 384 scale slots.
-template <class Src>
-__global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, int64_t rows) {
-  __shared__ float lds[128 * kTileLdsPitch];
-  __shared__ float lds_rs[128 + 256];
-  const int64_t col0 = int64_t(blockIdx.x) * 128;
-  const int64_t row0 = int64_t(blockIdx.y) * 128;
-  produce_tile(src, o, rows, row0, col0, lds, lds_rs);
+  // LDS for the transposed pass (one output at a time)
+  constexpr bool COMPACT = KIND == QK_POW2;
+  __shared__ float red[256];
+  __shared__ float rscale[128];
+  __shared__ __attribute__((aligned(16))) uint32_t lds_code[COMPACT ? 128 * 33 : 1];
+  __shared__ float lds_val[COMPACT ? 1 : 128 * kTileLdsPitch];
+
+#pragma unroll
+  for (int oi = 0; oi < NOUT; ++oi) {
+    const int64_t ocol = col0 + o.col_off[oi];  // output column of this tile
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = (tid >> 4) + 16 * it;
+      const int64_t grow = row0 + r;
+      const float* v = vv[it][oi];
+      float am = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+      if (KIND == QK_BLOCK || KIND == QK_POW2) {
+        const float s = block_scale(group_max16(am), KIND == QK_POW2);
+        uint32_t w0, w1;
+        if (KIND == QK_POW2) {
+          const float inv = 1.0f / s;  // exact: s is a power of two
+          w0 = enc_e4m3x4<HW>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+          w1 = enc_e4m3x4<HW>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        } else {
+          w0 = enc_e4m3x4<HW>(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
+          w1 = enc_e4m3x4<HW>(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
+        }
+        if (want_row && grow < rows) {
+          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
+              make_uint2(w0, w1);
+          if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.ld_row_s + (ocol >> 7)] = s;
+        }
+        if (want_col) {
+          if (COMPACT) {
+            lds_code[r * 33 + (cpos >> 2)] = w0;
+            lds_code[r * 33 + (cpos >> 2) + 1] = w1;
+            if ((tid & 15) == 0) rscale[r] = s;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
+          }
+        }
+      } else if (KIND == QK_MX) {
+        const uint32_t code = mx_code(group_max4(am));
+        const float inv = mx_inv_scale(code);
+        const uint32_t w0 = enc_e4m3x4<HW>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        const uint32_t w1 = enc_e4m3x4<HW>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        if (want_row && grow < rows) {
+          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
+              make_uint2(w0, w1);
+          if ((tid & 3) == 0)
+            static_cast<uint8_t*>(o.row_s)[grow * o.ld_row_s + ((ocol + cpos) >> 5)] = uint8_t(code);
+        }
+        if (want_col) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
+        }
+      } else {  // bf16
+        if (want_row && grow < rows) {
+          const uint4 pk = make_uint4(enc_bf16x2<HW>(v[0], v[1]), enc_bf16x2<HW>(v[2], v[3]),
+                                      enc_bf16x2<HW>(v[4], v[5]), enc_bf16x2<HW>(v[6], v[7]));
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) = pk;
+        }
+        if (want_col) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
+        }
+      }
+    }
+    if (!want_col) continue;
+    __syncthreads();
+
+    // ---- phase 2: thread -> column c = tid % 128, rows [64*h, 64*h + 64)
+    const int c = tid & 127, h = tid >> 7;
+    const int64_t gcol = ocol + c;
+    uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
+    if (KIND == QK_POW2) {
+      // column scale: the largest row scale of the tile (uniform over its columns)
+      if (tid < 64) {
+        float m = fmaxf(rscale[tid], rscale[tid + 64]);
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (tid == 0) red[0] = m;
+      }
+      __syncthreads();
+      const float st = red[0];
+      const float inv = 1.0f / st;  // exact: power of two
+      const int wsh = 8 * (c & 3);
+      for (int r16 = 0; r16 < 64; r16 += 16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float f[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int row = 64 * h + r16 + 4 * k + b;
+            const uint8_t code = uint8_t(lds_code[row * 33 + (c >> 2)] >> wsh);
+            f[b] = (e4m3_to_f32(code) * rscale[row]) * inv;
+          }
+          w[k] = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
+        }
+        *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      if (h == 0) static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + gcol] = st;
+    } else if (KIND == QK_BLOCK) {
+      float am = 0.f;
+      for (int r = 0; r < 64; ++r) am = fmaxf(am, fabsf(lds_val[(64 * h + r) * kTileLdsPitch + c]));
+      red[h * 128 + c] = am;
+      __syncthreads();
+      const float s = block_scale(fmaxf(red[c], red[128 + c]), false);
+      for (int r16 = 0; r16 < 64; r16 += 16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float* p = &lds_val[(64 * h + r16 + 4 * k) * kTileLdsPitch + c];
+          w[k] = enc_e4m3x4<HW>(p[0] / s, p[kTileLdsPitch] / s, p[2 * kTileLdsPitch] / s,
+                                p[3 * kTileLdsPitch] / s);
+        }
+        *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      if (h == 0) static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + gcol] = s;
+    } else if (KIND == QK_MX) {
+      for (int b = 0; b < 2; ++b) {  // two 32-row MX blocks per thread
+        const int rb = 64 * h + 32 * b;
+        float m = 0.f;
+        for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(lds_val[(rb + i) * kTileLdsPitch + c]));
+        const uint32_t code = mx_code(m);
+        const float inv = mx_inv_scale(code);
+        for (int r16 = 0; r16 < 32; r16 += 16) {
+          uint32_t w[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float* p = &lds_val[(rb + r16 + 4 * k) * kTileLdsPitch + c];
+            w[k] = enc_e4m3x4<HW>(p[0] * inv, p[kTileLdsPitch] * inv, p[2 * kTileLdsPitch] * inv,
+                                  p[3 * kTileLdsPitch] * inv);
+          }
+          *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + rb + r16) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        static_cast<uint8_t*>(o.col_s)[((row0 + rb) >> 5) * o.ld_col_s + gcol] = uint8_t(code);
+      }
+    } else {  // bf16 transpose
+      uint16_t* qt16 = static_cast<uint16_t*>(o.col_q);
+      for (int r8 = 0; r8 < 64; r8 += 8) {
+        const float* p = &lds_val[(64 * h + r8) * kTileLdsPitch + c];
+        const uint4 pk = make_uint4(enc_bf16x2<HW>(p[0], p[kTileLdsPitch]),
+                                    enc_bf16x2<HW>(p[2 * kTileLdsPitch], p[3 * kTileLdsPitch]),
+                                    enc_bf16x2<HW>(p[4 * kTileLdsPitch], p[5 * kTileLdsPitch]),
+                                    enc_bf16x2<HW>(p[6 * kTileLdsPitch], p[7 * kTileLdsPitch]));
+        *reinterpret_cast<uint4*>(qt16 + gcol * o.ld_col + row0 + 64 * h + r8) = pk;
+      }
+    }
+    if (oi + 1 < NOUT) __syncthreads();  // LDS is reused by the next output
+  }
 }
 
 // Validates a TileOut against the tile geometry; returns nonzero (with the
-// error set) on a mismatch.
-inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols) {
+// error set) on a mismatch.  `cols` is the source's column count per output.
+inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols, int nout) {
   FM_REQUIRE(cols > 0 && cols % 128 == 0, "cols must be a positive multiple of 128 (got %lld)",
              (long long)cols);
   FM_REQUIRE(rows >= 0, "rows must be >= 0");
   FM_REQUIRE(o.kind >= QK_BF16 && o.kind <= QK_MX, "unknown quant kind %d", o.kind);
   FM_REQUIRE(o.row_q != nullptr || o.col_q != nullptr, "no output requested");
+  const int64_t span = o.col_off[nout - 1] + cols;  // output columns touched
+  FM_REQUIRE(o.col_off[0] % 128 == 0 && o.col_off[nout - 1] % 128 == 0, "column offsets must be multiples of 128");
   if (o.row_q != nullptr) {
-    FM_REQUIRE(o.ld_row >= cols, "row output pitch %lld < cols %lld", (long long)o.ld_row,
-               (long long)cols);
+    FM_REQUIRE(o.ld_row >= span, "row output pitch %lld < columns %lld", (long long)o.ld_row,
+               (long long)span);
+    FM_REQUIRE(o.ld_row % 8 == 0, "row output pitch must be a multiple of 8");
     if (o.kind != QK_BF16) {
       FM_REQUIRE(o.row_s != nullptr, "row scale output missing");
-      FM_REQUIRE(o.ld_row_s >= (o.kind == QK_MX ? cols / 32 : cols / 128), "row scale pitch too small");
-      FM_REQUIRE(o.ld_row % 8 == 0, "fp8 row pitch must be a multiple of 8");
-    } else {
-      FM_REQUIRE(o.ld_row % 8 == 0, "bf16 row pitch must be a multiple of 8");
+      FM_REQUIRE(o.ld_row_s >= (o.kind == QK_MX ? span / 32 : span / 128), "row scale pitch too small");
     }
   }
   if (o.col_q != nullptr) {
@@ -255,7 +303,7 @@ inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols) {
     FM_REQUIRE(o.ld_col % 16 == 0, "transposed output pitch must be a multiple of 16");
     if (o.kind != QK_BF16) {
       FM_REQUIRE(o.col_s != nullptr, "transposed scale output missing");
-      FM_REQUIRE(o.ld_col_s >= cols, "transposed scale pitch too small");
+      FM_REQUIRE(o.ld_col_s >= span, "transposed scale pitch too small");
     }
   }
   return 0;
@@ -264,10 +312,15 @@ inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols) {
 template <class Src>
 int launch_tile_producer(const Src& src, const TileOut& o, int64_t rows, int64_t cols,
                          hipStream_t stream, const char* what) {
-  if (int rc = check_tile_out(o, rows, cols)) return rc;
+  if (int rc = check_tile_out(o, rows, cols, Src::kOut)) return rc;
   if (rows == 0) return 0;
   dim3 grid(unsigned(cols / 128), unsigned((rows + 127) / 128));
-  hipLaunchKernelGGL(tile_producer_kernel<Src>, grid, dim3(256), 0, stream, src, o, rows);
+  switch (o.kind) {
+    case QK_BF16: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_BF16>), grid, dim3(256), 0, stream, src, o, rows); break;
+    case QK_BLOCK: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_BLOCK>), grid, dim3(256), 0, stream, src, o, rows); break;
+    case QK_POW2: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_POW2>), grid, dim3(256), 0, stream, src, o, rows); break;
+    default: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_MX>), grid, dim3(256), 0, stream, src, o, rows); break;
+  }
   return check_launch(what);
 }
 

@@ -202,10 +202,10 @@ def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
 
 
 # ======================================================================= SwiGLU ====
-def _swiglu(g, u, rows, H, kind, row, col, dev):
+def _swiglu(g, u, rows, H, kind, row, col, dev, tile_valid=None):
     q, s, qt, st = _alloc_quant(rows, H, kind, row, col, dev)
     _lib.call("fm_swiglu_quantize", _lib.ptr(g), g.stride(0), _lib.ptr(u), u.stride(0), rows, H, kind,
-              *_tile_args(q, s, qt, st), _lib.stream_of(g))
+              *_tile_args(q, s, qt, st), _lib.ptr(tile_valid), _lib.stream_of(g))
     return q, s, qt, st
 
 
@@ -265,6 +265,8 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
                       fp8_gemm_threshold: int = 0) -> PermutedTokens:
     """Gather the rows of ``x`` [T, D] (bf16) into expert order, each expert's
     group padded to 128 rows (zeros), and quantise them in the same pass.
+    Rows past the last group (``plan.offsets[-1]`` up to ``plan.rows_max``)
+    are left unwritten.
 
     ``indices`` is the router's [T, K] expert indices or a RoutingPlan from an
     earlier call.  ``weights`` [T, K] (optional) scales each gathered row by
@@ -285,7 +287,7 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
         w = weights.reshape(-1).to(torch.float32).contiguous()
     _lib.call("fm_permute", _lib.ptr(x2), T, D, x2.stride(0), _lib.ptr(plan.assign_of_row),
               plan.rows_max, plan.top_k, _lib.ptr(w), kind, *_tile_args(q, s, qt, st),
-              _lib.stream_of(x2))
+              _lib.ptr(plan.tile_expert), _lib.stream_of(x2))
     row, col = _wrap(q, s, qt, st, kind)
     return PermutedTokens(plan, row, col)
 
@@ -642,11 +644,14 @@ class FP8FlowMoECompute:
                                    return_transpose=True)
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
+        h_cols = {}
         for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
             if kind is None:
                 continue
-            q, s, _, _ = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, False, dev)
-            hrow, _ = _wrap(q, s, None, None, kind)
+            # row blocks feed the down GEMM; the column blocks are kept for dW2
+            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, True, dev, plan.tile_expert)
+            hrow, hcol = _wrap(q, s, qt, st, kind)
+            h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
         out = fused_unpermute_unpad(Y, plan, wts)
         if self.capture_intermediates is not None:
@@ -655,6 +660,7 @@ class FP8FlowMoECompute:
         ctx.plan = plan
         ctx.kinds = (fp8_kind, use_bf16)
         ctx.saved_cols = {k: v[0] for k, v in saved.items()}
+        ctx.saved_hcols = h_cols
         ctx.wdtypes = (w1.dtype, w2.dtype, w3.dtype)
         ctx.save_for_backward(wts, GU, Y)
         return out
@@ -697,10 +703,9 @@ class FP8FlowMoECompute:
             gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev)
             _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
                       _lib.ptr(dH), dH.stride(0), R, H, kind, *_tile_args(gq, gs, gqt, gst),
-                      _lib.stream_of(GU))
+                      _lib.ptr(plan.tile_expert), _lib.stream_of(GU))
             dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
-            _, _, hqt, hst = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, False, True, dev)
-            _, h_col = _wrap(None, None, hqt, hst, kind)
+            h_col = ctx.saved_hcols[kind]
             # weight gradients: contraction over each expert's tokens
             _gemm_k(kind, h_col, dy[kind], plan, H, D, dW2, H * D, mask=mask, want=want)
             _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,
@@ -709,6 +714,7 @@ class FP8FlowMoECompute:
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
         dx = fused_unpermute_unpad(dXp, plan, None)
         ctx.saved_cols = None
+        ctx.saved_hcols = None
         return (dx.to(ctx.x_dtype), dw.reshape(T, K), dW1, dW2, dW3, None, None)
 
 

@@ -149,3 +149,38 @@ def test_rejects_bad_shapes(dev):
         fm.quantize_to_fp8(torch.zeros(128, 100, dtype=torch.bfloat16, device=dev))
     with pytest.raises((RuntimeError, ValueError)):
         fm.quantize_to_fp8(torch.zeros(100, 128, dtype=torch.bfloat16, device=dev), return_transpose=True)
+
+
+def test_hw_convert_matches_software(dev):
+    """The kernels encode with gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf16_f32;
+    they must agree bit for bit with the integer routines (which the CPU tests
+    pin against torch's casts) on every bf16 pattern, e4m3 midpoints and
+    random fp32 values around them."""
+    from nanopysche_amd import _lib
+
+    rng = np.random.default_rng(0)
+    pos = ofp8._POS.astype(np.float32)
+    mids = ((ofp8._POS[1:] + ofp8._POS[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([
+        (np.arange(0, 65536, dtype=np.uint32) << 16).view(np.float32),
+        rng.standard_normal(2_000_000).astype(np.float32) * np.float32(100),
+        rng.standard_normal(1_000_000).astype(np.float32) * np.float32(2e-3),
+        pos, -pos, mids, -mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e4)),
+        ((np.arange(0, 1 << 22, dtype=np.uint32) << 9) | 0x00007FFF).view(np.float32),  # bf16 ties +/- 1
+        ((np.arange(0, 1 << 22, dtype=np.uint32) << 9) | 0x00008000).view(np.float32),
+    ])
+    x = x[np.isfinite(x)]
+    x = x[: x.size // 4 * 4]
+    xd = torch.from_numpy(x).to(dev)
+    n = xd.numel()
+    e_hw = torch.empty(n, dtype=torch.uint8, device=dev)
+    e_sw = torch.empty_like(e_hw)
+    b_hw = torch.empty(n, dtype=torch.int16, device=dev)
+    b_sw = torch.empty_like(b_hw)
+    _lib.call("fm_convert_check", _lib.ptr(xd), n, _lib.ptr(e_hw), _lib.ptr(e_sw), _lib.ptr(b_hw),
+              _lib.ptr(b_sw), _lib.stream_of(xd))
+    assert torch.equal(e_hw, e_sw)
+    assert torch.equal(b_hw, b_sw)
+    # and the software path is the oracle's (torch's) cast
+    ref = ofp8.e4m3_encode(np.clip(x, -448, 448))
+    assert np.array_equal(e_sw.cpu().numpy(), ref)
