@@ -37,6 +37,12 @@ extern "C" {
 #define FM_QUANT_BLOCK 1  /* e4m3, fp32 scale per 128 block                     */
 #define FM_QUANT_POW2 2   /* e4m3, power-of-two fp32 scale per 128 block        */
 #define FM_QUANT_MX 3     /* e4m3, e8m0 scale per 32 block (OCP MXFP8)          */
+/* OR-ed into the kind of fm_quantize / fm_permute / fm_swiglu_quantize /
+ * fm_swiglu_backward: the row scales are stored block-major, s[block * ld_s +
+ * row] (ld_s >= rows), instead of s[row * ld_s + block].  A grouped-GEMM K step
+ * then reads the scales of 256 consecutive rows from one contiguous 1 KiB
+ * span (FmGemmOperand scale_row_stride 1, scale_kb_stride ld_s). */
+#define FM_SCALES_KMAJOR 0x100
 
 /* grouped GEMM arithmetic kinds */
 #define FM_GEMM_BF16 0
@@ -196,14 +202,16 @@ typedef struct FmGemmOperand {
 
 /* Replaces fp8_flow_moe.fp8_grouped_gemm (reference fp8/__init__.py:21) and
  * the per-expert torch.bmm calls of model/moe.py:1588-1591 (forward and
- * dgrad): out[r][n] = sum_k tokens[r][k] * weights_e[n][k] for every 128-row
- * tile r of the padded buffer, e = tile_expert[r/128] (tiles with e < 0, or
- * expert_mask[e] != mask_want when expert_mask != NULL, are skipped -- the
- * fp8_gemm_threshold switch of model/moe.py:1215-1216).  N, K multiples of 128. */
+ * dgrad): out[r][n] = sum_k tokens[r][k] * weights_e[n][k] for the rows r of
+ * expert e, offsets[e] <= r < offsets[e+1] (offsets and tile_expert as written
+ * by fm_route_sort: [E+1] padded group starts and the expert of each 128-row
+ * tile, -1 past the last group).  Experts with expert_mask[e] != mask_want
+ * when expert_mask != NULL are skipped -- the fp8_gemm_threshold switch of
+ * model/moe.py:1215-1216.  N, K multiples of 128. */
 int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
-                             int64_t m_tiles, const int32_t* tile_expert, int E, int64_t N,
-                             int64_t K, const int32_t* expert_mask, int mask_want, void* out,
-                             int out_dtype, int64_t ld_out, void* stream);
+                             int64_t m_tiles, const int32_t* tile_expert, const int32_t* offsets,
+                             int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
+                             void* out, int out_dtype, int64_t ld_out, void* stream);
 
 /* Weight-gradient grouped GEMM (autograd of model/moe.py:1588-1591 with
  * respect to w1/w2/w3): out_e[m][n] = sum over the tokens t of expert e

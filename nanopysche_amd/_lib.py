@@ -22,6 +22,7 @@ QUANT_BF16 = 0
 QUANT_BLOCK = 1
 QUANT_POW2 = 2
 QUANT_MX = 3
+SCALES_KMAJOR = 0x100   # OR-ed into a quant kind: row scales stored block-major
 
 GEMM_BF16 = 0
 GEMM_FP8_F32 = 1
@@ -78,8 +79,8 @@ SIGNATURES = {
                                   _i64, _vp, _i64, _vp, _vp]),
     "fm_swiglu_backward": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp,
                                   _i64, _vp, _i64, _vp, _i64, _vp, _vp]),
-    "fm_grouped_gemm_ragged_m": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _i32, _i64, _i64, _vp, _i32,
-                                        _vp, _i32, _i64, _vp]),
+    "fm_grouped_gemm_ragged_m": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _vp, _i32, _i64, _i64, _vp,
+                                        _i32, _vp, _i32, _i64, _vp]),
     "fm_grouped_gemm_ragged_k": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,
                                         _i64, _vp, _i64, _i64, _i32, _i64, _vp]),
 }

@@ -8,11 +8,13 @@
 // Modes
 //   ragged-M  (forward gate|up and down, dgrad): P = token rows of the padded
 //             expert-contiguous buffer, Q = that expert's weight [N, K];
-//             output C[token][n].  Each 128-token m-tile belongs to exactly one
-//             expert (groups are padded to 128 rows); tile_expert[] maps it.
-//   ragged-K  (weight gradients): contraction over the tokens of expert e,
-//             Q = [M, tokens] and P = [N, tokens] (column-quantised activations),
-//             output C_e[m][n]; rows m >= split go to a second tensor (dW1|dW3).
+//             output C[token][n].  Groups are padded to 128 rows.
+//   ragged-K  (weight gradients): contraction over the tokens of expert e of
+//             a_t [M, tokens] and b_t [N, tokens] (column-quantised
+//             activations), output C_e[m][n]; rows m >= split go to a second
+//             tensor (dW1|dW3).  The 256 x 256 kernel takes P = a_t, Q = b_t
+//             (output rows along j, like ragged-M); the fp32-promotion kernel
+//             takes Q = a_t, P = b_t.
 //
 // Arithmetic kinds
 //   BF16       v_mfma_f32_32x32x16_bf16
@@ -24,12 +26,19 @@
 //              promotion.
 //   FP8_MX     e4m3 with e8m0 scales per 32 (OCP MXFP8), same instruction.
 //
-// Tiling: 256 threads = 4 wave64 as 2 (i) x 2 (j); workgroup tile 256 (i) x
-// 128 (j), each wave 128 x 64 = 4 x 2 MFMA 32x32 blocks; K step 128 bytes
-// (128 e4m3 / 64 bf16).  Operands and scales stream into a 3-stage LDS ring by
-// direct global->LDS loads (see grouped_gemm_kernel).
+// Two kernels, 256 threads = 4 wave64 as 2 (i) x 2 (j), K step 128 bytes
+// (128 e4m3 / 64 bf16), operands streamed into LDS by direct global->LDS loads:
+//   gemm256_kernel  BF16 / FP8_POW2 / FP8_MX.  Tile 256 x 256, each wave
+//                   128 x 128 = 4 x 4 MFMA 32x32 blocks (256 accumulator
+//                   registers), two LDS stages of 66 KiB, fragments of the next
+//                   half step read while the MFMAs of the current one run.
+//                   In ragged-M a 256-token tile covers two 128-row groups of
+//                   one expert; the second half is idle at an odd group end.
+//   gemm_f32_kernel FP8_F32.  Tile 256 x 128 (each wave 128 x 64), three LDS
+//                   stages; the promotion needs a second set of partial-sum
+//                   registers, which the 4 x 4 wave tile has no room for.
 // Workgroup ids are remapped so each XCD walks a contiguous range of tiles,
-// grouped 8 m-tiles at a time for L2 reuse of weights and activations.
+// grouped 8 token tiles at a time for L2 reuse of weights and activations.
 #include "fm_common.h"
 #include "../../include/fm_hip.h"
 
@@ -59,9 +68,10 @@ struct GemmParams {
   int64_t n_i;        // extent of i (rows of Q per group)
   int64_t n_j;        // ragged-K: extent of j (rows of P)
   int64_t K;          // ragged-M: contraction length
-  const int32_t* tile_expert;  // ragged-M
+  const int32_t* tile_expert;  // ragged-M, 256 x 128 kernel: expert of each 128-row tile
   int64_t m_tiles;             // ragged-M: 128-row tiles in the padded buffer
-  const int32_t* offsets;      // ragged-K: [E+1] padded group starts
+  int64_t j_tiles;             // ragged-M, 256 x 256 kernel: bound on 256-row token tiles
+  const int32_t* offsets;      // [E+1] padded group starts (rows)
   int E;
   const int32_t* mask;         // optional per-expert flag; run expert e iff mask[e] == mask_want
   int mask_want;
@@ -84,18 +94,11 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * 128 + ((chunk ^ lds_swz(row)) << 4);
 }
 
-__device__ __forceinline__ float scale_f32(const Operand& o, int64_t g, int64_t row, int64_t kb) {
-  return static_cast<const float*>(o.s)[g * o.s_gs + (row >> o.s_shift) * o.s_row + kb * o.s_kb];
-}
-__device__ __forceinline__ uint32_t scale_e8m0(const Operand& o, int64_t g, int64_t row, int64_t kb) {
-  return static_cast<const uint8_t*>(o.s)[g * o.s_gs + (row >> o.s_shift) * o.s_row + kb * o.s_kb];
-}
-
 // LDS-DMA: the 64 lanes' `size`-byte loads land at consecutive LDS addresses
 // starting at `lds` (wave-uniform); `g` is each lane's own global source.
 // Issued from inline assembly so the compiler's wait insertion does not treat
 // them as pending LDS writes (it would wait for every prefetch in flight before
-// each LDS read); the kernel orders them with explicit vmcnt waits instead.
+// each LDS read); the kernels order them with explicit vmcnt waits instead.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return uint32_t(size_t((__attribute__((address_space(3))) const void*)(p)));
 }
@@ -109,6 +112,12 @@ __device__ __forceinline__ void dma4(const void* g, const void* lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
+// Scalar-base form: wave-uniform 64-bit base `g` plus a 32-bit per-lane offset.
+__device__ __forceinline__ void dma16s(const uint8_t* g, uint32_t voff, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(g), "s"(m)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits [3:0] and [15:14],
@@ -117,16 +126,458 @@ __device__ __forceinline__ void dma4(const void* g, const void* lds) {
 // allows the stage to be refilled.
 #define FM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4))
 
+// A barrier the compiler moves nothing across.  It carries no memory fence,
+// which would wait for the prefetches still in flight.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// ============================================================================
+// 256 x 256 kernel: BF16, FP8_POW2, FP8_MX
+// ============================================================================
+constexpr int kT = 256;
+
+template <int KIND>
+struct Smem256 {
+  static constexpr bool kScaled = KIND != GK_BF16;
+  static constexpr int kOp = kT * 128;                  // one operand, one K step
+  static constexpr int kS = kScaled ? kT * 4 : 0;       // its scales
+  static constexpr int kP = kOp, kQS = 2 * kOp, kPS = 2 * kOp + kS;
+  static constexpr int kStage = 2 * kOp + 2 * kS;
+};
+
+// One 256-row operand tile streams as 32 groups of 8 rows x 128 bytes per K
+// step, 8 groups per wave.  LDS chunk c = 64*group + lane holds row c/8 at
+// swizzled position c%8, so a lane's global offset inside a group depends only
+// on the group's parity.  Groups past the last valid row of the operand re-read
+// the last valid group (their rows produce outputs that are never stored).
+struct OpStream {
+  const uint8_t* base;    // tile row 0 at K offset 0 (wave-uniform)
+  int64_t group_bytes;    // 8 rows
+  uint32_t lane_off[2];   // even / odd group
+  int g_last;
+};
+
+__device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows,
+                                                int lane) {
+  OpStream s;
+  s.base = base;
+  s.group_bytes = 8 * row_bytes;
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int ch = (lane & 7) ^ ((par * 4 + (lane >> 4)) & 7);  // == chunk ^ lds_swz(row)
+    s.lane_off[par] = uint32_t((lane >> 3) * row_bytes + ch * 16);
+  }
+  s.g_last = int(rows / 8) - 1;
+  return s;
+}
+
+__device__ __forceinline__ void stream_issue(const OpStream& s, int64_t kbytes, uint8_t* dst, int wave,
+                                             int u) {
+  const int g = wave * 8 + u;
+  const int gc = g < s.g_last ? g : s.g_last;
+  dma16s(s.base + gc * s.group_bytes + kbytes, s.lane_off[u & 1], dst + g * 1024);
+}
+
+// Per-lane scale DMA sources (one dword per lane per K step and operand).
+struct ScaleSrc {
+  const uint8_t* qs;
+  const uint8_t* ps;
+  int64_t qs_k, ps_k;   // byte advance per K step
+};
+
+// Register fragments of one half of a K step: for e4m3 one 64-deep MFMA slice
+// (4 A + 4 B fragments of 32 bytes per lane, plus their e8m0 scale operands),
+// for bf16 two 16-deep slices.
+template <int KIND>
+struct Frag {
+  v8i a[4], b[4];
+  int sa[4], sb[4];
+};
+template <>
+struct Frag<GK_BF16> {
+  v8bf a[2][4], b[2][4];
+};
+
+// e4m3 fragment rows: lane half h holds K [16h, 16h+16) in bytes 0-15 and
+// K [32+16h, +16) in bytes 16-31 of the 64-deep slice, so bytes 0-15 of both
+// halves form the first 32-deep scale block (scale from lane `row`) and bytes
+// 16-31 the second (scale from lane `row + 32`).
+__device__ __forceinline__ v8i read_frag8(const uint8_t* base, int r, int half, int lhalf) {
+  const int c0 = half * 4 + lhalf;
+  const v4i x0 = *reinterpret_cast<const v4i*>(base + lds_off(r, c0));
+  const v4i x1 = *reinterpret_cast<const v4i*>(base + lds_off(r, c0 + 2));
+  return __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ v8bf read_frag16(const uint8_t* base, int r, int ks, int lhalf) {
+  return __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(base + lds_off(r, ks * 2 + lhalf)));
+}
+
+template <int KIND>
+__device__ __forceinline__ int read_scale(const uint8_t* st, int off, int r, int blk, bool mx_k) {
+  if (KIND == GK_FP8_POW2) return int((f2u(reinterpret_cast<const float*>(st + off)[r]) >> 23) & 0xffu);
+  return mx_k ? st[off + blk * kT + r] : st[off + r * 4 + blk];
+}
+
+struct WaveCoord {
+  int wave, lane, wi, wj, lrow, lhalf;
+  bool q_mx_k, p_mx_k;
+};
+
+// Reads half `half` of the K step held in stage `st`.
+template <int KIND>
+__device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND>& f, const WaveCoord& w) {
+  using SM = Smem256<KIND>;
+  if constexpr (KIND == GK_BF16) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
+        f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
+      }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, half, w.lhalf);
+      f.b[t] = read_frag8(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, half, w.lhalf);
+    }
+    const int blk = half * 2 + w.lhalf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.sa[t] = read_scale<KIND>(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, blk, w.q_mx_k);
+      f.sb[t] = read_scale<KIND>(st, SM::kPS, w.wj * 128 + t * 32 + w.lrow, blk, w.p_mx_k);
+    }
+  }
+}
+
+// Refills stage `dst` with the K step at element offset `k` and reads half 0
+// of the step held in `st`, two DMAs per fragment read.  The DMAs are inline
+// assembly with a memory clobber, so they keep this program order relative to
+// the LDS reads, and the caller's MFMA interleave spreads both between MFMAs.
+template <int KIND>
+__device__ __forceinline__ void refill_and_read_half0(const OpStream& qst, const OpStream& pst,
+                                                      const ScaleSrc& sc, int64_t k, uint8_t* dst,
+                                                      const uint8_t* st, Frag<KIND>& f,
+                                                      const WaveCoord& w) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const int64_t kb = k * ES;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    stream_issue(qst, kb, dst, w.wave, 2 * t);
+    stream_issue(qst, kb, dst, w.wave, 2 * t + 1);
+    if constexpr (KIND == GK_BF16) {
+      f.a[0][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
+      f.a[1][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, 1, w.lhalf);
+    } else {
+      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    stream_issue(pst, kb, dst + SM::kP, w.wave, 2 * t);
+    stream_issue(pst, kb, dst + SM::kP, w.wave, 2 * t + 1);
+    if constexpr (KIND == GK_BF16) {
+      f.b[0][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 0, w.lhalf);
+      f.b[1][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 1, w.lhalf);
+    } else {
+      f.b[t] = read_frag8(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 0, w.lhalf);
+    }
+  }
+  if constexpr (KIND != GK_BF16) {
+    const int64_t ks = k / KSTEP;
+    dma4(sc.qs + ks * sc.qs_k, dst + SM::kQS + w.wave * 256);
+    dma4(sc.ps + ks * sc.ps_k, dst + SM::kPS + w.wave * 256);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.sa[t] = read_scale<KIND>(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, w.lhalf, w.q_mx_k);
+      f.sb[t] = read_scale<KIND>(st, SM::kPS, w.wj * 128 + t * 32 + w.lrow, w.lhalf, w.p_mx_k);
+    }
+  }
+}
+
+template <int KIND>
+__device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
+                                           int64_t k, uint8_t* dst, int wave) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const int64_t kb = k * ES;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) stream_issue(qst, kb, dst, wave, u);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) stream_issue(pst, kb, dst + SM::kP, wave, u);
+  if constexpr (KIND != GK_BF16) {
+    const int64_t ks = k / KSTEP;
+    dma4(sc.qs + ks * sc.qs_k, dst + SM::kQS + wave * 256);
+    dma4(sc.ps + ks * sc.ps_k, dst + SM::kPS + wave * 256);
+  }
+}
+
+template <int KIND>
+__device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][4]) {
+  if constexpr (KIND == GK_BF16) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][a], f.b[s2][b], acc[a][b], 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[a], f.b[b], acc[a][b], 0, 0, 0,
+                                                                   f.sa[a], 0, f.sb[b]);
+  }
+}
+
+// Scheduling pattern for one half step: every MFMA is followed by LDS reads
+// of the next fragments (16 x 64-cycle e4m3 MFMAs or 32 x bf16 MFMAs), so the
+// reads hide behind the matrix pipe.
+template <int KIND>
+__device__ __forceinline__ void interleave_half() {
+  constexpr int kMfma = KIND == GK_BF16 ? 32 : 16;
+  constexpr int kReads = KIND == GK_BF16 ? 1 : 2;
+#pragma unroll
+  for (int i = 0; i < kMfma; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // LDS reads
+  }
+}
+
+template <int KIND, int MODE>
+__global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
+  constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
+  constexpr int NLOAD = 16 + (SM::kScaled ? 2 : 0);   // DMA instructions per wave per step
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
+
+  // ---------------------------------------------------------- tile decode ----
+  const int64_t per_xcd = (p.n_tiles + 7) / 8;
+  const int64_t L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (L >= p.n_tiles) return;
+  const int64_t NI = (p.n_i + kT - 1) / kT;
+  int64_t e = -1, i0 = 0, j0 = 0, j_end = 0, k_lo, k_hi;
+  if (MODE == GM_RAGGED_M) {
+    const int64_t JT = p.j_tiles;
+    const int64_t group = L / (kGroupM * NI);
+    const int64_t first = group * kGroupM;
+    const int64_t gsz = JT - first < kGroupM ? JT - first : kGroupM;
+    int64_t J = first + (L % gsz);
+    i0 = ((L % (kGroupM * NI)) / gsz) * kT;
+    // token tile J -> (expert, rows): expert x holds ceil(rows_x / 256) tiles
+    for (int x = 0; x < p.E; ++x) {
+      const int64_t o0 = p.offsets[x], o1 = p.offsets[x + 1];
+      const int64_t cnt = (o1 - o0 + kT - 1) / kT;
+      if (J < cnt) {
+        e = x;
+        j0 = o0 + J * kT;
+        j_end = o1;
+        break;
+      }
+      J -= cnt;
+    }
+    if (e < 0) return;
+    k_lo = 0;
+    k_hi = p.K;
+  } else {
+    const int64_t NJ = (p.n_j + kT - 1) / kT;
+    const int64_t per_e = NI * NJ;
+    e = L / per_e;
+    const int64_t Lr = L % per_e;
+    const int64_t group = Lr / (kGroupM * NJ);
+    const int64_t first = group * kGroupM;
+    const int64_t gsz = NI - first < kGroupM ? NI - first : kGroupM;
+    i0 = (first + (Lr % gsz)) * kT;
+    j0 = ((Lr % (kGroupM * NJ)) / gsz) * kT;
+    j_end = p.n_j;
+    k_lo = p.offsets[e];
+    k_hi = p.offsets[e + 1];
+  }
+  if (p.mask != nullptr && p.mask[e] != p.mask_want) return;
+
+  WaveCoord w;
+  w.lane = threadIdx.x & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  w.wi = w.wave >> 1;   // wave tile: i [128*wi, +128), j [128*wj, +128)
+  w.wj = w.wave & 1;
+  w.lrow = w.lane & 31;
+  w.lhalf = w.lane >> 5;
+  w.q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
+  w.p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
+  const int64_t q_group = MODE == GM_RAGGED_M ? e : 0;
+  // valid rows of each operand tile (multiples of 128: n_i, n_j and the group
+  // ends are)
+  const int64_t q_rows = p.n_i - i0 < kT ? p.n_i - i0 : kT;
+  const int64_t p_rows = j_end - j0 < kT ? j_end - j0 : kT;
+
+  const OpStream qst = make_stream(p.Q.p + (q_group * p.Q.gs + i0 * p.Q.ld) * ES, p.Q.ld * ES, q_rows, w.lane);
+  const OpStream pst = make_stream(p.P.p + j0 * p.P.ld * ES, p.P.ld * ES, p_rows, w.lane);
+
+  // Scales: one dword per lane and operand per K step.  fp32 / pow2 and
+  // row-major MX: lane = row (four consecutive 32-block bytes for MX); MX in
+  // k-major layout: lane packs four consecutive rows of one 32-block, so LDS
+  // holds [block][row] bytes.  Rows past the valid ones re-read the last one.
+  ScaleSrc sc{nullptr, nullptr, 0, 0};
+  if constexpr (SM::kScaled) {
+    const int li = w.wave * 64 + w.lane;   // 0..255
+    const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
+    if (w.q_mx_k) {
+      int64_t gr = i0 + (li * 4) % kT;
+      gr = gr + 4 <= i0 + q_rows ? gr : i0 + q_rows - 4;
+      sc.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + gr * p.Q.s_row + (li / 64) * p.Q.s_kb);
+    } else {
+      const int64_t gr = i0 + (li < q_rows ? li : q_rows - 1);
+      sc.qs = static_cast<const uint8_t*>(p.Q.s) +
+              (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * sbytes;
+    }
+    if (w.p_mx_k) {
+      int64_t gr = j0 + (li * 4) % kT;
+      gr = gr + 4 <= j0 + p_rows ? gr : j0 + p_rows - 4;
+      sc.ps = static_cast<const uint8_t*>(p.P.s) + (gr * p.P.s_row + (li / 64) * p.P.s_kb);
+    } else {
+      const int64_t gr = j0 + (li < p_rows ? li : p_rows - 1);
+      sc.ps = static_cast<const uint8_t*>(p.P.s) + ((gr >> p.P.s_shift) * p.P.s_row) * sbytes;
+    }
+    // per K step: one 128-block (pow2 scales) or four 32-blocks (MX)
+    sc.qs_k = (KIND == GK_FP8_MX ? 4 : 1) * p.Q.s_kb * sbytes;
+    sc.ps_k = (KIND == GK_FP8_MX ? 4 : 1) * p.P.s_kb * sbytes;
+  }
+
+  v16f acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  // Two-stage pipeline, K step t in stage t % 2, each step split in halves:
+  //   A  read half 1 of step t                 (stage t % 2)
+  //   B  MFMAs of half 0 of step t             (registers read during step t-1)
+  //   C  wait for step t+1's DMA and this wave's reads, barrier: every wave is
+  //      done with stage t % 2 and step t+1 has landed in stage (t+1) % 2
+  //   D  refill stage t % 2 with step t+2; read half 0 of step t+1
+  //   E  MFMAs of half 1 of step t
+  // Every step issues the same DMA group (clamped to the last step at the end;
+  // the re-read lands in a stage nobody reads again), which keeps the loop body
+  // one basic block.
+  const int64_t nk = (k_hi - k_lo) / KSTEP;
+  if (nk > 0) {
+    Frag<KIND> f0, f1;
+    issue_step<KIND>(qst, pst, sc, k_lo, smem, w.wave);
+    issue_step<KIND>(qst, pst, sc, k_lo + (nk > 1 ? KSTEP : 0), smem + SM::kStage, w.wave);
+    FM_WAIT_VMCNT(NLOAD);
+    block_barrier();
+    read_half<KIND>(smem, 0, f0, w);
+    int cur_off = 0;
+#pragma unroll 1
+    for (int64_t t = 0; t < nk; ++t) {
+      const int nxt_off = SM::kStage - cur_off;
+      read_half<KIND>(smem + cur_off, 1, f1, w);                                        // A
+      mma_half<KIND>(f0, acc);                                                          // B
+      interleave_half<KIND>();
+      FM_WAIT_VMCNT(0);                                                                 // C
+      block_barrier();
+      const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
+      refill_and_read_half0<KIND>(qst, pst, sc, k_lo + tn * KSTEP, smem + cur_off, smem + nxt_off, f0, w);  // D
+      mma_half<KIND>(f1, acc);                                                          // E
+      interleave_half<KIND>();
+      cur_off = nxt_off;
+    }
+    FM_WAIT_VMCNT(0);  // no LDS-DMA may still be in flight when the workgroup exits
+  }
+
+  // -------------------------------------------------------------- epilogue ----
+  // The output row is j (a token in ragged-M, an m row of the weight gradient
+  // in ragged-K, whose operands the launcher swapped) and the contiguous
+  // column is i, so each lane holds 4 consecutive columns of one row.  n_i,
+  // the valid rows and split are multiples of 128: every bound below holds or
+  // fails for a wave's whole 128 x 128 block.
+  const int wi = w.wi, wj = w.wj, lrow = w.lrow, lhalf = w.lhalf, lane = w.lane;
+  const int64_t ib = i0 + wi * 128, jb = j0 + wj * 128;
+  const bool live = ib < p.n_i && jb < j0 + p_rows;
+  // start of output row jb, column ib
+  int64_t row_off;
+  void* C;
+  if (MODE == GM_RAGGED_M) {
+    C = p.C;
+    row_off = jb * p.ldC + ib;
+  } else {
+    const bool second = jb >= p.split;
+    C = second ? p.C2 : p.C;
+    row_off = e * (second ? p.c2_gs : p.c_gs) + (second ? jb - p.split : jb) * p.ldC + ib;
+  }
+  if (!p.out_f32) {
+    // bf16: each wave stages its 128 x 128 block in its own 32 KiB of LDS and
+    // writes it back as whole 256-byte row segments.  Every wave's DMAs have
+    // landed and every read of the pipeline stages is done after this barrier.
+    block_barrier();
+    if (!live) return;
+    uint8_t* W = smem + w.wave * 32768;
+    // LDS [row jr][column ic], 16-byte chunk ic/8 swizzled with jr % 16
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int jr = b * 32 + lrow;
+          uint2 v;
+          v.x = hw_bf16x2(acc[a][b][4 * q], acc[a][b][4 * q + 1]);
+          v.y = hw_bf16x2(acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+          *reinterpret_cast<uint2*>(W + jr * 256 + (((a * 4 + q) ^ (jr & 15)) << 4) + lhalf * 8) = v;
+        }
+    // 16 lanes x 16 bytes per 128-column row, 4 rows per pass
+    const int c = lane & 15;
+    uint16_t* dst = static_cast<uint16_t*>(C) + row_off + c * 8;
+    const bool vec16 = (p.ldC & 7) == 0;
+#pragma unroll 4
+    for (int n = 0; n < 32; ++n) {
+      const int rr = n * 4 + (lane >> 4);
+      const uint4 v = *reinterpret_cast<const uint4*>(W + rr * 256 + ((c ^ (rr & 15)) << 4));
+      uint16_t* d = dst + rr * p.ldC;
+      if (vec16) {
+        *reinterpret_cast<uint4*>(d) = v;
+      } else {
+        reinterpret_cast<uint2*>(d)[0] = make_uint2(v.x, v.y);
+        reinterpret_cast<uint2*>(d)[1] = make_uint2(v.z, v.w);
+      }
+    }
+    return;
+  }
+  if (!live) return;
+  // fp32: straight from the accumulators, 4 consecutive columns per lane
+  float* dst = static_cast<float*>(C) + row_off + lrow * p.ldC + 4 * lhalf;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) =
+            make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+}
+
+// ============================================================================
+// 256 x 128 kernel: FP8_F32 (fp32 block scales, promotion per 128-deep block)
+// ============================================================================
 constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
 constexpr int kBJ = 128;   // workgroup tile along j (tokens / N)
 
-template <int KIND>
-struct GemmSmem {
-  static constexpr bool kScaled = KIND != GK_BF16;
+struct SmemF32 {
   static constexpr int kQ = kBI * 128;                 // operand bytes per stage
   static constexpr int kP = kBJ * 128;
-  static constexpr int kQS = kScaled ? kBI * 4 : 0;   // scale bytes per stage
-  static constexpr int kPS = kScaled ? kBI * 4 : 0;  // 256 slots, the upper 128 unused
+  static constexpr int kQS = kBI * 4;                  // scale bytes per stage
+  static constexpr int kPS = kBI * 4;                  // 256 slots, the upper 128 unused
   static constexpr int kStage = kQ + kP + kQS + kPS;
 };
 
@@ -139,331 +590,63 @@ struct TileSrc {
   int64_t qs_k, ps_k;    // scale byte advance per K step
 };
 
-template <int KIND>
-__device__ __forceinline__ void gemm_issue(const TileSrc& src, int64_t k, uint8_t* stage, int wave,
-                                           int lane) {
-  using SM = GemmSmem<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
-  constexpr int KSTEP = 128 / ES;
-  const int64_t kb = k * ES;
+__device__ __forceinline__ void f32_issue(const TileSrc& src, int64_t k, uint8_t* stage, int wave) {
+  using SM = SmemF32;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) dma16(src.q[u] + kb, stage + (wave * 8 + u) * 1024);
+  for (int u = 0; u < 8; ++u) dma16(src.q[u] + k, stage + (wave * 8 + u) * 1024);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) dma16(src.p[u] + kb, stage + SM::kQ + (wave * 4 + u) * 1024);
-  if (SM::kScaled) {
-    const int64_t ks = k / KSTEP;
-    dma4(src.qs + ks * src.qs_k, stage + SM::kQ + SM::kP + wave * 256);
-    dma4(src.ps + ks * src.ps_k, stage + SM::kQ + SM::kP + SM::kQS + wave * 256);
-  }
+  for (int u = 0; u < 4; ++u) dma16(src.p[u] + k, stage + SM::kQ + (wave * 4 + u) * 1024);
+  const int64_t ks = k / 128;
+  dma4(src.qs + ks * src.qs_k, stage + SM::kQ + SM::kP + wave * 256);
+  dma4(src.ps + ks * src.ps_k, stage + SM::kQ + SM::kP + SM::kQS + wave * 256);
 }
 
-// One 128-byte K step from a stage: 4 x 2 MFMA 32x32 blocks per wave.
-template <int KIND, int MODE>
-__device__ __forceinline__ void gemm_compute(const uint8_t* st, v16f (&acc)[4][2], int wi, int wj,
-                                             int lrow, int lhalf, bool q_mx_k, bool p_mx_k) {
-  using SM = GemmSmem<KIND>;
+// One 128-deep K step from a stage: 4 x 2 MFMA 32x32 blocks per wave, each
+// 128-deep partial sum promoted with the product of the block scales.
+template <int MODE>
+__device__ __forceinline__ void f32_compute(const uint8_t* st, v16f (&acc)[4][2], int wi, int wj,
+                                            int lrow, int lhalf) {
+  using SM = SmemF32;
   const uint8_t* lq = st;
   const uint8_t* lp = st + SM::kQ;
   const float* qs = reinterpret_cast<const float*>(st + SM::kQ + SM::kP);
   const float* ps = reinterpret_cast<const float*>(st + SM::kQ + SM::kP + SM::kQS);
-  const uint8_t* qs8 = st + SM::kQ + SM::kP;
-  const uint8_t* ps8 = st + SM::kQ + SM::kP + SM::kQS;
-  if (KIND == GK_BF16) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      v8bf fa[4], fb[2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        fa[t] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + t * 32 + lrow, ks * 2 + lhalf)));
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        fb[t] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + t * 32 + lrow, ks * 2 + lhalf)));
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-    }
-    return;
-  }
-  // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in bytes 0-15 and
-  // K [32+16h, +16) in bytes 16-31, so bytes 0-15 of both halves form the first
-  // 32-deep scale block (scale from lane `row`) and bytes 16-31 the second
-  // (scale from lane `row + 32`).
   v8i fa[2][4], fb[2][2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int c0 = ks * 4 + lhalf, c1 = c0 + 2;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = wi * 128 + t * 32 + lrow;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(lq + lds_off(r, c0));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(lq + lds_off(r, c1));
-      fa[ks][t] = v8i{int(x0.x), int(x0.y), int(x0.z), int(x0.w), int(x1.x), int(x1.y), int(x1.z), int(x1.w)};
-    }
+    for (int t = 0; t < 4; ++t) fa[ks][t] = read_frag8(lq, wi * 128 + t * 32 + lrow, ks, lhalf);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wj * 64 + t * 32 + lrow;
-      const uint4 x0 = *reinterpret_cast<const uint4*>(lp + lds_off(r, c0));
-      const uint4 x1 = *reinterpret_cast<const uint4*>(lp + lds_off(r, c1));
-      fb[ks][t] = v8i{int(x0.x), int(x0.y), int(x0.z), int(x0.w), int(x1.x), int(x1.y), int(x1.z), int(x1.w)};
-    }
+    for (int t = 0; t < 2; ++t) fb[ks][t] = read_frag8(lp, wj * 64 + t * 32 + lrow, ks, lhalf);
   }
-  if (KIND == GK_FP8_F32) {
-    // 128-deep partial sums, promoted with the product of the block scales
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        v16f part;
+    for (int b = 0; b < 2; ++b) {
+      v16f part;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[r] = 0.f;
-        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[0][a], fb[0][b], part, 0, 0, 0, 127, 0, 127);
-        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[1][a], fb[1][b], part, 0, 0, 0, 127, 0, 127);
-        const float sp = ps[wj * 64 + b * 32 + lrow];
-        if (MODE == GM_RAGGED_M) {
-          const float sc = qs[wi * 128] * sp;  // a wave's 128 rows are one 128x128 weight block
+      for (int r = 0; r < 16; ++r) part[r] = 0.f;
+      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[0][a], fb[0][b], part, 0, 0, 0, 127, 0, 127);
+      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[1][a], fb[1][b], part, 0, 0, 0, 127, 0, 127);
+      const float sp = ps[wj * 64 + b * 32 + lrow];
+      if (MODE == GM_RAGGED_M) {
+        const float s = qs[wi * 128] * sp;  // a wave's 128 rows are one 128x128 weight block
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[a][b][r] += part[r] * sc;
-        } else {
+        for (int r = 0; r < 16; ++r) acc[a][b][r] += part[r] * s;
+      } else {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int ii = wi * 128 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-            acc[a][b][r] += part[r] * (qs[ii] * sp);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int ii = wi * 128 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          acc[a][b][r] += part[r] * (qs[ii] * sp);
         }
       }
-    return;
-  }
-  int sa[2][4], sb[2][2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int blk = ks * 2 + lhalf;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = wi * 128 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) sa[ks][t] = int((f2u(qs[r]) >> 23) & 0xffu);
-      else sa[ks][t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
     }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wj * 64 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) sb[ks][t] = int((f2u(ps[r]) >> 23) & 0xffu);
-      else sb[ks][t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
-    }
-  }
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[ks][a], fb[ks][b], acc[a][b], 0, 0,
-                                                                   0, sa[ks][a], 0, sb[ks][b]);
 }
 
-// Register fragments for one half of a 128-byte K step: for e4m3 one 64-deep
-// MFMA K slice (4 A + 2 B fragments of 32 bytes per lane, plus their e8m0
-// scale operands), for bf16 two 16-deep slices.
-template <int KIND>
-struct HalfFrag {
-  v8i a[4], b[2];
-  int sa[4], sb[2];
-};
-template <>
-struct HalfFrag<GK_BF16> {
-  v8bf a[2][4], b[2][2];
-};
-
-// Loads half `half` (0 or 1) of the K step held in stage `st`.
-template <int KIND>
-__device__ __forceinline__ void load_half(const uint8_t* st, int half, HalfFrag<KIND>& f, int wi, int wj,
-                                          int lrow, int lhalf, bool q_mx_k, bool p_mx_k) {
-  using SM = GemmSmem<KIND>;
-  const uint8_t* lq = st;
-  const uint8_t* lp = st + SM::kQ;
-  if constexpr (KIND == GK_BF16) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const int ks = half * 2 + s2;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        f.a[s2][t] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + t * 32 + lrow, ks * 2 + lhalf)));
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        f.b[s2][t] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + t * 32 + lrow, ks * 2 + lhalf)));
-    }
-  } else {
-    // 32x32x64 e4m3 fragment: lane half h holds K [16h, 16h+16) in bytes 0-15
-    // and K [32+16h, +16) in bytes 16-31; bytes 0-15 of both halves form the
-    // first 32-deep scale block (scale from lane `row`), bytes 16-31 the second
-    // (scale from lane `row + 32`).
-    const int c0 = half * 4 + lhalf, c1 = c0 + 2;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = wi * 128 + t * 32 + lrow;
-      const v4i x0 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c0));
-      const v4i x1 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c1));
-      f.a[t] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wj * 64 + t * 32 + lrow;
-      const v4i x0 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c0));
-      const v4i x1 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c1));
-      f.b[t] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    const float* qs = reinterpret_cast<const float*>(st + SM::kQ + SM::kP);
-    const float* ps = reinterpret_cast<const float*>(st + SM::kQ + SM::kP + SM::kQS);
-    const uint8_t* qs8 = st + SM::kQ + SM::kP;
-    const uint8_t* ps8 = st + SM::kQ + SM::kP + SM::kQS;
-    const int blk = half * 2 + lhalf;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = wi * 128 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) f.sa[t] = int((f2u(qs[r]) >> 23) & 0xffu);
-      else f.sa[t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wj * 64 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) f.sb[t] = int((f2u(ps[r]) >> 23) & 0xffu);
-      else f.sb[t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
-    }
-  }
-}
-
-template <int KIND>
-__device__ __forceinline__ void mma_half(const HalfFrag<KIND>& f, v16f (&acc)[4][2]) {
-  if constexpr (KIND == GK_BF16) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][a], f.b[s2][b], acc[a][b], 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-        acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[a], f.b[b], acc[a][b], 0, 0, 0,
-                                                                   f.sa[a], 0, f.sb[b]);
-  }
-}
-
-// Phase C/D of the pipelined loop: refills stage `cur` with K step `k` (the 14
-// DMA instructions of gemm_issue) and loads half 0 of the next step from
-// `nxt`, two DMAs per group of fragment reads.  The DMAs are inline assembly
-// with a memory clobber, so they keep this program order relative to the LDS
-// reads, and the MFMA interleave pattern of the caller spreads both between
-// the MFMAs instead of queueing all DMAs ahead of them.
-template <int KIND>
-__device__ __forceinline__ void refill_and_load_half0(const TileSrc& src, int64_t k, uint8_t* cur,
-                                                      const uint8_t* nxt, HalfFrag<KIND>& f, int wave,
-                                                      int lane, int wi, int wj, int lrow, int lhalf,
-                                                      bool q_mx_k, bool p_mx_k) {
-  using SM = GemmSmem<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
-  constexpr int KSTEP = 128 / ES;
-  const int64_t kb = k * ES;
-  const uint8_t* lq = nxt;
-  const uint8_t* lp = nxt + SM::kQ;
-  if constexpr (KIND == GK_BF16) {
-    // half 0 = substeps 0 and 1: A fragments t = 0..3, B fragments t = 0..1
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      dma16(src.q[2 * u] + kb, cur + (wave * 8 + 2 * u) * 1024);
-      dma16(src.q[2 * u + 1] + kb, cur + (wave * 8 + 2 * u + 1) * 1024);
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-        f.a[s2][u] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lq + lds_off(wi * 128 + u * 32 + lrow, s2 * 2 + lhalf)));
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      dma16(src.p[2 * u] + kb, cur + SM::kQ + (wave * 4 + 2 * u) * 1024);
-      dma16(src.p[2 * u + 1] + kb, cur + SM::kQ + (wave * 4 + 2 * u + 1) * 1024);
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-        f.b[s2][u] = __builtin_bit_cast(
-            v8bf, *reinterpret_cast<const uint4*>(lp + lds_off(wj * 64 + u * 32 + lrow, s2 * 2 + lhalf)));
-    }
-  } else {
-    const int c0 = lhalf, c1 = c0 + 2;  // half 0
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      dma16(src.q[2 * u] + kb, cur + (wave * 8 + 2 * u) * 1024);
-      dma16(src.q[2 * u + 1] + kb, cur + (wave * 8 + 2 * u + 1) * 1024);
-      const int r = wi * 128 + u * 32 + lrow;
-      const v4i x0 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c0));
-      const v4i x1 = *reinterpret_cast<const v4i*>(lq + lds_off(r, c1));
-      f.a[u] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      dma16(src.p[2 * u] + kb, cur + SM::kQ + (wave * 4 + 2 * u) * 1024);
-      dma16(src.p[2 * u + 1] + kb, cur + SM::kQ + (wave * 4 + 2 * u + 1) * 1024);
-      const int r = wj * 64 + u * 32 + lrow;
-      const v4i x0 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c0));
-      const v4i x1 = *reinterpret_cast<const v4i*>(lp + lds_off(r, c1));
-      f.b[u] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    const int64_t ks = k / KSTEP;
-    dma4(src.qs + ks * src.qs_k, cur + SM::kQ + SM::kP + wave * 256);
-    dma4(src.ps + ks * src.ps_k, cur + SM::kQ + SM::kP + SM::kQS + wave * 256);
-    const float* qs = reinterpret_cast<const float*>(nxt + SM::kQ + SM::kP);
-    const float* ps = reinterpret_cast<const float*>(nxt + SM::kQ + SM::kP + SM::kQS);
-    const uint8_t* qs8 = nxt + SM::kQ + SM::kP;
-    const uint8_t* ps8 = nxt + SM::kQ + SM::kP + SM::kQS;
-    const int blk = lhalf;  // half 0
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = wi * 128 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) f.sa[t] = int((f2u(qs[r]) >> 23) & 0xffu);
-      else f.sa[t] = q_mx_k ? qs8[blk * kBI + r] : qs8[r * 4 + blk];
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wj * 64 + t * 32 + lrow;
-      if (KIND == GK_FP8_POW2) f.sb[t] = int((f2u(ps[r]) >> 23) & 0xffu);
-      else f.sb[t] = p_mx_k ? ps8[blk * kBJ + r] : ps8[r * 4 + blk];
-    }
-  }
-}
-
-// Scheduling pattern for one half step: each MFMA is followed by LDS reads of
-// the next fragments, so the MFMA pipe never waits for operands and the reads
-// hide behind the MFMAs (8 x 64-cycle e4m3 MFMAs, or 16 x bf16 MFMAs).
-template <int KIND>
-__device__ __forceinline__ void interleave_mfma_lds() {
-  constexpr int kMfma = KIND == GK_BF16 ? 16 : 8;
-  constexpr int kReads = KIND == GK_BF16 ? 1 : 2;
-#pragma unroll
-  for (int i = 0; i < kMfma; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // LDS reads
-  }
-}
-
-__device__ __forceinline__ void block_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int KIND, int MODE>
-__global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
-  using SM = GemmSmem<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
-  constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
-  constexpr bool SCALED = SM::kScaled;
-  constexpr int NLOAD = 12 + (SCALED ? 2 : 0);        // DMA instructions per wave per step
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
+  using SM = SmemF32;
+  constexpr int NLOAD = 14;   // DMA instructions per wave per step
   // three pipeline stages of one K step each (operands + scales)
   __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * SM::kStage];
   uint8_t* const smem0 = smem;
@@ -521,47 +704,25 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
     const int row = c >> 3, ch = (c & 7) ^ lds_swz(row);
     int64_t gr = i0 + row;
     gr = gr < i_last ? gr : i_last;
-    src.q[u] = p.Q.p + (q_group * p.Q.gs + gr * p.Q.ld) * ES + ch * 16;
+    src.q[u] = p.Q.p + (q_group * p.Q.gs + gr * p.Q.ld) + ch * 16;
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int c = (wave * 4 + u) * 64 + lane;
     const int row = c >> 3, ch = (c & 7) ^ lds_swz(row);
-    src.p[u] = p.P.p + ((j0 + row) * p.P.ld) * ES + ch * 16;
+    src.p[u] = p.P.p + ((j0 + row) * p.P.ld) + ch * 16;
   }
   // Scales: one row per lane, Q 256 rows, P 128 rows (lanes for P rows 128-255
   // re-read row 127 into unused slots, so every wave issues the same loads).
-  // MX scales in k-major layout pack four consecutive rows of one 32-block per
-  // lane instead ([block][row] bytes in LDS).
-  const bool q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
-  const bool p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
-  src.qs = src.ps = nullptr;
-  src.qs_k = src.ps_k = 0;
-  if (SCALED) {
-    const int qi = wave * 64 + lane;           // 0..255
-    const int pi = wave * 64 + lane;           // 0..255, rows >= 128 clamped below
-    const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
-    if (q_mx_k) {
-      const int b = (qi * 4) / kBI, row = (qi * 4) % kBI;
-      int64_t gr = i0 + row;
-      gr = gr + 3 <= i_last ? gr : i_last - 3;  // n_i is a multiple of 128
-      src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + gr * p.Q.s_row + b * p.Q.s_kb);
-    } else {
-      int64_t gr = i0 + qi;
-      gr = gr < i_last ? gr : i_last;
-      src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * sbytes;
-    }
-    if (p_mx_k) {
-      const int pc = pi < 128 ? pi : 127;      // 4 blocks x 128 rows = 128 lanes of 4 bytes
-      const int b = (pc * 4) / kBJ, row = (pc * 4) % kBJ;
-      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + row) * p.P.s_row + b * p.P.s_kb);
-    } else {
-      const int pc = pi < kBJ ? pi : kBJ - 1;
-      src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + pc) >> p.P.s_shift) * p.P.s_row * sbytes;
-    }
-    // per K step: one 128-block (fp32 / pow2 scales) or four 32-blocks (MX)
-    src.qs_k = (KIND == GK_FP8_MX ? 4 : 1) * p.Q.s_kb * sbytes;
-    src.ps_k = (KIND == GK_FP8_MX ? 4 : 1) * p.P.s_kb * sbytes;
+  {
+    const int qi = wave * 64 + lane;
+    int64_t gr = i0 + qi;
+    gr = gr < i_last ? gr : i_last;
+    src.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * 4;
+    const int pc = qi < kBJ ? qi : kBJ - 1;
+    src.ps = static_cast<const uint8_t*>(p.P.s) + ((j0 + pc) >> p.P.s_shift) * p.P.s_row * 4;
+    src.qs_k = p.Q.s_kb * 4;
+    src.ps_k = p.P.s_kb * 4;
   }
 
   v16f acc[4][2];
@@ -575,89 +736,35 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
   // Pipeline: stage t % 3 is filled two steps ahead.  Readiness of a stage is
   // this wave's own vmcnt wait (DMA writes land in LDS before the counter
   // drops) followed by a barrier; a stage is refilled only after every wave has
-  // passed the barrier that follows its last read of it.  The barrier carries
-  // no memory fence, which would wait for the prefetches still in flight.
-  const int64_t nk = (k_hi - k_lo) / KSTEP;
-  if constexpr (KIND == GK_FP8_F32) {
-    // fp32 block scales: each 128-deep partial sum is promoted as a whole, so
-    // this kind keeps the one-barrier-per-step loop over whole K steps.
-    if (nk > 0) gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
-    if (nk > 1) gemm_issue<KIND>(src, k_lo + KSTEP, smem1, wave, lane);
-    // Main loop: steps with a successor, whose loads are always in flight here,
-    // so an unconditional vmcnt(NLOAD) retires exactly the current stage's DMA
-    // (the compiler's wait tracking follows it and adds no wait of its own as
-    // long as every body issues the same loads).
-    int64_t t = 0;
-    while (t + 1 < nk) {
-  #pragma unroll
-      for (int u = 0; u < 3; ++u) {
-        if (t + 1 >= nk) break;
-        FM_WAIT_VMCNT(NLOAD);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        uint8_t* nxt = u == 0 ? smem2 : (u == 1 ? smem0 : smem1);
-        const uint8_t* cur = u == 0 ? smem0 : (u == 1 ? smem1 : smem2);
-        // unconditional (keeps the compiler's wait tracking exact): at t = nk-2
-        // this re-reads step nk-1 into the stage of step nk, which is never read
-        const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
-        gemm_issue<KIND>(src, k_lo + tn * KSTEP, nxt, wave, lane);
-        gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
-        ++t;
-      }
-    }
-    if (t < nk) {  // last step: nothing else in flight
-      FM_WAIT_VMCNT(0);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      const int sidx = int(t % 3);
-      const uint8_t* cur = sidx == 0 ? smem0 : (sidx == 1 ? smem1 : smem2);
-      gemm_compute<KIND, MODE>(cur, acc, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
-    }
-
-
-  } else {
-    // Register-pipelined loop.  Every K step t is split in two halves; while
-    // the MFMAs of one half run, the fragments of the next half are read:
-    //   A  read half 1 of step t          (stage t % 3)
-    //   B  MFMAs of half 0 of step t      (registers loaded during step t-1)
-    //   C  wait for step t+1's DMA, barrier, refill stage t % 3 with step t+3
-    //   D  read half 0 of step t+1        (stage (t+1) % 3)
-    //   E  MFMAs of half 1 of step t
-    // Each step issues exactly one group of DMA loads (clamped to the last step
-    // at the end; the re-read lands in a stage nobody reads again), so
-    // vmcnt(NLOAD) always retires exactly step t+1's group at C.
-    HalfFrag<KIND> f0, f1;
-    if (nk > 0) {
-      gemm_issue<KIND>(src, k_lo, smem0, wave, lane);
-      gemm_issue<KIND>(src, k_lo + (nk > 1 ? 1 : 0) * KSTEP, smem1, wave, lane);
-      gemm_issue<KIND>(src, k_lo + (nk > 2 ? 2 : nk - 1) * KSTEP, smem2, wave, lane);
-      FM_WAIT_VMCNT(2 * NLOAD);
+  // passed the barrier that follows its last read of it.
+  const int64_t nk = (k_hi - k_lo) / 128;
+  if (nk > 0) f32_issue(src, k_lo, smem0, wave);
+  if (nk > 1) f32_issue(src, k_lo + 128, smem1, wave);
+  // Main loop: steps with a successor, whose loads are always in flight here,
+  // so an unconditional vmcnt(NLOAD) retires exactly the current stage's DMA.
+  int64_t t = 0;
+  while (t + 1 < nk) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      if (t + 1 >= nk) break;
+      FM_WAIT_VMCNT(NLOAD);
       block_barrier();
-      load_half<KIND>(smem0, 0, f0, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);
+      uint8_t* nxt = u == 0 ? smem2 : (u == 1 ? smem0 : smem1);
+      const uint8_t* cur = u == 0 ? smem0 : (u == 1 ? smem1 : smem2);
+      // unconditional: at t = nk-2 this re-reads step nk-1 into the stage of
+      // step nk, which is never read
+      const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
+      f32_issue(src, k_lo + tn * 128, nxt, wave);
+      f32_compute<MODE>(cur, acc, wi, wj, lrow, lhalf);
+      ++t;
     }
-    int cur_off = 0;  // byte offset of stage t % 3
-#pragma unroll 1
-    for (int64_t t = 0; t < nk; ++t) {
-      const int nxt_off = cur_off == 2 * SM::kStage ? 0 : cur_off + SM::kStage;
-      uint8_t* cur = smem + cur_off;
-      load_half<KIND>(cur, 1, f1, wi, wj, lrow, lhalf, q_mx_k, p_mx_k);   // A
-      mma_half<KIND>(f0, acc);                                               // B
-      interleave_mfma_lds<KIND>();
-      FM_WAIT_VMCNT(NLOAD);                                                  // C
-      block_barrier();
-      // C+D: refill this stage with step t+3 and read half 0 of step t+1
-      // (unconditional: after the last step it reads a stage holding valid data
-      // that is never used, which keeps the body one basic block)
-      const int64_t tn = t + 3 < nk ? t + 3 : nk - 1;
-      refill_and_load_half0<KIND>(src, k_lo + tn * KSTEP, cur, smem + nxt_off, f0, wave, lane, wi, wj,
-                                  lrow, lhalf, q_mx_k, p_mx_k);
-      mma_half<KIND>(f1, acc);                                               // E
-      interleave_mfma_lds<KIND>();
-      cur_off = nxt_off;
-    }
-    FM_WAIT_VMCNT(0);  // no LDS-DMA may still be in flight when the workgroup exits
+  }
+  if (t < nk) {  // last step: nothing else in flight
+    FM_WAIT_VMCNT(0);
+    block_barrier();
+    const int sidx = int(t % 3);
+    const uint8_t* cur = sidx == 0 ? smem0 : (sidx == 1 ? smem1 : smem2);
+    f32_compute<MODE>(cur, acc, wi, wj, lrow, lhalf);
   }
 
   // -------------------------------------------------------------- epilogue ----
@@ -677,10 +784,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
                 make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
           } else {
             uint16_t* dst = static_cast<uint16_t*>(p.C) + j * p.ldC + i;
-            uint2 w;
-            w.x = uint32_t(f32_to_bf16(acc[a][b][4 * q])) | (uint32_t(f32_to_bf16(acc[a][b][4 * q + 1])) << 16);
-            w.y = uint32_t(f32_to_bf16(acc[a][b][4 * q + 2])) | (uint32_t(f32_to_bf16(acc[a][b][4 * q + 3])) << 16);
-            *reinterpret_cast<uint2*>(dst) = w;
+            uint2 v;
+            v.x = hw_bf16x2(acc[a][b][4 * q], acc[a][b][4 * q + 1]);
+            v.y = hw_bf16x2(acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+            *reinterpret_cast<uint2*>(dst) = v;
           }
         }
       } else {
@@ -699,19 +806,35 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmParams p) {
     }
 }
 
-template <int KIND, int MODE>
-void launch_gemm(const GemmParams& p, hipStream_t s) {
-  const int64_t grid = (p.n_tiles + 7) / 8 * 8;
-  hipLaunchKernelGGL((grouped_gemm_kernel<KIND, MODE>), dim3(unsigned(grid)), dim3(256), 0, s, p);
-}
-
+// ============================================================================
+// launch
+// ============================================================================
 template <int MODE>
-int dispatch_gemm(int kind, const GemmParams& p, hipStream_t s) {
+int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
+  if (MODE == GM_RAGGED_K && kind != GK_FP8_F32) {
+    // the 256 x 256 kernel writes rows along j: put the output's row operand
+    // (a_t, M rows) on the P side and its column operand (b_t) on the Q side
+    const Operand t = p.P;
+    p.P = p.Q;
+    p.Q = t;
+    const int64_t n = p.n_i;
+    p.n_i = p.n_j;
+    p.n_j = n;
+  }
+  const int64_t NI256 = (p.n_i + kT - 1) / kT;
+  if (kind == GK_FP8_F32) {
+    const int64_t NI = (p.n_i + kBI - 1) / kBI;
+    p.n_tiles = MODE == GM_RAGGED_M ? p.m_tiles * NI : int64_t(p.E) * NI * (p.n_j / kBJ);
+  } else {
+    p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256 : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT);
+  }
+  if (p.n_tiles == 0) return 0;
+  const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   switch (kind) {
-    case GK_BF16: launch_gemm<GK_BF16, MODE>(p, s); break;
-    case GK_FP8_F32: launch_gemm<GK_FP8_F32, MODE>(p, s); break;
-    case GK_FP8_POW2: launch_gemm<GK_FP8_POW2, MODE>(p, s); break;
-    case GK_FP8_MX: launch_gemm<GK_FP8_MX, MODE>(p, s); break;
+    case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block, 0, s, p); break;
+    case GK_FP8_F32: hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p); break;
+    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block, 0, s, p); break;
+    case GK_FP8_MX: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE>), grid, block, 0, s, p); break;
     default: set_error("grouped gemm: unknown kind %d", kind); return 1;
   }
   return check_launch("grouped gemm");
@@ -737,15 +860,16 @@ using namespace fm;
 extern "C" {
 
 int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
-                             int64_t m_tiles, const int32_t* tile_expert, int E, int64_t N,
-                             int64_t K, const int32_t* expert_mask, int mask_want, void* out,
-                             int out_dtype, int64_t ld_out, void* stream) {
-  FM_REQUIRE(tokens && weights && tile_expert && out, "fm_grouped_gemm_ragged_m: null pointer");
+                             int64_t m_tiles, const int32_t* tile_expert, const int32_t* offsets,
+                             int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
+                             void* out, int out_dtype, int64_t ld_out, void* stream) {
+  FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
   FM_REQUIRE(N > 0 && N % 128 == 0, "fm_grouped_gemm_ragged_m: N must be a positive multiple of 128 (got %lld)", (long long)N);
   FM_REQUIRE(K > 0 && K % 128 == 0, "fm_grouped_gemm_ragged_m: K must be a positive multiple of 128 (got %lld)", (long long)K);
   FM_REQUIRE(E >= 1, "fm_grouped_gemm_ragged_m: E must be >= 1");
+  FM_REQUIRE(m_tiles >= 0, "fm_grouped_gemm_ragged_m: m_tiles must be >= 0");
   FM_REQUIRE(tokens->ld >= K && weights->ld >= K, "fm_grouped_gemm_ragged_m: operand pitch < K");
   FM_REQUIRE(weights->group_stride >= K, "fm_grouped_gemm_ragged_m: weight group stride < K");
   FM_REQUIRE(ld_out >= N && ld_out % 4 == 0, "fm_grouped_gemm_ragged_m: output pitch must be >= N and a multiple of 4");
@@ -760,6 +884,9 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   p.K = K;
   p.tile_expert = tile_expert;
   p.m_tiles = m_tiles;
+  // sum over experts of ceil(tiles_e / 2) <= (m_tiles + E) / 2
+  p.j_tiles = (m_tiles + E + 1) / 2;
+  p.offsets = offsets;
   p.E = E;
   p.mask = expert_mask;
   p.mask_want = mask_want;
@@ -767,7 +894,6 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   p.ldC = ld_out;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
   p.split = INT64_MAX;
-  p.n_tiles = m_tiles * ((N + kBI - 1) / kBI);
   return dispatch_gemm<GM_RAGGED_M>(kind, p, static_cast<hipStream_t>(stream));
 }
 
@@ -783,7 +909,7 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
              "fm_grouped_gemm_ragged_k: M and N must be positive multiples of 128 (got %lld x %lld)",
              (long long)M, (long long)N);
   FM_REQUIRE(E >= 1, "fm_grouped_gemm_ragged_k: E must be >= 1");
-  FM_REQUIRE(ld_out >= N, "fm_grouped_gemm_ragged_k: output pitch < N");
+  FM_REQUIRE(ld_out >= N && ld_out % 4 == 0, "fm_grouped_gemm_ragged_k: output pitch must be >= N and a multiple of 4");
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_k: bad out dtype");
   FM_REQUIRE(split_rows >= M || (out2 != nullptr && split_rows % 128 == 0 && split_rows > 0),
              "fm_grouped_gemm_ragged_k: split output needs out2 and a 128-aligned split");
@@ -803,7 +929,6 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
   p.c2_gs = out2_gs;
   p.split = split_rows >= M ? INT64_MAX : split_rows;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
-  p.n_tiles = int64_t(E) * ((M + kBI - 1) / kBI) * (N / kBJ);
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
 }
 

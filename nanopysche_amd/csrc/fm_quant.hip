@@ -291,7 +291,7 @@ int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t 
   FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_quantize: bad input dtype %d",
              x_dtype);
   FM_REQUIRE(ld_x >= cols && ld_x % 8 == 0, "fm_quantize: input pitch must be >= cols and a multiple of 8");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, nullptr};
+  const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, nullptr);
   hipStream_t sm = static_cast<hipStream_t>(stream);
   if (x_dtype == FM_DTYPE_BF16)
     return launch_tile_producer(DenseSrc<uint16_t>{static_cast<const uint16_t*>(x), ld_x}, o, rows,

@@ -474,7 +474,7 @@ int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t*
   FM_REQUIRE(assign_of_row, "fm_permute: null assign_of_row");
   FM_REQUIRE(ld_x >= D && ld_x % 8 == 0, "fm_permute: input pitch must be >= D and a multiple of 8");
   FM_REQUIRE(K >= 1, "fm_permute: K must be >= 1");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, tile_valid};
+  const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, tile_valid);
   GatherSrc src{static_cast<const uint16_t*>(x), ld_x, assign_of_row, K, weights};
   return launch_tile_producer(src, o, rows, D, static_cast<hipStream_t>(stream), "fm_permute");
 }

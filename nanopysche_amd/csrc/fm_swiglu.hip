@@ -72,7 +72,7 @@ int fm_swiglu_quantize(const void* g, int64_t ld_g, const void* u, int64_t ld_u,
   FM_REQUIRE((g && u) || rows == 0, "fm_swiglu_quantize: null input");
   FM_REQUIRE(ld_g % 8 == 0 && ld_u % 8 == 0 && ld_g >= H && ld_u >= H,
              "fm_swiglu_quantize: pitches must be multiples of 8 and >= H");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, 0}, tile_valid};
+  const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, tile_valid);
   SwigluSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), ld_g, ld_u};
   return launch_tile_producer(src, o, rows, H, static_cast<hipStream_t>(stream),
                               "fm_swiglu_quantize");
@@ -86,7 +86,7 @@ int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u,
   FM_REQUIRE(H % 128 == 0, "fm_swiglu_backward: H must be a multiple of 128");
   FM_REQUIRE(ld_g % 8 == 0 && ld_u % 8 == 0 && ld_dh % 8 == 0,
              "fm_swiglu_backward: pitches must be multiples of 8");
-  TileOut o{kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, {0, H}, tile_valid};
+  const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, H, tile_valid);
   SwigluBwdSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
                    static_cast<const uint16_t*>(dh), ld_g, ld_u, ld_dh};
   return launch_tile_producer(src, o, rows, H, static_cast<hipStream_t>(stream),

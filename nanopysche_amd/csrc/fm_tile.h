@@ -16,6 +16,7 @@
 #pragma once
 
 #include "fm_common.h"
+#include "../../include/fm_hip.h"
 
 // e4m3 / bf16 conversion: the gfx950 convert instructions, or the integer
 // routines of fm_common.h.  Both are bit-identical (checked on the GPU by
@@ -39,8 +40,8 @@ struct TileOut {
   // row-major output (nullptr = not wanted)
   void* row_q;           // bf16 or e4m3 [rows, *] with pitch ld_row (elements)
   int64_t ld_row;
-  void* row_s;           // fp32 [rows, */128] or e8m0 [rows, */32]; pitch ld_row_s
-  int64_t ld_row_s;
+  void* row_s;           // fp32 per 128 block or e8m0 per 32 block of a row:
+  int64_t rs_row, rs_kb; //   row_s[row * rs_row + block * rs_kb]
   // transposed output (nullptr = not wanted); requires rows % 128 == 0
   void* col_q;           // bf16 or e4m3 [*, rows] with pitch ld_col (elements)
   int64_t ld_col;
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
         if (want_row && grow < rows) {
           *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
               make_uint2(w0, w1);
-          if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.ld_row_s + (ocol >> 7)] = s;
+          if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.rs_row + (ocol >> 7) * o.rs_kb] = s;
         }
         if (want_col) {
           if (COMPACT) {
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
           *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
               make_uint2(w0, w1);
           if ((tid & 3) == 0)
-            static_cast<uint8_t*>(o.row_s)[grow * o.ld_row_s + ((ocol + cpos) >> 5)] = uint8_t(code);
+            static_cast<uint8_t*>(o.row_s)[grow * o.rs_row + ((ocol + cpos) >> 5) * o.rs_kb] = uint8_t(code);
         }
         if (want_col) {
 #pragma unroll
@@ -279,6 +280,16 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
 
 // Validates a TileOut against the tile geometry; returns nonzero (with the
 // error set) on a mismatch.  `cols` is the source's column count per output.
+// TileOut from the C-ABI arguments; `kind` may carry FM_SCALES_KMAJOR.
+inline TileOut make_tile_out(int kind, void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt,
+                             int64_t ld_qt, void* st, int64_t ld_st, int64_t off0, int64_t off1,
+                             const int32_t* tile_valid) {
+  const bool kmajor = (kind & FM_SCALES_KMAJOR) != 0;
+  TileOut o{kind & ~FM_SCALES_KMAJOR, q, ld_q, s, kmajor ? 1 : ld_s, kmajor ? ld_s : 1,
+            qt, ld_qt, st, ld_st, {off0, off1}, tile_valid};
+  return o;
+}
+
 inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols, int nout) {
   FM_REQUIRE(cols > 0 && cols % 128 == 0, "cols must be a positive multiple of 128 (got %lld)",
              (long long)cols);
@@ -293,7 +304,9 @@ inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols, int nout
     FM_REQUIRE(o.ld_row % 8 == 0, "row output pitch must be a multiple of 8");
     if (o.kind != QK_BF16) {
       FM_REQUIRE(o.row_s != nullptr, "row scale output missing");
-      FM_REQUIRE(o.ld_row_s >= (o.kind == QK_MX ? span / 32 : span / 128), "row scale pitch too small");
+      const int64_t nblk = o.kind == QK_MX ? span / 32 : span / 128;
+      FM_REQUIRE((o.rs_kb == 1 && o.rs_row >= nblk) || (o.rs_row == 1 && o.rs_kb >= rows),
+                 "row scale pitch too small");
     }
   }
   if (o.col_q != nullptr) {

@@ -71,17 +71,22 @@ def _src_dtype(x: torch.Tensor) -> int:
     raise TypeError(f"expected bfloat16 or float32 input, got {x.dtype}")
 
 
-def _alloc_quant(rows: int, cols: int, kind: int, row: bool, col: bool, dev):
-    """Payload / scale buffers for a [rows, cols] source quantised as `kind`."""
+def _alloc_quant(rows: int, cols: int, kind: int, row: bool, col: bool, dev, kmajor: bool = False):
+    """Payload / scale buffers for a [rows, cols] source quantised as `kind`.
+    With ``kmajor`` the row scales [rows, blocks] are a transposed view of a
+    block-major [blocks, rows] buffer (the grouped GEMM reads one block of 256
+    rows from a contiguous span)."""
     u8, f32, bf = torch.uint8, torch.float32, torch.bfloat16
     q = s = qt = st = None
     pay = bf if kind == _lib.QUANT_BF16 else u8
     if row:
         q = torch.empty(rows, cols, dtype=pay, device=dev)
-        if kind in (_lib.QUANT_BLOCK, _lib.QUANT_POW2):
-            s = torch.empty(rows, cols // FP8_BLOCK_SIZE, dtype=f32, device=dev)
-        elif kind == _lib.QUANT_MX:
-            s = torch.empty(rows, cols // MX_BLOCK_SIZE, dtype=u8, device=dev)
+        if kind != _lib.QUANT_BF16:
+            blk, dt = (MX_BLOCK_SIZE, u8) if kind == _lib.QUANT_MX else (FP8_BLOCK_SIZE, f32)
+            if kmajor:
+                s = torch.empty(cols // blk, rows, dtype=dt, device=dev).t()
+            else:
+                s = torch.empty(rows, cols // blk, dtype=dt, device=dev)
     if col:
         qt = torch.empty(cols, rows, dtype=pay, device=dev)
         if kind in (_lib.QUANT_BLOCK, _lib.QUANT_POW2):
@@ -95,8 +100,14 @@ def _ld(t):
     return 0 if t is None else t.stride(0)
 
 
-def _tile_args(q, s, qt, st):
-    return (_lib.ptr(q), _ld(q), _lib.ptr(s), _ld(s), _lib.ptr(qt), _ld(qt), _lib.ptr(st), _ld(st))
+def _tile_args(kind, q, s, qt, st):
+    """(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st) for the tile producers;
+    block-major row scales (a transposed view) add SCALES_KMAJOR to the kind."""
+    ld_s = _ld(s)
+    if s is not None and s.stride(1) != 1:
+        kind |= _lib.SCALES_KMAJOR
+        ld_s = s.stride(1)
+    return (kind, _lib.ptr(q), _ld(q), _lib.ptr(s), ld_s, _lib.ptr(qt), _ld(qt), _lib.ptr(st), _ld(st))
 
 
 def _wrap(q, s, qt, st, kind):
@@ -147,8 +158,8 @@ def quantize_to_fp8(x: torch.Tensor,
     if want_col and R % 128:
         raise ValueError(f"column-block quantisation needs rows % 128 == 0, got {R}")
     q, s, qt, st = _alloc_quant(R, C, kind, want_row, want_col, x.device)
-    _lib.call("fm_quantize", _lib.ptr(x2), _src_dtype(x2), R, C, x2.stride(0), kind,
-              *_tile_args(q, s, qt, st), _lib.stream_of(x2))
+    _lib.call("fm_quantize", _lib.ptr(x2), _src_dtype(x2), R, C, x2.stride(0),
+              *_tile_args(kind, q, s, qt, st), _lib.stream_of(x2))
     row, col = _wrap(q, s, qt, st, kind)
     if want_row and return_transpose:
         return row, col
@@ -163,13 +174,13 @@ def dequantize_from_fp8(t: FP8Tensor, out_dtype: torch.dtype = torch.bfloat16) -
     g = BlockScalingGranularity(t.granularity)
     e8m0 = g in (G.MX_1x32, G.MX_32x1)
     if g == G.ROW_1x128:
-        shifts = (0, 7, s.stride(0), 1)
+        shifts = (0, 7, s.stride(0), s.stride(1))
     elif g == G.MX_1x32:
-        shifts = (0, 5, s.stride(0), 1)
+        shifts = (0, 5, s.stride(0), s.stride(1))
     elif g == G.BLOCK_128x128:
-        shifts = (7, 7, s.stride(0), 1)
+        shifts = (7, 7, s.stride(0), s.stride(1))
     elif g in (G.COL_128x1, G.MX_32x1):
-        shifts = (0, 7 if g == G.COL_128x1 else 5, 1, s.stride(0))
+        shifts = (0, 7 if g == G.COL_128x1 else 5, s.stride(1), s.stride(0))
     else:
         raise ValueError(g)
     out = torch.empty(R, C, dtype=out_dtype, device=q.device)
@@ -194,6 +205,8 @@ def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
     R, C = q.shape
     if R % 128 or C % 128:
         raise ValueError(f"scaling_aware_transpose needs both dims % 128 == 0, got {tuple(q.shape)}")
+    if s.stride(1) != 1:
+        s = s.contiguous()   # the kernel reads row-major scales
     qt = torch.empty(C, R, dtype=torch.uint8, device=q.device)
     st = torch.empty(R // 128, C, dtype=torch.float32, device=q.device)
     _lib.call("fm_scaling_aware_transpose", _lib.ptr(q), R, C, q.stride(0), _lib.ptr(s), s.stride(0),
@@ -202,10 +215,10 @@ def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
 
 
 # ======================================================================= SwiGLU ====
-def _swiglu(g, u, rows, H, kind, row, col, dev, tile_valid=None):
-    q, s, qt, st = _alloc_quant(rows, H, kind, row, col, dev)
-    _lib.call("fm_swiglu_quantize", _lib.ptr(g), g.stride(0), _lib.ptr(u), u.stride(0), rows, H, kind,
-              *_tile_args(q, s, qt, st), _lib.ptr(tile_valid), _lib.stream_of(g))
+def _swiglu(g, u, rows, H, kind, row, col, dev, tile_valid=None, kmajor=False):
+    q, s, qt, st = _alloc_quant(rows, H, kind, row, col, dev, kmajor)
+    _lib.call("fm_swiglu_quantize", _lib.ptr(g), g.stride(0), _lib.ptr(u), u.stride(0), rows, H,
+              *_tile_args(kind, q, s, qt, st), _lib.ptr(tile_valid), _lib.stream_of(g))
     return q, s, qt, st
 
 
@@ -262,7 +275,7 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
                       granularity: Optional[BlockScalingGranularity] = G.ROW_1x128,
                       pow2_scale: bool = False, return_transpose: bool = False,
                       weights: Optional[torch.Tensor] = None,
-                      fp8_gemm_threshold: int = 0) -> PermutedTokens:
+                      fp8_gemm_threshold: int = 0, kmajor_scales: bool = False) -> PermutedTokens:
     """Gather the rows of ``x`` [T, D] (bf16) into expert order, each expert's
     group padded to 128 rows (zeros), and quantise them in the same pass.
     Rows past the last group (``plan.offsets[-1]`` up to ``plan.rows_max``)
@@ -270,7 +283,9 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
 
     ``indices`` is the router's [T, K] expert indices or a RoutingPlan from an
     earlier call.  ``weights`` [T, K] (optional) scales each gathered row by
-    its router weight.  granularity None keeps bf16."""
+    its router weight.  granularity None keeps bf16.  ``kmajor_scales``
+    stores the row scales block-major (``rows.scale`` is then a transposed
+    view), the layout the grouped GEMM streams fastest."""
     _lib.require_device(x, "x")
     if x.dtype != torch.bfloat16:
         raise TypeError("x must be bfloat16")
@@ -281,12 +296,12 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
     if plan.num_tokens != T:
         raise ValueError(f"plan is for {plan.num_tokens} tokens, x has {T}")
     kind = _act_kind(granularity, pow2_scale)
-    q, s, qt, st = _alloc_quant(plan.rows_max, D, kind, True, return_transpose, x.device)
+    q, s, qt, st = _alloc_quant(plan.rows_max, D, kind, True, return_transpose, x.device, kmajor_scales)
     w = None
     if weights is not None:
         w = weights.reshape(-1).to(torch.float32).contiguous()
     _lib.call("fm_permute", _lib.ptr(x2), T, D, x2.stride(0), _lib.ptr(plan.assign_of_row),
-              plan.rows_max, plan.top_k, _lib.ptr(w), kind, *_tile_args(q, s, qt, st),
+              plan.rows_max, plan.top_k, _lib.ptr(w), *_tile_args(kind, q, s, qt, st),
               _lib.ptr(plan.tile_expert), _lib.stream_of(x2))
     row, col = _wrap(q, s, qt, st, kind)
     return PermutedTokens(plan, row, col)
@@ -328,7 +343,7 @@ def _token_operand(t, kind):
     """Row-major activations [rows, K] (FP8Tensor or bf16 tensor)."""
     if kind == _lib.QUANT_BF16:
         return _operand(t)
-    return _operand(t.data, t.scale, s_row=t.scale.stride(0), s_kb=1)
+    return _operand(t.data, t.scale, s_row=t.scale.stride(0), s_kb=t.scale.stride(1))
 
 
 def _col_operand(t, kind):
@@ -380,7 +395,8 @@ def _timed(name, flops, fn):
 def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=None, want=1):
     def launch():
         _lib.call("fm_grouped_gemm_ragged_m", _gemm_kind(kind), _token_operand(tokens, kind),
-                  w.operand(), plan.m_tiles, _lib.ptr(plan.tile_expert), plan.num_experts, w.N, w.K,
+                  w.operand(), plan.m_tiles, _lib.ptr(plan.tile_expert), _lib.ptr(plan.offsets),
+                  plan.num_experts, w.N, w.K,
                   _lib.ptr(mask), want, _lib.ptr(out), _dt(out), out.stride(0), _lib.stream_of(out))
 
     _timed(f"grouped_gemm_ragged_m/{_KIND_NAME[kind]}",
@@ -502,8 +518,8 @@ class ExpertWeights:
 
         def q(src, rows):
             qq, s, qt, st = _alloc_quant(rows, D, _lib.QUANT_MX, True, True, dev)
-            _lib.call("fm_quantize", _lib.ptr(src), _lib.DTYPE_BF16, rows, D, D, _lib.QUANT_MX,
-                      *_tile_args(qq, s, qt, st), stream)
+            _lib.call("fm_quantize", _lib.ptr(src), _lib.DTYPE_BF16, rows, D, D,
+                      *_tile_args(_lib.QUANT_MX, qq, s, qt, st), stream)
             return qq, s, qt, st
 
         W13, S13, W13t, S13t = q(W13src, E * 2 * H)
@@ -641,7 +657,7 @@ class FP8FlowMoECompute:
                 continue
             ew = self._weights(kind)
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                   return_transpose=True)
+                                   return_transpose=True, kmajor_scales=True)
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}
@@ -649,7 +665,8 @@ class FP8FlowMoECompute:
             if kind is None:
                 continue
             # row blocks feed the down GEMM; the column blocks are kept for dW2
-            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, True, dev, plan.tile_expert)
+            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, True, dev, plan.tile_expert,
+                                   kmajor=True)
             hrow, hcol = _wrap(q, s, qt, st, kind)
             h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
@@ -693,16 +710,16 @@ class FP8FlowMoECompute:
         for kind, want in runs:
             ew = self._weights(kind)
             pt = fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                   return_transpose=True, weights=wts)
+                                   return_transpose=True, weights=wts, kmajor_scales=True)
             _gemm_m(kind, pt.rows, ew.w2, plan, dH, mask, want)
             dy[kind] = pt.rows_t
         if self.capture_intermediates is not None:
             self.capture_intermediates["dh"] = dH.detach().clone()
         for kind, want in runs:
             ew = self._weights(kind)
-            gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev)
+            gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev, kmajor=True)
             _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
-                      _lib.ptr(dH), dH.stride(0), R, H, kind, *_tile_args(gq, gs, gqt, gst),
+                      _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst),
                       _lib.ptr(plan.tile_expert), _lib.stream_of(GU))
             dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
             h_col = ctx.saved_hcols[kind]

@@ -93,8 +93,9 @@ def test_route_sort_empty(dev):
     assert _np(plan.offsets).tolist() == [0] * 5
 
 
+@pytest.mark.parametrize("kmajor", [False, True])
 @pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
-def test_permute_bitexact(dev, kind):
+def test_permute_bitexact(dev, kind, kmajor):
     T, E, K, D = 3000, 8, 2, 512
     x = randn_bf16((T, D), seed=21)
     w, idx = zipf_routing(T, E, K, 1.1, seed=2, zero_experts=(3,))
@@ -102,8 +103,10 @@ def test_permute_bitexact(dev, kind):
             "pow2": fm.BlockScalingGranularity.ROW_1x128, "mx": fm.BlockScalingGranularity.MX_1x32}[kind]
     for weights in (None, w):
         pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2",
-                                  return_transpose=True,
+                                  return_transpose=True, kmajor_scales=kmajor,
                                   weights=None if weights is None else weights.to(dev))
+        if kmajor and kind != "bf16":
+            assert pt.rows.scale.stride(0) == 1  # block-major buffer viewed as [rows, blocks]
         ref = orouting.sort_assignments(idx.numpy(), E)
         xs = x.float().numpy()
         Xp = orouting.permute_pad(xs, ref["assign_of_row"], K)

@@ -67,8 +67,8 @@ def test_argument_validation_without_device():
                             None, 1024, None)
     assert rc != 0 and b"E must be" in lib.fm_last_error_string()
     op = _lib.FmGemmOperand()
-    rc = lib.fm_grouped_gemm_ragged_m(0, C.byref(op), C.byref(op), 1, C.c_void_p(16), 1, 128, 128,
-                                      None, 1, C.c_void_p(16), 0, 128, None)
+    rc = lib.fm_grouped_gemm_ragged_m(0, C.byref(op), C.byref(op), 1, C.c_void_p(16), C.c_void_p(16),
+                                      1, 128, 128, None, 1, C.c_void_p(16), 0, 128, None)
     assert rc != 0
     assert lib.fm_route_rows_max(16384, 8) == (16384 + 8 * 127 + 127) // 128 * 128
     try:
