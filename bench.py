@@ -75,6 +75,21 @@ class GemmTimer:
         return out
 
 
+def recorded_traffic(kernel, recipe):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy), or
+    None when no summary for this kernel and recipe is committed."""
+    path = ROOT / "profiles" / "c3_hbm_traffic.json"
+    try:
+        rec = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    ent = rec.get("kernels", {}).get(kernel)
+    if ent is None or rec.get("recipe") != recipe:
+        return None
+    return {"bytes_per_launch": ent["hbm_bytes_per_launch"], "source": "profiles/c3_hbm_traffic.json"}
+
+
 def cpu_baseline(T, D, H, E, K, budget_s=12.0):
     """The reference's BF16 per-expert loop (model/moe.py:1542-1596) restated in
     fp32 torch on the host cores, forward + backward, on a bounded token sample."""
@@ -116,6 +131,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against known bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
@@ -147,31 +165,37 @@ def main():
         out = blk(xr, wr, idx, 0, E)
         out.backward(go)
 
+    if args.copy_probe:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # timed region: HIP events around every grouped GEMM on its launch stream
+    timer = GemmTimer()
+    fmm.GEMM_TIMER = timer
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    fmm.GEMM_TIMER = None
     ms = elapsed * 1e3 / args.steps
 
-    # per-launch timing of the grouped GEMMs (separate pass, same work)
-    timer = GemmTimer()
-    fmm.GEMM_TIMER = timer
-    for _ in range(3):
-        step()
-    fmm.GEMM_TIMER = None
     summ = timer.summary()
     dom = max(summ, key=lambda k: summ[k]["ms"])
     d = summ[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
     peak = PEAK_TFLOPS["bf16" if args.recipe == "none" else "fp8"]
-    gemm_ms = sum(v["ms"] for v in summ.values()) / 3
+    gemm_ms = sum(v["ms"] for v in summ.values()) / args.steps
     kernels = {k: {"avg_us": round(v["ms"] * 1e3 / v["launches"], 2),
                    "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
-                   "launches_per_step": v["launches"] // 3} for k, v in summ.items()}
+                   "launches_per_step": v["launches"] // args.steps} for k, v in summ.items()}
+    traffic = recorded_traffic(dom, args.recipe)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(T, D, H, E, K)
     res = {
@@ -192,7 +216,10 @@ def main():
                    "routing": "exactly balanced (2048 assignments per expert)",
                    "recipe": args.recipe, "assignments": A},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": None, "kernel": dom},
+                     "frac": round(achieved / peak, 4),
+                     "traffic": None if traffic is None else traffic["bytes_per_launch"],
+                     "kernel": dom,
+                     "traffic_source": None if traffic is None else traffic["source"]},
         "gemm": {"tflops_all_gemms": round(18 * A * D * H / (gemm_ms * 1e-3) / 1e12, 1),
                  "gemm_ms_per_step": round(gemm_ms, 4), "kernels": kernels},
         "cpu_baseline": cpu,

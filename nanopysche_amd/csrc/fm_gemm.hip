@@ -26,17 +26,16 @@
 //              promotion.
 //   FP8_MX     e4m3 with e8m0 scales per 32 (OCP MXFP8), same instruction.
 //
-// Two kernels, 256 threads = 4 wave64 as 2 (i) x 2 (j), K step 128 bytes
-// (128 e4m3 / 64 bf16), operands streamed into LDS by direct global->LDS loads:
-//   gemm256_kernel  BF16 / FP8_POW2 / FP8_MX.  Tile 256 x 256, each wave
-//                   128 x 128 = 4 x 4 MFMA 32x32 blocks (256 accumulator
-//                   registers), two LDS stages of 66 KiB, fragments of the next
-//                   half step read while the MFMAs of the current one run.
-//                   In ragged-M a 256-token tile covers two 128-row groups of
-//                   one expert; the second half is idle at an odd group end.
-//   gemm_f32_kernel FP8_F32.  Tile 256 x 128 (each wave 128 x 64), three LDS
-//                   stages; the promotion needs a second set of partial-sum
-//                   registers, which the 4 x 4 wave tile has no room for.
+// Two kernels, K step 128 bytes (128 e4m3 / 64 bf16), operands streamed into
+// LDS by direct global->LDS loads, each wave 128 x 64 = 4 x 2 MFMA 32x32 blocks:
+//   gemm256_kernel  BF16 / FP8_POW2 / FP8_MX.  Tile 256 x 256, 512 threads =
+//                   8 wave64 as 2 (i) x 4 (j), two waves per SIMD, two LDS
+//                   stages of 66 KiB.  In ragged-M a 256-token tile covers two
+//                   128-row groups of one expert; its second half is idle at
+//                   an odd group end.
+//   gemm_f32_kernel FP8_F32.  Tile 256 x 128, 256 threads = 4 wave64 as
+//                   2 x 2, three LDS stages; each 128-deep partial sum is
+//                   promoted through a second set of accumulator registers.
 // Workgroup ids are remapped so each XCD walks a contiguous range of tiles,
 // grouped 8 token tiles at a time for L2 reuse of weights and activations.
 #include "fm_common.h"
@@ -174,33 +173,6 @@ __device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row
   return s;
 }
 
-__device__ __forceinline__ void stream_issue(const OpStream& s, int64_t kbytes, uint8_t* dst, int wave,
-                                             int u) {
-  const int g = wave * 8 + u;
-  const int gc = g < s.g_last ? g : s.g_last;
-  dma16s(s.base + gc * s.group_bytes + kbytes, s.lane_off[u & 1], dst + g * 1024);
-}
-
-// Per-lane scale DMA sources (one dword per lane per K step and operand).
-struct ScaleSrc {
-  const uint8_t* qs;
-  const uint8_t* ps;
-  int64_t qs_k, ps_k;   // byte advance per K step
-};
-
-// Register fragments of one half of a K step: for e4m3 one 64-deep MFMA slice
-// (4 A + 4 B fragments of 32 bytes per lane, plus their e8m0 scale operands),
-// for bf16 two 16-deep slices.
-template <int KIND>
-struct Frag {
-  v8i a[4], b[4];
-  int sa[4], sb[4];
-};
-template <>
-struct Frag<GK_BF16> {
-  v8bf a[2][4], b[2][4];
-};
-
 // e4m3 fragment rows: lane half h holds K [16h, 16h+16) in bytes 0-15 and
 // K [32+16h, +16) in bytes 16-31 of the 64-deep slice, so bytes 0-15 of both
 // halves form the first 32-deep scale block (scale from lane `row`) and bytes
@@ -215,18 +187,68 @@ __device__ __forceinline__ v8bf read_frag16(const uint8_t* base, int r, int ks, 
   return __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(base + lds_off(r, ks * 2 + lhalf)));
 }
 
+// Scales in LDS.  pow2: the DMA places the fp32 scale of tile row
+// 128*w + 32*t + l at float index 128*w + 4*l + t, so the four row blocks t of
+// a lane's fragment rows come from one 16-byte read per K step (both halves
+// use them).  MX: four e8m0 bytes per row and step, [block][row] bytes in the
+// k-major layout, [row][block] otherwise; read per half.
+__device__ __forceinline__ int scale_row_slot(int li) {   // LDS slot li holds tile row:
+  return (li >> 7) * 128 + (li & 3) * 32 + ((li & 127) >> 2);
+}
 template <int KIND>
-__device__ __forceinline__ int read_scale(const uint8_t* st, int off, int r, int blk, bool mx_k) {
-  if (KIND == GK_FP8_POW2) return int((f2u(reinterpret_cast<const float*>(st + off)[r]) >> 23) & 0xffu);
+__device__ __forceinline__ void read_pow2_scales(const uint8_t* st, int off, int w128, int lrow, int (&s)[4]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(st + off + (w128 + lrow * 4) * 4);
+  s[0] = int((v.x >> 23) & 0xffu);
+  s[1] = int((v.y >> 23) & 0xffu);
+  s[2] = int((v.z >> 23) & 0xffu);
+  s[3] = int((v.w >> 23) & 0xffu);
+}
+__device__ __forceinline__ int read_mx_scale(const uint8_t* st, int off, int r, int blk, bool mx_k) {
   return mx_k ? st[off + blk * kT + r] : st[off + r * 4 + blk];
 }
+
+// Waves as 2 (i) x 4 (j), each 128 x 64 = 4 x 2 MFMA blocks (128 accumulator
+// registers), so two waves share each SIMD: while one waits on LDS reads or
+// the per-step barrier the other keeps the matrix pipe busy.  Each wave
+// streams 4 of the 32 row groups of each operand and one dword of scales per
+// K step.
+template <int KIND>
+struct Frag {
+  v8i a[4], b[2];
+  int sa[4], sb[2];
+};
+template <>
+struct Frag<GK_BF16> {
+  v8bf a[2][4], b[2][2];
+};
 
 struct WaveCoord {
   int wave, lane, wi, wj, lrow, lhalf;
   bool q_mx_k, p_mx_k;
 };
 
-// Reads half `half` of the K step held in stage `st`.
+// One K step of DMA for this wave: 4 row groups of each operand, then one
+// scale dword per lane (waves 0-3: Q scale slots, 4-7: P scale slots).
+template <int KIND>
+__device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const uint8_t* sc,
+                                       int64_t sc_k, int sc_dst, int64_t k, uint8_t* dst, int wave) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const int64_t kb = k * ES;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int g = wave * 4 + u;
+    const int gq = g < qst.g_last ? g : qst.g_last;
+    dma16s(qst.base + gq * qst.group_bytes + kb, qst.lane_off[u & 1], dst + g * 1024);
+    const int gp = g < pst.g_last ? g : pst.g_last;
+    dma16s(pst.base + gp * pst.group_bytes + kb, pst.lane_off[u & 1], dst + SM::kP + g * 1024);
+  }
+  if constexpr (KIND != GK_BF16) dma4(sc + (k / KSTEP) * sc_k, dst + sc_dst);
+}
+
+// Reads half `half` of the K step in stage `st` (pow2 scales only for half 0:
+// one scale per 128-deep step).
 template <int KIND>
 __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND>& f, const WaveCoord& w) {
   using SM = Smem256<KIND>;
@@ -236,114 +258,55 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
-        f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
+        if (t < 2) f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
       }
   } else {
+    if constexpr (KIND == GK_FP8_MX) {   // scales first: the MFMAs wait on them
+      const int blk = half * 2 + w.lhalf;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        f.sa[t] = read_mx_scale(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, blk, w.q_mx_k);
+        if (t < 2) f.sb[t] = read_mx_scale(st, SM::kPS, w.wj * 64 + t * 32 + w.lrow, blk, w.p_mx_k);
+      }
+    } else if (half == 0) {
+      read_pow2_scales<KIND>(st, SM::kQS, w.wi * 128, w.lrow, f.sa);
+      // P rows 64*wj + 32*t + l sit in 128-row block wj/2 at slot t' = 2*(wj&1) + t
+      const uint2 v = *reinterpret_cast<const uint2*>(
+          st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+      f.sb[0] = int((v.x >> 23) & 0xffu);
+      f.sb[1] = int((v.y >> 23) & 0xffu);
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, half, w.lhalf);
-      f.b[t] = read_frag8(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, half, w.lhalf);
-    }
-    const int blk = half * 2 + w.lhalf;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f.sa[t] = read_scale<KIND>(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, blk, w.q_mx_k);
-      f.sb[t] = read_scale<KIND>(st, SM::kPS, w.wj * 128 + t * 32 + w.lrow, blk, w.p_mx_k);
-    }
-  }
-}
-
-// Refills stage `dst` with the K step at element offset `k` and reads half 0
-// of the step held in `st`, two DMAs per fragment read.  The DMAs are inline
-// assembly with a memory clobber, so they keep this program order relative to
-// the LDS reads, and the caller's MFMA interleave spreads both between MFMAs.
-template <int KIND>
-__device__ __forceinline__ void refill_and_read_half0(const OpStream& qst, const OpStream& pst,
-                                                      const ScaleSrc& sc, int64_t k, uint8_t* dst,
-                                                      const uint8_t* st, Frag<KIND>& f,
-                                                      const WaveCoord& w) {
-  using SM = Smem256<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
-  constexpr int KSTEP = 128 / ES;
-  const int64_t kb = k * ES;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    stream_issue(qst, kb, dst, w.wave, 2 * t);
-    stream_issue(qst, kb, dst, w.wave, 2 * t + 1);
-    if constexpr (KIND == GK_BF16) {
-      f.a[0][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
-      f.a[1][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, 1, w.lhalf);
-    } else {
-      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    stream_issue(pst, kb, dst + SM::kP, w.wave, 2 * t);
-    stream_issue(pst, kb, dst + SM::kP, w.wave, 2 * t + 1);
-    if constexpr (KIND == GK_BF16) {
-      f.b[0][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 0, w.lhalf);
-      f.b[1][t] = read_frag16(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 1, w.lhalf);
-    } else {
-      f.b[t] = read_frag8(st + SM::kP, w.wj * 128 + t * 32 + w.lrow, 0, w.lhalf);
-    }
-  }
-  if constexpr (KIND != GK_BF16) {
-    const int64_t ks = k / KSTEP;
-    dma4(sc.qs + ks * sc.qs_k, dst + SM::kQS + w.wave * 256);
-    dma4(sc.ps + ks * sc.ps_k, dst + SM::kPS + w.wave * 256);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f.sa[t] = read_scale<KIND>(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, w.lhalf, w.q_mx_k);
-      f.sb[t] = read_scale<KIND>(st, SM::kPS, w.wj * 128 + t * 32 + w.lrow, w.lhalf, w.p_mx_k);
+      if (t < 2) f.b[t] = read_frag8(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, half, w.lhalf);
     }
   }
 }
 
 template <int KIND>
-__device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
-                                           int64_t k, uint8_t* dst, int wave) {
-  using SM = Smem256<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
-  constexpr int KSTEP = 128 / ES;
-  const int64_t kb = k * ES;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) stream_issue(qst, kb, dst, wave, u);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) stream_issue(pst, kb, dst + SM::kP, wave, u);
-  if constexpr (KIND != GK_BF16) {
-    const int64_t ks = k / KSTEP;
-    dma4(sc.qs + ks * sc.qs_k, dst + SM::kQS + wave * 256);
-    dma4(sc.ps + ks * sc.ps_k, dst + SM::kPS + wave * 256);
-  }
-}
-
-template <int KIND>
-__device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][4]) {
+__device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][2]) {
   if constexpr (KIND == GK_BF16) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < 2; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][a], f.b[s2][b], acc[a][b], 0, 0, 0);
   } else {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 2; ++b)
         acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[a], f.b[b], acc[a][b], 0, 0, 0,
                                                                    f.sa[a], 0, f.sb[b]);
   }
 }
 
-// Scheduling pattern for one half step: every MFMA is followed by LDS reads
-// of the next fragments (16 x 64-cycle e4m3 MFMAs or 32 x bf16 MFMAs), so the
-// reads hide behind the matrix pipe.
 template <int KIND>
 __device__ __forceinline__ void interleave_half() {
-  constexpr int kMfma = KIND == GK_BF16 ? 32 : 16;
+  constexpr int kMfma = KIND == GK_BF16 ? 16 : 8;
   constexpr int kReads = KIND == GK_BF16 ? 1 : 2;
 #pragma unroll
   for (int i = 0; i < kMfma; ++i) {
@@ -353,11 +316,10 @@ __device__ __forceinline__ void interleave_half() {
 }
 
 template <int KIND, int MODE>
-__global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
+__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
   constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
-  constexpr int NLOAD = 16 + (SM::kScaled ? 2 : 0);   // DMA instructions per wave per step
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
 
   // ---------------------------------------------------------- tile decode ----
@@ -407,90 +369,91 @@ __global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
   WaveCoord w;
   w.lane = threadIdx.x & 63;
   w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-  w.wi = w.wave >> 1;   // wave tile: i [128*wi, +128), j [128*wj, +128)
-  w.wj = w.wave & 1;
+  w.wi = w.wave >> 2;   // wave tile: i [128*wi, +128), j [64*wj, +64)
+  w.wj = w.wave & 3;
   w.lrow = w.lane & 31;
   w.lhalf = w.lane >> 5;
   w.q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
   w.p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
   const int64_t q_group = MODE == GM_RAGGED_M ? e : 0;
-  // valid rows of each operand tile (multiples of 128: n_i, n_j and the group
-  // ends are)
+  // valid rows of each operand tile (multiples of 128)
   const int64_t q_rows = p.n_i - i0 < kT ? p.n_i - i0 : kT;
   const int64_t p_rows = j_end - j0 < kT ? j_end - j0 : kT;
 
   const OpStream qst = make_stream(p.Q.p + (q_group * p.Q.gs + i0 * p.Q.ld) * ES, p.Q.ld * ES, q_rows, w.lane);
   const OpStream pst = make_stream(p.P.p + j0 * p.P.ld * ES, p.P.ld * ES, p_rows, w.lane);
 
-  // Scales: one dword per lane and operand per K step.  fp32 / pow2 and
-  // row-major MX: lane = row (four consecutive 32-block bytes for MX); MX in
-  // k-major layout: lane packs four consecutive rows of one 32-block, so LDS
-  // holds [block][row] bytes.  Rows past the valid ones re-read the last one.
-  ScaleSrc sc{nullptr, nullptr, 0, 0};
+  // Scales: waves 0-3 fetch the Q scale slots, waves 4-7 the P slots, one
+  // dword per lane per K step.  fp32 / pow2 and row-major MX: one row per slot
+  // (pow2 slots permuted, see scale_row_slot); MX in k-major layout: four
+  // consecutive rows of one 32-block per slot ([block][row] bytes in LDS).
+  // Rows past the valid ones re-read the last one.
+  const uint8_t* sc = nullptr;
+  int64_t sc_k = 0;
+  int sc_dst = 0;
   if constexpr (SM::kScaled) {
-    const int li = w.wave * 64 + w.lane;   // 0..255
+    const bool is_q = w.wave < 4;
+    const Operand& o = is_q ? p.Q : p.P;
+    const int64_t r0 = is_q ? i0 : j0;
+    const int64_t rows = is_q ? q_rows : p_rows;
+    const int64_t og = is_q ? q_group : 0;
+    const bool mx_k = is_q ? w.q_mx_k : w.p_mx_k;
+    const int li = (w.wave & 3) * 64 + w.lane;   // slot 0..255
     const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
-    if (w.q_mx_k) {
-      int64_t gr = i0 + (li * 4) % kT;
-      gr = gr + 4 <= i0 + q_rows ? gr : i0 + q_rows - 4;
-      sc.qs = static_cast<const uint8_t*>(p.Q.s) + (q_group * p.Q.s_gs + gr * p.Q.s_row + (li / 64) * p.Q.s_kb);
+    if (mx_k) {
+      int64_t gr = r0 + (li * 4) % kT;
+      gr = gr + 4 <= r0 + rows ? gr : r0 + rows - 4;
+      sc = static_cast<const uint8_t*>(o.s) + (og * o.s_gs + gr * o.s_row + (li / 64) * o.s_kb);
     } else {
-      const int64_t gr = i0 + (li < q_rows ? li : q_rows - 1);
-      sc.qs = static_cast<const uint8_t*>(p.Q.s) +
-              (q_group * p.Q.s_gs + (gr >> p.Q.s_shift) * p.Q.s_row) * sbytes;
+      const int lr = KIND == GK_FP8_POW2 ? scale_row_slot(li) : li;
+      const int64_t gr = r0 + (lr < rows ? lr : rows - 1);
+      sc = static_cast<const uint8_t*>(o.s) + (og * o.s_gs + (gr >> o.s_shift) * o.s_row) * sbytes;
     }
-    if (w.p_mx_k) {
-      int64_t gr = j0 + (li * 4) % kT;
-      gr = gr + 4 <= j0 + p_rows ? gr : j0 + p_rows - 4;
-      sc.ps = static_cast<const uint8_t*>(p.P.s) + (gr * p.P.s_row + (li / 64) * p.P.s_kb);
-    } else {
-      const int64_t gr = j0 + (li < p_rows ? li : p_rows - 1);
-      sc.ps = static_cast<const uint8_t*>(p.P.s) + ((gr >> p.P.s_shift) * p.P.s_row) * sbytes;
-    }
-    // per K step: one 128-block (pow2 scales) or four 32-blocks (MX)
-    sc.qs_k = (KIND == GK_FP8_MX ? 4 : 1) * p.Q.s_kb * sbytes;
-    sc.ps_k = (KIND == GK_FP8_MX ? 4 : 1) * p.P.s_kb * sbytes;
+    sc_k = (KIND == GK_FP8_MX ? 4 : 1) * o.s_kb * sbytes;
+    sc_dst = (is_q ? SM::kQS : SM::kPS) + (w.wave & 3) * 256;
   }
 
-  v16f acc[4][4];
+  v16f acc[4][2];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  // Two-stage pipeline, K step t in stage t % 2, each step split in halves:
-  //   A  read half 1 of step t                 (stage t % 2)
-  //   B  MFMAs of half 0 of step t             (registers read during step t-1)
-  //   C  wait for step t+1's DMA and this wave's reads, barrier: every wave is
-  //      done with stage t % 2 and step t+1 has landed in stage (t+1) % 2
-  //   D  refill stage t % 2 with step t+2; read half 0 of step t+1
-  //   E  MFMAs of half 1 of step t
-  // Every step issues the same DMA group (clamped to the last step at the end;
-  // the re-read lands in a stage nobody reads again), which keeps the loop body
-  // one basic block.
+  // Two-stage pipeline, K step t in stage t % 2.  Each step: wait for this
+  // wave's DMA of step t, barrier (step t has landed for every wave and every
+  // wave is done with stage (t+1) % 2), refill that stage with step t+1, then
+  // the two halves of step t, the second half's reads under the first half's
+  // MFMAs.  The refill is unconditional (clamped to the last step), which
+  // keeps the loop body one basic block.
   const int64_t nk = (k_hi - k_lo) / KSTEP;
   if (nk > 0) {
     Frag<KIND> f0, f1;
-    issue_step<KIND>(qst, pst, sc, k_lo, smem, w.wave);
-    issue_step<KIND>(qst, pst, sc, k_lo + (nk > 1 ? KSTEP : 0), smem + SM::kStage, w.wave);
-    FM_WAIT_VMCNT(NLOAD);
-    block_barrier();
-    read_half<KIND>(smem, 0, f0, w);
+    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo, smem, w.wave);
     int cur_off = 0;
 #pragma unroll 1
     for (int64_t t = 0; t < nk; ++t) {
       const int nxt_off = SM::kStage - cur_off;
-      read_half<KIND>(smem + cur_off, 1, f1, w);                                        // A
-      mma_half<KIND>(f0, acc);                                                          // B
-      interleave_half<KIND>();
-      FM_WAIT_VMCNT(0);                                                                 // C
+      FM_WAIT_VMCNT(0);
       block_barrier();
-      const int64_t tn = t + 2 < nk ? t + 2 : nk - 1;
-      refill_and_read_half0<KIND>(qst, pst, sc, k_lo + tn * KSTEP, smem + cur_off, smem + nxt_off, f0, w);  // D
-      mma_half<KIND>(f1, acc);                                                          // E
+      const int64_t tn = t + 1 < nk ? t + 1 : nk - 1;
+      issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + tn * KSTEP, smem + nxt_off, w.wave);
+      read_half<KIND>(smem + cur_off, 0, f0, w);
+      __builtin_amdgcn_sched_barrier(0);
+      read_half<KIND>(smem + cur_off, 1, f1, w);   // under the first half's MFMAs
+      if constexpr (KIND == GK_FP8_POW2) {
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+          f1.sa[t2] = f0.sa[t2];
+          if (t2 < 2) f1.sb[t2] = f0.sb[t2];
+        }
+      }
+      mma_half<KIND>(f0, acc);
       interleave_half<KIND>();
+      __builtin_amdgcn_sched_barrier(0);
+      mma_half<KIND>(f1, acc);
+      __builtin_amdgcn_sched_barrier(0);
       cur_off = nxt_off;
     }
     FM_WAIT_VMCNT(0);  // no LDS-DMA may still be in flight when the workgroup exits
@@ -501,11 +464,10 @@ __global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
   // in ragged-K, whose operands the launcher swapped) and the contiguous
   // column is i, so each lane holds 4 consecutive columns of one row.  n_i,
   // the valid rows and split are multiples of 128: every bound below holds or
-  // fails for a wave's whole 128 x 128 block.
+  // fails for a wave's whole 128 x 64 block.
   const int wi = w.wi, wj = w.wj, lrow = w.lrow, lhalf = w.lhalf, lane = w.lane;
-  const int64_t ib = i0 + wi * 128, jb = j0 + wj * 128;
+  const int64_t ib = i0 + wi * 128, jb = j0 + wj * 64;
   const bool live = ib < p.n_i && jb < j0 + p_rows;
-  // start of output row jb, column ib
   int64_t row_off;
   void* C;
   if (MODE == GM_RAGGED_M) {
@@ -517,17 +479,16 @@ __global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
     row_off = e * (second ? p.c2_gs : p.c_gs) + (second ? jb - p.split : jb) * p.ldC + ib;
   }
   if (!p.out_f32) {
-    // bf16: each wave stages its 128 x 128 block in its own 32 KiB of LDS and
-    // writes it back as whole 256-byte row segments.  Every wave's DMAs have
-    // landed and every read of the pipeline stages is done after this barrier.
+    // bf16: each wave stages its 64 x 128 block in its own 16 KiB of LDS and
+    // writes it back as whole 256-byte row segments (after a barrier: every
+    // DMA has landed and every read of the stages is done).
     block_barrier();
     if (!live) return;
-    uint8_t* W = smem + w.wave * 32768;
-    // LDS [row jr][column ic], 16-byte chunk ic/8 swizzled with jr % 16
+    uint8_t* W = smem + w.wave * 16384;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int jr = b * 32 + lrow;
@@ -536,12 +497,11 @@ __global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
           v.y = hw_bf16x2(acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
           *reinterpret_cast<uint2*>(W + jr * 256 + (((a * 4 + q) ^ (jr & 15)) << 4) + lhalf * 8) = v;
         }
-    // 16 lanes x 16 bytes per 128-column row, 4 rows per pass
     const int c = lane & 15;
     uint16_t* dst = static_cast<uint16_t*>(C) + row_off + c * 8;
     const bool vec16 = (p.ldC & 7) == 0;
 #pragma unroll 4
-    for (int n = 0; n < 32; ++n) {
+    for (int n = 0; n < 16; ++n) {
       const int rr = n * 4 + (lane >> 4);
       const uint4 v = *reinterpret_cast<const uint4*>(W + rr * 256 + ((c ^ (rr & 15)) << 4));
       uint16_t* d = dst + rr * p.ldC;
@@ -555,12 +515,11 @@ __global__ __launch_bounds__(256) void gemm256_kernel(GemmParams p) {
     return;
   }
   if (!live) return;
-  // fp32: straight from the accumulators, 4 consecutive columns per lane
   float* dst = static_cast<float*>(C) + row_off + lrow * p.ldC + 4 * lhalf;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) =
@@ -830,11 +789,12 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   }
   if (p.n_tiles == 0) return 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
+  const dim3 block8(512);
   switch (kind) {
-    case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block, 0, s, p); break;
+    case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block8, 0, s, p); break;
     case GK_FP8_F32: hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p); break;
-    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block, 0, s, p); break;
-    case GK_FP8_MX: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE>), grid, block, 0, s, p); break;
+    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block8, 0, s, p); break;
+    case GK_FP8_MX: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE>), grid, block8, 0, s, p); break;
     default: set_error("grouped gemm: unknown kind %d", kind); return 1;
   }
   return check_launch("grouped gemm");
