@@ -67,6 +67,10 @@ void fm_host_decode_e4m3(const uint8_t* in, float* out, int64_t n);
  * asserts the two agree bit for bit. */
 int fm_convert_check(const float* x, int64_t n, void* e4m3_hw, void* e4m3_sw, void* bf16_hw,
                      void* bf16_sw, void* stream);
+/* Device decode check: e4m3 codes [n] (n % 4 == 0) decoded to fp32 by the
+ * gfx950 convert instruction (hw, used by the scaling-aware transpose) and by
+ * the integer routine (sw). */
+int fm_decode_check(const void* codes, int64_t n, float* hw, float* sw, void* stream);
 
 /* ------------------------------------------------------- quantisation ---- */
 /* Replaces fp8_flow_moe.quantize_to_fp8 for activations (1x128 / MX 1x32 row

@@ -56,6 +56,7 @@ SIGNATURES = {
     "fm_host_encode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_host_decode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_convert_check": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "fm_decode_check": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "fm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,
                            _vp, _i64, _vp]),
     "fm_quantize_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _i64,

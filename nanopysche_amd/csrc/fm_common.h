@@ -98,6 +98,21 @@ __device__ __forceinline__ uint32_t hw_e4m3x4(float a, float b, float c, float d
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return uint32_t(w);
 }
+// gfx950 v_cvt_pk_f32_fp8 on the four e4m3 bytes of w (byte i -> f[i]); exact.
+// test_gpu_quant.py::test_hw_decode_matches_software checks all 256 codes.
+__device__ __forceinline__ void hw_dec_e4m3x4(uint32_t w, float f[4]) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
+  const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true);
+  f[0] = lo[0];
+  f[1] = lo[1];
+  f[2] = hi[0];
+  f[3] = hi[1];
+}
+// clamp to +-448 in one v_med3_f32 (equal to clamp448 for every non-NaN value)
+__device__ __forceinline__ float clamp448_med3(float v) {
+  return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);
+}
 // gfx950 v_cvt_pk_bf16_f32 (round-to-nearest-even): low half = a.
 __device__ __forceinline__ uint32_t hw_bf16x2(float a, float b) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));

@@ -110,45 +110,54 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
     }
     return;
   }
-  red[tid] = am;
+  // block amax: wave maximum, then the four waves' through LDS
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-    __syncthreads();
-  }
-  const float s = block_scale(red[0], a.kind == QK_POW2);
+  const float s = block_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), a.kind == QK_POW2);
+  const float inv = 1.0f / s;  // exact for power-of-two scales
+  constexpr bool HW = FM_HW_CVT != 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = rr + 16 * i;
-    uint8_t qb[8];
+    float f[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qb[j] = quant_e4m3(v[i][j], s);
+    for (int j = 0; j < 8; ++j) f[j] = a.kind == QK_POW2 ? v[i][j] * inv : v[i][j] / s;
+    const uint32_t w0 = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
+    const uint32_t w1 = enc_e4m3x4<HW>(f[4], f[5], f[6], f[7]);
     if (a.q)
-      *reinterpret_cast<uint64_t*>(a.q + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
-          pack8_e4m3(qb);
-    tile[row][(cc >> 2)] = uint32_t(qb[0]) | (uint32_t(qb[1]) << 8) | (uint32_t(qb[2]) << 16) |
-                           (uint32_t(qb[3]) << 24);
-    tile[row][(cc >> 2) + 1] = uint32_t(qb[4]) | (uint32_t(qb[5]) << 8) |
-                               (uint32_t(qb[6]) << 16) | (uint32_t(qb[7]) << 24);
+      *reinterpret_cast<uint2*>(a.q + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
+          make_uint2(w0, w1);
+    tile[row][(cc >> 2)] = w0;
+    tile[row][(cc >> 2) + 1] = w1;
   }
   if (a.q && tid == 0) a.s[g * a.gs_s + ((r0 + a.q_row_off) >> 7) * a.ld_s + (c0 >> 7)] = s;
   if (!a.qt) return;
   __syncthreads();
-  uint8_t* dst = a.qt + g * a.gs_qt + (c0 + c) * a.ld_qt + a.qt_col_off + r0 + 64 * h;
-  for (int r16 = 0; r16 < 64; r16 += 16) {
-    uint32_t w4[4];
+  // transposed payload: thread -> columns [4 cg, +4) x rows [16 rg, +16), 4 x 4
+  // byte blocks transposed with v_perm_b32; the 8 lanes of one cg write a whole
+  // 128-byte row of the transpose
+  const int rg = tid & 7, cg = tid >> 3;
+  uint32_t cw[4][4];   // [column][4-row word]
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int row = 64 * h + r16 + 4 * k + b;
-        word |= ((tile[row][c >> 2] >> (8 * (c & 3))) & 0xffu) << (8 * b);
-      }
-      w4[k] = word;
-    }
-    *reinterpret_cast<uint4*>(dst + r16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  for (int k = 0; k < 4; ++k) {
+    const int rb = 16 * rg + 4 * k;
+    const uint32_t a0 = tile[rb][cg], a1 = tile[rb + 1][cg], a2 = tile[rb + 2][cg], a3 = tile[rb + 3][cg];
+    // D.byte[i] = {S0, S1}.byte[sel.byte[i]], bytes 0-3 from S1 and 4-7 from S0
+    const uint32_t p01l = __builtin_amdgcn_perm(a1, a0, 0x05010400u);  // a0c0 a1c0 a0c1 a1c1
+    const uint32_t p01h = __builtin_amdgcn_perm(a1, a0, 0x07030602u);  // a0c2 a1c2 a0c3 a1c3
+    const uint32_t p23l = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+    const uint32_t p23h = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+    cw[0][k] = __builtin_amdgcn_perm(p23l, p01l, 0x05040100u);         // a0c0 a1c0 a2c0 a3c0
+    cw[1][k] = __builtin_amdgcn_perm(p23l, p01l, 0x07060302u);
+    cw[2][k] = __builtin_amdgcn_perm(p23h, p01h, 0x05040100u);
+    cw[3][k] = __builtin_amdgcn_perm(p23h, p01h, 0x07060302u);
   }
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4)
+    *reinterpret_cast<uint4*>(a.qt + g * a.gs_qt + (c0 + 4 * cg + c4) * a.ld_qt + a.qt_col_off + r0 + 16 * rg) =
+        make_uint4(cw[c4][0], cw[c4][1], cw[c4][2], cw[c4][3]);
   if (tid == 0) a.st[g * a.gs_st + (c0 >> 7) * a.ld_st + ((r0 + a.qt_col_off) >> 7)] = s;
 }
 
@@ -265,11 +274,37 @@ __global__ __launch_bounds__(256) void convert_check_kernel(const float* x, int6
   }
 }
 
+// e4m3 -> f32 by the hardware convert and by the integer routine.
+__global__ __launch_bounds__(256) void decode_check_kernel(const uint32_t* codes, int64_t n4, float* hw,
+                                                           float* sw) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+    const uint32_t w = codes[i];
+    float d[4];
+    hw_dec_e4m3x4(w, d);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      hw[4 * i + b] = d[b];
+      sw[4 * i + b] = e4m3_to_f32(uint8_t(w >> (8 * b)));
+    }
+  }
+}
+
 }  // namespace fm
 
 using namespace fm;
 
 extern "C" {
+
+int fm_decode_check(const void* codes, int64_t n, float* hw, float* sw, void* stream) {
+  FM_REQUIRE(codes && hw && sw, "fm_decode_check: null pointer");
+  FM_REQUIRE(n % 4 == 0, "fm_decode_check: n must be a multiple of 4");
+  if (n == 0) return 0;
+  const int64_t n4 = n / 4;
+  const unsigned blocks = unsigned(n4 / 256 + 1 < 4096 ? n4 / 256 + 1 : 4096);
+  hipLaunchKernelGGL(decode_check_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint32_t*>(codes), n4, hw, sw);
+  return check_launch("fm_decode_check");
+}
 
 int fm_convert_check(const float* x, int64_t n, void* e4m3_hw, void* e4m3_sw, void* bf16_hw,
                      void* bf16_sw, void* stream) {

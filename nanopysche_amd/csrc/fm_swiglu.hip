@@ -5,7 +5,9 @@
 //   fm_swiglu_backward      -- [dg | du] from one read of g, u and dh, emitted
 //                              the same way (the [M, 2H] layout feeds the fused
 //                              dx = dg w1 + du w3 GEMM and the dW1|dW3 GEMM)
-// silu(g) = g / (1 + exp(-g)) in fp32; d silu = s (1 + g (1 - s)), s = sigmoid(g).
+// silu(g) = g * s, s = sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware
+// v_exp_f32 and v_rcp_f32 (a few fp32 ulps; test_gpu_swiglu.py holds the
+// results to torch's CPU silu and autograd); d silu = s (1 + g (1 - s)).
 #include "fm_tile.h"
 #include "../../include/fm_hip.h"
 
@@ -21,7 +23,9 @@ __device__ __forceinline__ void load8_bf16(const uint16_t* p, float v[8]) {
   }
 }
 
-__device__ __forceinline__ float sigmoidf(float g) { return 1.f / (1.f + expf(-g)); }
+__device__ __forceinline__ float sigmoidf(float g) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
 
 struct SwigluSrc {
   static constexpr int kOut = 1;
@@ -33,7 +37,7 @@ struct SwigluSrc {
     load8_bf16(g + row * ld_g + col, gv);
     load8_bf16(u + row * ld_u + col, uv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[0][i] = (gv[i] / (1.f + expf(-gv[i]))) * uv[i];
+    for (int i = 0; i < 8; ++i) v[0][i] = (gv[i] * sigmoidf(gv[i])) * uv[i];
   }
 };
 

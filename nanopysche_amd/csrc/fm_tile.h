@@ -57,7 +57,7 @@ constexpr int kTileLdsPitch = 129;
 template <bool HW>
 __device__ __forceinline__ uint32_t enc_e4m3x4(float a, float b, float c, float d) {
   if constexpr (HW) {
-    return hw_e4m3x4(clamp448(a), clamp448(b), clamp448(c), clamp448(d));
+    return hw_e4m3x4(clamp448_med3(a), clamp448_med3(b), clamp448_med3(c), clamp448_med3(d));
   } else {
     return uint32_t(f32_to_e4m3(clamp448(a))) | (uint32_t(f32_to_e4m3(clamp448(b))) << 8) |
            (uint32_t(f32_to_e4m3(clamp448(c))) << 16) | (uint32_t(f32_to_e4m3(clamp448(d))) << 24);
@@ -210,23 +210,41 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
       __syncthreads();
       const float st = red[0];
       const float inv = 1.0f / st;  // exact: power of two
-      const int wsh = 8 * (c & 3);
-      for (int r16 = 0; r16 < 64; r16 += 16) {
-        uint32_t w[4];
+      // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
+      // the 8 lanes of one cg write a whole 128-byte row of the transpose.
+      // decode(q) * (s_row / s_col) is exact (powers of two) and <= 448.
+      const int rg = tid & 7, cg = tid >> 3;
+      uint32_t w[4][4];   // [column][4-row word]
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          float f[4];
+      for (int k = 0; k < 4; ++k) {
+        float f[4][4];    // [row][column]
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const int row = 64 * h + r16 + 4 * k + b;
-            const uint8_t code = uint8_t(lds_code[row * 33 + (c >> 2)] >> wsh);
-            f[b] = (e4m3_to_f32(code) * rscale[row]) * inv;
+        for (int b = 0; b < 4; ++b) {
+          const int row = 16 * rg + 4 * k + b;
+          const float ratio = rscale[row] * inv;
+          const uint32_t word = lds_code[row * 33 + cg];
+          float d[4];
+          if constexpr (HW) {
+            hw_dec_e4m3x4(word, d);
+          } else {
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
           }
-          w[k] = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = d[c4] * ratio;
         }
-        *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
       }
-      if (h == 0) static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + gcol] = st;
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)
+        *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * o.ld_col + row0 + 16 * rg) =
+            make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+      if (rg == 0) {
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4)
+          static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + ocol + 4 * cg + c4] = st;
+      }
     } else if (KIND == QK_BLOCK) {
       float am = 0.f;
       for (int r = 0; r < 64; ++r) am = fmaxf(am, fabsf(lds_val[(64 * h + r) * kTileLdsPitch + c]));

@@ -184,3 +184,23 @@ def test_hw_convert_matches_software(dev):
     # and the software path is the oracle's (torch's) cast
     ref = ofp8.e4m3_encode(np.clip(x, -448, 448))
     assert np.array_equal(e_sw.cpu().numpy(), ref)
+
+
+def test_hw_decode_matches_software(dev):
+    """The scaling-aware transpose decodes e4m3 with gfx950's v_cvt_pk_f32_fp8;
+    it must equal the integer decode (pinned against torch on the CPU) for all
+    256 codes, NaN codes included."""
+    from nanopysche_amd import _lib
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).repeat(4).to(dev)
+    hw = torch.empty(codes.numel(), dtype=torch.float32, device=dev)
+    sw = torch.empty_like(hw)
+    _lib.call("fm_decode_check", _lib.ptr(codes), codes.numel(), _lib.ptr(hw), _lib.ptr(sw),
+              _lib.stream_of(codes))
+    h, s_ = hw.cpu().numpy(), sw.cpu().numpy()
+    nan = np.isnan(s_)
+    assert np.array_equal(np.isnan(h), nan) and nan.sum() == 2 * 4
+    assert np.array_equal(h[~nan].view(np.uint32), s_[~nan].view(np.uint32))
+    ref = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(ref), nan[:256])
+    assert np.array_equal(ref[~nan[:256]].view(np.uint32), s_[:256][~nan[:256]].view(np.uint32))
