@@ -1,15 +1,16 @@
 """Benchmark of the fp8_flow_moe expert block on one MI355X.
 
-Workload: T=8192 tokens, d_model=2048, 8 experts,
-top-2, SwiGLU ffn_hidden=1408, exactly balanced routing (2048 assignments per
-expert, router weights = softmax of seeded logits at those indices), FP8 GEMMs
-forced (threshold 0), recipe flow_moe (1x128 / 128x128 power-of-two scales).
-One step = expert-block forward + backward, including the routing sort, all
-quantisation and the re-quantisation of the expert weights (their cache is
-dropped every step, as after an optimizer update).  Inputs are resident in HBM
-before timing starts.
+Default workload (the metric's configuration): T=8192
+tokens, d_model=2048, 8 experts, top-2, SwiGLU ffn_hidden=1408, exactly
+balanced routing (2048 assignments per expert, router weights = softmax of
+seeded logits at those indices), FP8 GEMMs forced (threshold 0), recipe
+flow_moe (1x128 / 128x128 power-of-two scales).  One step = expert-block
+forward + backward, including the routing sort, all quantisation and the
+re-quantisation of the expert weights (their cache is dropped every step, as
+after an optimizer update).  Inputs are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--recipe flow_moe]
+    python bench.py --workload c1|c4|c5    # the other configs, one JSON line each
 
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
@@ -31,6 +32,7 @@ PEAK_TFLOPS = {"fp8": 5000.0, "bf16": 2500.0}
 
 
 def synthetic_inputs(T, D, H, E, K, seed, dev):
+    """configs[2] inputs: balanced routing, weights N(0, 0.02), upstream grad N(0, 1e-2)."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
@@ -43,6 +45,12 @@ def synthetic_inputs(T, D, H, E, K, seed, dev):
     w1, w2, w3 = [(torch.randn(E * H, D, generator=g) * 0.02).bfloat16() for _ in range(3)]
     go = (torch.randn(T, D, generator=g) * 1e-2).bfloat16()
     return [a.to(dev) for a in (x, w, idx, w1, w2, w3, go)]
+
+
+def device_normal(shape, std, gen, dev, dtype):
+    import torch
+
+    return (torch.randn(*shape, generator=gen, device=dev) * std).to(dtype)
 
 
 class GemmTimer:
@@ -73,6 +81,65 @@ class GemmTimer:
             d["ms"] += ms
             d["flops"] += flops
         return out
+
+
+def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, backward=True,
+               gemm_timer=True, pre_step=None):
+    """Times `steps` calls of the expert block (forward, + backward when
+    `backward`), weight cache dropped every step.  Returns (ms per step, GEMM
+    event summary or None)."""
+    import torch
+
+    import nanopysche_amd as fm
+    from nanopysche_amd import flow_moe as fmm
+
+    D = x.shape[1]
+    H = w1.shape[0] // E
+    cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, fm.FP8RecipeType(recipe)))
+    blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=threshold)
+    params = [t.detach().clone().requires_grad_(backward) for t in (w1, w2, w3)]
+    blk.set_weights(*params)
+    xr = x.detach().clone().requires_grad_(backward)
+    wr = w.detach().clone().requires_grad_(backward)
+
+    def step():
+        blk._cache.clear()  # weights change every training step: re-quantise them
+        r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
+        if backward:
+            for p in params:
+                p.grad = None
+            xr.grad = None
+            wr.grad = None
+            blk(xr, r_w, r_idx, 0, E).backward(go)
+        else:
+            with torch.no_grad():
+                blk(xr, r_w, r_idx, 0, E)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = GemmTimer() if gemm_timer else None
+    fmm.GEMM_TIMER = timer
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    fmm.GEMM_TIMER = None
+    return elapsed * 1e3 / steps, (None if timer is None else timer.summary())
+
+
+def gemm_report(summ, steps, flops_scale=1.0):
+    """GEMM event totals per step.  The timer counts 2*T*K*N*K' FLOPs per launch
+    (every routing slot); `flops_scale` = valid assignments / (T*K) corrects
+    that when some slots point outside the local experts."""
+    gemm_ms = sum(v["ms"] for v in summ.values()) / steps
+    kernels = {k: {"avg_us": round(v["ms"] * 1e3 / v["launches"], 2),
+                   "tflops": round(v["flops"] * flops_scale / (v["ms"] * 1e-3) / 1e12, 1),
+                   "launches_per_step": v["launches"] // steps} for k, v in summ.items()}
+    flops = sum(v["flops"] for v in summ.values()) * flops_scale / steps
+    return {"tflops_all_gemms": round(flops / (gemm_ms * 1e-3) / 1e12, 1),
+            "gemm_ms_per_step": round(gemm_ms, 4), "kernels": kernels}
 
 
 def recorded_traffic(kernel, recipe):
@@ -124,81 +191,27 @@ def cpu_baseline(T, D, H, E, K, budget_s=12.0):
                       f"per-expert loop fwd+bwd, median of {len(times)} runs; cpu: {model}"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
-                         "FETCH_SIZE / WRITE_SIZE against known bytes)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
-        sys.exit(2)
-
+# ============================================================== configs[2] ====
+def workload_c3(args, dev):
     import torch
 
-    import nanopysche_amd as fm
-    from nanopysche_amd import flow_moe as fmm
-
-    dev = torch.device("cuda:0")
     T, D, E, K, H = 8192, 2048, 8, 2, 1408
     A = T * K
     x, w, idx, w1, w2, w3, go = synthetic_inputs(T, D, H, E, K, seed=2, dev=dev)
-    rt = fm.FP8RecipeType(args.recipe)
-    cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, rt))
-    blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=0)
-    params = [t.clone().requires_grad_(True) for t in (w1, w2, w3)]
-    blk.set_weights(*params)
-    xr = x.clone().requires_grad_(True)
-    wr = w.clone().requires_grad_(True)
-
-    def step():
-        blk._cache.clear()  # weights change every training step: re-quantise them
-        for p in params:
-            p.grad = None
-        xr.grad = None
-        wr.grad = None
-        out = blk(xr, wr, idx, 0, E)
-        out.backward(go)
-
     if args.copy_probe:
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         b = torch.empty_like(a)
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # timed region: HIP events around every grouped GEMM on its launch stream
-    timer = GemmTimer()
-    fmm.GEMM_TIMER = timer
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    fmm.GEMM_TIMER = None
-    ms = elapsed * 1e3 / args.steps
-
-    summ = timer.summary()
+    ms, summ = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup)
     dom = max(summ, key=lambda k: summ[k]["ms"])
     d = summ[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
     peak = PEAK_TFLOPS["bf16" if args.recipe == "none" else "fp8"]
-    gemm_ms = sum(v["ms"] for v in summ.values()) / args.steps
-    kernels = {k: {"avg_us": round(v["ms"] * 1e3 / v["launches"], 2),
-                   "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
-                   "launches_per_step": v["launches"] // args.steps} for k, v in summ.items()}
     traffic = recorded_traffic(dom, args.recipe)
-
     cpu = None if args.no_cpu_baseline else cpu_baseline(T, D, H, E, K)
-    res = {
+    return {
         "metric": "MoE layer fwd+bwd tokens/s on 1 MI355X",
         "value": round(T / (ms * 1e-3), 1),
         "unit": "tokens/s",
@@ -220,11 +233,181 @@ def main():
                      "traffic": None if traffic is None else traffic["bytes_per_launch"],
                      "kernel": dom,
                      "traffic_source": None if traffic is None else traffic["source"]},
-        "gemm": {"tflops_all_gemms": round(18 * A * D * H / (gemm_ms * 1e-3) / 1e12, 1),
-                 "gemm_ms_per_step": round(gemm_ms, 4), "kernels": kernels},
+        "gemm": gemm_report(summ, args.steps),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res))
+
+
+# ============================================================== configs[0] ====
+def workload_c1(args, dev):
+    """BF16 expert block forward, top-1 softmax over 4 experts (the router's
+    top-k runs inside the step from precomputed gate logits)."""
+    import torch
+
+    import nanopysche_amd as fm
+
+    T, D, E, K, H = 4096, 2048, 4, 1, 5632
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = device_normal((T, D), 1.0, gen, dev, torch.bfloat16)
+    wg = device_normal((E, D), 0.02, gen, dev, torch.bfloat16)
+    bias = torch.full((E,), -1.0, device=dev)   # gate bias init, model/moe.py:107-109
+    logits = (x.float() @ wg.float().t() + bias).contiguous()
+    w1, w2, w3 = [device_normal((E * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
+    w0, i0 = fm.topk_gating(logits, K, "softmax")
+
+    def pre():
+        return fm.topk_gating(logits, K, "softmax")
+
+    ms, summ = time_layer(x, w0, i0, w1, w2, w3, None, E, "none", 1 << 40, args.steps, args.warmup,
+                          backward=False, pre_step=pre)
+    counts = torch.bincount(i0.reshape(-1), minlength=E).tolist()
+    flops = 6.0 * T * K * D * H
+    return {
+        "metric": "MoE layer fwd tokens/s on 1 MI355X (configs[0], BF16)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "configs[0]: BF16 expert block forward, top-1 softmax", "tokens": T,
+                   "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H, "tokens_per_expert": counts},
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),
+        "gemm": gemm_report(summ, args.steps),
+    }
+
+
+# ============================================================== configs[3] ====
+def zipf_gumbel_topk(T, E, K, s, seed):
+    """Per-token K distinct experts by Gumbel-top-K on log p_e, p_e proportional
+    to rank^-s over a seeded permutation; router weights softmax of the
+    perturbed scores at the chosen experts."""
+    import numpy as np
+    import torch
+
+    rng = np.random.default_rng(seed)
+    ranks = rng.permutation(E) + 1
+    logp = -s * np.log(ranks.astype(np.float64))
+    score = logp[None, :] + rng.gumbel(size=(T, E))
+    idx = np.argsort(-score, axis=1, kind="stable")[:, :K]
+    sel = np.take_along_axis(score, idx, axis=1)
+    w = np.exp(sel - sel.max(axis=1, keepdims=True))
+    w = w / w.sum(axis=1, keepdims=True)
+    return torch.from_numpy(w.astype(np.float32)), torch.from_numpy(idx.astype(np.int64))
+
+
+def workload_c4(args, dev):
+    """FP8 (flow_moe) vs BF16 grouped GEMM crossover, fwd+bwd, Zipf(1.1) routing."""
+    import torch
+
+    D, E, K, H = 4096, 8, 2, 14336
+    gen = torch.Generator(device=dev).manual_seed(3)
+    w1, w2, w3 = [device_normal((E * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
+    sweep = []
+    for t in (512, 1024, 2048, 4096, 8192, 16384):
+        T = 4 * t
+        w, idx = zipf_gumbel_topk(T, E, K, 1.1, seed=3)
+        w, idx = w.to(dev), idx.to(dev)
+        x = device_normal((T, D), 1.0, gen, dev, torch.bfloat16)
+        go = device_normal((T, D), 1e-2, gen, dev, torch.bfloat16)
+        flops = 18.0 * T * K * D * H
+        steps = max(2, min(args.steps, int(2e15 / flops) + 1))
+        row = {"tokens_per_expert": t, "tokens": T,
+               "max_tokens_per_expert": int(torch.bincount(idx.reshape(-1), minlength=E).max())}
+        for name, recipe in (("bf16", "none"), ("fp8", "flow_moe")):
+            ms, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False)
+            row[f"{name}_ms"] = round(ms, 3)
+            row[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        row["fp8_speedup"] = round(row["bf16_ms"] / row["fp8_ms"], 3)
+        sweep.append(row)
+        print(json.dumps({"progress": row}), file=sys.stderr, flush=True)
+        del x, go
+        torch.cuda.empty_cache()
+    faster = [r["tokens_per_expert"] for r in sweep if r["fp8_speedup"] > 1.0]
+    return {
+        "metric": "FP8 vs BF16 expert block fwd+bwd crossover on 1 MI355X (configs[3])",
+        "n_gpus": 1, "data": "synthetic", "dtype": "fp8-e4m3 vs bf16",
+        "config": {"workload": "configs[3]: D=4096, E=8, top-2, H=14336, Zipf(1.1) Gumbel-top-2 routing",
+                   "fp8_recipe": "flow_moe", "threshold": 0},
+        "sweep": sweep,
+        "fp8_faster_from_tokens_per_expert": min(faster) if faster else None,
+    }
+
+
+# ============================================================== configs[4] ====
+def workload_c5(args, dev):
+    """One GPU's 32-expert share of a 256-expert layer, MXFP8, fwd+bwd."""
+    import torch
+
+    import nanopysche_amd as fm
+
+    D, E_local, E_global, K, H, A_target = 7168, 32, 256, 8, 2048, 65536
+    gen = torch.Generator(device=dev).manual_seed(4)
+    # per-expert bias from Zipf(1.2) popularity (added before the sigmoid, model/moe.py:153-162);
+    # two local experts never receive tokens
+    g = torch.Generator().manual_seed(4)
+    ranks = torch.randperm(E_global, generator=g).float() + 1
+    bias = (-1.2 * torch.log(ranks)).to(dev)
+    bias[[5, 17]] = -1e9
+    # this rank receives the tokens with at least one assignment to its 32
+    # experts (ids 0-31), in order, until A_target local assignments
+    ws, ids, total = [], [], 0
+    while total < A_target:
+        logits = device_normal((65536, E_global), 1.0, gen, dev, torch.float32) + bias
+        w_, i_ = fm.topk_gating(logits.contiguous(), K, "sigmoid")
+        has = (i_ < E_local).any(dim=1)
+        ws.append(w_[has])
+        ids.append(i_[has])
+        total += int((i_[has] < E_local).sum())
+    wts, idx = torch.cat(ws), torch.cat(ids)
+    local = idx < E_local
+    csum = torch.cumsum(local.reshape(-1).int(), 0).reshape(idx.shape)
+    keep = local & (csum <= A_target)
+    n_tok = int((csum[:, 0] - local[:, 0].int() < A_target).sum())   # tokens holding a kept slot
+    # assignments outside this rank's experts carry an out-of-range index, which routing ignores
+    idx = torch.where(keep, idx, torch.full_like(idx, E_global))[:n_tok].contiguous()
+    wts = wts[:n_tok].contiguous()
+    A = int(keep[:n_tok].sum())
+    counts = torch.bincount(idx[idx < E_local], minlength=E_local)
+    x = device_normal((n_tok, D), 1.0, gen, dev, torch.bfloat16)
+    go = device_normal((n_tok, D), 1e-2, gen, dev, torch.bfloat16)
+    w1, w2, w3 = [device_normal((E_local * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
+    ms, summ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup)
+    flops = 18.0 * A * D * H
+    return {
+        "metric": "MoE expert block fwd+bwd assignments/s on 1 MI355X (configs[4], MXFP8)",
+        "value": round(A / (ms * 1e-3), 1), "unit": "assignments/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "dtype": "fp8-e4m3 (MX e8m0 1x32)", "data": "synthetic",
+        "config": {"workload": "configs[4]: 32 local experts of 256, sigmoid top-8 with Zipf(1.2) bias",
+                   "tokens": n_tok, "assignments": A, "d_model": D, "local_experts": E_local,
+                   "ffn_hidden": H, "zero_token_experts": int((counts == 0).sum()),
+                   "max_tokens_per_expert": int(counts.max())},
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "frac_of_fp8_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["fp8"], 4),
+        "gemm": gemm_report(summ, args.steps, flops_scale=A / (n_tok * K)),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c4", "c5"])
+    ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against known bytes)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    run = {"c3": workload_c3, "c1": workload_c1, "c4": workload_c4, "c5": workload_c5}[args.workload]
+    print(json.dumps(run(args, dev)))
 
 
 if __name__ == "__main__":

@@ -36,8 +36,9 @@
 //   gemm_f32_kernel FP8_F32.  Tile 256 x 128, 256 threads = 4 wave64 as
 //                   2 x 2, three LDS stages; each 128-deep partial sum is
 //                   promoted through a second set of accumulator registers.
-// Workgroup ids are remapped so each XCD walks a contiguous range of tiles,
-// grouped 8 token tiles at a time for L2 reuse of weights and activations.
+// Ragged-M workgroup ids are remapped so each XCD walks a contiguous range of
+// the valid tiles, grouped 8 token tiles at a time for L2 reuse of weights and
+// activations; ragged-K tiles keep launch order (balances uneven experts).
 #include "fm_common.h"
 #include "../../include/fm_hip.h"
 
@@ -323,13 +324,28 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
 
   // ---------------------------------------------------------- tile decode ----
-  const int64_t per_xcd = (p.n_tiles + 7) / 8;
-  const int64_t L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (L >= p.n_tiles) return;
+  // ragged-M: the valid 256-token tiles (sum over experts of ceil(rows / 256),
+  // from the device-side offsets; the launch is sized by a host bound) are
+  // split into 8 contiguous ranges, one per XCD (blockIdx % 8), for L2 reuse.
+  // ragged-K: tiles in launch order, so one expert's tiles (whose K lengths
+  // differ between experts) spread over every XCD and the hardware's dynamic
+  // workgroup dispatch balances them.
   const int64_t NI = (p.n_i + kT - 1) / kT;
+  int64_t JT = 0, L;
+  if (MODE == GM_RAGGED_M) {
+    for (int x = 0; x < p.E; ++x) JT += (p.offsets[x + 1] - p.offsets[x] + kT - 1) / kT;
+    const int64_t n_valid = JT * NI;
+    const int64_t per_xcd = (n_valid + 7) / 8;
+    const int64_t k = blockIdx.x / 8;
+    if (k >= per_xcd) return;
+    L = int64_t(blockIdx.x % 8) * per_xcd + k;
+    if (L >= n_valid) return;
+  } else {
+    L = blockIdx.x;
+    if (L >= p.n_tiles) return;
+  }
   int64_t e = -1, i0 = 0, j0 = 0, j_end = 0, k_lo, k_hi;
   if (MODE == GM_RAGGED_M) {
-    const int64_t JT = p.j_tiles;
     const int64_t group = L / (kGroupM * NI);
     const int64_t first = group * kGroupM;
     const int64_t gsz = JT - first < kGroupM ? JT - first : kGroupM;
@@ -613,13 +629,24 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
   uint8_t* const smem2 = smem + 2 * SM::kStage;
 
   // ---------------------------------------------------------- tile decode ----
-  const int64_t per_xcd = (p.n_tiles + 7) / 8;
-  const int64_t L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (L >= p.n_tiles) return;
+  // ragged-M: the valid 128-row tiles [0, offsets[E] / 128) split into one
+  // contiguous range per XCD; ragged-K: tiles in launch order (as above).
   int64_t e, i0, j0, k_lo, k_hi;
   const int64_t NI = (p.n_i + kBI - 1) / kBI;
+  int64_t L;
   if (MODE == GM_RAGGED_M) {
-    const int64_t MT = p.m_tiles;
+    const int64_t n_valid = int64_t(p.offsets[p.E] / kBJ) * NI;
+    const int64_t per_xcd = (n_valid + 7) / 8;
+    const int64_t k = blockIdx.x / 8;
+    if (k >= per_xcd) return;
+    L = int64_t(blockIdx.x % 8) * per_xcd + k;
+    if (L >= n_valid) return;
+  } else {
+    L = blockIdx.x;
+    if (L >= p.n_tiles) return;
+  }
+  if (MODE == GM_RAGGED_M) {
+    const int64_t MT = p.offsets[p.E] / kBJ;
     const int64_t group = L / (kGroupM * NI);
     const int64_t first = group * kGroupM;
     const int64_t gsz = MT - first < kGroupM ? MT - first : kGroupM;
