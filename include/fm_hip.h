@@ -85,6 +85,17 @@ int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t 
                 void* q, int64_t ld_q, void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st,
                 int64_t ld_st, void* stream);
 
+/* fm_quantize of the fused gate|up weight without materialising it: a and b
+ * are [groups, rows, cols] stacks (w1 and w3 of model/moe.py:1293-1295,
+ * groups = experts, rows = H; pitch ld, dtype bf16 or fp32) read as one
+ * [groups * 2 * rows, cols] matrix whose group g holds a's rows then b's
+ * (torch.cat([w1_e, w3_e]) per expert).  Outputs and kinds as fm_quantize (the
+ * MX recipe quantises expert weights this way: 1x32 along cols, 32x1 along
+ * the stacked rows). */
+int fm_quantize_pair(const void* a, const void* b, int dtype, int64_t groups, int64_t rows,
+                     int64_t cols, int64_t ld, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s,
+                     void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream);
+
 /* Replaces quantize_to_fp8 for expert weights (128x128 blocks), batched over
  * `groups` matrices [rows, cols] of w (pitch ld_w, group stride gs_w), writing
  * into row offset q_row_off of q (and column offset qt_col_off of the

@@ -59,6 +59,8 @@ SIGNATURES = {
     "fm_decode_check": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "fm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,
                            _vp, _i64, _vp]),
+    "fm_quantize_pair": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64,
+                                _vp, _i64, _vp, _i64, _vp]),
     "fm_quantize_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _i64,
                                   _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                                   _vp]),

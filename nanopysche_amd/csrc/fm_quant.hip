@@ -1,6 +1,8 @@
 // Blockwise e4m3 quantisation kernels and their C-ABI entry points:
 //   fm_quantize            -- 1x128 / 1x32 row blocks, optional fused 128x1 /
 //                             32x1 transposed output (one read of the source)
+//   fm_quantize_pair       -- fm_quantize of two interleaved expert weight stacks
+//                             (gate|up) read in place
 //   fm_quantize_weight     -- 128x128 blocks, batched over expert groups, with
 //                             optional transposed payload (same blocks)
 //   fm_dequantize          -- any block layout -> bf16 / fp32
@@ -38,6 +40,22 @@ __device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col,
   v[0][0] = a.x; v[0][1] = a.y; v[0][2] = a.z; v[0][3] = a.w;
   v[0][4] = b.x; v[0][5] = b.y; v[0][6] = b.z; v[0][7] = b.w;
 }
+
+// Two expert weight stacks a, b = [groups][rows][cols] read as one
+// [groups][2 rows][cols] matrix (group g: rows of a, then rows of b), the
+// layout of the fused gate|up weight -- without materialising it.
+template <typename T>
+struct PairSrc {
+  static constexpr int kOut = 1;
+  const T* a;
+  const T* b;
+  int64_t rows, ld;
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
+    const int64_t g = row / (2 * rows), r = row % (2 * rows);
+    const T* base = r < rows ? a : b;
+    DenseSrc<T>{base + (g * rows + (r < rows ? r : r - rows)) * ld, 0}.load8(0, col, v);
+  }
+};
 
 // ------------------------------------------------------- 128x128 weight blocks ----
 struct WeightQuantArgs {
@@ -333,6 +351,23 @@ int fm_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t 
                                 cols, sm, "fm_quantize");
   return launch_tile_producer(DenseSrc<float>{static_cast<const float*>(x), ld_x}, o, rows, cols,
                               sm, "fm_quantize");
+}
+
+int fm_quantize_pair(const void* a, const void* b, int dtype, int64_t groups, int64_t rows,
+                     int64_t cols, int64_t ld, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s,
+                     void* qt, int64_t ld_qt, void* st, int64_t ld_st, void* stream) {
+  FM_REQUIRE(a != nullptr && b != nullptr, "fm_quantize_pair: null input");
+  FM_REQUIRE(dtype == FM_DTYPE_BF16 || dtype == FM_DTYPE_F32, "fm_quantize_pair: bad input dtype %d", dtype);
+  FM_REQUIRE(groups > 0 && rows > 0, "fm_quantize_pair: groups and rows must be positive");
+  FM_REQUIRE(ld >= cols && ld % 8 == 0, "fm_quantize_pair: input pitch must be >= cols and a multiple of 8");
+  const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, nullptr);
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  const int64_t total = groups * 2 * rows;
+  if (dtype == FM_DTYPE_BF16)
+    return launch_tile_producer(PairSrc<uint16_t>{static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                                                  rows, ld}, o, total, cols, sm, "fm_quantize_pair");
+  return launch_tile_producer(PairSrc<float>{static_cast<const float*>(a), static_cast<const float*>(b), rows, ld},
+                              o, total, cols, sm, "fm_quantize_pair");
 }
 
 int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows, int64_t cols,

@@ -511,20 +511,16 @@ class ExpertWeights:
 
     def _build_mx(self, w1, w2, w3, E, H, D):
         dev = w1.device
-        W13src = torch.cat([w1.reshape(E, H, D), w3.reshape(E, H, D)], dim=1).reshape(E * 2 * H, D)
-        W13src = W13src.to(torch.bfloat16).contiguous()
-        W2src = w2.to(torch.bfloat16).contiguous()
+        w1, w2, w3 = (w.contiguous() for w in (w1, w2, w3))
         stream = _lib.stream_of(w1)
-
-        def q(src, rows):
-            qq, s, qt, st = _alloc_quant(rows, D, _lib.QUANT_MX, True, True, dev)
-            _lib.call("fm_quantize", _lib.ptr(src), _lib.DTYPE_BF16, rows, D, D,
-                      *_tile_args(_lib.QUANT_MX, qq, s, qt, st), stream)
-            return qq, s, qt, st
-
-        W13, S13, W13t, S13t = q(W13src, E * 2 * H)
-        W2, S2, W2t, S2t = q(W2src, E * H)
-        self._keep = (W13src, W2src)
+        MX = _lib.QUANT_MX
+        # gate|up: w1 and w3 read in place as the [E, 2H, D] stack
+        W13, S13, W13t, S13t = _alloc_quant(E * 2 * H, D, MX, True, True, dev)
+        _lib.call("fm_quantize_pair", _lib.ptr(w1), _lib.ptr(w3), _src_dtype(w1), E, H, D, D,
+                  *_tile_args(MX, W13, S13, W13t, S13t), stream)
+        W2, S2, W2t, S2t = _alloc_quant(E * H, D, MX, True, True, dev)
+        _lib.call("fm_quantize", _lib.ptr(w2), _src_dtype(w2), E * H, D, D, *_tile_args(MX, W2, S2, W2t, S2t),
+                  stream)
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 32, 1, 2 * H * D // 32, 0, 2 * H, D)
         self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H)
         self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D)

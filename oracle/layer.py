@@ -138,11 +138,14 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
     rt = orouting.sort_assignments(indices.cpu().numpy(), E)
     offs = rt["offsets"]
     Xp = orouting.permute_pad(xs, rt["assign_of_row"], K)
-    W1 = _bf16(_np(w1)).reshape(E, H, D)
-    W2 = _bf16(_np(w2)).reshape(E, H, D)
-    W3 = _bf16(_np(w3)).reshape(E, H, D)
-    Mp = int(offs[-1])
     fp8 = recipe is not None
+    # FP8 recipes quantise the parameters' own values (fp32 master weights stay
+    # fp32); the BF16 path multiplies their bf16 rounding
+    wv = (lambda a: _np(a).astype(np.float32)) if fp8 else (lambda a: _bf16(_np(a)))
+    W1 = wv(w1).reshape(E, H, D)
+    W2 = wv(w2).reshape(E, H, D)
+    W3 = wv(w3).reshape(E, H, D)
+    Mp = int(offs[-1])
     Xv = _q_rows(Xp, recipe) if fp8 else Xp
     GU = np.zeros((Mp, 2 * H), np.float32)
     Y = np.zeros((Mp, D), np.float32)

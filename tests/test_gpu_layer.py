@@ -147,3 +147,36 @@ def test_weight_cache_tracks_parameter_updates(dev):
         p[1].mul_(2.0)  # in-place update bumps _version
     b = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
     assert torch.allclose(b.float(), 2 * a.float(), rtol=2e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["block", "pow2", "mx"])
+def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
+    """The cached gate|up and down operands are the parameters' own values
+    quantised (fp32 master weights are not rounded to bf16 first): bytes and
+    scales equal the oracle quantiser applied to the [E, 2H, D] stack of w1|w3
+    (128x128 blocks, or 1x32 for MX) and to w2."""
+    import numpy as np
+
+    from nanopysche_amd import _lib
+    from nanopysche_amd.flow_moe import ExpertWeights
+    from oracle import fp8 as ofp8
+
+    E, H, D = 3, 256, 384
+    g = torch.Generator().manual_seed(5)
+    w1, w2, w3 = ((torch.randn(E * H, D, generator=g) * 0.02).to(param_dtype) for _ in range(3))
+    k = {"block": _lib.QUANT_BLOCK, "pow2": _lib.QUANT_POW2, "mx": _lib.QUANT_MX}[kind]
+    ew = ExpertWeights(k).refresh(w1.to(dev), w2.to(dev), w3.to(dev), E)
+    f = lambda t: t.float().numpy().reshape(E, H, D)
+    W13 = np.concatenate([f(w1), f(w3)], axis=1).reshape(E * 2 * H, D)
+    for op, src in ((ew.w13, W13), (ew.w2, f(w2).reshape(E * H, D))):
+        data = op.data.reshape(-1, D).cpu().numpy()
+        if kind == "mx":
+            q, c = ofp8.quant_mx_1x32(src)
+            assert np.array_equal(data, q)
+            assert np.array_equal(op.scale.reshape(-1, D // 32).cpu().numpy(), c)
+        else:
+            n = src.shape[0]
+            q, s = ofp8.quant_128x128(src, pow2=kind == "pow2")
+            assert np.array_equal(data[:n], q)
+            assert np.array_equal(op.scale.reshape(-1, D // 128).cpu().numpy()[: n // 128], s)
