@@ -108,13 +108,15 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* g, const void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+__device__ __forceinline__ void dma4a(const void* g, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
-// Scalar-base form: wave-uniform 64-bit base `g` plus a 32-bit per-lane offset.
-__device__ __forceinline__ void dma16s(const uint8_t* g, uint32_t voff, const void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+__device__ __forceinline__ void dma4(const void* g, const void* lds) { dma4a(g, lds_addr(lds)); }
+// Scalar-base form: wave-uniform 64-bit base `g` plus a 32-bit per-lane offset,
+// into LDS byte address `lds` (wave-uniform).
+__device__ __forceinline__ void dma16s(const uint8_t* g, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(g), "s"(m)
                : "memory", "m0");
 }
@@ -149,28 +151,29 @@ struct Smem256 {
 };
 
 // One 256-row operand tile streams as 32 groups of 8 rows x 128 bytes per K
-// step, 8 groups per wave.  LDS chunk c = 64*group + lane holds row c/8 at
-// swizzled position c%8, so a lane's global offset inside a group depends only
-// on the group's parity.  Groups past the last valid row of the operand re-read
-// the last valid group (their rows produce outputs that are never stored).
+// step, 4 consecutive groups per wave.  LDS chunk c = 64*group + lane holds row
+// c/8 at swizzled position c%8, so a lane's global offset inside a group
+// depends only on the group's parity.  The valid rows of a tile are a multiple
+// of 128, so a wave's 32 rows are all valid or all past the end; a wave past
+// the end re-reads the last valid 32 rows into its own LDS rows, which only
+// feed outputs that are never stored.
 struct OpStream {
-  const uint8_t* base;    // tile row 0 at K offset 0 (wave-uniform)
+  const uint8_t* base;    // this wave's first row group at K offset 0 (wave-uniform)
   int64_t group_bytes;    // 8 rows
   uint32_t lane_off[2];   // even / odd group
-  int g_last;
 };
 
-__device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows,
-                                                int lane) {
+__device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows, int lane,
+                                                int wave) {
   OpStream s;
-  s.base = base;
   s.group_bytes = 8 * row_bytes;
+  const int last = int(rows / 32) - 1;
+  s.base = base + int64_t(wave < last ? wave : last) * 4 * s.group_bytes;
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     const int ch = (lane & 7) ^ ((par * 4 + (lane >> 4)) & 7);  // == chunk ^ lds_swz(row)
     s.lane_off[par] = uint32_t((lane >> 3) * row_bytes + ch * 16);
   }
-  s.g_last = int(rows / 8) - 1;
   return s;
 }
 
@@ -196,13 +199,15 @@ __device__ __forceinline__ v8bf read_frag16(const uint8_t* base, int r, int ks, 
 __device__ __forceinline__ int scale_row_slot(int li) {   // LDS slot li holds tile row:
   return (li >> 7) * 128 + (li & 3) * 32 + ((li & 127) >> 2);
 }
-template <int KIND>
-__device__ __forceinline__ void read_pow2_scales(const uint8_t* st, int off, int w128, int lrow, int (&s)[4]) {
+// pow2 scales reach the MFMA packed: the e8m0 exponents of a lane's four row
+// blocks are the four bytes of one register (positive power-of-two floats: the
+// exponent is bits 23-30), and each MFMA selects its byte with op_sel.
+__device__ __forceinline__ int pack_exp4(uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
+  return int((x >> 23) | ((y >> 23) << 8) | ((z >> 23) << 16) | ((w >> 23) << 24));
+}
+__device__ __forceinline__ int read_pow2_scales(const uint8_t* st, int off, int w128, int lrow) {
   const uint4 v = *reinterpret_cast<const uint4*>(st + off + (w128 + lrow * 4) * 4);
-  s[0] = int((v.x >> 23) & 0xffu);
-  s[1] = int((v.y >> 23) & 0xffu);
-  s[2] = int((v.z >> 23) & 0xffu);
-  s[3] = int((v.w >> 23) & 0xffu);
+  return pack_exp4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ int read_mx_scale(const uint8_t* st, int off, int r, int blk, bool mx_k) {
   return mx_k ? st[off + blk * kT + r] : st[off + r * 4 + blk];
@@ -216,7 +221,9 @@ __device__ __forceinline__ int read_mx_scale(const uint8_t* st, int off, int r, 
 template <int KIND>
 struct Frag {
   v8i a[4], b[2];
-  int sa[4], sb[2];
+  // e8m0 scales of the 4 (a) and 2 (b) row blocks: one register each for MX,
+  // packed one byte each into sa[0] / sb[0] for pow2
+  int sa[KIND == GK_FP8_MX ? 4 : 1], sb[KIND == GK_FP8_MX ? 2 : 1];
 };
 template <>
 struct Frag<GK_BF16> {
@@ -232,20 +239,17 @@ struct WaveCoord {
 // scale dword per lane (waves 0-3: Q scale slots, 4-7: P scale slots).
 template <int KIND>
 __device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const uint8_t* sc,
-                                       int64_t sc_k, int sc_dst, int64_t k, uint8_t* dst, int wave) {
+                                       int64_t sc_k, int sc_dst, int64_t k, uint32_t dst, int wave) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   const int64_t kb = k * ES;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int g = wave * 4 + u;
-    const int gq = g < qst.g_last ? g : qst.g_last;
-    dma16s(qst.base + gq * qst.group_bytes + kb, qst.lane_off[u & 1], dst + g * 1024);
-    const int gp = g < pst.g_last ? g : pst.g_last;
-    dma16s(pst.base + gp * pst.group_bytes + kb, pst.lane_off[u & 1], dst + SM::kP + g * 1024);
+    dma16s(qst.base + (u * qst.group_bytes + kb), qst.lane_off[u & 1], dst + (wave * 4 + u) * 1024);
+    dma16s(pst.base + (u * pst.group_bytes + kb), pst.lane_off[u & 1], dst + SM::kP + (wave * 4 + u) * 1024);
   }
-  if constexpr (KIND != GK_BF16) dma4(sc + (k / KSTEP) * sc_k, dst + sc_dst);
+  if constexpr (KIND != GK_BF16) dma4a(sc + (k / KSTEP) * sc_k, dst + sc_dst);
 }
 
 // Reads half `half` of the K step in stage `st` (pow2 scales only for half 0:
@@ -270,12 +274,11 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
         if (t < 2) f.sb[t] = read_mx_scale(st, SM::kPS, w.wj * 64 + t * 32 + w.lrow, blk, w.p_mx_k);
       }
     } else if (half == 0) {
-      read_pow2_scales<KIND>(st, SM::kQS, w.wi * 128, w.lrow, f.sa);
+      f.sa[0] = read_pow2_scales(st, SM::kQS, w.wi * 128, w.lrow);
       // P rows 64*wj + 32*t + l sit in 128-row block wj/2 at slot t' = 2*(wj&1) + t
       const uint2 v = *reinterpret_cast<const uint2*>(
           st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
-      f.sb[0] = int((v.x >> 23) & 0xffu);
-      f.sb[1] = int((v.y >> 23) & 0xffu);
+      f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -283,6 +286,12 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
       if (t < 2) f.b[t] = read_frag8(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, half, w.lhalf);
     }
   }
+}
+
+template <int A, int B, int KIND>
+__device__ __forceinline__ void mma_scaled(const Frag<KIND>& f, v16f (&acc)[4][2]) {
+  acc[A][B] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[A], f.b[B], acc[A][B], 0, 0, A, f.sa[0], B,
+                                                             f.sb[0]);
 }
 
 template <int KIND>
@@ -295,13 +304,22 @@ __device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][2])
 #pragma unroll
         for (int b = 0; b < 2; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s2][a], f.b[s2][b], acc[a][b], 0, 0, 0);
-  } else {
+  } else if constexpr (KIND == GK_FP8_MX) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 2; ++b)
         acc[a][b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[a], f.b[b], acc[a][b], 0, 0, 0,
                                                                    f.sa[a], 0, f.sb[b]);
+  } else {
+    mma_scaled<0, 0>(f, acc);
+    mma_scaled<0, 1>(f, acc);
+    mma_scaled<1, 0>(f, acc);
+    mma_scaled<1, 1>(f, acc);
+    mma_scaled<2, 0>(f, acc);
+    mma_scaled<2, 1>(f, acc);
+    mma_scaled<3, 0>(f, acc);
+    mma_scaled<3, 1>(f, acc);
   }
 }
 
@@ -316,7 +334,10 @@ __device__ __forceinline__ void interleave_half() {
   }
 }
 
-template <int KIND, int MODE>
+// MXL (MX only): scale layouts, bit 0 = Q scales k-major, bit 1 = P scales
+// k-major (row-major otherwise); fixed per instantiation so the unused
+// address path costs no registers.
+template <int KIND, int MODE, int MXL = 0>
 __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
@@ -389,15 +410,16 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   w.wj = w.wave & 3;
   w.lrow = w.lane & 31;
   w.lhalf = w.lane >> 5;
-  w.q_mx_k = KIND == GK_FP8_MX && p.Q.s_kb != 1;
-  w.p_mx_k = KIND == GK_FP8_MX && p.P.s_kb != 1;
+  w.q_mx_k = KIND == GK_FP8_MX && (MXL & 1) != 0;
+  w.p_mx_k = KIND == GK_FP8_MX && (MXL & 2) != 0;
   const int64_t q_group = MODE == GM_RAGGED_M ? e : 0;
   // valid rows of each operand tile (multiples of 128)
   const int64_t q_rows = p.n_i - i0 < kT ? p.n_i - i0 : kT;
   const int64_t p_rows = j_end - j0 < kT ? j_end - j0 : kT;
 
-  const OpStream qst = make_stream(p.Q.p + (q_group * p.Q.gs + i0 * p.Q.ld) * ES, p.Q.ld * ES, q_rows, w.lane);
-  const OpStream pst = make_stream(p.P.p + j0 * p.P.ld * ES, p.P.ld * ES, p_rows, w.lane);
+  const OpStream qst = make_stream(p.Q.p + (q_group * p.Q.gs + i0 * p.Q.ld) * ES, p.Q.ld * ES, q_rows, w.lane,
+                                   w.wave);
+  const OpStream pst = make_stream(p.P.p + j0 * p.P.ld * ES, p.P.ld * ES, p_rows, w.lane, w.wave);
 
   // Scales: waves 0-3 fetch the Q scale slots, waves 4-7 the P slots, one
   // dword per lane per K step.  fp32 / pow2 and row-major MX: one row per slot
@@ -437,38 +459,47 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  // Two-stage pipeline, K step t in stage t % 2.  Each step: wait for this
-  // wave's DMA of step t, barrier (step t has landed for every wave and every
-  // wave is done with stage (t+1) % 2), refill that stage with step t+1, then
-  // the two halves of step t, the second half's reads under the first half's
-  // MFMAs.  The refill is unconditional (clamped to the last step), which
-  // keeps the loop body one basic block.
+  // Two-stage pipeline, K step t in stage t % 2, fragments read one half-step
+  // ahead into two register sets.  Iteration t (f0 holds half 0 of step t):
+  //   A: MFMAs of (t, 0) while reading (t, 1) into f1;
+  //   wait for this wave's DMA of step t+1 and its LDS reads, barrier (step
+  //      t+1 has landed for every wave; no wave still reads stage t % 2);
+  //   refill stage t % 2 with step t+2;
+  //   B: MFMAs of (t, 1) while reading (t+1, 0) into f0.
+  // No LDS read waits behind a barrier with the matrix pipe idle.  The refills
+  // are unconditional (clamped to the last step), which keeps the loop body
+  // one basic block; the reads after the last step re-read a valid stage.
   const int64_t nk = (k_hi - k_lo) / KSTEP;
   if (nk > 0) {
+    const uint32_t smem_lds = lds_addr(smem);
     Frag<KIND> f0, f1;
-    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo, smem, w.wave);
+    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo, smem_lds, w.wave);
+    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + (nk > 1 ? KSTEP : 0), smem_lds + SM::kStage, w.wave);
+    // step 0 has landed once at most step 1's DMAs are still in flight
+    FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
+    block_barrier();
+    read_half<KIND>(smem, 0, f0, w);
     int cur_off = 0;
 #pragma unroll 1
     for (int64_t t = 0; t < nk; ++t) {
       const int nxt_off = SM::kStage - cur_off;
-      FM_WAIT_VMCNT(0);
-      block_barrier();
-      const int64_t tn = t + 1 < nk ? t + 1 : nk - 1;
-      issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + tn * KSTEP, smem + nxt_off, w.wave);
-      read_half<KIND>(smem + cur_off, 0, f0, w);
       __builtin_amdgcn_sched_barrier(0);
-      read_half<KIND>(smem + cur_off, 1, f1, w);   // under the first half's MFMAs
+      read_half<KIND>(smem + cur_off, 1, f1, w);
       if constexpr (KIND == GK_FP8_POW2) {
-#pragma unroll
-        for (int t2 = 0; t2 < 4; ++t2) {
-          f1.sa[t2] = f0.sa[t2];
-          if (t2 < 2) f1.sb[t2] = f0.sb[t2];
-        }
+        f1.sa[0] = f0.sa[0];
+        f1.sb[0] = f0.sb[0];
       }
       mma_half<KIND>(f0, acc);
       interleave_half<KIND>();
       __builtin_amdgcn_sched_barrier(0);
+      FM_WAIT_VMCNT(0);
+      block_barrier();
+      const int64_t t2n = t + 2 < nk ? t + 2 : nk - 1;
+      issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + t2n * KSTEP, smem_lds + cur_off, w.wave);
+      __builtin_amdgcn_sched_barrier(0);
+      read_half<KIND>(smem + nxt_off, 0, f0, w);
       mma_half<KIND>(f1, acc);
+      interleave_half<KIND>();
       __builtin_amdgcn_sched_barrier(0);
       cur_off = nxt_off;
     }
@@ -821,7 +852,16 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
     case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block8, 0, s, p); break;
     case GK_FP8_F32: hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p); break;
     case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block8, 0, s, p); break;
-    case GK_FP8_MX: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE>), grid, block8, 0, s, p); break;
+    case GK_FP8_MX: {
+      const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
+      switch (mxl) {
+        case 0: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 0>), grid, block8, 0, s, p); break;
+        case 1: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 1>), grid, block8, 0, s, p); break;
+        case 2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 2>), grid, block8, 0, s, p); break;
+        default: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 3>), grid, block8, 0, s, p); break;
+      }
+      break;
+    }
     default: set_error("grouped gemm: unknown kind %d", kind); return 1;
   }
   return check_launch("grouped gemm");
