@@ -86,8 +86,12 @@ class GemmTimer:
 def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, backward=True,
                gemm_timer=True, pre_step=None):
     """Times `steps` calls of the expert block (forward, + backward when
-    `backward`), weight cache dropped every step.  Returns (ms per step, GEMM
-    event summary or None)."""
+    `backward`), weight cache dropped every step, with nothing recorded between
+    the launches.  With `gemm_timer`, a second pass of `steps` identical steps
+    then records HIP events around every grouped-GEMM launch (each event
+    record leaves a few-microsecond bubble in the stream, so this pass is not
+    the one the step time comes from).  Returns (ms per step, GEMM event
+    summary or None)."""
     import torch
 
     import nanopysche_amd as fm
@@ -118,15 +122,23 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    timer = GemmTimer() if gemm_timer else None
-    fmm.GEMM_TIMER = timer
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    fmm.GEMM_TIMER = None
-    return elapsed * 1e3 / steps, (None if timer is None else timer.summary())
+    summary = None
+    if gemm_timer:
+        timer = GemmTimer()
+        fmm.GEMM_TIMER = timer
+        try:
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+        finally:
+            fmm.GEMM_TIMER = None
+        summary = timer.summary()
+    return elapsed * 1e3 / steps, summary
 
 
 def gemm_report(summ, steps, flops_scale=1.0):

@@ -4,7 +4,8 @@
 //                          softmax for the load-balancing loss
 //   fm_aux_loss         -- E * sum_i f_i P_i from the counts and those sums
 //   fm_route_sort       -- stable counting sort of the T*K (token, slot)
-//                          assignments by expert: LDS histograms, one-block scan,
+//                          assignments by expert: ballot-counted histograms per
+//                          1024 assignments, per-expert wave scans,
 //                          wave-ballot ranks; padded group offsets (multiples of
 //                          128), row maps, and the m-tile -> expert table
 //   fm_permute          -- gather x rows into the padded expert-contiguous
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void aux_loss_kernel(const float* prob_partial
 }
 
 // ----------------------------------------------------------------- sort ----
-constexpr int kSortBlock = 4096;     // assignments per workgroup
+constexpr int kSortBlock = 1024;     // assignments per workgroup (256 per wave)
 constexpr int kSortMaxExperts = 1024;
 
 template <typename I>
@@ -149,27 +150,56 @@ __device__ __forceinline__ int load_expert(const I* idx, int64_t a, int E) {
   return (e >= 0 && e < E) ? int(e) : -1;
 }
 
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Lanes of the wave holding the same expert as this lane (one ballot per
+// expert-id bit); e < 0 marks lanes with no assignment.
+__device__ __forceinline__ uint64_t expert_peers(int e, int nbits) {
+  uint64_t peers = __ballot(e >= 0);
+#pragma unroll 1
+  for (int b = 0; b < nbits; ++b) {
+    const uint64_t ones = __ballot(e >= 0 && ((e >> b) & 1));
+    peers &= ((e >> b) & 1) ? ones : ~ones;
+  }
+  return e >= 0 ? peers : 0ull;
+}
+
+__device__ __forceinline__ int expert_bits(int E) {
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  return nbits;
+}
+
+// block_hist[e][b] = assignments of block b routed to expert e.  Each wave
+// counts 64 assignments at a time; the lowest lane of every group of equal
+// experts adds the group's size (one LDS atomic per distinct expert).
 template <typename I>
 __global__ __launch_bounds__(256) void sort_hist_kernel(const I* idx, int64_t A, int E,
-                                                        int32_t* block_hist) {
+                                                        int32_t* block_hist, int64_t n_blocks) {
   __shared__ int32_t hist[kSortMaxExperts];
   for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
   __syncthreads();
-  const int64_t base = int64_t(blockIdx.x) * kSortBlock;
-  for (int i = threadIdx.x; i < kSortBlock; i += 256) {
-    const int64_t a = base + i;
-    if (a < A) {
-      const int e = load_expert(idx, a, E);
-      if (e >= 0) atomicAdd(&hist[e], 1);
-    }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nbits = expert_bits(E);
+  const int64_t q0 = int64_t(blockIdx.x) * kSortBlock + int64_t(wave) * (kSortBlock / 4);
+  for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
+    const int64_t a = q0 + i0 + lane;
+    const int e = a < A ? load_expert(idx, a, E) : -1;
+    const uint64_t peers = expert_peers(e, nbits);
+    if (e >= 0 && (peers & lanemask_lt()) == 0) atomicAdd(&hist[e], __popcll(peers));
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 256) block_hist[int64_t(blockIdx.x) * E + e] = hist[e];
+  for (int e = threadIdx.x; e < E; e += 256) block_hist[int64_t(e) * n_blocks + blockIdx.x] = hist[e];
 }
 
-// One block of 1024 threads.  block_hist[b][e] becomes the exclusive prefix
-// over blocks; counts, padded offsets, the m-tile -> expert map and the
-// per-expert FP8/BF16 flag are written; assign_of_row is reset to -1.
+// One block of 1024 threads (16 waves).  Wave w scans experts w, w + 16, ...:
+// block_hist[e][*] becomes its exclusive prefix over blocks (64 blocks per
+// pass, wave prefix sums).  Then counts, padded offsets, the m-tile -> expert
+// map and the per-expert FP8/BF16 flag are written; assign_of_row is reset to
+// -1.
 __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* block_hist, int64_t n_blocks,
                                                          int E, int32_t* counts, int32_t* offsets,
                                                          int32_t* tile_expert, int64_t n_tiles_max,
@@ -177,17 +207,27 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* block_hist, in
                                                          int32_t* use_fp8, int64_t threshold) {
   __shared__ int32_t padded[kSortMaxExperts];
   __shared__ int32_t scan[kSortMaxExperts + 1];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 1024) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = wave; e < E; e += 16) {
+    int32_t* h = block_hist + int64_t(e) * n_blocks;
     int32_t run = 0;
-    for (int64_t b = 0; b < n_blocks; ++b) {
-      const int32_t h = block_hist[b * E + e];
-      block_hist[b * E + e] = run;
-      run += h;
+    for (int64_t b0 = 0; b0 < n_blocks; b0 += 64) {
+      const int64_t b = b0 + lane;
+      const int32_t v = b < n_blocks ? h[b] : 0;
+      int32_t incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int32_t o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+      }
+      if (b < n_blocks) h[b] = run + incl - v;
+      run += __shfl(incl, 63);
     }
-    counts[e] = run;
-    padded[e] = (run + 127) / 128 * 128;
-    if (use_fp8) use_fp8[e] = int64_t(run) >= threshold ? 1 : 0;
+    if (lane == 0) {
+      counts[e] = run;
+      padded[e] = (run + 127) / 128 * 128;
+      if (use_fp8) use_fp8[e] = int64_t(run) >= threshold ? 1 : 0;
+    }
   }
   __syncthreads();
   if (tid == 0) {
@@ -215,36 +255,31 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* block_hist, in
   for (int64_t r = tid; r < rows_max; r += 1024) assign_of_row[r] = -1;
 }
 
-__device__ __forceinline__ uint64_t lanemask_lt() {
-  const int lane = threadIdx.x & 63;
-  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
-}
-
-// Each wave owns a contiguous quarter (1024 assignments) of the block and
+// Each wave owns a contiguous quarter (256 assignments) of the block and
 // walks it 64 at a time; peers with the same expert are found with one ballot
 // per expert-id bit, so ranks follow assignment order (stable).
 template <typename I>
 __global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t A, int E,
-                                                           const int32_t* block_prefix,
+                                                           const int32_t* block_prefix, int64_t n_blocks,
                                                            const int32_t* offsets,
                                                            int32_t* row_of,
                                                            int32_t* assign_of_row) {
   __shared__ int32_t base[4][kSortMaxExperts];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nbits = expert_bits(E);
   for (int i = threadIdx.x; i < 4 * E; i += 256) base[i / E][i % E] = 0;
   __syncthreads();
   const int64_t q0 = int64_t(blockIdx.x) * kSortBlock + int64_t(wave) * (kSortBlock / 4);
-  for (int i = lane; i < kSortBlock / 4; i += 64) {
-    const int64_t a = q0 + i;
-    if (a < A) {
-      const int e = load_expert(idx, a, E);
-      if (e >= 0) atomicAdd(&base[wave][e], 1);
-    }
+  for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
+    const int64_t a = q0 + i0 + lane;
+    const int e = a < A ? load_expert(idx, a, E) : -1;
+    const uint64_t peers = expert_peers(e, nbits);
+    if (e >= 0 && (peers & lanemask_lt()) == 0) atomicAdd(&base[wave][e], __popcll(peers));
   }
   __syncthreads();
   // exclusive prefix over the 4 waves, plus the block prefix and group offset
   for (int e = threadIdx.x; e < E; e += 256) {
-    int32_t run = offsets[e] + block_prefix[int64_t(blockIdx.x) * E + e];
+    int32_t run = offsets[e] + block_prefix[int64_t(e) * n_blocks + blockIdx.x];
     for (int w = 0; w < 4; ++w) {
       const int32_t c = base[w][e];
       base[w][e] = run;
@@ -252,17 +287,10 @@ __global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t
     }
   }
   __syncthreads();
-  int nbits = 1;
-  while ((1 << nbits) < E) ++nbits;
   for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
     const int64_t a = q0 + i0 + lane;
     const int e = a < A ? load_expert(idx, a, E) : -1;
-    uint64_t peers = __ballot(e >= 0);
-#pragma unroll 1
-    for (int b = 0; b < nbits; ++b) {
-      const uint64_t ones = __ballot(e >= 0 && ((e >> b) & 1));
-      peers &= ((e >> b) & 1) ? ones : ~ones;
-    }
+    const uint64_t peers = expert_peers(e, nbits);
     int32_t my_base = 0;
     if (e >= 0) my_base = base[wave][e];
     __builtin_amdgcn_wave_barrier();
@@ -443,10 +471,10 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
   if (nb > 0) {
     if (indices_i64)
       hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int64_t*>(indices), A, E, bh);
+                         static_cast<const int64_t*>(indices), A, E, bh, nb);
     else
       hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int32_t*>(indices), A, E, bh);
+                         static_cast<const int32_t*>(indices), A, E, bh, nb);
     if (int rc = check_launch("fm_route_sort/hist")) return rc;
   }
   hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
@@ -455,11 +483,11 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
   if (nb > 0) {
     if (indices_i64)
       hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int64_t*>(indices), A, E, bh, offsets, row_of,
+                         static_cast<const int64_t*>(indices), A, E, bh, nb, offsets, row_of,
                          assign_of_row);
     else
       hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int32_t*>(indices), A, E, bh, offsets, row_of,
+                         static_cast<const int32_t*>(indices), A, E, bh, nb, offsets, row_of,
                          assign_of_row);
     if (int rc = check_launch("fm_route_sort/scatter")) return rc;
   }
