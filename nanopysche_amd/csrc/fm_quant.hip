@@ -15,31 +15,41 @@ namespace fm {
 
 // ------------------------------------------------------------------ sources ----
 template <typename T>
-struct DenseSrc {
+struct DenseSrc;
+
+template <>
+struct DenseSrc<uint16_t> {
   static constexpr int kOut = 1;
-  const T* p;
+  const uint16_t* p;
   int64_t ld;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const;
+  struct Raw {
+    uint4 pk;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
+    return Raw{*reinterpret_cast<const uint4*>(p + row * ld + col)};
+  }
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const { unpack8_bf16(r.pk, v[0]); }
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const { compute(fetch(row, col), v); }
 };
 
 template <>
-__device__ __forceinline__ void DenseSrc<uint16_t>::load8(int64_t row, int64_t col, float v[][8]) const {
-  const uint4 pk = *reinterpret_cast<const uint4*>(p + row * ld + col);
-  const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[0][2 * i] = u2f(w[i] << 16);
-    v[0][2 * i + 1] = u2f(w[i] & 0xffff0000u);
+struct DenseSrc<float> {
+  static constexpr int kOut = 1;
+  const float* p;
+  int64_t ld;
+  struct Raw {
+    float4 a, b;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
+    return Raw{*reinterpret_cast<const float4*>(p + row * ld + col),
+               *reinterpret_cast<const float4*>(p + row * ld + col + 4)};
   }
-}
-
-template <>
-__device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col, float v[][8]) const {
-  const float4 a = *reinterpret_cast<const float4*>(p + row * ld + col);
-  const float4 b = *reinterpret_cast<const float4*>(p + row * ld + col + 4);
-  v[0][0] = a.x; v[0][1] = a.y; v[0][2] = a.z; v[0][3] = a.w;
-  v[0][4] = b.x; v[0][5] = b.y; v[0][6] = b.z; v[0][7] = b.w;
-}
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
+    v[0][0] = r.a.x; v[0][1] = r.a.y; v[0][2] = r.a.z; v[0][3] = r.a.w;
+    v[0][4] = r.b.x; v[0][5] = r.b.y; v[0][6] = r.b.z; v[0][7] = r.b.w;
+  }
+  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const { compute(fetch(row, col), v); }
+};
 
 // Two expert weight stacks a, b = [groups][rows][cols] read as one
 // [groups][2 rows][cols] matrix (group g: rows of a, then rows of b), the
@@ -47,14 +57,16 @@ __device__ __forceinline__ void DenseSrc<float>::load8(int64_t row, int64_t col,
 template <typename T>
 struct PairSrc {
   static constexpr int kOut = 1;
+  using Raw = typename DenseSrc<T>::Raw;
   const T* a;
   const T* b;
   int64_t rows, ld;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
     const int64_t g = row / (2 * rows), r = row % (2 * rows);
     const T* base = r < rows ? a : b;
-    DenseSrc<T>{base + (g * rows + (r < rows ? r : r - rows)) * ld, 0}.load8(0, col, v);
+    return DenseSrc<T>{base + (g * rows + (r < rows ? r : r - rows)) * ld, 0}.fetch(0, col);
   }
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const { DenseSrc<T>{}.compute(r, v); }
 };
 
 // ------------------------------------------------------- 128x128 weight blocks ----

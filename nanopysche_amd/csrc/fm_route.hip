@@ -309,33 +309,47 @@ __global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t
 
 // -------------------------------------------------------------- permute ----
 // Row r of the padded buffer is x[assign_of_row[r] / K] (times the router
-// weight of that assignment when `w` is set), zeros for pad rows.
+// weight of that assignment when WEIGHTED), zeros for pad rows.  Branch-free:
+// a pad row reads assignment 0 and is zeroed by a select (the launcher uses
+// ZeroSrc when there are no assignments).
+template <bool WEIGHTED>
 struct GatherSrc {
   static constexpr int kOut = 1;
   const uint16_t* x;  // bf16 [T, D]
   int64_t ld;
   const int32_t* assign_of_row;
   int K;
-  const float* w;     // [T*K] or null
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
+  const float* w;     // [T*K] (WEIGHTED)
+  struct Raw {
+    uint4 pk;
+    float s;
+    bool ok;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
     const int32_t a = assign_of_row[row];
-    if (a < 0) {
+    const int32_t ac = a >= 0 ? a : 0;
+    Raw r;
+    r.ok = a >= 0;
+    r.pk = *reinterpret_cast<const uint4*>(x + int64_t(ac / K) * ld + col);
+    r.s = WEIGHTED ? w[ac] : 1.f;
+    return r;
+  }
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
+    float f[8];
+    unpack8_bf16(r.pk, f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[0][i] = 0.f;
-      return;
-    }
-    const uint4 pk = *reinterpret_cast<const uint4*>(x + int64_t(a / K) * ld + col);
-    const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+    for (int i = 0; i < 8; ++i) v[0][i] = r.ok ? (WEIGHTED ? r.s * f[i] : f[i]) : 0.f;
+  }
+};
+
+// All pad rows (no assignments at all).
+struct ZeroSrc {
+  static constexpr int kOut = 1;
+  struct Raw {};
+  __device__ __forceinline__ Raw fetch(int64_t, int64_t) const { return Raw{}; }
+  __device__ __forceinline__ void compute(const Raw&, float v[][8]) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[0][2 * i] = u2f(q[i] << 16);
-      v[0][2 * i + 1] = u2f(q[i] & 0xffff0000u);
-    }
-    if (w) {
-      const float s = w[a];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[0][i] = s * v[0][i];
-    }
+    for (int i = 0; i < 8; ++i) v[0][i] = 0.f;
   }
 };
 
@@ -503,8 +517,13 @@ int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t*
   FM_REQUIRE(ld_x >= D && ld_x % 8 == 0, "fm_permute: input pitch must be >= D and a multiple of 8");
   FM_REQUIRE(K >= 1, "fm_permute: K must be >= 1");
   const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, tile_valid);
-  GatherSrc src{static_cast<const uint16_t*>(x), ld_x, assign_of_row, K, weights};
-  return launch_tile_producer(src, o, rows, D, static_cast<hipStream_t>(stream), "fm_permute");
+  const hipStream_t sm = static_cast<hipStream_t>(stream);
+  if (T == 0) return launch_tile_producer(ZeroSrc{}, o, rows, D, sm, "fm_permute");
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  if (weights) return launch_tile_producer(GatherSrc<true>{xs, ld_x, assign_of_row, K, weights}, o, rows, D, sm,
+                                           "fm_permute");
+  return launch_tile_producer(GatherSrc<false>{xs, ld_x, assign_of_row, K, nullptr}, o, rows, D, sm,
+                              "fm_permute");
 }
 
 int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,

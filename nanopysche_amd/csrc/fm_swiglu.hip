@@ -13,16 +13,6 @@
 
 namespace fm {
 
-__device__ __forceinline__ void load8_bf16(const uint16_t* p, float v[8]) {
-  const uint4 pk = *reinterpret_cast<const uint4*>(p);
-  const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = u2f(q[i] << 16);
-    v[2 * i + 1] = u2f(q[i] & 0xffff0000u);
-  }
-}
-
 __device__ __forceinline__ float sigmoidf(float g) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
 }
@@ -32,10 +22,17 @@ struct SwigluSrc {
   const uint16_t* g;  // [M, H] pitch ld_g
   const uint16_t* u;  // [M, H] pitch ld_u
   int64_t ld_g, ld_u;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
+  struct Raw {
+    uint4 g, u;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
+    return Raw{*reinterpret_cast<const uint4*>(g + row * ld_g + col),
+               *reinterpret_cast<const uint4*>(u + row * ld_u + col)};
+  }
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
     float gv[8], uv[8];
-    load8_bf16(g + row * ld_g + col, gv);
-    load8_bf16(u + row * ld_u + col, uv);
+    unpack8_bf16(r.g, gv);
+    unpack8_bf16(r.u, uv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[0][i] = (gv[i] * sigmoidf(gv[i])) * uv[i];
   }
@@ -49,11 +46,19 @@ struct SwigluBwdSrc {
   const uint16_t* u;
   const uint16_t* dh;
   int64_t ld_g, ld_u, ld_dh;
-  __device__ __forceinline__ void load8(int64_t row, int64_t col, float v[][8]) const {
+  struct Raw {
+    uint4 g, u, dh;
+  };
+  __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
+    return Raw{*reinterpret_cast<const uint4*>(g + row * ld_g + col),
+               *reinterpret_cast<const uint4*>(u + row * ld_u + col),
+               *reinterpret_cast<const uint4*>(dh + row * ld_dh + col)};
+  }
+  __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
     float gv[8], uv[8], dv[8];
-    load8_bf16(g + row * ld_g + col, gv);
-    load8_bf16(u + row * ld_u + col, uv);
-    load8_bf16(dh + row * ld_dh + col, dv);
+    unpack8_bf16(r.g, gv);
+    unpack8_bf16(r.u, uv);
+    unpack8_bf16(r.dh, dv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float s = sigmoidf(gv[i]);

@@ -9,10 +9,11 @@
 // one 128-byte row segment), 16-byte transposed stores.
 //
 // LDS staging for the transposed output:
-//   QK_POW2  -- e4m3 codes [128][128 + 4 pad] + one row scale per row (17 KiB):
-//               the transposed output is the scaling-aware transpose of the
-//               row output, so the codes are all it needs.
-//   others   -- fp32 values [128][129] (66 KiB).
+//   QK_POW2  -- per output, e4m3 codes [128][128 + 4 pad] + one row scale per
+//               row (17 KiB): the transposed output is the scaling-aware
+//               transpose of the row output, so the codes are all it needs
+//               (pow2_tile).
+//   others   -- fp32 values [128][129] (66 KiB), one output at a time.
 #pragma once
 
 #include "fm_common.h"
@@ -83,6 +84,16 @@ __device__ __forceinline__ float group_max4(float v) {
   return v;
 }
 
+// 8 bf16 (one 16-byte load) -> 8 floats
+__device__ __forceinline__ void unpack8_bf16(const uint4& pk, float v[8]) {
+  const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = u2f(q[i] << 16);
+    v[2 * i + 1] = u2f(q[i] & 0xffff0000u);
+  }
+}
+
 __device__ __forceinline__ uint64_t pack8_e4m3(const uint8_t* b) {
   uint64_t r = 0;
 #pragma unroll
@@ -92,9 +103,119 @@ __device__ __forceinline__ uint64_t pack8_e4m3(const uint8_t* b) {
 
 // Source functor contract:
 //   static constexpr int kOut;                       // values per element (1 or 2)
-//   __device__ void load8(int64_t row, int64_t col, float v[kOut][8]) const;
-// loads columns [col, col+8) of logical row `row` (zeros for rows the source
-// treats as padding).
+//   struct Raw;                                      // what the loads of one row return
+//   __device__ Raw fetch(int64_t row, int64_t col) const;
+//   __device__ void compute(const Raw& r, float v[kOut][8]) const;
+// fetch issues the (branch-free) loads of columns [col, col+8) of logical row
+// `row`; compute turns them into values (zeros for rows the source treats as
+// padding).  The kernel fetches all of a thread's rows before computing any,
+// so their loads overlap, and converts one row at a time.
+// Power-of-two recipe: both outputs of a two-output source are quantised as
+// soon as a row is computed (the transposed output is the scaling-aware
+// transpose of the row output, so e4m3 codes + row scales in LDS are all it
+// needs, 17 KiB per output); no row values stay in registers.
+template <class Src, bool HW>
+__device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
+                                          int64_t col0, int cpos, bool want_row, bool want_col) {
+  constexpr int NOUT = Src::kOut;
+  const int tid = threadIdx.x;
+  __shared__ float p_red[NOUT];
+  __shared__ float p_rscale[NOUT][128];
+  __shared__ __attribute__((aligned(16))) uint32_t p_code[NOUT][128 * 33];
+  typename Src::Raw raw[8];
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int64_t grow = row0 + (tid >> 4) + 16 * it;
+    raw[it] = src.fetch(grow < rows ? grow : rows - 1, col0 + cpos);
+  }
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    float v[NOUT][8];
+    src.compute(raw[it], v);
+    const int r = (tid >> 4) + 16 * it;
+    const int64_t grow = row0 + r;
+    const bool ok = grow < rows;
+#pragma unroll
+    for (int oi = 0; oi < NOUT; ++oi) {
+      float am = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[oi][i] = ok ? v[oi][i] : 0.f;
+        am = fmaxf(am, fabsf(v[oi][i]));
+      }
+      const float sc = block_scale(group_max16(am), true);
+      const float inv = 1.0f / sc;  // exact: sc is a power of two
+      const uint32_t w0 = enc_e4m3x4<HW>(v[oi][0] * inv, v[oi][1] * inv, v[oi][2] * inv, v[oi][3] * inv);
+      const uint32_t w1 = enc_e4m3x4<HW>(v[oi][4] * inv, v[oi][5] * inv, v[oi][6] * inv, v[oi][7] * inv);
+      const int64_t ocol = col0 + o.col_off[oi];
+      if (want_row && ok) {
+        *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
+            make_uint2(w0, w1);
+        if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.rs_row + (ocol >> 7) * o.rs_kb] = sc;
+      }
+      if (want_col) {
+        p_code[oi][r * 33 + (cpos >> 2)] = w0;
+        p_code[oi][r * 33 + (cpos >> 2) + 1] = w1;
+        if ((tid & 15) == 0) p_rscale[oi][r] = sc;
+      }
+    }
+  }
+  if (!want_col) return;
+  __syncthreads();
+  // column scale of each output: the largest row scale of the tile
+  if (tid < 64) {
+#pragma unroll
+    for (int oi = 0; oi < NOUT; ++oi) {
+      float m = fmaxf(p_rscale[oi][tid], p_rscale[oi][tid + 64]);
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      if (tid == 0) p_red[oi] = m;
+    }
+  }
+  __syncthreads();
+  // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
+  // the 8 lanes of one cg write a whole 128-byte row of the transpose.
+  // decode(q) * (s_row / s_col) is exact (powers of two) and <= 448.
+  uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
+  const int rg = tid & 7, cg = tid >> 3;
+#pragma unroll
+  for (int oi = 0; oi < NOUT; ++oi) {
+    const int64_t ocol = col0 + o.col_off[oi];
+    const float st = p_red[oi];
+    const float inv = 1.0f / st;  // exact: power of two
+    uint32_t w[4][4];   // [column][4-row word]
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float f[4][4];    // [row][column]
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int row = 16 * rg + 4 * k + b;
+        const float ratio = p_rscale[oi][row] * inv;
+        const uint32_t word = p_code[oi][row * 33 + cg];
+        float d[4];
+        if constexpr (HW) {
+          hw_dec_e4m3x4(word, d);
+        } else {
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
+        }
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = d[c4] * ratio;
+      }
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
+    }
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+      *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * o.ld_col + row0 + 16 * rg) =
+          make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+    if (rg == 0) {
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)
+        static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + ocol + 4 * cg + c4] = st;
+    }
+  }
+}
+
 template <class Src, int KIND>
 __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, int64_t rows) {
   constexpr int NOUT = Src::kOut;
@@ -106,28 +227,37 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
   const bool want_col = o.col_q != nullptr;
   const bool want_row = o.row_q != nullptr;
 
-  // ---- phase 1: thread -> rows (tid/16) + 16*it, columns [8*(tid%16), +8)
+  // ---- phase 1: thread -> rows (tid/16) + 16*it, columns [8*(tid%16), +8).
+  // All 8 rows are fetched before any is computed, so their loads are in
+  // flight together; rows past the end re-read the last row and are zeroed by
+  // a select.
   const int cpos = (tid & 15) * 8;
+  if constexpr (KIND == QK_POW2) {
+    pow2_tile<Src, HW>(src, o, rows, row0, col0, cpos, want_row, want_col);
+    return;
+  }
   float vv[8][NOUT][8];
+  {
+    typename Src::Raw raw[8];
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int64_t grow = row0 + (tid >> 4) + 16 * it;
-    if (grow < rows) {
-      src.load8(grow, col0 + cpos, vv[it]);
-    } else {
+    for (int it = 0; it < 8; ++it) {
+      const int64_t grow = row0 + (tid >> 4) + 16 * it;
+      raw[it] = src.fetch(grow < rows ? grow : rows - 1, col0 + cpos);
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      src.compute(raw[it], vv[it]);
+      const bool ok = row0 + (tid >> 4) + 16 * it < rows;
 #pragma unroll
       for (int q = 0; q < NOUT; ++q)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vv[it][q][i] = 0.f;
+        for (int i = 0; i < 8; ++i) vv[it][q][i] = ok ? vv[it][q][i] : 0.f;
     }
   }
 
-  // LDS for the transposed pass (one output at a time)
-  constexpr bool COMPACT = KIND == QK_POW2;
+  // LDS for the transposed pass (one output at a time): fp32 values
   __shared__ float red[256];
-  __shared__ float rscale[128];
-  __shared__ __attribute__((aligned(16))) uint32_t lds_code[COMPACT ? 128 * 33 : 1];
-  __shared__ float lds_val[COMPACT ? 1 : 128 * kTileLdsPitch];
+  __shared__ float lds_val[128 * kTileLdsPitch];
 
 #pragma unroll
   for (int oi = 0; oi < NOUT; ++oi) {
@@ -140,31 +270,18 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
       float am = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-      if (KIND == QK_BLOCK || KIND == QK_POW2) {
-        const float s = block_scale(group_max16(am), KIND == QK_POW2);
-        uint32_t w0, w1;
-        if (KIND == QK_POW2) {
-          const float inv = 1.0f / s;  // exact: s is a power of two
-          w0 = enc_e4m3x4<HW>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-          w1 = enc_e4m3x4<HW>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-        } else {
-          w0 = enc_e4m3x4<HW>(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
-          w1 = enc_e4m3x4<HW>(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
-        }
+      if (KIND == QK_BLOCK) {
+        const float s = block_scale(group_max16(am), false);
+        const uint32_t w0 = enc_e4m3x4<HW>(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
+        const uint32_t w1 = enc_e4m3x4<HW>(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
         if (want_row && grow < rows) {
           *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
               make_uint2(w0, w1);
           if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.rs_row + (ocol >> 7) * o.rs_kb] = s;
         }
         if (want_col) {
-          if (COMPACT) {
-            lds_code[r * 33 + (cpos >> 2)] = w0;
-            lds_code[r * 33 + (cpos >> 2) + 1] = w1;
-            if ((tid & 15) == 0) rscale[r] = s;
-          } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
-          }
+          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
         }
       } else if (KIND == QK_MX) {
         const uint32_t code = mx_code(group_max4(am));
@@ -200,52 +317,7 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
     const int c = tid & 127, h = tid >> 7;
     const int64_t gcol = ocol + c;
     uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
-    if (KIND == QK_POW2) {
-      // column scale: the largest row scale of the tile (uniform over its columns)
-      if (tid < 64) {
-        float m = fmaxf(rscale[tid], rscale[tid + 64]);
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        if (tid == 0) red[0] = m;
-      }
-      __syncthreads();
-      const float st = red[0];
-      const float inv = 1.0f / st;  // exact: power of two
-      // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
-      // the 8 lanes of one cg write a whole 128-byte row of the transpose.
-      // decode(q) * (s_row / s_col) is exact (powers of two) and <= 448.
-      const int rg = tid & 7, cg = tid >> 3;
-      uint32_t w[4][4];   // [column][4-row word]
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float f[4][4];    // [row][column]
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int row = 16 * rg + 4 * k + b;
-          const float ratio = rscale[row] * inv;
-          const uint32_t word = lds_code[row * 33 + cg];
-          float d[4];
-          if constexpr (HW) {
-            hw_dec_e4m3x4(word, d);
-          } else {
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
-          }
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = d[c4] * ratio;
-        }
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
-      }
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4)
-        *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * o.ld_col + row0 + 16 * rg) =
-            make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
-      if (rg == 0) {
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4)
-          static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + ocol + 4 * cg + c4] = st;
-      }
-    } else if (KIND == QK_BLOCK) {
+    if (KIND == QK_BLOCK) {
       float am = 0.f;
       for (int r = 0; r < 64; ++r) am = fmaxf(am, fabsf(lds_val[(64 * h + r) * kTileLdsPitch + c]));
       red[h * 128 + c] = am;
