@@ -84,7 +84,7 @@ class GemmTimer:
 
 
 def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, backward=True,
-               gemm_timer=True, pre_step=None):
+               gemm_timer=True, pre_step=None, overlap=True):
     """Times `steps` calls of the expert block (forward, + backward when
     `backward`), weight cache dropped every step, with nothing recorded between
     the launches.  With `gemm_timer`, a second pass of `steps` identical steps
@@ -101,6 +101,7 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     H = w1.shape[0] // E
     cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, fm.FP8RecipeType(recipe)))
     blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=threshold)
+    blk.overlap_streams = overlap
     params = [t.detach().clone().requires_grad_(backward) for t in (w1, w2, w3)]
     blk.set_weights(*params)
     xr = x.detach().clone().requires_grad_(backward)
@@ -216,7 +217,8 @@ def workload_c3(args, dev):
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    ms, summ = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup)
+    ms, summ = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup,
+                          overlap=not args.no_overlap)
     dom = max(summ, key=lambda k: summ[k]["ms"])
     d = summ[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
@@ -325,7 +327,8 @@ def workload_c4(args, dev):
         row = {"tokens_per_expert": t, "tokens": T,
                "max_tokens_per_expert": int(torch.bincount(idx.reshape(-1), minlength=E).max())}
         for name, recipe in (("bf16", "none"), ("fp8", "flow_moe")):
-            ms, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False)
+            ms, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False,
+                               overlap=not args.no_overlap)
             row[f"{name}_ms"] = round(ms, 3)
             row[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
         row["fp8_speedup"] = round(row["bf16_ms"] / row["fp8_ms"], 3)
@@ -382,7 +385,8 @@ def workload_c5(args, dev):
     x = device_normal((n_tok, D), 1.0, gen, dev, torch.bfloat16)
     go = device_normal((n_tok, D), 1e-2, gen, dev, torch.bfloat16)
     w1, w2, w3 = [device_normal((E_local * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
-    ms, summ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup)
+    ms, summ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup,
+                          overlap=not args.no_overlap)
     flops = 18.0 * A * D * H
     return {
         "metric": "MoE expert block fwd+bwd assignments/s on 1 MI355X (configs[4], MXFP8)",
@@ -407,6 +411,8 @@ def main():
     ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c4", "c5"])
     ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="keep every launch on one stream (no dW2 / dH overlap)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")

@@ -527,6 +527,21 @@ class ExpertWeights:
         self.w2t = ExpertWeightOperand(W2t, S2t, E * H, H, 1, D, (H // 32) * D, 0, D, H)
 
 
+# ================================================================= streams ====
+_SIDE = {}
+
+
+def _side_stream(dev) -> torch.cuda.Stream:
+    """One extra stream per device, at the default priority."""
+    idx = torch.device(dev).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    s = _SIDE.get(idx)
+    if s is None:
+        s = _SIDE[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
 # ================================================================ expert block ====
 @dataclass
 class FP8FlowMoEConfig:
@@ -588,6 +603,9 @@ class FP8FlowMoECompute:
         # ("gate_up") and backward the bf16 dH GEMM output ("dh"), [rows_max, *];
         # used by parity tests to feed a CPU oracle the device's own GEMM results.
         self.capture_intermediates = None
+        # Run the dW2 grouped GEMM on a second stream beside dH (False keeps
+        # every launch on the caller's stream).
+        self.overlap_streams = True
 
     def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
         for w in (w1, w2, w3):
@@ -702,13 +720,20 @@ class FP8FlowMoECompute:
         if not (w1dt == w3dt and w1dt in (torch.float32, torch.bfloat16) and w2dt in (torch.float32, torch.bfloat16)):
             raise TypeError("expert weights must be float32 or bfloat16 (w1 and w3 alike)")
         runs = [(k, w) for k, w in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)) if k is not None]
-        dy = {}
+        dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
+                                      return_transpose=True, weights=wts, kmajor_scales=True) for kind, _ in runs}
+        # dW2 (contraction over each expert's tokens) runs on a second stream
+        # beside dH: each alone leaves the last round of workgroups part-empty
+        # when the hidden size is not a multiple of the 256-wide tile.
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev) if self.overlap_streams else main
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for kind, want in runs:
+                _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
+                        want=want)
         for kind, want in runs:
-            ew = self._weights(kind)
-            pt = fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                   return_transpose=True, weights=wts, kmajor_scales=True)
-            _gemm_m(kind, pt.rows, ew.w2, plan, dH, mask, want)
-            dy[kind] = pt.rows_t
+            _gemm_m(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, mask, want)
         if self.capture_intermediates is not None:
             self.capture_intermediates["dh"] = dH.detach().clone()
         for kind, want in runs:
@@ -718,14 +743,13 @@ class FP8FlowMoECompute:
                       _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst),
                       _lib.ptr(plan.tile_expert), _lib.stream_of(GU))
             dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
-            h_col = ctx.saved_hcols[kind]
-            # weight gradients: contraction over each expert's tokens
-            _gemm_k(kind, h_col, dy[kind], plan, H, D, dW2, H * D, mask=mask, want=want)
+            # dW1 | dW3: contraction over each expert's tokens
             _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,
                     mask=mask, want=want)
             # input gradient
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
         dx = fused_unpermute_unpad(dXp, plan, None)
+        main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None
         return (dx.to(ctx.x_dtype), dw.reshape(T, K), dW1, dW2, dW3, None, None)
