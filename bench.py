@@ -88,10 +88,10 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     """Times `steps` calls of the expert block (forward, + backward when
     `backward`), weight cache dropped every step, with nothing recorded between
     the launches.  With `gemm_timer`, a second pass of `steps` identical steps
-    then records HIP events around every grouped-GEMM launch (each event
-    record leaves a few-microsecond bubble in the stream, so this pass is not
-    the one the step time comes from).  Returns (ms per step, GEMM event
-    summary or None)."""
+    then records HIP events around every grouped-GEMM launch, on one stream so
+    that no other kernel runs beside the one timed (each event record leaves a
+    few-microsecond bubble in the stream, so this pass is not the one the step
+    time comes from).  Returns (ms per step, GEMM event summary or None)."""
     import torch
 
     import nanopysche_amd as fm
@@ -132,12 +132,14 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     if gemm_timer:
         timer = GemmTimer()
         fmm.GEMM_TIMER = timer
+        blk.overlap_streams = False
         try:
             for _ in range(steps):
                 step()
             torch.cuda.synchronize()
         finally:
             fmm.GEMM_TIMER = None
+            blk.overlap_streams = overlap
         summary = timer.summary()
     return elapsed * 1e3 / steps, summary
 
