@@ -353,8 +353,12 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   // workgroup dispatch balances them.
   const int64_t NI = (p.n_i + kT - 1) / kT;
   int64_t JT = 0, L;
+  // Experts masked out (the other precision's launch) own no tiles here, so
+  // the XCD ranges split only the work this launch does.
+  auto unmasked = [&](int x) { return p.mask == nullptr || p.mask[x] == p.mask_want; };
   if (MODE == GM_RAGGED_M) {
-    for (int x = 0; x < p.E; ++x) JT += (p.offsets[x + 1] - p.offsets[x] + kT - 1) / kT;
+    for (int x = 0; x < p.E; ++x)
+      if (unmasked(x)) JT += (p.offsets[x + 1] - p.offsets[x] + kT - 1) / kT;
     const int64_t n_valid = JT * NI;
     const int64_t per_xcd = (n_valid + 7) / 8;
     const int64_t k = blockIdx.x / 8;
@@ -372,10 +376,11 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
     const int64_t gsz = JT - first < kGroupM ? JT - first : kGroupM;
     int64_t J = first + (L % gsz);
     i0 = ((L % (kGroupM * NI)) / gsz) * kT;
-    // token tile J -> (expert, rows): expert x holds ceil(rows_x / 256) tiles
+    // token tile J -> (expert, rows): an unmasked expert x holds
+    // ceil(rows_x / 256) tiles
     for (int x = 0; x < p.E; ++x) {
       const int64_t o0 = p.offsets[x], o1 = p.offsets[x + 1];
-      const int64_t cnt = (o1 - o0 + kT - 1) / kT;
+      const int64_t cnt = unmasked(x) ? (o1 - o0 + kT - 1) / kT : 0;
       if (J < cnt) {
         e = x;
         j0 = o0 + J * kT;
@@ -662,11 +667,16 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
   // ---------------------------------------------------------- tile decode ----
   // ragged-M: the valid 128-row tiles [0, offsets[E] / 128) split into one
   // contiguous range per XCD; ragged-K: tiles in launch order (as above).
-  int64_t e, i0, j0, k_lo, k_hi;
+  int64_t e = -1, i0 = 0, j0 = 0, k_lo, k_hi;
   const int64_t NI = (p.n_i + kBI - 1) / kBI;
   int64_t L;
+  // 128-row tiles of unmasked experts only (see the 256-tile kernel)
+  auto unmasked = [&](int x) { return p.mask == nullptr || p.mask[x] == p.mask_want; };
+  int64_t MT = 0;
   if (MODE == GM_RAGGED_M) {
-    const int64_t n_valid = int64_t(p.offsets[p.E] / kBJ) * NI;
+    for (int x = 0; x < p.E; ++x)
+      if (unmasked(x)) MT += (p.offsets[x + 1] - p.offsets[x]) / kBJ;
+    const int64_t n_valid = MT * NI;
     const int64_t per_xcd = (n_valid + 7) / 8;
     const int64_t k = blockIdx.x / 8;
     if (k >= per_xcd) return;
@@ -677,15 +687,22 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
     if (L >= p.n_tiles) return;
   }
   if (MODE == GM_RAGGED_M) {
-    const int64_t MT = p.offsets[p.E] / kBJ;
     const int64_t group = L / (kGroupM * NI);
     const int64_t first = group * kGroupM;
     const int64_t gsz = MT - first < kGroupM ? MT - first : kGroupM;
-    const int64_t mt = first + (L % gsz);
+    int64_t mt = first + (L % gsz);
     const int64_t nt = (L % (kGroupM * NI)) / gsz;
-    e = p.tile_expert[mt];
+    for (int x = 0; x < p.E; ++x) {
+      const int64_t o0 = p.offsets[x];
+      const int64_t cnt = unmasked(x) ? (p.offsets[x + 1] - o0) / kBJ : 0;
+      if (mt < cnt) {
+        e = x;
+        j0 = o0 + mt * kBJ;
+        break;
+      }
+      mt -= cnt;
+    }
     if (e < 0) return;
-    j0 = mt * kBJ;
     i0 = nt * kBI;
     k_lo = 0;
     k_hi = p.K;
