@@ -10,7 +10,7 @@ re-quantisation of the expert weights (their cache is dropped every step, as
 after an optimizer update).  Inputs are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--recipe flow_moe]
-    python bench.py --workload c1|c4|c5    # the other configs, one JSON line each
+    python bench.py --workload c1|c2|c4|c5    # the other configs, one JSON line each
 
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
@@ -254,6 +254,97 @@ def workload_c3(args, dev):
     }
 
 
+# ============================================================== configs[1] ====
+def workload_c2(args, dev):
+    """Quantisation primitives on configs[1]'s inputs: x [8192, 4096] bf16
+    N(0,1) with 0.1% of entries x100, W [14336, 4096] bf16 N(0,0.02).  Each
+    primitive runs `steps` times back to back between two HIP events (outputs
+    preallocated, C ABI called directly); GB/s = algorithmic bytes (every input
+    byte read once, every output byte written once) / time per launch."""
+    import torch
+
+    from nanopysche_amd import _lib
+    from nanopysche_amd.flow_moe import _alloc_quant, _tile_args
+
+    R, C = 8192, 4096
+    WR = 14336
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(R, C, generator=gen, device=dev)
+    n_out = round(0.001 * R * C)
+    pos = torch.randperm(R * C, generator=gen, device=dev)[:n_out]
+    x.view(-1)[pos] *= 100.0
+    x = x.bfloat16()
+    w = device_normal((WR, C), 0.02, gen, dev, torch.bfloat16)
+    st = _lib.stream_of(x)
+    n = R * C
+    BLK, P2, MX = _lib.QUANT_BLOCK, _lib.QUANT_POW2, _lib.QUANT_MX
+
+    def quant_args(kind, row, col):
+        bufs = _alloc_quant(R, C, kind, row, col, dev)
+        return bufs, _tile_args(kind, *bufs)
+
+    rowb, rowb_a = quant_args(BLK, True, False)
+    rowp, rowp_a = quant_args(P2, True, False)
+    fused, fused_a = quant_args(BLK, True, True)
+    fusedp, fusedp_a = quant_args(P2, True, True)
+    mxb, mx_a = quant_args(MX, True, False)
+    q, s = rowb[0], rowb[1]
+    qt = torch.empty(C, R, dtype=torch.uint8, device=dev)
+    sct = torch.empty(R // 128, C, dtype=torch.float32, device=dev)
+    deq = torch.empty(R, C, dtype=torch.bfloat16, device=dev)
+    wq = torch.empty(WR, C, dtype=torch.uint8, device=dev)
+    ws = torch.empty(WR // 128, C // 128, dtype=torch.float32, device=dev)
+
+    def fm_quantize(a):
+        return lambda: _lib.call("fm_quantize", _lib.ptr(x), _lib.DTYPE_BF16, R, C, C, *a, st)
+
+    ops = [
+        ("quantize 1x128 (fp32 scale)", fm_quantize(rowb_a), n * 2 + n + n // 128 * 4),
+        ("quantize 1x128 (pow2 scale)", fm_quantize(rowp_a), n * 2 + n + n // 128 * 4),
+        ("quantize 1x128 + 128x1 transpose (fp32 scale)", fm_quantize(fused_a), n * 2 + 2 * n + 2 * (n // 128) * 4),
+        ("quantize 1x128 + scaling-aware transpose (pow2)", fm_quantize(fusedp_a),
+         n * 2 + 2 * n + 2 * (n // 128) * 4),
+        ("quantize MX 1x32 (e8m0)", fm_quantize(mx_a), n * 2 + n + n // 32),
+        ("scaling-aware transpose (from e4m3)",
+         lambda: _lib.call("fm_scaling_aware_transpose", _lib.ptr(q), R, C, C, _lib.ptr(s), C // 128,
+                           _lib.ptr(qt), R, _lib.ptr(sct), C, st), 2 * n + 2 * (n // 128) * 4),
+        ("dequantize 1x128 -> bf16",
+         lambda: _lib.call("fm_dequantize", _lib.ptr(q), R, C, C, _lib.ptr(s), 0, 0, 7, C // 128, 1,
+                           _lib.ptr(deq), _lib.DTYPE_BF16, C, st), n + n // 128 * 4 + 2 * n),
+        ("quantize weight 128x128", lambda: _lib.call(
+            "fm_quantize_weight", _lib.ptr(w), _lib.DTYPE_BF16, 1, WR, C, C, 0, BLK, _lib.ptr(wq), C, 0, 0, _lib.ptr(ws),
+            C // 128, 0, None, 0, 0, 0, None, 0, 0, st), WR * C * 3 + (WR // 128) * (C // 128) * 4),
+    ]
+    fm_quantize(rowb_a)()  # inputs of the transpose / dequantise
+    results = []
+    for name, fn, nbytes in ops:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / args.steps
+        results.append({"op": name, "us": round(us, 2), "bytes": nbytes,
+                        "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    head = results[3]   # the fused row + transposed quantisation the expert block uses
+    return {
+        "metric": "HBM GB/s of the FP8 quantisation primitives on 1 MI355X (configs[1])",
+        "value": head["GB_s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 3,
+        "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "vs_baseline": None,
+        "dtype": "bf16 -> e4m3", "data": "synthetic",
+        "config": {"workload": "configs[1]: x [8192, 4096] bf16 N(0,1), 0.1% outliers x100; W [14336, 4096] "
+                               "bf16 N(0,0.02)", "headline_op": head["op"]},
+        "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_hbm_peak"], "traffic": None},
+        "ops": results,
+    }
+
+
 # ============================================================== configs[0] ====
 def workload_c1(args, dev):
     """BF16 expert block forward, top-1 softmax over 4 experts (the router's
@@ -410,7 +501,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c4", "c5"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c2", "c4", "c5"])
     ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-overlap", action="store_true",
@@ -426,7 +517,8 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
-    run = {"c3": workload_c3, "c1": workload_c1, "c4": workload_c4, "c5": workload_c5}[args.workload]
+    run = {"c3": workload_c3, "c1": workload_c1, "c2": workload_c2, "c4": workload_c4,
+           "c5": workload_c5}[args.workload]
     print(json.dumps(run(args, dev)))
 
 

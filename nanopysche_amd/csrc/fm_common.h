@@ -109,6 +109,20 @@ __device__ __forceinline__ void hw_dec_e4m3x4(uint32_t w, float f[4]) {
   f[2] = hi[0];
   f[3] = hi[1];
 }
+// x / s rounded to nearest from y = 1 / s (the correctly rounded reciprocal,
+// computed once per block): one FMA correction of x*y gives the correctly
+// rounded quotient whenever it is a normal number (Markstein, IBM J. Res. Dev.
+// 34(1), 1990); below the normal range it can differ, and such quotients
+// encode to e4m3 zero either way.  A zero x*y is returned as is (the
+// correction would turn -0 into +0), NaN x as x / s would, and an infinite s
+// gives x * 0, as x / s does.
+__device__ __forceinline__ float div_rn(float x, float s, float y) {
+  const float q0 = x * y;
+  const float r = fmaf(q0, -s, x);
+  const float q1 = fmaf(r, y, q0);
+  return x != x ? x : (s <= 3.40282347e38f && q0 != 0.f ? q1 : q0);
+}
+
 // clamp to +-448 in one v_med3_f32 (equal to clamp448 for every non-NaN value)
 __device__ __forceinline__ float clamp448_med3(float v) {
   return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);

@@ -146,14 +146,14 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
   const float s = block_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), a.kind == QK_POW2);
-  const float inv = 1.0f / s;  // exact for power-of-two scales
+  const float inv = 1.0f / s;  // exact for power-of-two scales; the reciprocal div_rn needs otherwise
   constexpr bool HW = FM_HW_CVT != 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = rr + 16 * i;
     float f[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = a.kind == QK_POW2 ? v[i][j] * inv : v[i][j] / s;
+    for (int j = 0; j < 8; ++j) f[j] = a.kind == QK_POW2 ? v[i][j] * inv : div_rn(v[i][j], s, inv);
     const uint32_t w0 = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
     const uint32_t w1 = enc_e4m3x4<HW>(f[4], f[5], f[6], f[7]);
     if (a.q)
@@ -204,34 +204,52 @@ struct DequantArgs {
   int64_t ld_out;
 };
 
+// grid (column chunks, rows): thread -> CW consecutive columns of rows
+// blockIdx.y, blockIdx.y + gridDim.y, ...; the CW columns share one scale
+// (CW <= the block width).
+template <int CW>
 __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
-  const int64_t chunks_per_row = a.cols / 8;
-  const int64_t n = a.rows * chunks_per_row;
-  for (int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x; idx < n;
-       idx += int64_t(gridDim.x) * 256) {
-    const int64_t r = idx / chunks_per_row;
-    const int64_t c = (idx % chunks_per_row) * 8;
-    const uint64_t pk = *reinterpret_cast<const uint64_t*>(a.q + r * a.ld_q + c);
+  constexpr bool HW = FM_HW_CVT != 0;
+  const int64_t c = (int64_t(blockIdx.x) * 256 + threadIdx.x) * CW;
+  if (c >= a.cols) return;
+  for (int64_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
+    uint32_t wd[CW / 4];
+    if constexpr (CW == 16) {
+      const uint4 pk = *reinterpret_cast<const uint4*>(a.q + r * a.ld_q + c);
+      wd[0] = pk.x; wd[1] = pk.y; wd[2] = pk.z; wd[3] = pk.w;
+    } else {
+      const uint2 pk = *reinterpret_cast<const uint2*>(a.q + r * a.ld_q + c);
+      wd[0] = pk.x; wd[1] = pk.y;
+    }
     const int64_t si = (r >> a.row_shift) * a.s_row_stride + (c >> a.col_shift) * a.s_col_stride;
     const float sc = a.s_e8m0 ? e8m0_to_f32(static_cast<const uint8_t*>(a.s)[si])
                               : static_cast<const float*>(a.s)[si];
-    float v[8];
+    float v[CW];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f32(uint8_t(pk >> (8 * i))) * sc;
+    for (int i = 0; i < CW / 4; ++i) {
+      if constexpr (HW) {
+        hw_dec_e4m3x4(wd[i], &v[4 * i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * i + j] = e4m3_to_f32(uint8_t(wd[i] >> (8 * j)));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CW; ++i) v[i] *= sc;
     if (a.out_f32) {
       float* o = static_cast<float*>(a.out) + r * a.ld_out + c;
-      *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
-    } else {
-      uint16_t b[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) b[i] = f32_to_bf16(v[i]);
-      uint4 w;
-      w.x = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
-      w.y = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
-      w.z = uint32_t(b[4]) | (uint32_t(b[5]) << 16);
-      w.w = uint32_t(b[6]) | (uint32_t(b[7]) << 16);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + r * a.ld_out + c) = w;
+      for (int i = 0; i < CW / 4; ++i)
+        reinterpret_cast<float4*>(o)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    } else {
+      uint32_t b[CW / 2];
+#pragma unroll
+      for (int i = 0; i < CW / 2; ++i)
+        b[i] = HW ? hw_bf16x2(v[2 * i], v[2 * i + 1])
+                  : uint32_t(f32_to_bf16(v[2 * i])) | (uint32_t(f32_to_bf16(v[2 * i + 1])) << 16);
+      uint4* o = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + r * a.ld_out + c);
+#pragma unroll
+      for (int i = 0; i < CW / 8; ++i) o[i] = make_uint4(b[4 * i], b[4 * i + 1], b[4 * i + 2], b[4 * i + 3]);
     }
   }
 }
@@ -242,9 +260,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
 __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q, const float* s,
                                                   int64_t ld_s, uint8_t* qt, int64_t ld_qt,
                                                   float* st, int64_t ld_st) {
-  __shared__ uint32_t tile[128][33];
+  __shared__ __attribute__((aligned(16))) uint32_t tile[128 * 33];
   __shared__ float rs[128];
   __shared__ float smax;
+  constexpr bool HW = FM_HW_CVT != 0;
   const int tid = threadIdx.x;
   const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
   // load 128x128 bytes: thread -> 16 bytes x 4 rows
@@ -254,10 +273,11 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
   for (int i = 0; i < 4; ++i) {
     const int row = rr + 32 * i;
     const uint4 pk = *reinterpret_cast<const uint4*>(q + (r0 + row) * ld_q + c0 + cc);
-    tile[row][(cc >> 2) + 0] = pk.x;
-    tile[row][(cc >> 2) + 1] = pk.y;
-    tile[row][(cc >> 2) + 2] = pk.z;
-    tile[row][(cc >> 2) + 3] = pk.w;
+    uint32_t* t = &tile[row * 33 + (cc >> 2)];
+    t[0] = pk.x;
+    t[1] = pk.y;
+    t[2] = pk.z;
+    t[3] = pk.w;
   }
   if (tid < 128) rs[tid] = s[(r0 + tid) * ld_s + (c0 >> 7)];
   __syncthreads();
@@ -268,25 +288,41 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
   }
   __syncthreads();
   const float sc = smax;
-  const int c = tid & 127, h = tid >> 7;
-  uint8_t* dst = qt + (c0 + c) * ld_qt + r0 + 64 * h;
-  for (int r16 = 0; r16 < 64; r16 += 16) {
-    uint32_t w4[4];
+  const float y = 1.0f / sc;
+  // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
+  // the 8 lanes of one cg write a whole 128-byte row of the transpose.
+  // Each element is e4m3((decode(q) * s_row) / s_col).
+  const int rg = tid & 7, cg = tid >> 3;
+  uint32_t w[4][4];   // [column][4-row word]
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t word = 0;
+  for (int k = 0; k < 4; ++k) {
+    float f[4][4];    // [row][column]
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int row = 64 * h + r16 + 4 * k + b;
-        const uint8_t code = uint8_t((tile[row][c >> 2] >> (8 * (c & 3))) & 0xffu);
-        const float v = e4m3_to_f32(code) * rs[row];
-        word |= uint32_t(quant_e4m3(v, sc)) << (8 * b);
+    for (int b = 0; b < 4; ++b) {
+      const int row = 16 * rg + 4 * k + b;
+      const float srow = rs[row];
+      const uint32_t word = tile[row * 33 + cg];
+      float d[4];
+      if constexpr (HW) {
+        hw_dec_e4m3x4(word, d);
+      } else {
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
       }
-      w4[k] = word;
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = div_rn(d[c4] * srow, sc, y);
     }
-    *reinterpret_cast<uint4*>(dst + r16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
   }
-  if (tid < 128) st[(r0 >> 7) * ld_st + c0 + tid] = sc;
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4)
+    *reinterpret_cast<uint4*>(qt + (c0 + 4 * cg + c4) * ld_qt + r0 + 16 * rg) =
+        make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+  if (rg == 0) {
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) st[(r0 >> 7) * ld_st + c0 + 4 * cg + c4] = sc;
+  }
 }
 
 // Runs both e4m3 and both bf16 conversion paths on the same inputs.
@@ -429,9 +465,16 @@ int fm_dequantize(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
   if (rows == 0 || cols == 0) return 0;
   DequantArgs a{static_cast<const uint8_t*>(q), rows, cols, ld_q, s, s_e8m0, row_shift, col_shift,
                 s_row_stride, s_col_stride, out, out_dtype == FM_DTYPE_F32, ld_out};
-  const int64_t chunks = rows * (cols / 8);
-  const unsigned blocks = unsigned(chunks / 256 + 1 < 8192 ? chunks / 256 + 1 : 8192);
-  hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  // 16 columns per thread when every 16 share a scale and the pitches allow
+  // 16-byte loads, else 8
+  const bool wide = col_shift >= 4 && cols % 16 == 0 && ld_q % 16 == 0 && ld_out % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const int cw = wide ? 16 : 8;
+  const dim3 grid(unsigned((cols / cw + 255) / 256), unsigned(rows < 65535 ? rows : 65535));
+  if (wide)
+    hipLaunchKernelGGL(dequant_kernel<16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(dequant_kernel<8>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("fm_dequantize");
 }
 

@@ -272,8 +272,11 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
       for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
       if (KIND == QK_BLOCK) {
         const float s = block_scale(group_max16(am), false);
-        const uint32_t w0 = enc_e4m3x4<HW>(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
-        const uint32_t w1 = enc_e4m3x4<HW>(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
+        const float y = 1.0f / s;
+        const uint32_t w0 = enc_e4m3x4<HW>(div_rn(v[0], s, y), div_rn(v[1], s, y), div_rn(v[2], s, y),
+                                           div_rn(v[3], s, y));
+        const uint32_t w1 = enc_e4m3x4<HW>(div_rn(v[4], s, y), div_rn(v[5], s, y), div_rn(v[6], s, y),
+                                           div_rn(v[7], s, y));
         if (want_row && grow < rows) {
           *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
               make_uint2(w0, w1);
@@ -323,13 +326,14 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
       red[h * 128 + c] = am;
       __syncthreads();
       const float s = block_scale(fmaxf(red[c], red[128 + c]), false);
+      const float y = 1.0f / s;
       for (int r16 = 0; r16 < 64; r16 += 16) {
         uint32_t w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float* p = &lds_val[(64 * h + r16 + 4 * k) * kTileLdsPitch + c];
-          w[k] = enc_e4m3x4<HW>(p[0] / s, p[kTileLdsPitch] / s, p[2 * kTileLdsPitch] / s,
-                                p[3 * kTileLdsPitch] / s);
+          w[k] = enc_e4m3x4<HW>(div_rn(p[0], s, y), div_rn(p[kTileLdsPitch], s, y),
+                                div_rn(p[2 * kTileLdsPitch], s, y), div_rn(p[3 * kTileLdsPitch], s, y));
         }
         *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = make_uint4(w[0], w[1], w[2], w[3]);
       }

@@ -30,6 +30,11 @@ def _edge_matrix():
     x[6, 256:384] = -7.0                     # constant block
     x[7, 384:512] = torch.arange(128).float() * 2 ** -12  # e4m3-subnormal range after scaling
     x[8:128, 0:128] = 0.0                    # a whole 128x128 tile of zeros
+    x[9, 128:256] = -0.0                     # a negative-zero block (code 0x80)
+    x[10, 256:384:2] = -0.0                  # signed zeros beside regular values
+    x[10, 257:384:2] = 1.5
+    x[11, 384:512] = -1e-30                  # negative values that quantise to -0
+    x[11, 400] = 2.0
     return x.bfloat16()
 
 
@@ -67,6 +72,22 @@ def test_edge_blocks_bitexact(dev):
     mq = fm.quantize_to_fp8(x.to(dev), G.MX_1x32)
     oq, oc = ofp8.quant_mx_1x32(x.float().numpy())
     assert np.array_equal(_np(mq.data), oq) and np.array_equal(_np(mq.scale), oc)
+
+
+def test_edge_blocks_transpose_and_weights_bitexact(dev):
+    """fp32-scale paths on the edge matrix (signed zeros, tiny and saturating
+    values): the scaling-aware transpose of the row output and the 128x128
+    weight quantiser, bit-exact against the oracle."""
+    x = _edge_matrix()
+    xf = x.float().numpy()
+    row = fm.quantize_to_fp8(x.to(dev))
+    t = fm.scaling_aware_transpose(row)
+    cq, cs = ofp8.scaling_aware_transpose(_np(row.data), _np(row.scale))
+    assert np.array_equal(_np(t.scale), cs) and np.array_equal(_np(t.data), cq)
+    w = fm.quantize_to_fp8(x.to(dev), G.BLOCK_128x128)
+    wq, ws = ofp8.quant_128x128(xf)
+    assert np.array_equal(_np(w.scale), ws) and np.array_equal(_np(w.data), wq)
+    assert (_np(row.data)[9, 128:256] == 0x80).all()
 
 
 def test_fp32_input_and_ragged_rows(dev):
