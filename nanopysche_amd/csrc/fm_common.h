@@ -94,7 +94,7 @@ FM_HD uint8_t quant_e4m3(float x, float scale) { return f32_to_e4m3(clamp448(x /
 // test_gpu_quant.py::test_hw_convert_matches_software checks it against the
 // integer routine above.
 __device__ __forceinline__ uint32_t hw_e4m3x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);  // high half set below
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return uint32_t(w);
 }
@@ -109,20 +109,53 @@ __device__ __forceinline__ void hw_dec_e4m3x4(uint32_t w, float f[4]) {
   f[2] = hi[0];
   f[3] = hi[1];
 }
-// x / s rounded to nearest from y = 1 / s (the correctly rounded reciprocal,
-// computed once per block): one FMA correction of x*y gives the correctly
-// rounded quotient whenever it is a normal number (Markstein, IBM J. Res. Dev.
-// 34(1), 1990); below the normal range it can differ, and such quotients
-// encode to e4m3 zero either way.  A zero x*y is returned as is (the
-// correction would turn -0 into +0), NaN x as x / s would, and an infinite s
-// gives x * 0, as x / s does.
-__device__ __forceinline__ float div_rn(float x, float s, float y) {
-  const float q0 = x * y;
-  const float r = fmaf(q0, -s, x);
-  const float q1 = fmaf(r, y, q0);
-  return x != x ? x : (s <= 3.40282347e38f && q0 != 0.f ? q1 : q0);
+// x / s rounded to nearest for the quotients a block quantiser forms
+// (|x| <= 448 s up to rounding, or s infinite), from a reciprocal computed once
+// per block: y = RN(1/s), q0 = RN(x y), e = q0 s - x (exact, one FMA),
+// q = RN(q0 - e y) is the correctly rounded quotient whenever it is a normal
+// number (Markstein, IBM J. Res. Dev. 34(1), 1990); below the normal range it
+// can differ, and such quotients encode to e4m3 zero either way.  The
+// correction multiplies by ny = -y rather than negating e, so a zero x keeps
+// its sign (e = +0, e * ny = -0).  For an infinite s the correction uses 0 in
+// place of s, so q = x * 0, as x / s.
+struct Recip {
+  float sd;  // s, or 0 when s is infinite
+  float ny;  // -RN(1 / s)
+};
+__device__ __forceinline__ Recip recip_of(float s) { return Recip{s <= 3.40282347e38f ? s : 0.f, -(1.0f / s)}; }
+__device__ __forceinline__ float div_rn(float x, Recip d) {
+  const float q0 = x * -d.ny;
+  const float e = fmaf(q0, d.sd, -x);
+  return fmaf(e, d.ny, q0);
 }
-
+// a / 448 rounded to nearest for a >= 1e-12 (the amax floor), in three
+// operations: the Markstein correction with the constant RN(1/448) gives the
+// correctly rounded quotient for every finite a in that range (checked
+// exhaustively on the CPU against IEEE division); an infinite a is returned.
+__device__ __forceinline__ float div448(float a) {
+  constexpr float y = 1.0f / kE4M3Max;
+  const float q0 = a * y;
+  const float r = fmaf(q0, -kE4M3Max, a);
+  const float q = fmaf(r, y, q0);
+  return a <= 3.40282347e38f ? q : a;
+}
+// block_scale on the device, with div448 for the division.
+__device__ __forceinline__ float block_scale_dev(float amax, bool pow2) {
+  float s = div448(fmaxf(amax, kAmaxFloor));
+  if (pow2) {
+    uint32_t u = f2u(s);
+    uint32_t e = (u >> 23) & 0xffu;
+    if (u & 0x7fffffu) e += 1u;
+    s = u2f(e << 23);
+  }
+  return s;
+}
+// 1 / s for a power-of-two scale s = 2^k, k in [-126, 126], from the exponent
+// field (exact); 0 for an infinite s.
+__device__ __forceinline__ float pow2_recip(float s) {
+  const uint32_t e = (f2u(s) >> 23) & 0xffu;
+  return e == 0xffu ? 0.f : u2f((254u - e) << 23);
+}
 // clamp to +-448 in one v_med3_f32 (equal to clamp448 for every non-NaN value)
 __device__ __forceinline__ float clamp448_med3(float v) {
   return __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);

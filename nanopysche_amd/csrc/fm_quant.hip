@@ -54,20 +54,36 @@ struct DenseSrc<float> {
 // Two expert weight stacks a, b = [groups][rows][cols] read as one
 // [groups][2 rows][cols] matrix (group g: rows of a, then rows of b), the
 // layout of the fused gate|up weight -- without materialising it.
-template <typename T>
+// ALIGNED (rows % 128 == 0): every 128-row tile lies in one matrix, so
+// tile_source resolves the matrix and group once per tile and fetch is a
+// dense row access; otherwise each fetch maps its row.
+template <typename T, bool ALIGNED>
 struct PairSrc {
   static constexpr int kOut = 1;
   using Raw = typename DenseSrc<T>::Raw;
   const T* a;
   const T* b;
   int64_t rows, ld;
+  const T* tile_base;  // ALIGNED, set by tile_source: logical row r at tile_base + r * ld
   __device__ __forceinline__ Raw fetch(int64_t row, int64_t col) const {
-    const int64_t g = row / (2 * rows), r = row % (2 * rows);
-    const T* base = r < rows ? a : b;
-    return DenseSrc<T>{base + (g * rows + (r < rows ? r : r - rows)) * ld, 0}.fetch(0, col);
+    if constexpr (ALIGNED) {
+      return DenseSrc<T>{tile_base, ld}.fetch(row, col);
+    } else {
+      const int64_t g = row / (2 * rows), r = row % (2 * rows);
+      const T* base = r < rows ? a : b;
+      return DenseSrc<T>{base + (g * rows + (r < rows ? r : r - rows)) * ld, 0}.fetch(0, col);
+    }
   }
   __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const { DenseSrc<T>{}.compute(r, v); }
 };
+template <typename T>
+__device__ __forceinline__ PairSrc<T, true> tile_source(const PairSrc<T, true>& src, int64_t row0) {
+  PairSrc<T, true> t = src;
+  const int64_t g = row0 / (2 * src.rows), r = row0 - g * 2 * src.rows;
+  const T* m = r < src.rows ? src.a : src.b;
+  t.tile_base = m + (g * src.rows + (r < src.rows ? r : r - src.rows) - row0) * src.ld;
+  return t;
+}
 
 // ------------------------------------------------------- 128x128 weight blocks ----
 struct WeightQuantArgs {
@@ -145,15 +161,17 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
   for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
-  const float s = block_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), a.kind == QK_POW2);
-  const float inv = 1.0f / s;  // exact for power-of-two scales; the reciprocal div_rn needs otherwise
+  const float s = block_scale_dev(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), a.kind == QK_POW2);
+  const bool pow2 = a.kind == QK_POW2;
+  const float inv = pow2 ? pow2_recip(s) : 0.f;  // exact for power-of-two scales
+  const Recip d = recip_of(s);
   constexpr bool HW = FM_HW_CVT != 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = rr + 16 * i;
     float f[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = a.kind == QK_POW2 ? v[i][j] * inv : div_rn(v[i][j], s, inv);
+    for (int j = 0; j < 8; ++j) f[j] = pow2 ? v[i][j] * inv : div_rn(v[i][j], d);
     const uint32_t w0 = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
     const uint32_t w1 = enc_e4m3x4<HW>(f[4], f[5], f[6], f[7]);
     if (a.q)
@@ -173,16 +191,11 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int rb = 16 * rg + 4 * k;
-    const uint32_t a0 = tile[rb][cg], a1 = tile[rb + 1][cg], a2 = tile[rb + 2][cg], a3 = tile[rb + 3][cg];
-    // D.byte[i] = {S0, S1}.byte[sel.byte[i]], bytes 0-3 from S1 and 4-7 from S0
-    const uint32_t p01l = __builtin_amdgcn_perm(a1, a0, 0x05010400u);  // a0c0 a1c0 a0c1 a1c1
-    const uint32_t p01h = __builtin_amdgcn_perm(a1, a0, 0x07030602u);  // a0c2 a1c2 a0c3 a1c3
-    const uint32_t p23l = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
-    const uint32_t p23h = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
-    cw[0][k] = __builtin_amdgcn_perm(p23l, p01l, 0x05040100u);         // a0c0 a1c0 a2c0 a3c0
-    cw[1][k] = __builtin_amdgcn_perm(p23l, p01l, 0x07060302u);
-    cw[2][k] = __builtin_amdgcn_perm(p23h, p01h, 0x05040100u);
-    cw[3][k] = __builtin_amdgcn_perm(p23h, p01h, 0x07060302u);
+    const uint32_t in[4] = {tile[rb][cg], tile[rb + 1][cg], tile[rb + 2][cg], tile[rb + 3][cg]};
+    uint32_t out[4];
+    transpose4x4_bytes(in, out);
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) cw[c4][k] = out[c4];
   }
 #pragma unroll
   for (int c4 = 0; c4 < 4; ++c4)
@@ -288,37 +301,21 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
   }
   __syncthreads();
   const float sc = smax;
-  const float y = 1.0f / sc;
-  // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
-  // the 8 lanes of one cg write a whole 128-byte row of the transpose.
-  // Each element is e4m3((decode(q) * s_row) / s_col).
-  const int rg = tid & 7, cg = tid >> 3;
-  uint32_t w[4][4];   // [column][4-row word]
+  const Recip d = recip_of(sc);
+  // each element is e4m3((decode(q) * s_row) / s_col)
+  store_transposed_codes(tile, qt, ld_qt, c0, r0, [&](uint32_t word, int row) {
+    const float srow = rs[row];
+    float f[4];
+    if constexpr (HW) {
+      hw_dec_e4m3x4(word, f);
+    } else {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float f[4][4];    // [row][column]
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int row = 16 * rg + 4 * k + b;
-      const float srow = rs[row];
-      const uint32_t word = tile[row * 33 + cg];
-      float d[4];
-      if constexpr (HW) {
-        hw_dec_e4m3x4(word, d);
-      } else {
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
-      }
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = div_rn(d[c4] * srow, sc, y);
+      for (int c4 = 0; c4 < 4; ++c4) f[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
     }
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
-  }
-#pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4)
-    *reinterpret_cast<uint4*>(qt + (c0 + 4 * cg + c4) * ld_qt + r0 + 16 * rg) =
-        make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+    return enc_e4m3x4<HW>(div_rn(f[0] * srow, d), div_rn(f[1] * srow, d), div_rn(f[2] * srow, d),
+                          div_rn(f[3] * srow, d));
+  });
+  const int rg = tid & 7, cg = tid >> 3;
   if (rg == 0) {
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) st[(r0 >> 7) * ld_st + c0 + 4 * cg + c4] = sc;
@@ -411,11 +408,15 @@ int fm_quantize_pair(const void* a, const void* b, int dtype, int64_t groups, in
   const TileOut o = make_tile_out(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st, 0, 0, nullptr);
   hipStream_t sm = static_cast<hipStream_t>(stream);
   const int64_t total = groups * 2 * rows;
-  if (dtype == FM_DTYPE_BF16)
-    return launch_tile_producer(PairSrc<uint16_t>{static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
-                                                  rows, ld}, o, total, cols, sm, "fm_quantize_pair");
-  return launch_tile_producer(PairSrc<float>{static_cast<const float*>(a), static_cast<const float*>(b), rows, ld},
-                              o, total, cols, sm, "fm_quantize_pair");
+  auto launch = [&](auto tag) {
+    using T = decltype(tag);
+    const T* pa = static_cast<const T*>(a);
+    const T* pb = static_cast<const T*>(b);
+    if (rows % 128 == 0)
+      return launch_tile_producer(PairSrc<T, true>{pa, pb, rows, ld, nullptr}, o, total, cols, sm, "fm_quantize_pair");
+    return launch_tile_producer(PairSrc<T, false>{pa, pb, rows, ld, nullptr}, o, total, cols, sm, "fm_quantize_pair");
+  };
+  return dtype == FM_DTYPE_BF16 ? launch(uint16_t{}) : launch(float{});
 }
 
 int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows, int64_t cols,

@@ -5,15 +5,18 @@
 //   * a transposed output  (bf16, or e4m3 with 128x1 / 32x1 block scales),
 // reading the source exactly once.  A source may yield NOUT values per
 // element (SwiGLU backward yields dg and du), each with its own column offset
-// in the outputs.  HBM-bound: 16-byte loads, 8-byte row stores (16 lanes cover
-// one 128-byte row segment), 16-byte transposed stores.
+// in the outputs.  HBM-bound: 16-byte loads, 8-byte row stores (8 lanes cover
+// one 64-byte half of a row block), 16-byte transposed stores.
 //
 // LDS staging for the transposed output:
 //   QK_POW2  -- per output, e4m3 codes [128][128 + 4 pad] + one row scale per
 //               row (17 KiB): the transposed output is the scaling-aware
 //               transpose of the row output, so the codes are all it needs
 //               (pow2_tile).
+//   QK_BLOCK -- e4m3 codes already in the column scale (17 KiB); the values
+//               stay in registers (block_tile).
 //   others   -- fp32 values [128][129] (66 KiB), one output at a time.
+// A launch without the transposed output uses no LDS (rows_tile).
 #pragma once
 
 #include "fm_common.h"
@@ -70,18 +73,54 @@ __device__ __forceinline__ uint32_t enc_bf16x2(float a, float b) {
   else return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
 }
 
-__device__ __forceinline__ float group_max16(float v) {
-  // max over the 16 consecutive lanes that share a 128-column row block
-  v = fmaxf(v, __shfl_xor(v, 1, 16));
-  v = fmaxf(v, __shfl_xor(v, 2, 16));
-  v = fmaxf(v, __shfl_xor(v, 4, 16));
-  v = fmaxf(v, __shfl_xor(v, 8, 16));
-  return v;
+// e4m3 of four values already within +-448 (no clamp): power-of-two scaled
+// values, whose magnitude is at most 448 exactly.
+template <bool HW>
+__device__ __forceinline__ uint32_t enc_e4m3x4_inrange(float a, float b, float c, float d) {
+  if constexpr (HW) {
+    return hw_e4m3x4(a, b, c, d);
+  } else {
+    return uint32_t(f32_to_e4m3(a)) | (uint32_t(f32_to_e4m3(b)) << 8) | (uint32_t(f32_to_e4m3(c)) << 16) |
+           (uint32_t(f32_to_e4m3(d)) << 24);
+  }
 }
+
+// Lane exchanges for maxima of non-negative floats, done on their bit
+// patterns (integer order equals float order for them, and integer max needs
+// no NaN canonicalisation).  DPP within rows of 16 lanes: quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror (lane i <- 7 - i within 8), row_ror:8
+// (lane i <- i ^ 8 within 16).
+template <int CTRL>
+__device__ __forceinline__ int dpp_move(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppQuadSwap1 = 0xb1, kDppQuadSwap2 = 0x4e, kDppRowHalfMirror = 0x141, kDppRowRor8 = 0x128;
+
+// max over the 4 lanes of a quad
 __device__ __forceinline__ float group_max4(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1, 4));
-  v = fmaxf(v, __shfl_xor(v, 2, 4));
-  return v;
+  int u = __builtin_bit_cast(int, v);
+  u = max(u, dpp_move<kDppQuadSwap1>(u));
+  u = max(u, dpp_move<kDppQuadSwap2>(u));
+  return __builtin_bit_cast(float, u);
+}
+// max over 8 consecutive lanes (8-aligned): quad maxima, then the half mirror
+// pairs quad 0 with quad 1
+__device__ __forceinline__ float group_max8(float v) {
+  int u = __builtin_bit_cast(int, group_max4(v));
+  u = max(u, dpp_move<kDppRowHalfMirror>(u));
+  return __builtin_bit_cast(float, u);
+}
+// max over the 8 lanes l, l ^ 8, l ^ 16, ..., l ^ 56 (same l % 8): row_ror:8,
+// then v_permlane16_swap / v_permlane32_swap with both operands v, which
+// leave {v[l], v[l ^ 16]} / {v[l], v[l ^ 32]} in their two results.
+__device__ __forceinline__ float max_across_rowgroups(float v) {
+  int u = __builtin_bit_cast(int, v);
+  u = max(u, dpp_move<kDppRowRor8>(u));
+  const auto a = __builtin_amdgcn_permlane16_swap(uint32_t(u), uint32_t(u), false, false);
+  u = max(int(a[0]), int(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(uint32_t(u), uint32_t(u), false, false);
+  u = max(int(b[0]), int(b[1]));
+  return __builtin_bit_cast(float, u);
 }
 
 // 8 bf16 (one 16-byte load) -> 8 floats
@@ -103,64 +142,251 @@ __device__ __forceinline__ uint64_t pack8_e4m3(const uint8_t* b) {
 
 // Source functor contract:
 //   static constexpr int kOut;                       // values per element (1 or 2)
-//   struct Raw;                                      // what the loads of one row return
+//   struct Raw;                                      // what the loads of 8 columns return
 //   __device__ Raw fetch(int64_t row, int64_t col) const;
 //   __device__ void compute(const Raw& r, float v[kOut][8]) const;
 // fetch issues the (branch-free) loads of columns [col, col+8) of logical row
 // `row`; compute turns them into values (zeros for rows the source treats as
 // padding).  The kernel fetches all of a thread's rows before computing any,
 // so their loads overlap, and converts one row at a time.
-// Power-of-two recipe: both outputs of a two-output source are quantised as
-// soon as a row is computed (the transposed output is the scaling-aware
-// transpose of the row output, so e4m3 codes + row scales in LDS are all it
-// needs, 17 KiB per output); no row values stay in registers.
+//
+// Thread layout: lane8 = tid % 8, row group rg = tid / 8 (0..31); a thread
+// owns rows rg + 32 it (it = 0..3) and, in each, the two 8-column segments
+// [64 h + 8 lane8, +8) (h = 0, 1).  One load instruction of a wave covers 8
+// rows x 128 contiguous bytes of bf16 per row; the 8 lanes of a row group hold
+// a whole 128-column block, so a row block's scale costs one 8-lane reduction
+// per 16 values.
+constexpr int kRowsPerThread = 4;
+
+// Row-output addresses of one thread for one output: segment 0 of its row
+// and the scale of that row block (MX: of segment 0's 32-column block);
+// segment 1 is 64 columns (two MX blocks) further.  next() moves 32 rows down.
+template <int KIND>
+struct RowPtr {
+  uintptr_t q, s;
+  int64_t q_step, s_step, s_seg;
+  __device__ __forceinline__ RowPtr(const TileOut& o, int64_t row, int64_t ocol) {
+    constexpr int64_t qb = KIND == QK_BF16 ? 2 : 1;
+    const int64_t c = ocol + 8 * (threadIdx.x & 7);
+    q = uintptr_t(o.row_q) + uintptr_t((row * o.ld_row + c) * qb);
+    q_step = 32 * o.ld_row * qb;
+    if (KIND == QK_MX) {
+      s = uintptr_t(o.row_s) + uintptr_t(row * o.rs_row + (c >> 5) * o.rs_kb);
+      s_step = 32 * o.rs_row;
+      s_seg = 2 * o.rs_kb;
+    } else {
+      s = uintptr_t(o.row_s) + uintptr_t(4 * (row * o.rs_row + (ocol >> 7) * o.rs_kb));
+      s_step = 128 * o.rs_row;
+      s_seg = 0;
+    }
+  }
+  __device__ __forceinline__ uintptr_t qseg(int h) const { return q + uintptr_t(h * 64 * (KIND == QK_BF16 ? 2 : 1)); }
+  __device__ __forceinline__ void next() {
+    q += q_step;
+    s += s_step;
+  }
+};
+
+// Row output of one thread's 16 values of one row (v[h] = segment h): e4m3
+// codes with the row block's scale (or bf16), stored when `store`; returns the
+// code words {seg 0 cols 0-3, seg 0 cols 4-7, seg 1 cols 0-3, seg 1 cols 4-7}.
+template <int KIND, bool HW>
+__device__ __forceinline__ uint4 row_quant(const float (&v)[2][8], const RowPtr<KIND>& p, bool store, float& sc) {
+  const int lane8 = threadIdx.x & 7;
+  uint32_t w[4] = {0, 0, 0, 0};
+  sc = 0.f;
+  if constexpr (KIND == QK_BF16) {
+    if (store) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<uint4*>(p.qseg(h)) =
+            make_uint4(enc_bf16x2<HW>(v[h][0], v[h][1]), enc_bf16x2<HW>(v[h][2], v[h][3]),
+                       enc_bf16x2<HW>(v[h][4], v[h][5]), enc_bf16x2<HW>(v[h][6], v[h][7]));
+    }
+    return make_uint4(0, 0, 0, 0);
+  } else if constexpr (KIND == QK_MX) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float am = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[h][i]));
+      const uint32_t code = mx_code(group_max4(am));
+      const float inv = mx_inv_scale(code);
+      w[2 * h] = enc_e4m3x4<HW>(v[h][0] * inv, v[h][1] * inv, v[h][2] * inv, v[h][3] * inv);
+      w[2 * h + 1] = enc_e4m3x4<HW>(v[h][4] * inv, v[h][5] * inv, v[h][6] * inv, v[h][7] * inv);
+      if (store && (lane8 & 3) == 0) *reinterpret_cast<uint8_t*>(p.s + h * p.s_seg) = uint8_t(code);
+    }
+  } else {
+    float am = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[h][i]));
+    sc = block_scale_dev(group_max8(am), KIND == QK_POW2);
+    if constexpr (KIND == QK_POW2) {
+      const float inv = pow2_recip(sc);  // exact: sc is a power of two, |v * inv| <= 448
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[2 * h] = enc_e4m3x4_inrange<HW>(v[h][0] * inv, v[h][1] * inv, v[h][2] * inv, v[h][3] * inv);
+        w[2 * h + 1] = enc_e4m3x4_inrange<HW>(v[h][4] * inv, v[h][5] * inv, v[h][6] * inv, v[h][7] * inv);
+      }
+    } else {
+      const Recip d = recip_of(sc);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[2 * h] = enc_e4m3x4<HW>(div_rn(v[h][0], d), div_rn(v[h][1], d), div_rn(v[h][2], d), div_rn(v[h][3], d));
+        w[2 * h + 1] =
+            enc_e4m3x4<HW>(div_rn(v[h][4], d), div_rn(v[h][5], d), div_rn(v[h][6], d), div_rn(v[h][7], d));
+      }
+    }
+    if (store && lane8 == 0) *reinterpret_cast<float*>(p.s) = sc;
+  }
+  if (store) {
+    *reinterpret_cast<uint2*>(p.qseg(0)) = make_uint2(w[0], w[1]);
+    *reinterpret_cast<uint2*>(p.qseg(1)) = make_uint2(w[2], w[3]);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Fetch of a thread's rows rg + 32 it, both segments: rows past the end
+// re-read the last row (a full tile takes the unclamped path, whose addresses
+// are a base plus multiples of 32 rows).
+template <class Src>
+__device__ __forceinline__ void fetch_rows(const Src& src, typename Src::Raw (&raw)[kRowsPerThread][2],
+                                           int64_t rows, int64_t row0, int64_t col0) {
+  const int64_t r = row0 + (threadIdx.x >> 3);
+  const int64_t c = col0 + 8 * (threadIdx.x & 7);
+  if (row0 + 128 <= rows) {
+#pragma unroll
+    for (int it = 0; it < kRowsPerThread; ++it)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) raw[it][h] = src.fetch(r + 32 * it, c + 64 * h);
+  } else {
+#pragma unroll
+    for (int it = 0; it < kRowsPerThread; ++it) {
+      const int64_t g = r + 32 * it < rows ? r + 32 * it : rows - 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) raw[it][h] = src.fetch(g, c + 64 * h);
+    }
+  }
+}
+
+// Values of one row: v[oi][h][i] for output oi, segment h.
+template <class Src>
+__device__ __forceinline__ void compute_row(const Src& src, const typename Src::Raw (&raw)[2],
+                                            float (&v)[Src::kOut][2][8]) {
+  float t[2][Src::kOut][8];
+  src.compute(raw[0], t[0]);
+  src.compute(raw[1], t[1]);
+#pragma unroll
+  for (int oi = 0; oi < Src::kOut; ++oi)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[oi][h][i] = t[h][oi][i];
+}
+
+// 4x4 byte transpose: out[c] byte b = in[b] byte c.
+__device__ __forceinline__ void transpose4x4_bytes(const uint32_t (&in)[4], uint32_t (&out)[4]) {
+  const uint32_t lo01 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // i0b0 i1b0 i0b1 i1b1
+  const uint32_t hi01 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // i0b2 i1b2 i0b3 i1b3
+  const uint32_t lo23 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
+// Transposed store of a 128x128 e4m3 tile staged in LDS as code words
+// (code[row * 33 + c / 4] holds columns [c, c+4) of a row): thread -> columns
+// [4 cg, +4) x rows [16 rg, +16); the 8 lanes of one cg write a whole
+// 128-byte row of the transpose.  `tx` maps the four codes of one word (one
+// row, four columns) to their values in the transposed output; the identity
+// when the codes are already in the column scale.
+template <class TX>
+__device__ __forceinline__ void store_transposed_codes(const uint32_t* code, uint8_t* qt8, int64_t ld_col,
+                                                       int64_t ocol, int64_t row0, TX tx) {
+  const int tid = threadIdx.x;
+  const int rg = tid & 7, cg = tid >> 3;
+  uint32_t w[4][4];  // [column][4-row word]
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t in[4], out[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int row = 16 * rg + 4 * k + b;
+      in[b] = tx(code[row * 33 + cg], row);
+    }
+    transpose4x4_bytes(in, out);
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = out[c4];
+  }
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4)
+    *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * ld_col + row0 + 16 * rg) =
+        make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+}
+
+// LDS word index of segment h of row r in a [128][33]-word code tile
+__device__ __forceinline__ int code_word(int r, int h) { return r * 33 + 16 * h + 2 * (threadIdx.x & 7); }
+
+// Row output only: each row is quantised as soon as it is computed; no LDS.
+template <class Src, int KIND, bool HW>
+__device__ __forceinline__ void rows_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
+                                          int64_t col0) {
+  constexpr int NOUT = Src::kOut;
+  typename Src::Raw raw[kRowsPerThread][2];
+  fetch_rows(src, raw, rows, row0, col0);
+  const int64_t r = row0 + (threadIdx.x >> 3);
+  RowPtr<KIND> p[2] = {RowPtr<KIND>(o, r, col0 + o.col_off[0]), RowPtr<KIND>(o, r, col0 + o.col_off[NOUT - 1])};
+#pragma unroll
+  for (int it = 0; it < kRowsPerThread; ++it) {
+    float v[NOUT][2][8];
+    compute_row(src, raw[it], v);
+    const bool ok = r + 32 * it < rows;
+#pragma unroll
+    for (int oi = 0; oi < NOUT; ++oi) {
+      float sc;
+      row_quant<KIND, HW>(v[oi], p[oi], ok, sc);
+      p[oi].next();
+    }
+  }
+}
+
+// Power-of-two recipe with the transposed output: both outputs of a
+// two-output source are quantised as soon as a row is computed (the
+// transposed output is the scaling-aware transpose of the row output, so the
+// e4m3 codes + row scales in LDS are all it needs, 17 KiB per output); no row
+// values stay in registers.
 template <class Src, bool HW>
 __device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
-                                          int64_t col0, int cpos, bool want_row, bool want_col) {
+                                          int64_t col0, bool want_row) {
   constexpr int NOUT = Src::kOut;
   const int tid = threadIdx.x;
   __shared__ float p_red[NOUT];
   __shared__ float p_rscale[NOUT][128];
   __shared__ __attribute__((aligned(16))) uint32_t p_code[NOUT][128 * 33];
-  typename Src::Raw raw[8];
+  typename Src::Raw raw[kRowsPerThread][2];
+  fetch_rows(src, raw, rows, row0, col0);  // rows % 128 == 0: every row is in range
+  const int64_t rg = tid >> 3;
+  RowPtr<QK_POW2> p[2] = {RowPtr<QK_POW2>(o, row0 + rg, col0 + o.col_off[0]),
+                          RowPtr<QK_POW2>(o, row0 + rg, col0 + o.col_off[NOUT - 1])};
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int64_t grow = row0 + (tid >> 4) + 16 * it;
-    raw[it] = src.fetch(grow < rows ? grow : rows - 1, col0 + cpos);
-  }
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    float v[NOUT][8];
-    src.compute(raw[it], v);
-    const int r = (tid >> 4) + 16 * it;
-    const int64_t grow = row0 + r;
-    const bool ok = grow < rows;
+  for (int it = 0; it < kRowsPerThread; ++it) {
+    float v[NOUT][2][8];
+    compute_row(src, raw[it], v);
+    const int r = int(rg) + 32 * it;
 #pragma unroll
     for (int oi = 0; oi < NOUT; ++oi) {
-      float am = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[oi][i] = ok ? v[oi][i] : 0.f;
-        am = fmaxf(am, fabsf(v[oi][i]));
-      }
-      const float sc = block_scale(group_max16(am), true);
-      const float inv = 1.0f / sc;  // exact: sc is a power of two
-      const uint32_t w0 = enc_e4m3x4<HW>(v[oi][0] * inv, v[oi][1] * inv, v[oi][2] * inv, v[oi][3] * inv);
-      const uint32_t w1 = enc_e4m3x4<HW>(v[oi][4] * inv, v[oi][5] * inv, v[oi][6] * inv, v[oi][7] * inv);
-      const int64_t ocol = col0 + o.col_off[oi];
-      if (want_row && ok) {
-        *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
-            make_uint2(w0, w1);
-        if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.rs_row + (ocol >> 7) * o.rs_kb] = sc;
-      }
-      if (want_col) {
-        p_code[oi][r * 33 + (cpos >> 2)] = w0;
-        p_code[oi][r * 33 + (cpos >> 2) + 1] = w1;
-        if ((tid & 15) == 0) p_rscale[oi][r] = sc;
-      }
+      float sc;
+      const uint4 w = row_quant<QK_POW2, HW>(v[oi], p[oi], want_row, sc);
+      p[oi].next();
+      *reinterpret_cast<uint2*>(&p_code[oi][code_word(r, 0)]) = make_uint2(w.x, w.y);
+      *reinterpret_cast<uint2*>(&p_code[oi][code_word(r, 1)]) = make_uint2(w.z, w.w);
+      if ((tid & 7) == 0) p_rscale[oi][r] = sc;
     }
   }
-  if (!want_col) return;
   __syncthreads();
   // column scale of each output: the largest row scale of the tile
   if (tid < 64) {
@@ -172,43 +398,28 @@ __device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int6
     }
   }
   __syncthreads();
-  // thread -> columns [4 cg, +4) (one LDS word per row) x rows [16 rg, +16):
-  // the 8 lanes of one cg write a whole 128-byte row of the transpose.
-  // decode(q) * (s_row / s_col) is exact (powers of two) and <= 448.
-  uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
-  const int rg = tid & 7, cg = tid >> 3;
+  // decode(q) * (s_row / s_col) is exact (powers of two) and at most 448.
+  const int cg = tid >> 3;
 #pragma unroll
   for (int oi = 0; oi < NOUT; ++oi) {
     const int64_t ocol = col0 + o.col_off[oi];
     const float st = p_red[oi];
-    const float inv = 1.0f / st;  // exact: power of two
-    uint32_t w[4][4];   // [column][4-row word]
+    const float inv = pow2_recip(st);
+    const float* rs = p_rscale[oi];
+    store_transposed_codes(p_code[oi], static_cast<uint8_t*>(o.col_q), o.ld_col, ocol, row0,
+                           [&](uint32_t word, int row) {
+                             const float ratio = rs[row] * inv;
+                             float d[4];
+                             if constexpr (HW) {
+                               hw_dec_e4m3x4(word, d);
+                             } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float f[4][4];    // [row][column]
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int row = 16 * rg + 4 * k + b;
-        const float ratio = p_rscale[oi][row] * inv;
-        const uint32_t word = p_code[oi][row * 33 + cg];
-        float d[4];
-        if constexpr (HW) {
-          hw_dec_e4m3x4(word, d);
-        } else {
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
-        }
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) f[b][c4] = d[c4] * ratio;
-      }
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = enc_e4m3x4<HW>(f[0][c4], f[1][c4], f[2][c4], f[3][c4]);
-    }
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4)
-      *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * o.ld_col + row0 + 16 * rg) =
-          make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
-    if (rg == 0) {
+                               for (int c4 = 0; c4 < 4; ++c4) d[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
+                             }
+                             return enc_e4m3x4_inrange<HW>(d[0] * ratio, d[1] * ratio, d[2] * ratio,
+                                                           d[3] * ratio);
+                           });
+    if ((tid & 7) == 0) {
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4)
         static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + ocol + 4 * cg + c4] = st;
@@ -216,129 +427,134 @@ __device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int6
   }
 }
 
-template <class Src, int KIND>
-__global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, int64_t rows) {
+// fp32 scale (amax / 448) with the 128x1 transposed output: the tile's values
+// stay in registers; column amaxes are reduced across the 8 row groups of a
+// wave by lane exchanges and across the 4 waves through LDS, each thread
+// quantises its own values with their column's scale, and only the e4m3 codes
+// pass through LDS (17 KiB).
+template <class Src, bool HW>
+__device__ __forceinline__ void block_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
+                                           int64_t col0, bool want_row) {
   constexpr int NOUT = Src::kOut;
-  constexpr bool HW = FM_HW_CVT != 0;
-  const int64_t col0 = int64_t(blockIdx.x) * 128;
-  const int64_t row0 = int64_t(blockIdx.y) * 128;
-  if (o.tile_valid != nullptr && o.tile_valid[blockIdx.y] < 0) return;
   const int tid = threadIdx.x;
-  const bool want_col = o.col_q != nullptr;
-  const bool want_row = o.row_q != nullptr;
-
-  // ---- phase 1: thread -> rows (tid/16) + 16*it, columns [8*(tid%16), +8).
-  // All 8 rows are fetched before any is computed, so their loads are in
-  // flight together; rows past the end re-read the last row and are zeroed by
-  // a select.
-  const int cpos = (tid & 15) * 8;
-  if constexpr (KIND == QK_POW2) {
-    pow2_tile<Src, HW>(src, o, rows, row0, col0, cpos, want_row, want_col);
-    return;
-  }
-  float vv[8][NOUT][8];
+  const int wave = tid >> 6, lane8 = tid & 7;
+  __shared__ __attribute__((aligned(16))) float b_red[4][128];
+  __shared__ __attribute__((aligned(16))) float b_sd[128];
+  __shared__ __attribute__((aligned(16))) float b_ny[128];
+  __shared__ __attribute__((aligned(16))) uint32_t b_code[128 * 33];
+  float vv[kRowsPerThread][NOUT][2][8];
   {
-    typename Src::Raw raw[8];
+    typename Src::Raw raw[kRowsPerThread][2];
+    fetch_rows(src, raw, rows, row0, col0);
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int64_t grow = row0 + (tid >> 4) + 16 * it;
-      raw[it] = src.fetch(grow < rows ? grow : rows - 1, col0 + cpos);
-    }
-#pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      src.compute(raw[it], vv[it]);
-      const bool ok = row0 + (tid >> 4) + 16 * it < rows;
-#pragma unroll
-      for (int q = 0; q < NOUT; ++q)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vv[it][q][i] = ok ? vv[it][q][i] : 0.f;
-    }
+    for (int it = 0; it < kRowsPerThread; ++it) compute_row(src, raw[it], vv[it]);
   }
+  const int rg = tid >> 3;
+#pragma unroll
+  for (int oi = 0; oi < NOUT; ++oi) {
+    const int64_t ocol = col0 + o.col_off[oi];
+    float cm[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cm[h][i] = 0.f;
+    RowPtr<QK_BLOCK> p(o, row0 + rg, ocol);
+#pragma unroll
+    for (int it = 0; it < kRowsPerThread; ++it) {
+      float sc;
+      row_quant<QK_BLOCK, HW>(vv[it][oi], p, want_row, sc);
+      p.next();
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cm[h][i] = fmaxf(cm[h][i], fabsf(vv[it][oi][h][i]));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cm[h][i] = max_across_rowgroups(cm[h][i]);
+    if (oi > 0) __syncthreads();  // the previous output's transposed reads are done
+    if ((tid & 63) < 8) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float* dst = &b_red[wave][64 * h + 8 * lane8];
+        *reinterpret_cast<float4*>(dst) = make_float4(cm[h][0], cm[h][1], cm[h][2], cm[h][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(cm[h][4], cm[h][5], cm[h][6], cm[h][7]);
+      }
+    }
+    __syncthreads();
+    if (tid < 128) {
+      const float m = fmaxf(fmaxf(b_red[0][tid], b_red[1][tid]), fmaxf(b_red[2][tid], b_red[3][tid]));
+      const float s = block_scale_dev(m, false);
+      const Recip d = recip_of(s);
+      b_sd[tid] = d.sd;
+      b_ny[tid] = d.ny;
+      static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + ocol + tid] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 64 * h + 8 * lane8;
+      const float4 s0 = *reinterpret_cast<const float4*>(&b_sd[c]);
+      const float4 s1 = *reinterpret_cast<const float4*>(&b_sd[c + 4]);
+      const float4 y0 = *reinterpret_cast<const float4*>(&b_ny[c]);
+      const float4 y1 = *reinterpret_cast<const float4*>(&b_ny[c + 4]);
+      const Recip d[8] = {{s0.x, y0.x}, {s0.y, y0.y}, {s0.z, y0.z}, {s0.w, y0.w},
+                          {s1.x, y1.x}, {s1.y, y1.y}, {s1.z, y1.z}, {s1.w, y1.w}};
+#pragma unroll
+      for (int it = 0; it < kRowsPerThread; ++it) {
+        const float* v = vv[it][oi][h];
+        const uint32_t w0 =
+            enc_e4m3x4<HW>(div_rn(v[0], d[0]), div_rn(v[1], d[1]), div_rn(v[2], d[2]), div_rn(v[3], d[3]));
+        const uint32_t w1 =
+            enc_e4m3x4<HW>(div_rn(v[4], d[4]), div_rn(v[5], d[5]), div_rn(v[6], d[6]), div_rn(v[7], d[7]));
+        *reinterpret_cast<uint2*>(&b_code[code_word(rg + 32 * it, h)]) = make_uint2(w0, w1);
+      }
+    }
+    __syncthreads();
+    store_transposed_codes(b_code, static_cast<uint8_t*>(o.col_q), o.ld_col, ocol, row0,
+                           [](uint32_t word, int) { return word; });
+  }
+}
 
-  // LDS for the transposed pass (one output at a time): fp32 values
-  __shared__ float red[256];
+// MX (32x1) and bf16 transposed outputs: fp32 values staged in LDS
+// [128][129] (66 KiB), one output at a time.
+template <class Src, int KIND, bool HW>
+__device__ __forceinline__ void staged_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
+                                            int64_t col0, bool want_row) {
+  constexpr int NOUT = Src::kOut;
+  const int tid = threadIdx.x;
+  float vv[kRowsPerThread][NOUT][2][8];
+  {
+    typename Src::Raw raw[kRowsPerThread][2];
+    fetch_rows(src, raw, rows, row0, col0);
+#pragma unroll
+    for (int it = 0; it < kRowsPerThread; ++it) compute_row(src, raw[it], vv[it]);
+  }
   __shared__ float lds_val[128 * kTileLdsPitch];
-
+  const int rg = tid >> 3, lane8 = tid & 7;
 #pragma unroll
   for (int oi = 0; oi < NOUT; ++oi) {
     const int64_t ocol = col0 + o.col_off[oi];  // output column of this tile
+    RowPtr<KIND> p(o, row0 + rg, ocol);
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int r = (tid >> 4) + 16 * it;
-      const int64_t grow = row0 + r;
-      const float* v = vv[it][oi];
-      float am = 0.f;
+    for (int it = 0; it < kRowsPerThread; ++it) {
+      const int r = rg + 32 * it;
+      float sc;
+      row_quant<KIND, HW>(vv[it][oi], p, want_row, sc);
+      p.next();
 #pragma unroll
-      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-      if (KIND == QK_BLOCK) {
-        const float s = block_scale(group_max16(am), false);
-        const float y = 1.0f / s;
-        const uint32_t w0 = enc_e4m3x4<HW>(div_rn(v[0], s, y), div_rn(v[1], s, y), div_rn(v[2], s, y),
-                                           div_rn(v[3], s, y));
-        const uint32_t w1 = enc_e4m3x4<HW>(div_rn(v[4], s, y), div_rn(v[5], s, y), div_rn(v[6], s, y),
-                                           div_rn(v[7], s, y));
-        if (want_row && grow < rows) {
-          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
-              make_uint2(w0, w1);
-          if ((tid & 15) == 0) static_cast<float*>(o.row_s)[grow * o.rs_row + (ocol >> 7) * o.rs_kb] = s;
-        }
-        if (want_col) {
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
-        }
-      } else if (KIND == QK_MX) {
-        const uint32_t code = mx_code(group_max4(am));
-        const float inv = mx_inv_scale(code);
-        const uint32_t w0 = enc_e4m3x4<HW>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-        const uint32_t w1 = enc_e4m3x4<HW>(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-        if (want_row && grow < rows) {
-          *reinterpret_cast<uint2*>(static_cast<uint8_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) =
-              make_uint2(w0, w1);
-          if ((tid & 3) == 0)
-            static_cast<uint8_t*>(o.row_s)[grow * o.rs_row + ((ocol + cpos) >> 5) * o.rs_kb] = uint8_t(code);
-        }
-        if (want_col) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
-        }
-      } else {  // bf16
-        if (want_row && grow < rows) {
-          const uint4 pk = make_uint4(enc_bf16x2<HW>(v[0], v[1]), enc_bf16x2<HW>(v[2], v[3]),
-                                      enc_bf16x2<HW>(v[4], v[5]), enc_bf16x2<HW>(v[6], v[7]));
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(o.row_q) + grow * o.ld_row + ocol + cpos) = pk;
-        }
-        if (want_col) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + cpos + i] = v[i];
-        }
-      }
+        for (int i = 0; i < 8; ++i) lds_val[r * kTileLdsPitch + 64 * h + 8 * lane8 + i] = vv[it][oi][h][i];
     }
-    if (!want_col) continue;
     __syncthreads();
 
-    // ---- phase 2: thread -> column c = tid % 128, rows [64*h, 64*h + 64)
+    // thread -> column c = tid % 128, rows [64*h, 64*h + 64)
     const int c = tid & 127, h = tid >> 7;
     const int64_t gcol = ocol + c;
-    uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
-    if (KIND == QK_BLOCK) {
-      float am = 0.f;
-      for (int r = 0; r < 64; ++r) am = fmaxf(am, fabsf(lds_val[(64 * h + r) * kTileLdsPitch + c]));
-      red[h * 128 + c] = am;
-      __syncthreads();
-      const float s = block_scale(fmaxf(red[c], red[128 + c]), false);
-      const float y = 1.0f / s;
-      for (int r16 = 0; r16 < 64; r16 += 16) {
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float* p = &lds_val[(64 * h + r16 + 4 * k) * kTileLdsPitch + c];
-          w[k] = enc_e4m3x4<HW>(div_rn(p[0], s, y), div_rn(p[kTileLdsPitch], s, y),
-                                div_rn(p[2 * kTileLdsPitch], s, y), div_rn(p[3 * kTileLdsPitch], s, y));
-        }
-        *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + 64 * h + r16) = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-      if (h == 0) static_cast<float*>(o.col_s)[(row0 >> 7) * o.ld_col_s + gcol] = s;
-    } else if (KIND == QK_MX) {
+    if constexpr (KIND == QK_MX) {
+      uint8_t* qt8 = static_cast<uint8_t*>(o.col_q);
       for (int b = 0; b < 2; ++b) {  // two 32-row MX blocks per thread
         const int rb = 64 * h + 32 * b;
         float m = 0.f;
@@ -349,9 +565,9 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
           uint32_t w[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const float* p = &lds_val[(rb + r16 + 4 * k) * kTileLdsPitch + c];
-            w[k] = enc_e4m3x4<HW>(p[0] * inv, p[kTileLdsPitch] * inv, p[2 * kTileLdsPitch] * inv,
-                                  p[3 * kTileLdsPitch] * inv);
+            const float* pv = &lds_val[(rb + r16 + 4 * k) * kTileLdsPitch + c];
+            w[k] = enc_e4m3x4<HW>(pv[0] * inv, pv[kTileLdsPitch] * inv, pv[2 * kTileLdsPitch] * inv,
+                                  pv[3 * kTileLdsPitch] * inv);
           }
           *reinterpret_cast<uint4*>(qt8 + gcol * o.ld_col + row0 + rb + r16) = make_uint4(w[0], w[1], w[2], w[3]);
         }
@@ -360,15 +576,43 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src, TileOut o, 
     } else {  // bf16 transpose
       uint16_t* qt16 = static_cast<uint16_t*>(o.col_q);
       for (int r8 = 0; r8 < 64; r8 += 8) {
-        const float* p = &lds_val[(64 * h + r8) * kTileLdsPitch + c];
-        const uint4 pk = make_uint4(enc_bf16x2<HW>(p[0], p[kTileLdsPitch]),
-                                    enc_bf16x2<HW>(p[2 * kTileLdsPitch], p[3 * kTileLdsPitch]),
-                                    enc_bf16x2<HW>(p[4 * kTileLdsPitch], p[5 * kTileLdsPitch]),
-                                    enc_bf16x2<HW>(p[6 * kTileLdsPitch], p[7 * kTileLdsPitch]));
+        const float* pv = &lds_val[(64 * h + r8) * kTileLdsPitch + c];
+        const uint4 pk = make_uint4(enc_bf16x2<HW>(pv[0], pv[kTileLdsPitch]),
+                                    enc_bf16x2<HW>(pv[2 * kTileLdsPitch], pv[3 * kTileLdsPitch]),
+                                    enc_bf16x2<HW>(pv[4 * kTileLdsPitch], pv[5 * kTileLdsPitch]),
+                                    enc_bf16x2<HW>(pv[6 * kTileLdsPitch], pv[7 * kTileLdsPitch]));
         *reinterpret_cast<uint4*>(qt16 + gcol * o.ld_col + row0 + 64 * h + r8) = pk;
       }
     }
     if (oi + 1 < NOUT) __syncthreads();  // LDS is reused by the next output
+  }
+}
+
+// Per-tile view of a source: a source whose row -> address map is cheaper to
+// resolve once per 128-row tile overloads this (found by argument-dependent
+// lookup where the tile producer is instantiated).
+template <class Src>
+__device__ __forceinline__ Src tile_source(const Src& src, int64_t) {
+  return src;
+}
+
+// One workgroup per 128x128 tile.  COL: the transposed output is wanted
+// (a separate instantiation, so a row-only launch allocates no LDS).
+template <class Src, int KIND, bool COL>
+__global__ __launch_bounds__(256) void tile_producer_kernel(Src src_all, TileOut o, int64_t rows) {
+  constexpr bool HW = FM_HW_CVT != 0;
+  const int64_t col0 = int64_t(blockIdx.x) * 128;
+  const int64_t row0 = int64_t(blockIdx.y) * 128;
+  if (o.tile_valid != nullptr && o.tile_valid[blockIdx.y] < 0) return;
+  const Src src = tile_source(src_all, row0);
+  if constexpr (!COL) {
+    rows_tile<Src, KIND, HW>(src, o, rows, row0, col0);
+  } else {
+    // the transposed output requires rows % 128 == 0: every row is in range
+    const bool want_row = o.row_q != nullptr;
+    if constexpr (KIND == QK_POW2) pow2_tile<Src, HW>(src, o, rows, row0, col0, want_row);
+    else if constexpr (KIND == QK_BLOCK) block_tile<Src, HW>(src, o, rows, row0, col0, want_row);
+    else staged_tile<Src, KIND, HW>(src, o, rows, row0, col0, want_row);
   }
 }
 
@@ -422,12 +666,17 @@ int launch_tile_producer(const Src& src, const TileOut& o, int64_t rows, int64_t
   if (int rc = check_tile_out(o, rows, cols, Src::kOut)) return rc;
   if (rows == 0) return 0;
   dim3 grid(unsigned(cols / 128), unsigned((rows + 127) / 128));
+  const bool col = o.col_q != nullptr;
+#define FM_TILE_LAUNCH(K)                                                                                    \
+  if (col) hipLaunchKernelGGL((tile_producer_kernel<Src, K, true>), grid, dim3(256), 0, stream, src, o, rows); \
+  else hipLaunchKernelGGL((tile_producer_kernel<Src, K, false>), grid, dim3(256), 0, stream, src, o, rows);
   switch (o.kind) {
-    case QK_BF16: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_BF16>), grid, dim3(256), 0, stream, src, o, rows); break;
-    case QK_BLOCK: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_BLOCK>), grid, dim3(256), 0, stream, src, o, rows); break;
-    case QK_POW2: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_POW2>), grid, dim3(256), 0, stream, src, o, rows); break;
-    default: hipLaunchKernelGGL((tile_producer_kernel<Src, QK_MX>), grid, dim3(256), 0, stream, src, o, rows); break;
+    case QK_BF16: FM_TILE_LAUNCH(QK_BF16) break;
+    case QK_BLOCK: FM_TILE_LAUNCH(QK_BLOCK) break;
+    case QK_POW2: FM_TILE_LAUNCH(QK_POW2) break;
+    default: FM_TILE_LAUNCH(QK_MX) break;
   }
+#undef FM_TILE_LAUNCH
   return check_launch(what);
 }
 
