@@ -172,8 +172,8 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
     float f[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) f[j] = pow2 ? v[i][j] * inv : div_rn(v[i][j], d);
-    const uint32_t w0 = enc_e4m3x4<HW>(f[0], f[1], f[2], f[3]);
-    const uint32_t w1 = enc_e4m3x4<HW>(f[4], f[5], f[6], f[7]);
+    const uint32_t w0 = enc_e4m3x4_inrange<HW>(f[0], f[1], f[2], f[3]);
+    const uint32_t w1 = enc_e4m3x4_inrange<HW>(f[4], f[5], f[6], f[7]);
     if (a.q)
       *reinterpret_cast<uint2*>(a.q + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
           make_uint2(w0, w1);
@@ -217,59 +217,71 @@ struct DequantArgs {
   int64_t ld_out;
 };
 
-// grid (column chunks, rows): thread -> CW consecutive columns of rows
-// blockIdx.y, blockIdx.y + gridDim.y, ...; the CW columns share one scale
-// (CW <= the block width).
+// grid (column chunks, row groups): thread -> CW consecutive columns of the
+// kDequantRows rows of each row group blockIdx.y, blockIdx.y + gridDim.y, ...;
+// the CW columns share one scale (CW <= the block width).  A group's loads
+// (payload and scales) are all issued before any row is converted.
+constexpr int kDequantRows = 4;
 template <int CW>
 __global__ __launch_bounds__(256) void dequant_kernel(DequantArgs a) {
   constexpr bool HW = FM_HW_CVT != 0;
+  constexpr int RPT = kDequantRows;
   const int64_t c = (int64_t(blockIdx.x) * 256 + threadIdx.x) * CW;
   if (c >= a.cols) return;
-  for (int64_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
-    uint32_t wd[CW / 4];
-    if constexpr (CW == 16) {
-      const uint4 pk = *reinterpret_cast<const uint4*>(a.q + r * a.ld_q + c);
-      wd[0] = pk.x; wd[1] = pk.y; wd[2] = pk.z; wd[3] = pk.w;
-    } else {
-      const uint2 pk = *reinterpret_cast<const uint2*>(a.q + r * a.ld_q + c);
-      wd[0] = pk.x; wd[1] = pk.y;
-    }
-    const int64_t si = (r >> a.row_shift) * a.s_row_stride + (c >> a.col_shift) * a.s_col_stride;
-    const float sc = a.s_e8m0 ? e8m0_to_f32(static_cast<const uint8_t*>(a.s)[si])
-                              : static_cast<const float*>(a.s)[si];
-    float v[CW];
+  for (int64_t rb = int64_t(blockIdx.y) * RPT; rb < a.rows; rb += int64_t(gridDim.y) * RPT) {
+    uint32_t wd[RPT][CW / 4];
+    float sc[RPT];
 #pragma unroll
-    for (int i = 0; i < CW / 4; ++i) {
-      if constexpr (HW) {
-        hw_dec_e4m3x4(wd[i], &v[4 * i]);
+    for (int j = 0; j < RPT; ++j) {
+      const int64_t r = rb + j < a.rows ? rb + j : a.rows - 1;
+      if constexpr (CW == 16) {
+        const uint4 pk = *reinterpret_cast<const uint4*>(a.q + r * a.ld_q + c);
+        wd[j][0] = pk.x; wd[j][1] = pk.y; wd[j][2] = pk.z; wd[j][3] = pk.w;
       } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[4 * i + j] = e4m3_to_f32(uint8_t(wd[i] >> (8 * j)));
+        const uint2 pk = *reinterpret_cast<const uint2*>(a.q + r * a.ld_q + c);
+        wd[j][0] = pk.x; wd[j][1] = pk.y;
       }
+      const int64_t si = (r >> a.row_shift) * a.s_row_stride + (c >> a.col_shift) * a.s_col_stride;
+      sc[j] = a.s_e8m0 ? e8m0_to_f32(static_cast<const uint8_t*>(a.s)[si]) : static_cast<const float*>(a.s)[si];
     }
 #pragma unroll
-    for (int i = 0; i < CW; ++i) v[i] *= sc;
-    if (a.out_f32) {
-      float* o = static_cast<float*>(a.out) + r * a.ld_out + c;
+    for (int j = 0; j < RPT; ++j) {
+      const int64_t r = rb + j;
+      if (r >= a.rows) break;
+      float v[CW];
 #pragma unroll
-      for (int i = 0; i < CW / 4; ++i)
-        reinterpret_cast<float4*>(o)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-    } else {
-      uint32_t b[CW / 2];
+      for (int i = 0; i < CW / 4; ++i) {
+        if constexpr (HW) {
+          hw_dec_e4m3x4(wd[j][i], &v[4 * i]);
+        } else {
 #pragma unroll
-      for (int i = 0; i < CW / 2; ++i)
-        b[i] = HW ? hw_bf16x2(v[2 * i], v[2 * i + 1])
-                  : uint32_t(f32_to_bf16(v[2 * i])) | (uint32_t(f32_to_bf16(v[2 * i + 1])) << 16);
-      uint4* o = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + r * a.ld_out + c);
+          for (int k = 0; k < 4; ++k) v[4 * i + k] = e4m3_to_f32(uint8_t(wd[j][i] >> (8 * k)));
+        }
+      }
 #pragma unroll
-      for (int i = 0; i < CW / 8; ++i) o[i] = make_uint4(b[4 * i], b[4 * i + 1], b[4 * i + 2], b[4 * i + 3]);
+      for (int i = 0; i < CW; ++i) v[i] *= sc[j];
+      if (a.out_f32) {
+        float* o = static_cast<float*>(a.out) + r * a.ld_out + c;
+#pragma unroll
+        for (int i = 0; i < CW / 4; ++i)
+          reinterpret_cast<float4*>(o)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+      } else {
+        uint32_t b[CW / 2];
+#pragma unroll
+        for (int i = 0; i < CW / 2; ++i)
+          b[i] = HW ? hw_bf16x2(v[2 * i], v[2 * i + 1])
+                    : uint32_t(f32_to_bf16(v[2 * i])) | (uint32_t(f32_to_bf16(v[2 * i + 1])) << 16);
+        uint4* o = reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + r * a.ld_out + c);
+#pragma unroll
+        for (int i = 0; i < CW / 8; ++i) o[i] = make_uint4(b[4 * i], b[4 * i + 1], b[4 * i + 2], b[4 * i + 3]);
+      }
     }
   }
 }
 
 // --------------------------------------------------- scaling-aware transpose ----
 // grid (C/128, R/128).  Column-block scale = largest row scale of the tile;
-// qt[c][r] = e4m3(clamp(fp32(decode(q[r][c]) * s[r][c/128]) / st)).
+// qt[c][r] = e4m3(fp32(decode(q[r][c]) * s[r][c/128]) / st).
 __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q, const float* s,
                                                   int64_t ld_s, uint8_t* qt, int64_t ld_qt,
                                                   float* st, int64_t ld_st) {
@@ -279,20 +291,21 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
   constexpr bool HW = FM_HW_CVT != 0;
   const int tid = threadIdx.x;
   const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
-  // load 128x128 bytes: thread -> 16 bytes x 4 rows
+  // load 128x128 bytes: thread -> 16 bytes of rows rr + 32 i (i < 4)
   const int cc = (tid & 7) * 16;
-  const int rr = tid >> 3;  // rows rr + 32*i
+  const int rr = tid >> 3;
+  uint4 pk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pk[i] = *reinterpret_cast<const uint4*>(q + (r0 + rr + 32 * i) * ld_q + c0 + cc);
+  if (tid < 128) rs[tid] = s[(r0 + tid) * ld_s + (c0 >> 7)];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = rr + 32 * i;
-    const uint4 pk = *reinterpret_cast<const uint4*>(q + (r0 + row) * ld_q + c0 + cc);
-    uint32_t* t = &tile[row * 33 + (cc >> 2)];
-    t[0] = pk.x;
-    t[1] = pk.y;
-    t[2] = pk.z;
-    t[3] = pk.w;
+    uint32_t* t = &tile[code_idx(rr + 32 * i, cc >> 2)];
+    t[0] = pk[i].x;
+    t[1] = pk[i].y;
+    t[2] = pk[i].z;
+    t[3] = pk[i].w;
   }
-  if (tid < 128) rs[tid] = s[(r0 + tid) * ld_s + (c0 >> 7)];
   __syncthreads();
   if (tid < 64) {
     float m = fmaxf(rs[tid], rs[tid + 64]);
@@ -312,11 +325,12 @@ __global__ __launch_bounds__(256) void sat_kernel(const uint8_t* q, int64_t ld_q
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) f[c4] = e4m3_to_f32(uint8_t(word >> (8 * c4)));
     }
-    return enc_e4m3x4<HW>(div_rn(f[0] * srow, d), div_rn(f[1] * srow, d), div_rn(f[2] * srow, d),
-                          div_rn(f[3] * srow, d));
+    // |decode(q) s_row| <= 448 s_row (1 + 2^-24) and s_col >= s_row: within 464
+    return enc_e4m3x4_inrange<HW>(div_rn(f[0] * srow, d), div_rn(f[1] * srow, d), div_rn(f[2] * srow, d),
+                                  div_rn(f[3] * srow, d));
   });
-  const int rg = tid & 7, cg = tid >> 3;
-  if (rg == 0) {
+  if ((tid & 7) == 0) {
+    const int cg = tid >> 3;
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) st[(r0 >> 7) * ld_st + c0 + 4 * cg + c4] = sc;
   }
@@ -471,7 +485,8 @@ int fm_dequantize(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
   const bool wide = col_shift >= 4 && cols % 16 == 0 && ld_q % 16 == 0 && ld_out % 8 == 0 &&
                     (reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const int cw = wide ? 16 : 8;
-  const dim3 grid(unsigned((cols / cw + 255) / 256), unsigned(rows < 65535 ? rows : 65535));
+  const int64_t groups = (rows + kDequantRows - 1) / kDequantRows;
+  const dim3 grid(unsigned((cols / cw + 255) / 256), unsigned(groups < 65535 ? groups : 65535));
   if (wide)
     hipLaunchKernelGGL(dequant_kernel<16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   else

@@ -73,8 +73,12 @@ __device__ __forceinline__ uint32_t enc_bf16x2(float a, float b) {
   else return uint32_t(f32_to_bf16(a)) | (uint32_t(f32_to_bf16(b)) << 16);
 }
 
-// e4m3 of four values already within +-448 (no clamp): power-of-two scaled
-// values, whose magnitude is at most 448 exactly.
+// e4m3 of four values of magnitude at most 464, without a clamp: both
+// conversions round to nearest-even and give NaN only above 464 (the OCP
+// non-saturating rule), so such values encode as if clamped to +-448.  Block
+// quantisers produce them: a power-of-two scale bounds |x / s| by 448 exactly,
+// an fp32 scale RN(amax / 448) by 448 (1 + 2^-24) before rounding.  MX scales
+// (e8m0 from the amax exponent) allow up to 512 and keep the clamp.
 template <bool HW>
 __device__ __forceinline__ uint32_t enc_e4m3x4_inrange(float a, float b, float c, float d) {
   if constexpr (HW) {
@@ -234,9 +238,10 @@ __device__ __forceinline__ uint4 row_quant(const float (&v)[2][8], const RowPtr<
       const Recip d = recip_of(sc);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        w[2 * h] = enc_e4m3x4<HW>(div_rn(v[h][0], d), div_rn(v[h][1], d), div_rn(v[h][2], d), div_rn(v[h][3], d));
-        w[2 * h + 1] =
-            enc_e4m3x4<HW>(div_rn(v[h][4], d), div_rn(v[h][5], d), div_rn(v[h][6], d), div_rn(v[h][7], d));
+        w[2 * h] = enc_e4m3x4_inrange<HW>(div_rn(v[h][0], d), div_rn(v[h][1], d), div_rn(v[h][2], d),
+                                          div_rn(v[h][3], d));
+        w[2 * h + 1] = enc_e4m3x4_inrange<HW>(div_rn(v[h][4], d), div_rn(v[h][5], d), div_rn(v[h][6], d),
+                                              div_rn(v[h][7], d));
       }
     }
     if (store && lane8 == 0) *reinterpret_cast<float*>(p.s) = sc;
@@ -298,8 +303,15 @@ __device__ __forceinline__ void transpose4x4_bytes(const uint32_t (&in)[4], uint
   out[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
+// Word index of columns [4 cw, 4 cw + 4) of row `row` in a [128][33]-word
+// LDS code tile.  The transposed reader below has lanes (rg, cg) read rows
+// 16 rg + j; XOR-ing the word column with 8 in rows 64..127 puts its 64 lanes
+// on 64 distinct banks (gfx950 LDS: 64 banks of 4 bytes; rows 64 apart would
+// otherwise share one).  Groups of 4 aligned words stay together.
+__device__ __forceinline__ int code_idx(int row, int cw) { return row * 33 + (cw ^ (8 * ((row >> 6) & 1))); }
+
 // Transposed store of a 128x128 e4m3 tile staged in LDS as code words
-// (code[row * 33 + c / 4] holds columns [c, c+4) of a row): thread -> columns
+// (code[code_idx(row, c / 4)] holds columns [c, c+4) of a row): thread -> columns
 // [4 cg, +4) x rows [16 rg, +16); the 8 lanes of one cg write a whole
 // 128-byte row of the transpose.  `tx` maps the four codes of one word (one
 // row, four columns) to their values in the transposed output; the identity
@@ -316,7 +328,7 @@ __device__ __forceinline__ void store_transposed_codes(const uint32_t* code, uin
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int row = 16 * rg + 4 * k + b;
-      in[b] = tx(code[row * 33 + cg], row);
+      in[b] = tx(code[code_idx(row, cg)], row);
     }
     transpose4x4_bytes(in, out);
 #pragma unroll
@@ -328,8 +340,8 @@ __device__ __forceinline__ void store_transposed_codes(const uint32_t* code, uin
         make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
 }
 
-// LDS word index of segment h of row r in a [128][33]-word code tile
-__device__ __forceinline__ int code_word(int r, int h) { return r * 33 + 16 * h + 2 * (threadIdx.x & 7); }
+// LDS word index of segment h of row r (this thread's two words) in a code tile
+__device__ __forceinline__ int code_word(int r, int h) { return code_idx(r, 16 * h + 2 * (threadIdx.x & 7)); }
 
 // Row output only: each row is quantised as soon as it is computed; no LDS.
 template <class Src, int KIND, bool HW>
@@ -504,10 +516,10 @@ __device__ __forceinline__ void block_tile(const Src& src, const TileOut& o, int
 #pragma unroll
       for (int it = 0; it < kRowsPerThread; ++it) {
         const float* v = vv[it][oi][h];
-        const uint32_t w0 =
-            enc_e4m3x4<HW>(div_rn(v[0], d[0]), div_rn(v[1], d[1]), div_rn(v[2], d[2]), div_rn(v[3], d[3]));
-        const uint32_t w1 =
-            enc_e4m3x4<HW>(div_rn(v[4], d[4]), div_rn(v[5], d[5]), div_rn(v[6], d[6]), div_rn(v[7], d[7]));
+        const uint32_t w0 = enc_e4m3x4_inrange<HW>(div_rn(v[0], d[0]), div_rn(v[1], d[1]), div_rn(v[2], d[2]),
+                                                   div_rn(v[3], d[3]));
+        const uint32_t w1 = enc_e4m3x4_inrange<HW>(div_rn(v[4], d[4]), div_rn(v[5], d[5]), div_rn(v[6], d[6]),
+                                                   div_rn(v[7], d[7]));
         *reinterpret_cast<uint2*>(&b_code[code_word(rg + 32 * it, h)]) = make_uint2(w0, w1);
       }
     }
