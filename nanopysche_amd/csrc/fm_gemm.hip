@@ -113,14 +113,36 @@ __device__ __forceinline__ void dma4a(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* g, const void* lds) { dma4a(g, lds_addr(lds)); }
-// Scalar-base form: wave-uniform 64-bit base `g` plus a 32-bit per-lane offset,
-// into LDS byte address `lds` (wave-uniform).
-__device__ __forceinline__ void dma16s(const uint8_t* g, uint32_t voff, uint32_t lds) {
+// Buffer-resource form, the 256 x 256 kernel's path: a raw-buffer descriptor
+// of a wave-uniform base (the wave's first row of the tile), a 32-bit
+// per-lane offset and a 32-bit uniform offset (group + K position), so no
+// 64-bit address arithmetic is spent per load.  Measured on gfx950 it moves
+// the tile's 64 KiB per K step at the same rate as the flat form.
+// byte address = base + voff + soff.
+__device__ __forceinline__ void bdma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(g), "s"(m)
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+               "s"(m)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void bdma4(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+               "s"(m)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// Raw-buffer descriptor (stride 0, no range clipping) of a wave-uniform base.
+__device__ __forceinline__ v4i make_rsrc(const void* base) {
+  const uint64_t a = uint64_t(size_t(base));
+  v4i r;
+  r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xffffu));
+  r[2] = -1;
+  r[3] = 0x00020000;   // gfx9 raw buffer: 32-bit data format, no swizzle
+  return r;
+}
 
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits [3:0] and [15:14],
 // expcnt [6:4] left at its maximum, lgkmcnt [11:8]).  Draining lgkmcnt too
@@ -158,17 +180,17 @@ struct Smem256 {
 // the end re-reads the last valid 32 rows into its own LDS rows, which only
 // feed outputs that are never stored.
 struct OpStream {
-  const uint8_t* base;    // this wave's first row group at K offset 0 (wave-uniform)
-  int64_t group_bytes;    // 8 rows
+  v4i rsrc;               // descriptor of this wave's first row group at K offset 0
+  uint32_t group_bytes;   // 8 rows
   uint32_t lane_off[2];   // even / odd group
 };
 
 __device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows, int lane,
                                                 int wave) {
   OpStream s;
-  s.group_bytes = 8 * row_bytes;
+  s.group_bytes = uint32_t(8 * row_bytes);
   const int last = int(rows / 32) - 1;
-  s.base = base + int64_t(wave < last ? wave : last) * 4 * s.group_bytes;
+  s.rsrc = make_rsrc(base + int64_t(wave < last ? wave : last) * 32 * row_bytes);
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     const int ch = (lane & 7) ^ ((par * 4 + (lane >> 4)) & 7);  // == chunk ^ lds_swz(row)
@@ -213,6 +235,39 @@ __device__ __forceinline__ int read_mx_scale(const uint8_t* st, int off, int r, 
   return mx_k ? st[off + blk * kT + r] : st[off + r * 4 + blk];
 }
 
+// Per-lane scale source of one operand: descriptor of the operand's scales
+// (group base, wave-uniform), this lane's byte offset at K offset 0, byte
+// advance per K step, LDS byte offset of the slot.  fp32 / pow2 and row-major
+// MX: one row per slot (pow2 slots permuted, see scale_row_slot); MX in
+// k-major layout: four consecutive rows of one 32-block per slot ([block][row]
+// bytes in LDS).  Rows past the valid ones re-read the last one.
+struct ScaleSrc {
+  v4i rsrc;
+  uint32_t voff;
+  int64_t k;
+  int dst;
+};
+
+template <int KIND>
+__device__ __forceinline__ ScaleSrc make_scale_src(const Operand& o, int64_t r0, int64_t rows, int64_t og,
+                                                   bool mx_k, int li, int lds_base) {
+  ScaleSrc s;
+  const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
+  s.rsrc = make_rsrc(static_cast<const uint8_t*>(o.s) + og * o.s_gs * sbytes);
+  if (mx_k) {
+    int64_t gr = r0 + (li * 4) % kT;
+    gr = gr + 4 <= r0 + rows ? gr : r0 + rows - 4;
+    s.voff = uint32_t(gr * o.s_row + (li / 64) * o.s_kb);
+  } else {
+    const int lr = KIND == GK_FP8_POW2 ? scale_row_slot(li) : li;
+    const int64_t gr = r0 + (lr < rows ? lr : rows - 1);
+    s.voff = uint32_t((gr >> o.s_shift) * o.s_row * sbytes);
+  }
+  s.k = (KIND == GK_FP8_MX ? 4 : 1) * o.s_kb * sbytes;
+  s.dst = lds_base + li * 4;
+  return s;
+}
+
 // Waves as 2 (i) x 4 (j), each 128 x 64 = 4 x 2 MFMA blocks (128 accumulator
 // registers), so two waves share each SIMD: while one waits on LDS reads or
 // the per-step barrier the other keeps the matrix pipe busy.  Each wave
@@ -238,18 +293,18 @@ struct WaveCoord {
 // One K step of DMA for this wave: 4 row groups of each operand, then one
 // scale dword per lane (waves 0-3: Q scale slots, 4-7: P scale slots).
 template <int KIND>
-__device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const uint8_t* sc,
-                                       int64_t sc_k, int sc_dst, int64_t k, uint32_t dst, int wave) {
+__device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc, int64_t k,
+                                           uint32_t dst, int wave) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
-  const int64_t kb = k * ES;
+  const uint32_t kb = uint32_t(k * ES);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    dma16s(qst.base + (u * qst.group_bytes + kb), qst.lane_off[u & 1], dst + (wave * 4 + u) * 1024);
-    dma16s(pst.base + (u * pst.group_bytes + kb), pst.lane_off[u & 1], dst + SM::kP + (wave * 4 + u) * 1024);
+    bdma16(qst.rsrc, qst.lane_off[u & 1], u * qst.group_bytes + kb, dst + (wave * 4 + u) * 1024);
+    bdma16(pst.rsrc, pst.lane_off[u & 1], u * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + u) * 1024);
   }
-  if constexpr (KIND != GK_BF16) dma4a(sc + (k / KSTEP) * sc_k, dst + sc_dst);
+  if constexpr (KIND != GK_BF16) bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
 }
 
 // Reads half `half` of the K step in stage `st` (pow2 scales only for half 0:
@@ -334,23 +389,21 @@ __device__ __forceinline__ void interleave_half() {
   }
 }
 
-// MXL (MX only): scale layouts, bit 0 = Q scales k-major, bit 1 = P scales
-// k-major (row-major otherwise); fixed per instantiation so the unused
-// address path costs no registers.
-template <int KIND, int MODE, int MXL = 0>
-__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
-  using SM = Smem256<KIND>;
-  constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
-  constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
+// A 256 x 256 workgroup tile: expert, first weight row i0, first token (or
+// m) row j0, end of the valid j rows, and the contraction range.
+struct Tile256 {
+  int64_t e, i0, j0, j_end, k_lo, k_hi;
+};
 
-  // ---------------------------------------------------------- tile decode ----
-  // ragged-M: the valid 256-token tiles (sum over experts of ceil(rows / 256),
-  // from the device-side offsets; the launch is sized by a host bound) are
-  // split into 8 contiguous ranges, one per XCD (blockIdx % 8), for L2 reuse.
-  // ragged-K: tiles in launch order, so one expert's tiles (whose K lengths
-  // differ between experts) spread over every XCD and the hardware's dynamic
-  // workgroup dispatch balances them.
+// ragged-M: the valid 256-token tiles (sum over experts of ceil(rows / 256),
+// from the device-side offsets; the launch is sized by a host bound) are
+// split into 8 contiguous ranges, one per XCD (blockIdx % 8), for L2 reuse.
+// ragged-K: tiles in launch order, so one expert's tiles (whose K lengths
+// differ between experts) spread over every XCD and the hardware's dynamic
+// workgroup dispatch balances them.  Returns false when this workgroup has no
+// tile.
+template <int MODE>
+__device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) {
   const int64_t NI = (p.n_i + kT - 1) / kT;
   int64_t JT = 0, L;
   // Experts masked out (the other precision's launch) own no tiles here, so
@@ -362,20 +415,20 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
     const int64_t n_valid = JT * NI;
     const int64_t per_xcd = (n_valid + 7) / 8;
     const int64_t k = blockIdx.x / 8;
-    if (k >= per_xcd) return;
+    if (k >= per_xcd) return false;
     L = int64_t(blockIdx.x % 8) * per_xcd + k;
-    if (L >= n_valid) return;
+    if (L >= n_valid) return false;
   } else {
     L = blockIdx.x;
-    if (L >= p.n_tiles) return;
+    if (L >= p.n_tiles) return false;
   }
-  int64_t e = -1, i0 = 0, j0 = 0, j_end = 0, k_lo, k_hi;
+  int64_t e = -1;
   if (MODE == GM_RAGGED_M) {
     const int64_t group = L / (kGroupM * NI);
     const int64_t first = group * kGroupM;
     const int64_t gsz = JT - first < kGroupM ? JT - first : kGroupM;
     int64_t J = first + (L % gsz);
-    i0 = ((L % (kGroupM * NI)) / gsz) * kT;
+    t.i0 = ((L % (kGroupM * NI)) / gsz) * kT;
     // token tile J -> (expert, rows): an unmasked expert x holds
     // ceil(rows_x / 256) tiles
     for (int x = 0; x < p.E; ++x) {
@@ -383,15 +436,15 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
       const int64_t cnt = unmasked(x) ? (o1 - o0 + kT - 1) / kT : 0;
       if (J < cnt) {
         e = x;
-        j0 = o0 + J * kT;
-        j_end = o1;
+        t.j0 = o0 + J * kT;
+        t.j_end = o1;
         break;
       }
       J -= cnt;
     }
-    if (e < 0) return;
-    k_lo = 0;
-    k_hi = p.K;
+    if (e < 0) return false;
+    t.k_lo = 0;
+    t.k_hi = p.K;
   } else {
     const int64_t NJ = (p.n_j + kT - 1) / kT;
     const int64_t per_e = NI * NJ;
@@ -400,13 +453,30 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
     const int64_t group = Lr / (kGroupM * NJ);
     const int64_t first = group * kGroupM;
     const int64_t gsz = NI - first < kGroupM ? NI - first : kGroupM;
-    i0 = (first + (Lr % gsz)) * kT;
-    j0 = ((Lr % (kGroupM * NJ)) / gsz) * kT;
-    j_end = p.n_j;
-    k_lo = p.offsets[e];
-    k_hi = p.offsets[e + 1];
+    t.i0 = (first + (Lr % gsz)) * kT;
+    t.j0 = ((Lr % (kGroupM * NJ)) / gsz) * kT;
+    t.j_end = p.n_j;
+    t.k_lo = p.offsets[e];
+    t.k_hi = p.offsets[e + 1];
   }
-  if (p.mask != nullptr && p.mask[e] != p.mask_want) return;
+  if (p.mask != nullptr && p.mask[e] != p.mask_want) return false;
+  t.e = e;
+  return true;
+}
+
+// MXL (MX only): scale layouts, bit 0 = Q scales k-major, bit 1 = P scales
+// k-major (row-major otherwise); fixed per instantiation so the unused
+// address path costs no registers.
+template <int KIND, int MODE, int MXL = 0>
+__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
+  constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
+
+  Tile256 tile;
+  if (!decode_tile256<MODE>(p, tile)) return;
+  const int64_t e = tile.e, i0 = tile.i0, j0 = tile.j0, j_end = tile.j_end, k_lo = tile.k_lo, k_hi = tile.k_hi;
 
   WaveCoord w;
   w.lane = threadIdx.x & 63;
@@ -427,33 +497,13 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   const OpStream pst = make_stream(p.P.p + j0 * p.P.ld * ES, p.P.ld * ES, p_rows, w.lane, w.wave);
 
   // Scales: waves 0-3 fetch the Q scale slots, waves 4-7 the P slots, one
-  // dword per lane per K step.  fp32 / pow2 and row-major MX: one row per slot
-  // (pow2 slots permuted, see scale_row_slot); MX in k-major layout: four
-  // consecutive rows of one 32-block per slot ([block][row] bytes in LDS).
-  // Rows past the valid ones re-read the last one.
-  const uint8_t* sc = nullptr;
-  int64_t sc_k = 0;
-  int sc_dst = 0;
+  // dword per lane per K step.
+  ScaleSrc sc{};
   if constexpr (SM::kScaled) {
     const bool is_q = w.wave < 4;
-    const Operand& o = is_q ? p.Q : p.P;
-    const int64_t r0 = is_q ? i0 : j0;
-    const int64_t rows = is_q ? q_rows : p_rows;
-    const int64_t og = is_q ? q_group : 0;
-    const bool mx_k = is_q ? w.q_mx_k : w.p_mx_k;
     const int li = (w.wave & 3) * 64 + w.lane;   // slot 0..255
-    const int sbytes = KIND == GK_FP8_MX ? 1 : 4;
-    if (mx_k) {
-      int64_t gr = r0 + (li * 4) % kT;
-      gr = gr + 4 <= r0 + rows ? gr : r0 + rows - 4;
-      sc = static_cast<const uint8_t*>(o.s) + (og * o.s_gs + gr * o.s_row + (li / 64) * o.s_kb);
-    } else {
-      const int lr = KIND == GK_FP8_POW2 ? scale_row_slot(li) : li;
-      const int64_t gr = r0 + (lr < rows ? lr : rows - 1);
-      sc = static_cast<const uint8_t*>(o.s) + (og * o.s_gs + (gr >> o.s_shift) * o.s_row) * sbytes;
-    }
-    sc_k = (KIND == GK_FP8_MX ? 4 : 1) * o.s_kb * sbytes;
-    sc_dst = (is_q ? SM::kQS : SM::kPS) + (w.wave & 3) * 256;
+    sc = is_q ? make_scale_src<KIND>(p.Q, i0, q_rows, q_group, w.q_mx_k, li, SM::kQS)
+              : make_scale_src<KIND>(p.P, j0, p_rows, 0, w.p_mx_k, li, SM::kPS);
   }
 
   v16f acc[4][2];
@@ -478,8 +528,8 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   if (nk > 0) {
     const uint32_t smem_lds = lds_addr(smem);
     Frag<KIND> f0, f1;
-    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo, smem_lds, w.wave);
-    issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + (nk > 1 ? KSTEP : 0), smem_lds + SM::kStage, w.wave);
+    issue_step<KIND>(qst, pst, sc, k_lo, smem_lds, w.wave);
+    issue_step<KIND>(qst, pst, sc, k_lo + (nk > 1 ? KSTEP : 0), smem_lds + SM::kStage, w.wave);
     // step 0 has landed once at most step 1's DMAs are still in flight
     FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
     block_barrier();
@@ -500,7 +550,7 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
       FM_WAIT_VMCNT(0);
       block_barrier();
       const int64_t t2n = t + 2 < nk ? t + 2 : nk - 1;
-      issue_step<KIND>(qst, pst, sc, sc_k, sc_dst, k_lo + t2n * KSTEP, smem_lds + cur_off, w.wave);
+      issue_step<KIND>(qst, pst, sc, k_lo + t2n * KSTEP, smem_lds + cur_off, w.wave);
       __builtin_amdgcn_sched_barrier(0);
       read_half<KIND>(smem + nxt_off, 0, f0, w);
       mma_half<KIND>(f1, acc);
@@ -844,7 +894,29 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 // launch
 // ============================================================================
 template <int MODE>
+inline void launch256(int kind, dim3 grid, const GemmParams& p, hipStream_t s) {
+  const dim3 block(512);
+  switch (kind) {
+    case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block, 0, s, p); break;
+    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block, 0, s, p); break;
+    default: {
+      const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
+      switch (mxl) {
+        case 0: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 0>), grid, block, 0, s, p); break;
+        case 1: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 1>), grid, block, 0, s, p); break;
+        case 2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 2>), grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 3>), grid, block, 0, s, p); break;
+      }
+    }
+  }
+}
+
+template <int MODE>
 int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
+  if (kind < GK_BF16 || kind > GK_FP8_MX) {
+    set_error("grouped gemm: unknown kind %d", kind);
+    return 1;
+  }
   if (MODE == GM_RAGGED_K && kind != GK_FP8_F32) {
     // the 256 x 256 kernel writes rows along j: put the output's row operand
     // (a_t, M rows) on the P side and its column operand (b_t) on the Q side
@@ -864,22 +936,10 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   }
   if (p.n_tiles == 0) return 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
-  const dim3 block8(512);
-  switch (kind) {
-    case GK_BF16: hipLaunchKernelGGL((gemm256_kernel<GK_BF16, MODE>), grid, block8, 0, s, p); break;
-    case GK_FP8_F32: hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p); break;
-    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_POW2, MODE>), grid, block8, 0, s, p); break;
-    case GK_FP8_MX: {
-      const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
-      switch (mxl) {
-        case 0: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 0>), grid, block8, 0, s, p); break;
-        case 1: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 1>), grid, block8, 0, s, p); break;
-        case 2: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 2>), grid, block8, 0, s, p); break;
-        default: hipLaunchKernelGGL((gemm256_kernel<GK_FP8_MX, MODE, 3>), grid, block8, 0, s, p); break;
-      }
-      break;
-    }
-    default: set_error("grouped gemm: unknown kind %d", kind); return 1;
+  if (kind == GK_FP8_F32) {
+    hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
+  } else {
+    launch256<MODE>(kind, grid, p, s);
   }
   return check_launch("grouped gemm");
 }
@@ -894,6 +954,22 @@ inline int check_operand(const FmGemmOperand& o, int kind, const char* name) {
   FM_REQUIRE(o.ld % 16 == 0, "grouped gemm: operand %s pitch must be a multiple of 16 elements", name);
   FM_REQUIRE(kind == GK_BF16 || o.scale != nullptr, "grouped gemm: operand %s scales are null", name);
   FM_REQUIRE(o.scale_row_shift >= 0 && o.scale_row_shift <= 7, "grouped gemm: operand %s scale_row_shift out of range", name);
+  // the DMA addresses a wave's 64-row slab with 32-bit offsets from its base
+  FM_REQUIRE(o.ld * (kind == GK_BF16 ? 2 : 1) <= (int64_t(1) << 25),
+             "grouped gemm: operand %s pitch exceeds 32 MiB per row", name);
+  return 0;
+}
+
+// Largest scale byte offset a lane can address from its group base (rows of
+// the operand, contraction length), kept below 2^32 for the 32-bit buffer
+// offsets of the DMA.
+inline int check_scale_span(const FmGemmOperand& o, int kind, int64_t rows, int64_t K, const char* name) {
+  if (kind == GK_BF16) return 0;
+  const int64_t sb = kind == GK_FP8_MX ? 1 : 4;
+  const int64_t blk = kind == GK_FP8_MX ? 32 : 128;
+  const int64_t span = ((rows >> o.scale_row_shift) + 1) * o.scale_row_stride * sb + (K / blk + 1) * o.scale_kb_stride * sb;
+  FM_REQUIRE(o.scale_row_stride >= 0 && o.scale_kb_stride >= 0 && span < (int64_t(1) << 32),
+             "grouped gemm: operand %s scales span more than 4 GiB from their group base", name);
   return 0;
 }
 
@@ -910,6 +986,8 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
+  if (int rc = check_scale_span(*tokens, kind, m_tiles * 128, K, "tokens")) return rc;
+  if (int rc = check_scale_span(*weights, kind, N, K, "weights")) return rc;
   FM_REQUIRE(N > 0 && N % 128 == 0, "fm_grouped_gemm_ragged_m: N must be a positive multiple of 128 (got %lld)", (long long)N);
   FM_REQUIRE(K > 0 && K % 128 == 0, "fm_grouped_gemm_ragged_m: K must be a positive multiple of 128 (got %lld)", (long long)K);
   FM_REQUIRE(E >= 1, "fm_grouped_gemm_ragged_m: E must be >= 1");
@@ -949,6 +1027,9 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
   FM_REQUIRE(a_t && b_t && offsets && out, "fm_grouped_gemm_ragged_k: null pointer");
   if (int rc = check_operand(*a_t, kind, "a_t")) return rc;
   if (int rc = check_operand(*b_t, kind, "b_t")) return rc;
+  // contraction over token columns: at most the row pitch of the operands
+  if (int rc = check_scale_span(*a_t, kind, M, a_t->ld, "a_t")) return rc;
+  if (int rc = check_scale_span(*b_t, kind, N, b_t->ld, "b_t")) return rc;
   FM_REQUIRE(M > 0 && M % 128 == 0 && N > 0 && N % 128 == 0,
              "fm_grouped_gemm_ragged_k: M and N must be positive multiples of 128 (got %lld x %lld)",
              (long long)M, (long long)N);
