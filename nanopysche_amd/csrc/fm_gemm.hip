@@ -39,6 +39,9 @@
 // Ragged-M workgroup ids are remapped so each XCD walks a contiguous range of
 // the valid tiles, grouped 8 token tiles at a time for L2 reuse of weights and
 // activations; ragged-K tiles keep launch order (balances uneven experts).
+#include <atomic>
+#include <cstdlib>
+
 #include "fm_common.h"
 #include "../../include/fm_hip.h"
 
@@ -244,7 +247,7 @@ __device__ __forceinline__ int read_mx_scale(const uint8_t* st, int off, int r, 
 struct ScaleSrc {
   v4i rsrc;
   uint32_t voff;
-  int64_t k;
+  uint32_t k;
   int dst;
 };
 
@@ -263,7 +266,7 @@ __device__ __forceinline__ ScaleSrc make_scale_src(const Operand& o, int64_t r0,
     const int64_t gr = r0 + (lr < rows ? lr : rows - 1);
     s.voff = uint32_t((gr >> o.s_shift) * o.s_row * sbytes);
   }
-  s.k = (KIND == GK_FP8_MX ? 4 : 1) * o.s_kb * sbytes;
+  s.k = uint32_t((KIND == GK_FP8_MX ? 4 : 1) * o.s_kb * sbytes);
   s.dst = lds_base + li * 4;
   return s;
 }
@@ -665,6 +668,269 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
 }
 
 // ============================================================================
+// Persistent ragged-M variant of the 256 x 256 kernel
+// ============================================================================
+// One workgroup per CU walks a strided share of its XCD's contiguous tile
+// range (the same XCD split and L2 grouping as decode_tile256).  The last two
+// refills of a tile's K loop fetch the next tile's first two K steps instead
+// of clamped duplicates, and the bf16 epilogue stages through LDS beyond the
+// two operand stages (2 KiB per wave), so a tile's output stores, the next
+// tile's first loads and its decode (registers only: the per-expert tile
+// counts are read once per workgroup) overlap.  Needs at most 64 experts and
+// at least two K steps (the launcher falls back to gemm256_kernel otherwise).
+// Per-lane values (expert x = lane: tile count, inclusive scan, offsets) live
+// in the wave's own 1 KiB of LDS between tiles, so they cost no registers
+// across the K loop.
+struct TileQueue {
+  int* lds;                    // [4][64] ints of this wave
+  int NI, JT, n_valid, per_xcd, xcd, c0, nbx;
+};
+
+// A tile of the persistent kernel: expert, first weight row, first token row,
+// end of the expert's rows (32-bit: the padded buffer has int32 offsets).
+struct TileP {
+  int e, i0, j0, j_end;
+};
+
+__device__ __forceinline__ void tile_queue_init(const GemmParams& p, TileQueue& q, int* lds) {
+  const int lane = threadIdx.x & 63;
+  int cnt = 0, o0 = 0, o1 = 0;
+  if (lane < p.E) {
+    o0 = p.offsets[lane];
+    o1 = p.offsets[lane + 1];
+    if (p.mask == nullptr || p.mask[lane] == p.mask_want) cnt = (o1 - o0 + kT - 1) / kT;
+  }
+  const int incl = wave_incl_scan(cnt, lane);
+  q.lds = lds;
+  lds[lane] = cnt;
+  lds[64 + lane] = incl;
+  lds[128 + lane] = o0;
+  lds[192 + lane] = o1;
+  q.NI = int((p.n_i + kT - 1) / kT);
+  q.JT = __builtin_amdgcn_readlane(incl, 63);
+  q.n_valid = q.JT * q.NI;
+  q.per_xcd = (q.n_valid + 7) / 8;
+  q.xcd = int(blockIdx.x % 8);
+  q.c0 = int(blockIdx.x / 8);
+  q.nbx = int(gridDim.x / 8);
+}
+
+// The m-th tile of this workgroup, false past the end of its share.
+__device__ __forceinline__ bool tile_queue_get(const TileQueue& q, int m, TileP& t) {
+  const int loc = q.c0 + m * q.nbx;
+  if (loc >= q.per_xcd) return false;
+  const int L = q.xcd * q.per_xcd + loc;
+  if (L >= q.n_valid) return false;
+  const int group = L / (kGroupM * q.NI);
+  const int first = group * kGroupM;
+  const int gsz = q.JT - first < kGroupM ? q.JT - first : kGroupM;
+  const int J = first + (L % gsz);
+  t.i0 = ((L % (kGroupM * q.NI)) / gsz) * kT;
+  const int lane = threadIdx.x & 63;
+  const int cnt = q.lds[lane], incl = q.lds[64 + lane];
+  const unsigned long long hit = __ballot(cnt > 0 && J >= incl - cnt && J < incl);
+  if (hit == 0) return false;
+  const int xe = __builtin_amdgcn_readfirstlane(__ffsll(hit) - 1);
+  t.e = xe;
+  t.j0 = q.lds[128 + xe] + (J - (q.lds[64 + xe] - q.lds[xe])) * kT;
+  t.j_end = q.lds[192 + xe];
+  return true;
+}
+
+// DMA sources of one tile.
+struct TileStreams {
+  OpStream q, p;
+  ScaleSrc sc;
+};
+
+template <int KIND>
+__device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Operand& P, int64_t n_i, const TileP& t,
+                                                   const WaveCoord& w) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  TileStreams s;
+  const int64_t q_rows = n_i - t.i0 < kT ? n_i - t.i0 : kT;
+  const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
+  s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, w.lane, w.wave);
+  s.p = make_stream(P.p + int64_t(t.j0) * P.ld * ES, P.ld * ES, p_rows, w.lane, w.wave);
+  s.sc = ScaleSrc{};
+  if constexpr (SM::kScaled) {
+    const int li = (w.wave & 3) * 64 + w.lane;
+    s.sc = w.wave < 4 ? make_scale_src<KIND>(Q, t.i0, q_rows, t.e, w.q_mx_k, li, SM::kQS)
+                      : make_scale_src<KIND>(P, t.j0, p_rows, 0, w.p_mx_k, li, SM::kPS);
+  }
+  return s;
+}
+
+// Kernel-argument fields read back from the workgroup's LDS copy as
+// wave-uniform (scalar) values.
+__device__ __forceinline__ int64_t rfl64(int64_t v) {
+  const uint64_t u = uint64_t(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
+  return int64_t((uint64_t(hi) << 32) | lo);
+}
+__device__ __forceinline__ Operand uniform_operand(const Operand* o) {
+  Operand r;
+  r.p = reinterpret_cast<const uint8_t*>(rfl64(int64_t(size_t(o->p))));
+  r.ld = rfl64(o->ld);
+  r.gs = rfl64(o->gs);
+  r.s = reinterpret_cast<const void*>(rfl64(int64_t(size_t(o->s))));
+  r.s_row = rfl64(o->s_row);
+  r.s_kb = rfl64(o->s_kb);
+  r.s_gs = rfl64(o->s_gs);
+  r.s_shift = __builtin_amdgcn_readfirstlane(o->s_shift);
+  return r;
+}
+
+// bf16 epilogue of one wave's 128 (i) x 64 (j) block through its own 2 KiB
+// of LDS `W`: 8 passes of 32 rows x 32 columns (block b of the rows, block a
+// of the columns), each written back as 64-byte row segments.  16-byte chunk
+// q of row r sits at position q ^ ((r / 4) % 4).
+__device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8_t* W, uint16_t* C, int64_t ldC,
+                                                  int64_t row0, int64_t col0, const WaveCoord& w) {
+  const int lrow = w.lrow, lhalf = w.lhalf, lane = w.lane;
+  const bool vec16 = (ldC & 7) == 0;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 v;
+        v.x = hw_bf16x2(acc[a][b][4 * q], acc[a][b][4 * q + 1]);
+        v.y = hw_bf16x2(acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+        *reinterpret_cast<uint2*>(W + lrow * 64 + ((q ^ ((lrow >> 2) & 3)) << 4) + lhalf * 8) = v;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = u * 16 + (lane >> 2), c = lane & 3;
+        const uint4 v = *reinterpret_cast<const uint4*>(W + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
+        uint16_t* d = C + (row0 + b * 32 + r) * ldC + col0 + a * 32 + c * 8;
+        if (vec16) {
+          *reinterpret_cast<uint4*>(d) = v;
+        } else {
+          reinterpret_cast<uint2*>(d)[0] = make_uint2(v.x, v.y);
+          reinterpret_cast<uint2*>(d)[1] = make_uint2(v.z, v.w);
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
+template <int KIND, int MXL = 0>
+__global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
+  constexpr int kQueue = 8 * 1024;   // tile queue, 1 KiB per wave
+  constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage + kSpare + kQueue + kArgs];
+  // The operand descriptors are needed once per tile; the workgroup's LDS copy
+  // keeps them out of the scalar registers across the K loop.
+  GemmParams* const pl = reinterpret_cast<GemmParams*>(smem + 2 * SM::kStage + kSpare + kQueue);
+  if (threadIdx.x == 0) *pl = p;   // read only after the prologue barrier
+
+  WaveCoord w;
+  w.lane = threadIdx.x & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  w.wi = w.wave >> 2;
+  w.wj = w.wave & 3;
+  w.lrow = w.lane & 31;
+  w.lhalf = w.lane >> 5;
+  w.q_mx_k = KIND == GK_FP8_MX && (MXL & 1) != 0;
+  w.p_mx_k = KIND == GK_FP8_MX && (MXL & 2) != 0;
+
+  TileQueue tq;
+  tile_queue_init(p, tq, reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare + w.wave * 1024));
+  TileP cur;
+  if (!tile_queue_get(tq, 0, cur)) return;
+  TileStreams S = tile_streams<KIND>(p.Q, p.P, p.n_i, cur, w);
+  const int64_t nk = p.K / KSTEP;   // >= 2 (launcher)
+  const uint32_t smem_lds = lds_addr(smem);
+  uint8_t* const W = smem + 2 * SM::kStage + w.wave * 2048;
+
+  Frag<KIND> f0, f1;
+  issue_step<KIND>(S.q, S.p, S.sc, 0, smem_lds, w.wave);
+  issue_step<KIND>(S.q, S.p, S.sc, KSTEP, smem_lds + SM::kStage, w.wave);
+  FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
+  block_barrier();
+  read_half<KIND>(smem, 0, f0, w);
+  int cur_off = 0;
+
+  for (int m = 0;; ++m) {
+    TileP nxt;
+    const bool has_next = tile_queue_get(tq, m + 1, nxt);
+    v16f acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    // The loop of gemm256_kernel, as two branch-free loops (one basic block
+    // each, so the MFMA / LDS-read interleave and the explicit vmcnt waits hold):
+    // steps 0 .. nk-3 refill this tile's steps t+2; the last two refill the
+    // next tile's steps 0 and 1 (duplicates of the last step on the last tile).
+    auto step = [&](int64_t t, int64_t kn) {
+      const int nxt_off = SM::kStage - cur_off;
+      __builtin_amdgcn_sched_barrier(0);
+      read_half<KIND>(smem + cur_off, 1, f1, w);
+      if constexpr (KIND == GK_FP8_POW2) {
+        f1.sa[0] = f0.sa[0];
+        f1.sb[0] = f0.sb[0];
+      }
+      mma_half<KIND>(f0, acc);
+      interleave_half<KIND>();
+      __builtin_amdgcn_sched_barrier(0);
+      FM_WAIT_VMCNT(0);
+      block_barrier();
+      issue_step<KIND>(S.q, S.p, S.sc, kn * KSTEP, smem_lds + cur_off, w.wave);
+      __builtin_amdgcn_sched_barrier(0);
+      read_half<KIND>(smem + nxt_off, 0, f0, w);
+      mma_half<KIND>(f1, acc);
+      interleave_half<KIND>();
+      __builtin_amdgcn_sched_barrier(0);
+      cur_off = nxt_off;
+    };
+#pragma unroll 1
+    for (int64_t t = 0; t < nk - 2; ++t) step(t, t + 2);
+    // this tile's sources are dead now: S becomes the next tile's
+    if (has_next) {
+      const Operand Q = uniform_operand(&pl->Q), P = uniform_operand(&pl->P);
+      S = tile_streams<KIND>(Q, P, rfl64(pl->n_i), nxt, w);
+    }
+#pragma unroll 1
+    for (int64_t t = nk - 2; t < nk; ++t) step(t, has_next ? t + 2 - nk : nk - 1);
+
+    // epilogue of `cur` (output row j = token, contiguous column i)
+    const int64_t ib = cur.i0 + w.wi * 128, jb = cur.j0 + w.wj * 64;
+    const int p_rows = cur.j_end - cur.j0 < kT ? cur.j_end - cur.j0 : kT;
+    if (ib < p.n_i && jb < cur.j0 + p_rows) {
+      if (!p.out_f32) {
+        store_bf16_passes(acc, W, static_cast<uint16_t*>(p.C), p.ldC, jb, ib, w);
+      } else {
+        float* dst = static_cast<float*>(p.C) + jb * p.ldC + ib + w.lrow * p.ldC + 4 * w.lhalf;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) = make_float4(
+                  acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+      }
+    }
+    if (!has_next) break;
+    cur = nxt;
+  }
+  FM_WAIT_VMCNT(0);  // no LDS-DMA may still be in flight when the workgroup exits
+}
+
+// ============================================================================
 // 256 x 128 kernel: FP8_F32 (fp32 block scales, promotion per 128-deep block)
 // ============================================================================
 constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
@@ -929,6 +1195,49 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 // ============================================================================
 // launch
 // ============================================================================
+// Ragged-M launches are persistent unless FM_GEMM_PERSISTENT=0 (read once).
+inline bool gemm_persistent() {
+  static const bool on = [] {
+    const char* e = getenv("FM_GEMM_PERSISTENT");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Persistent ragged-M launch: one workgroup per CU (a multiple of 8, one
+// share per XCD), at most one per 256 x 256 tile of the host bound.
+inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
+  const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
+  const int64_t want = (p.n_tiles + 7) / 8 * 8;
+  const dim3 grid(unsigned(want < slots ? want : slots)), block(512);
+  switch (kind) {
+    case GK_BF16: hipLaunchKernelGGL((gemm256p_kernel<GK_BF16>), grid, block, 0, s, p); break;
+    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p); break;
+    default: {
+      const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
+      switch (mxl) {
+        case 0: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 0>), grid, block, 0, s, p); break;
+        case 1: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 1>), grid, block, 0, s, p); break;
+        case 2: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 2>), grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 3>), grid, block, 0, s, p); break;
+      }
+    }
+  }
+}
+
 template <int MODE>
 inline void launch256(int kind, dim3 grid, const GemmParams& p, hipStream_t s) {
   const dim3 block(512);
@@ -974,6 +1283,9 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
+  } else if (MODE == GM_RAGGED_M && p.E <= 64 && p.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
+             gemm_persistent()) {
+    launch256p(kind, p, s);
   } else {
     launch256<MODE>(kind, grid, p, s);
   }
