@@ -346,6 +346,70 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
   }
 }
 
+// Piece u of issue_step: u = 0..7 the operand row groups (even: Q group u/2,
+// odd: P group u/2), u = 8 the scale dword.
+template <int KIND>
+__device__ __forceinline__ void issue_piece(int u, const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
+                                            int64_t k, uint32_t dst, int wave) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  const uint32_t kb = uint32_t(k * ES);
+  if (u < 8) {
+    const int g = u >> 1;
+    if ((u & 1) == 0) bdma16(qst.rsrc, qst.lane_off[g & 1], g * qst.group_bytes + kb, dst + (wave * 4 + g) * 1024);
+    else bdma16(pst.rsrc, pst.lane_off[g & 1], g * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + g) * 1024);
+  } else if constexpr (KIND != GK_BF16) {
+    bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
+  }
+}
+
+// issue_step + read_half(st, 0, f) with the DMA instructions placed between
+// the fragment reads (in the same order as the two functions), so the
+// interleave puts them between the phase's MFMAs: issued as one burst after
+// the barrier, a step's 72 DMA instructions per CU (~16 texture-address
+// cycles each) held every wave back from its first MFMA.
+template <int KIND>
+__device__ __forceinline__ void issue_read_half0(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
+                                                 int64_t k, uint32_t dst, int wave, const uint8_t* st,
+                                                 Frag<KIND>& f, const WaveCoord& w) {
+  using SM = Smem256<KIND>;
+  if constexpr (KIND == GK_BF16) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, s2, w.lhalf);
+        if (t < 2) f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, s2, w.lhalf);
+      }
+      issue_piece<KIND>(2 * t, qst, pst, sc, k, dst, wave);
+      issue_piece<KIND>(2 * t + 1, qst, pst, sc, k, dst, wave);
+    }
+  } else {
+    if constexpr (KIND == GK_FP8_MX) {
+      const int blk = w.lhalf;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        f.sa[t] = read_mx_scale(st, SM::kQS, w.wi * 128 + t * 32 + w.lrow, blk, w.q_mx_k);
+        if (t < 2) f.sb[t] = read_mx_scale(st, SM::kPS, w.wj * 64 + t * 32 + w.lrow, blk, w.p_mx_k);
+      }
+    } else {
+      f.sa[0] = read_pow2_scales(st, SM::kQS, w.wi * 128, w.lrow);
+      const uint2 v = *reinterpret_cast<const uint2*>(
+          st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+      f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
+    }
+    issue_piece<KIND>(8, qst, pst, sc, k, dst, wave);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
+      issue_piece<KIND>(2 * t, qst, pst, sc, k, dst, wave);
+      if (t < 2) f.b[t] = read_frag8(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, 0, w.lhalf);
+      issue_piece<KIND>(2 * t + 1, qst, pst, sc, k, dst, wave);
+    }
+  }
+}
+
 template <int A, int B, int KIND>
 __device__ __forceinline__ void mma_scaled(const Frag<KIND>& f, v16f (&acc)[4][2]) {
   acc[A][B] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[A], f.b[B], acc[A][B], 0, 0, A, f.sa[0], B,
@@ -589,9 +653,7 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
       FM_WAIT_VMCNT(0);
       block_barrier();
       const int64_t t2n = t + 2 < nk ? t + 2 : nk - 1;
-      issue_step<KIND>(qst, pst, sc, k_lo + t2n * KSTEP, smem_lds + cur_off, w.wave);
-      __builtin_amdgcn_sched_barrier(0);
-      read_half<KIND>(smem + nxt_off, 0, f0, w);
+      issue_read_half0<KIND>(qst, pst, sc, k_lo + t2n * KSTEP, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
       mma_half<KIND>(f1, acc);
       interleave_half<KIND>();
       __builtin_amdgcn_sched_barrier(0);
@@ -888,9 +950,7 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
       FM_WAIT_VMCNT(0);
       block_barrier();
-      issue_step<KIND>(S.q, S.p, S.sc, kn * KSTEP, smem_lds + cur_off, w.wave);
-      __builtin_amdgcn_sched_barrier(0);
-      read_half<KIND>(smem + nxt_off, 0, f0, w);
+      issue_read_half0<KIND>(S.q, S.p, S.sc, kn * KSTEP, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
       mma_half<KIND>(f1, acc);
       interleave_half<KIND>();
       __builtin_amdgcn_sched_barrier(0);
