@@ -226,7 +226,7 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
         ("unpermute (weighted sum over top-k)",
          lambda: _lib.call("fm_unpermute", _lib.ptr(Y), Y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(wts), T, K, D,
                            _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), st), nb(Y, wts, out)),
-        ("expert weight re-quantisation (3 launches, 128x128 pow2 + transposed)",
+        ("expert weight re-quantisation (w1, w3, w2 in one launch, 128x128 pow2 + transposed)",
          lambda: ew._build(w1, w2, w3, E), wbytes),
     ]
     results = []

@@ -107,6 +107,28 @@ int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows,
                        int64_t ld_qt, int64_t gs_qt, int64_t qt_col_off, float* st, int64_t ld_st,
                        int64_t gs_st, void* stream);
 
+/* One fm_quantize_weight job (same arguments). */
+typedef struct FmWeightJob {
+  const void* w;
+  int w_dtype;
+  int64_t groups, rows, cols, ld_w, gs_w;
+  int kind;
+  void* q;
+  int64_t ld_q, gs_q, q_row_off;
+  float* s;
+  int64_t ld_s, gs_s;
+  void* qt;
+  int64_t ld_qt, gs_qt, qt_col_off;
+  float* st;
+  int64_t ld_st, gs_st;
+} FmWeightJob;
+
+/* Same replacement as fm_quantize_weight (quantize_to_fp8 for expert weights,
+ * reference fp8/__init__.py:14): up to 4 jobs with equal groups, rows, cols and
+ * w_dtype in one launch (w1, w3 and w2 of one recipe), so the block tails of
+ * separate launches do not add up. */
+int fm_quantize_weight_batch(const FmWeightJob* jobs, int n_jobs, void* stream);
+
 /* Replaces fp8_flow_moe.dequantize_from_fp8 (reference fp8/__init__.py:15).
  * out[r][c] = decode(q[r][c]) * S, S = s[(r >> row_shift) * s_row_stride +
  * (c >> col_shift) * s_col_stride] (fp32, or e8m0 when s_e8m0). */

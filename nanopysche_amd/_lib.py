@@ -46,6 +46,18 @@ class FmGemmOperand(C.Structure):
     ]
 
 
+class FmWeightJob(C.Structure):
+    _fields_ = [
+        ("w", C.c_void_p), ("w_dtype", C.c_int),
+        ("groups", C.c_int64), ("rows", C.c_int64), ("cols", C.c_int64), ("ld_w", C.c_int64),
+        ("gs_w", C.c_int64), ("kind", C.c_int),
+        ("q", C.c_void_p), ("ld_q", C.c_int64), ("gs_q", C.c_int64), ("q_row_off", C.c_int64),
+        ("s", C.c_void_p), ("ld_s", C.c_int64), ("gs_s", C.c_int64),
+        ("qt", C.c_void_p), ("ld_qt", C.c_int64), ("gs_qt", C.c_int64), ("qt_col_off", C.c_int64),
+        ("st", C.c_void_p), ("ld_st", C.c_int64), ("gs_st", C.c_int64),
+    ]
+
+
 _vp, _i64, _i32 = C.c_void_p, C.c_int64, C.c_int
 _OPND = C.POINTER(FmGemmOperand)
 
@@ -64,6 +76,7 @@ SIGNATURES = {
     "fm_quantize_weight": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _i64, _i64,
                                   _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                                   _vp]),
+    "fm_quantize_weight_batch": (_i32, [C.POINTER(FmWeightJob), _i32, _vp]),
     "fm_dequantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _i32, _i64, _i64, _vp, _i32,
                              _i64, _vp]),
     "fm_scaling_aware_transpose": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,

@@ -106,11 +106,9 @@ struct WeightQuantArgs {
 // shares one scale.  The transposed payload is staged through LDS so each
 // thread writes whole 16-byte pieces of a transposed row.
 template <typename T>
-__global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
-  __shared__ float red[256];
-  __shared__ uint32_t tile[128][65];  // [row][col/2] (bf16 pairs) or [row][col/4] (e4m3 quads)
+__device__ __forceinline__ void weight_quant_tile(const WeightQuantArgs& a, int64_t g, float (&red)[256],
+                                                  uint32_t (&tile)[128][65]) {
   const int tid = threadIdx.x;
-  const int64_t g = blockIdx.z;
   const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
   const int cc = (tid & 15) * 8;
   const int rr = tid >> 4;
@@ -202,6 +200,28 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
     *reinterpret_cast<uint4*>(a.qt + g * a.gs_qt + (c0 + 4 * cg + c4) * a.ld_qt + a.qt_col_off + r0 + 16 * rg) =
         make_uint4(cw[c4][0], cw[c4][1], cw[c4][2], cw[c4][3]);
   if (tid == 0) a.st[g * a.gs_st + (c0 >> 7) * a.ld_st + ((r0 + a.qt_col_off) >> 7)] = s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void weight_quant_kernel(WeightQuantArgs a) {
+  __shared__ float red[256];
+  __shared__ uint32_t tile[128][65];  // [row][col/2] (bf16 pairs) or [row][col/4] (e4m3 quads)
+  weight_quant_tile<T>(a, blockIdx.z, red, tile);
+}
+
+// Up to 4 jobs with one tile grid: blockIdx.z = job * groups + group.
+struct WeightQuantBatch {
+  WeightQuantArgs job[4];
+  int64_t groups;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void weight_quant_batch_kernel(WeightQuantBatch b) {
+  __shared__ float red[256];
+  __shared__ uint32_t tile[128][65];
+  const int64_t z = blockIdx.z;
+  const int j = int(z / b.groups);
+  weight_quant_tile<T>(b.job[j], z - j * b.groups, red, tile);
 }
 
 // ------------------------------------------------------------- dequantise ----
@@ -366,6 +386,9 @@ __global__ __launch_bounds__(256) void decode_check_kernel(const uint32_t* codes
   }
 }
 
+// argument checks of one weight job (defined with the entry points)
+int check_weight_job(const FmWeightJob& jb);
+
 }  // namespace fm
 
 using namespace fm;
@@ -438,6 +461,50 @@ int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows,
                        int64_t q_row_off, float* s, int64_t ld_s, int64_t gs_s, void* qt,
                        int64_t ld_qt, int64_t gs_qt, int64_t qt_col_off, float* st, int64_t ld_st,
                        int64_t gs_st, void* stream) {
+  const FmWeightJob job{w, w_dtype, groups, rows, cols, ld_w, gs_w, kind, q, ld_q, gs_q, q_row_off,
+                        s, ld_s, gs_s, qt, ld_qt, gs_qt, qt_col_off, st, ld_st, gs_st};
+  return fm_quantize_weight_batch(&job, 1, stream);
+}
+
+int fm_quantize_weight_batch(const FmWeightJob* jobs, int n_jobs, void* stream) {
+  FM_REQUIRE(jobs != nullptr && n_jobs >= 1 && n_jobs <= 4, "fm_quantize_weight: 1 to 4 jobs (got %d)", n_jobs);
+  WeightQuantBatch batch{};
+  for (int i = 0; i < n_jobs; ++i) {
+    const FmWeightJob& jb = jobs[i];
+    if (int rc = check_weight_job(jb)) return rc;
+    FM_REQUIRE(jb.groups == jobs[0].groups && jb.rows == jobs[0].rows && jb.cols == jobs[0].cols &&
+                   jb.w_dtype == jobs[0].w_dtype,
+               "fm_quantize_weight: batched jobs must share groups, rows, cols and dtype");
+    batch.job[i] = WeightQuantArgs{jb.w, jb.w_dtype == FM_DTYPE_F32, jb.ld_w, jb.gs_w, jb.kind,
+                                   static_cast<uint8_t*>(jb.q), jb.ld_q, jb.gs_q, jb.q_row_off, jb.s, jb.ld_s,
+                                   jb.gs_s, static_cast<uint8_t*>(jb.qt), jb.ld_qt, jb.gs_qt, jb.qt_col_off,
+                                   jb.st, jb.ld_st, jb.gs_st};
+  }
+  batch.groups = jobs[0].groups;
+  const dim3 grid(unsigned(jobs[0].cols / 128), unsigned(jobs[0].rows / 128), unsigned(jobs[0].groups * n_jobs));
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  if (n_jobs == 1) {
+    if (jobs[0].w_dtype == FM_DTYPE_F32) hipLaunchKernelGGL(weight_quant_kernel<float>, grid, dim3(256), 0, sm, batch.job[0]);
+    else hipLaunchKernelGGL(weight_quant_kernel<uint16_t>, grid, dim3(256), 0, sm, batch.job[0]);
+  } else if (jobs[0].w_dtype == FM_DTYPE_F32) {
+    hipLaunchKernelGGL(weight_quant_batch_kernel<float>, grid, dim3(256), 0, sm, batch);
+  } else {
+    hipLaunchKernelGGL(weight_quant_batch_kernel<uint16_t>, grid, dim3(256), 0, sm, batch);
+  }
+  return check_launch("fm_quantize_weight");
+}
+
+}  // extern "C"
+
+namespace fm {
+int check_weight_job(const FmWeightJob& jb) {
+  const void* w = jb.w;
+  const int w_dtype = jb.w_dtype;
+  const int64_t groups = jb.groups, rows = jb.rows, cols = jb.cols, ld_w = jb.ld_w, gs_w = jb.gs_w;
+  const int kind = jb.kind;
+  const void *q = jb.q, *qt = jb.qt;
+  const float *s = jb.s, *st = jb.st;
+  const int64_t ld_q = jb.ld_q, q_row_off = jb.q_row_off, ld_qt = jb.ld_qt, qt_col_off = jb.qt_col_off;
   FM_REQUIRE(w != nullptr, "fm_quantize_weight: null input");
   FM_REQUIRE(w_dtype == FM_DTYPE_BF16 || w_dtype == FM_DTYPE_F32, "fm_quantize_weight: bad dtype");
   FM_REQUIRE(kind == QK_BF16 || kind == QK_BLOCK || kind == QK_POW2,
@@ -454,19 +521,12 @@ int fm_quantize_weight(const void* w, int w_dtype, int64_t groups, int64_t rows,
     FM_REQUIRE(q == nullptr || ld_q % 8 == 0, "fm_quantize_weight: fp8 pitch must be a multiple of 8");
     FM_REQUIRE(qt == nullptr || ld_qt % 16 == 0, "fm_quantize_weight: transposed pitch must be a multiple of 16");
   }
-  WeightQuantArgs a{w, w_dtype == FM_DTYPE_F32, ld_w, gs_w, kind,
-                    static_cast<uint8_t*>(q), ld_q, gs_q, q_row_off, s, ld_s, gs_s,
-                    static_cast<uint8_t*>(qt), ld_qt, gs_qt, qt_col_off, st, ld_st, gs_st};
   FM_REQUIRE(ld_w % 8 == 0 && gs_w % 8 == 0, "fm_quantize_weight: source pitch must be a multiple of 8");
-  dim3 grid(unsigned(cols / 128), unsigned(rows / 128), unsigned(groups));
-  if (w_dtype == FM_DTYPE_F32)
-    hipLaunchKernelGGL(weight_quant_kernel<float>, grid, dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-  else
-    hipLaunchKernelGGL(weight_quant_kernel<uint16_t>, grid, dim3(256), 0,
-                       static_cast<hipStream_t>(stream), a);
-  return check_launch("fm_quantize_weight");
+  return 0;
 }
+}  // namespace fm
+
+extern "C" {
 
 int fm_dequantize(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const void* s,
                   int s_e8m0, int row_shift, int col_shift, int64_t s_row_stride,

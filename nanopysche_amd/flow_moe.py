@@ -492,17 +492,23 @@ class ExpertWeights:
         S2t = torch.empty(E, D // 128, H // 128, dtype=f32, device=dev) if fp8 else None
         stream = _lib.stream_of(w1)
 
-        def q(src, dst, s, dst_t, s_t, row_off, col_off, rows_out, s_rows_out):
-            src = src.contiguous()
-            _lib.call("fm_quantize_weight", _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind,
-                      _lib.ptr(dst), D, rows_out * D, row_off,
-                      _lib.ptr(s), D // 128, (s_rows_out // 128) * (D // 128),
-                      _lib.ptr(dst_t), rows_out, D * rows_out, col_off,
-                      _lib.ptr(s_t), s_rows_out // 128, (D // 128) * (s_rows_out // 128), stream)
+        srcs = [w.contiguous() for w in (w1, w3, w2)]
+        if len({w.dtype for w in srcs}) != 1:
+            srcs = [w.float() for w in srcs]
 
-        q(w1, W13, S13, W13t, S13t, 0, 0, 2 * H, 2 * H)
-        q(w3, W13, S13, W13t, S13t, H, H, 2 * H, 2 * H)
-        q(w2, W2, S2, W2t, S2t, 0, 0, H, H)
+        def job(src, dst, s, dst_t, s_t, row_off, col_off, rows_out):
+            return _lib.FmWeightJob(
+                _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind,
+                _lib.ptr(dst), D, rows_out * D, row_off, _lib.ptr(s), D // 128, (rows_out // 128) * (D // 128),
+                _lib.ptr(dst_t), rows_out, D * rows_out, col_off,
+                _lib.ptr(s_t), rows_out // 128, (D // 128) * (rows_out // 128))
+
+        # w1 and w3 into the rows (and transposed columns) of the [E, 2H, D]
+        # gate|up operand, w2 into its own: one launch
+        jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, W13t, S13t, 0, 0, 2 * H),
+                                      job(srcs[1], W13, S13, W13t, S13t, H, H, 2 * H),
+                                      job(srcs[2], W2, S2, W2t, S2t, 0, 0, H))
+        _lib.call("fm_quantize_weight_batch", jobs, 3, stream)
         sh = 7
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, (2 * H // 128) * (D // 128), sh, 2 * H, D)
         self.w13t = ExpertWeightOperand(W13t, S13t, 2 * H, D * 2 * H, 2 * H // 128, 1, (D // 128) * (2 * H // 128), sh, D, 2 * H)

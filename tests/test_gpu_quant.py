@@ -225,3 +225,46 @@ def test_hw_decode_matches_software(dev):
     ref = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
     assert np.array_equal(np.isnan(ref), nan[:256])
     assert np.array_equal(ref[~nan[:256]].view(np.uint32), s_[:256][~nan[:256]].view(np.uint32))
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kind", ["block", "pow2"])
+def test_weight_batch_matches_single_launches(dev, src_dtype, kind):
+    """fm_quantize_weight_batch (w1, w3 into one [E, 2H, D] operand, w2 into
+    its own, one launch) writes the same bytes and scales as one
+    fm_quantize_weight launch per job."""
+    from nanopysche_amd import _lib
+    E, H, D = 3, 256, 384
+    k = {"block": _lib.QUANT_BLOCK, "pow2": _lib.QUANT_POW2}[kind]
+    ws = [randn_bf16((E * H, D), seed=s, std=0.02).to(src_dtype).to(dev) for s in (31, 32, 33)]
+    dt = _lib.DTYPE_F32 if src_dtype == torch.float32 else _lib.DTYPE_BF16
+
+    def outputs():
+        u8, f32 = torch.uint8, torch.float32
+        return [torch.full((E, 2 * H, D), 0x55, dtype=u8, device=dev),
+                torch.full((E, 2 * H // 128, D // 128), -1.0, dtype=f32, device=dev),
+                torch.full((E, D, 2 * H), 0x55, dtype=u8, device=dev),
+                torch.full((E, D // 128, 2 * H // 128), -1.0, dtype=f32, device=dev),
+                torch.full((E, H, D), 0x55, dtype=u8, device=dev),
+                torch.full((E, H // 128, D // 128), -1.0, dtype=f32, device=dev),
+                torch.full((E, D, H), 0x55, dtype=u8, device=dev),
+                torch.full((E, D // 128, H // 128), -1.0, dtype=f32, device=dev)]
+
+    def args(src, q, s, qt, st, row_off, rows_out):
+        return (_lib.ptr(src), dt, E, H, D, D, H * D, k, _lib.ptr(q), D, rows_out * D, row_off,
+                _lib.ptr(s), D // 128, (rows_out // 128) * (D // 128), _lib.ptr(qt), rows_out, D * rows_out,
+                row_off, _lib.ptr(st), rows_out // 128, (D // 128) * (rows_out // 128))
+
+    st = _lib.stream_of(ws[0])
+    single, batch = outputs(), outputs()
+    plan = [(ws[0], 0, 0, 2 * H), (ws[1], 0, H, 2 * H), (ws[2], 4, 0, H)]
+    for src, o, off, rows_out in plan:
+        _lib.call("fm_quantize_weight", *args(src, *single[o:o + 4], off, rows_out), st)
+    jobs = (_lib.FmWeightJob * 3)(*[_lib.FmWeightJob(*args(src, *batch[o:o + 4], off, rows_out))
+                                    for src, o, off, rows_out in plan])
+    _lib.call("fm_quantize_weight_batch", jobs, 3, st)
+    torch.cuda.synchronize()
+    for a, b in zip(single, batch):
+        assert torch.equal(a, b)
+    # every byte and scale was written (the fill values are gone)
+    assert not (single[1] < 0).any() and not (single[5] < 0).any()
