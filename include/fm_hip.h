@@ -161,6 +161,40 @@ int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int
 int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
                 float* loss, void* stream);
 
+/* Replaces the gate of MoERouter.forward (reference model/moe.py:151-154):
+ * logits[t][e] = sum_d x[t][d] w[e][d] + bias[e] + score_bias[e] in fp32, the
+ * reference's gate(x.float()) (nn.Linear(D, E, bias=True), :107) plus the
+ * DeepSeek-V3 score bias.  x bf16 or fp32 [T, D] (pitch ld_x), w fp32 [E, D]
+ * (pitch ld_w), bias / score_bias fp32 [E] or null.  E <= 256, D % 8 == 0. */
+int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const float* w,
+                     int64_t ld_w, const float* bias, const float* score_bias, int E, float* logits,
+                     int64_t ld_l, void* stream);
+
+/* counts[e] = number of the n routed slots with index e (the f_i numerator of
+ * MoERouter._load_balancing_loss, model/moe.py:271-274); indices outside
+ * [0, E) are not counted.  E <= 1024. */
+int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts, void* stream);
+
+/* Backward of the gating and the load-balancing loss (reference
+ * model/moe.py:249-281 under autograd): dlogits [T, E] from the gradient of
+ * the top-k weights (dweights [T, K], or null) and of the loss (daux: device
+ * scalar, or null; needs counts [E] of the forward routing).  gating:
+ * FM_GATING_SOFTMAX (softmax over the K selected logits) or
+ * FM_GATING_SIGMOID (sigmoid scores / (sum + 1e-8)); logits as the forward
+ * used them (score bias included). */
+int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, const void* indices,
+                   int indices_i64, const float* weights, const float* dweights, const float* daux,
+                   const int32_t* counts, float* dlogits, int64_t ld_d, void* stream);
+
+/* Backward of the gate (reference nn.Linear of model/moe.py:107 under
+ * autograd): dx = dlogits w (x's dtype, null to skip), dw = dlogits^T x and
+ * db = sum_t dlogits (fp32, null to skip), summed in a fixed order; dw needs
+ * a workspace of fm_router_workspace_bytes(T, D, E) bytes. */
+int64_t fm_router_workspace_bytes(int64_t T, int64_t D, int E);
+int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x_dtype, int64_t ld_x, int64_t T,
+                       int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
+                       int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Sizes for fm_route_sort: padded-buffer row bound, and workspace bytes. */
 int64_t fm_route_rows_max(int64_t assignments, int E);
 int64_t fm_route_workspace_bytes(int64_t assignments, int E);

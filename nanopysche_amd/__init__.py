@@ -22,7 +22,8 @@ from .flow_moe import (
     quantize_to_fp8,
     scaling_aware_transpose,
 )
-from .routing import RoutingPlan, load_balancing_loss, route_tokens, topk_gating
+from .routing import (RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens, router_logits,
+                      topk_gating)
 
 __all__ = [
     "FP8FlowMoEConfig",
@@ -46,4 +47,7 @@ __all__ = [
     "route_tokens",
     "topk_gating",
     "load_balancing_loss",
+    "route",
+    "router_logits",
+    "expert_counts",
 ]

@@ -83,6 +83,13 @@ SIGNATURES = {
                                           _vp]),
     "fm_topk_gating": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp, _i64, _vp]),
     "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "fm_router_logits": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
+    "fm_expert_counts": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
+    "fm_gating_grad": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
+                              _vp]),
+    "fm_router_workspace_bytes": (_i64, [_i64, _i64, _i32]),
+    "fm_router_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp,
+                                  _i64, _vp, _vp, _i64, _vp]),
     "fm_route_rows_max": (_i64, [_i64, _i32]),
     "fm_route_workspace_bytes": (_i64, [_i64, _i32]),
     "fm_route_sort": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,

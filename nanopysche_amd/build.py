@@ -19,7 +19,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libfm_hip.so"
-SOURCES = ["fm_api.cpp", "fm_quant.hip", "fm_route.hip", "fm_swiglu.hip", "fm_gemm.hip"]
+SOURCES = ["fm_api.cpp", "fm_quant.hip", "fm_route.hip", "fm_swiglu.hip", "fm_gemm.hip", "fm_router.hip"]
 ARCH = "gfx950"
 
 

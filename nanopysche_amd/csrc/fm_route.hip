@@ -120,24 +120,27 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   }
 }
 
-// one block: P_e = sum over waves (fixed order) / T; loss = E * sum_e f_e P_e
+// one block: P_e = sum over the per-wave partials / T; loss = E * sum_e f_e P_e.
+// Expert by expert, the 256 threads sum strided partials and meet in a fixed
+// LDS tree (a serial sum of the 1024 partials per expert took ~140 us).
 __global__ __launch_bounds__(256) void aux_loss_kernel(const float* prob_partial, int64_t n_waves,
                                                        const int32_t* counts, int E, int64_t T,
                                                        float* loss) {
   __shared__ float red[256];
-  float acc = 0.f;
-  for (int e = threadIdx.x; e < E; e += 256) {
+  float acc = 0.f;   // thread 0
+  for (int e = 0; e < E; ++e) {
     float p = 0.f;
-    for (int64_t w = 0; w < n_waves; ++w) p += prob_partial[w * E + e];
-    acc += (float(counts[e]) / float(T)) * (p / float(T));
-  }
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+    for (int64_t w = threadIdx.x; w < n_waves; w += 256) p += prob_partial[w * E + e];
+    red[threadIdx.x] = p;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) acc += (float(counts[e]) / float(T)) * (red[0] / float(T));
     __syncthreads();
   }
-  if (threadIdx.x == 0) loss[0] = float(E) * red[0];
+  if (threadIdx.x == 0) loss[0] = float(E) * acc;
 }
 
 // ----------------------------------------------------------------- sort ----

@@ -117,3 +117,110 @@ def load_balancing_loss(prob_partial: torch.Tensor, counts: torch.Tensor, num_to
     _lib.call("fm_aux_loss", _lib.ptr(prob_partial), prob_partial.shape[0], _lib.ptr(counts), E,
               num_tokens, _lib.ptr(loss), _lib.stream_of(counts))
     return loss
+
+
+# ================================================================== router ====
+def _x_dtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if x.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise TypeError(f"router input must be bfloat16 or float32, got {x.dtype}")
+
+
+def router_logits(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, score_bias=None) -> torch.Tensor:
+    """fp32 logits [T, E] = x.float() @ gate_weight.T + gate_bias (+ score_bias),
+    the gate of MoERouter.forward (reference model/moe.py:151-154)."""
+    _lib.require_device(x, "x")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w = gate_weight.detach().float().contiguous()
+    E, D = w.shape
+    b = None if gate_bias is None else gate_bias.detach().float().contiguous()
+    sb = None if score_bias is None else score_bias.detach().float().contiguous()
+    T = x2.shape[0]
+    logits = torch.empty(T, E, dtype=torch.float32, device=x2.device)
+    _lib.call("fm_router_logits", _lib.ptr(x2), _x_dtype(x2), x2.stride(0), T, D, _lib.ptr(w), w.stride(0),
+              _lib.ptr(b), _lib.ptr(sb), E, _lib.ptr(logits), logits.stride(0), _lib.stream_of(x2))
+    return logits
+
+
+def expert_counts(indices: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """[E] int32 number of routed slots per expert (indices outside [0, E) ignored)."""
+    idx = indices.contiguous()
+    counts = torch.empty(num_experts, dtype=torch.int32, device=idx.device)
+    _lib.call("fm_expert_counts", _lib.ptr(idx), int(idx.dtype == torch.int64), idx.numel(), num_experts,
+              _lib.ptr(counts), _lib.stream_of(idx))
+    return counts
+
+
+class _RouterFunction(torch.autograd.Function):
+    """Gate + top-k gating + load-balancing loss, forward and backward on the GPU."""
+
+    @staticmethod
+    def forward(ctx, x, gate_weight, gate_bias, score_bias, top_k, gating):
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        T = x2.shape[0]
+        logits = router_logits(x2, gate_weight, gate_bias, score_bias)
+        E = logits.shape[1]
+        w, idx, part = topk_gating(logits, top_k, gating, return_prob_partial=True)
+        counts = expert_counts(idx, E)
+        aux = load_balancing_loss(part, counts, T)
+        ctx.save_for_backward(x2, gate_weight, logits, idx, w, counts)
+        ctx.gating = {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[
+            str(gating).lower().split(".")[-1]]
+        ctx.has_bias = gate_bias is not None
+        ctx.lead = lead
+        ctx.mark_non_differentiable(idx)
+        return w.reshape(*lead, top_k), idx.reshape(*lead, top_k), aux
+
+    @staticmethod
+    def backward(ctx, dweights, _dindices, daux):
+        x2, gate_weight, logits, idx, w, counts = ctx.saved_tensors
+        T, D = x2.shape
+        E = logits.shape[1]
+        K = idx.shape[1]
+        dev = x2.device
+        st = _lib.stream_of(x2)
+        dwts = None if dweights is None else dweights.reshape(T, K).float().contiguous()
+        da = None if daux is None else daux.reshape(1).float().contiguous()
+        dlogits = torch.empty(T, E, dtype=torch.float32, device=dev)
+        if dwts is None and da is None:
+            dlogits.zero_()
+        else:
+            _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, ctx.gating, _lib.ptr(idx),
+                      int(idx.dtype == torch.int64), _lib.ptr(w), _lib.ptr(dwts), _lib.ptr(da), _lib.ptr(counts),
+                      _lib.ptr(dlogits), dlogits.stride(0), st)
+        need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        wf = gate_weight.detach().float().contiguous()
+        dx = torch.empty_like(x2) if need_x else None
+        dW = torch.empty(E, D, dtype=torch.float32, device=dev) if need_w else None
+        db = torch.empty(E, dtype=torch.float32, device=dev) if (need_b and ctx.has_bias) else None
+        ws = None
+        if dW is not None:
+            ws = torch.empty(int(_lib.load().fm_router_workspace_bytes(T, D, E)), dtype=torch.uint8, device=dev)
+        if dx is not None or dW is not None or db is not None:
+            _lib.call("fm_router_backward", _lib.ptr(dlogits), dlogits.stride(0), _lib.ptr(x2), _x_dtype(x2),
+                      x2.stride(0), T, D, _lib.ptr(wf), wf.stride(0), E, _lib.ptr(dx),
+                      0 if dx is None else dx.stride(0), _lib.ptr(dW), 0 if dW is None else dW.stride(0),
+                      _lib.ptr(db), _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
+        if dx is not None:
+            dx = dx.reshape(*ctx.lead, D)
+        if dW is not None:
+            dW = dW.to(gate_weight.dtype)
+        return dx, dW, db, None, None, None
+
+
+def route(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, *, top_k: int, gating: str = "softmax",
+          score_bias=None):
+    """MoERouter.forward on the GPU (reference model/moe.py:133-184 without
+    jitter, routing replay, l2 normalisation or z-loss): fp32 gate logits
+    x.float() @ W.T + b (+ score_bias) -> top-k gating (softmax over the K
+    selected logits, or sigmoid / (sum + 1e-8)) -> (weights [..., K] fp32,
+    indices [..., K] int64, load-balancing loss E * sum_i f_i P_i).
+    Differentiable in x, gate_weight and gate_bias through the weights and the
+    loss."""
+    _lib.require_device(x, "x")
+    return _RouterFunction.apply(x, gate_weight, gate_bias, score_bias, int(top_k), gating)

@@ -124,3 +124,14 @@ def unpermute_unpad(y: np.ndarray, row_of: np.ndarray, weights, num_tokens: int,
     for k in range(top_k):
         acc = (acc + (w[:, k : k + 1] * rows[:, k]).astype(np.float32)).astype(np.float32)
     return acc
+
+
+def router_logits(x: np.ndarray, w: np.ndarray, b=None, score_bias=None) -> np.ndarray:
+    """model/moe.py:151-154: gate(x.float()) (nn.Linear, fp32) + score_bias.
+    Computed in float64 and rounded to fp32 once."""
+    out = np.asarray(x, dtype=np.float64) @ np.asarray(w, dtype=np.float64).T
+    if b is not None:
+        out = out + np.asarray(b, dtype=np.float64)
+    if score_bias is not None:
+        out = out + np.asarray(score_bias, dtype=np.float64)
+    return out.astype(np.float32)

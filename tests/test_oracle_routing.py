@@ -125,3 +125,24 @@ def test_permute_and_unpermute_brute_force():
         rows = [r["row_of"][t * K + int((idx[t] == e).nonzero()[0])] for t in tok.tolist()]
         ref[tok] += pw[:, None] * torch.from_numpy(y[rows])
     assert np.allclose(out, ref.numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_router_logits_matches_reference_linear():
+    """oracle.router_logits against the reference's gate: nn.Linear(D, E,
+    bias=True) applied to x.float() (model/moe.py:107, :151), plus score_bias
+    (:153-154), evaluated in float64 by torch."""
+    g = torch.Generator().manual_seed(3)
+    T, D, E = 64, 96, 12
+    x = torch.randn(T, D, generator=g).bfloat16()
+    gate = torch.nn.Linear(D, E, bias=True).double()
+    with torch.no_grad():
+        gate.weight.copy_(torch.randn(E, D, generator=g) * 0.02)
+        gate.bias.fill_(-1.0)
+    sb = torch.randn(E, generator=g) * 0.1
+    ref = (gate(x.double()) + sb.double()).detach().numpy()
+    got = orouting.router_logits(x.float().numpy(), gate.weight.detach().float().numpy(),
+                                 gate.bias.detach().float().numpy(), sb.numpy())
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+    # a transposed operand or a dropped bias is caught
+    bad = orouting.router_logits(x.float().numpy(), gate.weight.detach().float().numpy())
+    assert not np.allclose(bad, ref, atol=1e-3)
