@@ -84,6 +84,7 @@ struct GemmParams {
   int64_t c2_gs, split;
   int out_f32;
   int64_t n_tiles;    // logical tiles
+  int rk_xcd;         // ragged-K, 256 x 256 kernel: allow the contiguous XCD split
 };
 
 constexpr int kGroupM = 8;
@@ -465,10 +466,12 @@ struct Tile256 {
 // ragged-M: the valid 256-token tiles (sum over experts of ceil(rows / 256),
 // from the device-side offsets; the launch is sized by a host bound) are
 // split into 8 contiguous ranges, one per XCD (blockIdx % 8), for L2 reuse.
-// ragged-K: tiles in launch order, so one expert's tiles (whose K lengths
-// differ between experts) spread over every XCD and the hardware's dynamic
-// workgroup dispatch balances them.  Returns false when this workgroup has no
-// tile.
+// ragged-K: when every expert runs and none holds more than 9/8 of the mean
+// rows, the tiles are split into 8 contiguous ranges as well (each XCD then
+// reads about one expert's operands); otherwise they stay in launch order, so
+// one expert's tiles (whose K lengths differ between experts) spread over
+// every XCD and the hardware's dynamic workgroup dispatch balances them.
+// Returns false when this workgroup has no tile.
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -514,6 +517,19 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
     if (L >= n_valid) return false;
   } else {
     L = blockIdx.x;
+    if (p.rk_xcd && p.mask == nullptr && p.E <= 64) {
+      int rows = lane < p.E ? p.offsets[lane + 1] - p.offsets[lane] : 0;
+      int sum = rows, mx = rows;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        sum += __shfl_xor(sum, d, 64);
+        mx = max(mx, __shfl_xor(mx, d, 64));
+      }
+      if (__builtin_amdgcn_readfirstlane(int(int64_t(mx) * p.E * 8 <= int64_t(sum) * 9))) {
+        const int64_t per_xcd = (p.n_tiles + 7) / 8;
+        L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+      }
+    }
     if (L >= p.n_tiles) return false;
   }
   int64_t e = -1;
@@ -1255,6 +1271,16 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 // ============================================================================
 // launch
 // ============================================================================
+// FM_RK_XCD=0: ragged-K launches keep their tiles in launch order even for
+// balanced experts (read once).
+inline bool gemm_rk_xcd_split() {
+  static const bool on = [] {
+    const char* e = getenv("FM_RK_XCD");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
 // Ragged-M launches are persistent unless FM_GEMM_PERSISTENT=0 (read once).
 inline bool gemm_persistent() {
   static const bool on = [] {
@@ -1340,6 +1366,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
     p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256 : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT);
   }
   if (p.n_tiles == 0) return 0;
+  p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);

@@ -100,12 +100,19 @@ def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
-def test_ragged_k_weight_grad(dev, kind):
+@pytest.mark.parametrize("balanced", [False, True])
+def test_ragged_k_weight_grad(dev, kind, balanced):
+    """Skewed routing with a zero-token expert keeps the tiles in launch
+    order; balanced routing takes the contiguous per-XCD split."""
     E, T, K, D, H = 6, 2500, 2, 256, 256
     k = KINDS[kind]
     x = randn_bf16((T, D), seed=5)
     g = randn_bf16((T, 2 * H), seed=6)
-    _, idx = zipf_routing(T, E, K, 1.2, seed=3, zero_experts=(4,))
+    if balanced:
+        t = torch.arange(T)
+        idx = torch.stack([t % E, (t + 1) % E], 1)
+    else:
+        _, idx = zipf_routing(T, E, K, 1.2, seed=3, zero_experts=(4,))
     gran = {"bf16": None, "block": "1x128", "pow2": "1x128", "mx": "1x32"}[kind]
     px = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2",
                               return_transpose=True)
