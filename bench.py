@@ -11,6 +11,7 @@ after an optimizer update).  Inputs are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--recipe flow_moe]
     python bench.py --workload c1|c2|c4|c5    # the other configs, one JSON line each
+    python bench.py --workload shared         # shared expert / dense SwiGLU FFN at configs[2]'s shapes
 
 Prints one JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
@@ -331,6 +332,78 @@ def workload_c3(args, dev):
     }
 
 
+# ======================================================= shared expert ====
+def workload_shared(args, dev):
+    """Shared expert / dense SwiGLU FFN (FP8SharedExpertCompute: one group on
+    the grouped-GEMM path) at configs[2]'s shapes: every one of T = 8192
+    tokens through one SwiGLU FFN, D = 2048, H = 1408, fwd + bwd, weights
+    re-quantised every step."""
+    import torch
+
+    import nanopysche_amd as fm
+    from nanopysche_amd import flow_moe as fmm
+
+    T, D, H = 8192, 2048, 1408
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(T, D, device=dev, generator=g).bfloat16().requires_grad_(True)
+    params = [(torch.randn(H, D, device=dev, generator=g) * 0.02).bfloat16().requires_grad_(True)
+              for _ in range(3)]
+    go = (torch.randn(T, D, device=dev, generator=g) * 1e-2).bfloat16()
+    cfg = fm.FP8FlowMoEConfig(enabled=args.recipe != "none",
+                              fp8_recipe=fm.FP8RecipeConfig(args.recipe != "none", fm.FP8RecipeType(args.recipe)))
+    blk = fm.FP8SharedExpertCompute(cfg, D, H)
+    blk.set_weights(*params)
+
+    def step():
+        blk.block._cache.clear()
+        for p in params + [x]:
+            p.grad = None
+        blk(x).backward(go)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    timer = GemmTimer()
+    fmm.GEMM_TIMER = timer
+    blk.block.overlap_streams = False
+    try:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        fmm.GEMM_TIMER = None
+    summ = timer.summary()
+    dom = max(summ, key=lambda k: summ[k]["ms"])
+    d = summ[dom]
+    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
+    peak = PEAK_TFLOPS["bf16" if args.recipe == "none" else "fp8"]
+    return {
+        "metric": "Shared-expert SwiGLU FFN fwd+bwd tokens/s on 1 MI355X",
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if args.recipe == "none" else "fp8-e4m3",
+        "data": "synthetic",
+        "config": {"workload": "shared expert at configs[2]'s shapes (one group on the grouped-GEMM path)",
+                   "tokens": T, "d_model": D, "ffn_hidden": H, "recipe": args.recipe},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": None, "kernel": dom},
+        "gemm": gemm_report(summ, args.steps),
+        "cpu_baseline": None,
+    }
+
+
 # ============================================================== configs[1] ====
 def workload_c2(args, dev):
     """Quantisation primitives on configs[1]'s inputs: x [8192, 4096] bf16
@@ -612,7 +685,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c2", "c4", "c5"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c2", "c4", "c5", "shared"])
     ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-overlap", action="store_true",
@@ -629,7 +702,7 @@ def main():
 
     dev = torch.device("cuda:0")
     run = {"c3": workload_c3, "c1": workload_c1, "c2": workload_c2, "c4": workload_c4,
-           "c5": workload_c5}[args.workload]
+           "c5": workload_c5, "shared": workload_shared}[args.workload]
     print(json.dumps(run(args, dev)))
 
 

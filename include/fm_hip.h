@@ -295,6 +295,23 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
                              void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
                              int64_t ld_out, void* stream);
 
+/* fm_grouped_gemm_ragged_k with each expert's token range cut into `splits`
+ * slices on its 128-row grid, for launches with fewer output tiles than CUs
+ * (one group, as for a shared expert, or few small experts): the slices'
+ * fp32 partial products go to `workspace` ([splits][E][M][N] fp32, 16-byte
+ * aligned, fm_grouped_gemm_ragged_k_split_workspace_bytes() bytes), and a
+ * second kernel sums them in slice order (the result does not depend on
+ * scheduling) into out / out2 as above.  Same reference counterpart as
+ * fm_grouped_gemm_ragged_k; splits in [1, 16], 1 = the unsplit launch
+ * (workspace unused); the fp32-scale blockwise kind takes splits = 1 only. */
+int64_t fm_grouped_gemm_ragged_k_split_workspace_bytes(int E, int64_t M, int64_t N, int splits);
+int fm_grouped_gemm_ragged_k_split(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                                   const int32_t* offsets, int E, int64_t M, int64_t N,
+                                   const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
+                                   void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
+                                   int64_t ld_out, int splits, void* workspace, int64_t workspace_bytes,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@ from .flow_moe import (
     ExpertWeights,
     FP8FlowMoECompute,
     FP8FlowMoEConfig,
+    FP8SharedExpertCompute,
     FP8Tensor,
     PermutedTokens,
     dequantize_from_fp8,
@@ -28,6 +29,7 @@ from .routing import (RoutingPlan, expert_counts, load_balancing_loss, route, ro
 __all__ = [
     "FP8FlowMoEConfig",
     "FP8FlowMoECompute",
+    "FP8SharedExpertCompute",
     "FP8RecipeConfig",
     "FP8RecipeType",
     "BlockScalingGranularity",

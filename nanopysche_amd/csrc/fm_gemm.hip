@@ -85,6 +85,8 @@ struct GemmParams {
   int out_f32;
   int64_t n_tiles;    // logical tiles
   int rk_xcd;         // ragged-K, 256 x 256 kernel: allow the contiguous XCD split
+  int splits;         // ragged-K, 256 x 256 kernel: K slices per tile (>1: fp32 partials, C = workspace)
+  int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
 };
 
 constexpr int kGroupM = 8;
@@ -460,7 +462,7 @@ __device__ __forceinline__ void interleave_half() {
 // A 256 x 256 workgroup tile: expert, first weight row i0, first token (or
 // m) row j0, end of the valid j rows, and the contraction range.
 struct Tile256 {
-  int64_t e, i0, j0, j_end, k_lo, k_hi;
+  int64_t e, i0, j0, j_end, k_lo, k_hi, slice;
 };
 
 // ragged-M: the valid 256-token tiles (sum over experts of ceil(rows / 256),
@@ -567,6 +569,10 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
   } else {
     const int64_t NJ = (p.n_j + kT - 1) / kT;
     const int64_t per_e = NI * NJ;
+    // split K: slice s of every tile follows all tiles of slice s - 1
+    const int64_t per_slice = p.n_tiles / p.splits;
+    t.slice = L / per_slice;
+    L %= per_slice;
     e = L / per_e;
     const int64_t Lr = L % per_e;
     const int64_t group = Lr / (kGroupM * NJ);
@@ -577,6 +583,11 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
     t.j_end = p.n_j;
     t.k_lo = p.offsets[e];
     t.k_hi = p.offsets[e + 1];
+    if (p.splits > 1) {   // slice boundaries on the 128-row grid of the offsets
+      const int64_t n = (t.k_hi - t.k_lo) / 128;
+      t.k_hi = t.k_lo + 128 * (n * (t.slice + 1) / p.splits);
+      t.k_lo += 128 * (n * t.slice / p.splits);
+    }
   }
   if (p.mask != nullptr && p.mask[e] != p.mask_want) return false;
   t.e = e;
@@ -594,6 +605,7 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
 
   Tile256 tile;
+  tile.slice = 0;
   if (!decode_tile256<MODE>(p, tile)) return;
   const int64_t e = tile.e, i0 = tile.i0, j0 = tile.j0, j_end = tile.j_end, k_lo = tile.k_lo, k_hi = tile.k_hi;
 
@@ -695,7 +707,7 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
   } else {
     const bool second = jb >= p.split;
     C = second ? p.C2 : p.C;
-    row_off = e * (second ? p.c2_gs : p.c_gs) + (second ? jb - p.split : jb) * p.ldC + ib;
+    row_off = e * (second ? p.c2_gs : p.c_gs) + (second ? jb - p.split : jb) * p.ldC + ib + tile.slice * p.ws_slice;
   }
   if (!p.out_f32) {
     // bf16: each wave stages its 64 x 128 block in its own 16 KiB of LDS and
@@ -1363,7 +1375,9 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
     const int64_t NI = (p.n_i + kBI - 1) / kBI;
     p.n_tiles = MODE == GM_RAGGED_M ? p.m_tiles * NI : int64_t(p.E) * NI * (p.n_j / kBJ);
   } else {
-    p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256 : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT);
+    if (p.splits < 1) p.splits = 1;
+    p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256
+                                    : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT) * p.splits;
   }
   if (p.n_tiles == 0) return 0;
   p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
@@ -1406,6 +1420,53 @@ inline int check_scale_span(const FmGemmOperand& o, int kind, int64_t rows, int6
   FM_REQUIRE(o.scale_row_stride >= 0 && o.scale_kb_stride >= 0 && span < (int64_t(1) << 32),
              "grouped gemm: operand %s scales span more than 4 GiB from their group base", name);
   return 0;
+}
+
+// ============================================================================
+// split-K reduction of the ragged-K partials
+// ============================================================================
+// ws [splits][E][M][N] fp32 -> out / out2 rows (row < split: out, else out2 at
+// row - split), summed in slice order (deterministic), 4 columns per thread.
+// Experts that the mask leaves to the other launch are not written.
+struct SplitReduceArgs {
+  const float* ws;
+  int64_t slice, E, M, N;
+  int splits;
+  const int32_t* mask;
+  int mask_want;
+  void* out;
+  void* out2;
+  int64_t out_gs, out2_gs, split, ld;
+  int out_f32;
+};
+
+__global__ __launch_bounds__(256) void split_reduce_kernel(SplitReduceArgs a) {
+  const int64_t n4 = a.N / 4;
+  const int64_t total = a.E * a.M * n4;
+  for (int64_t v = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; v < total;
+       v += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t c = (v % n4) * 4;
+    const int64_t r = (v / n4) % a.M;
+    const int64_t e = v / (n4 * a.M);
+    if (a.mask != nullptr && a.mask[e] != a.mask_want) continue;
+    const float* src = a.ws + (e * a.M + r) * a.N + c;
+    float4 acc = *reinterpret_cast<const float4*>(src);
+    for (int s = 1; s < a.splits; ++s) {
+      const float4 u = *reinterpret_cast<const float4*>(src + s * a.slice);
+      acc.x += u.x;
+      acc.y += u.y;
+      acc.z += u.z;
+      acc.w += u.w;
+    }
+    const bool second = r >= a.split;
+    const int64_t off = e * (second ? a.out2_gs : a.out_gs) + (second ? r - a.split : r) * a.ld + c;
+    if (a.out_f32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(second ? a.out2 : a.out) + off) = acc;
+    } else {
+      uint16_t* d = static_cast<uint16_t*>(second ? a.out2 : a.out) + off;
+      *reinterpret_cast<uint2*>(d) = make_uint2(hw_bf16x2(acc.x, acc.y), hw_bf16x2(acc.z, acc.w));
+    }
+  }
 }
 
 }  // namespace fm
@@ -1454,11 +1515,13 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   return dispatch_gemm<GM_RAGGED_M>(kind, p, static_cast<hipStream_t>(stream));
 }
 
-int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
-                             const int32_t* offsets, int E, int64_t M, int64_t N,
-                             const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
-                             void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
-                             int64_t ld_out, void* stream) {
+namespace {
+
+// Checks the ragged-K arguments and fills the launch parameters (the public
+// entries differ only in the split).
+int ragged_k_params(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t, const int32_t* offsets, int E,
+                    int64_t M, int64_t N, const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
+                    void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype, int64_t ld_out, GemmParams& p) {
   FM_REQUIRE(a_t && b_t && offsets && out, "fm_grouped_gemm_ragged_k: null pointer");
   if (int rc = check_operand(*a_t, kind, "a_t")) return rc;
   if (int rc = check_operand(*b_t, kind, "b_t")) return rc;
@@ -1473,7 +1536,7 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_k: bad out dtype");
   FM_REQUIRE(split_rows >= M || (out2 != nullptr && split_rows % 128 == 0 && split_rows > 0),
              "fm_grouped_gemm_ragged_k: split output needs out2 and a 128-aligned split");
-  GemmParams p{};
+  p = GemmParams{};
   p.P = make_operand(*b_t);
   p.Q = make_operand(*a_t);
   p.n_i = M;
@@ -1489,7 +1552,81 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
   p.c2_gs = out2_gs;
   p.split = split_rows >= M ? INT64_MAX : split_rows;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
+  p.splits = 1;
+  return 0;
+}
+
+}  // namespace
+
+int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                             const int32_t* offsets, int E, int64_t M, int64_t N,
+                             const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
+                             void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
+                             int64_t ld_out, void* stream) {
+  GemmParams p;
+  if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M, N, expert_mask, mask_want, out, out_gs, out2,
+                               out2_gs, split_rows, out_dtype, ld_out, p))
+    return rc;
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
+}
+
+int64_t fm_grouped_gemm_ragged_k_split_workspace_bytes(int E, int64_t M, int64_t N, int splits) {
+  if (E < 1 || M < 0 || N < 0 || splits < 1) return -1;
+  return int64_t(splits) * E * M * N * int64_t(sizeof(float));
+}
+
+int fm_grouped_gemm_ragged_k_split(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                                   const int32_t* offsets, int E, int64_t M, int64_t N,
+                                   const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
+                                   void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
+                                   int64_t ld_out, int splits, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  GemmParams p;
+  if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M, N, expert_mask, mask_want, out, out_gs, out2,
+                               out2_gs, split_rows, out_dtype, ld_out, p))
+    return rc;
+  FM_REQUIRE(splits >= 1 && splits <= 16, "fm_grouped_gemm_ragged_k_split: splits must be in [1, 16] (got %d)",
+             splits);
+  FM_REQUIRE(kind != GK_FP8_F32 || splits == 1,
+             "fm_grouped_gemm_ragged_k_split: the fp32-scale blockwise kind takes no K split");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (splits == 1) return dispatch_gemm<GM_RAGGED_K>(kind, p, s);
+  const int64_t need = fm_grouped_gemm_ragged_k_split_workspace_bytes(E, M, N, splits);
+  FM_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+             "fm_grouped_gemm_ragged_k_split: workspace of %lld bytes needed, %lld given", (long long)need,
+             (long long)workspace_bytes);
+  FM_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+             "fm_grouped_gemm_ragged_k_split: workspace must be 16-byte aligned");
+  SplitReduceArgs r{};
+  r.ws = static_cast<const float*>(workspace);
+  r.slice = int64_t(E) * M * N;
+  r.E = E;
+  r.M = M;
+  r.N = N;
+  r.splits = splits;
+  r.mask = expert_mask;
+  r.mask_want = mask_want;
+  r.out = p.C;
+  r.out2 = p.C2;
+  r.out_gs = p.c_gs;
+  r.out2_gs = p.c2_gs;
+  r.split = p.split;
+  r.ld = p.ldC;
+  r.out_f32 = p.out_f32;
+  // the GEMM writes fp32 partials [splits][E][M][N] into the workspace
+  p.C = workspace;
+  p.C2 = nullptr;
+  p.ldC = N;
+  p.c_gs = M * N;
+  p.split = INT64_MAX;
+  p.out_f32 = 1;
+  p.splits = splits;
+  p.ws_slice = r.slice;
+  if (int rc = dispatch_gemm<GM_RAGGED_K>(kind, p, s)) return rc;
+  const int64_t total = int64_t(E) * M * (N / 4);
+  const int64_t blocks = (total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192;
+  hipLaunchKernelGGL(split_reduce_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, r);
+  return check_launch("grouped gemm split-K reduction");
 }
 
 }  // extern "C"

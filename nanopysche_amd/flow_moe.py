@@ -17,6 +17,7 @@ expert_offset, num_local_experts)``) is the reference's.
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -403,13 +404,69 @@ def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=N
            2.0 * plan.num_tokens * plan.top_k * w.N * w.K, launch)
 
 
+# Model of a ragged-K launch for choosing its K split: ~1.3 us per 128-deep K
+# step of a 256 x 256 tile, and the partials' HBM round trip at ~5 TB/s.
+_K_STEP_US = 1.3
+_HBM_BYTES_PER_US = 5.0e6
+_CUS = {}
+
+
+def _cus(dev) -> int:
+    n = _CUS.get(dev)
+    if n is None:
+        n = _CUS[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return n
+
+
+def _k_splits(kind, plan: RoutingPlan, M, N, dev) -> int:
+    """K slices per weight-gradient tile: more than one only when the launch
+    has fewer 256 x 256 output tiles than the GPU has CUs (one group, as for a
+    shared expert, or few small experts).  Chosen on the host from the shapes
+    and the padded row bound alone (no read of the device counts), minimising
+    rounds x slice length + the fp32 partials' write and re-read.
+    FM_RK_SPLITS=<n> fixes it (1 = never split)."""
+    forced = os.environ.get("FM_RK_SPLITS")
+    if kind == _lib.QUANT_BLOCK:
+        return 1   # the fp32-scale kernel takes no split
+    if forced is not None:
+        return max(1, min(16, int(forced)))
+    E = plan.num_experts
+    tiles = E * -(-M // 256) * -(-N // 256)
+    cus = _cus(dev)
+    if tiles >= cus:
+        return 1
+    steps = plan.rows_max / E / 128
+    part_us = E * M * N * 4 / _HBM_BYTES_PER_US
+    best, best_us = 1, -(-tiles // cus) * steps * _K_STEP_US
+    for S in range(2, 9):
+        if steps / S < 4:
+            break
+        us = -(-tiles * S // cus) * steps / S * _K_STEP_US + (S + 0.5) * part_us
+        if us < best_us:
+            best, best_us = S, us
+    return best
+
+
 def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out2_gs=0, split=None,
-            mask=None, want=1):
+            mask=None, want=1, may_split=True):
+    S = _k_splits(kind, plan, M, N, out.device) if may_split else 1
+    ws = None
+    if S > 1:
+        nbytes = int(_lib.load().fm_grouped_gemm_ragged_k_split_workspace_bytes(plan.num_experts, M, N, S))
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=out.device)
+
     def launch():
-        _lib.call("fm_grouped_gemm_ragged_k", _gemm_kind(kind), _col_operand(a_t, kind),
-                  _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
-                  _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
-                  M if split is None else split, _dt(out), N, _lib.stream_of(out))
+        if ws is None:
+            _lib.call("fm_grouped_gemm_ragged_k", _gemm_kind(kind), _col_operand(a_t, kind),
+                      _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
+                      _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
+                      M if split is None else split, _dt(out), N, _lib.stream_of(out))
+        else:
+            _lib.call("fm_grouped_gemm_ragged_k_split", _gemm_kind(kind), _col_operand(a_t, kind),
+                      _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
+                      _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
+                      M if split is None else split, _dt(out), N, S, _lib.ptr(ws), ws.numel() * 4,
+                      _lib.stream_of(out))
 
     _timed(f"grouped_gemm_ragged_k/{_KIND_NAME[kind]}",
            2.0 * plan.num_tokens * plan.top_k * M * N, launch)
@@ -713,10 +770,13 @@ class FP8FlowMoECompute:
         dev = GU.device
         dO = grad_out.reshape(T, D).to(torch.bfloat16).contiguous()
         mask = plan.use_fp8 if (fp8_kind is not None and use_bf16) else None
-        # router-weight gradient from the saved expert outputs
-        dw = torch.empty(T * K, dtype=torch.float32, device=dev)
-        _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
-                  _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
+        # router-weight gradient from the saved expert outputs (skipped when
+        # the weights need none, e.g. the constant weights of a shared expert)
+        dw = None
+        if ctx.needs_input_grad[1]:
+            dw = torch.empty(T * K, dtype=torch.float32, device=dev)
+            _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
+                      _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
         dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
         dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         w1dt, w2dt, w3dt = ctx.wdtypes
@@ -730,14 +790,15 @@ class FP8FlowMoECompute:
                                       return_transpose=True, weights=wts, kmajor_scales=True) for kind, _ in runs}
         # dW2 (contraction over each expert's tokens) runs on a second stream
         # beside dH: each alone leaves the last round of workgroups part-empty
-        # when the hidden size is not a multiple of the 256-wide tile.
+        # when the hidden size is not a multiple of the 256-wide tile.  There
+        # it takes no K split: the CUs it leaves idle run dH.
         main = torch.cuda.current_stream(dev)
         side = _side_stream(dev) if self.overlap_streams else main
         side.wait_stream(main)
         with torch.cuda.stream(side):
             for kind, want in runs:
                 _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
-                        want=want)
+                        want=want, may_split=side is main)
         for kind, want in runs:
             _gemm_m(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, mask, want)
         if self.capture_intermediates is not None:
@@ -758,7 +819,47 @@ class FP8FlowMoECompute:
         main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None
-        return (dx.to(ctx.x_dtype), dw.reshape(T, K), dW1, dW2, dW3, None, None)
+        return (dx.to(ctx.x_dtype), None if dw is None else dw.reshape(T, K), dW1, dW2, dW3, None, None)
+
+
+class FP8SharedExpertCompute:
+    """A dense SwiGLU FFN ``(silu(x w1^T) * (x w3^T)) w2^T`` on the expert
+    block's path as a single group: the shared expert of a DeepSeek-V2 style
+    MoE (reference ``model/moe.py:1299-1301``, added to the routed output at
+    ``:1383-1384`` and ``:1686-1687``; ``ExpertMLP`` ``:1164-1183``) or the
+    bias-free dense FFN (``model/feed_forward.py:74-80`` with silu).
+
+    Every token goes to the one group with weight 1, so routing reduces to
+    padding the rows to a multiple of 128, and the same fused quantisers,
+    grouped GEMMs and SwiGLU kernels run as for the routed experts (FP8 per
+    the recipe; ``fp8_gemm_threshold`` > number of tokens selects BF16).
+    ``set_weights(w1 [H, D], w2 [H, D], w3 [H, D])`` borrows the weights
+    (``w2`` stored as ``[H, D]``, i.e. the transpose of ``nn.Linear(H, D)``'s
+    weight, like the expert block's); ``__call__(x [..., D]) -> [..., D]`` is
+    differentiable with respect to x, w1, w2 and w3.
+    """
+
+    def __init__(self, config: FP8FlowMoEConfig, d_model: int, hidden_size: int,
+                 fp8_gemm_threshold: int = 0):
+        self._block = FP8FlowMoECompute(config, d_model, hidden_size, 1, fp8_gemm_threshold)
+        self._route = {}
+
+    @property
+    def block(self) -> FP8FlowMoECompute:
+        return self._block
+
+    def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
+        self._block.set_weights(w1, w2, w3)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        _lib.require_device(x, "x")
+        T = x.numel() // x.shape[-1]
+        key = (T, x.device)
+        r = self._route.get(key)
+        if r is None:
+            r = self._route[key] = (torch.ones(T, 1, dtype=torch.float32, device=x.device),
+                                    torch.zeros(T, 1, dtype=torch.int64, device=x.device))
+        return self._block(x, r[0], r[1])
 
 
 def _gran(kind):

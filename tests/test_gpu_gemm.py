@@ -101,9 +101,14 @@ def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros):
 
 @pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
 @pytest.mark.parametrize("balanced", [False, True])
-def test_ragged_k_weight_grad(dev, kind, balanced):
+@pytest.mark.parametrize("splits", [None, "3"])
+def test_ragged_k_weight_grad(dev, kind, balanced, splits, monkeypatch):
     """Skewed routing with a zero-token expert keeps the tiles in launch
-    order; balanced routing takes the contiguous per-XCD split."""
+    order; balanced routing takes the contiguous per-XCD split.  splits = 3
+    forces the split-K form (fp32 partials + ordered reduction; slices of the
+    small experts are empty), except for the fp32-scale kind, which has none."""
+    if splits is not None:
+        monkeypatch.setenv("FM_RK_SPLITS", splits)
     E, T, K, D, H = 6, 2500, 2, 256, 256
     k = KINDS[kind]
     x = randn_bf16((T, D), seed=5)

@@ -95,8 +95,13 @@ def test_bf16_block_matches_reference_loop(dev, param_dtype):
     assert grads["w1"].dtype == param_dtype
 
 
-def test_threshold_mixed_fp8_and_bf16(dev):
-    """Experts with >= threshold assignments take FP8, the rest BF16."""
+@pytest.mark.parametrize("splits", [None, "2"])
+def test_threshold_mixed_fp8_and_bf16(dev, splits, monkeypatch):
+    """Experts with >= threshold assignments take FP8, the rest BF16 (with
+    splits = 2 the weight gradients take the split-K form, whose reduction
+    must leave the other precision's experts alone)."""
+    if splits is not None:
+        monkeypatch.setenv("FM_RK_SPLITS", splits)
     T, D, H, E, K = 1024, 256, 256, 4, 1
     x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=9)
     idx = torch.tensor([0] * 600 + [1] * 300 + [2] * 124, dtype=torch.int64).reshape(T, 1)
