@@ -4,6 +4,7 @@ from nanopysche_amd.flow_moe import (  # noqa: F401
     FP8_BLOCK_SIZE,
     FP8FlowMoECompute,
     FP8FlowMoEConfig,
+    FP8SharedExpertCompute,
     dequantize_from_fp8,
     fp8_grouped_gemm,
     fused_permute_pad,
