@@ -669,6 +669,12 @@ class FP8FlowMoECompute:
         # Run the dW2 grouped GEMM on a second stream beside dH (False keeps
         # every launch on the caller's stream).
         self.overlap_streams = True
+        # One group, every token in it with weight 1 (set by
+        # FP8SharedExpertCompute): the routing plan is the identity, built once
+        # per token count, and the outputs are the padded buffers' first rows
+        # (no unpermute copies).
+        self._dense = False
+        self._dense_plans = {}
 
     def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
         for w in (w1, w2, w3):
@@ -721,9 +727,15 @@ class FP8FlowMoECompute:
         E, H = self.num_experts, self.hidden_size
         K = indices.shape[1]
         fp8_kind, use_bf16 = self.modes(T * K)
-        plan = route_tokens(indices, E, self.fp8_gemm_threshold if fp8_kind is not None else 1 << 62)
-        wts = weights.to(torch.float32).contiguous()
         dev = x.device
+        thr = self.fp8_gemm_threshold if fp8_kind is not None else 1 << 62
+        if self._dense:
+            plan = self._dense_plans.get((T, dev))
+            if plan is None:
+                plan = self._dense_plans[(T, dev)] = route_tokens(indices, E, thr)
+        else:
+            plan = route_tokens(indices, E, thr)
+        wts = weights.to(torch.float32).contiguous()
         R = plan.rows_max
         GU = torch.empty(R, 2 * H, dtype=torch.bfloat16, device=dev)
         Y = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
@@ -747,7 +759,7 @@ class FP8FlowMoECompute:
             hrow, hcol = _wrap(q, s, qt, st, kind)
             h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
-        out = fused_unpermute_unpad(Y, plan, wts)
+        out = Y[:T] if self._dense else fused_unpermute_unpad(Y, plan, wts)
         if self.capture_intermediates is not None:
             self.capture_intermediates["gate_up"] = GU.detach().clone()
         ctx.compute = self
@@ -757,7 +769,7 @@ class FP8FlowMoECompute:
         ctx.saved_hcols = h_cols
         ctx.wdtypes = (w1.dtype, w2.dtype, w3.dtype)
         ctx.save_for_backward(wts, GU, Y)
-        return out
+        return out if ctx.x_dtype == torch.bfloat16 else out.to(ctx.x_dtype)
 
     # ----------------------------------------------------------------- backward ----
     def _backward(self, ctx, grad_out):
@@ -787,7 +799,8 @@ class FP8FlowMoECompute:
             raise TypeError("expert weights must be float32 or bfloat16 (w1 and w3 alike)")
         runs = [(k, w) for k, w in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)) if k is not None]
         dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                      return_transpose=True, weights=wts, kmajor_scales=True) for kind, _ in runs}
+                                      return_transpose=True, weights=None if self._dense else wts,
+                                      kmajor_scales=True) for kind, _ in runs}
         # dW2 (contraction over each expert's tokens) runs on a second stream
         # beside dH: each alone leaves the last round of workgroups part-empty
         # when the hidden size is not a multiple of the 256-wide tile.  There
@@ -815,7 +828,7 @@ class FP8FlowMoECompute:
                     mask=mask, want=want)
             # input gradient
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
-        dx = fused_unpermute_unpad(dXp, plan, None)
+        dx = dXp[:T] if self._dense else fused_unpermute_unpad(dXp, plan, None)
         main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None
@@ -830,9 +843,12 @@ class FP8SharedExpertCompute:
     bias-free dense FFN (``model/feed_forward.py:74-80`` with silu).
 
     Every token goes to the one group with weight 1, so routing reduces to
-    padding the rows to a multiple of 128, and the same fused quantisers,
-    grouped GEMMs and SwiGLU kernels run as for the routed experts (FP8 per
-    the recipe; ``fp8_gemm_threshold`` > number of tokens selects BF16).
+    padding the rows to a multiple of 128 (the identity plan is built once
+    per token count and the output and input gradient are the first rows of
+    the padded buffers: no sort and no unpermute copies per step), and the
+    same fused quantisers, grouped GEMMs and SwiGLU kernels run as for the
+    routed experts (FP8 per the recipe; ``fp8_gemm_threshold`` > number of
+    tokens selects BF16).
     ``set_weights(w1 [H, D], w2 [H, D], w3 [H, D])`` borrows the weights
     (``w2`` stored as ``[H, D]``, i.e. the transpose of ``nn.Linear(H, D)``'s
     weight, like the expert block's); ``__call__(x [..., D]) -> [..., D]`` is
@@ -842,6 +858,7 @@ class FP8SharedExpertCompute:
     def __init__(self, config: FP8FlowMoEConfig, d_model: int, hidden_size: int,
                  fp8_gemm_threshold: int = 0):
         self._block = FP8FlowMoECompute(config, d_model, hidden_size, 1, fp8_gemm_threshold)
+        self._block._dense = True
         self._route = {}
 
     @property

@@ -85,6 +85,25 @@ def test_shared_expert_bf16_matches_expert_mlp(dev):
         assert e <= 1e-2, (name, e)
 
 
+def test_shared_expert_fp32_input_and_repeat(dev):
+    """fp32 x gives an fp32 output and gradient; a second call on the cached
+    identity plan, with other inputs, matches its own oracle."""
+    T, D, H = 384, 256, 256
+    blk = _make("flow_moe", D, H)
+    for seed in (21, 22):
+        x, w1, w2, w3, go = _case(T, D, H, seed=seed)
+        taps = {}
+        blk.block.capture_intermediates = taps
+        out, grads = _run(dev, blk, x.float(), w1, w2, w3, go)
+        assert out.dtype == torch.float32 and grads["x"].dtype == torch.float32
+        taps = {k: v.float().cpu().numpy() for k, v in taps.items()}
+        ones, zeros = torch.ones(T, 1), torch.zeros(T, 1, dtype=torch.int64)
+        ref_out, ref_grads = olayer.moe_flow_reference(x, ones, zeros, w1, w2, w3, 1, go, recipe="flow_moe",
+                                                       taps=taps)
+        assert olayer.max_rel_err(out.detach().cpu().numpy(), ref_out) <= 2e-2
+        assert olayer.max_rel_err(grads["x"].cpu().numpy(), ref_grads["x"]) <= 2e-2
+
+
 def test_shared_expert_adds_to_routed_output(dev):
     """MoE with a shared expert (model/moe.py:1383-1384): routed block output +
     shared expert output, both through the grouped GEMM path; the sum matches
