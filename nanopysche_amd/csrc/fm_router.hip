@@ -155,15 +155,23 @@ constexpr int kGateLdsFloats = 16 * 1024;
 // Sum of v[i] over the 64 lanes for 32 values per lane as a reduce-scatter:
 // each exchange halves the values a lane keeps (32 shuffles in all, against
 // 32 x 6 for separate wave sums); lane l ends with the total of value l / 2.
+// The lane's choice between v[i] and v[i + half] is made on the bits with a
+// mask: written as `up ? v[i] : v[i + half]` the compiler turned it into
+// v[i + (up ? 0 : half)], a runtime index into the 32 registers, i.e.
+// compare/select chains over all of them (~3300 instructions per call).
 __device__ __forceinline__ float wave_reduce_scatter32(float (&v)[32], int lane) {
 #pragma unroll
-  for (int o = 32, half = 16; o >= 2; o >>= 1, half >>= 1) {
-    const bool up = (lane & o) != 0;
+  for (int l = 0; l < 5; ++l) {
+    const int o = 32 >> l, half = 16 >> l;
+    const uint32_t m = (lane & o) != 0 ? 0xffffffffu : 0u;   // up: send the low half
 #pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float send = up ? v[i] : v[i + half];
-      const float keep = up ? v[i + half] : v[i];
-      v[i] = keep + __shfl_xor(send, o);
+    for (int i = 0; i < 16; ++i) {
+      if (i < half) {
+        const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + half]);
+        const float send = __uint_as_float((lo & m) | (hi & ~m));
+        const float keep = __uint_as_float((hi & m) | (lo & ~m));
+        v[i] = keep + __shfl_xor(send, o);
+      }
     }
   }
   return v[0] + __shfl_xor(v[0], 1);
@@ -174,31 +182,37 @@ __device__ __forceinline__ void load8_row(const T* row, int64_t col, float (&v)[
   load8f(row + col, v);
 }
 
+__device__ __forceinline__ void bf16x8_to_f32(const uint4 u, float (&v)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = u2f(w[j] << 16);
+    v[2 * j + 1] = u2f(w[j] & 0xffff0000u);
+  }
+}
+
+// acc[row][expert] += x chunk (8 values of each of 4 rows) . gate chunk
+__device__ __forceinline__ void router_fma_chunk(float (&acc)[32], const float (&xv)[4][8], const float* wc,
+                                                 int64_t D) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float4 w0 = *reinterpret_cast<const float4*>(wc + e * D);
+    const float4 w1 = *reinterpret_cast<const float4*>(wc + e * D + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[r * 8 + e] = fmaf(xv[r][j], wv[j], acc[r * 8 + e]);
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) {
   extern __shared__ __attribute__((aligned(16))) float wl[];   // [8][D]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = int64_t(blockIdx.x) * kRouterRows + wave * 4;
   const int64_t D = a.D;
-  {
-    // 8 D floats (<= 16 Ki) over 256 threads: at most 16 float4 each, all
-    // loads issued before the stores
-    constexpr int kPer = kGateLdsFloats / 1024;
-    float4 v[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int64_t i = (int64_t(threadIdx.x) + 256 * u) * 4;
-      const int e = int(i / D);
-      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (i < 8 * D && e < a.E) v[u] = *reinterpret_cast<const float4*>(a.w + e * a.ld_w + i % D);
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int64_t i = (int64_t(threadIdx.x) + 256 * u) * 4;
-      if (i < 8 * D) *reinterpret_cast<float4*>(&wl[i]) = v[u];
-    }
-  }
-  __syncthreads();
+  const int nc = int(D / kRouterCols);   // D % 512 == 0 (launcher)
   // rows past T re-read the last row (their sums are not stored)
   const T* rows[4];
 #pragma unroll
@@ -206,32 +220,70 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) 
     const int64_t row = r0 + r < a.T ? r0 + r : a.T - 1;
     rows[r] = static_cast<const T*>(a.x) + row * a.ld_x + lane * 8;
   }
+  // bf16 rows of at most 2048 columns: all of this wave's x loads are issued
+  // before the gate staging, so the two memory latencies overlap and the
+  // chunk loop waits on none
+  constexpr bool kWhole = sizeof(T) == 2;
+  const bool whole = kWhole && nc <= 4;
+  uint4 xr[4][4];
+  if (whole) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (c < nc) xr[c][r] = *reinterpret_cast<const uint4*>(rows[r] + int64_t(c) * kRouterCols);
+  }
+  {
+    // 8 gate rows of D <= 2048 floats over 256 threads: per row at most two
+    // float4 per thread (expert x column loop, no index division), all loads
+    // issued before the stores
+    constexpr int kPerRow = kGateLdsFloats / 8 / 1024;
+    float4 v[8][kPerRow];
+    const int Di = int(D);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int u = 0; u < kPerRow; ++u) {
+        const int c = (int(threadIdx.x) + 256 * u) * 4;
+        v[e][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < Di && e < a.E) v[e][u] = *reinterpret_cast<const float4*>(a.w + e * a.ld_w + c);
+      }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int u = 0; u < kPerRow; ++u) {
+        const int c = (int(threadIdx.x) + 256 * u) * 4;
+        if (c < Di) *reinterpret_cast<float4*>(&wl[e * Di + c]) = v[e][u];
+      }
+  }
+  __syncthreads();
   float acc[32];   // [row][expert]
 #pragma unroll
   for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-  float cur[4][8], nxt[4][8];
+  if (whole) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) load8f(rows[r], cur[r]);
-  const int nc = int(D / kRouterCols);   // D % 512 == 0 (launcher)
-  for (int c = 0; c < nc; ++c) {
-    const int cn = c + 1 < nc ? c + 1 : c;
+    for (int c = 0; c < 4; ++c) {
+      if (c < nc) {
+        float xv[4][8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) load8f(rows[r] + int64_t(cn) * kRouterCols, nxt[r]);
-    const float* wc = wl + int64_t(c) * kRouterCols + lane * 8;
+        for (int r = 0; r < 4; ++r) bf16x8_to_f32(xr[c][r], xv[r]);
+        router_fma_chunk(acc, xv, wl + int64_t(c) * kRouterCols + lane * 8, D);
+      }
+    }
+  } else {
+    float cur[4][8], nxt[4][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float4 w0 = *reinterpret_cast<const float4*>(wc + e * D);
-      const float4 w1 = *reinterpret_cast<const float4*>(wc + e * D + 4);
-      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    for (int r = 0; r < 4; ++r) load8f(rows[r], cur[r]);
+    for (int c = 0; c < nc; ++c) {
+      const int cn = c + 1 < nc ? c + 1 : c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load8f(rows[r] + int64_t(cn) * kRouterCols, nxt[r]);
+      router_fma_chunk(acc, cur, wl + int64_t(c) * kRouterCols + lane * 8, D);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[r * 8 + e] = fmaf(cur[r][j], wv[j], acc[r * 8 + e]);
+        for (int j = 0; j < 8; ++j) cur[r][j] = nxt[r][j];
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) cur[r][j] = nxt[r][j];
   }
   const float sum = wave_reduce_scatter32(acc, lane);
   const int vi = lane >> 1, r = vi >> 3, e = vi & 7;
