@@ -569,10 +569,14 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
   } else {
     const int64_t NJ = (p.n_j + kT - 1) / kT;
     const int64_t per_e = NI * NJ;
-    // split K: slice s of every tile follows all tiles of slice s - 1
-    const int64_t per_slice = p.n_tiles / p.splits;
-    t.slice = L / per_slice;
-    L %= per_slice;
+    // split K: slice s of every tile follows all tiles of slice s - 1 (no
+    // division on the unsplit path)
+    t.slice = 0;
+    if (p.splits > 1) {
+      const int64_t per_slice = p.n_tiles / p.splits;
+      t.slice = L / per_slice;
+      L -= t.slice * per_slice;
+    }
     e = L / per_e;
     const int64_t Lr = L % per_e;
     const int64_t group = Lr / (kGroupM * NJ);
