@@ -120,6 +120,66 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   }
 }
 
+// E <= 16: a wave takes 64 / EP tokens at once (EP = E rounded up to a power
+// of two; lane = token slot * EP + expert), so the reductions run over EP
+// lanes (log2 EP steps) for NT tokens together instead of over 64 lanes for
+// one token.  Same selection rule, weights (sum over k in k order) and
+// per-wave softmax partials as topk_kernel.
+template <int EP>
+__global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
+  constexpr int NT = 64 / EP;
+  const int lane = threadIdx.x & 63, g = lane / EP, e = lane % EP;
+  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t n_waves = int64_t(gridDim.x) * 4;
+  const bool ev = e < a.E;
+  float psum = 0.f;
+  for (int64_t tg = wave; tg * NT < a.T; tg += n_waves) {
+    const int64_t t = tg * NT + g;
+    const bool tv = t < a.T;
+    const float v = (tv && ev) ? a.logits[t * a.ld + e] : -INFINITY;
+    float sc = a.sigmoid ? (ev ? 1.f / (1.f + expf(-v)) : -INFINITY) : v;
+    if (a.prob_partial) {
+      float m = v;
+#pragma unroll
+      for (int off = EP / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      const float ex = ev ? expf(v - m) : 0.f;
+      float sm = ex;
+#pragma unroll
+      for (int off = EP / 2; off > 0; off >>= 1) sm += __shfl_xor(sm, off);
+      if (tv) psum += ex / sm;
+    }
+    float top_first = 0.f, wsum = 0.f, my_w = 0.f;
+    int my_i = 0;
+    for (int k = 0; k < a.K; ++k) {
+      float bv = ev ? sc : -INFINITY;
+      int bi = ev ? e : 0x7fffffff;
+#pragma unroll
+      for (int off = EP / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (bi == e) sc = -INFINITY;   // the winner leaves the race
+      const float lg = __shfl(v, g * EP + (bi & (EP - 1)));
+      if (k == 0) top_first = lg;
+      const float wk = a.sigmoid ? bv : expf(lg - top_first);
+      wsum += wk;
+      if (e == k) { my_w = wk; my_i = bi; }
+    }
+    if (tv && e < a.K) {
+      const float wn = a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum;
+      a.w[t * a.K + e] = wn;
+      if (a.idx_i64) static_cast<int64_t*>(a.idx)[t * a.K + e] = my_i;
+      else static_cast<int32_t*>(a.idx)[t * a.K + e] = my_i;
+    }
+  }
+  if (a.prob_partial) {
+#pragma unroll
+    for (int off = EP; off < 64; off <<= 1) psum += __shfl_xor(psum, off);
+    if (lane < a.E) a.prob_partial[wave * a.E + lane] = psum;
+  }
+}
+
 // one block: P_e = sum over the per-wave partials / T; loss = E * sum_e f_e P_e.
 // Expert by expert, the 256 threads sum strided partials and meet in a fixed
 // LDS tree (a serial sum of the 1024 partials per expert took ~140 us).
@@ -447,8 +507,13 @@ int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int
   if (T == 0) return 0;
   TopkArgs a{logits, T, ld, E, K, gating == FM_GATING_SIGMOID, weights, indices, indices_i64,
              prob_partial};
-  hipLaunchKernelGGL(topk_kernel, dim3(unsigned(n_waves / 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  const dim3 grid(unsigned(n_waves / 4)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (E <= 2) hipLaunchKernelGGL(topk_small_kernel<2>, grid, block, 0, s, a);
+  else if (E <= 4) hipLaunchKernelGGL(topk_small_kernel<4>, grid, block, 0, s, a);
+  else if (E <= 8) hipLaunchKernelGGL(topk_small_kernel<8>, grid, block, 0, s, a);
+  else if (E <= 16) hipLaunchKernelGGL(topk_small_kernel<16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(topk_kernel, grid, block, 0, s, a);
   return check_launch("fm_topk_gating");
 }
 

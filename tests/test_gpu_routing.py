@@ -18,10 +18,14 @@ def _np(t):
 
 
 @pytest.mark.parametrize("E,K,gating", [(4, 1, "softmax"), (8, 2, "softmax"), (256, 8, "sigmoid"),
-                                        (64, 6, "softmax"), (3, 3, "sigmoid")])
+                                        (64, 6, "softmax"), (3, 3, "sigmoid"), (1, 1, "softmax"),
+                                        (2, 1, "sigmoid"), (12, 3, "softmax"), (16, 4, "sigmoid")])
 def test_topk_gating(dev, E, K, gating):
+    """T = 4093 tokens: the waves of the E <= 16 kernel (64 / EP tokens at a
+    time) end on a partial group."""
+    T = 4093
     g = torch.Generator().manual_seed(E * 10 + K)
-    logits = torch.randn(4096, E, generator=g)
+    logits = torch.randn(T, E, generator=g)
     w, idx, part = fm.topk_gating(logits.to(dev), K, gating, return_prob_partial=True)
     fn = orouting.softmax_topk if gating == "softmax" else orouting.sigmoid_topk
     rw, ridx = fn(logits.numpy(), K)
@@ -30,7 +34,7 @@ def test_topk_gating(dev, E, K, gating):
     if gating == "softmax" and K == 1:
         assert np.all(_np(w) == 1.0)  # model/moe.py:253-254 with one selected logit
     plan = fm.route_tokens(idx, E)
-    loss = fm.load_balancing_loss(part, plan.counts, 4096)
+    loss = fm.load_balancing_loss(part, plan.counts, T)
     ref = orouting.load_balancing_loss(logits.numpy(), ridx, E)
     assert abs(loss.item() - ref) <= 1e-5 * max(1.0, abs(ref))
 
