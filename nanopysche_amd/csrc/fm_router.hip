@@ -484,7 +484,25 @@ __global__ __launch_bounds__(256) void router_dw_kernel(RouterBwdArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[e][j] = 0.f;
   if (col < a.D) {
-    for (int64_t t = t_lo + wave; t < t_hi; t += 4) {
+    int64_t t = t_lo + wave;
+    // four of the wave's rows per round: all their loads before any FMA (one
+    // memory latency per four rows), the FMAs in row order as below
+    for (; t + 12 < t_hi; t += 16) {
+      float xv[4][8], dv[4][EG];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        load8f(x + (t + 4 * u) * a.ld_x + col, xv[u]);
+#pragma unroll
+        for (int e = 0; e < EG; ++e) dv[u][e] = e0 + e < a.E ? a.dl[(t + 4 * u) * a.ld_dl + e0 + e] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < EG; ++e)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(dv[u][e], xv[u][j], acc[e][j]);
+    }
+    for (; t < t_hi; t += 4) {
       float xv[8];
       load8f(x + t * a.ld_x + col, xv);
 #pragma unroll
