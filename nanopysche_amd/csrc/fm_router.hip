@@ -543,6 +543,9 @@ __global__ __launch_bounds__(256) void router_db_kernel(const float* dl, int64_t
   __shared__ float red[256];
   const int e = blockIdx.x;
   float v = 0.f;
+  // unrolled so the loads of several rows are in flight at once; the adds
+  // keep their order
+#pragma unroll 8
   for (int64_t t = threadIdx.x; t < T; t += 256) v += dl[t * ld_dl + e];
   red[threadIdx.x] = v;
   __syncthreads();
