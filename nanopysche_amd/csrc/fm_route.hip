@@ -180,27 +180,28 @@ __global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
   }
 }
 
-// one block: P_e = sum over the per-wave partials / T; loss = E * sum_e f_e P_e.
-// Expert by expert, the 256 threads sum strided partials and meet in a fixed
-// LDS tree (a serial sum of the 1024 partials per expert took ~140 us).
-__global__ __launch_bounds__(256) void aux_loss_kernel(const float* prob_partial, int64_t n_waves,
+// one block of 512 threads: wave w sums experts w, w + 8, ... -- each lane a
+// strided run of the per-wave partials, then a fixed shuffle tree -- so no
+// workgroup barrier sits inside the per-expert sums; thread 0 then adds
+// f_e * P_e in expert order.  loss = E * sum_e f_e P_e, P_e = sum / T.
+__global__ __launch_bounds__(512) void aux_loss_kernel(const float* prob_partial, int64_t n_waves,
                                                        const int32_t* counts, int E, int64_t T,
                                                        float* loss) {
-  __shared__ float red[256];
-  float acc = 0.f;   // thread 0
-  for (int e = 0; e < E; ++e) {
+  __shared__ float term[1024];   // E <= 1024 (launcher)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = wave; e < E; e += 8) {
     float p = 0.f;
-    for (int64_t w = threadIdx.x; w < n_waves; w += 256) p += prob_partial[w * E + e];
-    red[threadIdx.x] = p;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) acc += (float(counts[e]) / float(T)) * (red[0] / float(T));
-    __syncthreads();
+    for (int64_t w = lane; w < n_waves; w += 64) p += prob_partial[w * E + e];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+    if (lane == 0) term[e] = (float(counts[e]) / float(T)) * (p / float(T));
   }
-  if (threadIdx.x == 0) loss[0] = float(E) * acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc += term[e];
+    loss[0] = float(E) * acc;
+  }
 }
 
 // ----------------------------------------------------------------- sort ----
@@ -520,8 +521,8 @@ int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int
 int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
                 float* loss, void* stream) {
   FM_REQUIRE(prob_partial && counts && loss, "fm_aux_loss: null pointer");
-  FM_REQUIRE(T > 0 && E > 0, "fm_aux_loss: T and E must be positive");
-  hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+  FM_REQUIRE(T > 0 && E > 0 && E <= 1024, "fm_aux_loss: T must be positive and E in [1, 1024] (got %d)", E);
+  hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(512), 0, static_cast<hipStream_t>(stream),
                      prob_partial, n_waves, counts, E, T, loss);
   return check_launch("fm_aux_loss");
 }
