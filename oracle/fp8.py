@@ -56,13 +56,16 @@ def _e4m3_positive_table() -> np.ndarray:
 _POS = _e4m3_positive_table()
 
 
+_LUT = np.empty(256, dtype=np.float32)
+_LUT[:127] = _POS
+_LUT[127] = np.nan
+_LUT[128:] = -_LUT[:128]
+
+
 def e4m3_decode(codes: np.ndarray) -> np.ndarray:
-    """uint8 e4m3fn codes -> float32 (0x7F/0xFF -> NaN)."""
-    c = np.asarray(codes, dtype=np.uint8)
-    mag = c & 0x7F
-    out = np.where(mag == 0x7F, np.nan, _POS[np.minimum(mag, 126)])
-    out = np.where(c & 0x80, -out, out)
-    return out.astype(np.float32)
+    """uint8 e4m3fn codes -> float32 (0x7F/0xFF -> NaN), by a 256-entry table
+    built from the OCP formula above."""
+    return _LUT[np.asarray(codes, dtype=np.uint8)]
 
 
 def e4m3_encode(x: np.ndarray, saturate: bool = False) -> np.ndarray:
@@ -96,6 +99,34 @@ def e4m3_encode(x: np.ndarray, saturate: bool = False) -> np.ndarray:
     return code
 
 
+def e4m3_encode_fast(x: np.ndarray, saturate: bool = False) -> np.ndarray:
+    """``e4m3_encode`` through torch's CPU cast to float8_e4m3fn (RNE,
+    non-saturating), for the large arrays of the layer oracle: the search
+    encoder above costs ~1 s per million values.  Same results bit for bit
+    (tests/test_oracle_fp8.py pins the two on every float32 bit pattern class
+    that matters: ~1M random values, all e4m3 midpoints, the overflow edges and
+    NaN); NaN inputs are mapped to 0x7F with their sign as the spec does."""
+    import torch
+
+    x = np.asarray(x, dtype=np.float32)
+    nan_in = np.isnan(x)
+    y = np.clip(x, -E4M3_MAX, E4M3_MAX) if saturate else x
+    code = torch.from_numpy(np.ascontiguousarray(y)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    if nan_in.any():
+        code = np.where(nan_in, np.uint8(0x7F) | (np.signbit(x).astype(np.uint8) << 7), code)
+    return code.astype(np.uint8)
+
+
+# arrays at least this large take the torch-cast encoder
+_FAST_ENCODE_MIN = 1 << 16
+
+
+def _encode(x: np.ndarray, saturate: bool = False) -> np.ndarray:
+    if np.size(x) >= _FAST_ENCODE_MIN:
+        return e4m3_encode_fast(x, saturate)
+    return e4m3_encode(x, saturate)
+
+
 # ------------------------------------------------------------------ e8m0 ----
 def f32_biased_exponent(x: np.ndarray) -> np.ndarray:
     return ((np.asarray(x, dtype=np.float32).view(np.uint32) >> 23) & 0xFF).astype(np.int32)
@@ -103,7 +134,7 @@ def f32_biased_exponent(x: np.ndarray) -> np.ndarray:
 
 def e8m0_decode(codes: np.ndarray) -> np.ndarray:
     c = np.asarray(codes, dtype=np.int32)
-    return np.ldexp(np.float32(1.0), c - 127).astype(np.float32)
+    return np.ldexp(np.float32(1.0), c - 127).astype(np.float32, copy=False)
 
 
 def pow2_ceil(r: np.ndarray) -> np.ndarray:
@@ -119,14 +150,43 @@ def pow2_ceil(r: np.ndarray) -> np.ndarray:
 def block_scale(amax: np.ndarray, pow2: bool) -> np.ndarray:
     """scale = max(amax, 1e-12) / 448 (fp32 IEEE division); pow2 rounds up."""
     amax = np.maximum(np.asarray(amax, dtype=np.float32), AMAX_FLOOR)
-    s = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+    s = (amax / np.float32(E4M3_MAX)).astype(np.float32, copy=False)
     return pow2_ceil(s) if pow2 else s
 
 
+# Arrays of at least _FAST_ENCODE_MIN elements take torch CPU ops (threaded)
+# for the elementwise steps below; each step is the same IEEE fp32 operation
+# as the numpy one (division, max of absolute values, product with a scale),
+# and tests/test_oracle_fp8.py pins both paths equal bit for bit.
+def _tt(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+
+
+def _amax(xb: np.ndarray, axis) -> np.ndarray:
+    if np.size(xb) >= _FAST_ENCODE_MIN:
+        return _tt(xb).abs().amax(dim=axis).numpy()
+    return np.abs(xb).max(axis=axis)
+
+
 def _quant_with_scale(x: np.ndarray, s: np.ndarray) -> np.ndarray:
-    y = (x.astype(np.float32) / s.astype(np.float32)).astype(np.float32)
+    if np.size(x) >= _FAST_ENCODE_MIN:
+        y = (_tt(x) / _tt(s)).clamp_(-E4M3_MAX, E4M3_MAX).numpy()
+        return _encode(y)
+    y = (x.astype(np.float32, copy=False) / s.astype(np.float32, copy=False)).astype(np.float32, copy=False)
     y = np.clip(y, -E4M3_MAX, E4M3_MAX)
-    return e4m3_encode(y)
+    return _encode(y)
+
+
+def _scaled_decode(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """decode(q) * s with s broadcast against q's shape."""
+    if np.size(q) >= _FAST_ENCODE_MIN:
+        import torch
+
+        v = torch.from_numpy(np.ascontiguousarray(q, dtype=np.uint8)).view(torch.float8_e4m3fn).float()
+        return (v * _tt(s)).numpy()
+    return e4m3_decode(q) * np.asarray(s, dtype=np.float32)
 
 
 def quant_1x128(x: np.ndarray, pow2: bool = False):
@@ -135,7 +195,7 @@ def quant_1x128(x: np.ndarray, pow2: bool = False):
     R, C = x.shape
     assert C % BLOCK == 0
     xb = x.reshape(R, C // BLOCK, BLOCK)
-    s = block_scale(np.abs(xb).max(axis=-1), pow2)
+    s = block_scale(_amax(xb, -1), pow2)
     q = _quant_with_scale(xb, s[..., None]).reshape(R, C)
     return q, s
 
@@ -153,7 +213,7 @@ def quant_128x128(w: np.ndarray, pow2: bool = False):
     R, C = w.shape
     assert R % BLOCK == 0 and C % BLOCK == 0
     wb = w.reshape(R // BLOCK, BLOCK, C // BLOCK, BLOCK)
-    s = block_scale(np.abs(wb).max(axis=(1, 3)), pow2)
+    s = block_scale(_amax(wb, (1, 3)), pow2)
     q = _quant_with_scale(wb, s[:, None, :, None]).reshape(R, C)
     return q, s
 
@@ -175,10 +235,10 @@ def quant_mx_1x32(x: np.ndarray):
     R, C = x.shape
     assert C % MX_BLOCK == 0
     xb = x.reshape(R, C // MX_BLOCK, MX_BLOCK)
-    code = mx_scale_code(np.abs(xb).max(axis=-1))
-    inv = np.ldexp(np.float32(1.0), 127 - code.astype(np.int32)).astype(np.float32)
-    y = (xb * inv[..., None]).astype(np.float32)
-    q = e4m3_encode(y, saturate=True).reshape(R, C)
+    code = mx_scale_code(_amax(xb, -1))
+    inv = np.ldexp(np.float32(1.0), 127 - code.astype(np.int32)).astype(np.float32, copy=False)
+    y = (xb * inv[..., None]).astype(np.float32, copy=False)
+    q = _encode(y, saturate=True).reshape(R, C)
     return q, code
 
 
@@ -191,21 +251,21 @@ def quant_mx_32x1(x: np.ndarray):
 # ------------------------------------------------------------- dequant ----
 def dequant_1x128(q, s):
     R, C = q.shape
-    v = e4m3_decode(q).reshape(R, C // BLOCK, BLOCK) * s[..., None].astype(np.float32)
-    return v.astype(np.float32).reshape(R, C)
+    v = _scaled_decode(q.reshape(R, C // BLOCK, BLOCK), np.asarray(s, dtype=np.float32)[..., None])
+    return v.reshape(R, C)
 
 
 def dequant_128x128(q, s):
     R, C = q.shape
-    v = e4m3_decode(q).reshape(R // BLOCK, BLOCK, C // BLOCK, BLOCK)
-    v = v * s[:, None, :, None].astype(np.float32)
-    return v.astype(np.float32).reshape(R, C)
+    v = _scaled_decode(q.reshape(R // BLOCK, BLOCK, C // BLOCK, BLOCK),
+                       np.asarray(s, dtype=np.float32)[:, None, :, None])
+    return v.reshape(R, C)
 
 
 def dequant_mx_1x32(q, code):
     R, C = q.shape
-    v = e4m3_decode(q).reshape(R, C // MX_BLOCK, MX_BLOCK) * e8m0_decode(code)[..., None]
-    return v.astype(np.float32).reshape(R, C)
+    v = _scaled_decode(q.reshape(R, C // MX_BLOCK, MX_BLOCK), e8m0_decode(code)[..., None])
+    return v.reshape(R, C)
 
 
 # ---------------------------------------------------- scaling-aware transpose ----
@@ -222,21 +282,28 @@ def scaling_aware_transpose(q: np.ndarray, s: np.ndarray):
     R, C = q.shape
     assert R % BLOCK == 0 and C % BLOCK == 0
     s = np.asarray(s, dtype=np.float32)
-    s_full = np.repeat(s, BLOCK, axis=1)  # [R, C] per-element row scale
-    v = (e4m3_decode(q) * s_full).astype(np.float32)
-    st = s_full.reshape(R // BLOCK, BLOCK, C).max(axis=1)  # [R/128, C]
-    st_full = np.repeat(st, BLOCK, axis=0)  # [R, C]
-    y = (v / st_full).astype(np.float32)
-    y = np.clip(y, -E4M3_MAX, E4M3_MAX)
-    qt = np.ascontiguousarray(e4m3_encode(y).T)
-    return qt, st
+    # per-element row scale s[r, c // 128], as a broadcast over [R, C/128, 128]
+    v = _scaled_decode(q.reshape(R, C // BLOCK, BLOCK), s[..., None])
+    st = s.reshape(R // BLOCK, BLOCK, C // BLOCK).max(axis=1)  # [R/128, C/128]
+    # column block j of row block b takes the largest row scale of the tile
+    y = _quant_with_scale(v.reshape(R // BLOCK, BLOCK, C // BLOCK, BLOCK), st[:, None, :, None])
+    qt = np.ascontiguousarray(y.reshape(R, C).T)
+    return qt, np.repeat(st, BLOCK, axis=1)
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    """float32 -> bfloat16 (RNE) -> float32, written with integer ops."""
+    """float32 -> bfloat16 (RNE) -> float32, written with integer ops (torch's
+    bf16 cast for large arrays, NaN canonicalised the same way; pinned equal)."""
     x = np.asarray(x, dtype=np.float32)
-    b = x.view(np.uint32).astype(np.uint64)
-    lsb = (b >> 16) & 1
-    r = ((b + 0x7FFF + lsb) >> 16) << 16
-    r = np.where(np.isnan(x), 0x7FC00000, r)
-    return r.astype(np.uint32).view(np.float32)
+    if x.size >= _FAST_ENCODE_MIN:
+        import torch
+
+        r = torch.from_numpy(np.ascontiguousarray(x)).bfloat16().float().numpy()
+        nan = np.isnan(x)
+        return np.where(nan, np.float32(np.nan), r).astype(np.float32, copy=False) if nan.any() else r
+    b = x.view(np.uint32)
+    nan = (b & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    r = b + (np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1)))   # no wrap for non-NaN b
+    r &= np.uint32(0xFFFF0000)
+    r = np.where(nan, np.uint32(0x7FC00000), r)
+    return r.view(np.float32)

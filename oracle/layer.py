@@ -113,8 +113,16 @@ def _mm(a, b_t):
             @ torch.from_numpy(np.ascontiguousarray(b_t, dtype=np.float32)).T).numpy()
 
 
-def _silu(g):
-    return (g / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+def _silu_sigmoid(g):
+    """(silu(g), sigmoid(g)) of fp32 g, each evaluated in float64 and rounded
+    to fp32 once (torch CPU ops, threaded)."""
+    g64 = _t(g).double()
+    sg = 1.0 / (1.0 + torch.exp(-g64))
+    return (g64 * sg).float().numpy(), sg.float().numpy()
 
 
 def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=None,
@@ -134,14 +142,16 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
     K = indices.shape[1]
     H = w1.shape[0] // E
     xs = _bf16(_np(x))
-    wts = _np(weights).astype(np.float32)
-    rt = orouting.sort_assignments(indices.cpu().numpy(), E)
+    wts = _np(weights).astype(np.float32, copy=False)
+    # slots whose index lies outside [0, E) (experts held by another GPU) are
+    # dropped, as the reference loop only walks the local experts
+    rt = orouting.sort_assignments(indices.cpu().numpy(), E, drop_out_of_range=True)
     offs = rt["offsets"]
     Xp = orouting.permute_pad(xs, rt["assign_of_row"], K)
     fp8 = recipe is not None
     # FP8 recipes quantise the parameters' own values (fp32 master weights stay
     # fp32); the BF16 path multiplies their bf16 rounding
-    wv = (lambda a: _np(a).astype(np.float32)) if fp8 else (lambda a: _bf16(_np(a)))
+    wv = (lambda a: _np(a).astype(np.float32, copy=False)) if fp8 else (lambda a: _bf16(_np(a)))
     W1 = wv(w1).reshape(E, H, D)
     W2 = wv(w2).reshape(E, H, D)
     W3 = wv(w3).reshape(E, H, D)
@@ -158,8 +168,9 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         GU[r0:r1] = _bf16(_mm(Xv[r0:r1], Bv))
     if taps is not None and "gate_up" in taps:
         GU = _bf16(np.asarray(taps["gate_up"], dtype=np.float32)[:Mp])
-    g, u = GU[:, :H], GU[:, H:]
-    h = (_silu(g) * u).astype(np.float32)
+    g, u = np.ascontiguousarray(GU[:, :H]), np.ascontiguousarray(GU[:, H:])
+    silu_g, sg = _silu_sigmoid(g)
+    h = (_t(silu_g) * _t(u)).numpy()
     Hv = _q_rows(h, recipe) if fp8 else _bf16(h)
     for e in range(E):
         r0, r1 = offs[e], offs[e + 1]
@@ -177,9 +188,13 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
     a_rows = rt["assign_of_row"]
     valid = a_rows >= 0
     dYp = np.zeros((Mp, D), np.float32)
-    dYp[valid] = (wts.reshape(-1)[a_rows[valid], None] * dO[a_rows[valid] // K]).astype(np.float32)
-    dw = np.einsum("td,tkd->tk", dO.astype(np.float64),
-                   Y[rt["row_of"].reshape(T, K)].astype(np.float64)).astype(np.float32)
+    av = torch.from_numpy(a_rows[valid].astype(np.int64))
+    dYp[valid] = (_t(wts.reshape(-1))[av, None] * _t(dO)[av // K]).numpy()
+    ro = torch.from_numpy(rt["row_of"].reshape(T, K).astype(np.int64))
+    dO64, Y64 = _t(dO).double(), _t(Y).double()
+    dw = torch.stack([(dO64 * Y64[ro[:, k].clamp(min=0)]).sum(-1) for k in range(K)], dim=1).float()
+    dw[ro < 0] = 0.0
+    dw = dw.numpy()
     if fp8:
         dYv = _q_rows(dYp, recipe)
         dYvT = _q_cols(dYp, recipe)          # [D, Mp]
@@ -195,10 +210,10 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         dH[r0:r1] = _bf16(_mm(dYv[r0:r1], Bv))
     if taps is not None and "dh" in taps:
         dH = _bf16(np.asarray(taps["dh"], dtype=np.float32)[:Mp])
-    sg = (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
-    dg = (dH * u * sg * (1.0 + g * (1.0 - sg))).astype(np.float32)
-    du = (dH * (g * sg)).astype(np.float32)
-    dGU = np.concatenate([dg, du], axis=1)
+    tdH, tu, tg, tsg = _t(dH), _t(u), _t(g), _t(sg)
+    dg = tdH * tu * tsg * (1.0 + tg * (1.0 - tsg))
+    du = tdH * (tg * tsg)
+    dGU = torch.cat([dg, du], dim=1).numpy()
     if fp8:
         dGUv = _q_rows(dGU, recipe)
         dGUvT = _q_cols(dGU, recipe)         # [2H, Mp]

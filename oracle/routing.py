@@ -41,17 +41,17 @@ def softmax_topk(logits: np.ndarray, k: int):
     idx = topk_lower_index(logits, k)
     sel = np.take_along_axis(logits, idx, axis=-1).astype(np.float64)
     e = np.exp(sel - sel.max(axis=-1, keepdims=True))
-    w = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    w = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32, copy=False)
     return w, idx
 
 
 def sigmoid_topk(logits: np.ndarray, k: int):
     """model/moe.py:257-265 (score bias, if any, is already inside ``logits``)."""
     logits = np.asarray(logits, dtype=np.float32)
-    s = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))).astype(np.float32)
+    s = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))).astype(np.float32, copy=False)
     idx = topk_lower_index(s, k)
     sel = np.take_along_axis(s, idx, axis=-1).astype(np.float64)
-    w = (sel / (sel.sum(axis=-1, keepdims=True) + 1e-8)).astype(np.float32)
+    w = (sel / (sel.sum(axis=-1, keepdims=True) + 1e-8)).astype(np.float32, copy=False)
     return w, idx
 
 
@@ -68,32 +68,39 @@ def load_balancing_loss(logits: np.ndarray, idx: np.ndarray, num_experts: int) -
     return float(num_experts * (f * P).sum())
 
 
-def sort_assignments(idx: np.ndarray, num_experts: int, pad: int = PAD):
+def sort_assignments(idx: np.ndarray, num_experts: int, pad: int = PAD, drop_out_of_range: bool = False):
     """Stable counting sort of the flat assignments a = t*K + k by expert.
+
+    With ``drop_out_of_range`` an index outside [0, E) -- a slot routed to an
+    expert this GPU does not hold -- takes no row (``row_of`` = -1) and is not
+    counted, as the reference loop never selects it (``model/moe.py:1560-1567``
+    walks only the local experts); otherwise such an index raises.
 
     Returns a dict:
       counts      [E] int32       assignments per expert
       offsets     [E+1] int32     padded group starts (multiples of ``pad``)
-      row_of      [T*K] int32     padded row of each assignment
+      row_of      [T*K] int32     padded row of each assignment (-1: dropped)
       assign_of_row [offsets[E]] int32  assignment in each row, -1 for pad
-      perm        [T*K] int64     assignments in sorted order (unpadded)
+      perm        [A'] int64      kept assignments in sorted order (unpadded)
     """
     flat = np.asarray(idx, dtype=np.int64).reshape(-1)
-    if flat.size and (flat.min() < 0 or flat.max() >= num_experts):
+    valid = (flat >= 0) & (flat < num_experts)
+    if not drop_out_of_range and not valid.all():
         raise ValueError("expert index out of range")
-    counts = np.bincount(flat, minlength=num_experts).astype(np.int64)
-    perm = np.argsort(flat, kind="stable")
+    key = np.where(valid, flat, num_experts)
+    counts = np.bincount(key, minlength=num_experts + 1)[:num_experts].astype(np.int64)
+    perm = np.argsort(key, kind="stable")[: int(counts.sum())]
     padded = (counts + pad - 1) // pad * pad
     offsets = np.zeros(num_experts + 1, dtype=np.int64)
     offsets[1:] = np.cumsum(padded)
     starts = np.zeros(num_experts + 1, dtype=np.int64)
     starts[1:] = np.cumsum(counts)
-    row_of = np.empty(flat.size, dtype=np.int64)
-    pos = np.arange(flat.size)
+    row_of = np.full(flat.size, -1, dtype=np.int64)
+    pos = np.arange(perm.size)
     e_sorted = flat[perm]
     row_of[perm] = offsets[e_sorted] + (pos - starts[e_sorted])
     assign_of_row = np.full(int(offsets[-1]), -1, dtype=np.int64)
-    assign_of_row[row_of] = np.arange(flat.size)
+    assign_of_row[row_of[perm]] = perm
     return dict(
         counts=counts.astype(np.int32),
         offsets=offsets.astype(np.int32),
@@ -105,25 +112,33 @@ def sort_assignments(idx: np.ndarray, num_experts: int, pad: int = PAD):
 
 def permute_pad(x: np.ndarray, assign_of_row: np.ndarray, top_k: int) -> np.ndarray:
     """Row r of the output is x[assign_of_row[r] // K], zeros for pad rows."""
-    x = np.asarray(x)
-    out = np.zeros((assign_of_row.size, x.shape[1]), dtype=x.dtype)
-    valid = assign_of_row >= 0
-    out[valid] = x[assign_of_row[valid] // top_k]
-    return out
+    import torch
+
+    xt = torch.from_numpy(np.ascontiguousarray(x))
+    a = torch.from_numpy(np.asarray(assign_of_row).astype(np.int64))
+    valid = (a >= 0)[:, None]
+    out = xt.index_select(0, a.clamp(min=0) // top_k)
+    return torch.where(valid, out, torch.zeros((), dtype=out.dtype)).numpy()
 
 
 def unpermute_unpad(y: np.ndarray, row_of: np.ndarray, weights, num_tokens: int, top_k: int):
-    """out[t] = sum_k w[t,k] * y[row_of[t*K+k]], summed in fp32 in k order."""
-    y = np.asarray(y, dtype=np.float32)
-    rows = y[np.asarray(row_of).reshape(num_tokens, top_k)]  # [T, K, D]
+    """out[t] = sum_k w[t,k] * y[row_of[t*K+k]], summed in fp32 in k order
+    (each product and sum rounded to fp32); slots with row_of = -1 (dropped)
+    add nothing.  Torch CPU ops on the numpy buffers."""
+    import torch
+
+    yt = torch.from_numpy(np.ascontiguousarray(y, dtype=np.float32))
+    ro = torch.from_numpy(np.asarray(row_of).reshape(num_tokens, top_k).astype(np.int64))
     if weights is None:
-        w = np.ones((num_tokens, top_k), dtype=np.float32)
+        w = torch.ones(num_tokens, top_k, dtype=torch.float32)
     else:
-        w = np.asarray(weights, dtype=np.float32).reshape(num_tokens, top_k)
-    acc = np.zeros((num_tokens, y.shape[1]), dtype=np.float32)
+        w = torch.from_numpy(np.ascontiguousarray(weights, dtype=np.float32).reshape(num_tokens, top_k))
+    acc = torch.zeros(num_tokens, yt.shape[1], dtype=torch.float32)
     for k in range(top_k):
-        acc = (acc + (w[:, k : k + 1] * rows[:, k]).astype(np.float32)).astype(np.float32)
-    return acc
+        keep = (ro[:, k] >= 0)[:, None]
+        term = w[:, k : k + 1] * yt.index_select(0, ro[:, k].clamp(min=0))
+        acc = acc + torch.where(keep, term, torch.zeros((), dtype=torch.float32))
+    return acc.numpy()
 
 
 def router_logits(x: np.ndarray, w: np.ndarray, b=None, score_bias=None) -> np.ndarray:
@@ -134,4 +149,4 @@ def router_logits(x: np.ndarray, w: np.ndarray, b=None, score_bias=None) -> np.n
         out = out + np.asarray(b, dtype=np.float64)
     if score_bias is not None:
         out = out + np.asarray(score_bias, dtype=np.float64)
-    return out.astype(np.float32)
+    return out.astype(np.float32, copy=False)

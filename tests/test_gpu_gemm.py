@@ -49,9 +49,12 @@ def _weight_values(w, kind):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "block", "pow2", "mx"])
-@pytest.mark.parametrize("E,T,K,zeros", [(4, 2048, 2, ()), (8, 3000, 2, (2, 5))])
-def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros):
-    D, H = 512, 384
+@pytest.mark.parametrize("E,T,K,zeros,D,H", [
+    (4, 2048, 2, (), 512, 384), (8, 3000, 2, (2, 5), 512, 384),
+    # the non-persistent ragged-M kernel: more than 64 experts (serial walk of
+    # the expert table per tile), and a single 128-deep FP8 K step
+    (80, 3000, 2, (3, 70), 256, 256), (4, 1000, 2, (1,), 128, 128)])
+def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros, D, H):
     k = KINDS[kind]
     x = randn_bf16((T, D), seed=1)
     _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)

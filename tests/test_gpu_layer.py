@@ -185,3 +185,18 @@ def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
             q, s = ofp8.quant_128x128(src, pow2=kind == "pow2")
             assert np.array_equal(data[:n], q)
             assert np.array_equal(op.scale.reshape(-1, D // 128).cpu().numpy()[: n // 128], s)
+    # the dgrad operands: w13t [E][D, 2H] and w2t [E][D, H] (128x128 blocks of
+    # each expert's transpose; for MX the 32x1 column blocks of the whole
+    # [E*2H, D] / [E*H, D] stack, stored transposed)
+    for op, src, n in ((ew.w13t, W13, 2 * H), (ew.w2t, f(w2).reshape(E * H, D), H)):
+        if kind == "mx":
+            qt, ct = ofp8.quant_mx_32x1(src)
+            assert np.array_equal(op.data.reshape(D, E * n).cpu().numpy(), qt)
+            assert np.array_equal(op.scale.reshape(E * n // 32, D).cpu().numpy(), ct)
+        else:
+            data = op.data.reshape(E, D, n).cpu().numpy()
+            scale = op.scale.reshape(E, D // 128, n // 128).cpu().numpy()
+            for e in range(E):
+                q, s = ofp8.quant_128x128(np.ascontiguousarray(src[e * n:(e + 1) * n].T), pow2=kind == "pow2")
+                assert np.array_equal(data[e], q), e
+                assert np.array_equal(scale[e], s), e

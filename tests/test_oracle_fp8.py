@@ -46,6 +46,41 @@ def test_encode_matches_torch_cast():
     assert np.array_equal(a[~nan_a], b[~nan_a])
 
 
+@pytest.mark.parametrize("saturate", [False, True])
+def test_fast_encoder_equals_search_encoder(saturate):
+    """The torch-cast encoder the layer oracle uses on large arrays gives the
+    search encoder's codes bit for bit, NaN codes and their signs included,
+    and the quantisers give the same bytes through either encoder."""
+    rng = np.random.default_rng(7)
+    mids = ((ofp8._POS[1:] + ofp8._POS[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([
+        (np.arange(0, 65536, dtype=np.uint32) << 16).view(np.float32),
+        rng.standard_normal(300_000).astype(np.float32) * np.float32(60),
+        mids, -mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e4)),
+        np.float32([464.0, -464.0, 463.99997, 464.00003, 1e6, -1e6, np.inf, -np.inf, np.nan, -np.nan]),
+    ])
+    assert np.array_equal(ofp8.e4m3_encode_fast(x, saturate), ofp8.e4m3_encode(x, saturate))
+    a = (rng.standard_normal((512, 256)) * np.exp(rng.standard_normal((512, 1)) * 4)).astype(np.float32)
+    old = ofp8._FAST_ENCODE_MIN
+    try:
+        ofp8._FAST_ENCODE_MIN = 1 << 62
+        slow = [ofp8.quant_1x128(a), ofp8.quant_128x128(a, pow2=True), ofp8.quant_mx_1x32(a),
+                ofp8.scaling_aware_transpose(*ofp8.quant_1x128(a, pow2=True))]
+        slow_deq = [ofp8.dequant_1x128(*slow[0]), ofp8.dequant_128x128(*slow[1]),
+                    ofp8.dequant_mx_1x32(*slow[2]), ofp8.bf16_round(x)]
+        ofp8._FAST_ENCODE_MIN = 0
+        fast = [ofp8.quant_1x128(a), ofp8.quant_128x128(a, pow2=True), ofp8.quant_mx_1x32(a),
+                ofp8.scaling_aware_transpose(*ofp8.quant_1x128(a, pow2=True))]
+        fast_deq = [ofp8.dequant_1x128(*slow[0]), ofp8.dequant_128x128(*slow[1]),
+                    ofp8.dequant_mx_1x32(*slow[2]), ofp8.bf16_round(x)]
+    finally:
+        ofp8._FAST_ENCODE_MIN = old
+    for (qs, ss), (qf, sf) in zip(slow, fast):
+        assert np.array_equal(qs, qf) and np.array_equal(ss, sf)
+    for vs, vf in zip(slow_deq, fast_deq):
+        assert np.array_equal(vs.view(np.uint32), vf.view(np.uint32))
+
+
 def test_saturating_encode():
     x = np.float32([447.0, 448.0, 460.0, 470.0, 1e6, -1e6, -500.0])
     assert ofp8.e4m3_encode(x, saturate=True).tolist() == [0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0xFE]

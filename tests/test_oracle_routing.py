@@ -66,7 +66,7 @@ def _brute_force_sort(idx, E, pad=128):
                     counts[e] += 1
         off += -(-counts[e] // pad) * pad
     offsets.append(off)
-    return counts, offsets, [rows[a] for a in range(T * K)]
+    return counts, offsets, [rows.get(a, -1) for a in range(T * K)]
 
 
 @pytest.mark.parametrize("T,E,K,s,zeros", [(300, 4, 1, 0.0, ()), (257, 8, 2, 1.1, (3,)),
@@ -82,6 +82,34 @@ def test_sort_matches_brute_force(T, E, K, s, zeros):
     aor = r["assign_of_row"]
     assert sorted(aor[aor >= 0].tolist()) == list(range(T * K))
     assert (aor[np.asarray(rows)] == np.arange(T * K)).all()
+
+
+def test_sort_drops_out_of_range_like_the_reference_loop():
+    """Slots routed outside [0, E) (another GPU's experts; negative after an
+    expert offset) take no row, as the reference loop walks only the local
+    experts (model/moe.py:1560-1567): the kept slots sort exactly as the brute
+    force over the in-range slots, and unpermute adds nothing for the others."""
+    rng = np.random.default_rng(11)
+    T, E, K, D = 120, 6, 4, 8
+    idx = rng.integers(-3, E + 5, size=(T, K))
+    r = orouting.sort_assignments(idx, E, drop_out_of_range=True)
+    counts, offsets, rows = _brute_force_sort(idx, E)   # ignores indices outside [0, E)
+    assert r["counts"].tolist() == counts
+    assert r["offsets"].tolist() == offsets
+    valid = ((idx >= 0) & (idx < E)).reshape(-1)
+    assert (r["row_of"][~valid] == -1).all()
+    assert np.array_equal(r["row_of"][valid], np.asarray(rows)[valid])
+    y = rng.standard_normal((r["assign_of_row"].size, D)).astype(np.float32)
+    w = rng.random((T, K)).astype(np.float32)
+    out = orouting.unpermute_unpad(y, r["row_of"], w, T, K)
+    for t in range(T):
+        acc = np.zeros(D, np.float32)
+        for k in range(K):
+            if 0 <= idx[t, k] < E:
+                acc = (acc + w[t, k] * y[r["row_of"][t * K + k]]).astype(np.float32)
+        assert np.array_equal(out[t], acc)
+    with pytest.raises(ValueError):
+        orouting.sort_assignments(idx, E)
 
 
 def test_sort_order_equals_reference_nonzero():
