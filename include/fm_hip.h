@@ -212,6 +212,22 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
                   int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
                   int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference.  fm_route_sort without the workspace
+ * argument and without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Outputs and their meaning are fm_route_sort's.  The
+ * block histogram lives in a fixed device array of
+ * fm_route_sort_noalloc_max_workspace_bytes() bytes (2 MiB) per GPU, held
+ * until the process ends; a call needing more than that
+ * (fm_route_workspace_bytes(T*K, E) larger) is rejected with an error.  All
+ * calls on one GPU share that array: calls that overlap on one GPU (other
+ * streams or host threads) race; calls ordered on one stream do not. */
+int64_t fm_route_sort_noalloc_max_workspace_bytes(void);
+int fm_route_sort_noalloc(const void* indices, int indices_i64, int64_t T, int K, int E,
+                          int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
+                          int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
+                          int32_t* use_fp8, void* stream);
+
 /* Replaces fp8_flow_moe.fused_permute_pad (reference fp8/__init__.py:19) and
  * the gather + pad of model/moe.py:1571,1577-1580: row r of the padded buffer
  * is x[assign_of_row[r] / K] (times weights[assign_of_row[r]] if weights !=

@@ -14,6 +14,8 @@
 //   fm_unpermute        -- out[t] = sum_k w[t,k] * y[row(t,k)], fp32 sum, one
 //                          rounding
 //   fm_router_weight_grad -- dw[t,k] = <dout[t], y[row(t,k)]>
+#include <mutex>
+
 #include "fm_tile.h"
 #include "../../include/fm_hip.h"
 
@@ -489,6 +491,78 @@ __global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* dout, 
   }
 }
 
+// ----------------------------------------------------- sort launcher ----
+// The three sort kernels on one stream.  block_hist ([E][blocks] int32) is
+// written in full by sort_hist_kernel before anything reads it, so the
+// buffer needs no clearing.
+static int route_sort_launch(const void* indices, int indices_i64, int64_t T, int K, int E,
+                             int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
+                             int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
+                             int32_t* use_fp8, int32_t* bh, hipStream_t sm, const char* what) {
+  const int64_t A = T * K;
+  FM_REQUIRE(indices || A == 0, "%s: null indices", what);
+  FM_REQUIRE(E >= 1 && E <= kSortMaxExperts, "%s: E must be in [1, %d]", what, kSortMaxExperts);
+  FM_REQUIRE(counts && offsets && assign_of_row && tile_expert && (row_of || A == 0), "%s: null output", what);
+  FM_REQUIRE(rows_max >= fm_route_rows_max(A, E) && rows_max % 128 == 0,
+             "%s: rows_max must be >= fm_route_rows_max() and a multiple of 128", what);
+  const int64_t nb = (A + kSortBlock - 1) / kSortBlock;
+  if (nb > 0) {
+    if (indices_i64)
+      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int64_t*>(indices), A, E, bh, nb);
+    else
+      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int32_t*>(indices), A, E, bh, nb);
+    if (int rc = check_launch(what)) return rc;
+  }
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
+                     tile_expert, rows_max / 128, assign_of_row, rows_max, use_fp8, threshold);
+  if (int rc = check_launch(what)) return rc;
+  if (nb > 0) {
+    if (indices_i64)
+      hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int64_t*>(indices), A, E, bh, nb, offsets, row_of,
+                         assign_of_row);
+    else
+      hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int32_t*>(indices), A, E, bh, nb, offsets, row_of,
+                         assign_of_row);
+    if (int rc = check_launch(what)) return rc;
+  }
+  return 0;
+}
+
+// ------------------------------------------------ allocation-free scratch ----
+// The block histogram of fm_route_sort_noalloc lives in this fixed device
+// array (one copy per GPU, held until the process ends).  Host code never
+// passes `scratch` itself to a kernel: its device address is looked up once
+// per device with hipGetSymbolAddress and cached below.  Every call on a GPU
+// shares that GPU's array, so calls that overlap on one GPU (two streams, two
+// host threads) race; calls ordered on one stream do not.
+constexpr int64_t kRouteScratchBytes = int64_t(2) << 20;   // 2 MiB: E * ceil(A / 1024) <= 524288
+static __device__ __align__(256) uint8_t scratch[kRouteScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+static int route_scratch_ptr(int32_t** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  FM_REQUIRE(err == hipSuccess, "fm_route_sort_noalloc: hipGetDevice failed: %s", hipGetErrorString(err));
+  FM_REQUIRE(dev >= 0 && dev < kMaxDevices, "fm_route_sort_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    FM_REQUIRE(err == hipSuccess && p, "fm_route_sort_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+               hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace fm
 
 using namespace fm;
@@ -540,41 +614,31 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
                   int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
                   int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
                   int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream) {
-  const int64_t A = T * K;
-  FM_REQUIRE(indices || A == 0, "fm_route_sort: null indices");
-  FM_REQUIRE(E >= 1 && E <= kSortMaxExperts, "fm_route_sort: E must be in [1, %d]", kSortMaxExperts);
-  FM_REQUIRE(counts && offsets && assign_of_row && tile_expert && workspace,
-             "fm_route_sort: null output");
-  FM_REQUIRE(rows_max >= fm_route_rows_max(A, E) && rows_max % 128 == 0,
-             "fm_route_sort: rows_max must be >= fm_route_rows_max() and a multiple of 128");
-  FM_REQUIRE(workspace_bytes >= fm_route_workspace_bytes(A, E), "fm_route_sort: workspace too small");
-  hipStream_t sm = static_cast<hipStream_t>(stream);
-  const int64_t nb = (A + kSortBlock - 1) / kSortBlock;
-  int32_t* bh = static_cast<int32_t*>(workspace);
-  if (nb > 0) {
-    if (indices_i64)
-      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int64_t*>(indices), A, E, bh, nb);
-    else
-      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int32_t*>(indices), A, E, bh, nb);
-    if (int rc = check_launch("fm_route_sort/hist")) return rc;
-  }
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
-                     tile_expert, rows_max / 128, assign_of_row, rows_max, use_fp8, threshold);
-  if (int rc = check_launch("fm_route_sort/scan")) return rc;
-  if (nb > 0) {
-    if (indices_i64)
-      hipLaunchKernelGGL(sort_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int64_t*>(indices), A, E, bh, nb, offsets, row_of,
-                         assign_of_row);
-    else
-      hipLaunchKernelGGL(sort_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int32_t*>(indices), A, E, bh, nb, offsets, row_of,
-                         assign_of_row);
-    if (int rc = check_launch("fm_route_sort/scatter")) return rc;
-  }
-  return 0;
+  FM_REQUIRE(workspace, "fm_route_sort: null workspace");
+  FM_REQUIRE(workspace_bytes >= fm_route_workspace_bytes(T * K, E), "fm_route_sort: workspace too small");
+  return route_sort_launch(indices, indices_i64, T, K, E, threshold, counts, offsets, row_of, assign_of_row,
+                           rows_max, tile_expert, use_fp8, static_cast<int32_t*>(workspace),
+                           static_cast<hipStream_t>(stream), "fm_route_sort");
+}
+
+int64_t fm_route_sort_noalloc_max_workspace_bytes(void) { return kRouteScratchBytes; }
+
+int fm_route_sort_noalloc(const void* indices, int indices_i64, int64_t T, int K, int E,
+                          int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
+                          int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
+                          int32_t* use_fp8, void* stream) {
+  FM_REQUIRE(E >= 1 && E <= kSortMaxExperts, "fm_route_sort_noalloc: E must be in [1, %d]", kSortMaxExperts);
+  FM_REQUIRE(T >= 0 && K >= 1, "fm_route_sort_noalloc: T must be >= 0 and K >= 1");
+  const int64_t need = fm_route_workspace_bytes(T * K, E);
+  FM_REQUIRE(need <= kRouteScratchBytes,
+             "fm_route_sort_noalloc: %lld assignments over %d experts need %lld bytes of scratch, more than "
+             "the %lld this entry point holds (use fm_route_sort with a workspace)",
+             (long long)(T * K), E, (long long)need, (long long)kRouteScratchBytes);
+  int32_t* bh = nullptr;
+  if (int rc = route_scratch_ptr(&bh)) return rc;
+  return route_sort_launch(indices, indices_i64, T, K, E, threshold, counts, offsets, row_of, assign_of_row,
+                           rows_max, tile_expert, use_fp8, bh, static_cast<hipStream_t>(stream),
+                           "fm_route_sort_noalloc");
 }
 
 int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,
