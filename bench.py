@@ -48,6 +48,17 @@ def synthetic_inputs(T, D, H, E, K, seed, dev):
     return [a.to(dev) for a in (x, w, idx, w1, w2, w3, go)]
 
 
+def router_params(D, E, seed, dev):
+    """Router gate of configs[2]: nn.Linear(D, E, bias=True) weight and bias
+    N(0, 0.02) (bf16 parameters, as the reference's model under bf16)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed + 1000)
+    gw = (torch.randn(E, D, generator=g) * 0.02).bfloat16()
+    gb = (torch.randn(E, generator=g) * 0.02).bfloat16()
+    return gw.to(dev), gb.to(dev)
+
+
 def device_normal(shape, std, gen, dev, dtype):
     import torch
 
@@ -85,14 +96,19 @@ class GemmTimer:
 
 
 def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, backward=True,
-               gemm_timer=True, pre_step=None, overlap=True):
+               gemm_timer=True, pre_step=None, overlap=True, router=None):
     """Times `steps` calls of the expert block (forward, + backward when
     `backward`), weight cache dropped every step, with nothing recorded between
-    the launches.  With `gemm_timer`, a second pass of `steps` identical steps
-    then records HIP events around every grouped-GEMM launch, on one stream so
-    that no other kernel runs beside the one timed (each event record leaves a
-    few-microsecond bubble in the stream, so this pass is not the one the step
-    time comes from).  Returns (ms per step, GEMM event summary or None)."""
+    the launches.  With `router` = (gate weight, gate bias, top_k, gating) the
+    step is the MoE layer: the router (gate GEMM, gating with `idx` replayed as
+    an R3 routing mask, expert counts, load-balancing loss) runs first and the
+    backward takes out * go + aux loss through both (the Trainer's
+    `loss + aux_loss`, reference train/trainer.py:320-339).  With `gemm_timer`,
+    a second pass of `steps` identical steps then records HIP events around
+    every grouped-GEMM launch, on one stream so that no other kernel runs
+    beside the one timed (each event record leaves a few-microsecond bubble in
+    the stream, so this pass is not the one the step time comes from).
+    Returns (ms per step, GEMM event summary or None)."""
     import torch
 
     import nanopysche_amd as fm
@@ -107,18 +123,36 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     blk.set_weights(*params)
     xr = x.detach().clone().requires_grad_(backward)
     wr = w.detach().clone().requires_grad_(backward)
+    gparams = []
+    if router is not None:
+        gparams = [t.detach().clone().requires_grad_(backward) for t in router[:2]]
+    one = torch.ones((), device=x.device)
+
+    replay = router[4] if router is not None and len(router) > 4 else True
+
+    def routed():
+        if router is not None:
+            return fm.route(xr, gparams[0], gparams[1], top_k=router[2], gating=router[3],
+                            replay_indices=idx if replay else None)
+        r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
+        return r_w, r_idx, None
 
     def step():
         blk._cache.clear()  # weights change every training step: re-quantise them
-        r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
         if backward:
-            for p in params:
+            for p in params + gparams:
                 p.grad = None
             xr.grad = None
             wr.grad = None
-            blk(xr, r_w, r_idx, 0, E).backward(go)
+            r_w, r_idx, aux = routed()
+            out = blk(xr, r_w, r_idx, 0, E)
+            if aux is None:
+                out.backward(go)
+            else:
+                torch.autograd.backward([out, aux], [go, one])
         else:
             with torch.no_grad():
+                r_w, r_idx, _ = routed()
                 blk(xr, r_w, r_idx, 0, E)
 
     for _ in range(warmup):
@@ -202,6 +236,14 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
     def nb(*ts):
         return sum(t.numel() * t.element_size() for t in ts if t is not None)
 
+    # buffers of the padded expert layout hold R = rows_max rows, of which the
+    # producers write (and the consumers read) only the offsets[E] rows of
+    # the expert groups: count those
+    R_used = int(plan.offsets[-1].item())
+
+    def nbq(*ts):
+        return nb(*ts) * R_used // R
+
     pq = _alloc_quant(R, D, P2, True, True, dev, True)
     sq = _alloc_quant(R, H, P2, True, True, dev, True)
     gq = _alloc_quant(R, 2 * H, P2, True, True, dev, True)
@@ -213,20 +255,21 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
     ops = [
         ("permute + quantise (x rows, row + transposed, pow2)",
          lambda: _lib.call("fm_permute", _lib.ptr(x), T, D, x.stride(0), _lib.ptr(plan.assign_of_row), R, K, None,
-                           *_tile_args(P2, *pq), _lib.ptr(plan.tile_expert), st), nb(x, *pq)),
+                           *_tile_args(P2, *pq), _lib.ptr(plan.tile_expert), st), nb(x) + nbq(*pq)),
         ("permute + quantise (dY rows x router weight)",
          lambda: _lib.call("fm_permute", _lib.ptr(go), T, D, go.stride(0), _lib.ptr(plan.assign_of_row), R, K,
-                           _lib.ptr(wts), *_tile_args(P2, *pq), _lib.ptr(plan.tile_expert), st), nb(go, wts, *pq)),
+                           _lib.ptr(wts), *_tile_args(P2, *pq), _lib.ptr(plan.tile_expert), st),
+         nb(go, wts) + nbq(*pq)),
         ("SwiGLU + quantise (row + transposed)",
          lambda: _lib.call("fm_swiglu_quantize", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0), R, H,
-                           *_tile_args(P2, *sq), _lib.ptr(plan.tile_expert), st), nb(GU, *sq)),
+                           *_tile_args(P2, *sq), _lib.ptr(plan.tile_expert), st), nbq(GU, *sq)),
         ("SwiGLU backward + quantise (dg|du row + transposed)",
          lambda: _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
                            _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(P2, *gq), _lib.ptr(plan.tile_expert), st),
-         nb(GU, dH, *gq)),
+         nbq(GU, dH, *gq)),
         ("unpermute (weighted sum over top-k)",
          lambda: _lib.call("fm_unpermute", _lib.ptr(Y), Y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(wts), T, K, D,
-                           _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), st), nb(Y, wts, out)),
+                           _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), st), nbq(Y) + nb(wts, out)),
         ("expert weight re-quantisation (w1, w3, w2 in one launch, 128x128 pow2 + transposed)",
          lambda: ew._build(w1, w2, w3, E), wbytes),
     ]
@@ -248,38 +291,52 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
     return results
 
 
-def cpu_baseline(T, D, H, E, K, budget_s=12.0):
-    """The reference's BF16 per-expert loop (model/moe.py:1542-1596) restated in
-    fp32 torch on the host cores, forward + backward, on a bounded token sample."""
-    import torch
-
-    from oracle.layer import moe_bf16_loop
-
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    Ts = 1024
-    x, w, idx, w1, w2, w3, go = synthetic_inputs(Ts, D, H, E, K, seed=2, dev="cpu")
-    moe_bf16_loop(x, w, idx, w1, w2, w3, E, go)  # warmup
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 5):
-        t0 = time.perf_counter()
-        moe_bf16_loop(x, w, idx, w1, w2, w3, E, go)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    model = ""
+def cpu_model_name():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(Ts / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{Ts} tokens of the same layer (D={D}, H={H}, E={E}, top-{K}), fp32 torch CPU "
-                      f"per-expert loop fwd+bwd, median of {len(times)} runs; cpu: {model}"}
+    return ""
+
+
+def cpu_baseline(T, D, H, E, K, runs=2):
+    """configs[2]'s layer step on the host cores, all T tokens: the router
+    (fp32 gate, softmax of the replayed balanced experts, load-balancing loss;
+    reference model/moe.py:151-281) and the expert block as the FP8 flow's
+    dequantise-then-fp32-matmul restatement, forward + backward (the oracle's
+    moe_flow_reference: numpy quantisers, torch CPU matmuls).  1 warmup, then
+    the median of `runs` timed runs."""
+    import numpy as np
+    import torch
+
+    from oracle import layer as olayer
+    from oracle import routing as orouting
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x, w, idx, w1, w2, w3, go = synthetic_inputs(T, D, H, E, K, seed=2, dev="cpu")
+    gw, gb = router_params(D, E, 2, "cpu")
+
+    def once():
+        logits = orouting.router_logits(x.float().numpy(), gw.float().numpy(), gb.float().numpy())
+        wts, ridx = orouting.replay_gating(logits, idx.numpy(), K)
+        orouting.load_balancing_loss(logits, ridx, E)
+        olayer.moe_flow_reference(x, torch.from_numpy(wts), torch.from_numpy(ridx), w1, w2, w3, E, go,
+                                  recipe="flow_moe")
+
+    once()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(T / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all {T} tokens of configs[2] (D={D}, H={H}, E={E}, top-{K}): router + FP8 flow_moe expert "
+                      f"block as dequantise-then-fp32-matmul, fwd+bwd (torch CPU matmuls on "
+                      f"{torch.get_num_threads()} threads, numpy quantisers on one), median of {runs} runs, "
+                      f"{med:.2f} s per step; cpu: {cpu_model_name()}"}
 
 
 # ============================================================== configs[2] ====
@@ -295,8 +352,9 @@ def workload_c3(args, dev):
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
+    gw, gb = router_params(D, E, 2, dev)
     ms, summ = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup,
-                          overlap=not args.no_overlap)
+                          overlap=not args.no_overlap, router=(gw, gb, K, "softmax"))
     dom = max(summ, key=lambda k: summ[k]["ms"])
     d = summ[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
@@ -317,9 +375,11 @@ def workload_c3(args, dev):
         "vs_baseline": None,
         "dtype": "bf16" if args.recipe == "none" else "fp8-e4m3",
         "data": "synthetic",
-        "config": {"workload": "configs[2]: FP8-Flow-MoE expert block fwd+bwd, FP8 forced",
+        "config": {"workload": "configs[2]: router + FP8-Flow-MoE expert block, fwd+bwd of out*grad + aux loss, "
+                               "FP8 forced",
                    "tokens": T, "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H,
-                   "routing": "exactly balanced (2048 assignments per expert)",
+                   "routing": "top-2 softmax router (fp32 gate, load-balancing loss) with the exactly balanced "
+                              "assignment (2048 per expert) replayed as its R3 routing mask",
                    "recipe": args.recipe, "assignments": A},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
@@ -531,26 +591,22 @@ def cpu_baseline_quant(C, budget_s=10.0):
 
 # ============================================================== configs[0] ====
 def workload_c1(args, dev):
-    """BF16 expert block forward, top-1 softmax over 4 experts (the router's
-    top-k runs inside the step from precomputed gate logits)."""
+    """BF16 MoE layer forward, top-1 softmax router over 4 experts (gate GEMM,
+    top-1 gating, counts and load-balancing loss run inside the step)."""
     import torch
-
-    import nanopysche_amd as fm
 
     T, D, E, K, H = 4096, 2048, 4, 1, 5632
     gen = torch.Generator(device=dev).manual_seed(0)
     x = device_normal((T, D), 1.0, gen, dev, torch.bfloat16)
     wg = device_normal((E, D), 0.02, gen, dev, torch.bfloat16)
-    bias = torch.full((E,), -1.0, device=dev)   # gate bias init, model/moe.py:107-109
-    logits = (x.float() @ wg.float().t() + bias).contiguous()
+    bg = device_normal((E,), 0.02, gen, dev, torch.bfloat16)
     w1, w2, w3 = [device_normal((E * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
-    w0, i0 = fm.topk_gating(logits, K, "softmax")
+    import nanopysche_amd as fm
 
-    def pre():
-        return fm.topk_gating(logits, K, "softmax")
-
+    with torch.no_grad():
+        w0, i0, _ = fm.route(x, wg, bg, top_k=K, gating="softmax")
     ms, summ = time_layer(x, w0, i0, w1, w2, w3, None, E, "none", 1 << 40, args.steps, args.warmup,
-                          backward=False, pre_step=pre)
+                          backward=False, router=(wg, bg, K, "softmax", False))
     counts = torch.bincount(i0.reshape(-1), minlength=E).tolist()
     flops = 6.0 * T * K * D * H
     return {
@@ -558,7 +614,7 @@ def workload_c1(args, dev):
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "configs[0]: BF16 expert block forward, top-1 softmax", "tokens": T,
+        "config": {"workload": "configs[0]: router + BF16 expert block forward, top-1 softmax", "tokens": T,
                    "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H, "tokens_per_expert": counts},
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),

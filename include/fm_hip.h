@@ -146,20 +146,32 @@ int fm_scaling_aware_transpose(const void* q, int64_t rows, int64_t cols, int64_
                                int64_t ld_st, void* stream);
 
 /* ------------------------------------------------------------ routing ---- */
-/* Replaces MoERouter._softmax_gating / _sigmoid_gating (reference
- * model/moe.py:249-265): per token, top-K of the logits (softmax, weights =
- * softmax over the K selected logits) or of sigmoid(logits) (weights / (sum +
- * 1e-8)); ties go to the lower expert index.  E <= 256, K <= min(E, 64).
- * If prob_partial != NULL it receives [n_waves, E] per-wave sums of the full
- * softmax for fm_aux_loss.  n_waves: positive multiple of 4 (grid size). */
-int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating,
-                   float* weights, void* indices, int indices_i64, float* prob_partial,
-                   int64_t n_waves, void* stream);
+/* Replaces MoERouter._softmax_gating / _sigmoid_gating /
+ * _routing_replay_gating and the l2 weight normalisation of MoERouter.forward
+ * (reference model/moe.py:158-170, :187-265): per token, top-K of the logits
+ * (softmax: weights = softmax over the K selected logits) or of
+ * sigmoid(logits) (weights / (sum + 1e-8)).  Selection order: NaN above
+ * every number (as torch.topk), then larger, then the lower expert index; an
+ * expert is selected at most once.  replay_indices [T, K] (int64 or int32,
+ * or NULL): R3 routing replay -- weights = softmax(all logits) restricted to
+ * the replayed experts and renormalised (sum clamped to >= 1e-8), the K
+ * largest in order, whatever `gating` is.  flags: FM_GATING_L2_NORMALIZE
+ * divides the K weights by their l2 norm + 1e-8.  E <= 256,
+ * K <= min(E, 64).  prob_partial [n_waves, E] (or NULL) receives per-wave sums
+ * of the full softmax, z_partial [n_waves] (or NULL) per-wave sums of
+ * logsumexp(logits)^2, both for fm_aux_loss.  n_waves: positive multiple of 4
+ * (grid size). */
+#define FM_GATING_L2_NORMALIZE 1
+int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating, int flags,
+                   const void* replay_indices, int replay_i64, float* weights, void* indices, int indices_i64,
+                   float* prob_partial, float* z_partial, int64_t n_waves, void* stream);
 
-/* Replaces MoERouter._load_balancing_loss (reference model/moe.py:267-281):
- * loss[0] = E * sum_e (counts[e] / T) * (sum_w prob_partial[w][e] / T). */
+/* Replaces MoERouter._load_balancing_loss and the z-loss term (reference
+ * model/moe.py:172-178, :267-281):
+ * loss[0] = E * sum_e (counts[e] / T) * (sum_w prob_partial[w][e] / T)
+ *           + z_loss_multiplier * sum_w z_partial[w] / T   (z_partial may be NULL). */
 int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
-                float* loss, void* stream);
+                const float* z_partial, float z_loss_multiplier, float* loss, void* stream);
 
 /* Replaces the gate of MoERouter.forward (reference model/moe.py:151-154):
  * logits[t][e] = sum_d x[t][d] w[e][d] + bias[e] + score_bias[e] in fp32, the
@@ -172,19 +184,38 @@ int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_
 
 /* counts[e] = number of the n routed slots with index e (the f_i numerator of
  * MoERouter._load_balancing_loss, model/moe.py:271-274); indices outside
- * [0, E) are not counted.  E <= 1024. */
-int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts, void* stream);
+ * [0, E) are not counted.  E <= 1024.  With tokens_per_expert [E] and
+ * total_tokens [1] (int64, both or neither) the counts are also added to those
+ * running totals and `tokens` (the number of routed tokens) to total_tokens:
+ * MoERouter._update_expert_counts (:284-292), which adds per-expert slot
+ * counts and indices.shape[0] * indices.shape[1] = B * S tokens for its
+ * [B, S, K] indices, kept on the device. */
+int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts,
+                     int64_t* tokens_per_expert, int64_t* total_tokens, int64_t tokens, void* stream);
 
-/* Backward of the gating and the load-balancing loss (reference
- * model/moe.py:249-281 under autograd): dlogits [T, E] from the gradient of
- * the top-k weights (dweights [T, K], or null) and of the loss (daux: device
- * scalar, or null; needs counts [E] of the forward routing).  gating:
- * FM_GATING_SOFTMAX (softmax over the K selected logits) or
- * FM_GATING_SIGMOID (sigmoid scores / (sum + 1e-8)); logits as the forward
- * used them (score bias included). */
-int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, const void* indices,
-                   int indices_i64, const float* weights, const float* dweights, const float* daux,
-                   const int32_t* counts, float* dlogits, int64_t ld_d, void* stream);
+/* Replaces MoERouter.post_batch on one GPU (reference model/moe.py:294-321,
+ * the DeepSeek-V3 score-bias update): if total_tokens != 0,
+ * score_bias[e] += gamma * (tokens_per_expert[e] / total_tokens - 1 / E) in
+ * fp32 and both running totals are set to 0; otherwise nothing changes.  The
+ * reference's sign is kept (an expert above its share gets a larger bias).
+ * With expert parallelism the caller all-reduces the two totals first, as
+ * the reference does (:303-305). */
+int fm_score_bias_update(int64_t* tokens_per_expert, int64_t* total_tokens, int E, float gamma, float* score_bias,
+                         void* stream);
+
+/* Backward of the gating, the weight normalisation, the load-balancing loss
+ * and the z-loss (reference model/moe.py:158-184, :187-281 under autograd):
+ * dlogits [T, E] from the gradient of the top-k weights (dweights [T, K], or
+ * null) and of the aux loss (daux: device scalar, or null; needs counts [E]
+ * of the forward routing).  gating: FM_GATING_SOFTMAX (softmax over the K
+ * selected logits) or FM_GATING_SIGMOID (sigmoid scores / (sum + 1e-8));
+ * replay != 0: the forward replayed `indices` (R3: softmax over them, for
+ * either gating).  flags: FM_GATING_L2_NORMALIZE as the forward used it.
+ * z_loss_multiplier: 0 when the loss had no z-loss term.  logits as the
+ * forward used them (score bias included). */
+int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, int flags,
+                   int replay, const void* indices, int indices_i64, const float* dweights, const float* daux,
+                   const int32_t* counts, float z_loss_multiplier, float* dlogits, int64_t ld_d, void* stream);
 
 /* Backward of the gate (reference nn.Linear of model/moe.py:107 under
  * autograd): dx = dlogits w (x's dtype, null to skip), dw = dlogits^T x and

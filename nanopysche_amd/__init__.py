@@ -23,8 +23,8 @@ from .flow_moe import (
     quantize_to_fp8,
     scaling_aware_transpose,
 )
-from .routing import (RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens, router_logits,
-                      topk_gating)
+from .routing import (ExpertLoadTracker, RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens,
+                      router_logits, topk_gating)
 
 __all__ = [
     "FP8FlowMoEConfig",
@@ -52,4 +52,5 @@ __all__ = [
     "route",
     "router_logits",
     "expert_counts",
+    "ExpertLoadTracker",
 ]

@@ -31,6 +31,7 @@ GEMM_FP8_MX = 3
 
 GATING_SOFTMAX = 0
 GATING_SIGMOID = 1
+GATING_L2_NORMALIZE = 1   # fm_topk_gating / fm_gating_grad flag
 
 
 class FmGemmOperand(C.Structure):
@@ -81,12 +82,14 @@ SIGNATURES = {
                              _i64, _vp]),
     "fm_scaling_aware_transpose": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
                                           _vp]),
-    "fm_topk_gating": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _vp, _i64, _vp]),
-    "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, _vp]),
+    "fm_topk_gating": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
+                               _i64, _vp]),
+    "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, C.c_float, _vp, _vp]),
     "fm_router_logits": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
-    "fm_expert_counts": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
-    "fm_gating_grad": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64,
-                              _vp]),
+    "fm_expert_counts": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _i64, _vp]),
+    "fm_score_bias_update": (_i32, [_vp, _vp, _i32, C.c_float, _vp, _vp]),
+    "fm_gating_grad": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, C.c_float,
+                              _vp, _i64, _vp]),
     "fm_router_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "fm_router_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp,
                                   _i64, _vp, _vp, _i64, _vp]),

@@ -27,21 +27,53 @@ struct TopkArgs {
   int64_t T, ld;
   int E, K;
   int sigmoid;
+  int l2;                // normalise the K weights by their l2 norm (+1e-8)
+  const void* replay;    // [T, K] experts to replay (R3), or null
+  int replay_i64;
   float* w;              // [T, K]
   void* idx;             // [T, K] int64 or int32
   int idx_i64;
   float* prob_partial;   // [n_waves, E] or null: per-wave sums of softmax(logits)
+  float* z_partial;      // [n_waves] or null: per-wave sums of logsumexp(logits)^2
 };
 
 constexpr int kTopkMaxPerLane = 4;  // E <= 256
 
+// Selection order of top-k: NaN above every number (as torch.topk orders
+// it), then the larger value, then the lower expert index.
+__device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
+  const bool an = av != av, bn = bv != bv;
+  if (an || bn) return an && (!bn || ai < bi);
+  return av > bv || (av == bv && ai < bi);
+}
+
+__device__ __forceinline__ int load_index(const void* p, int i64, int64_t i) {
+  return i64 ? int(static_cast<const int64_t*>(p)[i]) : static_cast<const int32_t*>(p)[i];
+}
+
+__device__ __forceinline__ void store_index(void* p, int i64, int64_t i, int v) {
+  if (i64) static_cast<int64_t*>(p)[i] = v;
+  else static_cast<int32_t*>(p)[i] = v;
+}
+
+// One token per wave; lane l holds experts l + 64 j.  Each of the K rounds is
+// a wave arg-max over the experts not yet taken (a per-lane taken mask, so an
+// expert never wins twice even when every remaining score is -inf).
+//   softmax:  top-k of the logits, w = softmax over the K selected logits
+//   sigmoid:  top-k of sigmoid(logits), w = s / (sum s + 1e-8)
+//   replay:   p = softmax(all logits), w_e = p_e / max(sum over the replayed
+//             experts of p, 1e-8) on the replayed experts and 0 elsewhere;
+//             the K largest w in order (the reference's R3 gating)
+// then optionally w / (||w||_2 + 1e-8).
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t n_waves = int64_t(gridDim.x) * 4;
+  const bool need_p = a.prob_partial || a.replay || a.z_partial;
   float psum[kTopkMaxPerLane];
 #pragma unroll
   for (int j = 0; j < kTopkMaxPerLane; ++j) psum[j] = 0.f;
+  float zsum = 0.f;
   for (int64_t t = wave; t < a.T; t += n_waves) {
     float v[kTopkMaxPerLane];   // logits of experts lane + 64*j
     float sc[kTopkMaxPerLane];  // selection scores
@@ -49,9 +81,9 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     for (int j = 0; j < kTopkMaxPerLane; ++j) {
       const int e = lane + 64 * j;
       v[j] = e < a.E ? a.logits[t * a.ld + e] : -INFINITY;
-      sc[j] = a.sigmoid ? (e < a.E ? 1.f / (1.f + expf(-v[j])) : -INFINITY) : v[j];
+      sc[j] = a.sigmoid ? 1.f / (1.f + expf(-v[j])) : v[j];
     }
-    if (a.prob_partial) {
+    if (need_p) {
       float m = -INFINITY;
 #pragma unroll
       for (int j = 0; j < kTopkMaxPerLane; ++j) m = fmaxf(m, v[j]);
@@ -64,12 +96,31 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       }
       for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
 #pragma unroll
-      for (int j = 0; j < kTopkMaxPerLane; ++j) psum[j] += ex[j] / s;
+      for (int j = 0; j < kTopkMaxPerLane; ++j) {
+        ex[j] /= s;
+        psum[j] += ex[j];
+      }
+      const float lse = m + logf(s);
+      zsum += lse * lse;
+      if (a.replay) {
+        // masked, renormalised probabilities become the selection scores
+        const int r = lane < a.K ? load_index(a.replay, a.replay_i64, t * a.K + lane) : -1;
+        float msum = 0.f;
+#pragma unroll
+        for (int j = 0; j < kTopkMaxPerLane; ++j) {
+          bool hit = false;
+          for (int k = 0; k < a.K; ++k) hit |= __shfl(r, k) == lane + 64 * j;
+          sc[j] = hit ? ex[j] : 0.f;
+          msum += sc[j];
+        }
+        for (int off = 32; off > 0; off >>= 1) msum += __shfl_xor(msum, off);
+        msum = fmaxf(msum, 1e-8f);
+#pragma unroll
+        for (int j = 0; j < kTopkMaxPerLane; ++j) sc[j] /= msum;
+      }
     }
-    // K rounds of wave arg-max; ties -> lower expert index
-    float top_first = 0.f;
-    float wsum = 0.f;
-    float my_w = 0.f;
+    uint32_t taken = 0;
+    float top_first = 0.f, wsum = 0.f, my_w = 0.f;
     int my_i = 0;
     for (int k = 0; k < a.K; ++k) {
       float bv = -INFINITY;
@@ -77,40 +128,34 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 #pragma unroll
       for (int j = 0; j < kTopkMaxPerLane; ++j) {
         const int e = lane + 64 * j;
-        if (e < a.E && (sc[j] > bv || (sc[j] == bv && e < bi))) { bv = sc[j]; bi = e; }
+        if (e < a.E && !((taken >> j) & 1u) && beats(sc[j], e, bv, bi)) { bv = sc[j]; bi = e; }
       }
       for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off);
         const int oi = __shfl_xor(bi, off);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
       }
-      // remove the winner from its owner lane
-      if ((bi & 63) == lane) {
+      const int jw = bi >> 6;   // bi < E: K <= E candidates exist in every round
+      if ((bi & 63) == lane) taken |= 1u << jw;
+      float vj = v[0];
 #pragma unroll
-        for (int j = 0; j < kTopkMaxPerLane; ++j)
-          if (lane + 64 * j == bi) sc[j] = -INFINITY;
-      }
-      float lg = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kTopkMaxPerLane; ++j)
-        if (lane + 64 * j == bi) lg = v[j];
-      for (int off = 32; off > 0; off >>= 1) lg = fmaxf(lg, __shfl_xor(lg, off));
+      for (int j = 1; j < kTopkMaxPerLane; ++j) vj = jw == j ? v[j] : vj;
+      const float lg = __shfl(vj, bi & 63);
       if (k == 0) top_first = lg;
-      // lane k keeps slot k
-      float wk;
-      if (a.sigmoid) {
-        wk = bv;  // sigmoid score
-      } else {
-        wk = expf(lg - top_first);  // top_first is the max of the selected logits
-      }
+      // sigmoid and replay weights are the scores; softmax: exp(l - l_max)
+      const float wk = (a.sigmoid || a.replay) ? bv : expf(lg - top_first);
       wsum += wk;
       if (lane == k) { my_w = wk; my_i = bi; }
     }
+    float wn = a.replay ? my_w : (a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum);
+    if (a.l2) {
+      float sq = lane < a.K ? wn * wn : 0.f;
+      for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+      wn = wn / (sqrtf(sq) + 1e-8f);
+    }
     if (lane < a.K) {
-      const float wn = a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum;
       a.w[t * a.K + lane] = wn;
-      if (a.idx_i64) static_cast<int64_t*>(a.idx)[t * a.K + lane] = my_i;
-      else static_cast<int32_t*>(a.idx)[t * a.K + lane] = my_i;
+      store_index(a.idx, a.idx_i64, t * a.K + lane, my_i);
     }
   }
   if (a.prob_partial) {
@@ -120,13 +165,14 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       if (e < a.E) a.prob_partial[wave * a.E + e] = psum[j];
     }
   }
+  if (a.z_partial && lane == 0) a.z_partial[wave] = zsum;
 }
 
 // E <= 16: a wave takes 64 / EP tokens at once (EP = E rounded up to a power
 // of two; lane = token slot * EP + expert), so the reductions run over EP
 // lanes (log2 EP steps) for NT tokens together instead of over 64 lanes for
-// one token.  Same selection rule, weights (sum over k in k order) and
-// per-wave softmax partials as topk_kernel.
+// one token.  Same selection rule, weights (sum over k in k order), replay,
+// l2 normalisation and per-wave partials as topk_kernel.
 template <int EP>
 __global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
   constexpr int NT = 64 / EP;
@@ -134,45 +180,66 @@ __global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
   const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t n_waves = int64_t(gridDim.x) * 4;
   const bool ev = e < a.E;
-  float psum = 0.f;
+  const bool need_p = a.prob_partial || a.replay || a.z_partial;
+  float psum = 0.f, zsum = 0.f;
   for (int64_t tg = wave; tg * NT < a.T; tg += n_waves) {
     const int64_t t = tg * NT + g;
     const bool tv = t < a.T;
     const float v = (tv && ev) ? a.logits[t * a.ld + e] : -INFINITY;
-    float sc = a.sigmoid ? (ev ? 1.f / (1.f + expf(-v)) : -INFINITY) : v;
-    if (a.prob_partial) {
+    float sc = a.sigmoid ? 1.f / (1.f + expf(-v)) : v;
+    if (need_p) {
       float m = v;
 #pragma unroll
       for (int off = EP / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-      const float ex = ev ? expf(v - m) : 0.f;
-      float sm = ex;
+      float p = ev ? expf(v - m) : 0.f;
+      float sm = p;
 #pragma unroll
       for (int off = EP / 2; off > 0; off >>= 1) sm += __shfl_xor(sm, off);
-      if (tv) psum += ex / sm;
+      p /= sm;
+      if (tv) psum += p;
+      const float lse = m + logf(sm);
+      if (tv && e == 0) zsum += lse * lse;
+      if (a.replay) {
+        const int r = (tv && e < a.K) ? load_index(a.replay, a.replay_i64, t * a.K + e) : -1;
+        bool hit = false;
+        for (int k = 0; k < a.K; ++k) hit |= __shfl(r, g * EP + k) == e;
+        sc = (ev && hit) ? p : 0.f;
+        float msum = sc;
+#pragma unroll
+        for (int off = EP / 2; off > 0; off >>= 1) msum += __shfl_xor(msum, off);
+        sc /= fmaxf(msum, 1e-8f);
+      }
     }
+    bool taken = false;
     float top_first = 0.f, wsum = 0.f, my_w = 0.f;
     int my_i = 0;
     for (int k = 0; k < a.K; ++k) {
-      float bv = ev ? sc : -INFINITY;
-      int bi = ev ? e : 0x7fffffff;
+      const bool cand = ev && !taken;
+      float bv = cand ? sc : -INFINITY;
+      int bi = cand ? e : 0x7fffffff;
 #pragma unroll
       for (int off = EP / 2; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off);
         const int oi = __shfl_xor(bi, off);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
       }
-      if (bi == e) sc = -INFINITY;   // the winner leaves the race
+      if (bi == e) taken = true;   // the winner leaves the race
       const float lg = __shfl(v, g * EP + (bi & (EP - 1)));
       if (k == 0) top_first = lg;
-      const float wk = a.sigmoid ? bv : expf(lg - top_first);
+      const float wk = (a.sigmoid || a.replay) ? bv : expf(lg - top_first);
       wsum += wk;
       if (e == k) { my_w = wk; my_i = bi; }
     }
+    float wn = a.replay ? my_w : (a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum);
+    if (a.l2) {
+      float sq = e < a.K ? wn * wn : 0.f;
+#pragma unroll
+      for (int off = EP / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+      wn = wn / (sqrtf(sq) + 1e-8f);
+    }
     if (tv && e < a.K) {
-      const float wn = a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum;
       a.w[t * a.K + e] = wn;
-      if (a.idx_i64) static_cast<int64_t*>(a.idx)[t * a.K + e] = my_i;
-      else static_cast<int32_t*>(a.idx)[t * a.K + e] = my_i;
+      store_index(a.idx, a.idx_i64, t * a.K + e, my_i);
     }
   }
   if (a.prob_partial) {
@@ -180,16 +247,24 @@ __global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
     for (int off = EP; off < 64; off <<= 1) psum += __shfl_xor(psum, off);
     if (lane < a.E) a.prob_partial[wave * a.E + lane] = psum;
   }
+  if (a.z_partial) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) zsum += __shfl_xor(zsum, off);
+    if (lane == 0) a.z_partial[wave] = zsum;
+  }
 }
 
 // one block of 512 threads: wave w sums experts w, w + 8, ... -- each lane a
 // strided run of the per-wave partials, then a fixed shuffle tree -- so no
 // workgroup barrier sits inside the per-expert sums; thread 0 then adds
-// f_e * P_e in expert order.  loss = E * sum_e f_e P_e, P_e = sum / T.
+// f_e * P_e in expert order.  loss = E * sum_e f_e P_e, P_e = sum / T, plus
+// z_mult * (sum of the per-wave logsumexp^2 partials) / T when z_partial is
+// given (the z-loss of model/moe.py:176-178).
 __global__ __launch_bounds__(512) void aux_loss_kernel(const float* prob_partial, int64_t n_waves,
                                                        const int32_t* counts, int E, int64_t T,
-                                                       float* loss) {
+                                                       const float* z_partial, float z_mult, float* loss) {
   __shared__ float term[1024];   // E <= 1024 (launcher)
+  __shared__ float zterm;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int e = wave; e < E; e += 8) {
     float p = 0.f;
@@ -198,11 +273,21 @@ __global__ __launch_bounds__(512) void aux_loss_kernel(const float* prob_partial
     for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
     if (lane == 0) term[e] = (float(counts[e]) / float(T)) * (p / float(T));
   }
+  if (wave == 7) {
+    float z = 0.f;
+    if (z_partial)
+      for (int64_t w = lane; w < n_waves; w += 64) z += z_partial[w];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off);
+    if (lane == 0) zterm = z / float(T);
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
     float acc = 0.f;
     for (int e = 0; e < E; ++e) acc += term[e];
-    loss[0] = float(E) * acc;
+    float l = float(E) * acc;
+    if (z_partial) l = l + z_mult * zterm;
+    loss[0] = l;
   }
 }
 
@@ -569,19 +654,20 @@ using namespace fm;
 
 extern "C" {
 
-int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating,
-                   float* weights, void* indices, int indices_i64, float* prob_partial,
-                   int64_t n_waves, void* stream) {
+int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int gating, int flags,
+                   const void* replay_indices, int replay_i64, float* weights, void* indices, int indices_i64,
+                   float* prob_partial, float* z_partial, int64_t n_waves, void* stream) {
   FM_REQUIRE(logits && weights && indices, "fm_topk_gating: null pointer");
   FM_REQUIRE(E >= 1 && E <= 64 * kTopkMaxPerLane, "fm_topk_gating: E must be in [1, %d] (got %d)",
              64 * kTopkMaxPerLane, E);
   FM_REQUIRE(K >= 1 && K <= E && K <= 64, "fm_topk_gating: K must be in [1, min(E, 64)] (got %d)", K);
   FM_REQUIRE(gating == FM_GATING_SOFTMAX || gating == FM_GATING_SIGMOID, "fm_topk_gating: bad gating");
+  FM_REQUIRE((flags & ~FM_GATING_L2_NORMALIZE) == 0, "fm_topk_gating: unknown flags 0x%x", flags);
   FM_REQUIRE(ld >= E, "fm_topk_gating: pitch < E");
   FM_REQUIRE(n_waves >= 4 && n_waves % 4 == 0, "fm_topk_gating: n_waves must be a positive multiple of 4");
   if (T == 0) return 0;
-  TopkArgs a{logits, T, ld, E, K, gating == FM_GATING_SIGMOID, weights, indices, indices_i64,
-             prob_partial};
+  TopkArgs a{logits, T, ld, E, K, gating == FM_GATING_SIGMOID, (flags & FM_GATING_L2_NORMALIZE) ? 1 : 0,
+             replay_indices, replay_i64, weights, indices, indices_i64, prob_partial, z_partial};
   const dim3 grid(unsigned(n_waves / 4)), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (E <= 2) hipLaunchKernelGGL(topk_small_kernel<2>, grid, block, 0, s, a);
@@ -593,11 +679,11 @@ int fm_topk_gating(const float* logits, int64_t T, int E, int64_t ld, int K, int
 }
 
 int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* counts, int E, int64_t T,
-                float* loss, void* stream) {
+                const float* z_partial, float z_loss_multiplier, float* loss, void* stream) {
   FM_REQUIRE(prob_partial && counts && loss, "fm_aux_loss: null pointer");
   FM_REQUIRE(T > 0 && E > 0 && E <= 1024, "fm_aux_loss: T must be positive and E in [1, 1024] (got %d)", E);
   hipLaunchKernelGGL(aux_loss_kernel, dim3(1), dim3(512), 0, static_cast<hipStream_t>(stream),
-                     prob_partial, n_waves, counts, E, T, loss);
+                     prob_partial, n_waves, counts, E, T, z_partial, z_loss_multiplier, loss);
   return check_launch("fm_aux_loss");
 }
 

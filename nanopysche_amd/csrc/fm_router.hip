@@ -297,8 +297,11 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) 
 
 // --------------------------------------------------------------- counts ----
 // One workgroup: LDS histogram over all T*K slots (fixed E <= 1024 bins).
+// With `acc` the counts are also added to the running per-expert totals and
+// `tokens` to acc_total (the workgroup owns them: no atomics).
 template <typename I>
-__global__ __launch_bounds__(1024) void expert_counts_kernel(const I* idx, int64_t n, int E, int32_t* counts) {
+__global__ __launch_bounds__(1024) void expert_counts_kernel(const I* idx, int64_t n, int E, int32_t* counts,
+                                                             int64_t* acc, int64_t* acc_total, int64_t tokens) {
   __shared__ int32_t h[1024];
   for (int e = threadIdx.x; e < E; e += 1024) h[e] = 0;
   __syncthreads();
@@ -307,7 +310,28 @@ __global__ __launch_bounds__(1024) void expert_counts_kernel(const I* idx, int64
     if (e >= 0 && e < E) atomicAdd(&h[e], 1);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) counts[e] = h[e];
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    counts[e] = h[e];
+    if (acc) acc[e] += h[e];
+  }
+  if (acc && threadIdx.x == 0) acc_total[0] += tokens;
+}
+
+// post_batch: score_bias[e] += gamma * (acc[e] / total - 1 / E) in fp32, then
+// the running totals are cleared; nothing happens while total is 0.
+__global__ __launch_bounds__(1024) void score_bias_update_kernel(int64_t* acc, int64_t* acc_total, int E,
+                                                                 float gamma, float* score_bias) {
+#pragma clang fp contract(off)   // separately rounded multiply and add, as the reference's tensor ops
+  const int64_t total = acc_total[0];
+  __syncthreads();   // every thread has read the total before thread 0 clears it
+  if (total == 0) return;
+  const float ideal = 1.0f / float(E);
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    const float actual = float(acc[e]) / float(total);
+    score_bias[e] = score_bias[e] + gamma * (actual - ideal);
+    acc[e] = 0;
+  }
+  if (threadIdx.x == 0) acc_total[0] = 0;
 }
 
 // ---------------------------------------------------------- gating grad ----
@@ -315,20 +339,34 @@ struct GatingGradArgs {
   const float* logits;   // [T, ld_l]
   int64_t T, ld_l;
   int E, K;
-  int sigmoid;
+  int sigmoid;           // sigmoid weights (0: softmax over the selected logits, also for replay)
+  int l2;                // the forward divided the weights by their l2 norm + 1e-8
   const void* idx;       // [T, K]
   int idx_i64;
-  const float* w;        // [T, K] forward weights
   const float* dw;       // [T, K] or null
   const float* daux;     // scalar or null
   const int32_t* counts; // [E] (needed with daux)
+  float z_mult;          // z-loss multiplier (0: no z-loss)
   float* dlogits;        // [T, ld_d]
   int64_t ld_d;
 };
 
 constexpr int kGateMaxPerLane = 4;  // E <= 256
 
-// One wave per token (grid-stride); lane holds experts lane + 64 j.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// One wave per token (grid-stride); lane holds experts lane + 64 j, and lane
+// k < K also slot k of the token.  The weights before the optional l2
+// normalisation are recomputed from the logits:
+//   softmax (and R3 replay): u_k = softmax over the K selected logits
+//   sigmoid:                 u_k = s_k / (S + 1e-8), S = sum_k s_k
+// l2: w = u / (n + 1e-8), n = ||u||, so du = dw / (n + 1e-8) - u (u.dw) / (n (n + 1e-8)^2).
+// Then c = sum_k u_k du_k and expert i_k gets
+//   softmax: u_k (du_k - c);  sigmoid: (du_k - c) / (S + 1e-8) * s_k (1 - s_k).
 __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t n_waves = int64_t(gridDim.x) * 4;
@@ -341,43 +379,58 @@ __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
       v[j] = e < a.E ? a.logits[t * a.ld_l + e] : -INFINITY;
       g[j] = 0.f;
     }
-    // top-k weights: c = sum_k w_k dw_k; selected expert i_k gets
-    //   softmax: w_k (dw_k - c);  sigmoid: (dw_k - c) / (S + 1e-8) * s (1 - s)
     if (a.dw) {
-      float c = 0.f, S = 0.f;
-      for (int k = 0; k < a.K; ++k) {
-        c += a.w[t * a.K + k] * a.dw[t * a.K + k];
-        if (a.sigmoid) {
-          const int ik = a.idx_i64 ? int(static_cast<const int64_t*>(a.idx)[t * a.K + k])
-                                   : static_cast<const int32_t*>(a.idx)[t * a.K + k];
-          if (ik >= 0 && ik < a.E) S += 1.f / (1.f + expf(-a.logits[t * a.ld_l + ik]));
+      // slots outside [0, E) carry no weight and no gradient
+      int ik = -1;
+      float lk = -INFINITY, dk = 0.f;
+      if (lane < a.K) {
+        const int64_t i = int64_t(t) * a.K + lane;
+        ik = a.idx_i64 ? int(static_cast<const int64_t*>(a.idx)[i]) : static_cast<const int32_t*>(a.idx)[i];
+        if (ik >= 0 && ik < a.E) {
+          lk = a.logits[t * a.ld_l + ik];
+          dk = a.dw[i];
+        } else {
+          ik = -1;
         }
       }
+      float u, S = 0.f, sk = 0.f;
+      if (a.sigmoid) {
+        sk = ik >= 0 ? 1.f / (1.f + expf(-lk)) : 0.f;
+        S = wave_sum(sk);
+        u = sk / (S + 1e-8f);
+      } else {
+        const float mk = wave_max(lk);
+        const float ek = ik >= 0 ? expf(lk - mk) : 0.f;
+        u = ek / wave_sum(ek);
+      }
+      float du = dk;
+      if (a.l2) {
+        const float n = sqrtf(wave_sum(u * u));
+        const float dot = wave_sum(u * dk);
+        const float ne = n + 1e-8f;
+        du = dk / ne - (n > 0.f ? u * dot / (n * ne * ne) : 0.f);
+      }
+      const float c = wave_sum(u * du);
+      const float gk = ik < 0 ? 0.f
+                              : (a.sigmoid ? (du - c) / (S + 1e-8f) * sk * (1.f - sk) : u * (du - c));
       for (int k = 0; k < a.K; ++k) {
-        const int ik = a.idx_i64 ? int(static_cast<const int64_t*>(a.idx)[t * a.K + k])
-                                 : static_cast<const int32_t*>(a.idx)[t * a.K + k];
-        if (ik < 0 || ik >= a.E || (ik & 63) != lane) continue;   // slots outside [0, E) carry no gradient
-        const float wk = a.w[t * a.K + k], dk = a.dw[t * a.K + k];
+        const int ek = __shfl(ik, k);
+        const float gv = __shfl(gk, k);
+        if (ek >= 0 && (ek & 63) == lane) {
 #pragma unroll
-        for (int j = 0; j < kGateMaxPerLane; ++j) {
-          if (lane + 64 * j != ik) continue;
-          if (a.sigmoid) {
-            const float s = 1.f / (1.f + expf(-v[j]));
-            g[j] += (dk - c) / (S + 1e-8f) * s * (1.f - s);
-          } else {
-            g[j] += wk * (dk - c);
-          }
+          for (int j = 0; j < kGateMaxPerLane; ++j)
+            if ((ek >> 6) == j) g[j] += gv;
         }
       }
     }
     // load-balancing loss: d/dl_e = daux * (E / T) * p_e * (f_e - sum_j f_j p_j),
-    // p = softmax over all E, f_e = counts_e / T
+    // p = softmax over all E, f_e = counts_e / T; z-loss (mean over tokens of
+    // logsumexp^2): d/dl_e = daux * z_mult * (2 / T) * lse * p_e
     if (a.daux) {
       float m = -INFINITY;
 #pragma unroll
       for (int j = 0; j < kGateMaxPerLane; ++j) m = fmaxf(m, v[j]);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      m = wave_max(m);
       float p[kGateMaxPerLane], f[kGateMaxPerLane], s = 0.f;
 #pragma unroll
       for (int j = 0; j < kGateMaxPerLane; ++j) {
@@ -395,8 +448,9 @@ __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
       }
       fp = wave_sum(fp);
       const float scale = aux * float(a.E) / float(a.T);
+      const float zs = a.z_mult != 0.f ? aux * a.z_mult * 2.f * (m + logf(s)) / float(a.T) : 0.f;
 #pragma unroll
-      for (int j = 0; j < kGateMaxPerLane; ++j) g[j] += scale * p[j] * (f[j] - fp);
+      for (int j = 0; j < kGateMaxPerLane; ++j) g[j] += scale * p[j] * (f[j] - fp) + zs * p[j];
     }
 #pragma unroll
     for (int j = 0; j < kGateMaxPerLane; ++j) {
@@ -601,33 +655,47 @@ int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_
   return check_launch("fm_router_logits");
 }
 
-int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts, void* stream) {
+int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts,
+                     int64_t* tokens_per_expert, int64_t* total_tokens, int64_t tokens, void* stream) {
   FM_REQUIRE(indices && counts, "fm_expert_counts: null pointer");
   FM_REQUIRE(E >= 1 && E <= 1024, "fm_expert_counts: E must be in [1, 1024] (got %d)", E);
-  FM_REQUIRE(n >= 0, "fm_expert_counts: n must be >= 0");
+  FM_REQUIRE(n >= 0 && tokens >= 0, "fm_expert_counts: n and tokens must be >= 0");
+  FM_REQUIRE((tokens_per_expert == nullptr) == (total_tokens == nullptr),
+             "fm_expert_counts: tokens_per_expert and total_tokens go together");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (indices_i64)
     hipLaunchKernelGGL((expert_counts_kernel<int64_t>), dim3(1), dim3(1024), 0, s,
-                       static_cast<const int64_t*>(indices), n, E, counts);
+                       static_cast<const int64_t*>(indices), n, E, counts, tokens_per_expert, total_tokens, tokens);
   else
     hipLaunchKernelGGL((expert_counts_kernel<int32_t>), dim3(1), dim3(1024), 0, s,
-                       static_cast<const int32_t*>(indices), n, E, counts);
+                       static_cast<const int32_t*>(indices), n, E, counts, tokens_per_expert, total_tokens, tokens);
   return check_launch("fm_expert_counts");
 }
 
-int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, const void* indices,
-                   int indices_i64, const float* weights, const float* dweights, const float* daux,
-                   const int32_t* counts, float* dlogits, int64_t ld_d, void* stream) {
-  FM_REQUIRE(logits && indices && weights && dlogits, "fm_gating_grad: null pointer");
+int fm_score_bias_update(int64_t* tokens_per_expert, int64_t* total_tokens, int E, float gamma, float* score_bias,
+                         void* stream) {
+  FM_REQUIRE(tokens_per_expert && total_tokens && score_bias, "fm_score_bias_update: null pointer");
+  FM_REQUIRE(E >= 1 && E <= 1024, "fm_score_bias_update: E must be in [1, 1024] (got %d)", E);
+  hipLaunchKernelGGL(score_bias_update_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                     tokens_per_expert, total_tokens, E, gamma, score_bias);
+  return check_launch("fm_score_bias_update");
+}
+
+int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, int flags,
+                   int replay, const void* indices, int indices_i64, const float* dweights, const float* daux,
+                   const int32_t* counts, float z_loss_multiplier, float* dlogits, int64_t ld_d, void* stream) {
+  FM_REQUIRE(logits && indices && dlogits, "fm_gating_grad: null pointer");
   FM_REQUIRE(E >= 1 && E <= 64 * kGateMaxPerLane, "fm_gating_grad: E must be in [1, %d] (got %d)",
              64 * kGateMaxPerLane, E);
-  FM_REQUIRE(K >= 1 && K <= E, "fm_gating_grad: K must be in [1, E] (got %d)", K);
+  FM_REQUIRE(K >= 1 && K <= E && K <= 64, "fm_gating_grad: K must be in [1, min(E, 64)] (got %d)", K);
   FM_REQUIRE(gating == FM_GATING_SOFTMAX || gating == FM_GATING_SIGMOID, "fm_gating_grad: bad gating");
+  FM_REQUIRE((flags & ~FM_GATING_L2_NORMALIZE) == 0, "fm_gating_grad: unknown flags 0x%x", flags);
   FM_REQUIRE(daux == nullptr || counts != nullptr, "fm_gating_grad: the aux-loss gradient needs counts");
   FM_REQUIRE(ld_l >= E && ld_d >= E, "fm_gating_grad: pitch < E");
   if (T == 0) return 0;
-  const GatingGradArgs a{logits, T, ld_l, E, K, gating == FM_GATING_SIGMOID, indices, indices_i64, weights,
-                         dweights, daux, counts, dlogits, ld_d};
+  const GatingGradArgs a{logits, T, ld_l, E, K, (gating == FM_GATING_SIGMOID && !replay) ? 1 : 0,
+                         (flags & FM_GATING_L2_NORMALIZE) ? 1 : 0, indices, indices_i64, dweights, daux,
+                         counts, z_loss_multiplier, dlogits, ld_d};
   const int64_t blocks = (T + 3) / 4 < 4096 ? (T + 3) / 4 : 4096;
   hipLaunchKernelGGL(gating_grad_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("fm_gating_grad");

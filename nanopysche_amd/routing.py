@@ -84,11 +84,34 @@ def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: in
                        tile_expert, use_fp8)
 
 
+def _gating_code(gating) -> int:
+    return {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[str(gating).lower().split(".")[-1]]
+
+
+def _norm_flags(normalize) -> int:
+    if normalize is None:
+        return 0
+    if str(normalize).lower() == "l2":
+        return _lib.GATING_L2_NORMALIZE
+    raise ValueError(f"normalize_expert_weights must be None or 'l2', got {normalize!r}")
+
+
+N_WAVES = 1024   # waves of the gating kernel = rows of its per-wave partials
+
+
 def topk_gating(logits: torch.Tensor, top_k: int, gating: str = "softmax",
-                return_prob_partial: bool = False):
+                return_prob_partial: bool = False, *, replay_indices=None, normalize=None,
+                return_z_partial: bool = False):
     """Top-k gating over the last dimension of fp32 ``logits`` [..., E].
 
-    Returns (weights [..., K] fp32, indices [..., K] int64[, prob_partial])."""
+    ``replay_indices`` [..., K] (R3 routing replay, reference
+    ``model/moe.py:187-247``): the weights are softmax(logits) restricted to
+    those experts and renormalised, the K largest in order, for either gating.
+    ``normalize="l2"`` divides the K weights by their l2 norm + 1e-8
+    (``:167-170``).  Selection: NaN above every number, then larger, then the
+    lower expert index; no expert twice.
+
+    Returns (weights [..., K] fp32, indices [..., K] int64[, prob_partial][, z_partial])."""
     _lib.require_device(logits, "logits")
     if logits.dtype != torch.float32:
         raise TypeError("logits must be float32 (the router runs the gate in fp32)")
@@ -98,24 +121,35 @@ def topk_gating(logits: torch.Tensor, top_k: int, gating: str = "softmax",
     T = lg.shape[0]
     w = torch.empty(T, top_k, dtype=torch.float32, device=lg.device)
     idx = torch.empty(T, top_k, dtype=torch.int64, device=lg.device)
-    n_waves = 1024
-    part = torch.empty(n_waves, E, dtype=torch.float32, device=lg.device) if return_prob_partial else None
-    g = {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[str(gating).lower().split(".")[-1]]
-    _lib.call("fm_topk_gating", _lib.ptr(lg), T, E, E, top_k, g, _lib.ptr(w), _lib.ptr(idx), 1,
-              _lib.ptr(part), n_waves, _lib.stream_of(lg))
+    part = torch.empty(N_WAVES, E, dtype=torch.float32, device=lg.device) if return_prob_partial else None
+    zpart = torch.empty(N_WAVES, dtype=torch.float32, device=lg.device) if return_z_partial else None
+    rep = None
+    if replay_indices is not None:
+        rep = replay_indices.reshape(T, top_k)
+        if rep.dtype not in (torch.int64, torch.int32):
+            raise TypeError("replay_indices must be int64 or int32")
+        rep = rep.contiguous()
+    _lib.call("fm_topk_gating", _lib.ptr(lg), T, E, E, top_k, _gating_code(gating), _norm_flags(normalize),
+              _lib.ptr(rep), int(rep is not None and rep.dtype == torch.int64), _lib.ptr(w), _lib.ptr(idx), 1,
+              _lib.ptr(part), _lib.ptr(zpart), N_WAVES, _lib.stream_of(lg))
     w = w.reshape(*lead, top_k)
     idx = idx.reshape(*lead, top_k)
+    out = (w, idx)
     if return_prob_partial:
-        return w, idx, part
-    return w, idx
+        out += (part,)
+    if return_z_partial:
+        out += (zpart,)
+    return out
 
 
-def load_balancing_loss(prob_partial: torch.Tensor, counts: torch.Tensor, num_tokens: int) -> torch.Tensor:
-    """E * sum_e (counts[e]/T) * mean_t softmax(logits)[t, e] as a 0-d fp32 tensor."""
+def load_balancing_loss(prob_partial: torch.Tensor, counts: torch.Tensor, num_tokens: int,
+                        z_partial: torch.Tensor = None, z_loss_multiplier: float = 0.0) -> torch.Tensor:
+    """E * sum_e (counts[e]/T) * mean_t softmax(logits)[t, e] (+ z_loss_multiplier
+    * mean_t logsumexp(logits[t])^2 with ``z_partial``) as a 0-d fp32 tensor."""
     E = counts.numel()
     loss = torch.empty((), dtype=torch.float32, device=counts.device)
     _lib.call("fm_aux_loss", _lib.ptr(prob_partial), prob_partial.shape[0], _lib.ptr(counts), E,
-              num_tokens, _lib.ptr(loss), _lib.stream_of(counts))
+              num_tokens, _lib.ptr(z_partial), float(z_loss_multiplier), _lib.ptr(loss), _lib.stream_of(counts))
     return loss
 
 
@@ -146,31 +180,68 @@ def router_logits(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, sc
     return logits
 
 
-def expert_counts(indices: torch.Tensor, num_experts: int) -> torch.Tensor:
-    """[E] int32 number of routed slots per expert (indices outside [0, E) ignored)."""
+def expert_counts(indices: torch.Tensor, num_experts: int, load_tracker=None) -> torch.Tensor:
+    """[E] int32 number of routed slots per expert (indices outside [0, E) ignored);
+    with ``load_tracker`` also added to its running totals (with the number of
+    tokens, indices.numel() / K)."""
     idx = indices.contiguous()
     counts = torch.empty(num_experts, dtype=torch.int32, device=idx.device)
+    acc = tot = None
+    tokens = 0
+    if load_tracker is not None:
+        acc, tot = load_tracker.tokens_per_expert, load_tracker.total_tokens
+        tokens = idx.numel() // idx.shape[-1]
     _lib.call("fm_expert_counts", _lib.ptr(idx), int(idx.dtype == torch.int64), idx.numel(), num_experts,
-              _lib.ptr(counts), _lib.stream_of(idx))
+              _lib.ptr(counts), _lib.ptr(acc), _lib.ptr(tot), tokens, _lib.stream_of(idx))
     return counts
 
 
+class ExpertLoadTracker:
+    """Device-resident per-expert token counts of the DeepSeek-V3 score-bias
+    update (reference ``MoERouter._update_expert_counts`` / ``post_batch``,
+    ``model/moe.py:284-321``), with every tensor on the GPU (the reference adds
+    ``counts.cpu()`` into a buffer that lives on the model's device).
+
+    ``route(..., load_tracker=t)`` adds each forward's counts; ``t.post_batch(
+    score_bias, gamma)`` applies ``score_bias += gamma * (counts / tokens - 1 /
+    E)`` (the reference's sign) and clears the totals, no host sync.  With
+    expert parallelism all-reduce ``tokens_per_expert`` and ``total_tokens``
+    before ``post_batch``, as the reference does."""
+
+    def __init__(self, num_experts: int, device):
+        self.num_experts = num_experts
+        self.tokens_per_expert = torch.zeros(num_experts, dtype=torch.int64, device=device)
+        self.total_tokens = torch.zeros(1, dtype=torch.int64, device=device)
+
+    @torch.no_grad()
+    def post_batch(self, score_bias: torch.Tensor, gamma: float) -> None:
+        if score_bias.dtype != torch.float32 or not score_bias.is_contiguous() or score_bias.numel() != self.num_experts:
+            raise ValueError("score_bias must be a contiguous float32 tensor of num_experts values")
+        _lib.require_device(score_bias, "score_bias")
+        _lib.call("fm_score_bias_update", _lib.ptr(self.tokens_per_expert), _lib.ptr(self.total_tokens),
+                  self.num_experts, float(gamma), _lib.ptr(score_bias), _lib.stream_of(score_bias))
+
+
 class _RouterFunction(torch.autograd.Function):
-    """Gate + top-k gating + load-balancing loss, forward and backward on the GPU."""
+    """Gate + gating (top-k or replay, optional l2) + load-balancing loss (+ z-loss),
+    forward and backward on the GPU."""
 
     @staticmethod
-    def forward(ctx, x, gate_weight, gate_bias, score_bias, top_k, gating):
+    def forward(ctx, x, gate_weight, gate_bias, score_bias, top_k, gating, replay, normalize, z_mult, tracker):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1]).contiguous()
         T = x2.shape[0]
         logits = router_logits(x2, gate_weight, gate_bias, score_bias)
         E = logits.shape[1]
-        w, idx, part = topk_gating(logits, top_k, gating, return_prob_partial=True)
-        counts = expert_counts(idx, E)
-        aux = load_balancing_loss(part, counts, T)
-        ctx.save_for_backward(x2, gate_weight, logits, idx, w, counts)
-        ctx.gating = {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[
-            str(gating).lower().split(".")[-1]]
+        w, idx, part, zpart = topk_gating(logits, top_k, gating, True, replay_indices=replay, normalize=normalize,
+                                          return_z_partial=True)
+        counts = expert_counts(idx, E, tracker)
+        aux = load_balancing_loss(part, counts, T, zpart if z_mult else None, z_mult)
+        ctx.save_for_backward(x2, gate_weight, logits, idx, counts)
+        ctx.gating = _gating_code(gating)
+        ctx.flags = _norm_flags(normalize)
+        ctx.replay = replay is not None
+        ctx.z_mult = float(z_mult)
         ctx.has_bias = gate_bias is not None
         ctx.lead = lead
         ctx.mark_non_differentiable(idx)
@@ -178,7 +249,7 @@ class _RouterFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dweights, _dindices, daux):
-        x2, gate_weight, logits, idx, w, counts = ctx.saved_tensors
+        x2, gate_weight, logits, idx, counts = ctx.saved_tensors
         T, D = x2.shape
         E = logits.shape[1]
         K = idx.shape[1]
@@ -190,9 +261,9 @@ class _RouterFunction(torch.autograd.Function):
         if dwts is None and da is None:
             dlogits.zero_()
         else:
-            _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, ctx.gating, _lib.ptr(idx),
-                      int(idx.dtype == torch.int64), _lib.ptr(w), _lib.ptr(dwts), _lib.ptr(da), _lib.ptr(counts),
-                      _lib.ptr(dlogits), dlogits.stride(0), st)
+            _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, ctx.gating, ctx.flags,
+                      int(ctx.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), _lib.ptr(dwts), _lib.ptr(da),
+                      _lib.ptr(counts), ctx.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
         need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         wf = gate_weight.detach().float().contiguous()
         dx = torch.empty_like(x2) if need_x else None
@@ -210,17 +281,23 @@ class _RouterFunction(torch.autograd.Function):
             dx = dx.reshape(*ctx.lead, D)
         if dW is not None:
             dW = dW.to(gate_weight.dtype)
-        return dx, dW, db, None, None, None
+        return dx, dW, db, None, None, None, None, None, None, None
 
 
 def route(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, *, top_k: int, gating: str = "softmax",
-          score_bias=None):
-    """MoERouter.forward on the GPU (reference model/moe.py:133-184 without
-    jitter, routing replay, l2 normalisation or z-loss): fp32 gate logits
-    x.float() @ W.T + b (+ score_bias) -> top-k gating (softmax over the K
-    selected logits, or sigmoid / (sum + 1e-8)) -> (weights [..., K] fp32,
-    indices [..., K] int64, load-balancing loss E * sum_i f_i P_i).
-    Differentiable in x, gate_weight and gate_bias through the weights and the
-    loss."""
+          score_bias=None, replay_indices=None, normalize_expert_weights=None, z_loss_multiplier=None,
+          load_tracker: ExpertLoadTracker = None):
+    """MoERouter.forward on the GPU (reference model/moe.py:133-184, jitter
+    aside): fp32 gate logits x.float() @ W.T + b (+ score_bias) -> gating
+    (softmax over the K selected logits, sigmoid / (sum + 1e-8), or R3 replay
+    of ``replay_indices``) -> optional l2 normalisation of the weights ->
+    (weights [..., K] fp32, indices [..., K] int64, aux loss = E * sum_i f_i P_i
+    (+ z_loss_multiplier * mean logsumexp(logits)^2)).  ``load_tracker``
+    accumulates the per-expert counts for ``ExpertLoadTracker.post_batch``
+    (``_update_expert_counts``, :284-292; the reference does this whenever it
+    has a score bias).  Differentiable in x, gate_weight and gate_bias through
+    the weights and the loss."""
     _lib.require_device(x, "x")
-    return _RouterFunction.apply(x, gate_weight, gate_bias, score_bias, int(top_k), gating)
+    z = 0.0 if z_loss_multiplier is None else float(z_loss_multiplier)
+    return _RouterFunction.apply(x, gate_weight, gate_bias, score_bias, int(top_k), gating, replay_indices,
+                                 normalize_expert_weights, z, load_tracker)

@@ -30,8 +30,13 @@ PAD = 128
 
 
 def topk_lower_index(scores: np.ndarray, k: int) -> np.ndarray:
-    """Indices of the k largest per row, descending, ties -> lower index."""
-    order = np.argsort(-scores, axis=-1, kind="stable")
+    """Indices of the k largest per row, descending, ties -> lower index;
+    NaN ranks above every number (torch.topk's order), lower index first."""
+    scores = np.asarray(scores)
+    nan = np.isnan(scores)
+    key = np.where(nan, 0.0, -scores.astype(np.float64))
+    cols = np.broadcast_to(np.arange(scores.shape[-1]), scores.shape)
+    order = np.lexsort((cols, key, ~nan), axis=-1)
     return order[:, :k].astype(np.int64)
 
 
@@ -53,6 +58,51 @@ def sigmoid_topk(logits: np.ndarray, k: int):
     sel = np.take_along_axis(s, idx, axis=-1).astype(np.float64)
     w = (sel / (sel.sum(axis=-1, keepdims=True) + 1e-8)).astype(np.float32, copy=False)
     return w, idx
+
+
+def replay_gating(logits: np.ndarray, replay_idx: np.ndarray, k: int):
+    """model/moe.py:187-247 (R3 routing replay): p = softmax(logits) over all
+    E; weights = p on the replayed experts renormalised by their sum (clamped
+    to >= 1e-8); the k largest of that masked distribution, descending (ties
+    to the lower index).  Softmax in float64, rounded to fp32 at the end."""
+    logits = np.asarray(logits, dtype=np.float64)
+    p = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    p = p / p.sum(axis=-1, keepdims=True)
+    mask = np.zeros_like(p)
+    np.put_along_axis(mask, np.asarray(replay_idx, dtype=np.int64), 1.0, axis=-1)
+    mp = p * mask
+    mp = mp / np.maximum(mp.sum(axis=-1, keepdims=True), 1e-8)
+    mp32 = mp.astype(np.float32)
+    idx = topk_lower_index(mp32, k)
+    return np.take_along_axis(mp32, idx, axis=-1), idx
+
+
+def l2_normalize(w: np.ndarray) -> np.ndarray:
+    """model/moe.py:167-170: w / (||w||_2 + 1e-8) over the K weights (float64 inside)."""
+    w64 = np.asarray(w, dtype=np.float64)
+    return (w64 / (np.sqrt((w64 * w64).sum(axis=-1, keepdims=True)) + 1e-8)).astype(np.float32)
+
+
+def z_loss(logits: np.ndarray) -> float:
+    """model/moe.py:176-178: mean over tokens of logsumexp(logits)^2 (float64)."""
+    lg = np.asarray(logits, dtype=np.float64)
+    m = lg.max(axis=-1, keepdims=True)
+    lse = (m + np.log(np.exp(lg - m).sum(axis=-1, keepdims=True)))[..., 0]
+    return float((lse * lse).mean())
+
+
+def score_bias_update(score_bias: np.ndarray, tokens_per_expert: np.ndarray, total_tokens: int, gamma: float):
+    """model/moe.py:294-321 on one GPU, in fp32 as the reference's tensors are:
+    score_bias + gamma * (tokens_per_expert / total - 1 / E); unchanged when
+    total is 0.  ``total`` counts tokens (B * S), so the actual fractions sum
+    to K (``_update_expert_counts``, :284-292)."""
+    sb = np.asarray(score_bias, dtype=np.float32)
+    if total_tokens == 0:
+        return sb.copy()
+    E = sb.size
+    actual = np.asarray(tokens_per_expert).astype(np.float32) / np.float32(total_tokens)
+    ideal = np.float32(1.0) / np.float32(E)
+    return (sb + np.float32(gamma) * (actual - ideal)).astype(np.float32)
 
 
 def load_balancing_loss(logits: np.ndarray, idx: np.ndarray, num_experts: int) -> float:

@@ -167,3 +167,58 @@ def test_router_weight_grad(dev):
     rows = y.float()[plan.row_of.long()].reshape(T, K, D)
     ref = torch.einsum("td,tkd->tk", dout.float().double(), rows.double()).reshape(-1)
     assert torch.allclose(dw.double(), ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("E,K,gating", [(4, 1, "softmax"), (8, 2, "sigmoid"), (16, 4, "softmax"),
+                                        (64, 6, "sigmoid"), (256, 8, "softmax")])
+def test_topk_replay_and_l2(dev, E, K, gating):
+    """R3 replay (model/moe.py:187-247; softmax of the training logits over the
+    replayed experts, whatever the gating) and the l2 weight normalisation
+    (:167-170) against the oracle; T = 4093 ends the E <= 16 kernel's waves on
+    a partial group."""
+    T = 4093
+    g = torch.Generator().manual_seed(E * 7 + K)
+    logits = torch.randn(T, E, generator=g) * 2
+    mask = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    w, idx = fm.topk_gating(logits.to(dev), K, gating, replay_indices=mask.to(dev))
+    rw, ridx = orouting.replay_gating(logits.numpy(), mask.numpy(), K)
+    assert np.array_equal(_np(idx), ridx)
+    assert np.allclose(_np(w), rw, rtol=2e-6, atol=1e-7)
+    fn = orouting.softmax_topk if gating == "softmax" else orouting.sigmoid_topk
+    for replay in (None, mask.to(dev)):
+        w2, idx2 = fm.topk_gating(logits.to(dev), K, gating, replay_indices=replay, normalize="l2")
+        base = (rw, ridx) if replay is not None else fn(logits.numpy(), K)
+        assert np.array_equal(_np(idx2), base[1])
+        assert np.allclose(_np(w2), orouting.l2_normalize(base[0]), rtol=3e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("E", [8, 64])
+def test_topk_nan_and_minus_inf(dev, E):
+    """NaN ranks first (torch.topk's order), -inf logits (or a -inf score bias)
+    never make an expert win twice: indices equal the oracle's and every row
+    holds K distinct experts."""
+    K = 4
+    T = 256
+    g = torch.Generator().manual_seed(E)
+    logits = torch.randn(T, E, generator=g)
+    logits[::3, : E - 2] = -float("inf")      # only 2 finite experts: K-2 slots among -inf, lower index first
+    logits[1::7, 5] = float("nan")
+    for gating in ("softmax", "sigmoid"):
+        _, idx = fm.topk_gating(logits.to(dev), K, gating)
+        scores = logits.numpy() if gating == "softmax" else 1 / (1 + np.exp(-logits.numpy().astype(np.float64)))
+        ridx = orouting.topk_lower_index(scores.astype(np.float32), K)
+        assert np.array_equal(_np(idx), ridx), gating
+        assert all(len(set(r)) == K for r in _np(idx).tolist())
+        assert (_np(idx)[1::7, 0] == 5).all()   # NaN first
+
+
+def test_aux_loss_with_z_loss(dev):
+    T, E, K = 3000, 16, 2
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(T, E, generator=g) * 3
+    w, idx, part, zpart = fm.topk_gating(logits.to(dev), K, "softmax", True, return_z_partial=True)
+    counts = fm.expert_counts(idx, E)
+    z_mult = 0.01
+    loss = fm.load_balancing_loss(part, counts, T, zpart, z_mult)
+    ref = orouting.load_balancing_loss(logits.numpy(), _np(idx), E) + z_mult * orouting.z_loss(logits.numpy())
+    assert abs(loss.item() - ref) <= 1e-5 * abs(ref)

@@ -63,8 +63,8 @@ def test_argument_validation_without_device():
     rc = lib.fm_quantize(C.c_void_p(16), 0, 128, 100, 128, 1, C.c_void_p(16), 128, C.c_void_p(16), 1,
                          None, 0, None, 0, None)
     assert rc != 0 and b"multiple of 128" in lib.fm_last_error_string()
-    rc = lib.fm_topk_gating(C.c_void_p(16), 10, 300, 300, 2, 0, C.c_void_p(16), C.c_void_p(16), 1,
-                            None, 1024, None)
+    rc = lib.fm_topk_gating(C.c_void_p(16), 10, 300, 300, 2, 0, 0, None, 0, C.c_void_p(16), C.c_void_p(16), 1,
+                            None, None, 1024, None)
     assert rc != 0 and b"E must be" in lib.fm_last_error_string()
     op = _lib.FmGemmOperand()
     rc = lib.fm_grouped_gemm_ragged_m(0, C.byref(op), C.byref(op), 1, C.c_void_p(16), C.c_void_p(16),

@@ -174,3 +174,68 @@ def test_router_logits_matches_reference_linear():
     # a transposed operand or a dropped bias is caught
     bad = orouting.router_logits(x.float().numpy(), gate.weight.detach().float().numpy())
     assert not np.allclose(bad, ref, atol=1e-3)
+
+
+def _replay_reference(logits, mask_idx, K):
+    """MoERouter._routing_replay_gating (model/moe.py:187-247) as torch ops, float64."""
+    train_probs = F.softmax(logits, dim=-1)
+    N, E = logits.shape
+    full_mask = torch.zeros(N, E, dtype=logits.dtype)
+    for k in range(K):
+        full_mask.scatter_(1, mask_idx[:, k : k + 1], 1.0)
+    masked = train_probs * full_mask
+    s = masked.sum(dim=-1, keepdim=True).clamp(min=1e-8)
+    return (masked / s).topk(K, dim=-1)
+
+
+@pytest.mark.parametrize("E,K", [(8, 2), (64, 6), (256, 8)])
+def test_replay_gating_matches_reference_ops(E, K):
+    g = torch.Generator().manual_seed(E + K)
+    logits = torch.randn(300, E, generator=g) * 3
+    mask = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(300)])
+    rw, ridx = _replay_reference(logits.double(), mask, K)
+    w, idx = orouting.replay_gating(logits.numpy(), mask.numpy(), K)
+    assert np.array_equal(idx, ridx.numpy())
+    assert np.allclose(w, rw.numpy(), rtol=1e-6, atol=1e-9)
+    # the replayed experts are exactly the ones selected
+    assert all(set(a) == set(b) for a, b in zip(idx.tolist(), mask.tolist()))
+    # a permuted mask replays the same routing; a wrong one does not
+    w2, idx2 = orouting.replay_gating(logits.numpy(), mask.flip(1).numpy(), K)
+    assert np.array_equal(idx2, idx) and np.array_equal(w2, w)
+
+
+def test_l2_normalize_and_z_loss_match_reference_ops():
+    g = torch.Generator().manual_seed(5)
+    w = torch.rand(200, 4, generator=g)
+    ref = w.double() / (w.double().norm(dim=-1, keepdim=True) + 1e-8)      # model/moe.py:167-170
+    assert np.allclose(orouting.l2_normalize(w.numpy()), ref.numpy(), rtol=1e-6)
+    logits = torch.randn(2, 128, 16, generator=g) * 4
+    zref = torch.logsumexp(logits.double(), dim=-1).square().mean()         # model/moe.py:176-178
+    assert abs(orouting.z_loss(logits.reshape(-1, 16).numpy()) - float(zref)) < 1e-9 * float(zref)
+
+
+def test_score_bias_update_matches_reference_ops():
+    """post_batch's fp32 arithmetic (model/moe.py:307-317) as torch ops: bit-exact."""
+    g = torch.Generator().manual_seed(6)
+    E, K, B, S = 16, 2, 4, 256
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(B * S)]).reshape(B, S, K)
+    counts = torch.stack([(idx == e).sum() for e in range(E)])                 # :288-289
+    total = torch.tensor(idx.shape[0] * idx.shape[1])                            # :291 (B * S tokens)
+    sb = torch.randn(E, generator=g) * 0.1
+    gamma = 0.003
+    actual = counts.float() / total.float()
+    ideal = torch.ones(E) / E
+    ref = sb + gamma * (actual - ideal)
+    got = orouting.score_bias_update(sb.numpy(), counts.numpy(), int(total), gamma)
+    assert np.array_equal(got.view(np.uint32), ref.numpy().view(np.uint32))
+    assert np.isclose(actual.sum().item(), K)                                    # fractions sum to K
+    assert np.array_equal(orouting.score_bias_update(sb.numpy(), counts.numpy(), 0, gamma), sb.numpy())
+
+
+def test_topk_nan_first_and_no_duplicates():
+    s = np.array([[1, 3, np.nan, 3, -np.inf, -np.inf], [-np.inf] * 6, [np.nan, 0, np.nan, 1, 2, 3]],
+                 np.float32)
+    idx = orouting.topk_lower_index(s, 6)
+    assert idx.tolist() == [[2, 1, 3, 0, 4, 5], [0, 1, 2, 3, 4, 5], [0, 2, 5, 4, 3, 1]]
+    t = torch.from_numpy(s).topk(6).indices.numpy()
+    assert t[0, 0] == 2 and all(len(set(r)) == 6 for r in t)   # torch: NaN first, no repeats
