@@ -303,6 +303,14 @@ int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u,
                        void* s, int64_t ld_s, void* qt, int64_t ld_qt, void* st, int64_t ld_st,
                        const int32_t* tile_valid, void* stream);
 
+/* The fp32 values fm_swiglu_quantize (dh == NULL: h = silu(g) * u, out [rows, H])
+ * and fm_swiglu_backward (out [rows, 2H] = [dg | du]) quantise, computed by
+ * the same device code and written unrounded -- for checking those fused
+ * kernels' arithmetic against the reference's silu (model/moe.py:1181-1183)
+ * and their quantisation against a quantiser applied to these values. */
+int fm_swiglu_values(const void* g, int64_t ld_g, const void* u, int64_t ld_u, const void* dh, int64_t ld_dh,
+                     int64_t rows, int64_t H, float* out, int64_t ld_out, void* stream);
+
 /* ------------------------------------------------------- grouped GEMM ---- */
 /* One operand of the grouped GEMM: K-contiguous rows.  Scale of (row, kb) is
  * scale[g*scale_group_stride + (row >> scale_row_shift)*scale_row_stride +

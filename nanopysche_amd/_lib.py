@@ -108,6 +108,7 @@ SIGNATURES = {
                                   _i64, _vp, _i64, _vp, _vp]),
     "fm_swiglu_backward": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp,
                                   _i64, _vp, _i64, _vp, _i64, _vp, _vp]),
+    "fm_swiglu_values": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "fm_grouped_gemm_ragged_m": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _vp, _i32, _i64, _i64, _vp,
                                         _i32, _vp, _i32, _i64, _vp]),
     "fm_grouped_gemm_ragged_k": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,

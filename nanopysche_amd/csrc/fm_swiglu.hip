@@ -5,16 +5,32 @@
 //   fm_swiglu_backward      -- [dg | du] from one read of g, u and dh, emitted
 //                              the same way (the [M, 2H] layout feeds the fused
 //                              dx = dg w1 + du w3 GEMM and the dW1|dW3 GEMM)
-// silu(g) = g * s, s = sigmoid(g) = 1 / (1 + 2^(-g log2 e)) from the hardware
-// v_exp_f32 and v_rcp_f32 (a few fp32 ulps; test_gpu_swiglu.py holds the
-// results to torch's CPU silu and autograd); d silu = s (1 + g (1 - s)).
+// silu(g) = g / (1 + e^-g) and d silu = s (1 + g (1 - s)), s = 1 / (1 + e^-g),
+// in the reference's (torch's) order of operations; test_gpu_swiglu.py holds
+// the results to within 2 ulp of torch's CPU silu and autograd.
 #include "fm_tile.h"
 #include "../../include/fm_hip.h"
 
 namespace fm {
 
-__device__ __forceinline__ float sigmoidf(float g) {
-  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+// sigmoid(g) = 1 / d and silu(g) = g / d, d = 1 + e^-g: the expressions of the
+// reference's torch silu and its backward (x / (1 + exp(-x)), sigmoid =
+// 1 / (1 + exp(-x))).  e^-g from the device libm expf (~1 ulp); both
+// quotients from the hardware reciprocal refined by one Newton step and a
+// residual correction (within an ulp of the rounded quotient).  d infinite
+// (g < -88.7): sigmoid 0 and silu -0, as IEEE division gives.
+struct SigSilu {
+  float s, silu;
+};
+__device__ __forceinline__ SigSilu sig_silu(float g) {
+  const float e = expf(-g);
+  const float d = 1.f + e;
+  float r = __builtin_amdgcn_rcpf(d);
+  r = fmaf(fmaf(-d, r, 1.f), r, r);
+  float q = g * r;
+  q = fmaf(fmaf(-d, q, g), r, q);
+  const bool fin = d <= 3.40282347e38f;
+  return SigSilu{fin ? r : 0.f, fin ? q : g * 0.f};
 }
 
 struct SwigluSrc {
@@ -30,11 +46,12 @@ struct SwigluSrc {
                *reinterpret_cast<const uint4*>(u + row * ld_u + col)};
   }
   __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
+#pragma clang fp contract(off)   // every product rounded: the same values in every kernel that inlines this
     float gv[8], uv[8];
     unpack8_bf16(r.g, gv);
     unpack8_bf16(r.u, uv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[0][i] = (gv[i] * sigmoidf(gv[i])) * uv[i];
+    for (int i = 0; i < 8; ++i) v[0][i] = sig_silu(gv[i]).silu * uv[i];
   }
 };
 
@@ -55,18 +72,40 @@ struct SwigluBwdSrc {
                *reinterpret_cast<const uint4*>(dh + row * ld_dh + col)};
   }
   __device__ __forceinline__ void compute(const Raw& r, float v[][8]) const {
+#pragma clang fp contract(off)   // every product and sum rounded, as in the other kernels inlining this
     float gv[8], uv[8], dv[8];
     unpack8_bf16(r.g, gv);
     unpack8_bf16(r.u, uv);
     unpack8_bf16(r.dh, dv);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float s = sigmoidf(gv[i]);
-      v[0][i] = dv[i] * uv[i] * s * (1.f + gv[i] * (1.f - s));
-      v[1][i] = dv[i] * (gv[i] * s);
+      // torch autograd of silu(g) * u: dy = dh * u, dg = dy * s * (1 + g (1 - s)),
+      // du = dh * silu(g), each operation rounded in this order
+      const SigSilu ss = sig_silu(gv[i]);
+      v[0][i] = ((dv[i] * uv[i]) * ss.s) * (1.f + gv[i] * (1.f - ss.s));
+      v[1][i] = dv[i] * ss.silu;
     }
   }
 };
+
+// The fp32 values a source hands to the tile producer, written out as they
+// are (one thread per 8 columns of a row): what the fused quantisers round.
+template <typename Src>
+__global__ __launch_bounds__(256) void source_values_kernel(Src src, int64_t rows, int64_t cols, float* out,
+                                                            int64_t ld_out, int64_t col_off1) {
+  const int64_t chunks = cols / 8;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < rows * chunks; i += int64_t(gridDim.x) * 256) {
+    const int64_t r = i / chunks, c = (i % chunks) * 8;
+    float v[Src::kOut][8];
+    src.compute(src.fetch(r, c), v);
+#pragma unroll
+    for (int o = 0; o < Src::kOut; ++o) {
+      float* p = out + r * ld_out + c + o * col_off1;
+      *reinterpret_cast<float4*>(p) = make_float4(v[o][0], v[o][1], v[o][2], v[o][3]);
+      *reinterpret_cast<float4*>(p + 4) = make_float4(v[o][4], v[o][5], v[o][6], v[o][7]);
+    }
+  }
+}
 
 }  // namespace fm
 
@@ -100,6 +139,29 @@ int fm_swiglu_backward(const void* g, int64_t ld_g, const void* u, int64_t ld_u,
                    static_cast<const uint16_t*>(dh), ld_g, ld_u, ld_dh};
   return launch_tile_producer(src, o, rows, H, static_cast<hipStream_t>(stream),
                               "fm_swiglu_backward");
+}
+
+int fm_swiglu_values(const void* g, int64_t ld_g, const void* u, int64_t ld_u, const void* dh, int64_t ld_dh,
+                     int64_t rows, int64_t H, float* out, int64_t ld_out, void* stream) {
+  FM_REQUIRE((g && u && out) || rows == 0, "fm_swiglu_values: null pointer");
+  FM_REQUIRE(H % 8 == 0 && ld_g % 8 == 0 && ld_u % 8 == 0 && (dh == nullptr || ld_dh % 8 == 0),
+             "fm_swiglu_values: H and pitches must be multiples of 8");
+  FM_REQUIRE(ld_out % 4 == 0 && ld_out >= (dh ? 2 * H : H), "fm_swiglu_values: output pitch too small");
+  if (rows == 0) return 0;
+  const int64_t n = rows * (H / 8);
+  const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  if (dh) {
+    SwigluBwdSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+                     static_cast<const uint16_t*>(dh), ld_g, ld_u, ld_dh};
+    hipLaunchKernelGGL(source_values_kernel<SwigluBwdSrc>, dim3(blocks), dim3(256), 0, sm, src, rows, H, out,
+                       ld_out, H);
+  } else {
+    SwigluSrc src{static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), ld_g, ld_u};
+    hipLaunchKernelGGL(source_values_kernel<SwigluSrc>, dim3(blocks), dim3(256), 0, sm, src, rows, H, out,
+                       ld_out, 0);
+  }
+  return check_launch("fm_swiglu_values");
 }
 
 }  // extern "C"
