@@ -57,6 +57,10 @@ extern "C" {
 /* ------------------------------------------------------------ library ---- */
 const char* fm_last_error_string(void);
 const char* fm_version(void);
+/* Hash of the sources the library was built from (csrc/ and include/), set
+ * by the build; the Python loader refuses a library whose hash differs from
+ * the sources beside it (a stale build). */
+const char* fm_source_hash(void);
 /* Host-side codec (no GPU): the same f32 -> e4m3 routine the kernels use,
  * exported so tests can check it against other implementations. */
 void fm_host_encode_e4m3(const float* in, uint8_t* out, int64_t n);
@@ -226,7 +230,9 @@ int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x
                        int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
                        int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Sizes for fm_route_sort: padded-buffer row bound, and workspace bytes. */
+/* Sizes for fm_route_sort: padded-buffer row bound 128 * max(1, floor((A +
+ * 127 E) / 128)) (every group padded to 128 rows fits; one group: exactly
+ * the padded rows), and workspace bytes. */
 int64_t fm_route_rows_max(int64_t assignments, int E);
 int64_t fm_route_workspace_bytes(int64_t assignments, int E);
 

@@ -66,6 +66,7 @@ _OPND = C.POINTER(FmGemmOperand)
 SIGNATURES = {
     "fm_last_error_string": (C.c_char_p, []),
     "fm_version": (C.c_char_p, []),
+    "fm_source_hash": (C.c_char_p, []),
     "fm_host_encode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_host_decode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_convert_check": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
@@ -138,6 +139,13 @@ def load() -> C.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            from .build import source_hash
+
+            built, now = lib.fm_source_hash().decode(), source_hash()
+            if built != now:
+                raise RuntimeError(
+                    f"{LIB_PATH} was built from other sources (stamp {built}, sources {now}): rebuild it "
+                    "with `python -m nanopysche_amd.build`")
             _lib = lib
     return _lib
 

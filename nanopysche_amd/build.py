@@ -23,6 +23,22 @@ SOURCES = ["fm_api.cpp", "fm_quant.hip", "fm_route.hip", "fm_swiglu.hip", "fm_ge
 ARCH = "gfx950"
 
 
+def source_hash() -> str:
+    """Hash of every file the library is built from (csrc/ and include/); the
+    build stamps it into libfm_hip.so and the loader refuses a library whose
+    stamp differs from the sources beside it."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *CSRC.glob("*.cpp"),
+                    *(PKG.parent / "include").glob("*.h")])
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -48,10 +64,13 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     obj_dir.mkdir(exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
 
+    stamp = source_hash()
+
     def compile_one(src: str) -> Path:
         obj = obj_dir / (src.replace(".", "_") + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmd = [hipcc, *_flags(), *lang, "-c", str(CSRC / src), "-o", str(obj)]
+        extra = [f'-DFM_SOURCE_HASH="{stamp}"'] if src == "fm_api.cpp" else []
+        cmd = [hipcc, *_flags(), *extra, *lang, "-c", str(CSRC / src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -33,7 +33,12 @@ extern "C" {
 
 const char* fm_last_error_string(void) { return fm::g_error; }
 
-const char* fm_version(void) { return "fm_hip 0.1 gfx950"; }
+const char* fm_version(void) { return "fm_hip 0.2 gfx950"; }
+
+#ifndef FM_SOURCE_HASH
+#define FM_SOURCE_HASH "unstamped"
+#endif
+const char* fm_source_hash(void) { return FM_SOURCE_HASH; }
 
 void fm_host_encode_e4m3(const float* in, uint8_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = fm::f32_to_e4m3(in[i]);

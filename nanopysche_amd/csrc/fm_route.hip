@@ -687,8 +687,12 @@ int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* count
   return check_launch("fm_aux_loss");
 }
 
+// sum_e ceil(n_e / 128) <= sum_e (n_e + 127) / 128 = (A + 127 E) / 128, an
+// integer, so the padded groups fit in floor((A + 127 E) / 128) tiles (E = 1:
+// exactly ceil(A / 128)); at least one tile.
 int64_t fm_route_rows_max(int64_t assignments, int E) {
-  return (assignments + int64_t(E) * 127 + 127) / 128 * 128;
+  const int64_t tiles = (assignments + int64_t(E) * 127) / 128;
+  return (tiles > 0 ? tiles : 1) * 128;
 }
 
 int64_t fm_route_workspace_bytes(int64_t assignments, int E) {

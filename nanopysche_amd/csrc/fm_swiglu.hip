@@ -13,22 +13,46 @@
 
 namespace fm {
 
-// sigmoid(g) = 1 / d and silu(g) = g / d, d = 1 + e^-g: the expressions of the
-// reference's torch silu and its backward (x / (1 + exp(-x)), sigmoid =
-// 1 / (1 + exp(-x))).  e^-g from the device libm expf (~1 ulp); both
-// quotients from the hardware reciprocal refined by one Newton step and a
+// e^-g to about an ulp: 2^(-g log2 e) with the product split into a rounded
+// part and its exact remainder (the remainder's share of the exponent would
+// otherwise cost |g| 2^-24 ln 2 relative), the hardware 2^x on the fraction
+// of the rounded part plus the remainder (|x| <= 0.5 + 2^-24), and the integer
+// part as an exponent.  Overflow (g < -88.7) gives +inf, which the callers
+// treat as IEEE division would.
+__device__ __forceinline__ float exp_neg(float g) {
+#pragma clang fp contract(off)   // ph must be rounded: pl is its exact remainder
+  constexpr float kL = 1.44269502162933349609375f;   // RN(log2 e)
+  constexpr float kLlo = 1.925963033500011e-08f;     // log2 e - kL
+  const float ph = -g * kL;
+  const float pl = fmaf(-g, kLlo, fmaf(-g, kL, -ph));
+  const float n = __builtin_rintf(ph);   // 2^x on x in [-0.5, 0.5], then the exponent
+  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), int(n));
+}
+
+// silu(g) = g / d and sigmoid(g) = 1 / d, d = 1 + e^-g: the expressions of
+// the reference's torch silu and its backward (x / (1 + exp(-x)), sigmoid =
+// 1 / (1 + exp(-x))).  Quotients from the hardware reciprocal with a
 // residual correction (within an ulp of the rounded quotient).  d infinite
 // (g < -88.7): sigmoid 0 and silu -0, as IEEE division gives.
+__device__ __forceinline__ float silu_only(float g) {
+#pragma clang fp contract(off)
+  const float d = 1.f + exp_neg(g);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q0 = g * r;
+  const float q = fmaf(fmaf(-d, q0, g), r, q0);
+  return d <= 3.40282347e38f ? q : g * 0.f;
+}
+
 struct SigSilu {
   float s, silu;
 };
 __device__ __forceinline__ SigSilu sig_silu(float g) {
-  const float e = expf(-g);
-  const float d = 1.f + e;
+#pragma clang fp contract(off)
+  const float d = 1.f + exp_neg(g);
   float r = __builtin_amdgcn_rcpf(d);
   r = fmaf(fmaf(-d, r, 1.f), r, r);
-  float q = g * r;
-  q = fmaf(fmaf(-d, q, g), r, q);
+  const float q0 = g * r;
+  const float q = fmaf(fmaf(-d, q0, g), r, q0);
   const bool fin = d <= 3.40282347e38f;
   return SigSilu{fin ? r : 0.f, fin ? q : g * 0.f};
 }
@@ -51,7 +75,7 @@ struct SwigluSrc {
     unpack8_bf16(r.g, gv);
     unpack8_bf16(r.u, uv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[0][i] = sig_silu(gv[i]).silu * uv[i];
+    for (int i = 0; i < 8; ++i) v[0][i] = silu_only(gv[i]) * uv[i];
   }
 };
 

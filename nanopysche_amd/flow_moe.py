@@ -514,39 +514,47 @@ class ExpertWeights:
     w2t   [E][D, H]   forward down             (w2_e transposed)
     w2    [E][H, D]   dgrad dH = dY w2_e^T
     w13t  [E][D, 2H]  dgrad dX = [dg|du] [w1_e; w3_e]
-    """
+
+    The forward pair is always built; the dgrad pair only when ``need_dgrad``
+    (a forward that records a backward), from the same read of the weights
+    (the transposed outputs of one launch)."""
 
     def __init__(self, kind: int):
         self.kind = kind
         self.key = None
+        self.has_dgrad = False
         self.w13 = self.w2t = self.w2 = self.w13t = None
 
-    def refresh(self, w1, w2, w3, E: int) -> "ExpertWeights":
+    def refresh(self, w1, w2, w3, E: int, need_dgrad: bool = True) -> "ExpertWeights":
         key = tuple((w.data_ptr(), w._version, w.dtype) for w in (w1, w2, w3))
-        if key != self.key:
-            self._build(w1.detach(), w2.detach(), w3.detach(), E)
+        if key != self.key or (need_dgrad and not self.has_dgrad):
+            self.w13 = self.w2t = self.w2 = self.w13t = None
+            self._build(w1.detach(), w2.detach(), w3.detach(), E, need_dgrad)
             self.key = key
+            self.has_dgrad = need_dgrad
         return self
 
-    def _build(self, w1, w2, w3, E):
+    def _build(self, w1, w2, w3, E, dgrad=True):
         EH, D = w1.shape
         H = EH // E
         dev = w1.device
         kind = self.kind
         if kind == _lib.QUANT_MX:
-            self._build_mx(w1, w2, w3, E, H, D)
+            self._build_mx(w1, w2, w3, E, H, D, dgrad)
             return
         pay = torch.bfloat16 if kind == _lib.QUANT_BF16 else torch.uint8
         f32 = torch.float32
-        W13 = torch.empty(E, 2 * H, D, dtype=pay, device=dev)
-        W13t = torch.empty(E, D, 2 * H, dtype=pay, device=dev)
-        W2 = torch.empty(E, H, D, dtype=pay, device=dev)
-        W2t = torch.empty(E, D, H, dtype=pay, device=dev)
         fp8 = kind != _lib.QUANT_BF16
+        W13 = torch.empty(E, 2 * H, D, dtype=pay, device=dev)
+        W2t = torch.empty(E, D, H, dtype=pay, device=dev)
         S13 = torch.empty(E, 2 * H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
-        S13t = torch.empty(E, D // 128, 2 * H // 128, dtype=f32, device=dev) if fp8 else None
-        S2 = torch.empty(E, H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
         S2t = torch.empty(E, D // 128, H // 128, dtype=f32, device=dev) if fp8 else None
+        W13t = W2 = S13t = S2 = None
+        if dgrad:
+            W13t = torch.empty(E, D, 2 * H, dtype=pay, device=dev)
+            W2 = torch.empty(E, H, D, dtype=pay, device=dev)
+            S13t = torch.empty(E, D // 128, 2 * H // 128, dtype=f32, device=dev) if fp8 else None
+            S2 = torch.empty(E, H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
         stream = _lib.stream_of(w1)
 
         srcs = [w.contiguous() for w in (w1, w3, w2)]
@@ -560,34 +568,37 @@ class ExpertWeights:
                 _lib.ptr(dst_t), rows_out, D * rows_out, col_off,
                 _lib.ptr(s_t), rows_out // 128, (D // 128) * (rows_out // 128))
 
-        # w1 and w3 into the rows (and transposed columns) of the [E, 2H, D]
-        # gate|up operand, w2 into its own: one launch
+        # w1 and w3 into the rows (and transposed columns) of the [E, 2H, D] gate|up
+        # operand, w2 into its transpose (and its own rows): one launch
         jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, W13t, S13t, 0, 0, 2 * H),
                                       job(srcs[1], W13, S13, W13t, S13t, H, H, 2 * H),
                                       job(srcs[2], W2, S2, W2t, S2t, 0, 0, H))
         _lib.call("fm_quantize_weight_batch", jobs, 3, stream)
         sh = 7
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, (2 * H // 128) * (D // 128), sh, 2 * H, D)
-        self.w13t = ExpertWeightOperand(W13t, S13t, 2 * H, D * 2 * H, 2 * H // 128, 1, (D // 128) * (2 * H // 128), sh, D, 2 * H)
-        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, (H // 128) * (D // 128), sh, H, D)
         self.w2t = ExpertWeightOperand(W2t, S2t, H, D * H, H // 128, 1, (D // 128) * (H // 128), sh, D, H)
+        if dgrad:
+            self.w13t = ExpertWeightOperand(W13t, S13t, 2 * H, D * 2 * H, 2 * H // 128, 1,
+                                            (D // 128) * (2 * H // 128), sh, D, 2 * H)
+            self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, (H // 128) * (D // 128), sh, H, D)
 
-    def _build_mx(self, w1, w2, w3, E, H, D):
+    def _build_mx(self, w1, w2, w3, E, H, D, dgrad):
         dev = w1.device
         w1, w2, w3 = (w.contiguous() for w in (w1, w2, w3))
         stream = _lib.stream_of(w1)
         MX = _lib.QUANT_MX
         # gate|up: w1 and w3 read in place as the [E, 2H, D] stack
-        W13, S13, W13t, S13t = _alloc_quant(E * 2 * H, D, MX, True, True, dev)
+        W13, S13, W13t, S13t = _alloc_quant(E * 2 * H, D, MX, True, dgrad, dev)
         _lib.call("fm_quantize_pair", _lib.ptr(w1), _lib.ptr(w3), _src_dtype(w1), E, H, D, D,
                   *_tile_args(MX, W13, S13, W13t, S13t), stream)
-        W2, S2, W2t, S2t = _alloc_quant(E * H, D, MX, True, True, dev)
+        W2, S2, W2t, S2t = _alloc_quant(E * H, D, MX, dgrad, True, dev)
         _lib.call("fm_quantize", _lib.ptr(w2), _src_dtype(w2), E * H, D, D, *_tile_args(MX, W2, S2, W2t, S2t),
                   stream)
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 32, 1, 2 * H * D // 32, 0, 2 * H, D)
-        self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H)
-        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D)
         self.w2t = ExpertWeightOperand(W2t, S2t, E * H, H, 1, D, (H // 32) * D, 0, D, H)
+        if dgrad:
+            self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H)
+            self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D)
 
 
 # ================================================================= streams ====
@@ -675,6 +686,7 @@ class FP8FlowMoECompute:
         # (no unpermute copies).
         self._dense = False
         self._dense_plans = {}
+        self._record = True
 
     def set_weights(self, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> None:
         for w in (w1, w2, w3):
@@ -683,11 +695,11 @@ class FP8FlowMoECompute:
                                  f"[{self.num_experts * self.hidden_size}, {self.d_model}], got {tuple(w.shape)}")
         self._w = (w1, w2, w3)
 
-    def _weights(self, kind: int) -> ExpertWeights:
+    def _weights(self, kind: int, need_dgrad: bool = True) -> ExpertWeights:
         ew = self._cache.get(kind)
         if ew is None:
             ew = self._cache[kind] = ExpertWeights(kind)
-        return ew.refresh(*self._w, self.num_experts)
+        return ew.refresh(*self._w, self.num_experts, need_dgrad)
 
     def modes(self, num_assignments: int):
         """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
@@ -713,6 +725,9 @@ class FP8FlowMoECompute:
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         K = indices.shape[-1]
+        # the dgrad weight operands are built only for a forward that records a backward
+        self._record = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (x, weights, *self._w))
         out = _FlowMoEFunction.apply(x2, weights.reshape(-1, K), *self._w,
                                      indices.reshape(-1, K), self)
         return out.reshape(shape)
@@ -744,9 +759,9 @@ class FP8FlowMoECompute:
         for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
             if kind is None:
                 continue
-            ew = self._weights(kind)
+            ew = self._weights(kind, self._record)
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                   return_transpose=True, kmajor_scales=True)
+                                   return_transpose=self._record, kmajor_scales=True)
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}
@@ -754,12 +769,17 @@ class FP8FlowMoECompute:
             if kind is None:
                 continue
             # row blocks feed the down GEMM; the column blocks are kept for dW2
-            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, True, dev, plan.tile_expert,
+            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, self._record, dev, plan.tile_expert,
                                    kmajor=True)
             hrow, hcol = _wrap(q, s, qt, st, kind)
             h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
-        out = Y[:T] if self._dense else fused_unpermute_unpad(Y, plan, wts)
+        if self._dense:
+            # the output must not be a view made inside this Function (callers
+            # combine it in place): the padded buffer itself when T fills it
+            out = Y if R == T else Y[:T].clone()
+        else:
+            out = fused_unpermute_unpad(Y, plan, wts)
         if self.capture_intermediates is not None:
             self.capture_intermediates["gate_up"] = GU.detach().clone()
         ctx.compute = self
@@ -768,7 +788,9 @@ class FP8FlowMoECompute:
         ctx.saved_cols = {k: v[0] for k, v in saved.items()}
         ctx.saved_hcols = h_cols
         ctx.wdtypes = (w1.dtype, w2.dtype, w3.dtype)
-        ctx.save_for_backward(wts, GU, Y)
+        # Y only feeds the router-weight gradient (the dense path's outputs are
+        # views of Y: not saving it leaves them free for in-place use)
+        ctx.save_for_backward(wts, GU, Y if ctx.needs_input_grad[1] else None)
         return out if ctx.x_dtype == torch.bfloat16 else out.to(ctx.x_dtype)
 
     # ----------------------------------------------------------------- backward ----

@@ -200,3 +200,24 @@ def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
                 q, s = ofp8.quant_128x128(np.ascontiguousarray(src[e * n:(e + 1) * n].T), pow2=kind == "pow2")
                 assert np.array_equal(data[e], q), e
                 assert np.array_equal(scale[e], s), e
+
+
+def test_forward_without_grad_builds_forward_operands_only(dev):
+    """A no_grad forward quantises only the forward weight operands (w13,
+    w2t) and no column blocks; a later forward that records a backward
+    builds the dgrad operands and gives the same output."""
+    T, D, H, E, K = 512, 256, 256, 4, 2
+    x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=12)
+    cfg = fm.FP8FlowMoEConfig(True, fm.FP8RecipeConfig(True, fm.FP8RecipeType.FLOW_MOE))
+    blk = fm.FP8FlowMoECompute(cfg, D, H, E, fp8_gemm_threshold=0)
+    p = [t.to(dev).requires_grad_(True) for t in (w1, w2, w3)]
+    blk.set_weights(*p)
+    with torch.no_grad():
+        a = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
+    ew = next(iter(blk._cache.values()))
+    assert ew.w13 is not None and ew.w2t is not None and ew.w13t is None and ew.w2 is None
+    b = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
+    b.backward(go.to(dev))
+    assert ew.has_dgrad and ew.w13t is not None and ew.w2 is not None
+    assert torch.equal(a, b.detach())
+    assert p[0].grad is not None

@@ -40,16 +40,17 @@ def _case(T, D, H, seed):
 
 
 @pytest.mark.parametrize("recipe", ["blockwise", "flow_moe", "mxfp8"])
-@pytest.mark.parametrize("T", [1000, 2048])
-def test_shared_expert_fp8_matches_flow_oracle(dev, recipe, T):
-    """T = 1000: stage-synchronised (the oracle takes the device's bf16
-    gate|up and dH GEMM outputs), max|err| / max|ref| <= 2e-2.  T = 2048:
-    free-running, mean relative error <= 5e-3 and max <= 5e-2: on this case
-    the oracle against itself, with its gate|up sums perturbed by 1e-5
-    relative (the size of the MFMA's summation differences), already moves
-    the flow_moe output by 3.1% max-rel (one FP8 rounding or power-of-two
-    scale flips), so 2e-2 bounds only stage-synchronised runs here."""
-    D, H = 512, 384
+@pytest.mark.parametrize("shape", [(1000, 512, 384), (8192, 2048, 1408)])
+@pytest.mark.timeout(300)
+def test_shared_expert_fp8_matches_flow_oracle(dev, recipe, shape):
+    """T = 1000, D = 512: stage-synchronised (the oracle takes the device's
+    bf16 gate|up and dH GEMM outputs).  The configs[2] shape (T = 8192,
+    D = 2048, H = 1408): free-running, no shared intermediates, plus a mean
+    relative error <= 5e-3.  Both within max|err| / max|ref| <= 2e-2.  (On
+    small free-running cases one e4m3 rounding or power-of-two scale flip from
+    the MFMA's ~1e-5 relative summation differences weighs several percent of
+    a 512-deep output; at the configuration's sizes it does not.)"""
+    T, D, H = shape
     x, w1, w2, w3, go = _case(T, D, H, seed=T)
     blk = _make(recipe, D, H)
     taps = {} if T == 1000 else None
@@ -65,7 +66,7 @@ def test_shared_expert_fp8_matches_flow_oracle(dev, recipe, T):
         ref = ref.numpy() if torch.is_tensor(ref) else np.asarray(ref)
         g = got.float().cpu().numpy()
         e = olayer.max_rel_err(g, ref)
-        assert e <= (2e-2 if taps is not None else 5e-2), (recipe, name, e)
+        assert e <= 2e-2, (recipe, name, e)
         if taps is None:
             assert abs(g - ref).mean() <= 5e-3 * abs(ref).mean(), (recipe, name)
 
@@ -133,3 +134,23 @@ def test_shared_expert_adds_to_routed_output(dev):
     r2, _ = olayer.moe_flow_reference(x, torch.ones(T, 1), torch.zeros(T, 1, dtype=torch.int64), *sw, 1,
                                       recipe="flow_moe", taps=t2)
     assert olayer.max_rel_err(out.detach().float().cpu().numpy(), np.asarray(r1) + np.asarray(r2)) <= 2e-2
+
+
+def test_shared_expert_output_combined_in_place(dev):
+    """The dense path returns the first rows of its padded output buffer; the
+    reference combines it out of place (model/moe.py:1383-1384), and an
+    in-place combine must work too, backward included."""
+    T, D, H = 300, 256, 256
+    x, w1, w2, w3, go = _case(T, D, H, seed=3)
+    blk = _make("flow_moe", D, H)
+    p = [t.to(dev).requires_grad_(True) for t in (w1, w2, w3)]
+    blk.set_weights(*p)
+    xd = x.to(dev).requires_grad_(True)
+    routed = torch.randn(T, D, device=dev).bfloat16()
+    out = blk(xd)
+    ref = out.detach().float() + routed.float()
+    out += routed
+    out.backward(go.to(dev))
+    torch.cuda.synchronize()
+    assert torch.allclose(out.detach().float(), ref, rtol=1e-2, atol=1e-2)
+    assert xd.grad is not None and all(t.grad is not None for t in p)

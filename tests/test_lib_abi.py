@@ -70,8 +70,30 @@ def test_argument_validation_without_device():
     rc = lib.fm_grouped_gemm_ragged_m(0, C.byref(op), C.byref(op), 1, C.c_void_p(16), C.c_void_p(16),
                                       1, 128, 128, None, 1, C.c_void_p(16), 0, 128, None)
     assert rc != 0
-    assert lib.fm_route_rows_max(16384, 8) == (16384 + 8 * 127 + 127) // 128 * 128
+    assert lib.fm_route_rows_max(16384, 8) == (16384 + 8 * 127) // 128 * 128
+    assert lib.fm_route_rows_max(8192, 1) == 8192 and lib.fm_route_rows_max(1000, 1) == 1024
+    assert lib.fm_route_rows_max(0, 1) == 128
+    # the bound holds for every split of A over E experts (brute force, small sizes)
+    import itertools
+    for E in (1, 2, 3):
+        for counts in itertools.product(range(0, 300, 37), repeat=E):
+            need = sum(-(-c // 128) * 128 for c in counts)
+            assert lib.fm_route_rows_max(sum(counts), E) >= need, counts
     try:
         _lib.check(1, "probe")
     except RuntimeError as e:
         assert "probe" in str(e)
+
+
+def test_library_stamp_matches_sources(monkeypatch):
+    """The loader refuses a library built from other sources."""
+    from nanopysche_amd import build
+
+    assert _lib.load().fm_source_hash().decode() == build.source_hash()
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(build, "source_hash", lambda: "0000000000000000")
+    try:
+        _lib.load()
+        raise AssertionError("a stale library was accepted")
+    except RuntimeError as e:
+        assert "rebuild" in str(e)
