@@ -99,9 +99,10 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
                gemm_timer=True, pre_step=None, overlap=True, router=None):
     """Times `steps` calls of the expert block (forward, + backward when
     `backward`), weight cache dropped every step, with nothing recorded between
-    the launches.  With `router` = (gate weight, gate bias, top_k, gating) the
-    step is the MoE layer: the router (gate GEMM, gating with `idx` replayed as
-    an R3 routing mask, expert counts, load-balancing loss) runs first and the
+    the launches.  With `router` = (gate weight, gate bias, top_k, gating[,
+    replay]) the step is the MoE layer (FP8FlowMoELayer): the router (gate
+    GEMM, gating -- with `idx` replayed as an R3 routing mask unless replay is
+    False --, expert counts, load-balancing loss) and the expert block, and the
     backward takes out * go + aux loss through both (the Trainer's
     `loss + aux_loss`, reference train/trainer.py:320-339).  With `gemm_timer`,
     a second pass of `steps` identical steps then records HIP events around
@@ -124,18 +125,16 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     xr = x.detach().clone().requires_grad_(backward)
     wr = w.detach().clone().requires_grad_(backward)
     gparams = []
+    layer = None
     if router is not None:
+        # the MoE layer: router + expert block under one autograd node
         gparams = [t.detach().clone().requires_grad_(backward) for t in router[:2]]
+        layer = fm.FP8FlowMoELayer(cfg, D, H, E, router[2], gating=router[3], fp8_gemm_threshold=threshold)
+        layer.set_weights(*gparams, *params)
+        layer.block.overlap_streams = overlap
+        blk = layer.block
     one = torch.ones((), device=x.device)
-
-    replay = router[4] if router is not None and len(router) > 4 else True
-
-    def routed():
-        if router is not None:
-            return fm.route(xr, gparams[0], gparams[1], top_k=router[2], gating=router[3],
-                            replay_indices=idx if replay else None)
-        r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
-        return r_w, r_idx, None
+    replay = idx if (router is None or len(router) <= 4 or router[4]) else None
 
     def step():
         blk._cache.clear()  # weights change every training step: re-quantise them
@@ -144,16 +143,19 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
                 p.grad = None
             xr.grad = None
             wr.grad = None
-            r_w, r_idx, aux = routed()
-            out = blk(xr, r_w, r_idx, 0, E)
-            if aux is None:
-                out.backward(go)
-            else:
+            if layer is not None:
+                out, aux = layer(xr, replay_indices=replay)
                 torch.autograd.backward([out, aux], [go, one])
+            else:
+                r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
+                blk(xr, r_w, r_idx, 0, E).backward(go)
         else:
             with torch.no_grad():
-                r_w, r_idx, _ = routed()
-                blk(xr, r_w, r_idx, 0, E)
+                if layer is not None:
+                    layer(xr, replay_indices=replay)
+                else:
+                    r_w, r_idx = (wr, idx) if pre_step is None else pre_step()
+                    blk(xr, r_w, r_idx, 0, E)
 
     for _ in range(warmup):
         step()
@@ -269,7 +271,7 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
          nbq(GU, dH, *gq)),
         ("unpermute (weighted sum over top-k)",
          lambda: _lib.call("fm_unpermute", _lib.ptr(Y), Y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(wts), T, K, D,
-                           _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), st), nbq(Y) + nb(wts, out)),
+                           _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), None, 0, st), nbq(Y) + nb(wts, out)),
         ("expert weight re-quantisation (w1, w3, w2 in one launch, 128x128 pow2 + transposed)",
          lambda: ew._build(w1, w2, w3, E), wbytes),
     ]

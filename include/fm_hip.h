@@ -279,11 +279,14 @@ int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t*
 
 /* Replaces fp8_flow_moe.fused_unpermute_unpad (reference fp8/__init__.py:20)
  * and the weighted scatter-add of model/moe.py:1594:
- * out[t] = sum_k weights[t*K+k] * y[row_of[t*K+k]] (weights NULL -> 1),
- * fp32 sum in slot order, one rounding to out_dtype. */
+ * out[t] = addend[t] + sum_k weights[t*K+k] * y[row_of[t*K+k]] (weights NULL
+ * -> 1, addend bf16 [T, D] pitch ld_add or NULL -> 0), fp32 sum in slot order,
+ * one rounding to out_dtype.  The addend lets a MoE layer's input gradient
+ * take the router's share in the same pass (the sum autograd forms for an
+ * input feeding both the router and the experts, model/moe.py:1347-1375). */
 int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
                  int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
-                 void* stream);
+                 const void* addend, int64_t ld_add, void* stream);
 
 /* Gradient of the combine with respect to the router weights (autograd of
  * model/moe.py:1594 in the reference): dw[a] = <dout[a/K], y[row_of[a]]>. */

@@ -23,6 +23,7 @@ from .flow_moe import (
     quantize_to_fp8,
     scaling_aware_transpose,
 )
+from .moe_layer import FP8FlowMoELayer
 from .routing import (ExpertLoadTracker, RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens,
                       router_logits, topk_gating)
 
@@ -53,4 +54,5 @@ __all__ = [
     "router_logits",
     "expert_counts",
     "ExpertLoadTracker",
+    "FP8FlowMoELayer",
 ]

@@ -786,6 +786,8 @@ struct TileP {
   int e, i0, j0, j_end;
 };
 
+// Every wave computes the same values; wave 0 writes the one LDS copy, which
+// the others read after the barrier that follows.
 __device__ __forceinline__ void tile_queue_init(const GemmParams& p, TileQueue& q, int* lds) {
   const int lane = threadIdx.x & 63;
   int cnt = 0, o0 = 0, o1 = 0;
@@ -796,10 +798,12 @@ __device__ __forceinline__ void tile_queue_init(const GemmParams& p, TileQueue& 
   }
   const int incl = wave_incl_scan(cnt, lane);
   q.lds = lds;
-  lds[lane] = cnt;
-  lds[64 + lane] = incl;
-  lds[128 + lane] = o0;
-  lds[192 + lane] = o1;
+  if (threadIdx.x < 64) {
+    lds[lane] = cnt;
+    lds[64 + lane] = incl;
+    lds[128 + lane] = o0;
+    lds[192 + lane] = o1;
+  }
   q.NI = int((p.n_i + kT - 1) / kT);
   q.JT = __builtin_amdgcn_readlane(incl, 63);
   q.n_valid = q.JT * q.NI;
@@ -919,7 +923,7 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
-  constexpr int kQueue = 8 * 1024;   // tile queue, 1 KiB per wave
+  constexpr int kQueue = 1024;       // tile queue
   constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage + kSpare + kQueue + kArgs];
   // The operand descriptors are needed once per tile; the workgroup's LDS copy
@@ -938,7 +942,8 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
   w.p_mx_k = KIND == GK_FP8_MX && (MXL & 2) != 0;
 
   TileQueue tq;
-  tile_queue_init(p, tq, reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare + w.wave * 1024));
+  tile_queue_init(p, tq, reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare));
+  block_barrier();   // the tile queue is in LDS
   TileP cur;
   if (!tile_queue_get(tq, 0, cur)) return;
   TileStreams S = tile_streams<KIND>(p.Q, p.P, p.n_i, cur, w);

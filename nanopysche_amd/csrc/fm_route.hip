@@ -511,15 +511,26 @@ struct ZeroSrc {
 __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64_t ld_y,
                                                         const int32_t* row_of, const float* w,
                                                         int64_t T, int K, int64_t D,
-                                                        void* out, int out_f32, int64_t ld_out) {
+                                                        void* out, int out_f32, int64_t ld_out,
+                                                        const uint16_t* addend, int64_t ld_add) {
 #pragma clang fp contract(off)
   const int64_t chunks = D / 8;
   const int64_t n = T * chunks;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
     const int64_t t = i / chunks, c = (i % chunks) * 8;
     float acc[8];
+    if (addend) {   // the sum starts from the addend's row (bf16)
+      const uint4 pk = *reinterpret_cast<const uint4*>(addend + t * ld_add + c);
+      const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = u2f(q[j] << 16);
+        acc[2 * j + 1] = u2f(q[j] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    }
     for (int k = 0; k < K; ++k) {
       const int32_t r = row_of[t * K + k];
       if (r < 0) continue;
@@ -751,9 +762,9 @@ int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t*
 
 int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
                  int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
-                 void* stream) {
+                 const void* addend, int64_t ld_add, void* stream) {
   FM_REQUIRE((y && row_of && out) || T == 0, "fm_unpermute: null pointer");
-  FM_REQUIRE(D % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0,
+  FM_REQUIRE(D % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0 && (addend == nullptr || ld_add % 8 == 0),
              "fm_unpermute: D and pitches must be multiples of 8");
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_unpermute: bad out dtype");
   if (T == 0) return 0;
@@ -761,7 +772,7 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
   const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
   hipLaunchKernelGGL(unpermute_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
-                     out_dtype == FM_DTYPE_F32, ld_out);
+                     out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add);
   return check_launch("fm_unpermute");
 }
 

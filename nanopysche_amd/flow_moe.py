@@ -310,19 +310,25 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
 
 def fused_unpermute_unpad(y: torch.Tensor, plan: RoutingPlan,
                           weights: Optional[torch.Tensor] = None,
-                          out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """out[t] = sum_k weights[t, k] * y[row(t, k)] (weights None -> 1), summed
-    in fp32 in slot order and rounded once.  y is bf16 [rows_max, D]."""
+                          out_dtype: torch.dtype = torch.bfloat16,
+                          addend: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[t] = addend[t] + sum_k weights[t, k] * y[row(t, k)] (weights None ->
+    1, addend None -> 0), summed in fp32 in slot order and rounded once.  y
+    and addend are bf16 ([rows_max, D] and [T, D])."""
     _lib.require_device(y, "y")
     if y.dtype != torch.bfloat16:
         raise TypeError("y must be bfloat16")
     D = y.shape[1]
     T, K = plan.num_tokens, plan.top_k
+    if addend is not None and (addend.dtype != torch.bfloat16 or tuple(addend.shape) != (T, D)
+                               or addend.stride(1) != 1):
+        raise ValueError("addend must be a bf16 [T, D] tensor with unit column stride")
     out = torch.empty(T, D, dtype=out_dtype, device=y.device)
     w = None if weights is None else weights.reshape(-1).to(torch.float32).contiguous()
     od = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
     _lib.call("fm_unpermute", _lib.ptr(y), y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(w), T, K, D,
-              _lib.ptr(out), od, out.stride(0), _lib.stream_of(y))
+              _lib.ptr(out), od, out.stride(0), _lib.ptr(addend), 0 if addend is None else addend.stride(0),
+              _lib.stream_of(y))
     return out
 
 
@@ -794,7 +800,11 @@ class FP8FlowMoECompute:
         return out if ctx.x_dtype == torch.bfloat16 else out.to(ctx.x_dtype)
 
     # ----------------------------------------------------------------- backward ----
-    def _backward(self, ctx, grad_out):
+    def _backward(self, ctx, grad_out, on_router_grad=None):
+        """Gradients of the expert block.  ``on_router_grad(dw)`` (a MoE layer
+        whose router feeds this block) is called with the router-weight
+        gradient as soon as it exists and returns a bf16 [T, D] addend for the
+        input gradient (the router's share of it), summed in the unpermute."""
         wts, GU, Y = ctx.saved_tensors
         plan = ctx.plan
         fp8_kind, use_bf16 = ctx.kinds
@@ -811,6 +821,7 @@ class FP8FlowMoECompute:
             dw = torch.empty(T * K, dtype=torch.float32, device=dev)
             _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
                       _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
+        dx_addend = None if on_router_grad is None else on_router_grad(None if dw is None else dw.reshape(T, K))
         dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
         dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         w1dt, w2dt, w3dt = ctx.wdtypes
@@ -850,7 +861,10 @@ class FP8FlowMoECompute:
                     mask=mask, want=want)
             # input gradient
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
-        dx = dXp[:T] if self._dense else fused_unpermute_unpad(dXp, plan, None)
+        if self._dense:
+            dx = dXp[:T] if dx_addend is None else dXp[:T] + dx_addend
+        else:
+            dx = fused_unpermute_unpad(dXp, plan, None, addend=dx_addend)
         main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None

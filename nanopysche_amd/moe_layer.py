@@ -1,0 +1,141 @@
+"""The MoE layer on the MI355X path: router, FP8-Flow-MoE expert block and an
+optional shared expert as one differentiable call -- the composition of
+``MoEBase.forward`` (reference ``model/moe.py:1338-1393``: route ->
+expert compute -> combine -> shared expert) at expert-parallel size 1, with
+the router of ``MoERouter.forward`` (``:133-184``).
+
+Beyond calling ``route`` and ``FP8FlowMoECompute`` one after the other, the
+layer runs both under one autograd node, so the input gradient -- which
+autograd would otherwise form as the sum of the router's and the experts'
+shares in a separate pass -- is summed inside the expert block's unpermute,
+and the router's gating gradient is formed as soon as the experts' backward
+has the router-weight gradient.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .flow_moe import FP8FlowMoECompute, FP8FlowMoEConfig, FP8SharedExpertCompute
+from .routing import ExpertLoadTracker, router_backward, router_forward
+
+
+class _BlockCtx:
+    """The part of an autograd ctx FP8FlowMoECompute's forward and backward use,
+    so they can run inside the layer's own autograd Function."""
+
+    def __init__(self, needs_input_grad):
+        self.needs_input_grad = needs_input_grad
+        self.saved_tensors = ()
+
+    def save_for_backward(self, *tensors):
+        self.saved_tensors = tensors
+
+
+class _MoELayerFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, gate_weight, gate_bias, w1, w2, w3, layer, replay, tracker):
+        lead = x.shape[:-1]
+        D = x.shape[-1]
+        x2 = x.reshape(-1, D)
+        if x2.dtype != torch.bfloat16:
+            x2 = x2.to(torch.bfloat16)
+        x2 = x2.contiguous()
+        w, idx, aux, state = router_forward(x2, gate_weight, gate_bias, layer.score_bias, layer.top_k, layer.gating,
+                                            replay, layer.normalize_expert_weights, layer.z_loss_multiplier, tracker)
+        need_x, need_gw, need_gb = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        bctx = _BlockCtx((need_x, need_x or need_gw or need_gb, *ctx.needs_input_grad[3:6], False, False))
+        out = layer.block._forward(bctx, x2, w, w1, w2, w3, idx)
+        ctx.save_for_backward(x2, gate_weight)
+        ctx.state = state
+        ctx.bctx = bctx
+        ctx.layer = layer
+        ctx.lead = lead
+        ctx.x_dtype = x.dtype
+        ctx.has_bias = gate_bias is not None
+        ctx.set_materialize_grads(False)
+        return out.to(x.dtype).reshape(*lead, D), aux
+
+    @staticmethod
+    def backward(ctx, dout, daux):
+        x2, gate_weight = ctx.saved_tensors
+        T, D = x2.shape
+        need_x, need_gw, need_gb = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        if dout is None:
+            dout = torch.zeros(T, D, dtype=torch.bfloat16, device=x2.device)
+        grads = {}
+
+        def on_router_grad(dw):
+            dx_r, dW, db = router_backward(ctx.state, x2, gate_weight, dw, daux, need_x, need_gw,
+                                           need_gb and ctx.has_bias)
+            grads["gw"], grads["gb"] = dW, db
+            return dx_r
+
+        dx, _, dW1, dW2, dW3, _, _ = ctx.layer.block._backward(ctx.bctx, dout.reshape(T, D), on_router_grad)
+        ctx.bctx = None
+        dx = None if not need_x else dx.to(ctx.x_dtype).reshape(*ctx.lead, D)
+        dgw = grads.get("gw")
+        if dgw is not None:
+            dgw = dgw.to(gate_weight.dtype)
+        return dx, dgw, grads.get("gb"), dW1, dW2, dW3, None, None, None
+
+
+class FP8FlowMoELayer:
+    """``MoEBase.forward`` at expert-parallel size 1 on the MI355X path:
+    ``(out, aux_loss) = layer(x)`` with x [..., D].
+
+    Router (``MoERouter``, reference ``model/moe.py:133-184``): fp32 gate
+    ``x.float() @ gate_weight.T + gate_bias (+ score_bias)``, softmax or
+    sigmoid top-k gating (or R3 replay of ``replay_indices``), optional l2
+    weight normalisation, load-balancing loss plus optional z-loss.  Experts:
+    ``FP8FlowMoECompute`` with the given FP8 recipe and threshold.  Shared
+    expert (``shared_hidden_size``): ``FP8SharedExpertCompute``, added out of
+    place as ``:1383-1384`` does.  Differentiable in x, the gate weight and
+    bias, w1, w2, w3 and the shared expert's weights; the object owns no
+    parameters (``set_weights`` borrows them)."""
+
+    def __init__(self, config: FP8FlowMoEConfig, d_model: int, hidden_size: int, num_experts: int, top_k: int,
+                 gating: str = "softmax", fp8_gemm_threshold: int = 0,
+                 normalize_expert_weights: Optional[str] = None, z_loss_multiplier: Optional[float] = None,
+                 shared_hidden_size: Optional[int] = None):
+        self.block = FP8FlowMoECompute(config, d_model, hidden_size, num_experts, fp8_gemm_threshold)
+        self.num_experts = num_experts
+        self.top_k = int(top_k)
+        self.gating = gating
+        self.normalize_expert_weights = normalize_expert_weights
+        self.z_loss_multiplier = 0.0 if z_loss_multiplier is None else float(z_loss_multiplier)
+        self.shared = (FP8SharedExpertCompute(config, d_model, shared_hidden_size, fp8_gemm_threshold)
+                       if shared_hidden_size else None)
+        self.gate_weight = self.gate_bias = self.score_bias = None
+
+    def set_weights(self, gate_weight: torch.Tensor, gate_bias: Optional[torch.Tensor], w1: torch.Tensor,
+                    w2: torch.Tensor, w3: torch.Tensor, score_bias: Optional[torch.Tensor] = None,
+                    shared: Optional[tuple] = None) -> None:
+        """gate_weight [E, D] (+ gate_bias [E]) of the router's nn.Linear, the
+        experts' w1, w2, w3 [E*H, D], the DeepSeek-V3 score bias [E] (optional),
+        and the shared expert's (w1, w2, w3) [H_s, D] each when it has one."""
+        if tuple(gate_weight.shape) != (self.num_experts, self.block.d_model):
+            raise ValueError(f"gate_weight must be [E, D] = [{self.num_experts}, {self.block.d_model}]")
+        self.gate_weight, self.gate_bias, self.score_bias = gate_weight, gate_bias, score_bias
+        self.block.set_weights(w1, w2, w3)
+        if (shared is None) != (self.shared is None):
+            raise ValueError("shared expert weights must be given exactly when the layer has a shared expert")
+        if shared is not None:
+            self.shared.set_weights(*shared)
+
+    def __call__(self, x: torch.Tensor, replay_indices: Optional[torch.Tensor] = None,
+                 load_tracker: Optional[ExpertLoadTracker] = None):
+        if self.gate_weight is None:
+            raise RuntimeError("set_weights() must be called before the layer runs")
+        _lib.require_device(x, "x")
+        w1, w2, w3 = self.block._w
+        self.block._record = torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (x, self.gate_weight, self.gate_bias, w1, w2, w3))
+        out, aux = _MoELayerFunction.apply(x, self.gate_weight, self.gate_bias, w1, w2, w3, self, replay_indices,
+                                           load_tracker)
+        if self.shared is not None:
+            out = out + self.shared(x)
+        return out, aux

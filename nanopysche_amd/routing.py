@@ -222,6 +222,68 @@ class ExpertLoadTracker:
                   self.num_experts, float(gamma), _lib.ptr(score_bias), _lib.stream_of(score_bias))
 
 
+@dataclass
+class RouterState:
+    """What the router's backward needs from its forward."""
+
+    logits: torch.Tensor     # [T, E] fp32, score bias included
+    indices: torch.Tensor    # [T, K]
+    counts: torch.Tensor     # [E] int32
+    gating: int
+    flags: int
+    replay: bool
+    z_mult: float
+
+
+def router_forward(x2, gate_weight, gate_bias, score_bias, top_k, gating, replay=None, normalize=None,
+                   z_mult=0.0, tracker=None):
+    """Gate, gating, counts and aux loss of MoERouter.forward (reference
+    model/moe.py:133-184) on x2 [T, D]: (weights [T, K], indices [T, K], aux, state)."""
+    T = x2.shape[0]
+    logits = router_logits(x2, gate_weight, gate_bias, score_bias)
+    E = logits.shape[1]
+    w, idx, part, zpart = topk_gating(logits, top_k, gating, True, replay_indices=replay, normalize=normalize,
+                                      return_z_partial=True)
+    counts = expert_counts(idx, E, tracker)
+    aux = load_balancing_loss(part, counts, T, zpart if z_mult else None, z_mult)
+    state = RouterState(logits, idx, counts, _gating_code(gating), _norm_flags(normalize), replay is not None,
+                        float(z_mult))
+    return w, idx, aux, state
+
+
+def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=True, need_w=True, need_b=True):
+    """Gradients of the router (dx [T, D] in x2's dtype, dW [E, D] fp32, db [E] fp32;
+    None where not needed) from those of its weights [T, K] and aux loss."""
+    logits, idx = state.logits, state.indices
+    T, D = x2.shape
+    E = logits.shape[1]
+    K = idx.shape[1]
+    dev = x2.device
+    st = _lib.stream_of(x2)
+    dwts = None if dweights is None else dweights.reshape(T, K).float().contiguous()
+    da = None if daux is None else daux.reshape(1).float().contiguous()
+    dlogits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    if dwts is None and da is None:
+        dlogits.zero_()
+    else:
+        _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, state.gating, state.flags,
+                  int(state.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), _lib.ptr(dwts), _lib.ptr(da),
+                  _lib.ptr(state.counts), state.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
+    wf = gate_weight.detach().float().contiguous()
+    dx = torch.empty_like(x2) if need_x else None
+    dW = torch.empty(E, D, dtype=torch.float32, device=dev) if need_w else None
+    db = torch.empty(E, dtype=torch.float32, device=dev) if need_b else None
+    ws = None
+    if dW is not None:
+        ws = torch.empty(int(_lib.load().fm_router_workspace_bytes(T, D, E)), dtype=torch.uint8, device=dev)
+    if dx is not None or dW is not None or db is not None:
+        _lib.call("fm_router_backward", _lib.ptr(dlogits), dlogits.stride(0), _lib.ptr(x2), _x_dtype(x2),
+                  x2.stride(0), T, D, _lib.ptr(wf), wf.stride(0), E, _lib.ptr(dx),
+                  0 if dx is None else dx.stride(0), _lib.ptr(dW), 0 if dW is None else dW.stride(0),
+                  _lib.ptr(db), _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
+    return dx, dW, db
+
+
 class _RouterFunction(torch.autograd.Function):
     """Gate + gating (top-k or replay, optional l2) + load-balancing loss (+ z-loss),
     forward and backward on the GPU."""
@@ -230,55 +292,24 @@ class _RouterFunction(torch.autograd.Function):
     def forward(ctx, x, gate_weight, gate_bias, score_bias, top_k, gating, replay, normalize, z_mult, tracker):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1]).contiguous()
-        T = x2.shape[0]
-        logits = router_logits(x2, gate_weight, gate_bias, score_bias)
-        E = logits.shape[1]
-        w, idx, part, zpart = topk_gating(logits, top_k, gating, True, replay_indices=replay, normalize=normalize,
-                                          return_z_partial=True)
-        counts = expert_counts(idx, E, tracker)
-        aux = load_balancing_loss(part, counts, T, zpart if z_mult else None, z_mult)
-        ctx.save_for_backward(x2, gate_weight, logits, idx, counts)
-        ctx.gating = _gating_code(gating)
-        ctx.flags = _norm_flags(normalize)
-        ctx.replay = replay is not None
-        ctx.z_mult = float(z_mult)
+        w, idx, aux, state = router_forward(x2, gate_weight, gate_bias, score_bias, top_k, gating, replay,
+                                            normalize, z_mult, tracker)
+        ctx.save_for_backward(x2, gate_weight)
+        ctx.state = state
         ctx.has_bias = gate_bias is not None
         ctx.lead = lead
         ctx.mark_non_differentiable(idx)
+        ctx.set_materialize_grads(False)   # no zero gradient for the indices
         return w.reshape(*lead, top_k), idx.reshape(*lead, top_k), aux
 
     @staticmethod
     def backward(ctx, dweights, _dindices, daux):
-        x2, gate_weight, logits, idx, counts = ctx.saved_tensors
-        T, D = x2.shape
-        E = logits.shape[1]
-        K = idx.shape[1]
-        dev = x2.device
-        st = _lib.stream_of(x2)
-        dwts = None if dweights is None else dweights.reshape(T, K).float().contiguous()
-        da = None if daux is None else daux.reshape(1).float().contiguous()
-        dlogits = torch.empty(T, E, dtype=torch.float32, device=dev)
-        if dwts is None and da is None:
-            dlogits.zero_()
-        else:
-            _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, ctx.gating, ctx.flags,
-                      int(ctx.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), _lib.ptr(dwts), _lib.ptr(da),
-                      _lib.ptr(counts), ctx.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
+        x2, gate_weight = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-        wf = gate_weight.detach().float().contiguous()
-        dx = torch.empty_like(x2) if need_x else None
-        dW = torch.empty(E, D, dtype=torch.float32, device=dev) if need_w else None
-        db = torch.empty(E, dtype=torch.float32, device=dev) if (need_b and ctx.has_bias) else None
-        ws = None
-        if dW is not None:
-            ws = torch.empty(int(_lib.load().fm_router_workspace_bytes(T, D, E)), dtype=torch.uint8, device=dev)
-        if dx is not None or dW is not None or db is not None:
-            _lib.call("fm_router_backward", _lib.ptr(dlogits), dlogits.stride(0), _lib.ptr(x2), _x_dtype(x2),
-                      x2.stride(0), T, D, _lib.ptr(wf), wf.stride(0), E, _lib.ptr(dx),
-                      0 if dx is None else dx.stride(0), _lib.ptr(dW), 0 if dW is None else dW.stride(0),
-                      _lib.ptr(db), _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
+        dx, dW, db = router_backward(ctx.state, x2, gate_weight, dweights, daux, need_x, need_w,
+                                     need_b and ctx.has_bias)
         if dx is not None:
-            dx = dx.reshape(*ctx.lead, D)
+            dx = dx.reshape(*ctx.lead, x2.shape[1])
         if dW is not None:
             dW = dW.to(gate_weight.dtype)
         return dx, dW, db, None, None, None, None, None, None, None
