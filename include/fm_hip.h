@@ -288,6 +288,18 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
                  int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
                  const void* addend, int64_t ld_add, void* stream);
 
+/* fm_unpermute plus the router's share of a MoE layer's input gradient,
+ * dx[t] += sum_e dlogits[t][e] * gate_w[e] (the backward of the gate
+ * nn.Linear of reference model/moe.py:107, :151 for an input that also feeds
+ * the experts), in the same pass: out[t] = addend[t] + sum_k weights[t*K+k]
+ * y[row_of[t*K+k]] + sum_e dlogits[t*ld_dl+e] gate_w[e*ld_w + :], fp32 sums in
+ * that order (the router's terms as fused multiply-adds), one rounding.
+ * E <= 8; gate_w bf16 or fp32 [E, D]. */
+int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
+                        int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
+                        const void* addend, int64_t ld_add, const float* dlogits, int64_t ld_dl,
+                        const void* gate_w, int gate_dtype, int64_t ld_w, int E, void* stream);
+
 /* Gradient of the combine with respect to the router weights (autograd of
  * model/moe.py:1594 in the reference): dw[a] = <dout[a/K], y[row_of[a]]>. */
 int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_t ld_y,

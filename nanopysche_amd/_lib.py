@@ -104,6 +104,8 @@ SIGNATURES = {
     "fm_permute": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _vp, _i64, _vp, _i64,
                           _vp, _i64, _vp, _i64, _vp, _vp]),
     "fm_unpermute": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _vp]),
+    "fm_unpermute_router": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i64,
+                                   _vp, _i32, _i64, _i32, _vp]),
     "fm_router_weight_grad": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _vp, _vp]),
     "fm_swiglu_quantize": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp,
                                   _i64, _vp, _i64, _vp, _vp]),

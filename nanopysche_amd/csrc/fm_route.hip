@@ -15,6 +15,7 @@
 //                          rounding
 //   fm_router_weight_grad -- dw[t,k] = <dout[t], y[row(t,k)]>
 #include <mutex>
+#include <type_traits>
 
 #include "fm_tile.h"
 #include "../../include/fm_hip.h"
@@ -558,6 +559,141 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64
   }
 }
 
+// Unpermute with the router's share of the input gradient folded in (E <= 8):
+//   out[t] = addend[t] + sum_k w[t,k] y[row_of[t,k]] + sum_e dl[t,e] W[e]
+// i.e. the experts' and the router's input gradients of a MoE layer in one
+// pass (no [T, D] router gradient written and read back).  Thread i of a
+// workgroup owns columns 8 i .. 8 i + 8 of a 2048-column span (blockIdx.x)
+// and keeps W's 8 x 8 values of them in registers; the workgroup walks the
+// tokens [blockIdx.y * tpb, +tpb), four at a time with every load of the four
+// issued before any use (KC = K when K is 1, 2 or 4, else 0 = a loop over
+// K).  fp32 sums in the order addend, slots in order (separately rounded
+// products and sums), then the router's terms; one rounding to the output
+// dtype.
+__device__ __forceinline__ void add_bf16x8(float (&acc)[8], uint4 pk, float s) {
+#pragma clang fp contract(off)
+  const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[2 * j] = acc[2 * j] + s * u2f(q[j] << 16);
+    acc[2 * j + 1] = acc[2 * j + 1] + s * u2f(q[j] & 0xffff0000u);
+  }
+}
+
+template <typename WT, int KC>
+__global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* y, int64_t ld_y,
+                                                               const int32_t* row_of, const float* w,
+                                                               int64_t T, int K, int64_t D,
+                                                               void* out, int out_f32, int64_t ld_out,
+                                                               const uint16_t* addend, int64_t ld_add,
+                                                               const float* dl, int64_t ld_dl,
+                                                               const WT* W, int64_t ld_w, int E, int64_t tpb) {
+  const int64_t c = int64_t(blockIdx.x) * 2048 + threadIdx.x * 8;
+  if (c >= D) return;
+  float wr[8][8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (e < E) {
+      if constexpr (sizeof(WT) == 4) {
+        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + e * ld_w + c);
+        const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + e * ld_w + c + 4);
+        wr[e][0] = a.x; wr[e][1] = a.y; wr[e][2] = a.z; wr[e][3] = a.w;
+        wr[e][4] = b.x; wr[e][5] = b.y; wr[e][6] = b.z; wr[e][7] = b.w;
+      } else {
+        const uint4 pk = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(W) + e * ld_w + c);
+        const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wr[e][2 * j] = u2f(q[j] << 16);
+          wr[e][2 * j + 1] = u2f(q[j] & 0xffff0000u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wr[e][j] = 0.f;
+    }
+  }
+  const int64_t t0 = int64_t(blockIdx.y) * tpb;
+  const int64_t t1 = t0 + tpb < T ? t0 + tpb : T;
+  for (int64_t tb = t0; tb < t1; tb += 4) {
+    constexpr int KS = KC > 0 ? KC : 1;
+    float acc[4][8];
+    int32_t r[4][KS];
+    float sw[4][KS];
+    uint4 yv[4][KS];
+    float d[4][8];
+    // every load of the four tokens first (a token past t1 re-reads t1 - 1)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t t = tb + u < t1 ? tb + u : t1 - 1;
+      if constexpr (KC > 0) {
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          r[u][k] = row_of[t * KC + k];
+          sw[u][k] = w ? w[t * KC + k] : 1.f;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[u][e] = e < E ? dl[t * ld_dl + e] : 0.f;
+      if (addend) {
+        const uint4 pk = *reinterpret_cast<const uint4*>(addend + t * ld_add + c);
+        const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[u][2 * j] = u2f(q[j] << 16);
+          acc[u][2 * j + 1] = u2f(q[j] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[u][j] = 0.f;
+      }
+    }
+    if constexpr (KC > 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+          yv[u][k] = *reinterpret_cast<const uint4*>(y + int64_t(r[u][k] >= 0 ? r[u][k] : 0) * ld_y + c);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+          if (r[u][k] >= 0) add_bf16x8(acc[u], yv[u][k], sw[u][k]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t t = tb + u < t1 ? tb + u : t1 - 1;
+        for (int k = 0; k < K; ++k) {
+          const int32_t rr = row_of[t * K + k];
+          if (rr < 0) continue;
+          add_bf16x8(acc[u], *reinterpret_cast<const uint4*>(y + int64_t(rr) * ld_y + c), w ? w[t * K + k] : 1.f);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (tb + u >= t1) break;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[u][j] = fmaf(d[u][e], wr[e][j], acc[u][j]);
+      const int64_t t = tb + u;
+      if (out_f32) {
+        float* o = static_cast<float*>(out) + t * ld_out + c;
+        *reinterpret_cast<float4*>(o) = make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+        *reinterpret_cast<float4*>(o + 4) = make_float4(acc[u][4], acc[u][5], acc[u][6], acc[u][7]);
+      } else {
+        uint4 pk;
+        pk.x = hw_bf16x2(acc[u][0], acc[u][1]);
+        pk.y = hw_bf16x2(acc[u][2], acc[u][3]);
+        pk.z = hw_bf16x2(acc[u][4], acc[u][5]);
+        pk.w = hw_bf16x2(acc[u][6], acc[u][7]);
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + t * ld_out + c) = pk;
+      }
+    }
+  }
+}
+
 // one wave per assignment: dw[a] = sum_d dout[t][d] * y[row_of[a]][d]
 __global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* dout, int64_t ld_do,
                                                           const uint16_t* y, int64_t ld_y,
@@ -774,6 +910,41 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
                      static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
                      out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add);
   return check_launch("fm_unpermute");
+}
+
+int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
+                        int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
+                        const void* addend, int64_t ld_add, const float* dlogits, int64_t ld_dl,
+                        const void* gate_w, int gate_dtype, int64_t ld_w, int E, void* stream) {
+  FM_REQUIRE((y && row_of && out && dlogits && gate_w) || T == 0, "fm_unpermute_router: null pointer");
+  FM_REQUIRE(E >= 1 && E <= 8, "fm_unpermute_router: E must be in [1, 8] (got %d)", E);
+  FM_REQUIRE(D % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0 && ld_w % 8 == 0 &&
+                 (addend == nullptr || ld_add % 8 == 0) && ld_dl >= E,
+             "fm_unpermute_router: D and pitches must be multiples of 8");
+  FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_unpermute_router: bad out dtype");
+  FM_REQUIRE(gate_dtype == FM_DTYPE_BF16 || gate_dtype == FM_DTYPE_F32, "fm_unpermute_router: bad gate dtype");
+  if (T == 0) return 0;
+  const int64_t nx = (D + 2047) / 2048;
+  int64_t tpb = (T * nx + 1023) / 1024;   // about 1024 workgroups
+  if (tpb < 1) tpb = 1;
+  const dim3 grid(unsigned(nx), unsigned((T + tpb - 1) / tpb));
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  auto go = [&](auto wt, auto kc) {
+    using WT = decltype(wt);
+    hipLaunchKernelGGL((unpermute_router_kernel<WT, decltype(kc)::value>), grid, dim3(256), 0, sm,
+                       static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
+                       out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add, dlogits,
+                       ld_dl, static_cast<const WT*>(gate_w), ld_w, E, tpb);
+  };
+  auto go_k = [&](auto wt) {
+    if (K == 1) go(wt, std::integral_constant<int, 1>{});
+    else if (K == 2) go(wt, std::integral_constant<int, 2>{});
+    else if (K == 4) go(wt, std::integral_constant<int, 4>{});
+    else go(wt, std::integral_constant<int, 0>{});
+  };
+  if (gate_dtype == FM_DTYPE_F32) go_k(float{});
+  else go_k(uint16_t{});
+  return check_launch("fm_unpermute_router");
 }
 
 int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_t ld_y,

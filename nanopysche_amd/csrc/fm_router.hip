@@ -709,11 +709,11 @@ int64_t fm_router_workspace_bytes(int64_t T, int64_t D, int E) {
 int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x_dtype, int64_t ld_x, int64_t T,
                        int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
                        int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream) {
-  FM_REQUIRE(dlogits && x && w, "fm_router_backward: null pointer");
+  FM_REQUIRE(dlogits && x && (w || dx == nullptr), "fm_router_backward: null pointer");
   FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_router_backward: bad x dtype %d", x_dtype);
   FM_REQUIRE(E >= 1 && E <= 256, "fm_router_backward: E must be in [1, 256] (got %d)", E);
   FM_REQUIRE(D > 0 && D % 8 == 0, "fm_router_backward: D must be a positive multiple of 8");
-  FM_REQUIRE(ld_dl >= E && ld_x >= D && ld_x % 8 == 0 && ld_w >= D && ld_w % 4 == 0,
+  FM_REQUIRE(ld_dl >= E && ld_x >= D && ld_x % 8 == 0 && (w == nullptr || (ld_w >= D && ld_w % 4 == 0)),
              "fm_router_backward: bad pitches");
   FM_REQUIRE(dx == nullptr || (ld_dx >= D && ld_dx % 8 == 0), "fm_router_backward: bad dx pitch");
   FM_REQUIRE(dw == nullptr || (ld_dw >= D), "fm_router_backward: bad dw pitch");

@@ -311,10 +311,14 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
 def fused_unpermute_unpad(y: torch.Tensor, plan: RoutingPlan,
                           weights: Optional[torch.Tensor] = None,
                           out_dtype: torch.dtype = torch.bfloat16,
-                          addend: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          addend: Optional[torch.Tensor] = None,
+                          router_terms: Optional[tuple] = None) -> torch.Tensor:
     """out[t] = addend[t] + sum_k weights[t, k] * y[row(t, k)] (weights None ->
     1, addend None -> 0), summed in fp32 in slot order and rounded once.  y
-    and addend are bf16 ([rows_max, D] and [T, D])."""
+    and addend are bf16 ([rows_max, D] and [T, D]).  ``router_terms`` =
+    (dlogits [T, E] fp32, gate_weight [E, D] bf16 / fp32), E <= 8, adds
+    sum_e dlogits[t, e] gate_weight[e] in the same pass (a MoE layer's input
+    gradient: the router's share)."""
     _lib.require_device(y, "y")
     if y.dtype != torch.bfloat16:
         raise TypeError("y must be bfloat16")
@@ -326,6 +330,15 @@ def fused_unpermute_unpad(y: torch.Tensor, plan: RoutingPlan,
     out = torch.empty(T, D, dtype=out_dtype, device=y.device)
     w = None if weights is None else weights.reshape(-1).to(torch.float32).contiguous()
     od = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    if router_terms is not None:
+        dl, gw = router_terms
+        gw = gw.detach()
+        if gw.dtype not in (torch.float32, torch.bfloat16) or gw.stride(1) != 1:
+            gw = gw.float().contiguous()
+        _lib.call("fm_unpermute_router", _lib.ptr(y), y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(w), T, K, D,
+                  _lib.ptr(out), od, out.stride(0), _lib.ptr(addend), 0 if addend is None else addend.stride(0),
+                  _lib.ptr(dl), dl.stride(0), _lib.ptr(gw), _dt(gw), gw.stride(0), gw.shape[0], _lib.stream_of(y))
+        return out
     _lib.call("fm_unpermute", _lib.ptr(y), y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(w), T, K, D,
               _lib.ptr(out), od, out.stride(0), _lib.ptr(addend), 0 if addend is None else addend.stride(0),
               _lib.stream_of(y))
@@ -801,10 +814,12 @@ class FP8FlowMoECompute:
 
     # ----------------------------------------------------------------- backward ----
     def _backward(self, ctx, grad_out, on_router_grad=None):
-        """Gradients of the expert block.  ``on_router_grad(dw)`` (a MoE layer
-        whose router feeds this block) is called with the router-weight
-        gradient as soon as it exists and returns a bf16 [T, D] addend for the
-        input gradient (the router's share of it), summed in the unpermute."""
+        """Gradients of the expert block.  ``on_router_grad(dw, can_fold)`` (a
+        MoE layer whose router feeds this block) is called with the
+        router-weight gradient as soon as it exists and returns the router's
+        share of the input gradient, summed in the unpermute: {"addend": bf16
+        [T, D]}, or with ``can_fold`` {"dlogits": [T, E], "gate_w": [E, D]}
+        (E <= 8) for the unpermute to form it itself."""
         wts, GU, Y = ctx.saved_tensors
         plan = ctx.plan
         fp8_kind, use_bf16 = ctx.kinds
@@ -821,7 +836,10 @@ class FP8FlowMoECompute:
             dw = torch.empty(T * K, dtype=torch.float32, device=dev)
             _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
                       _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
-        dx_addend = None if on_router_grad is None else on_router_grad(None if dw is None else dw.reshape(T, K))
+        # the router's share of the input gradient: a [T, D] addend, or its
+        # (dlogits, gate weight) terms folded into the unpermute
+        rshare = {} if on_router_grad is None else on_router_grad(None if dw is None else dw.reshape(T, K),
+                                                                  not self._dense)
         dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
         dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         w1dt, w2dt, w3dt = ctx.wdtypes
@@ -861,10 +879,12 @@ class FP8FlowMoECompute:
                     mask=mask, want=want)
             # input gradient
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
+        dx_addend = rshare.get("addend")
         if self._dense:
             dx = dXp[:T] if dx_addend is None else dXp[:T] + dx_addend
         else:
-            dx = fused_unpermute_unpad(dXp, plan, None, addend=dx_addend)
+            terms = (rshare["dlogits"], rshare["gate_w"]) if "dlogits" in rshare else None
+            dx = fused_unpermute_unpad(dXp, plan, None, addend=dx_addend, router_terms=terms)
         main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None

@@ -68,11 +68,16 @@ class _MoELayerFunction(torch.autograd.Function):
             dout = torch.zeros(T, D, dtype=torch.bfloat16, device=x2.device)
         grads = {}
 
-        def on_router_grad(dw):
-            dx_r, dW, db = router_backward(ctx.state, x2, gate_weight, dw, daux, need_x, need_gw,
-                                           need_gb and ctx.has_bias)
+        def on_router_grad(dw, can_fold):
+            # E <= 8: the unpermute forms the router's share of dx from dlogits and
+            # the gate weight itself; otherwise the router's own kernel writes it
+            fold = need_x and can_fold and ctx.state.logits.shape[1] <= 8
+            dx_r, dW, db, dlogits = router_backward(ctx.state, x2, gate_weight, dw, daux, need_x and not fold,
+                                                    need_gw, need_gb and ctx.has_bias)
             grads["gw"], grads["gb"] = dW, db
-            return dx_r
+            if fold:
+                return {"dlogits": dlogits, "gate_w": gate_weight}
+            return {} if dx_r is None else {"addend": dx_r}
 
         dx, _, dW1, dW2, dW3, _, _ = ctx.layer.block._backward(ctx.bctx, dout.reshape(T, D), on_router_grad)
         ctx.bctx = None

@@ -253,7 +253,8 @@ def router_forward(x2, gate_weight, gate_bias, score_bias, top_k, gating, replay
 
 def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=True, need_w=True, need_b=True):
     """Gradients of the router (dx [T, D] in x2's dtype, dW [E, D] fp32, db [E] fp32;
-    None where not needed) from those of its weights [T, K] and aux loss."""
+    None where not needed) from those of its weights [T, K] and aux loss, and
+    the logits' gradient dlogits [T, E] fp32 they come from."""
     logits, idx = state.logits, state.indices
     T, D = x2.shape
     E = logits.shape[1]
@@ -269,7 +270,7 @@ def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=
         _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, state.gating, state.flags,
                   int(state.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), _lib.ptr(dwts), _lib.ptr(da),
                   _lib.ptr(state.counts), state.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
-    wf = gate_weight.detach().float().contiguous()
+    wf = gate_weight.detach().float().contiguous() if need_x else None
     dx = torch.empty_like(x2) if need_x else None
     dW = torch.empty(E, D, dtype=torch.float32, device=dev) if need_w else None
     db = torch.empty(E, dtype=torch.float32, device=dev) if need_b else None
@@ -278,10 +279,10 @@ def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=
         ws = torch.empty(int(_lib.load().fm_router_workspace_bytes(T, D, E)), dtype=torch.uint8, device=dev)
     if dx is not None or dW is not None or db is not None:
         _lib.call("fm_router_backward", _lib.ptr(dlogits), dlogits.stride(0), _lib.ptr(x2), _x_dtype(x2),
-                  x2.stride(0), T, D, _lib.ptr(wf), wf.stride(0), E, _lib.ptr(dx),
+                  x2.stride(0), T, D, _lib.ptr(wf), 0 if wf is None else wf.stride(0), E, _lib.ptr(dx),
                   0 if dx is None else dx.stride(0), _lib.ptr(dW), 0 if dW is None else dW.stride(0),
                   _lib.ptr(db), _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
-    return dx, dW, db
+    return dx, dW, db, dlogits
 
 
 class _RouterFunction(torch.autograd.Function):
@@ -306,8 +307,8 @@ class _RouterFunction(torch.autograd.Function):
     def backward(ctx, dweights, _dindices, daux):
         x2, gate_weight = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-        dx, dW, db = router_backward(ctx.state, x2, gate_weight, dweights, daux, need_x, need_w,
-                                     need_b and ctx.has_bias)
+        dx, dW, db, _ = router_backward(ctx.state, x2, gate_weight, dweights, daux, need_x, need_w,
+                                        need_b and ctx.has_bias)
         if dx is not None:
             dx = dx.reshape(*ctx.lead, x2.shape[1])
         if dW is not None:
