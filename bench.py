@@ -254,7 +254,29 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
     ew._build(w1, w2, w3, E)
     wbytes = nb(w1, w2, w3) + sum(nb(o.data, o.scale) for o in (ew.w13, ew.w13t, ew.w2, ew.w2t))
 
+    # RMSNorm ahead of the MoE on the residual stream (x stands in for it)
+    nw = torch.ones(D, dtype=torch.float32, device=dev)
+    ny = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    nq = torch.empty(T, D, dtype=torch.uint8, device=dev)
+    ns = torch.empty(T, D // 128, dtype=torch.float32, device=dev)
+    nr = torch.empty(T, dtype=torch.float32, device=dev)
+    ndx = torch.empty_like(ny)
+    ndw = torch.empty(D, dtype=torch.float32, device=dev)
+    nws = torch.empty(int(_lib.load().fm_rmsnorm_backward_workspace_bytes(T, D)) // 4, dtype=torch.float32,
+                      device=dev)
+    _lib.call("fm_rmsnorm_quantize", _lib.ptr(x), _lib.DTYPE_BF16, x.stride(0), T, D, _lib.ptr(nw), _lib.DTYPE_F32,
+              1e-6, None, 0, -1, None, 0, None, 0, _lib.ptr(nr), st)
+
     ops = [
+        ("RMSNorm + quantise (residual stream -> bf16 y + e4m3 row blocks, pow2, + rsqrt)",
+         lambda: _lib.call("fm_rmsnorm_quantize", _lib.ptr(x), _lib.DTYPE_BF16, x.stride(0), T, D, _lib.ptr(nw),
+                           _lib.DTYPE_F32, 1e-6, _lib.ptr(ny), D, P2, _lib.ptr(nq), D, _lib.ptr(ns), D // 128,
+                           _lib.ptr(nr), st), nb(x, nw, ny, nq, ns, nr)),
+        ("RMSNorm backward (dx + dw)",
+         lambda: _lib.call("fm_rmsnorm_backward", _lib.ptr(go), go.stride(0), _lib.ptr(x), _lib.DTYPE_BF16,
+                           x.stride(0), T, D, _lib.ptr(nw), _lib.DTYPE_F32, _lib.ptr(nr), _lib.ptr(ndx), D,
+                           _lib.ptr(ndw), _lib.DTYPE_F32, _lib.ptr(nws), nws.numel() * 4, st),
+         nb(go, x, nw, nr, ndx, ndw)),
         ("permute + quantise (x rows, row + transposed, pow2)",
          lambda: _lib.call("fm_permute", _lib.ptr(x), T, D, x.stride(0), _lib.ptr(plan.assign_of_row), R, K, None,
                            *_tile_args(P2, *pq), _lib.ptr(plan.tile_expert), st), nb(x) + nbq(*pq)),

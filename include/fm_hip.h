@@ -230,6 +230,29 @@ int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x
                        int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
                        int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Replaces RMSNorm.forward (reference model/norm.py:32-49, full_precision) as
+ * MoEHybridTransformerBlock applies it before the MoE (model/transformer.py:
+ * 261-263), fused with the activation quantisation: r = 1 / sqrt(mean(x^2) +
+ * eps) and y = (x r) w per row in fp32.  x bf16 or fp32 [T, D] (pitch ld_x),
+ * w bf16 or fp32 [D]; D = 512 n, n in 1..8, 10, 12, 14, 16.  Outputs, each
+ * optional: y as bf16 [T, D] (pitch ld_y); the e4m3 row blocks of that bf16 y
+ * (kind FM_QUANT_BLOCK / _POW2: fp32 scale per 128 columns, s [T, ld_s];
+ * FM_QUANT_MX: e8m0 per 32 columns; kind -1: none); rstd [T] (r, for the
+ * backward).  One read of x. */
+int fm_rmsnorm_quantize(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
+                        float eps, void* y, int64_t ld_y, int kind, void* q, int64_t ld_q, void* s, int64_t ld_s,
+                        float* rstd, void* stream);
+
+/* Backward of RMSNorm (reference model/norm.py:32-49 under autograd): with
+ * g = dy w, dx = r g - (r^3 / D) (sum_j g_j x_j) x in x's dtype, and
+ * dw = sum_t dy x r (fp32 sums, written as dw_dtype; null to skip), summed in
+ * a fixed order through a workspace of fm_rmsnorm_backward_workspace_bytes(T,
+ * D) bytes.  dy in x's dtype; rstd as fm_rmsnorm_quantize wrote it. */
+int64_t fm_rmsnorm_backward_workspace_bytes(int64_t T, int64_t D);
+int fm_rmsnorm_backward(const void* dy, int64_t ld_dy, const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D,
+                        const void* w, int w_dtype, const float* rstd, void* dx, int64_t ld_dx, void* dw,
+                        int dw_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Sizes for fm_route_sort: padded-buffer row bound 128 * max(1, floor((A +
  * 127 E) / 128)) (every group padded to 128 rows fits; one group: exactly
  * the padded rows), and workspace bytes. */

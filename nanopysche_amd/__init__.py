@@ -24,6 +24,7 @@ from .flow_moe import (
     scaling_aware_transpose,
 )
 from .moe_layer import FP8FlowMoELayer
+from .norm import NormOutput, RMSNorm, rmsnorm, rmsnorm_backward, rmsnorm_quantize
 from .routing import (ExpertLoadTracker, RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens,
                       router_logits, topk_gating)
 
@@ -55,4 +56,9 @@ __all__ = [
     "expert_counts",
     "ExpertLoadTracker",
     "FP8FlowMoELayer",
+    "RMSNorm",
+    "rmsnorm",
+    "rmsnorm_quantize",
+    "rmsnorm_backward",
+    "NormOutput",
 ]

@@ -94,6 +94,11 @@ SIGNATURES = {
     "fm_router_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "fm_router_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp,
                                   _i64, _vp, _vp, _i64, _vp]),
+    "fm_rmsnorm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, C.c_float, _vp, _i64, _i32, _vp, _i64,
+                                   _vp, _i64, _vp, _vp]),
+    "fm_rmsnorm_backward_workspace_bytes": (_i64, [_i64, _i64]),
+    "fm_rmsnorm_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _i32,
+                                   _vp, _i64, _vp]),
     "fm_route_rows_max": (_i64, [_i64, _i32]),
     "fm_route_workspace_bytes": (_i64, [_i64, _i32]),
     "fm_route_sort": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,

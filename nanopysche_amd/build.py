@@ -19,7 +19,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libfm_hip.so"
-SOURCES = ["fm_api.cpp", "fm_quant.hip", "fm_route.hip", "fm_swiglu.hip", "fm_gemm.hip", "fm_router.hip"]
+SOURCES = ["fm_api.cpp", "fm_quant.hip", "fm_route.hip", "fm_swiglu.hip", "fm_gemm.hip", "fm_router.hip",
+           "fm_norm.hip"]
 ARCH = "gfx950"
 
 

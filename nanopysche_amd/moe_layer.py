@@ -20,6 +20,7 @@ import torch
 
 from . import _lib
 from .flow_moe import FP8FlowMoECompute, FP8FlowMoEConfig, FP8SharedExpertCompute
+from .norm import DEFAULT_EPS, rmsnorm
 from .routing import ExpertLoadTracker, router_backward, router_forward
 
 
@@ -98,14 +99,18 @@ class FP8FlowMoELayer:
     weight normalisation, load-balancing loss plus optional z-loss.  Experts:
     ``FP8FlowMoECompute`` with the given FP8 recipe and threshold.  Shared
     expert (``shared_hidden_size``): ``FP8SharedExpertCompute``, added out of
-    place as ``:1383-1384`` does.  Differentiable in x, the gate weight and
-    bias, w1, w2, w3 and the shared expert's weights; the object owns no
+    place as ``:1383-1384`` does.  Pre-norm (``pre_norm=True``): the layer
+    takes the residual stream h and applies RMSNorm with ``norm_weight``
+    first, as ``MoEHybridTransformerBlock`` feeds ``self.moe_norm(h)`` to the
+    MoE (``model/transformer.py:261-263``); the residual add stays with the
+    caller.  Differentiable in x, the gate weight and bias, w1, w2, w3, the
+    norm weight and the shared expert's weights; the object owns no
     parameters (``set_weights`` borrows them)."""
 
     def __init__(self, config: FP8FlowMoEConfig, d_model: int, hidden_size: int, num_experts: int, top_k: int,
                  gating: str = "softmax", fp8_gemm_threshold: int = 0,
                  normalize_expert_weights: Optional[str] = None, z_loss_multiplier: Optional[float] = None,
-                 shared_hidden_size: Optional[int] = None):
+                 shared_hidden_size: Optional[int] = None, pre_norm: bool = False, norm_eps: float = DEFAULT_EPS):
         self.block = FP8FlowMoECompute(config, d_model, hidden_size, num_experts, fp8_gemm_threshold)
         self.num_experts = num_experts
         self.top_k = int(top_k)
@@ -115,13 +120,17 @@ class FP8FlowMoELayer:
         self.shared = (FP8SharedExpertCompute(config, d_model, shared_hidden_size, fp8_gemm_threshold)
                        if shared_hidden_size else None)
         self.gate_weight = self.gate_bias = self.score_bias = None
+        self.pre_norm = bool(pre_norm)
+        self.norm_eps = float(norm_eps)
+        self.norm_weight = None
 
     def set_weights(self, gate_weight: torch.Tensor, gate_bias: Optional[torch.Tensor], w1: torch.Tensor,
                     w2: torch.Tensor, w3: torch.Tensor, score_bias: Optional[torch.Tensor] = None,
-                    shared: Optional[tuple] = None) -> None:
+                    shared: Optional[tuple] = None, norm_weight: Optional[torch.Tensor] = None) -> None:
         """gate_weight [E, D] (+ gate_bias [E]) of the router's nn.Linear, the
         experts' w1, w2, w3 [E*H, D], the DeepSeek-V3 score bias [E] (optional),
-        and the shared expert's (w1, w2, w3) [H_s, D] each when it has one."""
+        the shared expert's (w1, w2, w3) [H_s, D] each when it has one, and the
+        RMSNorm weight [D] exactly when the layer is pre-norm."""
         if tuple(gate_weight.shape) != (self.num_experts, self.block.d_model):
             raise ValueError(f"gate_weight must be [E, D] = [{self.num_experts}, {self.block.d_model}]")
         self.gate_weight, self.gate_bias, self.score_bias = gate_weight, gate_bias, score_bias
@@ -130,12 +139,19 @@ class FP8FlowMoELayer:
             raise ValueError("shared expert weights must be given exactly when the layer has a shared expert")
         if shared is not None:
             self.shared.set_weights(*shared)
+        if (norm_weight is None) == self.pre_norm:
+            raise ValueError("norm_weight must be given exactly when the layer is pre-norm")
+        if norm_weight is not None and tuple(norm_weight.shape) != (self.block.d_model,):
+            raise ValueError(f"norm_weight must be [D] = [{self.block.d_model}]")
+        self.norm_weight = norm_weight
 
     def __call__(self, x: torch.Tensor, replay_indices: Optional[torch.Tensor] = None,
                  load_tracker: Optional[ExpertLoadTracker] = None):
         if self.gate_weight is None:
             raise RuntimeError("set_weights() must be called before the layer runs")
         _lib.require_device(x, "x")
+        if self.pre_norm:
+            x = rmsnorm(x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16), self.norm_weight, self.norm_eps)
         w1, w2, w3 = self.block._w
         self.block._record = torch.is_grad_enabled() and any(
             t is not None and t.requires_grad for t in (x, self.gate_weight, self.gate_bias, w1, w2, w3))
