@@ -180,11 +180,30 @@ int fm_aux_loss(const float* prob_partial, int64_t n_waves, const int32_t* count
 /* Replaces the gate of MoERouter.forward (reference model/moe.py:151-154):
  * logits[t][e] = sum_d x[t][d] w[e][d] + bias[e] + score_bias[e] in fp32, the
  * reference's gate(x.float()) (nn.Linear(D, E, bias=True), :107) plus the
- * DeepSeek-V3 score bias.  x bf16 or fp32 [T, D] (pitch ld_x), w fp32 [E, D]
- * (pitch ld_w), bias / score_bias fp32 [E] or null.  E <= 256, D % 8 == 0. */
-int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const float* w,
-                     int64_t ld_w, const float* bias, const float* score_bias, int E, float* logits,
-                     int64_t ld_l, void* stream);
+ * DeepSeek-V3 score bias.  x bf16 or fp32 [T, D] (pitch ld_x), w fp32 or bf16
+ * (w_dtype) [E, D] (pitch ld_w, a multiple of 4), bias [E] in w's dtype or
+ * null, score_bias fp32 [E] or null.  E <= 256, D % 8 == 0. */
+int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
+                     int64_t ld_w, const void* bias, const float* score_bias, int E, float* logits, int64_t ld_l,
+                     void* stream);
+
+/* Replaces MoERouter.forward (reference model/moe.py:133-184, jitter aside)
+ * with its load-balancing loss (:267-281) and expert-count update
+ * (:284-292): the gate as fm_router_logits (logits written, score bias
+ * included), the gating as fm_topk_gating (gating, flags, replay), counts[E]
+ * of the T*K slots (added to tokens_per_expert / total_tokens when given, as
+ * fm_expert_counts with tokens = T) and loss = E * sum_e f_e P_e (+ z-loss
+ * with z_loss_multiplier != 0) as fm_aux_loss.  For E <= 8 and D = 512 n <=
+ * 2048 the gate, gating, loss partials and counts run as one pass over x plus
+ * one small kernel; other shapes launch the steps separately.  T > 0; the
+ * workspace holds fm_router_forward_workspace_bytes(T, E) bytes. */
+int64_t fm_router_forward_workspace_bytes(int64_t T, int E);
+int fm_router_forward(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
+                      int64_t ld_w, const void* bias, const float* score_bias, int E, int K, int gating, int flags,
+                      const void* replay_indices, int replay_i64, float* logits, int64_t ld_l, float* weights,
+                      void* indices, int indices_i64, int32_t* counts, int64_t* tokens_per_expert,
+                      int64_t* total_tokens, float z_loss_multiplier, float* loss, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 /* counts[e] = number of the n routed slots with index e (the f_i numerator of
  * MoERouter._load_balancing_loss, model/moe.py:271-274); indices outside
@@ -221,14 +240,29 @@ int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, i
                    int replay, const void* indices, int indices_i64, const float* dweights, const float* daux,
                    const int32_t* counts, float z_loss_multiplier, float* dlogits, int64_t ld_d, void* stream);
 
+/* fm_gating_grad with the weights' gradient formed in the same pass instead
+ * of read (reference MoEBase.forward's output = sum_k w[t,k] y[row(t,k)]
+ * under autograd, model/moe.py:1594, and the gating of :158-184):
+ * dweights[t][k] = <dout[t], y[row_of[t K + k]]> in fp32 (0 for a slot with
+ * row -1), dout bf16 [T, D] (pitch ld_do), y bf16 expert outputs (pitch ld_y);
+ * K <= 8.  dweights_out [T, K] receives it when not null.  With dout null it
+ * is fm_gating_grad. */
+int fm_gating_grad_dot(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, int flags, int replay,
+                       const void* indices, int indices_i64, const float* dweights, const void* dout, int64_t ld_do,
+                       const void* y, int64_t ld_y, const int32_t* row_of, int64_t D, float* dweights_out,
+                       const float* daux, const int32_t* counts, float z_loss_multiplier, float* dlogits,
+                       int64_t ld_d, void* stream);
+
 /* Backward of the gate (reference nn.Linear of model/moe.py:107 under
- * autograd): dx = dlogits w (x's dtype, null to skip), dw = dlogits^T x and
- * db = sum_t dlogits (fp32, null to skip), summed in a fixed order; dw needs
- * a workspace of fm_router_workspace_bytes(T, D, E) bytes. */
+ * autograd): dx = dlogits w (x's dtype, null to skip; w fp32 or bf16),
+ * dw = dlogits^T x and db = sum_t dlogits (fp32 sums, null to skip, written
+ * as dw_dtype / db_dtype), summed in a fixed order; dw and db need a
+ * workspace of fm_router_workspace_bytes(T, D, E) bytes. */
 int64_t fm_router_workspace_bytes(int64_t T, int64_t D, int E);
 int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x_dtype, int64_t ld_x, int64_t T,
-                       int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
-                       int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream);
+                       int64_t D, const void* w, int w_dtype, int64_t ld_w, int E, void* dx, int64_t ld_dx, void* dw,
+                       int dw_dtype, int64_t ld_dw, void* db, int db_dtype, void* workspace, int64_t workspace_bytes,
+                       void* stream);
 
 /* Replaces RMSNorm.forward (reference model/norm.py:32-49, full_precision) as
  * MoEHybridTransformerBlock applies it before the MoE (model/transformer.py:

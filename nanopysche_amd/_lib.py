@@ -86,14 +86,20 @@ SIGNATURES = {
     "fm_topk_gating": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
                                _i64, _vp]),
     "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, C.c_float, _vp, _vp]),
-    "fm_router_logits": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
+    "fm_router_logits": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
+    "fm_router_forward_workspace_bytes": (_i64, [_i64, _i32]),
+    "fm_router_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
+                                 _vp, _i32, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _vp, C.c_float, _vp, _vp, _i64,
+                                 _vp]),
     "fm_expert_counts": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _i64, _vp]),
     "fm_score_bias_update": (_i32, [_vp, _vp, _i32, C.c_float, _vp, _vp]),
     "fm_gating_grad": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, C.c_float,
                               _vp, _i64, _vp]),
+    "fm_gating_grad_dot": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i64, _vp,
+                                  _i64, _vp, _i64, _vp, _vp, _vp, C.c_float, _vp, _i64, _vp]),
     "fm_router_workspace_bytes": (_i64, [_i64, _i64, _i32]),
-    "fm_router_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp,
-                                  _i64, _vp, _vp, _i64, _vp]),
+    "fm_router_backward": (_i32, [_vp, _i64, _vp, _i32, _i64, _i64, _i64, _vp, _i32, _i64, _i32, _vp, _i64, _vp,
+                                  _i32, _i64, _vp, _i32, _vp, _i64, _vp]),
     "fm_rmsnorm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, C.c_float, _vp, _i64, _i32, _vp, _i64,
                                    _vp, _i64, _vp, _vp]),
     "fm_rmsnorm_backward_workspace_bytes": (_i64, [_i64, _i64]),

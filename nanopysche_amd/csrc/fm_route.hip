@@ -17,6 +17,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "fm_gating.h"
 #include "fm_tile.h"
 #include "../../include/fm_hip.h"
 
@@ -39,23 +40,6 @@ struct TopkArgs {
 };
 
 constexpr int kTopkMaxPerLane = 4;  // E <= 256
-
-// Selection order of top-k: NaN above every number (as torch.topk orders
-// it), then the larger value, then the lower expert index.
-__device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
-  const bool an = av != av, bn = bv != bv;
-  if (an || bn) return an && (!bn || ai < bi);
-  return av > bv || (av == bv && ai < bi);
-}
-
-__device__ __forceinline__ int load_index(const void* p, int i64, int64_t i) {
-  return i64 ? int(static_cast<const int64_t*>(p)[i]) : static_cast<const int32_t*>(p)[i];
-}
-
-__device__ __forceinline__ void store_index(void* p, int i64, int64_t i, int v) {
-  if (i64) static_cast<int64_t*>(p)[i] = v;
-  else static_cast<int32_t*>(p)[i] = v;
-}
 
 // One token per wave; lane l holds experts l + 64 j.  Each of the K rounds is
 // a wave arg-max over the experts not yet taken (a per-lane taken mask, so an
@@ -180,68 +164,14 @@ __global__ __launch_bounds__(256) void topk_small_kernel(TopkArgs a) {
   const int lane = threadIdx.x & 63, g = lane / EP, e = lane % EP;
   const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t n_waves = int64_t(gridDim.x) * 4;
-  const bool ev = e < a.E;
-  const bool need_p = a.prob_partial || a.replay || a.z_partial;
+  const GateOut go{a.E, a.K, a.sigmoid, a.l2, a.replay, a.replay_i64, a.w, a.idx, a.idx_i64,
+                   (a.prob_partial || a.replay || a.z_partial) ? 1 : 0};
   float psum = 0.f, zsum = 0.f;
   for (int64_t tg = wave; tg * NT < a.T; tg += n_waves) {
     const int64_t t = tg * NT + g;
     const bool tv = t < a.T;
-    const float v = (tv && ev) ? a.logits[t * a.ld + e] : -INFINITY;
-    float sc = a.sigmoid ? 1.f / (1.f + expf(-v)) : v;
-    if (need_p) {
-      float m = v;
-#pragma unroll
-      for (int off = EP / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-      float p = ev ? expf(v - m) : 0.f;
-      float sm = p;
-#pragma unroll
-      for (int off = EP / 2; off > 0; off >>= 1) sm += __shfl_xor(sm, off);
-      p /= sm;
-      if (tv) psum += p;
-      const float lse = m + logf(sm);
-      if (tv && e == 0) zsum += lse * lse;
-      if (a.replay) {
-        const int r = (tv && e < a.K) ? load_index(a.replay, a.replay_i64, t * a.K + e) : -1;
-        bool hit = false;
-        for (int k = 0; k < a.K; ++k) hit |= __shfl(r, g * EP + k) == e;
-        sc = (ev && hit) ? p : 0.f;
-        float msum = sc;
-#pragma unroll
-        for (int off = EP / 2; off > 0; off >>= 1) msum += __shfl_xor(msum, off);
-        sc /= fmaxf(msum, 1e-8f);
-      }
-    }
-    bool taken = false;
-    float top_first = 0.f, wsum = 0.f, my_w = 0.f;
-    int my_i = 0;
-    for (int k = 0; k < a.K; ++k) {
-      const bool cand = ev && !taken;
-      float bv = cand ? sc : -INFINITY;
-      int bi = cand ? e : 0x7fffffff;
-#pragma unroll
-      for (int off = EP / 2; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-      }
-      if (bi == e) taken = true;   // the winner leaves the race
-      const float lg = __shfl(v, g * EP + (bi & (EP - 1)));
-      if (k == 0) top_first = lg;
-      const float wk = (a.sigmoid || a.replay) ? bv : expf(lg - top_first);
-      wsum += wk;
-      if (e == k) { my_w = wk; my_i = bi; }
-    }
-    float wn = a.replay ? my_w : (a.sigmoid ? my_w / (wsum + 1e-8f) : my_w / wsum);
-    if (a.l2) {
-      float sq = e < a.K ? wn * wn : 0.f;
-#pragma unroll
-      for (int off = EP / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
-      wn = wn / (sqrtf(sq) + 1e-8f);
-    }
-    if (tv && e < a.K) {
-      a.w[t * a.K + e] = wn;
-      store_index(a.idx, a.idx_i64, t * a.K + e, my_i);
-    }
+    const float v = (tv && e < a.E) ? a.logits[t * a.ld + e] : -INFINITY;
+    gate_group<EP>(go, t, tv, g, e, v, psum, zsum);
   }
   if (a.prob_partial) {
 #pragma unroll

@@ -1,19 +1,27 @@
 // Router gate of the MoE layer (reference MoERouter.forward, model/moe.py:133-184):
+//   fm_router_forward    the whole forward of the router in two launches for small gates
+//                        (E <= 8, D = 512 n <= 2048): logits, top-k gating, the softmax
+//                        and logsumexp^2 partials and per-workgroup expert histograms in
+//                        one pass over x, then counts + load-balancing (+ z) loss; other
+//                        shapes run the same steps as separate kernels
 //   fm_router_logits     logits[t][e] = sum_d x[t][d] * w[e][d] + bias[e] + score_bias[e], fp32
 //                        (the reference's gate(x.float()) + score_bias, :151-154)
 //   fm_expert_counts     counts[e] = number of the T*K slots routed to e (the f_i of the
 //                        load-balancing loss, :267-281)
 //   fm_gating_grad       dlogits from the gradient of the top-k weights (softmax over the K
 //                        selected logits, :249-255, or normalised sigmoid, :257-265) plus the
-//                        gradient of the load-balancing loss E * sum_i f_i P_i
-//   fm_router_backward   dx = dlogits w, dw = dlogits^T x, db = sum_t dlogits (fp32; dw and
-//                        db summed in a fixed order: dw as per-slice partials in a caller
-//                        workspace, then the slices in order; db as one tree per expert)
+//                        gradient of the load-balancing loss E * sum_i f_i P_i;
+//                        fm_gating_grad_dot forms the weights' gradient itself from the
+//                        expert outputs, <dout[t], y[row(t, k)]>, in the same pass
+//   fm_router_backward   dx = dlogits w, dw = dlogits^T x, db = sum_t dlogits (fp32 sums in a
+//                        fixed order: per-slice partials in a caller workspace, then the
+//                        slices in order), dw and db written in the parameters' dtype
 //
 // The gate is a skinny GEMM (E <= 256 outputs per token): x is read once at
 // its size and the FMAs run on the VALU in fp32, as the reference computes it;
-// HBM, not arithmetic, bounds it at the layer's shapes.
-#include "fm_common.h"
+// HBM, not arithmetic, bounds it at the layer's shapes.  Gate weights are
+// read as stored (fp32 or bf16).
+#include "fm_gating.h"
 #include "../../include/fm_hip.h"
 
 namespace fm {
@@ -54,12 +62,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Gate weights are read as stored (fp32, or bf16 widened exactly), so the
+// fp32 arithmetic sees the parameter's own values with no conversion pass.
+__device__ __forceinline__ float4 ldw4(const void* w, int bf16, int64_t i) {
+  if (bf16) {
+    const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + i);
+    return make_float4(u2f(u.x << 16), u2f(u.x & 0xffff0000u), u2f(u.y << 16), u2f(u.y & 0xffff0000u));
+  }
+  return *reinterpret_cast<const float4*>(static_cast<const float*>(w) + i);
+}
+__device__ __forceinline__ float ldw1(const void* w, int bf16, int64_t i) {
+  return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(w)[i]) : static_cast<const float*>(w)[i];
+}
+
 // Stages w[e0 .. e0+EC)[c0 .. c0+kRouterCols) into LDS (zero past E or D).
 // All of a thread's loads are issued before its LDS stores (a fixed trip
 // count), so staging costs one memory latency, not one per element group.
 template <int EC>
-__device__ __forceinline__ void stage_gate(float (&wl)[EC][kRouterCols], const float* w, int64_t ld_w, int E,
-                                           int64_t D, int e0, int64_t c0) {
+__device__ __forceinline__ void stage_gate(float (&wl)[EC][kRouterCols], const void* w, int w_bf16, int64_t ld_w,
+                                           int E, int64_t D, int e0, int64_t c0) {
   constexpr int kPer = EC * kRouterCols / 4 / 256;
   float4 v[kPer];
 #pragma unroll
@@ -67,7 +88,7 @@ __device__ __forceinline__ void stage_gate(float (&wl)[EC][kRouterCols], const f
     const int i = threadIdx.x + 256 * u;
     const int e = i / (kRouterCols / 4), c = (i % (kRouterCols / 4)) * 4;
     v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (e0 + e < E && c0 + c < D) v[u] = *reinterpret_cast<const float4*>(w + (e0 + e) * ld_w + c0 + c);
+    if (e0 + e < E && c0 + c < D) v[u] = ldw4(w, w_bf16, (e0 + e) * ld_w + c0 + c);
   }
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
@@ -80,9 +101,10 @@ __device__ __forceinline__ void stage_gate(float (&wl)[EC][kRouterCols], const f
 struct RouterArgs {
   const void* x;
   int64_t ld_x, T, D;
-  const float* w;
+  const void* w;          // [E, ld_w] fp32 or bf16 (w_bf16)
   int64_t ld_w;
-  const float* bias;
+  const void* bias;       // [E], the weight's dtype, or null
+  int w_bf16;
   const float* score_bias;
   int E;
   float* logits;
@@ -105,7 +127,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
     for (int e = 0; e < EC; ++e) acc[r][e] = 0.f;
   for (int64_t c0 = 0; c0 < a.D; c0 += kRouterCols) {
     __syncthreads();
-    stage_gate<EC>(wl, a.w, a.ld_w, a.E, a.D, e0, c0);
+    stage_gate<EC>(wl, a.w, a.w_bf16, a.ld_w, a.E, a.D, e0, c0);
     __syncthreads();
     const int64_t col = c0 + lane * 8;
     if (col < a.D) {
@@ -139,7 +161,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
       const int eg = e0 + e;
       if (lane == e && eg < a.E && r0 + r < a.T) {
         float v = s;
-        if (a.bias) v += a.bias[eg];
+        if (a.bias) v += ldw1(a.bias, a.w_bf16, eg);
         if (a.score_bias) v += a.score_bias[eg];
         a.logits[(r0 + r) * a.ld_l + eg] = v;
       }
@@ -206,10 +228,25 @@ __device__ __forceinline__ void router_fma_chunk(float (&acc)[32], const float (
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) {
+// With FUSED the same workgroup also gates its 16 tokens (gate_group, the
+// gating kernel's per-token code, on the logits it just formed), writes the
+// per-wave softmax / logsumexp^2 partials of the load-balancing and z losses,
+// and its expert histogram of the routed slots (router_finish_kernel turns
+// those into counts and the loss).
+struct RouterFuse {
+  GateOut go;
+  float* prob_partial;   // [E, gridDim.x]: per-workgroup softmax sums (waves 0..3 in order)
+  float* z_partial;      // [gridDim.x] or null
+  int32_t* block_hist;   // [E, gridDim.x]
+};
+
+template <typename T, bool FUSED>
+__global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, RouterFuse f) {
   extern __shared__ __attribute__((aligned(16))) float wl[];   // [8][D]
+  __shared__ int32_t hist[8];
+  __shared__ float wpart[4][9];   // per wave: softmax sums of experts 0..7, logsumexp^2
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (FUSED && threadIdx.x < 8) hist[threadIdx.x] = 0;
   const int64_t r0 = int64_t(blockIdx.x) * kRouterRows + wave * 4;
   const int64_t D = a.D;
   const int nc = int(D / kRouterCols);   // D % 512 == 0 (launcher)
@@ -246,7 +283,7 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) 
       for (int u = 0; u < kPerRow; ++u) {
         const int c = (int(threadIdx.x) + 256 * u) * 4;
         v[e][u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (c < Di && e < a.E) v[e][u] = *reinterpret_cast<const float4*>(a.w + e * a.ld_w + c);
+        if (c < Di && e < a.E) v[e][u] = ldw4(a.w, a.w_bf16, e * a.ld_w + c);
       }
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -287,11 +324,97 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a) 
   }
   const float sum = wave_reduce_scatter32(acc, lane);
   const int vi = lane >> 1, r = vi >> 3, e = vi & 7;
-  if ((lane & 1) == 0 && e < a.E && r0 + r < a.T) {
-    float v = sum;
-    if (a.bias) v += a.bias[e];
-    if (a.score_bias) v += a.score_bias[e];
-    a.logits[(r0 + r) * a.ld_l + e] = v;
+  float lv = sum;
+  if (e < a.E) {
+    if (a.bias) lv += ldw1(a.bias, a.w_bf16, e);
+    if (a.score_bias) lv += a.score_bias[e];
+  }
+  if ((lane & 1) == 0 && e < a.E && r0 + r < a.T) a.logits[(r0 + r) * a.ld_l + e] = lv;
+  if constexpr (FUSED) {
+    // token slot g = lane / 8 (tokens r0 .. r0 + 3; slots 4..7 idle), expert lane % 8
+    const int g = lane >> 3, ge = lane & 7;
+    const float lg = __shfl(lv, 2 * (8 * (g & 3) + ge));
+    const int64_t t = r0 + g;
+    const bool tv = g < 4 && t < a.T;
+    float psum = 0.f, zsum = 0.f;
+    const int my_i = gate_group<8>(f.go, t, tv, g, ge, (tv && ge < a.E) ? lg : -INFINITY, psum, zsum);
+    if (tv && ge < f.go.K) atomicAdd(&hist[my_i], 1);
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) psum += __shfl_xor(psum, off);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) zsum += __shfl_xor(zsum, off);
+    if (lane < 8) wpart[wave][lane] = psum;
+    if (lane == 0) wpart[wave][8] = zsum;
+    __syncthreads();
+    const int64_t nb = gridDim.x;
+    if (threadIdx.x < a.E) {
+      const int e = threadIdx.x;
+      f.block_hist[e * nb + blockIdx.x] = hist[e];
+      f.prob_partial[e * nb + blockIdx.x] = ((wpart[0][e] + wpart[1][e]) + wpart[2][e]) + wpart[3][e];
+    }
+    if (f.z_partial && threadIdx.x == 0)
+      f.z_partial[blockIdx.x] = ((wpart[0][8] + wpart[1][8]) + wpart[2][8]) + wpart[3][8];
+  }
+}
+
+// Counts and loss after the fused router forward (one workgroup: wave e < E
+// per expert, wave 8 for the z-loss): counts[e] = sum of the workgroups'
+// histograms (exact), optionally added to the running totals; loss = E *
+// sum_e (counts_e / T) (P_e / T) with P_e the sum of the per-workgroup softmax
+// partials, plus z_mult * (sum of the logsumexp^2 partials) / T.  Each wave
+// sums its contiguous row of partials in lane-strided runs of eight loads,
+// then a fixed shuffle tree.
+__global__ __launch_bounds__(576) void router_finish_kernel(const int32_t* block_hist, int64_t nb, int E,
+                                                            int32_t* counts, int64_t* acc, int64_t* acc_total,
+                                                            int64_t T, const float* prob_partial,
+                                                            const float* z_partial, float z_mult, float* loss) {
+  __shared__ float term[8];
+  __shared__ float zterm;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool zw = wave == 8;
+  if (wave < E || (zw && z_partial)) {
+    const int32_t* hrow = block_hist + int64_t(wave) * nb;
+    const float* prow = zw ? z_partial : prob_partial + int64_t(wave) * nb;
+    int c = 0;
+    float p = 0.f;
+    for (int64_t b0 = 0; b0 < nb; b0 += 512) {
+      int cv[8];
+      float pv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t b = b0 + u * 64 + lane;
+        cv[u] = (!zw && b < nb) ? hrow[b] : 0;
+        pv[u] = b < nb ? prow[b] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        c += cv[u];
+        p += pv[u];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      c += __shfl_xor(c, off);
+      p += __shfl_xor(p, off);
+    }
+    if (lane == 0) {
+      if (zw) {
+        zterm = p / float(T);
+      } else {
+        counts[wave] = c;
+        if (acc) acc[wave] += c;
+        term[wave] = (float(c) / float(T)) * (p / float(T));
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (acc_total) acc_total[0] += T;
+    float sum = 0.f;
+    for (int e = 0; e < E; ++e) sum += term[e];
+    float l = float(E) * sum;
+    if (z_partial) l = l + z_mult * zterm;
+    loss[0] = l;
   }
 }
 
@@ -349,7 +472,62 @@ struct GatingGradArgs {
   float z_mult;          // z-loss multiplier (0: no z-loss)
   float* dlogits;        // [T, ld_d]
   int64_t ld_d;
+  // the weights' gradient formed here instead of read from dw (DOT kernels):
+  // dw[t, k] = <dout[t], y[row_of[t K + k]]> (0 for a dropped slot, row -1)
+  const uint16_t* dout;  // bf16 [T, ld_do]
+  int64_t ld_do;
+  const uint16_t* y;     // bf16 [rows, ld_y]
+  int64_t ld_y;
+  const int32_t* row_of; // [T K]
+  int64_t D;
+  float* dw_out;         // [T, K] or null: the formed weights' gradient
 };
+
+constexpr int kDotMaxK = 8;
+
+// dots[k] (every lane) = <dout[t], y[row_of[t K + k]]> for k < K <= KD: lane
+// l takes columns 8 l .. of each 512-column chunk; a pass over CH chunks
+// issues all of its dout and y loads before the FMAs (8 / KD chunks, so at
+// most nine 16-byte loads per lane wait at once); the K partial sums meet in
+// a wave sum each.
+template <int KD>
+__device__ __forceinline__ void slot_dots(const GatingGradArgs& a, int64_t t, int lane, float (&dots)[kDotMaxK]) {
+  constexpr int CH = KD >= 8 ? 1 : 8 / KD;
+  int rk[KD];
+#pragma unroll
+  for (int k = 0; k < kDotMaxK; ++k) dots[k] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KD; ++k) rk[k] = k < a.K ? a.row_of[t * a.K + k] : -1;
+  const uint16_t* g = a.dout + t * a.ld_do;
+  for (int64_t c0 = 0; c0 < a.D; c0 += 512 * CH) {
+    uint4 gr[CH], yr[KD][CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int64_t col = c0 + 512 * c + lane * 8;
+      const bool cv = col < a.D;
+      gr[c] = cv ? *reinterpret_cast<const uint4*>(g + col) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < KD; ++k)
+        yr[k][c] = (cv && rk[k] >= 0) ? *reinterpret_cast<const uint4*>(a.y + int64_t(rk[k]) * a.ld_y + col)
+                                      : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float gv[8];
+      bf16x8_to_f32(gr[c], gv);
+#pragma unroll
+      for (int k = 0; k < KD; ++k) {
+        float yv[8];
+        bf16x8_to_f32(yr[k][c], yv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dots[k] += gv[j] * yv[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KD; ++k)
+    if (k < a.K) dots[k] = wave_sum(dots[k]);
+}
 
 constexpr int kGateMaxPerLane = 4;  // E <= 256
 
@@ -367,7 +545,9 @@ __device__ __forceinline__ float wave_max(float v) {
 // l2: w = u / (n + 1e-8), n = ||u||, so du = dw / (n + 1e-8) - u (u.dw) / (n (n + 1e-8)^2).
 // Then c = sum_k u_k du_k and expert i_k gets
 //   softmax: u_k (du_k - c);  sigmoid: (du_k - c) / (S + 1e-8) * s_k (1 - s_k).
+template <int KD>   // KD > 0: the weights' gradient formed here, K <= KD
 __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
+  constexpr bool DOT = KD > 0;
   const int lane = threadIdx.x & 63;
   const int64_t n_waves = int64_t(gridDim.x) * 4;
   const float aux = a.daux ? a.daux[0] : 0.f;
@@ -379,7 +559,15 @@ __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
       v[j] = e < a.E ? a.logits[t * a.ld_l + e] : -INFINITY;
       g[j] = 0.f;
     }
-    if (a.dw) {
+    if (DOT || a.dw) {
+      float mine = 0.f;
+      if constexpr (DOT) {
+        float dots[kDotMaxK];
+        slot_dots<KD>(a, t, lane, dots);
+#pragma unroll
+        for (int k = 0; k < kDotMaxK; ++k) mine = lane == k ? dots[k] : mine;
+        if (a.dw_out && lane < a.K) a.dw_out[int64_t(t) * a.K + lane] = mine;
+      }
       // slots outside [0, E) carry no weight and no gradient
       int ik = -1;
       float lk = -INFINITY, dk = 0.f;
@@ -388,7 +576,7 @@ __global__ __launch_bounds__(256) void gating_grad_kernel(GatingGradArgs a) {
         ik = a.idx_i64 ? int(static_cast<const int64_t*>(a.idx)[i]) : static_cast<const int32_t*>(a.idx)[i];
         if (ik >= 0 && ik < a.E) {
           lk = a.logits[t * a.ld_l + ik];
-          dk = a.dw[i];
+          dk = DOT ? mine : a.dw[i];
         } else {
           ik = -1;
         }
@@ -466,12 +654,14 @@ struct RouterBwdArgs {
   int64_t ld_dl;
   const void* x;         // [T, ld_x]
   int64_t ld_x, T, D;
-  const float* w;        // [E, ld_w]
+  const void* w;         // [E, ld_w], fp32 or bf16 (w_bf16)
   int64_t ld_w;
+  int w_bf16;
   int E;
   void* dx;              // [T, ld_dx], x's dtype (null: skip)
   int64_t ld_dx;
   float* part;           // [slices][E][D] partial dw
+  float* part_db;        // [slices][E] partial db, or null
   int64_t slices, rows_per_slice;
 };
 
@@ -492,7 +682,7 @@ __global__ __launch_bounds__(256) void router_dx_kernel(RouterBwdArgs a) {
       for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
     for (int e0 = 0; e0 < a.E; e0 += 16) {
       __syncthreads();
-      stage_gate<16>(wl, a.w, a.ld_w, a.E, a.D, e0, c0);
+      stage_gate<16>(wl, a.w, a.w_bf16, a.ld_w, a.E, a.D, e0, c0);
       __syncthreads();
       if (col < a.D) {
 #pragma unroll 4
@@ -519,58 +709,68 @@ __global__ __launch_bounds__(256) void router_dx_kernel(RouterBwdArgs a) {
 
 // Partial dw: grid (ceil(D / 512), slices, ceil(E / 8)); the slice's rows are
 // split over the 4 waves (row t of the slice to wave t % 4), lane l owns
-// columns 8 l .. of the chunk for 8 experts; the 4 waves' sums meet in LDS
-// in a fixed order.
+// columns 8 l .. of the chunk for 8 experts; each wave issues the loads of
+// eight of its rows before their FMAs (row order kept), and the 4 waves'
+// sums meet in LDS in a fixed order.  The workgroups of column chunk 0 also
+// form the slice's db partial (each wave's rows in order, then waves 0..3).
 template <typename T>
 __global__ __launch_bounds__(256) void router_dw_kernel(RouterBwdArgs a) {
-  constexpr int EG = 8;
+  constexpr int EG = 8, RB = 8;
   __shared__ __attribute__((aligned(16))) float red[4][EG][kRouterCols];
+  __shared__ float dbred[4][EG];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t col = int64_t(blockIdx.x) * kRouterCols + lane * 8;
   const int64_t s = blockIdx.y;
   const int e0 = blockIdx.z * EG;
+  const bool want_db = a.part_db != nullptr && blockIdx.x == 0;
   const int64_t t_lo = s * a.rows_per_slice;
   const int64_t t_hi = t_lo + a.rows_per_slice < a.T ? t_lo + a.rows_per_slice : a.T;
   const T* x = static_cast<const T*>(a.x);
-  float acc[EG][8];
+  const bool cv = col < a.D;
+  const int64_t cl = cv ? col : 0;   // rows are read in full; columns past D are not stored
+  float acc[EG][8], dbacc[EG];
 #pragma unroll
-  for (int e = 0; e < EG; ++e)
+  for (int e = 0; e < EG; ++e) {
+    dbacc[e] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[e][j] = 0.f;
-  if (col < a.D) {
-    int64_t t = t_lo + wave;
-    // four of the wave's rows per round: all their loads before any FMA (one
-    // memory latency per four rows), the FMAs in row order as below
-    for (; t + 12 < t_hi; t += 16) {
-      float xv[4][8], dv[4][EG];
+  }
+  int64_t t = t_lo + wave;
+  for (; t + 4 * (RB - 1) < t_hi; t += 4 * RB) {
+    float xv[RB][8], dv[RB][EG];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        load8f(x + (t + 4 * u) * a.ld_x + col, xv[u]);
+    for (int u = 0; u < RB; ++u) {
+      load8f(x + (t + 4 * u) * a.ld_x + cl, xv[u]);
 #pragma unroll
-        for (int e = 0; e < EG; ++e) dv[u][e] = e0 + e < a.E ? a.dl[(t + 4 * u) * a.ld_dl + e0 + e] : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int e = 0; e < EG; ++e)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(dv[u][e], xv[u][j], acc[e][j]);
+      for (int e = 0; e < EG; ++e) dv[u][e] = e0 + e < a.E ? a.dl[(t + 4 * u) * a.ld_dl + e0 + e] : 0.f;
     }
-    for (; t < t_hi; t += 4) {
-      float xv[8];
-      load8f(x + t * a.ld_x + col, xv);
+#pragma unroll
+    for (int u = 0; u < RB; ++u)
 #pragma unroll
       for (int e = 0; e < EG; ++e) {
-        const float d = e0 + e < a.E ? a.dl[t * a.ld_dl + e0 + e] : 0.f;
+        dbacc[e] += dv[u][e];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(d, xv[j], acc[e][j]);
+        for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(dv[u][e], xv[u][j], acc[e][j]);
       }
+  }
+  for (; t < t_hi; t += 4) {
+    float xv[8];
+    load8f(x + t * a.ld_x + cl, xv);
+#pragma unroll
+    for (int e = 0; e < EG; ++e) {
+      const float d = e0 + e < a.E ? a.dl[t * a.ld_dl + e0 + e] : 0.f;
+      dbacc[e] += d;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(d, xv[j], acc[e][j]);
     }
   }
 #pragma unroll
   for (int e = 0; e < EG; ++e)
 #pragma unroll
     for (int j = 0; j < 8; ++j) red[wave][e][lane * 8 + j] = acc[e][j];
+  if (want_db && lane == 0)
+#pragma unroll
+    for (int e = 0; e < EG; ++e) dbred[wave][e] = dbacc[e];
   __syncthreads();
   for (int i = threadIdx.x; i < EG * kRouterCols; i += 256) {
     const int e = i / kRouterCols, c = i % kRouterCols;
@@ -578,43 +778,92 @@ __global__ __launch_bounds__(256) void router_dw_kernel(RouterBwdArgs a) {
     if (e0 + e < a.E && gc < a.D)
       a.part[(s * a.E + e0 + e) * a.D + gc] = ((red[0][e][c] + red[1][e][c]) + red[2][e][c]) + red[3][e][c];
   }
+  if (want_db && threadIdx.x < EG && e0 + int(threadIdx.x) < a.E) {
+    const int e = threadIdx.x;
+    a.part_db[s * a.E + e0 + e] = ((dbred[0][e] + dbred[1][e]) + dbred[2][e]) + dbred[3][e];
+  }
 }
 
-// dw[e][d] = sum over slices (in order) of the partials.
-__global__ __launch_bounds__(256) void router_dw_reduce_kernel(RouterBwdArgs a, float* dw, int64_t ld_dw) {
+// dw[e][d] = sum over the slices of the partials: a workgroup owns 64
+// elements, wave q sums slices q, q + 4, ... (eight loads in flight), and the
+// four wave sums are added in wave order.  The last workgroup forms db the
+// same way per expert (lane-strided slices, then a fixed shuffle tree).  Both
+// are written as fp32 or bf16.
+__global__ __launch_bounds__(256) void router_dw_reduce_kernel(RouterBwdArgs a, void* dw, int64_t ld_dw, int dw_bf16,
+                                                               void* db, int db_bf16) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
   const int64_t n = int64_t(a.E) * a.D;
-  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
-    float v = 0.f;
+  if (blockIdx.x == gridDim.x - 1) {
+    if (db == nullptr) return;
+    for (int e = q; e < a.E; e += 4) {
+      float v = 0.f;
 #pragma unroll 8
-    for (int64_t s = 0; s < a.slices; ++s) v += a.part[s * n + i];
-    dw[(i / a.D) * ld_dw + i % a.D] = v;
+      for (int64_t sl = lane; sl < a.slices; sl += 64) v += a.part_db[sl * a.E + e];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+      if (lane == 0) {
+        if (db_bf16) static_cast<uint16_t*>(db)[e] = f32_to_bf16(v);
+        else static_cast<float*>(db)[e] = v;
+      }
+    }
+    return;
   }
-}
-
-// db[e] = sum_t dl[t][e]: workgroup e, tokens strided over the threads, then
-// a fixed-order tree in LDS.
-__global__ __launch_bounds__(256) void router_db_kernel(const float* dl, int64_t ld_dl, int64_t T, float* db) {
-  __shared__ float red[256];
-  const int e = blockIdx.x;
+  if (dw == nullptr) return;
+  const int64_t i = int64_t(blockIdx.x) * 64 + lane;
   float v = 0.f;
-  // unrolled so the loads of several rows are in flight at once; the adds
-  // keep their order
+  if (i < n) {
 #pragma unroll 8
-  for (int64_t t = threadIdx.x; t < T; t += 256) v += dl[t * ld_dl + e];
-  red[threadIdx.x] = v;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-    __syncthreads();
+    for (int64_t sl = q; sl < a.slices; sl += 4) v += a.part[sl * n + i];
   }
-  if (threadIdx.x == 0) db[e] = red[0];
+  red[q][lane] = v;
+  __syncthreads();
+  if (q == 0 && i < n) {
+    const float t = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    const int64_t o = (i / a.D) * ld_dw + i % a.D;
+    if (dw_bf16) static_cast<uint16_t*>(dw)[o] = f32_to_bf16(t);
+    else static_cast<float*>(dw)[o] = t;
+  }
 }
 
-// slices of the token range for the dw partials: at most 64, and at most
+// The fused forward takes the small-gate kernel's shapes; others fall back to
+// separate kernels (their gating uses this many waves of partials).
+constexpr int64_t kRouterForwardWaves = 1024;
+
+inline bool router_small_ok(int E, int64_t D) { return E <= 8 && 8 * D <= kGateLdsFloats && D % kRouterCols == 0; }
+
+int router_logits_launch(const RouterArgs& a, int x_dtype, const RouterFuse* f, int fused, hipStream_t s,
+                         const char* what) {
+  const unsigned rb = unsigned((a.T + kRouterRows - 1) / kRouterRows);
+  const bool xb = x_dtype == FM_DTYPE_BF16;
+  if (router_small_ok(a.E, a.D)) {
+    const size_t lds = size_t(8 * a.D) * sizeof(float);
+    const RouterFuse none{};
+    const RouterFuse& ff = f ? *f : none;
+    if (fused) {
+      if (xb) hipLaunchKernelGGL((router_logits_small_kernel<uint16_t, true>), dim3(rb), dim3(256), lds, s, a, ff);
+      else hipLaunchKernelGGL((router_logits_small_kernel<float, true>), dim3(rb), dim3(256), lds, s, a, ff);
+    } else {
+      if (xb) hipLaunchKernelGGL((router_logits_small_kernel<uint16_t, false>), dim3(rb), dim3(256), lds, s, a, ff);
+      else hipLaunchKernelGGL((router_logits_small_kernel<float, false>), dim3(rb), dim3(256), lds, s, a, ff);
+    }
+  } else if (a.E <= 8) {
+    const dim3 grid(rb, 1);
+    if (xb) hipLaunchKernelGGL((router_logits_kernel<uint16_t, 8>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((router_logits_kernel<float, 8>), grid, dim3(256), 0, s, a);
+  } else {
+    const dim3 grid(rb, unsigned((a.E + 15) / 16));
+    if (xb) hipLaunchKernelGGL((router_logits_kernel<uint16_t, 16>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((router_logits_kernel<float, 16>), grid, dim3(256), 0, s, a);
+  }
+  return check_launch(what);
+}
+
+// slices of the token range for the dw partials: at most 128, and at most
 // 32 MiB of partials
 inline int64_t router_slices(int64_t T, int64_t D, int E) {
   int64_t s = (32ll << 20) / (int64_t(E) * D * 4);
-  s = s < 64 ? s : 64;
+  s = s < 128 ? s : 128;
   s = s < 1 ? 1 : s;
   const int64_t per = (T + s - 1) / s;
   return per > 0 ? (T + per - 1) / per : 1;
@@ -626,33 +875,78 @@ using namespace fm;
 
 extern "C" {
 
-int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const float* w,
-                     int64_t ld_w, const float* bias, const float* score_bias, int E, float* logits,
-                     int64_t ld_l, void* stream) {
+int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
+                     int64_t ld_w, const void* bias, const float* score_bias, int E, float* logits, int64_t ld_l,
+                     void* stream) {
   FM_REQUIRE(x && w && logits, "fm_router_logits: null pointer");
   FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_router_logits: bad x dtype %d", x_dtype);
+  FM_REQUIRE(w_dtype == FM_DTYPE_BF16 || w_dtype == FM_DTYPE_F32, "fm_router_logits: bad gate dtype %d", w_dtype);
   FM_REQUIRE(E >= 1 && E <= 256, "fm_router_logits: E must be in [1, 256] (got %d)", E);
   FM_REQUIRE(D > 0 && D % 8 == 0, "fm_router_logits: D must be a positive multiple of 8 (got %lld)", (long long)D);
   FM_REQUIRE(ld_x >= D && ld_x % 8 == 0 && ld_w >= D && ld_w % 4 == 0 && ld_l >= E,
              "fm_router_logits: bad pitches");
   if (T == 0) return 0;
-  const RouterArgs a{x, ld_x, T, D, w, ld_w, bias, score_bias, E, logits, ld_l};
+  const RouterArgs a{x, ld_x, T, D, w, ld_w, bias, w_dtype == FM_DTYPE_BF16, score_bias, E, logits, ld_l};
+  return router_logits_launch(a, x_dtype, nullptr, 0, static_cast<hipStream_t>(stream), "fm_router_logits");
+}
+
+int64_t fm_router_forward_workspace_bytes(int64_t T, int E) {
+  if (T <= 0 || E <= 0) return 0;
+  const int64_t nb = (T + kRouterRows - 1) / kRouterRows;
+  const int64_t fused = nb * (int64_t(E) + 1) * 4 + nb * int64_t(E) * 4;
+  const int64_t plain = kRouterForwardWaves * (int64_t(E) + 1) * 4;
+  return fused > plain ? fused : plain;
+}
+
+int fm_router_forward(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
+                      int64_t ld_w, const void* bias, const float* score_bias, int E, int K, int gating, int flags,
+                      const void* replay_indices, int replay_i64, float* logits, int64_t ld_l, float* weights,
+                      void* indices, int indices_i64, int32_t* counts, int64_t* tokens_per_expert,
+                      int64_t* total_tokens, float z_loss_multiplier, float* loss, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  FM_REQUIRE(x && w && logits && weights && indices && counts && loss, "fm_router_forward: null pointer");
+  FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_router_forward: bad x dtype %d", x_dtype);
+  FM_REQUIRE(w_dtype == FM_DTYPE_BF16 || w_dtype == FM_DTYPE_F32, "fm_router_forward: bad gate dtype %d", w_dtype);
+  FM_REQUIRE(E >= 1 && E <= 256, "fm_router_forward: E must be in [1, 256] (got %d)", E);
+  FM_REQUIRE(K >= 1 && K <= E && K <= 64, "fm_router_forward: K must be in [1, min(E, 64)] (got %d)", K);
+  FM_REQUIRE(gating == FM_GATING_SOFTMAX || gating == FM_GATING_SIGMOID, "fm_router_forward: bad gating");
+  FM_REQUIRE((flags & ~FM_GATING_L2_NORMALIZE) == 0, "fm_router_forward: unknown flags 0x%x", flags);
+  FM_REQUIRE(D > 0 && D % 8 == 0, "fm_router_forward: D must be a positive multiple of 8 (got %lld)", (long long)D);
+  FM_REQUIRE(ld_x >= D && ld_x % 8 == 0 && ld_w >= D && ld_w % 4 == 0 && ld_l >= E,
+             "fm_router_forward: bad pitches");
+  FM_REQUIRE((tokens_per_expert == nullptr) == (total_tokens == nullptr),
+             "fm_router_forward: tokens_per_expert and total_tokens go together");
+  FM_REQUIRE(T > 0, "fm_router_forward: T must be positive (the loss divides by it)");
+  FM_REQUIRE(workspace != nullptr && workspace_bytes >= fm_router_forward_workspace_bytes(T, E),
+             "fm_router_forward: workspace of fm_router_forward_workspace_bytes(T, E) bytes required");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned rb = unsigned((T + kRouterRows - 1) / kRouterRows);
-  if (E <= 8 && 8 * D <= kGateLdsFloats && D % kRouterCols == 0) {
-    const size_t lds = size_t(8 * D) * sizeof(float);
-    if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_logits_small_kernel<uint16_t>), dim3(rb), dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((router_logits_small_kernel<float>), dim3(rb), dim3(256), lds, s, a);
-  } else if (E <= 8) {
-    const dim3 grid(rb, 1);
-    if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_logits_kernel<uint16_t, 8>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((router_logits_kernel<float, 8>), grid, dim3(256), 0, s, a);
-  } else {
-    const dim3 grid(rb, unsigned((E + 15) / 16));
-    if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_logits_kernel<uint16_t, 16>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((router_logits_kernel<float, 16>), grid, dim3(256), 0, s, a);
+  const RouterArgs a{x, ld_x, T, D, w, ld_w, bias, w_dtype == FM_DTYPE_BF16, score_bias, E, logits, ld_l};
+  const int sigmoid = gating == FM_GATING_SIGMOID;
+  const int l2 = (flags & FM_GATING_L2_NORMALIZE) ? 1 : 0;
+  const float zm = z_loss_multiplier;
+  float* base = static_cast<float*>(workspace);
+  if (router_small_ok(E, D)) {
+    const int64_t nb = (T + kRouterRows - 1) / kRouterRows;
+    float* part = base;
+    float* zpart = base + nb * E;
+    int32_t* hist = reinterpret_cast<int32_t*>(zpart + nb);
+    const RouterFuse f{GateOut{E, K, sigmoid, l2, replay_indices, replay_i64, weights, indices, indices_i64, 1},
+                       part, zm != 0.f ? zpart : nullptr, hist};
+    if (int rc = router_logits_launch(a, x_dtype, &f, 1, s, "fm_router_forward")) return rc;
+    hipLaunchKernelGGL(router_finish_kernel, dim3(1), dim3(576), 0, s, hist, nb, E, counts, tokens_per_expert,
+                       total_tokens, T, part, zm != 0.f ? zpart : nullptr, zm, loss);
+    return check_launch("fm_router_forward");
   }
-  return check_launch("fm_router_logits");
+  // other shapes: logits, then gating, counts and loss as separate kernels
+  float* part = base;
+  float* zpart = base + kRouterForwardWaves * E;
+  if (int rc = router_logits_launch(a, x_dtype, nullptr, 0, s, "fm_router_forward")) return rc;
+  if (int rc = fm_topk_gating(logits, T, E, ld_l, K, gating, flags, replay_indices, replay_i64, weights, indices,
+                              indices_i64, part, zm != 0.f ? zpart : nullptr, kRouterForwardWaves, stream))
+    return rc;
+  if (int rc = fm_expert_counts(indices, indices_i64, T * K, E, counts, tokens_per_expert, total_tokens, T, stream))
+    return rc;
+  return fm_aux_loss(part, kRouterForwardWaves, counts, E, T, zm != 0.f ? zpart : nullptr, zm, loss, stream);
 }
 
 int fm_expert_counts(const void* indices, int indices_i64, int64_t n, int E, int32_t* counts,
@@ -684,6 +978,15 @@ int fm_score_bias_update(int64_t* tokens_per_expert, int64_t* total_tokens, int 
 int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, int flags,
                    int replay, const void* indices, int indices_i64, const float* dweights, const float* daux,
                    const int32_t* counts, float z_loss_multiplier, float* dlogits, int64_t ld_d, void* stream) {
+  return fm_gating_grad_dot(logits, T, E, ld_l, K, gating, flags, replay, indices, indices_i64, dweights, nullptr, 0,
+                            nullptr, 0, nullptr, 0, nullptr, daux, counts, z_loss_multiplier, dlogits, ld_d, stream);
+}
+
+int fm_gating_grad_dot(const float* logits, int64_t T, int E, int64_t ld_l, int K, int gating, int flags, int replay,
+                       const void* indices, int indices_i64, const float* dweights, const void* dout, int64_t ld_do,
+                       const void* y, int64_t ld_y, const int32_t* row_of, int64_t D, float* dweights_out,
+                       const float* daux, const int32_t* counts, float z_loss_multiplier, float* dlogits,
+                       int64_t ld_d, void* stream) {
   FM_REQUIRE(logits && indices && dlogits, "fm_gating_grad: null pointer");
   FM_REQUIRE(E >= 1 && E <= 64 * kGateMaxPerLane, "fm_gating_grad: E must be in [1, %d] (got %d)",
              64 * kGateMaxPerLane, E);
@@ -692,57 +995,72 @@ int fm_gating_grad(const float* logits, int64_t T, int E, int64_t ld_l, int K, i
   FM_REQUIRE((flags & ~FM_GATING_L2_NORMALIZE) == 0, "fm_gating_grad: unknown flags 0x%x", flags);
   FM_REQUIRE(daux == nullptr || counts != nullptr, "fm_gating_grad: the aux-loss gradient needs counts");
   FM_REQUIRE(ld_l >= E && ld_d >= E, "fm_gating_grad: pitch < E");
+  const bool dot = dout != nullptr;
+  FM_REQUIRE(!dot || (y && row_of && dweights == nullptr), "fm_gating_grad: the fused dot needs y and row_of, "
+             "and takes no dweights");
+  FM_REQUIRE(!dot || (K <= kDotMaxK && D > 0 && D % 8 == 0 && ld_do >= D && ld_y >= D && ld_do % 8 == 0 &&
+                      ld_y % 8 == 0),
+             "fm_gating_grad: the fused dot needs K <= %d, D a positive multiple of 8 and pitches >= D (multiples "
+             "of 8)", kDotMaxK);
   if (T == 0) return 0;
   const GatingGradArgs a{logits, T, ld_l, E, K, (gating == FM_GATING_SIGMOID && !replay) ? 1 : 0,
                          (flags & FM_GATING_L2_NORMALIZE) ? 1 : 0, indices, indices_i64, dweights, daux,
-                         counts, z_loss_multiplier, dlogits, ld_d};
+                         counts, z_loss_multiplier, dlogits, ld_d, static_cast<const uint16_t*>(dout), ld_do,
+                         static_cast<const uint16_t*>(y), ld_y, row_of, D, dweights_out};
   const int64_t blocks = (T + 3) / 4 < 4096 ? (T + 3) / 4 : 4096;
-  hipLaunchKernelGGL(gating_grad_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid{unsigned(blocks)}, block{256};
+  if (!dot) hipLaunchKernelGGL(gating_grad_kernel<0>, grid, block, 0, s, a);
+  else if (K <= 2) hipLaunchKernelGGL(gating_grad_kernel<2>, grid, block, 0, s, a);
+  else if (K <= 4) hipLaunchKernelGGL(gating_grad_kernel<4>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(gating_grad_kernel<8>, grid, block, 0, s, a);
   return check_launch("fm_gating_grad");
 }
 
 int64_t fm_router_workspace_bytes(int64_t T, int64_t D, int E) {
   if (T <= 0 || D <= 0 || E <= 0) return 0;
-  return router_slices(T, D, E) * int64_t(E) * D * int64_t(sizeof(float));
+  return router_slices(T, D, E) * int64_t(E) * (D + 1) * int64_t(sizeof(float));
 }
 
 int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x_dtype, int64_t ld_x, int64_t T,
-                       int64_t D, const float* w, int64_t ld_w, int E, void* dx, int64_t ld_dx, float* dw,
-                       int64_t ld_dw, float* db, void* workspace, int64_t workspace_bytes, void* stream) {
+                       int64_t D, const void* w, int w_dtype, int64_t ld_w, int E, void* dx, int64_t ld_dx, void* dw,
+                       int dw_dtype, int64_t ld_dw, void* db, int db_dtype, void* workspace, int64_t workspace_bytes,
+                       void* stream) {
   FM_REQUIRE(dlogits && x && (w || dx == nullptr), "fm_router_backward: null pointer");
   FM_REQUIRE(x_dtype == FM_DTYPE_BF16 || x_dtype == FM_DTYPE_F32, "fm_router_backward: bad x dtype %d", x_dtype);
+  FM_REQUIRE(w_dtype == FM_DTYPE_BF16 || w_dtype == FM_DTYPE_F32, "fm_router_backward: bad gate dtype %d", w_dtype);
+  FM_REQUIRE(dw_dtype == FM_DTYPE_BF16 || dw_dtype == FM_DTYPE_F32, "fm_router_backward: bad dw dtype %d", dw_dtype);
+  FM_REQUIRE(db_dtype == FM_DTYPE_BF16 || db_dtype == FM_DTYPE_F32, "fm_router_backward: bad db dtype %d", db_dtype);
   FM_REQUIRE(E >= 1 && E <= 256, "fm_router_backward: E must be in [1, 256] (got %d)", E);
   FM_REQUIRE(D > 0 && D % 8 == 0, "fm_router_backward: D must be a positive multiple of 8");
   FM_REQUIRE(ld_dl >= E && ld_x >= D && ld_x % 8 == 0 && (w == nullptr || (ld_w >= D && ld_w % 4 == 0)),
              "fm_router_backward: bad pitches");
   FM_REQUIRE(dx == nullptr || (ld_dx >= D && ld_dx % 8 == 0), "fm_router_backward: bad dx pitch");
   FM_REQUIRE(dw == nullptr || (ld_dw >= D), "fm_router_backward: bad dw pitch");
-  if (dw != nullptr)
+  if (dw != nullptr || db != nullptr)
     FM_REQUIRE(workspace != nullptr && workspace_bytes >= fm_router_workspace_bytes(T, D, E),
                "fm_router_backward: workspace of fm_router_workspace_bytes(T, D, E) bytes required");
   if (T == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  RouterBwdArgs a{dlogits, ld_dl, x, ld_x, T, D, w, ld_w, E, dx, ld_dx, static_cast<float*>(workspace), 1, T};
+  RouterBwdArgs a{dlogits, ld_dl, x, ld_x, T, D, w, ld_w, w_dtype == FM_DTYPE_BF16, E, dx, ld_dx,
+                  static_cast<float*>(workspace), nullptr, 1, T};
   if (dx != nullptr) {
     const dim3 grid(unsigned((T + kRouterRows - 1) / kRouterRows));
     if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_dx_kernel<uint16_t>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((router_dx_kernel<float>), grid, dim3(256), 0, s, a);
     if (int rc = check_launch("fm_router_backward")) return rc;
   }
-  if (dw != nullptr) {
+  if (dw != nullptr || db != nullptr) {
     a.slices = router_slices(T, D, E);
     a.rows_per_slice = (T + a.slices - 1) / a.slices;
+    a.part_db = db != nullptr ? a.part + a.slices * int64_t(E) * D : nullptr;
     const dim3 grid(unsigned((D + kRouterCols - 1) / kRouterCols), unsigned(a.slices), unsigned((E + 7) / 8));
     if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_dw_kernel<uint16_t>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((router_dw_kernel<float>), grid, dim3(256), 0, s, a);
     if (int rc = check_launch("fm_router_backward")) return rc;
-    const int64_t n = int64_t(E) * D;
-    const unsigned rblocks = unsigned((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
-    hipLaunchKernelGGL(router_dw_reduce_kernel, dim3(rblocks), dim3(256), 0, s, a, dw, ld_dw);
-    if (int rc = check_launch("fm_router_backward")) return rc;
-  }
-  if (db != nullptr) {
-    hipLaunchKernelGGL(router_db_kernel, dim3(unsigned(E)), dim3(256), 0, s, dlogits, ld_dl, T, db);
+    const unsigned rblocks = unsigned((int64_t(E) * D + 63) / 64) + 1;
+    hipLaunchKernelGGL(router_dw_reduce_kernel, dim3(rblocks), dim3(256), 0, s, a, dw, ld_dw,
+                       int(dw_dtype == FM_DTYPE_BF16), db, int(db_dtype == FM_DTYPE_BF16));
     return check_launch("fm_router_backward");
   }
   return 0;

@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 from .recipes import BlockScalingGranularity, FP8RecipeConfig, FP8RecipeType
-from .routing import PAD_ROWS, RoutingPlan, route_tokens
+from .routing import PAD_ROWS, RouterDotInputs, RoutingPlan, route_tokens
 
 FP8_BLOCK_SIZE = 128
 MX_BLOCK_SIZE = 32
@@ -814,12 +814,15 @@ class FP8FlowMoECompute:
 
     # ----------------------------------------------------------------- backward ----
     def _backward(self, ctx, grad_out, on_router_grad=None):
-        """Gradients of the expert block.  ``on_router_grad(dw, can_fold)`` (a
-        MoE layer whose router feeds this block) is called with the
-        router-weight gradient as soon as it exists and returns the router's
-        share of the input gradient, summed in the unpermute: {"addend": bf16
-        [T, D]}, or with ``can_fold`` {"dlogits": [T, E], "gate_w": [E, D]}
-        (E <= 8) for the unpermute to form it itself."""
+        """Gradients of the expert block.  ``on_router_grad(dw, can_fold, dot)``
+        (a MoE layer whose router feeds this block) is called with the
+        router-weight gradient as soon as it exists -- or, when the hook has
+        ``fused_dot`` set and K <= 8, with ``dot`` (RouterDotInputs: the
+        upstream gradient, the saved expert outputs and the row map) for the
+        router's gating backward to form it in its own pass -- and returns the
+        router's share of the input gradient, summed in the unpermute:
+        {"addend": bf16 [T, D]}, or with ``can_fold`` {"dlogits": [T, E],
+        "gate_w": [E, D]} (E <= 8) for the unpermute to form it itself."""
         wts, GU, Y = ctx.saved_tensors
         plan = ctx.plan
         fp8_kind, use_bf16 = ctx.kinds
@@ -831,15 +834,17 @@ class FP8FlowMoECompute:
         mask = plan.use_fp8 if (fp8_kind is not None and use_bf16) else None
         # router-weight gradient from the saved expert outputs (skipped when
         # the weights need none, e.g. the constant weights of a shared expert)
-        dw = None
-        if ctx.needs_input_grad[1]:
+        dw = dot = None
+        if ctx.needs_input_grad[1] and getattr(on_router_grad, "fused_dot", False) and K <= 8 and not self._dense:
+            dot = RouterDotInputs(dO, Y, plan.row_of)
+        elif ctx.needs_input_grad[1]:
             dw = torch.empty(T * K, dtype=torch.float32, device=dev)
             _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
                       _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
         # the router's share of the input gradient: a [T, D] addend, or its
         # (dlogits, gate weight) terms folded into the unpermute
         rshare = {} if on_router_grad is None else on_router_grad(None if dw is None else dw.reshape(T, K),
-                                                                  not self._dense)
+                                                                  not self._dense, dot)
         dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
         dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         w1dt, w2dt, w3dt = ctx.wdtypes

@@ -57,6 +57,7 @@ class _MoELayerFunction(torch.autograd.Function):
         ctx.lead = lead
         ctx.x_dtype = x.dtype
         ctx.has_bias = gate_bias is not None
+        ctx.bias_dtype = None if gate_bias is None else gate_bias.dtype
         ctx.set_materialize_grads(False)
         return out.to(x.dtype).reshape(*lead, D), aux
 
@@ -69,17 +70,21 @@ class _MoELayerFunction(torch.autograd.Function):
             dout = torch.zeros(T, D, dtype=torch.bfloat16, device=x2.device)
         grads = {}
 
-        def on_router_grad(dw, can_fold):
+        def on_router_grad(dw, can_fold, dot=None):
             # E <= 8: the unpermute forms the router's share of dx from dlogits and
-            # the gate weight itself; otherwise the router's own kernel writes it
+            # the gate weight itself; otherwise the router's own kernel writes it.
+            # With `dot` the gating backward forms the router-weight gradient from
+            # the expert outputs in its own pass.
             fold = need_x and can_fold and ctx.state.logits.shape[1] <= 8
             dx_r, dW, db, dlogits = router_backward(ctx.state, x2, gate_weight, dw, daux, need_x and not fold,
-                                                    need_gw, need_gb and ctx.has_bias)
+                                                    need_gw, need_gb and ctx.has_bias, bias_dtype=ctx.bias_dtype,
+                                                    dot=dot)
             grads["gw"], grads["gb"] = dW, db
             if fold:
                 return {"dlogits": dlogits, "gate_w": gate_weight}
             return {} if dx_r is None else {"addend": dx_r}
 
+        on_router_grad.fused_dot = True
         dx, _, dW1, dW2, dW3, _, _ = ctx.layer.block._backward(ctx.bctx, dout.reshape(T, D), on_router_grad)
         ctx.bctx = None
         dx = None if not need_x else dx.to(ctx.x_dtype).reshape(*ctx.lead, D)

@@ -162,21 +162,37 @@ def _x_dtype(x: torch.Tensor) -> int:
     raise TypeError(f"router input must be bfloat16 or float32, got {x.dtype}")
 
 
+def _gate_params(gate_weight: torch.Tensor, gate_bias, score_bias):
+    """The gate weight and bias as stored (fp32 or bf16; the bias in the
+    weight's dtype, as nn.Linear keeps them) and the fp32 score bias."""
+    w = gate_weight.detach()
+    if w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.float()
+    if w.stride(-1) != 1 or w.stride(0) % 4:
+        w = w.contiguous()
+    b = None if gate_bias is None else gate_bias.detach().to(w.dtype).contiguous()
+    sb = None if score_bias is None else score_bias.detach().float().contiguous()
+    return w, b, sb
+
+
+def _dt_code(t: torch.Tensor) -> int:
+    return _lib.DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.DTYPE_F32
+
+
 def router_logits(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, score_bias=None) -> torch.Tensor:
     """fp32 logits [T, E] = x.float() @ gate_weight.T + gate_bias (+ score_bias),
-    the gate of MoERouter.forward (reference model/moe.py:151-154)."""
+    the gate of MoERouter.forward (reference model/moe.py:151-154); a bf16 gate
+    is read as stored (its values widened exactly)."""
     _lib.require_device(x, "x")
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    w = gate_weight.detach().float().contiguous()
+    w, b, sb = _gate_params(gate_weight, gate_bias, score_bias)
     E, D = w.shape
-    b = None if gate_bias is None else gate_bias.detach().float().contiguous()
-    sb = None if score_bias is None else score_bias.detach().float().contiguous()
     T = x2.shape[0]
     logits = torch.empty(T, E, dtype=torch.float32, device=x2.device)
-    _lib.call("fm_router_logits", _lib.ptr(x2), _x_dtype(x2), x2.stride(0), T, D, _lib.ptr(w), w.stride(0),
-              _lib.ptr(b), _lib.ptr(sb), E, _lib.ptr(logits), logits.stride(0), _lib.stream_of(x2))
+    _lib.call("fm_router_logits", _lib.ptr(x2), _x_dtype(x2), x2.stride(0), T, D, _lib.ptr(w), _dt_code(w),
+              w.stride(0), _lib.ptr(b), _lib.ptr(sb), E, _lib.ptr(logits), logits.stride(0), _lib.stream_of(x2))
     return logits
 
 
@@ -238,23 +254,62 @@ class RouterState:
 def router_forward(x2, gate_weight, gate_bias, score_bias, top_k, gating, replay=None, normalize=None,
                    z_mult=0.0, tracker=None):
     """Gate, gating, counts and aux loss of MoERouter.forward (reference
-    model/moe.py:133-184) on x2 [T, D]: (weights [T, K], indices [T, K], aux, state)."""
-    T = x2.shape[0]
-    logits = router_logits(x2, gate_weight, gate_bias, score_bias)
-    E = logits.shape[1]
-    w, idx, part, zpart = topk_gating(logits, top_k, gating, True, replay_indices=replay, normalize=normalize,
-                                      return_z_partial=True)
-    counts = expert_counts(idx, E, tracker)
-    aux = load_balancing_loss(part, counts, T, zpart if z_mult else None, z_mult)
+    model/moe.py:133-184) on x2 [T, D]: (weights [T, K], indices [T, K], aux, state).
+    One library call (fm_router_forward): for E <= 8 and D = 512 n <= 2048 a
+    single pass over x forms the logits, the gating, the loss partials and the
+    expert histograms, and one small kernel the counts and the loss."""
+    T, D = x2.shape
+    if T == 0:
+        raise ValueError("the router needs at least one token")
+    w_, b, sb = _gate_params(gate_weight, gate_bias, score_bias)
+    E = w_.shape[0]
+    if w_.shape[1] != D:
+        raise ValueError(f"gate_weight must be [E, {D}], got {tuple(w_.shape)}")
+    K = int(top_k)
+    dev = x2.device
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    w = torch.empty(T, K, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, K, dtype=torch.int64, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    ws = torch.empty(int(_lib.load().fm_router_forward_workspace_bytes(T, E)), dtype=torch.uint8, device=dev)
+    rep = None
+    if replay is not None:
+        rep = replay.reshape(T, K)
+        if rep.dtype not in (torch.int64, torch.int32):
+            raise TypeError("replay_indices must be int64 or int32")
+        rep = rep.contiguous()
+    acc = tot = None
+    if tracker is not None:
+        acc, tot = tracker.tokens_per_expert, tracker.total_tokens
+    _lib.call("fm_router_forward", _lib.ptr(x2), _x_dtype(x2), x2.stride(0), T, D, _lib.ptr(w_), _dt_code(w_),
+              w_.stride(0), _lib.ptr(b), _lib.ptr(sb), E, K, _gating_code(gating), _norm_flags(normalize),
+              _lib.ptr(rep), int(rep is not None and rep.dtype == torch.int64), _lib.ptr(logits), logits.stride(0),
+              _lib.ptr(w), _lib.ptr(idx), 1, _lib.ptr(counts), _lib.ptr(acc), _lib.ptr(tot), float(z_mult),
+              _lib.ptr(aux), _lib.ptr(ws), ws.numel(), _lib.stream_of(x2))
     state = RouterState(logits, idx, counts, _gating_code(gating), _norm_flags(normalize), replay is not None,
                         float(z_mult))
     return w, idx, aux, state
 
 
-def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=True, need_w=True, need_b=True):
-    """Gradients of the router (dx [T, D] in x2's dtype, dW [E, D] fp32, db [E] fp32;
-    None where not needed) from those of its weights [T, K] and aux loss, and
-    the logits' gradient dlogits [T, E] fp32 they come from."""
+@dataclass
+class RouterDotInputs:
+    """What the router-weight gradient is formed from when the gating backward
+    forms it itself: dw[t, k] = <dout[t], y[row_of[t K + k]]> (the expert
+    block's upstream gradient and its saved expert outputs, both bf16)."""
+
+    dout: torch.Tensor      # [T, D]
+    y: torch.Tensor         # [rows, D]
+    row_of: torch.Tensor    # [T * K] int32
+
+
+def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=True, need_w=True, need_b=True,
+                    bias_dtype=None, dot: RouterDotInputs = None):
+    """Gradients of the router (dx [T, D] in x2's dtype, dW [E, D] in the gate
+    weight's dtype, db [E] in ``bias_dtype`` (default fp32); None where not
+    needed) from those of its weights [T, K] (or ``dot``: formed in the gating
+    backward from the expert outputs, K <= 8) and aux loss, and the logits'
+    gradient dlogits [T, E] fp32 they come from."""
     logits, idx = state.logits, state.indices
     T, D = x2.shape
     E = logits.shape[1]
@@ -264,24 +319,30 @@ def router_backward(state: RouterState, x2, gate_weight, dweights, daux, need_x=
     dwts = None if dweights is None else dweights.reshape(T, K).float().contiguous()
     da = None if daux is None else daux.reshape(1).float().contiguous()
     dlogits = torch.empty(T, E, dtype=torch.float32, device=dev)
-    if dwts is None and da is None:
+    if dot is not None:
+        _lib.call("fm_gating_grad_dot", _lib.ptr(logits), T, E, logits.stride(0), K, state.gating, state.flags,
+                  int(state.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), None, _lib.ptr(dot.dout),
+                  dot.dout.stride(0), _lib.ptr(dot.y), dot.y.stride(0), _lib.ptr(dot.row_of), D, None, _lib.ptr(da),
+                  _lib.ptr(state.counts), state.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
+    elif dwts is None and da is None:
         dlogits.zero_()
     else:
         _lib.call("fm_gating_grad", _lib.ptr(logits), T, E, logits.stride(0), K, state.gating, state.flags,
                   int(state.replay), _lib.ptr(idx), int(idx.dtype == torch.int64), _lib.ptr(dwts), _lib.ptr(da),
                   _lib.ptr(state.counts), state.z_mult, _lib.ptr(dlogits), dlogits.stride(0), st)
-    wf = gate_weight.detach().float().contiguous() if need_x else None
+    w, _, _ = _gate_params(gate_weight, None, None)
     dx = torch.empty_like(x2) if need_x else None
-    dW = torch.empty(E, D, dtype=torch.float32, device=dev) if need_w else None
-    db = torch.empty(E, dtype=torch.float32, device=dev) if need_b else None
+    dW = torch.empty(E, D, dtype=w.dtype, device=dev) if need_w else None
+    db = torch.empty(E, dtype=bias_dtype or torch.float32, device=dev) if need_b else None
     ws = None
-    if dW is not None:
+    if dW is not None or db is not None:
         ws = torch.empty(int(_lib.load().fm_router_workspace_bytes(T, D, E)), dtype=torch.uint8, device=dev)
     if dx is not None or dW is not None or db is not None:
         _lib.call("fm_router_backward", _lib.ptr(dlogits), dlogits.stride(0), _lib.ptr(x2), _x_dtype(x2),
-                  x2.stride(0), T, D, _lib.ptr(wf), 0 if wf is None else wf.stride(0), E, _lib.ptr(dx),
-                  0 if dx is None else dx.stride(0), _lib.ptr(dW), 0 if dW is None else dW.stride(0),
-                  _lib.ptr(db), _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
+                  x2.stride(0), T, D, _lib.ptr(w), _dt_code(w), w.stride(0), E, _lib.ptr(dx),
+                  0 if dx is None else dx.stride(0), _lib.ptr(dW), _lib.DTYPE_F32 if dW is None else _dt_code(dW),
+                  0 if dW is None else dW.stride(0), _lib.ptr(db), _lib.DTYPE_F32 if db is None else _dt_code(db),
+                  _lib.ptr(ws), 0 if ws is None else ws.numel(), st)
     return dx, dW, db, dlogits
 
 
@@ -298,6 +359,7 @@ class _RouterFunction(torch.autograd.Function):
         ctx.save_for_backward(x2, gate_weight)
         ctx.state = state
         ctx.has_bias = gate_bias is not None
+        ctx.bias_dtype = None if gate_bias is None else gate_bias.dtype
         ctx.lead = lead
         ctx.mark_non_differentiable(idx)
         ctx.set_materialize_grads(False)   # no zero gradient for the indices
@@ -308,7 +370,7 @@ class _RouterFunction(torch.autograd.Function):
         x2, gate_weight = ctx.saved_tensors
         need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         dx, dW, db, _ = router_backward(ctx.state, x2, gate_weight, dweights, daux, need_x, need_w,
-                                        need_b and ctx.has_bias)
+                                        need_b and ctx.has_bias, bias_dtype=ctx.bias_dtype)
         if dx is not None:
             dx = dx.reshape(*ctx.lead, x2.shape[1])
         if dW is not None:

@@ -184,3 +184,111 @@ def test_score_bias_update_on_device(dev):
     assert int(tracker.total_tokens.item()) == 0 and int(tracker.tokens_per_expert.abs().sum().item()) == 0
     tracker.post_batch(sb, 0.01)
     assert np.array_equal(sb.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def _separate(x, w, b, sb, K, gating, replay, normalize, z_mult):
+    """The router forward as separate kernels: gate, gating, counts, loss."""
+    T, E = x.shape[0], w.shape[0]
+    logits = fm.router_logits(x, w, b, sb)
+    wts, idx, part, zpart = fm.topk_gating(logits, K, gating, True, replay_indices=replay, normalize=normalize,
+                                           return_z_partial=True)
+    counts = fm.expert_counts(idx, E)
+    aux = fm.load_balancing_loss(part, counts, T, zpart if z_mult else None, z_mult)
+    return logits, wts, idx, counts, aux
+
+
+@pytest.mark.parametrize("T,D,E,K,gating,replay,normalize,z_mult", [
+    (8192, 2048, 8, 2, "softmax", False, None, 0.0),     # configs[2]'s router: the fused pass
+    (1000, 512, 4, 2, "sigmoid", False, "l2", 1e-3),
+    (333, 1536, 8, 8, "softmax", True, None, 1e-2),
+    (77, 512, 1, 1, "softmax", False, None, 0.0),
+    (500, 256, 8, 2, "softmax", False, None, 0.0),       # D not a multiple of 512: separate kernels
+    (300, 512, 24, 4, "sigmoid", True, "l2", 1e-3),      # E > 8: separate kernels
+])
+@pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
+def test_fused_router_forward_matches_separate_kernels(dev, T, D, E, K, gating, replay, normalize, z_mult, w_dtype):
+    """fm_router_forward (one pass over x for small gates, then the counts and
+    the loss) against the same steps as separate kernels: logits, weights,
+    indices and counts bit for bit, the loss within float32 rounding of its
+    per-wave partial sums (grouped differently); the load tracker's totals."""
+    from nanopysche_amd.routing import router_forward
+
+    x, w, b, sb = _inputs(T, D, E, 7, torch.bfloat16, True)
+    x, w, b, sb = x.to(dev), w.to(w_dtype).to(dev), b.to(w_dtype).to(dev), sb.to(dev)
+    rep = None
+    if replay:
+        g = torch.Generator().manual_seed(8)
+        rep = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(dev)
+    tracker = fm.ExpertLoadTracker(E, dev)
+    wf, idxf, auxf, st = router_forward(x, w, b, sb, K, gating, rep, normalize, z_mult, tracker)
+    logits, wts, idx, counts, aux = _separate(x, w, b, sb, K, gating, rep, normalize, z_mult)
+    torch.cuda.synchronize()
+    assert torch.equal(st.logits, logits)
+    assert torch.equal(wf, wts) and torch.equal(idxf, idx)
+    assert torch.equal(st.counts, counts)
+    assert abs(float(auxf) - float(aux)) <= 1e-6 * abs(float(aux)) + 1e-12
+    assert torch.equal(tracker.tokens_per_expert, counts.long()) and int(tracker.total_tokens) == T
+    if w_dtype == torch.bfloat16:
+        # a bf16 gate is read as stored: the same logits as its fp32 widening
+        assert torch.equal(logits, fm.router_logits(x, w.float(), b.float(), sb))
+
+
+@pytest.mark.parametrize("E,K,drop", [(8, 2, False), (8, 8, True), (4, 1, False)])
+def test_gating_grad_dot_matches_separate_kernels(dev, E, K, drop):
+    """fm_gating_grad_dot (the router-weight gradient <dout[t], y[row(t,k)]>
+    formed inside the gating backward) against fm_router_weight_grad then
+    fm_gating_grad: dlogits and the weight gradient bit for bit, dropped slots
+    (row -1) included."""
+    from nanopysche_amd import _lib
+    from nanopysche_amd.routing import router_forward
+
+    T, D = 1000, 2048
+    x, w, b, _ = _inputs(T, D, E, 11, torch.bfloat16, False)
+    x, w, b = x.to(dev), w.to(dev), b.to(dev)
+    _, idx, _, st = router_forward(x, w, b, None, K, "softmax")
+    plan_idx = idx.clone()
+    if drop:
+        plan_idx[::7, 0] = E + 3       # out-of-range slots: row -1
+    plan = fm.route_tokens(plan_idx, E, 0)
+    g = torch.Generator().manual_seed(12)
+    y = (torch.randn(plan.rows_max, D, generator=g)).bfloat16().to(dev)
+    dout = (torch.randn(T, D, generator=g) * 1e-2).bfloat16().to(dev)
+    daux = torch.tensor(0.3, device=dev)
+    dw = torch.empty(T * K, dtype=torch.float32, device=dev)
+    _lib.call("fm_router_weight_grad", _lib.ptr(dout), D, _lib.ptr(y), D, _lib.ptr(plan.row_of), T, K, D,
+              _lib.ptr(dw), _lib.stream_of(dout))
+    dl1 = torch.empty(T, E, dtype=torch.float32, device=dev)
+    _lib.call("fm_gating_grad", _lib.ptr(st.logits), T, E, E, K, st.gating, st.flags, 0, _lib.ptr(idx), 1,
+              _lib.ptr(dw), _lib.ptr(daux), _lib.ptr(st.counts), 0.0, _lib.ptr(dl1), E, _lib.stream_of(dout))
+    dl2 = torch.empty_like(dl1)
+    dw2 = torch.empty_like(dw)
+    _lib.call("fm_gating_grad_dot", _lib.ptr(st.logits), T, E, E, K, st.gating, st.flags, 0, _lib.ptr(idx), 1,
+              None, _lib.ptr(dout), D, _lib.ptr(y), D, _lib.ptr(plan.row_of), D, _lib.ptr(dw2), _lib.ptr(daux),
+              _lib.ptr(st.counts), 0.0, _lib.ptr(dl2), E, _lib.stream_of(dout))
+    torch.cuda.synchronize()
+    assert torch.equal(dw, dw2) and torch.equal(dl1, dl2)
+    if drop:
+        assert torch.all(dw2.reshape(T, K)[::7, 0] == 0)
+
+
+def test_router_backward_writes_parameter_dtypes(dev):
+    """dW and db come out in the gate's own dtype: for a bf16 gate, the
+    fp32 sums rounded once (equal to the fp32 result rounded to bf16)."""
+    from nanopysche_amd.routing import router_backward, router_forward
+
+    T, D, E, K = 2000, 1024, 8, 2
+    x, w, b, _ = _inputs(T, D, E, 13, torch.bfloat16, False)
+    w, b = w.bfloat16().float(), b.bfloat16().float()   # the same values in both dtypes
+    x = x.to(dev)
+    daux = torch.tensor(1.0, device=dev)
+    dws = torch.randn(T, K, generator=torch.Generator().manual_seed(14)).to(dev)
+    out = {}
+    for dt in (torch.float32, torch.bfloat16):
+        wd, bd = w.to(dt).to(dev), b.to(dt).to(dev)
+        _, _, _, st = router_forward(x, wd.float(), bd.float(), None, K, "softmax")
+        _, dW, db, _ = router_backward(st, x, wd, dws, daux, need_x=False, bias_dtype=dt)
+        out[dt] = (dW, db)
+    torch.cuda.synchronize()
+    assert out[torch.bfloat16][0].dtype == torch.bfloat16 and out[torch.bfloat16][1].dtype == torch.bfloat16
+    assert torch.equal(out[torch.bfloat16][0], out[torch.float32][0].bfloat16())
+    assert torch.equal(out[torch.bfloat16][1], out[torch.float32][1].bfloat16())
