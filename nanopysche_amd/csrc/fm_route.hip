@@ -520,29 +520,39 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* y
                                                                const WT* W, int64_t ld_w, int E, int64_t tpb) {
   const int64_t c = int64_t(blockIdx.x) * 2048 + threadIdx.x * 8;
   if (c >= D) return;
-  float wr[8][8];
+  // the gate's columns of this thread for the 8 experts, kept as stored
+  // (bf16 packed in 32 registers, widened where used; fp32 in 64)
+  constexpr int WW = sizeof(WT) == 2 ? 4 : 8;
+  uint32_t wr[8][WW];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     if (e < E) {
-      if constexpr (sizeof(WT) == 4) {
-        const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + e * ld_w + c);
-        const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(W) + e * ld_w + c + 4);
-        wr[e][0] = a.x; wr[e][1] = a.y; wr[e][2] = a.z; wr[e][3] = a.w;
-        wr[e][4] = b.x; wr[e][5] = b.y; wr[e][6] = b.z; wr[e][7] = b.w;
-      } else {
-        const uint4 pk = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(W) + e * ld_w + c);
-        const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
+      const uint4* p = reinterpret_cast<const uint4*>(W + e * ld_w + c);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          wr[e][2 * j] = u2f(q[j] << 16);
-          wr[e][2 * j + 1] = u2f(q[j] & 0xffff0000u);
-        }
+      for (int h = 0; h < WW / 4; ++h) {
+        const uint4 q = p[h];
+        wr[e][4 * h] = q.x; wr[e][4 * h + 1] = q.y; wr[e][4 * h + 2] = q.z; wr[e][4 * h + 3] = q.w;
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) wr[e][j] = 0.f;
+      for (int j = 0; j < WW; ++j) wr[e][j] = 0u;
     }
   }
+  auto w_row = [&](int e, float (&v)[8]) {
+    if constexpr (sizeof(WT) == 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // opaque to the optimiser, so the widening stays here instead of being
+        // hoisted out of the token loop into 64 live registers
+        asm volatile("" : "+v"(wr[e][j]));
+        v[2 * j] = u2f(wr[e][j] << 16);
+        v[2 * j + 1] = u2f(wr[e][j] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = u2f(wr[e][j]);
+    }
+  };
   const int64_t t0 = int64_t(blockIdx.y) * tpb;
   const int64_t t1 = t0 + tpb < T ? t0 + tpb : T;
   for (int64_t tb = t0; tb < t1; tb += 4) {
@@ -563,8 +573,15 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* y
           sw[u][k] = w ? w[t * KC + k] : 1.f;
         }
       }
+      if (E == 8 && ld_dl % 4 == 0) {   // the token's 8 dlogits as two 16-byte loads
+        const float4 p0 = *reinterpret_cast<const float4*>(dl + t * ld_dl);
+        const float4 p1 = *reinterpret_cast<const float4*>(dl + t * ld_dl + 4);
+        d[u][0] = p0.x; d[u][1] = p0.y; d[u][2] = p0.z; d[u][3] = p0.w;
+        d[u][4] = p1.x; d[u][5] = p1.y; d[u][6] = p1.z; d[u][7] = p1.w;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d[u][e] = e < E ? dl[t * ld_dl + e] : 0.f;
+        for (int e = 0; e < 8; ++e) d[u][e] = e < E ? dl[t * ld_dl + e] : 0.f;
+      }
       if (addend) {
         const uint4 pk = *reinterpret_cast<const uint4*>(addend + t * ld_add + c);
         const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
@@ -600,13 +617,19 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* y
         }
       }
     }
+    // router term: sum over experts in expert order, after the slots' sum
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float wv[8];
+      w_row(e, wv);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[u][j] = fmaf(d[u][e], wv[j], acc[u][j]);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (tb + u >= t1) break;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[u][j] = fmaf(d[u][e], wr[e][j], acc[u][j]);
       const int64_t t = tb + u;
       if (out_f32) {
         float* o = static_cast<float*>(out) + t * ld_out + c;

@@ -21,6 +21,8 @@
 // its size and the FMAs run on the VALU in fp32, as the reference computes it;
 // HBM, not arithmetic, bounds it at the layer's shapes.  Gate weights are
 // read as stored (fp32 or bf16).
+#include <type_traits>
+
 #include "fm_gating.h"
 #include "../../include/fm_hip.h"
 
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(RouterArgs a) {
 // floats, at most 64 KiB: two workgroups per CU), staged once, and each wave
 // walks its 4 rows over D with the next 512-column chunk of x already in
 // flight (no barrier inside the loop).
-constexpr int kGateLdsFloats = 16 * 1024;
+constexpr int kGateLdsBytes = 64 * 1024;
 
 // Sum of v[i] over the 64 lanes for 32 values per lane as a reduce-scatter:
 // each exchange halves the values a lane keeps (32 shuffles in all, against
@@ -214,13 +216,22 @@ __device__ __forceinline__ void bf16x8_to_f32(const uint4 u, float (&v)[8]) {
 }
 
 // acc[row][expert] += x chunk (8 values of each of 4 rows) . gate chunk
-__device__ __forceinline__ void router_fma_chunk(float (&acc)[32], const float (&xv)[4][8], const float* wc,
+// acc[row][expert] += x chunk (8 values of each of 4 rows) . gate chunk; the
+// gate in LDS as fp32 or as the bf16 it was stored in (widened here, exactly)
+template <typename WL>
+__device__ __forceinline__ void router_fma_chunk(float (&acc)[32], const float (&xv)[4][8], const WL* wc,
                                                  int64_t D) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float4 w0 = *reinterpret_cast<const float4*>(wc + e * D);
-    const float4 w1 = *reinterpret_cast<const float4*>(wc + e * D + 4);
-    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float wv[8];
+    if constexpr (sizeof(WL) == 2) {
+      bf16x8_to_f32(*reinterpret_cast<const uint4*>(wc + e * D), wv);
+    } else {
+      const float4 w0 = *reinterpret_cast<const float4*>(wc + e * D);
+      const float4 w1 = *reinterpret_cast<const float4*>(wc + e * D + 4);
+      wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+      wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -240,9 +251,10 @@ struct RouterFuse {
   int32_t* block_hist;   // [E, gridDim.x]
 };
 
-template <typename T, bool FUSED>
+template <typename T, typename WL, bool FUSED>
 __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, RouterFuse f) {
-  extern __shared__ __attribute__((aligned(16))) float wl[];   // [8][D]
+  extern __shared__ __attribute__((aligned(16))) uint4 wl_raw[];
+  WL* wl = reinterpret_cast<WL*>(wl_raw);   // [8][D]: fp32, or the bf16 gate as stored
   __shared__ int32_t hist[8];
   __shared__ float wpart[4][9];   // per wave: softmax sums of experts 0..7, logsumexp^2
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -258,23 +270,49 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, 
     rows[r] = static_cast<const T*>(a.x) + row * a.ld_x + lane * 8;
   }
   // bf16 rows of at most 2048 columns: all of this wave's x loads are issued
-  // before the gate staging, so the two memory latencies overlap and the
-  // chunk loop waits on none
+  // right after the gate's loads and before the gate's LDS stores, so the
+  // stores wait only for the gate (loads complete in issue order) and the two
+  // memory latencies overlap; the chunk loop then waits on none
   constexpr bool kWhole = sizeof(T) == 2;
   const bool whole = kWhole && nc <= 4;
   uint4 xr[4][4];
-  if (whole) {
+  auto load_x = [&]() {
+    if (whole) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (c < nc) xr[c][r] = *reinterpret_cast<const uint4*>(rows[r] + int64_t(c) * kRouterCols);
-  }
-  {
+        for (int r = 0; r < 4; ++r)
+          if (c < nc) xr[c][r] = *reinterpret_cast<const uint4*>(rows[r] + int64_t(c) * kRouterCols);
+    }
+  };
+  if constexpr (sizeof(WL) == 2) {
+    // the bf16 gate copied as stored: 8 rows of D <= 4096 over 256 threads, at
+    // most two 16-byte pieces per thread and row, all loads before the stores
+    constexpr int kPerRow = kGateLdsBytes / 8 / 16 / 256;
+    uint4 v[8][kPerRow];
+    const int Di = int(D);
+    const uint16_t* w = static_cast<const uint16_t*>(a.w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int u = 0; u < kPerRow; ++u) {
+        const int c = (int(threadIdx.x) + 256 * u) * 8;
+        v[e][u] = make_uint4(0, 0, 0, 0);
+        if (c < Di && e < a.E) v[e][u] = *reinterpret_cast<const uint4*>(w + e * a.ld_w + c);
+      }
+    load_x();
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int u = 0; u < kPerRow; ++u) {
+        const int c = (int(threadIdx.x) + 256 * u) * 8;
+        if (c < Di) *reinterpret_cast<uint4*>(&wl[e * Di + c]) = v[e][u];
+      }
+  } else {
     // 8 gate rows of D <= 2048 floats over 256 threads: per row at most two
     // float4 per thread (expert x column loop, no index division), all loads
     // issued before the stores
-    constexpr int kPerRow = kGateLdsFloats / 8 / 1024;
+    constexpr int kPerRow = kGateLdsBytes / 4 / 8 / 1024;
     float4 v[8][kPerRow];
     const int Di = int(D);
 #pragma unroll
@@ -285,6 +323,7 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, 
         v[e][u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < Di && e < a.E) v[e][u] = ldw4(a.w, a.w_bf16, e * a.ld_w + c);
       }
+    load_x();
 #pragma unroll
     for (int e = 0; e < 8; ++e)
 #pragma unroll
@@ -707,19 +746,26 @@ __global__ __launch_bounds__(256) void router_dx_kernel(RouterBwdArgs a) {
   }
 }
 
-// Partial dw: grid (ceil(D / 512), slices, ceil(E / 8)); the slice's rows are
+// Partial dw: grid (ceil(D / 256), slices, ceil(E / 8)); the slice's rows are
 // split over the 4 waves (row t of the slice to wave t % 4), lane l owns
-// columns 8 l .. of the chunk for 8 experts; each wave issues the loads of
-// eight of its rows before their FMAs (row order kept), and the 4 waves'
-// sums meet in LDS in a fixed order.  The workgroups of column chunk 0 also
-// form the slice's db partial (each wave's rows in order, then waves 0..3).
+// columns 4 l .. 4 l + 3 of the workgroup's 256 for 8 experts (narrow
+// columns: twice the workgroups for the same partials).  Each wave issues
+// the loads of eight of its rows before their FMAs (row order kept): x stays
+// packed in registers, and the dlogits of a row -- the same for every lane --
+// come as two 16-byte loads of a wave-uniform address.  The 4 waves' sums meet
+// in one 4 KiB LDS buffer in wave order (wave 0 writes, waves 1, 2, 3 add).
+// The workgroups of column block 0 also form the slice's db partial (each
+// wave's rows in order, then waves 0..3).
+constexpr int kDwCols = 256;
+
 template <typename T>
 __global__ __launch_bounds__(256) void router_dw_kernel(RouterBwdArgs a) {
   constexpr int EG = 8, RB = 8;
-  __shared__ __attribute__((aligned(16))) float red[4][EG][kRouterCols];
+  __shared__ __attribute__((aligned(16))) float red[EG][kDwCols];
   __shared__ float dbred[4][EG];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t col = int64_t(blockIdx.x) * kRouterCols + lane * 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int64_t col = int64_t(blockIdx.x) * kDwCols + lane * 4;
   const int64_t s = blockIdx.y;
   const int e0 = blockIdx.z * EG;
   const bool want_db = a.part_db != nullptr && blockIdx.x == 0;
@@ -728,55 +774,90 @@ __global__ __launch_bounds__(256) void router_dw_kernel(RouterBwdArgs a) {
   const T* x = static_cast<const T*>(a.x);
   const bool cv = col < a.D;
   const int64_t cl = cv ? col : 0;   // rows are read in full; columns past D are not stored
-  float acc[EG][8], dbacc[EG];
+  const bool full8 = e0 + EG <= a.E && a.ld_dl % 4 == 0;
+  using Raw = typename std::conditional<sizeof(T) == 2, uint2, float4>::type;
+  float acc[EG][4], dbacc[EG];
 #pragma unroll
   for (int e = 0; e < EG; ++e) {
     dbacc[e] = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[e][j] = 0.f;
+    for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
   }
-  int64_t t = t_lo + wave;
-  for (; t + 4 * (RB - 1) < t_hi; t += 4 * RB) {
-    float xv[RB][8], dv[RB][EG];
+  auto dl_row = [&](int64_t t, float (&d)[EG]) {
+    const float* p = a.dl + t * a.ld_dl + e0;
+    if (full8) {
+      const float4 v0 = *reinterpret_cast<const float4*>(p);
+      const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
+      d[0] = v0.x; d[1] = v0.y; d[2] = v0.z; d[3] = v0.w;
+      d[4] = v1.x; d[5] = v1.y; d[6] = v1.z; d[7] = v1.w;
+    } else {
 #pragma unroll
-    for (int u = 0; u < RB; ++u) {
-      load8f(x + (t + 4 * u) * a.ld_x + cl, xv[u]);
-#pragma unroll
-      for (int e = 0; e < EG; ++e) dv[u][e] = e0 + e < a.E ? a.dl[(t + 4 * u) * a.ld_dl + e0 + e] : 0.f;
+      for (int e = 0; e < EG; ++e) d[e] = e0 + e < a.E ? p[e] : 0.f;
     }
-#pragma unroll
-    for (int u = 0; u < RB; ++u)
-#pragma unroll
-      for (int e = 0; e < EG; ++e) {
-        dbacc[e] += dv[u][e];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(dv[u][e], xv[u][j], acc[e][j]);
-      }
-  }
-  for (; t < t_hi; t += 4) {
-    float xv[8];
-    load8f(x + t * a.ld_x + cl, xv);
+  };
+  auto widen4 = [](const Raw& r, float (&v)[4]) {
+    if constexpr (sizeof(T) == 2) {
+      const uint2 u = *reinterpret_cast<const uint2*>(&r);
+      v[0] = u2f(u.x << 16); v[1] = u2f(u.x & 0xffff0000u);
+      v[2] = u2f(u.y << 16); v[3] = u2f(u.y & 0xffff0000u);
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>(&r);
+      v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    }
+  };
+  auto row_fma = [&](const float (&xv)[4], const float (&d)[EG]) {
 #pragma unroll
     for (int e = 0; e < EG; ++e) {
-      const float d = e0 + e < a.E ? a.dl[t * a.ld_dl + e0 + e] : 0.f;
-      dbacc[e] += d;
+      dbacc[e] += d[e];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[e][j] = fmaf(d, xv[j], acc[e][j]);
+      for (int j = 0; j < 4; ++j) acc[e][j] = fmaf(d[e], xv[j], acc[e][j]);
+    }
+  };
+  int64_t t = t_lo + wave;
+  for (; t + 4 * (RB - 1) < t_hi; t += 4 * RB) {
+    Raw xr[RB];
+    float dv[RB][EG];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      xr[u] = *reinterpret_cast<const Raw*>(x + (t + 4 * u) * a.ld_x + cl);
+      dl_row(t + 4 * u, dv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      float xv[4];
+      widen4(xr[u], xv);
+      row_fma(xv, dv[u]);
     }
   }
-#pragma unroll
-  for (int e = 0; e < EG; ++e)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) red[wave][e][lane * 8 + j] = acc[e][j];
+  for (; t < t_hi; t += 4) {
+    float xv[4], d[EG];
+    widen4(*reinterpret_cast<const Raw*>(x + t * a.ld_x + cl), xv);
+    dl_row(t, d);
+    row_fma(xv, d);
+  }
   if (want_db && lane == 0)
 #pragma unroll
     for (int e = 0; e < EG; ++e) dbred[wave][e] = dbacc[e];
-  __syncthreads();
-  for (int i = threadIdx.x; i < EG * kRouterCols; i += 256) {
-    const int e = i / kRouterCols, c = i % kRouterCols;
-    const int64_t gc = int64_t(blockIdx.x) * kRouterCols + c;
+  // ((w0 + w1) + w2) + w3 through one buffer
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int e = 0; e < EG; ++e) {
+        float4* p = reinterpret_cast<float4*>(&red[e][lane * 4]);
+        float4 q = w == 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : *p;
+        if (w == 0) q = make_float4(acc[e][0], acc[e][1], acc[e][2], acc[e][3]);
+        else { q.x += acc[e][0]; q.y += acc[e][1]; q.z += acc[e][2]; q.w += acc[e][3]; }
+        *p = q;
+      }
+    }
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < EG * kDwCols / 4; i += 256) {
+    const int e = i / (kDwCols / 4), c = (i % (kDwCols / 4)) * 4;
+    const int64_t gc = int64_t(blockIdx.x) * kDwCols + c;
     if (e0 + e < a.E && gc < a.D)
-      a.part[(s * a.E + e0 + e) * a.D + gc] = ((red[0][e][c] + red[1][e][c]) + red[2][e][c]) + red[3][e][c];
+      *reinterpret_cast<float4*>(a.part + (s * a.E + e0 + e) * a.D + gc) =
+          *reinterpret_cast<const float4*>(&red[e][c]);
   }
   if (want_db && threadIdx.x < EG && e0 + int(threadIdx.x) < a.E) {
     const int e = threadIdx.x;
@@ -830,23 +911,30 @@ __global__ __launch_bounds__(256) void router_dw_reduce_kernel(RouterBwdArgs a, 
 // separate kernels (their gating uses this many waves of partials).
 constexpr int64_t kRouterForwardWaves = 1024;
 
-inline bool router_small_ok(int E, int64_t D) { return E <= 8 && 8 * D <= kGateLdsFloats && D % kRouterCols == 0; }
+// the small-gate kernel: E <= 8, D = 512 n, the gate [8, D] in at most 64 KiB of LDS (fp32: D <= 2048;
+// a bf16 gate stays bf16: D <= 4096)
+inline bool router_small_ok(int E, int64_t D, int w_bf16) {
+  return E <= 8 && D % kRouterCols == 0 && 8 * D * (w_bf16 ? 2 : 4) <= kGateLdsBytes;
+}
 
 int router_logits_launch(const RouterArgs& a, int x_dtype, const RouterFuse* f, int fused, hipStream_t s,
                          const char* what) {
   const unsigned rb = unsigned((a.T + kRouterRows - 1) / kRouterRows);
   const bool xb = x_dtype == FM_DTYPE_BF16;
-  if (router_small_ok(a.E, a.D)) {
-    const size_t lds = size_t(8 * a.D) * sizeof(float);
+  if (router_small_ok(a.E, a.D, a.w_bf16)) {
+    const size_t lds = size_t(8 * a.D) * (a.w_bf16 ? 2 : 4);
     const RouterFuse none{};
     const RouterFuse& ff = f ? *f : none;
+    const dim3 g(rb), b(256);
+#define FM_SMALL(XT, WL, FU) hipLaunchKernelGGL((router_logits_small_kernel<XT, WL, FU>), g, b, lds, s, a, ff)
     if (fused) {
-      if (xb) hipLaunchKernelGGL((router_logits_small_kernel<uint16_t, true>), dim3(rb), dim3(256), lds, s, a, ff);
-      else hipLaunchKernelGGL((router_logits_small_kernel<float, true>), dim3(rb), dim3(256), lds, s, a, ff);
+      if (a.w_bf16) { if (xb) FM_SMALL(uint16_t, uint16_t, true); else FM_SMALL(float, uint16_t, true); }
+      else { if (xb) FM_SMALL(uint16_t, float, true); else FM_SMALL(float, float, true); }
     } else {
-      if (xb) hipLaunchKernelGGL((router_logits_small_kernel<uint16_t, false>), dim3(rb), dim3(256), lds, s, a, ff);
-      else hipLaunchKernelGGL((router_logits_small_kernel<float, false>), dim3(rb), dim3(256), lds, s, a, ff);
+      if (a.w_bf16) { if (xb) FM_SMALL(uint16_t, uint16_t, false); else FM_SMALL(float, uint16_t, false); }
+      else { if (xb) FM_SMALL(uint16_t, float, false); else FM_SMALL(float, float, false); }
     }
+#undef FM_SMALL
   } else if (a.E <= 8) {
     const dim3 grid(rb, 1);
     if (xb) hipLaunchKernelGGL((router_logits_kernel<uint16_t, 8>), grid, dim3(256), 0, s, a);
@@ -925,7 +1013,7 @@ int fm_router_forward(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64
   const int l2 = (flags & FM_GATING_L2_NORMALIZE) ? 1 : 0;
   const float zm = z_loss_multiplier;
   float* base = static_cast<float*>(workspace);
-  if (router_small_ok(E, D)) {
+  if (router_small_ok(E, D, w_dtype == FM_DTYPE_BF16)) {
     const int64_t nb = (T + kRouterRows - 1) / kRouterRows;
     float* part = base;
     float* zpart = base + nb * E;
@@ -1054,7 +1142,7 @@ int fm_router_backward(const float* dlogits, int64_t ld_dl, const void* x, int x
     a.slices = router_slices(T, D, E);
     a.rows_per_slice = (T + a.slices - 1) / a.slices;
     a.part_db = db != nullptr ? a.part + a.slices * int64_t(E) * D : nullptr;
-    const dim3 grid(unsigned((D + kRouterCols - 1) / kRouterCols), unsigned(a.slices), unsigned((E + 7) / 8));
+    const dim3 grid(unsigned((D + kDwCols - 1) / kDwCols), unsigned(a.slices), unsigned((E + 7) / 8));
     if (x_dtype == FM_DTYPE_BF16) hipLaunchKernelGGL((router_dw_kernel<uint16_t>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((router_dw_kernel<float>), grid, dim3(256), 0, s, a);
     if (int rc = check_launch("fm_router_backward")) return rc;
