@@ -775,6 +775,17 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
 // Per-lane values (expert x = lane: tile count, inclusive scan, offsets) live
 // in the wave's own 1 KiB of LDS between tiles, so they cost no registers
 // across the K loop.
+// The lane id read from the hardware (v_mbcnt) at each use.  Volatile, so the
+// compiler neither hoists nor shares it: values derived from the lane between
+// tiles are rebuilt from it instead of being kept live across the K loops,
+// where the register budget is spent (a spilled value's reload waits for
+// every load in flight, the operand prefetch included).
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 struct TileQueue {
   int* lds;                    // [4][64] ints of this wave
   int NI, JT, n_valid, per_xcd, xcd, c0, nbx;
@@ -824,7 +835,7 @@ __device__ __forceinline__ bool tile_queue_get(const TileQueue& q, int m, TileP&
   const int gsz = q.JT - first < kGroupM ? q.JT - first : kGroupM;
   const int J = first + (L % gsz);
   t.i0 = ((L % (kGroupM * q.NI)) / gsz) * kT;
-  const int lane = threadIdx.x & 63;
+  const int lane = fresh_lane();
   const int cnt = q.lds[lane], incl = q.lds[64 + lane];
   const unsigned long long hit = __ballot(cnt > 0 && J >= incl - cnt && J < incl);
   if (hit == 0) return false;
@@ -849,11 +860,12 @@ __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Oper
   TileStreams s;
   const int64_t q_rows = n_i - t.i0 < kT ? n_i - t.i0 : kT;
   const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
-  s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, w.lane, w.wave);
-  s.p = make_stream(P.p + int64_t(t.j0) * P.ld * ES, P.ld * ES, p_rows, w.lane, w.wave);
+  const int lane = fresh_lane();
+  s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, lane, w.wave);
+  s.p = make_stream(P.p + int64_t(t.j0) * P.ld * ES, P.ld * ES, p_rows, lane, w.wave);
   s.sc = ScaleSrc{};
   if constexpr (SM::kScaled) {
-    const int li = (w.wave & 3) * 64 + w.lane;
+    const int li = (w.wave & 3) * 64 + lane;
     s.sc = w.wave < 4 ? make_scale_src<KIND>(Q, t.i0, q_rows, t.e, w.q_mx_k, li, SM::kQS)
                       : make_scale_src<KIND>(P, t.j0, p_rows, 0, w.p_mx_k, li, SM::kPS);
   }
@@ -1007,10 +1019,14 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
     const int64_t ib = cur.i0 + w.wi * 128, jb = cur.j0 + w.wj * 64;
     const int p_rows = cur.j_end - cur.j0 < kT ? cur.j_end - cur.j0 : kT;
     if (ib < p.n_i && jb < cur.j0 + p_rows) {
+      WaveCoord we = w;
+      we.lane = fresh_lane();
+      we.lrow = we.lane & 31;
+      we.lhalf = we.lane >> 5;
       if (!p.out_f32) {
-        store_bf16_passes(acc, W, static_cast<uint16_t*>(p.C), p.ldC, jb, ib, w);
+        store_bf16_passes(acc, W, static_cast<uint16_t*>(p.C), p.ldC, jb, ib, we);
       } else {
-        float* dst = static_cast<float*>(p.C) + jb * p.ldC + ib + w.lrow * p.ldC + 4 * w.lhalf;
+        float* dst = static_cast<float*>(p.C) + jb * p.ldC + ib + we.lrow * p.ldC + 4 * we.lhalf;
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
