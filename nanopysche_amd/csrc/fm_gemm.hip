@@ -38,7 +38,12 @@
 //                   promoted through a second set of accumulator registers.
 // Ragged-M workgroup ids are remapped so each XCD walks a contiguous range of
 // the valid tiles, grouped 8 token tiles at a time for L2 reuse of weights and
-// activations; ragged-K tiles keep launch order (balances uneven experts).
+// activations; within a group the weight tiles vary fastest, so the workgroups
+// running together share a few token tiles and cover all the weight tiles: a
+// weight tile is fetched from HBM in the first round only, while the token
+// operand, written by the kernel just before, is cached in every round.
+// Ragged-K tiles keep launch order (balances uneven experts) unless the
+// experts are balanced (contiguous XCD ranges, see decode_tile256).
 #include <atomic>
 #include <cstdlib>
 
@@ -87,6 +92,7 @@ struct GemmParams {
   int rk_xcd;         // ragged-K, 256 x 256 kernel: allow the contiguous XCD split
   int splits;         // ragged-K, 256 x 256 kernel: K slices per tile (>1: fp32 partials, C = workspace)
   int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
+  int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
 };
 
 constexpr int kGroupM = 8;
@@ -539,8 +545,9 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
     const int64_t group = L / (kGroupM * NI);
     const int64_t first = group * kGroupM;
     const int64_t gsz = JT - first < kGroupM ? JT - first : kGroupM;
-    int64_t J = first + (L % gsz);
-    t.i0 = ((L % (kGroupM * NI)) / gsz) * kT;
+    const int64_t rem = L - group * kGroupM * NI;   // < gsz * NI
+    int64_t J = first + (p.w_fast ? rem / NI : rem % gsz);
+    t.i0 = (p.w_fast ? rem % NI : rem / gsz) * kT;
     // token tile J -> (expert, rows): an unmasked expert x holds
     // ceil(rows_x / 256) tiles
     if (wide) {
@@ -788,7 +795,7 @@ __device__ __forceinline__ int fresh_lane() {
 
 struct TileQueue {
   int* lds;                    // [4][64] ints of this wave
-  int NI, JT, n_valid, per_xcd, xcd, c0, nbx;
+  int NI, JT, n_valid, per_xcd, xcd, c0, nbx, w_fast;
 };
 
 // A tile of the persistent kernel: expert, first weight row, first token row,
@@ -822,6 +829,7 @@ __device__ __forceinline__ void tile_queue_init(const GemmParams& p, TileQueue& 
   q.xcd = int(blockIdx.x % 8);
   q.c0 = int(blockIdx.x / 8);
   q.nbx = int(gridDim.x / 8);
+  q.w_fast = p.w_fast;
 }
 
 // The m-th tile of this workgroup, false past the end of its share.
@@ -833,8 +841,9 @@ __device__ __forceinline__ bool tile_queue_get(const TileQueue& q, int m, TileP&
   const int group = L / (kGroupM * q.NI);
   const int first = group * kGroupM;
   const int gsz = q.JT - first < kGroupM ? q.JT - first : kGroupM;
-  const int J = first + (L % gsz);
-  t.i0 = ((L % (kGroupM * q.NI)) / gsz) * kT;
+  const int rem = L - group * kGroupM * q.NI;   // < gsz * NI
+  const int J = first + (q.w_fast ? rem / q.NI : rem % gsz);
+  t.i0 = (q.w_fast ? rem % q.NI : rem / gsz) * kT;
   const int lane = fresh_lane();
   const int cnt = q.lds[lane], incl = q.lds[64 + lane];
   const unsigned long long hit = __ballot(cnt > 0 && J >= incl - cnt && J < incl);
@@ -1327,6 +1336,16 @@ inline bool gemm_persistent() {
   return on;
 }
 
+// Ragged-M tiles take the weight tiles fastest within a group of token tiles
+// unless FM_GEMM_ORDER=t (token tiles fastest; read once).
+inline bool gemm_weight_fast() {
+  static const bool on = [] {
+    const char* e = getenv("FM_GEMM_ORDER");
+    return e == nullptr || e[0] != 't';
+  }();
+  return on;
+}
+
 // Compute units of the current device (cached per device).
 inline int device_cus() {
   static std::atomic<int> cache[64];
@@ -1406,6 +1425,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   }
   if (p.n_tiles == 0) return 0;
   p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
+  p.w_fast = gemm_weight_fast() ? 1 : 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
