@@ -8,7 +8,7 @@
 //                         the backward -- all from one read of x
 //   fm_rmsnorm_backward   dx = r g - (r^3 / D) (sum_j g_j x_j) x with g = dy w,
 //                         and dw = sum_t dy x r (fp32, per-slice partials in a
-//                         caller workspace summed in slice order)
+//                         caller workspace summed in a fixed order)
 // One wave64 owns a row: the row (D = 512 n <= 8192) sits in registers, lane l
 // holding columns 512 c + 8 l .. +8, so the sum of squares is one wave
 // reduction and each 128-column block (32-column MX block) is the 16 (4)
@@ -316,11 +316,11 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_split_kernel(NormBwdArgs a) {
   }
 }
 
-// dw from the slices' partial rows [slices, D], summed in slice order in two
-// levels: group g adds slices 16 g .. 16 g + 15 (one wave per 256 columns and
-// group), then the group sums are added in group order.  With one group the
-// first level writes dw.
-constexpr int kDwGroup = 16;
+// dw from the slices' partial rows [slices, D], summed in a fixed order in two
+// levels: group g adds slices 32 g .. 32 g + 31 (one wave per 256 columns and
+// group), then the group sums are added in four consecutive runs whose totals
+// are added in run order.  With one group the first level writes dw.
+constexpr int kDwGroup = 32;
 
 __device__ __forceinline__ void store_dw4(void* dw, int dw_f32, int64_t col, const float4& t) {
   if (dw_f32) {
@@ -354,16 +354,23 @@ __global__ __launch_bounds__(64) void rmsnorm_dw_groups_kernel(const float* part
   else *reinterpret_cast<float4*>(groups + int64_t(blockIdx.y) * D + col) = t;
 }
 
-__global__ __launch_bounds__(64) void rmsnorm_dw_final_kernel(const float* groups, int n_groups, int64_t D, void* dw,
-                                                              int dw_f32) {
-  const int64_t col = int64_t(blockIdx.x) * 256 + threadIdx.x * 4;
+// Second level: four waves per 256 columns, wave w summing groups
+// [w q, (w + 1) q) (q = ceil(groups / 4)) in runs of eight loads, the four
+// wave sums then added in wave order.
+__global__ __launch_bounds__(256) void rmsnorm_dw_final_kernel(const float* groups, int n_groups, int64_t D, void* dw,
+                                                               int dw_f32) {
+  __shared__ float4 wsum[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t col = int64_t(blockIdx.x) * 256 + lane * 4;
+  const int q = (n_groups + 3) / 4;
+  const int g_lo = wave * q, g_hi = g_lo + q < n_groups ? g_lo + q : n_groups;
   float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int g0 = 0; g0 < n_groups; g0 += 8) {
+  for (int g0 = g_lo; g0 < g_hi; g0 += 8) {
     float4 v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      v[i] = g0 + i < n_groups ? *reinterpret_cast<const float4*>(groups + int64_t(g0 + i) * D + col)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[i] = g0 + i < g_hi ? *reinterpret_cast<const float4*>(groups + int64_t(g0 + i) * D + col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       t.x += v[i].x;
@@ -372,7 +379,14 @@ __global__ __launch_bounds__(64) void rmsnorm_dw_final_kernel(const float* group
       t.w += v[i].w;
     }
   }
-  store_dw4(dw, dw_f32, col, t);
+  wsum[wave][lane] = t;
+  __syncthreads();
+  if (wave == 0) {
+    const float4 a = wsum[0][lane], b = wsum[1][lane], c = wsum[2][lane], d = wsum[3][lane];
+    store_dw4(dw, dw_f32, col,
+              make_float4(((a.x + b.x) + c.x) + d.x, ((a.y + b.y) + c.y) + d.y, ((a.z + b.z) + c.z) + d.z,
+                          ((a.w + b.w) + c.w) + d.w));
+  }
 }
 
 // D / 512 chunks per lane (D <= 8192)
@@ -501,7 +515,7 @@ int fm_rmsnorm_backward(const void* dy, int64_t ld_dy, const void* x, int x_dtyp
   hipLaunchKernelGGL(rmsnorm_dw_groups_kernel, dim3(unsigned(D / 256), unsigned(groups)), dim3(64), 0, sm, part,
                      slices, D, part + slices * D, dw, f32);
   if (groups > 1)
-    hipLaunchKernelGGL(rmsnorm_dw_final_kernel, dim3(unsigned(D / 256)), dim3(64), 0, sm, part + slices * D,
+    hipLaunchKernelGGL(rmsnorm_dw_final_kernel, dim3(unsigned(D / 256)), dim3(256), 0, sm, part + slices * D,
                        int(groups), D, dw, f32);
   return check_launch("fm_rmsnorm_backward");
 }
