@@ -49,6 +49,13 @@ extern "C" {
 #define FM_GEMM_FP8_F32 1  /* fp32 block scales, promoted per 128-deep K block */
 #define FM_GEMM_FP8_POW2 2 /* power-of-two scales through the scaled MFMA      */
 #define FM_GEMM_FP8_MX 3   /* e8m0 per-32 scales through the scaled MFMA       */
+/* OR-ed into the kind of fm_grouped_gemm_ragged_k(_split): the output tiles of
+ * an expert are walked with a_t's tiles varying fastest (by default b_t's).
+ * The workgroups running at one time then cover all of that operand's tiles,
+ * which are fetched from memory in the first round only, so pass it when a_t is
+ * the operand not in cache (written long before the launch) and b_t the one
+ * just written.  The results do not depend on it. */
+#define FM_GEMM_A_FAST 0x100
 
 /* gating functions (reference model/moe.py:44-46 GatingFunction) */
 #define FM_GATING_SOFTMAX 0

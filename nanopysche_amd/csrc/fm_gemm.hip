@@ -93,6 +93,7 @@ struct GemmParams {
   int splits;         // ragged-K, 256 x 256 kernel: K slices per tile (>1: fp32 partials, C = workspace)
   int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
   int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
+  int rk_jfast;       // ragged-K: j tiles (a_t's) vary fastest within a group of i tiles
 };
 
 constexpr int kGroupM = 8;
@@ -589,8 +590,9 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
     const int64_t group = Lr / (kGroupM * NJ);
     const int64_t first = group * kGroupM;
     const int64_t gsz = NI - first < kGroupM ? NI - first : kGroupM;
-    t.i0 = (first + (Lr % gsz)) * kT;
-    t.j0 = ((Lr % (kGroupM * NJ)) / gsz) * kT;
+    const int64_t rem = Lr - group * kGroupM * NJ;   // < gsz * NJ
+    t.i0 = (first + (p.rk_jfast ? rem / NJ : rem % gsz)) * kT;
+    t.j0 = (p.rk_jfast ? rem % NJ : rem / gsz) * kT;
     t.j_end = p.n_j;
     t.k_lo = p.offsets[e];
     t.k_hi = p.offsets[e + 1];
@@ -1608,10 +1610,13 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
                              const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
                              void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
                              int64_t ld_out, void* stream) {
+  const int a_fast = (kind & FM_GEMM_A_FAST) != 0;
+  kind &= ~FM_GEMM_A_FAST;
   GemmParams p;
   if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M, N, expert_mask, mask_want, out, out_gs, out2,
                                out2_gs, split_rows, out_dtype, ld_out, p))
     return rc;
+  p.rk_jfast = a_fast;
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
 }
 
@@ -1626,10 +1631,13 @@ int fm_grouped_gemm_ragged_k_split(int kind, const FmGemmOperand* a_t, const FmG
                                    void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
                                    int64_t ld_out, int splits, void* workspace, int64_t workspace_bytes,
                                    void* stream) {
+  const int a_fast = (kind & FM_GEMM_A_FAST) != 0;
+  kind &= ~FM_GEMM_A_FAST;
   GemmParams p;
   if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M, N, expert_mask, mask_want, out, out_gs, out2,
                                out2_gs, split_rows, out_dtype, ld_out, p))
     return rc;
+  p.rk_jfast = a_fast;
   FM_REQUIRE(splits >= 1 && splits <= 16, "fm_grouped_gemm_ragged_k_split: splits must be in [1, 16] (got %d)",
              splits);
   FM_REQUIRE(kind != GK_FP8_F32 || splits == 1,

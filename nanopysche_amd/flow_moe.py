@@ -467,8 +467,12 @@ def _k_splits(kind, plan: RoutingPlan, M, N, dev) -> int:
 
 
 def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out2_gs=0, split=None,
-            mask=None, want=1, may_split=True):
+            mask=None, want=1, may_split=True, a_cold=False):
+    """Weight-gradient grouped GEMM.  ``a_cold``: a_t was written long before
+    this launch (saved by the forward) and b_t just now, so a_t's tiles are
+    walked fastest (GEMM_A_FAST: fetched from memory once); by default b_t's."""
     S = _k_splits(kind, plan, M, N, out.device) if may_split else 1
+    gk = _gemm_kind(kind) | (_lib.GEMM_A_FAST if a_cold else 0)
     ws = None
     if S > 1:
         nbytes = int(_lib.load().fm_grouped_gemm_ragged_k_split_workspace_bytes(plan.num_experts, M, N, S))
@@ -476,12 +480,12 @@ def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out
 
     def launch():
         if ws is None:
-            _lib.call("fm_grouped_gemm_ragged_k", _gemm_kind(kind), _col_operand(a_t, kind),
+            _lib.call("fm_grouped_gemm_ragged_k", gk, _col_operand(a_t, kind),
                       _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
                       _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
                       M if split is None else split, _dt(out), N, _lib.stream_of(out))
         else:
-            _lib.call("fm_grouped_gemm_ragged_k_split", _gemm_kind(kind), _col_operand(a_t, kind),
+            _lib.call("fm_grouped_gemm_ragged_k_split", gk, _col_operand(a_t, kind),
                       _col_operand(b_t, kind), _lib.ptr(plan.offsets), plan.num_experts, M, N,
                       _lib.ptr(mask), want, _lib.ptr(out), out_gs, _lib.ptr(out2), out2_gs,
                       M if split is None else split, _dt(out), N, S, _lib.ptr(ws), ws.numel() * 4,
@@ -866,8 +870,9 @@ class FP8FlowMoECompute:
         side.wait_stream(main)
         with torch.cuda.stream(side):
             for kind, want in runs:
+                # the forward's saved SwiGLU columns are the operand not in cache
                 _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
-                        want=want, may_split=side is main)
+                        want=want, may_split=side is main, a_cold=True)
         for kind, want in runs:
             _gemm_m(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, mask, want)
         if self.capture_intermediates is not None:

@@ -109,7 +109,8 @@ def test_ragged_k_weight_grad(dev, kind, balanced, splits, monkeypatch):
     """Skewed routing with a zero-token expert keeps the tiles in launch
     order; balanced routing takes the contiguous per-XCD split.  splits = 3
     forces the split-K form (fp32 partials + ordered reduction; slices of the
-    small experts are empty), except for the fp32-scale kind, which has none."""
+    small experts are empty), except for the fp32-scale kind, which has none.
+    The a_t-fastest tile order (FM_GEMM_A_FAST) gives the same bits."""
     if splits is not None:
         monkeypatch.setenv("FM_RK_SPLITS", splits)
     E, T, K, D, H = 6, 2500, 2, 256, 256
@@ -131,6 +132,9 @@ def test_ragged_k_weight_grad(dev, kind, balanced, splits, monkeypatch):
         dW1 = torch.full((E * H, D), float("nan"), dtype=out_dtype, device=dev)
         dW3 = torch.full((E * H, D), float("nan"), dtype=out_dtype, device=dev)
         _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H)
+        aw1, aw3 = torch.full_like(dW1, float("nan")), torch.full_like(dW3, float("nan"))
+        _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, aw1, H * D, aw3, H * D, split=H, a_cold=True)
+        assert torch.equal(aw1, dW1) and torch.equal(aw3, dW3)
         av = _deq_cols(pg.rows_t, kind)  # [2H, R]
         bv = _deq_cols(px.rows_t, kind)  # [D, R]
         offs = plan.offsets.cpu().numpy()
