@@ -38,10 +38,11 @@
 //                   promoted through a second set of accumulator registers.
 // Ragged-M workgroup ids are remapped so each XCD walks a contiguous range of
 // the valid tiles, grouped 8 token tiles at a time for L2 reuse of weights and
-// activations; within a group the weight tiles vary fastest, so the workgroups
-// running together share a few token tiles and cover all the weight tiles: a
-// weight tile is fetched from HBM in the first round only, while the token
-// operand, written by the kernel just before, is cached in every round.
+// activations; within a group the weight tiles vary fastest when an expert's
+// weights are small enough to stay cached, so the workgroups running together
+// share a few token tiles and cover all the weight tiles: a weight tile is
+// fetched from HBM in the first round only, while the token operand, written
+// by the kernel just before, is cached in every round (gemm_weight_fast).
 // Ragged-K tiles keep launch order (balances uneven experts) unless the
 // experts are balanced (contiguous XCD ranges, see decode_tile256).
 #include <atomic>
@@ -1338,14 +1339,19 @@ inline bool gemm_persistent() {
   return on;
 }
 
-// Ragged-M tiles take the weight tiles fastest within a group of token tiles
-// unless FM_GEMM_ORDER=t (token tiles fastest; read once).
-inline bool gemm_weight_fast() {
-  static const bool on = [] {
+// Ragged-M tile order within a group of token tiles.  Weight tiles fastest
+// when one expert's weight operand fits an eighth of the 256 MiB Infinity
+// Cache (each XCD walks about one expert at a time, so eight of them must
+// stay cached for the later rounds to find their weight tiles there); token
+// tiles fastest otherwise, so each weight tile is fetched once per group.
+// FM_GEMM_ORDER=t / =w forces either order (read once).
+constexpr int64_t kWeightFastMaxBytes = int64_t(32) << 20;
+inline bool gemm_weight_fast(int64_t weight_bytes) {
+  static const int forced = [] {
     const char* e = getenv("FM_GEMM_ORDER");
-    return e == nullptr || e[0] != 't';
+    return e == nullptr ? 0 : e[0] == 't' ? 1 : e[0] == 'w' ? 2 : 0;
   }();
-  return on;
+  return forced == 0 ? weight_bytes <= kWeightFastMaxBytes : forced == 2;
 }
 
 // Compute units of the current device (cached per device).
@@ -1427,7 +1433,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   }
   if (p.n_tiles == 0) return 0;
   p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
-  p.w_fast = gemm_weight_fast() ? 1 : 0;
+  p.w_fast = MODE == GM_RAGGED_M && gemm_weight_fast(p.n_i * p.K * (kind == GK_BF16 ? 2 : 1)) ? 1 : 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
