@@ -95,8 +95,42 @@ class GemmTimer:
         return out
 
 
+GRAPH_ERRORS = []
+
+
+def time_graphed(step, leaves, steps, warmup):
+    """ms per replay of `step` captured as a HIP graph (GraphedStep), or None
+    (with the reason kept in GRAPH_ERRORS) if the capture raised."""
+    import torch
+
+    import nanopysche_amd as fm
+
+    try:
+        gstep = fm.GraphedStep(step, leaves, warmup=2)
+    except RuntimeError as e:
+        GRAPH_ERRORS.append(str(e).splitlines()[0][:200])
+        torch.cuda.synchronize()
+        return None
+    for _ in range(warmup):
+        gstep.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        gstep.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def launch_note(args):
+    if args.eager:
+        return "eager"
+    if GRAPH_ERRORS:
+        return "eager (HIP graph capture failed: " + GRAPH_ERRORS[-1] + ")"
+    return "hip_graph: the step captured once, replayed per step"
+
+
 def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, backward=True,
-               gemm_timer=True, pre_step=None, overlap=True, router=None):
+               gemm_timer=True, pre_step=None, overlap=True, router=None, graph=False):
     """Times `steps` calls of the expert block (forward, + backward when
     `backward`), weight cache dropped every step, with nothing recorded between
     the launches.  With `router` = (gate weight, gate bias, top_k, gating[,
@@ -109,7 +143,13 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
     every grouped-GEMM launch, on one stream so that no other kernel runs
     beside the one timed (each event record leaves a few-microsecond bubble in
     the stream, so this pass is not the one the step time comes from).
-    Returns (ms per step, GEMM event summary or None)."""
+    With `graph` the step is then captured once as a HIP graph
+    (nanopysche_amd.GraphedStep: every kernel of the step, weight
+    re-quantisation included, with no host work between launches) and `steps`
+    replays are timed; the eager step time is returned beside it.
+    Returns (ms per step, GEMM event summary or None, eager ms per step)."""
+    if pre_step is not None and graph:
+        raise ValueError("a graphed step takes no per-step host input")
     import torch
 
     import nanopysche_amd as fm
@@ -165,6 +205,12 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    eager_ms = elapsed * 1e3 / steps
+    if graph:
+        leaves = (params + gparams + [xr] + ([] if layer is not None else [wr])) if backward else []
+        graph_ms = time_graphed(step, leaves, steps, warmup)
+        if graph_ms is not None:
+            elapsed = graph_ms * steps / 1e3
     summary = None
     if gemm_timer:
         timer = GemmTimer()
@@ -178,7 +224,7 @@ def time_layer(x, w, idx, w1, w2, w3, go, E, recipe, threshold, steps, warmup, b
             fmm.GEMM_TIMER = None
             blk.overlap_streams = overlap
         summary = timer.summary()
-    return elapsed * 1e3 / steps, summary
+    return elapsed * 1e3 / steps, summary, eager_ms
 
 
 def gemm_report(summ, steps, flops_scale=1.0):
@@ -377,8 +423,9 @@ def workload_c3(args, dev):
         torch.cuda.synchronize()
         del a, b
     gw, gb = router_params(D, E, 2, dev)
-    ms, summ = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup,
-                          overlap=not args.no_overlap, router=(gw, gb, K, "softmax"))
+    ms, summ, eager_ms = time_layer(x, w, idx, w1, w2, w3, go, E, args.recipe, 0, args.steps, args.warmup,
+                                    overlap=not args.no_overlap, router=(gw, gb, K, "softmax"),
+                                    graph=not args.eager)
     dom = max(summ, key=lambda k: summ[k]["ms"])
     d = summ[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
@@ -404,7 +451,9 @@ def workload_c3(args, dev):
                    "tokens": T, "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H,
                    "routing": "top-2 softmax router (fp32 gate, load-balancing loss) with the exactly balanced "
                               "assignment (2048 per expert) replayed as its R3 routing mask",
-                   "recipe": args.recipe, "assignments": A},
+                   "recipe": args.recipe, "assignments": A,
+                   "launch": launch_note(args)},
+        "eager_ms_per_step": round(eager_ms, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": None if traffic is None else traffic["bytes_per_launch"],
@@ -451,7 +500,10 @@ def workload_shared(args, dev):
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    if not args.eager:
+        graph_ms = time_graphed(step, params + [x], args.steps, args.warmup)
+        ms = eager_ms if graph_ms is None else graph_ms
     timer = GemmTimer()
     fmm.GEMM_TIMER = timer
     blk.block.overlap_streams = False
@@ -480,7 +532,9 @@ def workload_shared(args, dev):
         "dtype": "bf16" if args.recipe == "none" else "fp8-e4m3",
         "data": "synthetic",
         "config": {"workload": "shared expert at configs[2]'s shapes (one group on the grouped-GEMM path)",
-                   "tokens": T, "d_model": D, "ffn_hidden": H, "recipe": args.recipe},
+                   "tokens": T, "d_model": D, "ffn_hidden": H, "recipe": args.recipe,
+                   "launch": launch_note(args)},
+        "eager_ms_per_step": round(eager_ms, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": None, "kernel": dom},
         "gemm": gemm_report(summ, args.steps),
@@ -629,8 +683,8 @@ def workload_c1(args, dev):
 
     with torch.no_grad():
         w0, i0, _ = fm.route(x, wg, bg, top_k=K, gating="softmax")
-    ms, summ = time_layer(x, w0, i0, w1, w2, w3, None, E, "none", 1 << 40, args.steps, args.warmup,
-                          backward=False, router=(wg, bg, K, "softmax", False))
+    ms, summ, eager_ms = time_layer(x, w0, i0, w1, w2, w3, None, E, "none", 1 << 40, args.steps, args.warmup,
+                                    backward=False, router=(wg, bg, K, "softmax", False), graph=not args.eager)
     counts = torch.bincount(i0.reshape(-1), minlength=E).tolist()
     flops = 6.0 * T * K * D * H
     return {
@@ -639,7 +693,9 @@ def workload_c1(args, dev):
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "configs[0]: router + BF16 expert block forward, top-1 softmax", "tokens": T,
-                   "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H, "tokens_per_expert": counts},
+                   "d_model": D, "experts": E, "top_k": K, "ffn_hidden": H, "tokens_per_expert": counts,
+                   "launch": launch_note(args)},
+        "eager_ms_per_step": round(eager_ms, 4),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),
         "gemm": gemm_report(summ, args.steps),
@@ -684,7 +740,7 @@ def workload_c4(args, dev):
         row = {"tokens_per_expert": t, "tokens": T,
                "max_tokens_per_expert": int(torch.bincount(idx.reshape(-1), minlength=E).max())}
         for name, recipe in (("bf16", "none"), ("fp8", "flow_moe")):
-            ms, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False,
+            ms, _, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False,
                                overlap=not args.no_overlap)
             row[f"{name}_ms"] = round(ms, 3)
             row[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
@@ -742,7 +798,7 @@ def workload_c5(args, dev):
     x = device_normal((n_tok, D), 1.0, gen, dev, torch.bfloat16)
     go = device_normal((n_tok, D), 1e-2, gen, dev, torch.bfloat16)
     w1, w2, w3 = [device_normal((E_local * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
-    ms, summ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup,
+    ms, summ, _ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup,
                           overlap=not args.no_overlap)
     flops = 18.0 * A * D * H
     return {
@@ -768,6 +824,9 @@ def main():
     ap.add_argument("--workload", default="c3", choices=["c3", "c1", "c2", "c4", "c5", "shared"])
     ap.add_argument("--recipe", default="flow_moe", choices=["flow_moe", "blockwise", "mxfp8", "none"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eagerly issued steps instead of replays of the step captured as a HIP graph "
+                         "(configs[2], configs[0], shared expert)")
     ap.add_argument("--no-overlap", action="store_true",
                     help="keep every launch on one stream (no dW2 / dH overlap)")
     ap.add_argument("--copy-probe", action="store_true",

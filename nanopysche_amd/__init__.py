@@ -23,6 +23,7 @@ from .flow_moe import (
     quantize_to_fp8,
     scaling_aware_transpose,
 )
+from .graph import GraphedStep
 from .moe_layer import FP8FlowMoELayer
 from .norm import NormOutput, RMSNorm, rmsnorm, rmsnorm_backward, rmsnorm_quantize
 from .routing import (ExpertLoadTracker, RoutingPlan, expert_counts, load_balancing_loss, route, route_tokens,
@@ -56,6 +57,7 @@ __all__ = [
     "expert_counts",
     "ExpertLoadTracker",
     "FP8FlowMoELayer",
+    "GraphedStep",
     "RMSNorm",
     "rmsnorm",
     "rmsnorm_quantize",
