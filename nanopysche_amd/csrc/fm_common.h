@@ -19,6 +19,7 @@
 #pragma once
 
 #include <stdint.h>
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #define FM_HD __host__ __device__ __forceinline__
@@ -191,6 +192,29 @@ FM_HD uint8_t quant_mx(float x, float inv_scale) { return f32_to_e4m3(clamp448(x
 namespace fm {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Workgroups of `kernel` (`block` threads, no dynamic LDS) that fit on the
+// device at once: its occupancy per CU (registers, LDS) x the CUs.  A launch
+// of that many workgroups runs in one round, with no partly filled last one.
+template <typename F>
+inline int64_t resident_workgroups(F kernel, int block) {
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, block, 0) != hipSuccess || nb < 1) nb = 1;
+  return int64_t(nb) * device_cus();
+}
 }  // namespace fm
 
 #define FM_REQUIRE(cond, ...)            \

@@ -1354,19 +1354,6 @@ inline bool gemm_weight_fast(int64_t weight_bytes) {
   return forced == 0 ? weight_bytes <= kWeightFastMaxBytes : forced == 2;
 }
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 // Persistent ragged-M launch: one workgroup per CU (a multiple of 8, one
 // share per XCD), at most one per 256 x 256 tile of the host bound.
 inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {

@@ -511,13 +511,15 @@ __device__ __forceinline__ void add_bf16x8(float (&acc)[8], uint4 pk, float s) {
 }
 
 template <typename WT, int KC>
-__global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* y, int64_t ld_y,
-                                                               const int32_t* row_of, const float* w,
+__global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* __restrict__ y, int64_t ld_y,
+                                                               const int32_t* __restrict__ row_of,
+                                                               const float* __restrict__ w,
                                                                int64_t T, int K, int64_t D,
-                                                               void* out, int out_f32, int64_t ld_out,
-                                                               const uint16_t* addend, int64_t ld_add,
-                                                               const float* dl, int64_t ld_dl,
-                                                               const WT* W, int64_t ld_w, int E, int64_t tpb) {
+                                                               void* __restrict__ out, int out_f32, int64_t ld_out,
+                                                               const uint16_t* __restrict__ addend, int64_t ld_add,
+                                                               const float* __restrict__ dl, int64_t ld_dl,
+                                                               const WT* __restrict__ W, int64_t ld_w, int E,
+                                                               int64_t tpb) {
   const int64_t c = int64_t(blockIdx.x) * 2048 + threadIdx.x * 8;
   if (c >= D) return;
   // the gate's columns of this thread for the 8 experts, kept as stored
@@ -878,12 +880,15 @@ int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, cons
   FM_REQUIRE(gate_dtype == FM_DTYPE_BF16 || gate_dtype == FM_DTYPE_F32, "fm_unpermute_router: bad gate dtype");
   if (T == 0) return 0;
   const int64_t nx = (D + 2047) / 2048;
-  int64_t tpb = (T * nx + 1023) / 1024;   // about 1024 workgroups
-  if (tpb < 1) tpb = 1;
-  const dim3 grid(unsigned(nx), unsigned((T + tpb - 1) / tpb));
   hipStream_t sm = static_cast<hipStream_t>(stream);
   auto go = [&](auto wt, auto kc) {
     using WT = decltype(wt);
+    // as many workgroups as fit at once (one round: a partly filled second
+    // round measured 26 against 23 us at configs[2]), each a run of tokens
+    static const int64_t nwg = resident_workgroups(unpermute_router_kernel<WT, decltype(kc)::value>, 256);
+    int64_t tpb = (T * nx + nwg - 1) / nwg;
+    if (tpb < 1) tpb = 1;
+    const dim3 grid(unsigned(nx), unsigned((T + tpb - 1) / tpb));
     hipLaunchKernelGGL((unpermute_router_kernel<WT, decltype(kc)::value>), grid, dim3(256), 0, sm,
                        static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
                        out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add, dlogits,
