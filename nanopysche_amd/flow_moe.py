@@ -845,10 +845,17 @@ class FP8FlowMoECompute:
             dw = torch.empty(T * K, dtype=torch.float32, device=dev)
             _lib.call("fm_router_weight_grad", _lib.ptr(dO), dO.stride(0), _lib.ptr(Y), Y.stride(0),
                       _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), _lib.stream_of(dO))
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev) if self.overlap_streams else main
         # the router's share of the input gradient: a [T, D] addend, or its
-        # (dlogits, gate weight) terms folded into the unpermute
-        rshare = {} if on_router_grad is None else on_router_grad(None if dw is None else dw.reshape(T, K),
-                                                                  not self._dense, dot)
+        # (dlogits, gate weight) terms folded into the unpermute.  Its backward
+        # reads only dO, the saved expert outputs and x, so it runs on the second
+        # stream beside the dY permute and dH; the unpermute waits for it.
+        rshare = {}
+        if on_router_grad is not None:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                rshare = on_router_grad(None if dw is None else dw.reshape(T, K), not self._dense, dot)
         dH = torch.empty(R, H, dtype=torch.bfloat16, device=dev)
         dXp = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         w1dt, w2dt, w3dt = ctx.wdtypes
@@ -861,12 +868,10 @@ class FP8FlowMoECompute:
         dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                       return_transpose=True, weights=None if self._dense else wts,
                                       kmajor_scales=True) for kind, _ in runs}
-        # dW2 (contraction over each expert's tokens) runs on a second stream
+        # dW2 (contraction over each expert's tokens) runs on the second stream
         # beside dH: each alone leaves the last round of workgroups part-empty
         # when the hidden size is not a multiple of the 256-wide tile.  There
         # it takes no K split: the CUs it leaves idle run dH.
-        main = torch.cuda.current_stream(dev)
-        side = _side_stream(dev) if self.overlap_streams else main
         side.wait_stream(main)
         with torch.cuda.stream(side):
             for kind, want in runs:
@@ -889,13 +894,15 @@ class FP8FlowMoECompute:
                     mask=mask, want=want)
             # input gradient
             _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
+        # the router's backward and dW2 (and the buffers they read, referenced
+        # until here) are done before the router's dx share is summed
+        main.wait_stream(side)
         dx_addend = rshare.get("addend")
         if self._dense:
             dx = dXp[:T] if dx_addend is None else dXp[:T] + dx_addend
         else:
             terms = (rshare["dlogits"], rshare["gate_w"]) if "dlogits" in rshare else None
             dx = fused_unpermute_unpad(dXp, plan, None, addend=dx_addend, router_terms=terms)
-        main.wait_stream(side)   # dW2 and the buffers it read stay referenced until here
         ctx.saved_cols = None
         ctx.saved_hcols = None
         return (dx.to(ctx.x_dtype), None if dw is None else dw.reshape(T, K), dW1, dW2, dW3, None, None)
