@@ -724,6 +724,29 @@ class FP8FlowMoECompute:
             ew = self._cache[kind] = ExpertWeights(kind)
         return ew.refresh(*self._w, self.num_experts, need_dgrad)
 
+    def prefetch_weights(self, num_assignments: int) -> None:
+        """While a HIP graph is being captured: re-quantises the expert weights
+        (when they changed) on the second stream, a branch of the graph beside
+        what the caller issues next (the router and the routing sort); the next
+        forward waits for it before its first GEMM.  Eagerly issued steps keep
+        the re-quantisation inline: beside the router kernels on a second
+        stream it measured 0.89 against 0.82 ms per C3 step, while a replayed
+        graph gains ~1%."""
+        if (not self.overlap_streams or self._w is None
+                or not torch.cuda.is_current_stream_capturing()):
+            return
+        dev = self._w[0].device
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(main)
+        fp8_kind, use_bf16 = self.modes(num_assignments)
+        with torch.cuda.stream(side):
+            for kind in (fp8_kind, _lib.QUANT_BF16 if use_bf16 else None):
+                if kind is not None:
+                    self._weights(kind, self._record)
+        self._wq_event = torch.cuda.Event()
+        self._wq_event.record(side)
+
     def modes(self, num_assignments: int):
         """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
         the host from the threshold alone (no read of the device counts)."""
@@ -785,6 +808,9 @@ class FP8FlowMoECompute:
             ew = self._weights(kind, self._record)
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                    return_transpose=self._record, kmajor_scales=True)
+            if getattr(self, "_wq_event", None) is not None:   # weights re-quantised on the second stream
+                torch.cuda.current_stream(dev).wait_event(self._wq_event)
+                self._wq_event = None
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}
