@@ -439,11 +439,18 @@ struct ZeroSrc {
 // grid-stride over (token, 8-column chunk); K rows summed in slot order
 // with separately rounded multiply and add (contraction into FMA is switched
 // off for this kernel), one rounding to the output dtype at the end.
-__global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64_t ld_y,
-                                                        const int32_t* row_of, const float* w,
-                                                        int64_t T, int K, int64_t D,
-                                                        void* out, int out_f32, int64_t ld_out,
-                                                        const uint16_t* addend, int64_t ld_add) {
+// KC > 0 (K == KC): a thread loads the token's KC row indices and weights,
+// then issues every slot's row load before the first sum, instead of one
+// index-then-row round trip per slot (at top-8 with most slots outside the
+// local experts that chain was 8 dependent loads per token); the sums keep
+// the slot order.  KC == 0: any K, one slot at a time.
+template <int KC>
+__global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* __restrict__ y, int64_t ld_y,
+                                                        const int32_t* __restrict__ row_of,
+                                                        const float* __restrict__ w, int64_t T, int K,
+                                                        int64_t D, void* __restrict__ out, int out_f32,
+                                                        int64_t ld_out, const uint16_t* __restrict__ addend,
+                                                        int64_t ld_add) {
 #pragma clang fp contract(off)
   const int64_t chunks = D / 8;
   const int64_t n = T * chunks;
@@ -462,16 +469,34 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* y, int64
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = 0.f;
     }
-    for (int k = 0; k < K; ++k) {
-      const int32_t r = row_of[t * K + k];
-      if (r < 0) continue;
-      const float s = w ? w[t * K + k] : 1.f;
-      const uint4 pk = *reinterpret_cast<const uint4*>(y + int64_t(r) * ld_y + c);
+    auto add_row = [&](uint4 pk, float s) {
       const uint32_t q[4] = {pk.x, pk.y, pk.z, pk.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[2 * j] = acc[2 * j] + s * u2f(q[j] << 16);
         acc[2 * j + 1] = acc[2 * j + 1] + s * u2f(q[j] & 0xffff0000u);
+      }
+    };
+    if constexpr (KC > 0) {
+      int32_t r[KC];
+      float sw[KC];
+      uint4 pk[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        r[k] = row_of[t * KC + k];
+        sw[k] = w ? w[t * KC + k] : 1.f;
+      }
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+        pk[k] = r[k] >= 0 ? *reinterpret_cast<const uint4*>(y + int64_t(r[k]) * ld_y + c) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+        if (r[k] >= 0) add_row(pk[k], sw[k]);
+    } else {
+      for (int k = 0; k < K; ++k) {
+        const int32_t r = row_of[t * K + k];
+        if (r < 0) continue;
+        add_row(*reinterpret_cast<const uint4*>(y + int64_t(r) * ld_y + c), w ? w[t * K + k] : 1.f);
       }
     }
     if (out_f32) {
@@ -861,9 +886,17 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
   if (T == 0) return 0;
   const int64_t n = T * (D / 8);
   const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
-  hipLaunchKernelGGL(unpermute_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
-                     out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add);
+  auto go = [&](auto kc) {
+    hipLaunchKernelGGL((unpermute_kernel<decltype(kc)::value>), dim3(blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), ld_y, row_of, weights,
+                       T, K, D, out, out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend),
+                       ld_add);
+  };
+  if (K == 1) go(std::integral_constant<int, 1>{});
+  else if (K == 2) go(std::integral_constant<int, 2>{});
+  else if (K == 4) go(std::integral_constant<int, 4>{});
+  else if (K == 8) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 0>{});
   return check_launch("fm_unpermute");
 }
 

@@ -137,12 +137,19 @@ def test_permute_bitexact(dev, kind, kmajor):
         assert np.array_equal(_np(pt.rows_t.scale)[:nb], cs)
 
 
-def test_unpermute_bitexact(dev):
-    T, E, K, D = 2000, 16, 4, 256
+@pytest.mark.parametrize("K,drop", [(1, False), (2, False), (3, True), (4, False), (8, True)])
+def test_unpermute_bitexact(dev, K, drop):
+    """K = 1, 2, 4, 8 take the kernels that load every slot's row before the
+    sums, K = 3 the one-slot-at-a-time loop; `drop`: a third of the slots route
+    outside the local experts (no row), as at configs[4]."""
+    T, E, D = 2000, 16, 256
     w, idx = zipf_routing(T, E, K, 1.2, seed=7, zero_experts=(2,))
+    if drop:
+        g = torch.Generator().manual_seed(12)
+        idx = torch.where(torch.rand(idx.shape, generator=g) < 0.33, idx + E + 3, idx)
     plan = fm.route_tokens(idx.to(dev), E)
     y = randn_bf16((plan.rows_max, D), seed=8)
-    ref = orouting.sort_assignments(idx.numpy(), E)
+    ref = orouting.sort_assignments(idx.numpy(), E, drop_out_of_range=drop)
     for weights in (w, None):
         out = fm.fused_unpermute_unpad(y.to(dev), plan, None if weights is None else weights.to(dev),
                                        out_dtype=torch.float32)
