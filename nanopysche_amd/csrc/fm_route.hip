@@ -674,11 +674,13 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* _
   }
 }
 
-// one wave per assignment: dw[a] = sum_d dout[t][d] * y[row_of[a]][d]
-__global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* dout, int64_t ld_do,
-                                                          const uint16_t* y, int64_t ld_y,
-                                                          const int32_t* row_of, int64_t A, int K,
-                                                          int64_t D, float* dw) {
+// one wave per assignment: dw[a] = sum_d dout[t][d] * y[row_of[a]][d], four
+// 512-column chunks' loads issued before their products (summed in column
+// order, as one chunk at a time would)
+__global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* __restrict__ dout, int64_t ld_do,
+                                                          const uint16_t* __restrict__ y, int64_t ld_y,
+                                                          const int32_t* __restrict__ row_of, int64_t A, int K,
+                                                          int64_t D, float* __restrict__ dw) {
   const int lane = threadIdx.x & 63;
   for (int64_t a = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); a < A;
        a += int64_t(gridDim.x) * 4) {
@@ -687,14 +689,23 @@ __global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* dout, 
     if (r >= 0) {
       const uint16_t* g = dout + (a / K) * ld_do;
       const uint16_t* yy = y + int64_t(r) * ld_y;
-      for (int64_t c = int64_t(lane) * 8; c < D; c += 512) {
-        const uint4 p = *reinterpret_cast<const uint4*>(g + c);
-        const uint4 q = *reinterpret_cast<const uint4*>(yy + c);
-        const uint32_t pw[4] = {p.x, p.y, p.z, p.w}, qw[4] = {q.x, q.y, q.z, q.w};
+      for (int64_t c0 = int64_t(lane) * 8; c0 < D; c0 += 4 * 512) {
+        uint4 p[4], q[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc += u2f(pw[j] << 16) * u2f(qw[j] << 16);
-          acc += u2f(pw[j] & 0xffff0000u) * u2f(qw[j] & 0xffff0000u);
+        for (int u = 0; u < 4; ++u) {
+          const int64_t c = c0 + 512 * u;
+          p[u] = c < D ? *reinterpret_cast<const uint4*>(g + c) : make_uint4(0, 0, 0, 0);
+          q[u] = c < D ? *reinterpret_cast<const uint4*>(yy + c) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (c0 + 512 * u >= D) break;
+          const uint32_t pw[4] = {p[u].x, p[u].y, p[u].z, p[u].w}, qw[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc += u2f(pw[j] << 16) * u2f(qw[j] << 16);
+            acc += u2f(pw[j] & 0xffff0000u) * u2f(qw[j] & 0xffff0000u);
+          }
         }
       }
     }
