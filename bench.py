@@ -298,7 +298,8 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
     out = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     ew = ExpertWeights(P2)
     ew._build(w1, w2, w3, E)
-    wbytes = nb(w1, w2, w3) + sum(nb(o.data, o.scale) for o in (ew.w13, ew.w13t, ew.w2, ew.w2t))
+    wouts = {o.data.data_ptr(): o for o in (ew.w13, ew.w13t, ew.w2, ew.w2t)}   # [K][N] operands alias the rows
+    wbytes = nb(w1, w2, w3) + sum(nb(o.data, o.scale) for o in wouts.values())
 
     # RMSNorm ahead of the MoE on the residual stream (x stands in for it)
     nw = torch.ones(D, dtype=torch.float32, device=dev)
@@ -340,7 +341,8 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
         ("unpermute (weighted sum over top-k)",
          lambda: _lib.call("fm_unpermute", _lib.ptr(Y), Y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(wts), T, K, D,
                            _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), None, 0, st), nbq(Y) + nb(wts, out)),
-        ("expert weight re-quantisation (w1, w3, w2 in one launch, 128x128 pow2 + transposed)",
+        ("expert weight re-quantisation (w1, w3, w2 in one launch, 128x128 pow2 "
+         + ("rows; the down and dX GEMMs read them as [K][N])" if ew.w2t.kmajor else "+ transposed)"),
          lambda: ew._build(w1, w2, w3, E), wbytes),
     ]
     results = []

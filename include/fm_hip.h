@@ -56,6 +56,15 @@ extern "C" {
  * the operand not in cache (written long before the launch) and b_t the one
  * just written.  The results do not depend on it. */
 #define FM_GEMM_A_FAST 0x100
+/* OR-ed into the kind of fm_grouped_gemm_ragged_m: the weights are stored
+ * [K][N] -- element (n, k) of expert e at data[e * group_stride + k * ld + n]
+ * (ld >= N), e.g. an expert's w2 [H, D] rows for the down projection -- and
+ * read transposed in LDS, so no [N][K] copy is needed.  FM_GEMM_FP8_POW2 with
+ * 128 x 128 weight blocks (scale of rows n, K block kb at
+ * s[e * scale_group_stride + (n >> 7) * scale_row_stride + kb * scale_kb_stride]),
+ * E <= 64, N a multiple of 256 and K >= 256.  The results are those of the
+ * [N][K] layout bit for bit. */
+#define FM_GEMM_W_KMAJOR 0x200
 
 /* gating functions (reference model/moe.py:44-46 GatingFunction) */
 #define FM_GATING_SOFTMAX 0

@@ -29,6 +29,7 @@ GEMM_FP8_F32 = 1
 GEMM_FP8_POW2 = 2
 GEMM_FP8_MX = 3
 GEMM_A_FAST = 0x100       # OR-ed into a ragged-K kind: a_t's tiles vary fastest (a_t not in cache)
+GEMM_W_KMAJOR = 0x200     # OR-ed into a ragged-M FP8 pow2 kind: weights stored [K][N]
 
 GATING_SOFTMAX = 0
 GATING_SIGMOID = 1

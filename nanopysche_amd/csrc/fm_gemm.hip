@@ -95,6 +95,7 @@ struct GemmParams {
   int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
   int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
   int rk_jfast;       // ragged-K: j tiles (a_t's) vary fastest within a group of i tiles
+  int q_nn;           // ragged-M: the weights stored [K][N] (persistent FP8 pow2 kernel only)
 };
 
 constexpr int kGroupM = 8;
@@ -195,8 +196,9 @@ struct Smem256 {
 // feed outputs that are never stored.
 struct OpStream {
   v4i rsrc;               // descriptor of this wave's first row group at K offset 0
-  uint32_t group_bytes;   // 8 rows
+  uint32_t group_bytes;   // 8 rows (NN layout: 4 K rows)
   uint32_t lane_off[2];   // even / odd group
+  uint32_t k_row_bytes;   // NN layout: bytes per K row (a K step advances 128 of them)
 };
 
 __device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows, int lane,
@@ -225,6 +227,55 @@ __device__ __forceinline__ v8i read_frag8(const uint8_t* base, int r, int half, 
 }
 __device__ __forceinline__ v8bf read_frag16(const uint8_t* base, int r, int ks, int lhalf) {
   return __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(base + lds_off(r, ks * 2 + lhalf)));
+}
+
+// NN weight operand (FP8, stored [K][N]: element (i, k) at k * ld + i).  A K
+// step of a 256-row tile is 128 K rows of 256 bytes in LDS, K row k's 16-byte
+// chunk c stored at chunk c ^ 2 (k % 8) (32-byte windows rotated by k % 8, so
+// the eight K rows one transposed read touches fall on distinct banks).  The
+// DMA moves 32 groups of 4 K rows (1 KiB) per step, 4 consecutive groups per
+// wave; lane n of a group loads K row n / 16, global chunk (n % 16) ^ 2 k % 8.
+__device__ __forceinline__ OpStream make_stream_nn(const uint8_t* base, int64_t ld, int lane, int wave) {
+  OpStream s;
+  s.group_bytes = uint32_t(4 * ld);
+  s.k_row_bytes = uint32_t(ld);
+  s.rsrc = make_rsrc(base + int64_t(wave) * 16 * ld);
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int row = lane >> 4, kk = 4 * par + row;
+    s.lane_off[par] = uint32_t(row * ld + 16 * ((lane & 15) ^ (2 * kk)));
+  }
+  return s;
+}
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+// ds_read_b64_tr_b8 (gfx950): in each 16-lane group, lanes 2r and 2r + 1 give
+// the addresses of bytes 0-7 and 8-15 of row r (r = 0..7), and lane m of the
+// group receives byte m of every row (8 bytes, row order).  Established with
+// an in-bounds probe of the instruction on the device.
+__device__ __forceinline__ v2i lds_read_tr8(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+      reinterpret_cast<__attribute__((address_space(3))) v2i*>(
+          reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds_addr(p))));
+}
+
+// NN A fragment of rows ibase + (lane % 32) (ibase a multiple of 32), K half
+// `half` of the step: lane l supplies K row 8-block base + (l % 16) / 2 at
+// columns ibase + 16 ((l / 16) % 2) + 8 (l % 2), so it receives its own row's
+// K bytes [16 h, 16 h + 16) and [32 + 16 h, +16) (h = l / 32) in four reads --
+// the byte order of the NT fragment (read_frag8).
+__device__ __forceinline__ v8i read_frag8_nn(const uint8_t* st, int ibase, int half, int lane) {
+  const int h = lane >> 5, r = (lane >> 1) & 7;
+  const int col = (ibase + ((lane >> 4) & 1) * 16 + (lane & 1) * 8) ^ (32 * r);   // every K row read has k % 8 == r
+  const uint8_t* b = st + (half * 64 + 16 * h + r) * 256 + col;
+  const v2i p0 = lds_read_tr8(b);
+  const v2i p1 = lds_read_tr8(b + 8 * 256);
+  const v2i p2 = lds_read_tr8(b + 32 * 256);
+  const v2i p3 = lds_read_tr8(b + 40 * 256);
+  v8i f;
+  f[0] = p0[0]; f[1] = p0[1]; f[2] = p1[0]; f[3] = p1[1];
+  f[4] = p2[0]; f[5] = p2[1]; f[6] = p3[0]; f[7] = p3[1];
+  return f;
 }
 
 // Scales in LDS.  pow2: the DMA places the fp32 scale of tile row
@@ -306,16 +357,17 @@ struct WaveCoord {
 
 // One K step of DMA for this wave: 4 row groups of each operand, then one
 // scale dword per lane (waves 0-3: Q scale slots, 4-7: P scale slots).
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc, int64_t k,
                                            uint32_t dst, int wave) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   const uint32_t kb = uint32_t(k * ES);
+  const uint32_t kq = QNN ? uint32_t(k) * qst.k_row_bytes : kb;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    bdma16(qst.rsrc, qst.lane_off[u & 1], u * qst.group_bytes + kb, dst + (wave * 4 + u) * 1024);
+    bdma16(qst.rsrc, qst.lane_off[u & 1], u * qst.group_bytes + kq, dst + (wave * 4 + u) * 1024);
     bdma16(pst.rsrc, pst.lane_off[u & 1], u * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + u) * 1024);
   }
   if constexpr (KIND != GK_BF16) bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
@@ -323,7 +375,7 @@ __device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& 
 
 // Reads half `half` of the K step in stage `st` (pow2 scales only for half 0:
 // one scale per 128-deep step).
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND>& f, const WaveCoord& w) {
   using SM = Smem256<KIND>;
   if constexpr (KIND == GK_BF16) {
@@ -351,7 +403,8 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, half, w.lhalf);
+      if constexpr (QNN) f.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, half, w.lane);
+      else f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, half, w.lhalf);
       if (t < 2) f.b[t] = read_frag8(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, half, w.lhalf);
     }
   }
@@ -359,16 +412,17 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
 
 // Piece u of issue_step: u = 0..7 the operand row groups (even: Q group u/2,
 // odd: P group u/2), u = 8 the scale dword.
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ void issue_piece(int u, const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
                                             int64_t k, uint32_t dst, int wave) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   const uint32_t kb = uint32_t(k * ES);
+  const uint32_t kq = QNN ? uint32_t(k) * qst.k_row_bytes : kb;
   if (u < 8) {
     const int g = u >> 1;
-    if ((u & 1) == 0) bdma16(qst.rsrc, qst.lane_off[g & 1], g * qst.group_bytes + kb, dst + (wave * 4 + g) * 1024);
+    if ((u & 1) == 0) bdma16(qst.rsrc, qst.lane_off[g & 1], g * qst.group_bytes + kq, dst + (wave * 4 + g) * 1024);
     else bdma16(pst.rsrc, pst.lane_off[g & 1], g * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + g) * 1024);
   } else if constexpr (KIND != GK_BF16) {
     bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
@@ -380,7 +434,7 @@ __device__ __forceinline__ void issue_piece(int u, const OpStream& qst, const Op
 // interleave puts them between the phase's MFMAs: issued as one burst after
 // the barrier, a step's 72 DMA instructions per CU (~16 texture-address
 // cycles each) held every wave back from its first MFMA.
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ void issue_read_half0(const OpStream& qst, const OpStream& pst, const ScaleSrc& sc,
                                                  int64_t k, uint32_t dst, int wave, const uint8_t* st,
                                                  Frag<KIND>& f, const WaveCoord& w) {
@@ -410,13 +464,14 @@ __device__ __forceinline__ void issue_read_half0(const OpStream& qst, const OpSt
           st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
       f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
     }
-    issue_piece<KIND>(8, qst, pst, sc, k, dst, wave);
+    issue_piece<KIND, QNN>(8, qst, pst, sc, k, dst, wave);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
-      issue_piece<KIND>(2 * t, qst, pst, sc, k, dst, wave);
+      if constexpr (QNN) f.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
+      else f.a[t] = read_frag8(st, w.wi * 128 + t * 32 + w.lrow, 0, w.lhalf);
+      issue_piece<KIND, QNN>(2 * t, qst, pst, sc, k, dst, wave);
       if (t < 2) f.b[t] = read_frag8(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, 0, w.lhalf);
-      issue_piece<KIND>(2 * t + 1, qst, pst, sc, k, dst, wave);
+      issue_piece<KIND, QNN>(2 * t + 1, qst, pst, sc, k, dst, wave);
     }
   }
 }
@@ -456,10 +511,10 @@ __device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][2])
   }
 }
 
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ void interleave_half() {
   constexpr int kMfma = KIND == GK_BF16 ? 16 : 8;
-  constexpr int kReads = KIND == GK_BF16 ? 1 : 2;
+  constexpr int kReads = KIND == GK_BF16 ? 1 : QNN ? 3 : 2;   // NN: four 8-byte reads per A fragment
 #pragma unroll
   for (int i = 0; i < kMfma; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
@@ -864,7 +919,7 @@ struct TileStreams {
   ScaleSrc sc;
 };
 
-template <int KIND>
+template <int KIND, bool QNN = false>
 __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Operand& P, int64_t n_i, const TileP& t,
                                                    const WaveCoord& w) {
   using SM = Smem256<KIND>;
@@ -873,7 +928,8 @@ __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Oper
   const int64_t q_rows = n_i - t.i0 < kT ? n_i - t.i0 : kT;
   const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
   const int lane = fresh_lane();
-  s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, lane, w.wave);
+  if constexpr (QNN) s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
+  else s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, lane, w.wave);
   s.p = make_stream(P.p + int64_t(t.j0) * P.ld * ES, P.ld * ES, p_rows, lane, w.wave);
   s.sc = ScaleSrc{};
   if constexpr (SM::kScaled) {
@@ -941,7 +997,9 @@ __device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8
     }
 }
 
-template <int KIND, int MXL = 0>
+// QNN (FP8 pow2 only): the weight operand Q is stored [K][N] (make_stream_nn,
+// read_frag8_nn); all N tiles are full (N % 256 == 0, checked by the launcher).
+template <int KIND, int MXL = 0, bool QNN = false>
 __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
@@ -970,17 +1028,17 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
   block_barrier();   // the tile queue is in LDS
   TileP cur;
   if (!tile_queue_get(tq, 0, cur)) return;
-  TileStreams S = tile_streams<KIND>(p.Q, p.P, p.n_i, cur, w);
+  TileStreams S = tile_streams<KIND, QNN>(p.Q, p.P, p.n_i, cur, w);
   const int64_t nk = p.K / KSTEP;   // >= 2 (launcher)
   const uint32_t smem_lds = lds_addr(smem);
   uint8_t* const W = smem + 2 * SM::kStage + w.wave * 2048;
 
   Frag<KIND> f0, f1;
-  issue_step<KIND>(S.q, S.p, S.sc, 0, smem_lds, w.wave);
-  issue_step<KIND>(S.q, S.p, S.sc, KSTEP, smem_lds + SM::kStage, w.wave);
+  issue_step<KIND, QNN>(S.q, S.p, S.sc, 0, smem_lds, w.wave);
+  issue_step<KIND, QNN>(S.q, S.p, S.sc, KSTEP, smem_lds + SM::kStage, w.wave);
   FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
   block_barrier();
-  read_half<KIND>(smem, 0, f0, w);
+  read_half<KIND, QNN>(smem, 0, f0, w);
   int cur_off = 0;
 
   for (int m = 0;; ++m) {
@@ -1001,19 +1059,19 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
     auto step = [&](int64_t t, int64_t kn) {
       const int nxt_off = SM::kStage - cur_off;
       __builtin_amdgcn_sched_barrier(0);
-      read_half<KIND>(smem + cur_off, 1, f1, w);
+      read_half<KIND, QNN>(smem + cur_off, 1, f1, w);
       if constexpr (KIND == GK_FP8_POW2) {
         f1.sa[0] = f0.sa[0];
         f1.sb[0] = f0.sb[0];
       }
       mma_half<KIND>(f0, acc);
-      interleave_half<KIND>();
+      interleave_half<KIND, QNN>();
       __builtin_amdgcn_sched_barrier(0);
       FM_WAIT_VMCNT(0);
       block_barrier();
-      issue_read_half0<KIND>(S.q, S.p, S.sc, kn * KSTEP, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
+      issue_read_half0<KIND, QNN>(S.q, S.p, S.sc, kn * KSTEP, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
       mma_half<KIND>(f1, acc);
-      interleave_half<KIND>();
+      interleave_half<KIND, QNN>();
       __builtin_amdgcn_sched_barrier(0);
       cur_off = nxt_off;
     };
@@ -1022,7 +1080,7 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
     // this tile's sources are dead now: S becomes the next tile's
     if (has_next) {
       const Operand Q = uniform_operand(&pl->Q), P = uniform_operand(&pl->P);
-      S = tile_streams<KIND>(Q, P, rfl64(pl->n_i), nxt, w);
+      S = tile_streams<KIND, QNN>(Q, P, rfl64(pl->n_i), nxt, w);
     }
 #pragma unroll 1
     for (int64_t t = nk - 2; t < nk; ++t) step(t, has_next ? t + 2 - nk : nk - 1);
@@ -1362,7 +1420,10 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
   const dim3 grid(unsigned(want < slots ? want : slots)), block(512);
   switch (kind) {
     case GK_BF16: hipLaunchKernelGGL((gemm256p_kernel<GK_BF16>), grid, block, 0, s, p); break;
-    case GK_FP8_POW2: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p); break;
+    case GK_FP8_POW2:
+      if (p.q_nn) hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2, 0, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
+      break;
     default: {
       const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
       switch (mxl) {
@@ -1425,7 +1486,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
   } else if (MODE == GM_RAGGED_M && p.E <= 64 && p.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
-             gemm_persistent()) {
+             (gemm_persistent() || p.q_nn)) {
     launch256p(kind, p, s);
   } else {
     launch256<MODE>(kind, grid, p, s);
@@ -1519,7 +1580,13 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
                              int64_t m_tiles, const int32_t* tile_expert, const int32_t* offsets,
                              int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
                              void* out, int out_dtype, int64_t ld_out, void* stream) {
+  const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
+  kind &= ~FM_GEMM_W_KMAJOR;
   FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
+  FM_REQUIRE(!nn || (kind == GK_FP8_POW2 && E <= 64 && N % 256 == 0 && K >= 256 && weights->ld >= N &&
+                     weights->group_stride >= K * weights->ld),
+             "fm_grouped_gemm_ragged_m: [K][N] weights need the pow2 kind, E <= 64, N a multiple of 256, K >= 256, "
+             "a row pitch >= N and a group stride >= K x pitch");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
   if (int rc = check_scale_span(*tokens, kind, m_tiles * 128, K, "tokens")) return rc;
@@ -1528,8 +1595,8 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   FM_REQUIRE(K > 0 && K % 128 == 0, "fm_grouped_gemm_ragged_m: K must be a positive multiple of 128 (got %lld)", (long long)K);
   FM_REQUIRE(E >= 1, "fm_grouped_gemm_ragged_m: E must be >= 1");
   FM_REQUIRE(m_tiles >= 0, "fm_grouped_gemm_ragged_m: m_tiles must be >= 0");
-  FM_REQUIRE(tokens->ld >= K && weights->ld >= K, "fm_grouped_gemm_ragged_m: operand pitch < K");
-  FM_REQUIRE(weights->group_stride >= K, "fm_grouped_gemm_ragged_m: weight group stride < K");
+  FM_REQUIRE(tokens->ld >= K && (nn || weights->ld >= K), "fm_grouped_gemm_ragged_m: operand pitch < K");
+  FM_REQUIRE(nn || weights->group_stride >= K, "fm_grouped_gemm_ragged_m: weight group stride < K");
   FM_REQUIRE(ld_out >= N && ld_out % 4 == 0, "fm_grouped_gemm_ragged_m: output pitch must be >= N and a multiple of 4");
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_m: bad out dtype");
   FM_REQUIRE(kind != GK_FP8_F32 || weights->scale_row_shift == 7,
@@ -1552,6 +1619,7 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   p.ldC = ld_out;
   p.out_f32 = out_dtype == FM_DTYPE_F32;
   p.split = INT64_MAX;
+  p.q_nn = nn;
   return dispatch_gemm<GM_RAGGED_M>(kind, p, static_cast<hipStream_t>(stream));
 }
 

@@ -375,7 +375,9 @@ def _col_operand(t, kind):
 
 @dataclass
 class ExpertWeightOperand:
-    """One expert-weight GEMM operand: E matrices [N, K] (K contiguous)."""
+    """One expert-weight GEMM operand: E matrices [N, K] (K contiguous), or,
+    with ``kmajor``, E matrices stored [K, N] (N contiguous) that the FP8 pow2
+    GEMM reads transposed."""
 
     data: torch.Tensor
     scale: Optional[torch.Tensor]
@@ -387,6 +389,7 @@ class ExpertWeightOperand:
     shift: int = 0
     N: int = 0
     K: int = 0
+    kmajor: bool = False
 
     def operand(self):
         return _operand(self.data, self.scale, ld=self.ld, gs=self.gs, s_row=self.s_row,
@@ -414,7 +417,8 @@ def _timed(name, flops, fn):
 
 def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=None, want=1):
     def launch():
-        _lib.call("fm_grouped_gemm_ragged_m", _gemm_kind(kind), _token_operand(tokens, kind),
+        gk = _gemm_kind(kind) | (_lib.GEMM_W_KMAJOR if w.kmajor else 0)
+        _lib.call("fm_grouped_gemm_ragged_m", gk, _token_operand(tokens, kind),
                   w.operand(), plan.m_tiles, _lib.ptr(plan.tile_expert), _lib.ptr(plan.offsets),
                   plan.num_experts, w.N, w.K,
                   _lib.ptr(mask), want, _lib.ptr(out), _dt(out), out.stride(0), _lib.stream_of(out))
@@ -540,7 +544,20 @@ class ExpertWeights:
 
     The forward pair is always built; the dgrad pair only when ``need_dgrad``
     (a forward that records a backward), from the same read of the weights
-    (the transposed outputs of one launch)."""
+    (the transposed outputs of one launch).
+
+    FP8 pow2 with at most 64 experts, D a multiple of 256 and H >= 256
+    (``kmajor_ok``): only the row operands w13 and w2 are quantised, and w2t /
+    w13t are those same bytes read as [K][N] weights (``kmajor``) -- the
+    128 x 128 blocks of a transpose are the transposed blocks, so the GEMMs
+    give the bits of the transposed copies, and the weight pass writes half
+    the bytes."""
+
+    KMAJOR = True   # class switch: build the transposed copies instead (for comparisons)
+
+    @staticmethod
+    def kmajor_ok(kind: int, E: int, H: int, D: int) -> bool:
+        return (ExpertWeights.KMAJOR and kind == _lib.QUANT_POW2 and E <= 64 and D % 256 == 0 and H >= 256)
 
     def __init__(self, kind: int):
         self.kind = kind
@@ -552,9 +569,9 @@ class ExpertWeights:
         key = tuple((w.data_ptr(), w._version, w.dtype) for w in (w1, w2, w3))
         if key != self.key or (need_dgrad and not self.has_dgrad):
             self.w13 = self.w2t = self.w2 = self.w13t = None
+            self.has_dgrad = need_dgrad
             self._build(w1.detach(), w2.detach(), w3.detach(), E, need_dgrad)
             self.key = key
-            self.has_dgrad = need_dgrad
         return self
 
     def _build(self, w1, w2, w3, E, dgrad=True):
@@ -564,6 +581,9 @@ class ExpertWeights:
         kind = self.kind
         if kind == _lib.QUANT_MX:
             self._build_mx(w1, w2, w3, E, H, D, dgrad)
+            return
+        if self.kmajor_ok(kind, E, H, D):
+            self._build_kmajor(w1, w2, w3, E, H, D)
             return
         pay = torch.bfloat16 if kind == _lib.QUANT_BF16 else torch.uint8
         f32 = torch.float32
@@ -604,6 +624,38 @@ class ExpertWeights:
             self.w13t = ExpertWeightOperand(W13t, S13t, 2 * H, D * 2 * H, 2 * H // 128, 1,
                                             (D // 128) * (2 * H // 128), sh, D, 2 * H)
             self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, (H // 128) * (D // 128), sh, H, D)
+
+    def _build_kmajor(self, w1, w2, w3, E, H, D):
+        """Row operands only (one launch over w1, w3, w2); the down and dX GEMMs
+        read them as [K][N] weights.  Forward and dgrad operands together."""
+        dev = w1.device
+        W13 = torch.empty(E, 2 * H, D, dtype=torch.uint8, device=dev)
+        W2 = torch.empty(E, H, D, dtype=torch.uint8, device=dev)
+        S13 = torch.empty(E, 2 * H // 128, D // 128, dtype=torch.float32, device=dev)
+        S2 = torch.empty(E, H // 128, D // 128, dtype=torch.float32, device=dev)
+        srcs = [w.contiguous() for w in (w1, w3, w2)]
+        if len({w.dtype for w in srcs}) != 1:
+            srcs = [w.float() for w in srcs]
+        kind = self.kind
+
+        def job(src, dst, s, row_off, rows_out):
+            return _lib.FmWeightJob(
+                _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind,
+                _lib.ptr(dst), D, rows_out * D, row_off, _lib.ptr(s), D // 128, (rows_out // 128) * (D // 128),
+                None, 0, 0, 0, None, 0, 0)
+
+        jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, 0, 2 * H), job(srcs[1], W13, S13, H, 2 * H),
+                                      job(srcs[2], W2, S2, 0, H))
+        _lib.call("fm_quantize_weight_batch", jobs, 3, _lib.stream_of(w1))
+        sh = 7
+        g13, g2 = (2 * H // 128) * (D // 128), (H // 128) * (D // 128)
+        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, g13, sh, 2 * H, D)
+        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, g2, sh, H, D)
+        # element (n = d, k) of the [K][N] reading: rows k, column d; scale
+        # block (d >> 7, k >> 7) at s[(k >> 7) * D/128 + (d >> 7)]
+        self.w2t = ExpertWeightOperand(W2, S2, D, H * D, 1, D // 128, g2, sh, D, H, kmajor=True)
+        self.w13t = ExpertWeightOperand(W13, S13, D, 2 * H * D, 1, D // 128, g13, sh, D, 2 * H, kmajor=True)
+        self.has_dgrad = True
 
     def _build_mx(self, w1, w2, w3, E, H, D, dgrad):
         dev = w1.device

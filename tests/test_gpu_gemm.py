@@ -165,3 +165,42 @@ def test_expert_mask_skips_tiles(dev):
     o = out.cpu().numpy()
     assert np.all(o[offs[1]:offs[2]] == 7.0) and np.all(o[offs[3]:offs[4]] == 7.0)
     assert not np.all(o[offs[0]:offs[1]] == 7.0)
+
+
+def _kmajor(w: "ExpertWeightOperand", E):
+    """The [E][K, N] rows operand ``w`` (N = w.K columns) read as [N, K] weights."""
+    from nanopysche_amd.flow_moe import ExpertWeightOperand
+    K, N = w.N, w.K
+    return ExpertWeightOperand(w.data, w.scale, ld=N, gs=K * N, s_row=1, s_kb=N // 128,
+                               s_gs=(K // 128) * (N // 128), shift=7, N=N, K=K, kmajor=True)
+
+
+@pytest.mark.parametrize("E,T,K,zeros,D,H", [(8, 3000, 2, (2, 5), 512, 384), (5, 2500, 3, (0,), 768, 256),
+                                             (64, 6000, 4, (7, 63), 256, 256)])
+def test_ragged_m_kmajor_weights_match(dev, E, T, K, zeros, D, H):
+    """FM_GEMM_W_KMAJOR: the down (w2 rows [H, D]) and dgrad dX (w13 rows
+    [2H, D]) GEMMs reading the row-quantised weights transposed in LDS give the
+    bits of the same GEMMs on the separately quantised transposed copies (the
+    same 128 x 128 blocks, so the same codes and scales)."""
+    x = randn_bf16((T, D), seed=1)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=s, std=0.02) for s in (2, 3, 4))
+    ew = ExpertWeights(_lib.QUANT_POW2).refresh(w1.to(dev), w2.to(dev), w3.to(dev), E)
+    pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity="1x128", pow2_scale=True)
+    plan = pt.plan
+    for kk, w_nt, w_rows in ((H, ew.w2t, ew.w2), (2 * H, ew.w13t, ew.w13)):
+        a = randn_bf16((plan.rows_max, kk), seed=kk).to(dev)
+        aq = fm.quantize_to_fp8(a, "1x128", pow2_scale=True)
+        nn = _kmajor(w_rows, E)
+        assert (nn.N, nn.K) == (w_nt.N, w_nt.K) == (D, kk)
+        for dt in (torch.float32, torch.bfloat16):
+            ref = fm.fp8_grouped_gemm(aq, w_nt, plan, out_dtype=dt)
+            got = fm.fp8_grouped_gemm(aq, nn, plan, out_dtype=dt)
+            offs = plan.offsets.cpu().numpy()
+            for e in range(E):
+                r0, r1 = offs[e], offs[e + 1]
+                assert torch.equal(got[r0:r1], ref[r0:r1]), (kk, dt, e)
+    if H % 256:   # w2t's rows read as [K = D][N = H] weights: N not a multiple of 256 is refused
+        aq = fm.quantize_to_fp8(randn_bf16((plan.rows_max, D), seed=9).to(dev), "1x128", pow2_scale=True)
+        with pytest.raises(RuntimeError, match=r"\[K\]\[N\] weights need"):
+            fm.fp8_grouped_gemm(aq, _kmajor(ew.w2t, E), plan)

@@ -155,19 +155,20 @@ def test_weight_cache_tracks_parameter_updates(dev):
 
 
 @pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("kind", ["block", "pow2", "mx"])
-def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
+@pytest.mark.parametrize("kind,D", [("block", 384), ("pow2", 384), ("pow2", 512), ("mx", 384)])
+def test_weight_cache_quantises_parameter_values(dev, kind, D, param_dtype):
     """The cached gate|up and down operands are the parameters' own values
     quantised (fp32 master weights are not rounded to bf16 first): bytes and
     scales equal the oracle quantiser applied to the [E, 2H, D] stack of w1|w3
-    (128x128 blocks, or 1x32 for MX) and to w2."""
+    (128x128 blocks, or 1x32 for MX) and to w2.  pow2 with D a multiple of 256
+    keeps no transposed copies: w2t / w13t read the row operands as [K][N]."""
     import numpy as np
 
     from nanopysche_amd import _lib
     from nanopysche_amd.flow_moe import ExpertWeights
     from oracle import fp8 as ofp8
 
-    E, H, D = 3, 256, 384
+    E, H = 3, 256
     g = torch.Generator().manual_seed(5)
     w1, w2, w3 = ((torch.randn(E * H, D, generator=g) * 0.02).to(param_dtype) for _ in range(3))
     k = {"block": _lib.QUANT_BLOCK, "pow2": _lib.QUANT_POW2, "mx": _lib.QUANT_MX}[kind]
@@ -188,8 +189,14 @@ def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
     # the dgrad operands: w13t [E][D, 2H] and w2t [E][D, H] (128x128 blocks of
     # each expert's transpose; for MX the 32x1 column blocks of the whole
     # [E*2H, D] / [E*H, D] stack, stored transposed)
+    assert ew.w2t.kmajor == ew.w13t.kmajor == (kind == "pow2" and D % 256 == 0)
     for op, src, n in ((ew.w13t, W13, 2 * H), (ew.w2t, f(w2).reshape(E * H, D), H)):
-        if kind == "mx":
+        if op.kmajor:
+            rows = ew.w13 if n == 2 * H else ew.w2
+            assert op.data.data_ptr() == rows.data.data_ptr() and op.scale.data_ptr() == rows.scale.data_ptr()
+            assert (op.N, op.K, op.ld, op.gs, op.s_row, op.s_kb, op.s_gs, op.shift) == \
+                (D, n, D, n * D, 1, D // 128, (n // 128) * (D // 128), 7)
+        elif kind == "mx":
             qt, ct = ofp8.quant_mx_32x1(src)
             assert np.array_equal(op.data.reshape(D, E * n).cpu().numpy(), qt)
             assert np.array_equal(op.scale.reshape(E * n // 32, D).cpu().numpy(), ct)
@@ -202,10 +209,15 @@ def test_weight_cache_quantises_parameter_values(dev, kind, param_dtype):
                 assert np.array_equal(scale[e], s), e
 
 
-def test_forward_without_grad_builds_forward_operands_only(dev):
+@pytest.mark.parametrize("kmajor", [True, False])
+def test_forward_without_grad_builds_forward_operands_only(dev, kmajor, monkeypatch):
     """A no_grad forward quantises only the forward weight operands (w13,
     w2t) and no column blocks; a later forward that records a backward
-    builds the dgrad operands and gives the same output."""
+    builds the dgrad operands and gives the same output.  With [K][N]
+    weights (kmajor) the forward's row operands are the dgrad's too."""
+    from nanopysche_amd.flow_moe import ExpertWeights
+
+    monkeypatch.setattr(ExpertWeights, "KMAJOR", kmajor)
     T, D, H, E, K = 512, 256, 256, 4, 2
     x, w, idx, w1, w2, w3, go = _case(T, D, H, E, K, seed=12)
     cfg = fm.FP8FlowMoEConfig(True, fm.FP8RecipeConfig(True, fm.FP8RecipeType.FLOW_MOE))
@@ -215,7 +227,11 @@ def test_forward_without_grad_builds_forward_operands_only(dev):
     with torch.no_grad():
         a = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
     ew = next(iter(blk._cache.values()))
-    assert ew.w13 is not None and ew.w2t is not None and ew.w13t is None and ew.w2 is None
+    assert ew.w2t.kmajor == kmajor
+    if kmajor:   # the row operands serve the forward and the dgrad GEMMs alike
+        assert ew.has_dgrad and ew.w13t.data is ew.w13.data and ew.w2t.data is ew.w2.data
+    else:
+        assert ew.w13 is not None and ew.w2t is not None and ew.w13t is None and ew.w2 is None
     b = blk(x.to(dev), w.to(dev), idx.to(dev), 0, E)
     b.backward(go.to(dev))
     assert ew.has_dgrad and ew.w13t is not None and ew.w2 is not None
