@@ -830,7 +830,8 @@ def main():
                     help="time eagerly issued steps instead of replays of the step captured as a HIP graph "
                          "(configs[2], configs[0], shared expert)")
     ap.add_argument("--no-overlap", action="store_true",
-                    help="keep every launch on one stream (no dW2 / dH overlap)")
+                    help="keep every launch on one stream (the router's backward not beside the dY "
+                         "permute and dH + dW2; MX: no dW2 / dH overlap)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")

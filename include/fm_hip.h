@@ -444,6 +444,25 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
                              void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
                              int64_t ld_out, void* stream);
 
+/* fm_grouped_gemm_ragged_m followed by fm_grouped_gemm_ragged_k on the same
+ * stream, with the same offsets, E and expert mask, as one grid: for a
+ * backward's dgrad dH = dY w2_e (reference model/moe.py:1588-1591, the bmm's
+ * input gradient) and the weight gradient dW2 = h^T dY (the bmm's weight
+ * gradient), which read the same permuted dY and are independent.  Run back
+ * to back each leaves its last round of tiles part-empty; in one grid the
+ * weight-gradient tiles fill the dgrad's last round.  The arguments are those
+ * of the two entries (M2, N2, out2 ... ld_out2: fm_grouped_gemm_ragged_k's M,
+ * N, out ... ld_out); `kind` takes FM_GEMM_A_FAST for the weight gradient and
+ * FM_GEMM_W_KMAJOR for the dgrad.  The outputs equal those of the two calls
+ * bit for bit.  Kinds other than BF16 and FP8 pow2, and [K][N] weights, run
+ * as the two launches. */
+int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
+                               int64_t m_tiles, const int32_t* tile_expert, int64_t N, int64_t K, void* out,
+                               int out_dtype, int64_t ld_out, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                               int64_t M2, int64_t N2, void* out2, int64_t out2_gs, void* out2b, int64_t out2b_gs,
+                               int64_t split_rows, int out2_dtype, int64_t ld_out2, const int32_t* offsets, int E,
+                               const int32_t* expert_mask, int mask_want, void* stream);
+
 /* fm_grouped_gemm_ragged_k with each expert's token range cut into `splits`
  * slices on its 128-row grid, for launches with fewer output tiles than CUs
  * (one group, as for a shared expert, or few small experts): the slices'

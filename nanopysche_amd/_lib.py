@@ -129,6 +129,9 @@ SIGNATURES = {
                                         _i32, _vp, _i32, _i64, _vp]),
     "fm_grouped_gemm_ragged_k": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,
                                         _i64, _vp, _i64, _i64, _i32, _i64, _vp]),
+    "fm_grouped_gemm_ragged_m_k": (_i32, [_i32, _OPND, _OPND, _i64, _vp, _i64, _i64, _vp, _i32, _i64,
+                                          _OPND, _OPND, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i64,
+                                          _vp, _i32, _vp, _i32, _vp]),
     "fm_grouped_gemm_ragged_k_split_workspace_bytes": (_i64, [_i32, _i64, _i64, _i32]),
     "fm_grouped_gemm_ragged_k_split": (_i32, [_i32, _OPND, _OPND, _vp, _i32, _i64, _i64, _vp, _i32, _vp,
                                               _i64, _vp, _i64, _i64, _i32, _i64, _i32, _vp, _i64, _vp]),

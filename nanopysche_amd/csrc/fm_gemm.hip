@@ -548,7 +548,7 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 }
 
 template <int MODE>
-__device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) {
+__device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t, int64_t bid) {
   const int64_t NI = (p.n_i + kT - 1) / kT;
   int64_t JT = 0, L;
   // Experts masked out (the other precision's launch) own no tiles here, so
@@ -576,12 +576,12 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
     }
     const int64_t n_valid = JT * NI;
     const int64_t per_xcd = (n_valid + 7) / 8;
-    const int64_t k = blockIdx.x / 8;
+    const int64_t k = bid / 8;
     if (k >= per_xcd) return false;
-    L = int64_t(blockIdx.x % 8) * per_xcd + k;
+    L = (bid % 8) * per_xcd + k;
     if (L >= n_valid) return false;
   } else {
-    L = blockIdx.x;
+    L = bid;
     if (p.rk_xcd && p.mask == nullptr && p.E <= 64) {
       int rows = lane < p.E ? p.offsets[lane + 1] - p.offsets[lane] : 0;
       int sum = rows, mx = rows;
@@ -592,7 +592,7 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
       }
       if (__builtin_amdgcn_readfirstlane(int(int64_t(mx) * p.E * 8 <= int64_t(sum) * 9))) {
         const int64_t per_xcd = (p.n_tiles + 7) / 8;
-        L = int64_t(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+        L = (bid % 8) * per_xcd + bid / 8;
       }
     }
     if (L >= p.n_tiles) return false;
@@ -663,19 +663,19 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t) 
   return true;
 }
 
-// MXL (MX only): scale layouts, bit 0 = Q scales k-major, bit 1 = P scales
-// k-major (row-major otherwise); fixed per instantiation so the unused
-// address path costs no registers.
+// One 256 x 256 output tile of launch `p` (block index `bid` of that launch,
+// two LDS stages at `smem`).  MXL (MX only): scale layouts, bit 0 = Q scales
+// k-major, bit 1 = P scales k-major (row-major otherwise); fixed per
+// instantiation so the unused address path costs no registers.
 template <int KIND, int MODE, int MXL = 0>
-__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
+__device__ __forceinline__ void gemm256_tile(const GemmParams& p, int64_t bid, uint8_t* smem) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;         // element size
   constexpr int KSTEP = 128 / ES;                     // elements per 128-byte K step
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage];
 
   Tile256 tile;
   tile.slice = 0;
-  if (!decode_tile256<MODE>(p, tile)) return;
+  if (!decode_tile256<MODE>(p, tile, bid)) return;
   const int64_t e = tile.e, i0 = tile.i0, j0 = tile.j0, j_end = tile.j_end, k_lo = tile.k_lo, k_hi = tile.k_hi;
 
   WaveCoord w;
@@ -824,6 +824,25 @@ __global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) =
             make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+}
+
+template <int KIND, int MODE, int MXL = 0>
+__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * Smem256<KIND>::kStage];
+  gemm256_tile<KIND, MODE, MXL>(p, blockIdx.x, smem);
+}
+
+// A ragged-M launch (blocks [0, nbm), nbm a multiple of 8 so both keep their
+// XCD mapping) and a ragged-K launch (the blocks after it) as one grid: the
+// dgrad dH = dY w2 and the weight gradient dW2 read the same permuted dY and
+// are independent, and run back to back each leaves its last round of tiles
+// part-empty (1.5 rounds each at configs[2]'s shapes; 3 rounds together).
+template <int KIND>
+__global__ __launch_bounds__(512) void gemm256_mk_kernel(GemmParams pm, GemmParams pk, int64_t nbm) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * Smem256<KIND>::kStage];
+  const int64_t b = blockIdx.x;
+  if (b < nbm) gemm256_tile<KIND, GM_RAGGED_M>(pm, b, smem);
+  else gemm256_tile<KIND, GM_RAGGED_K>(pk, b - nbm, smem);
 }
 
 // ============================================================================
@@ -1388,6 +1407,16 @@ inline bool gemm_rk_xcd_split() {
   return on;
 }
 
+// fm_grouped_gemm_ragged_m_k runs its two launches as one grid unless
+// FM_GEMM_MK=0 (then back to back; read once).
+inline bool gemm_mk_one_grid() {
+  static const bool on = [] {
+    const char* e = getenv("FM_GEMM_MK");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
 // Ragged-M launches are persistent unless FM_GEMM_PERSISTENT=0 (read once).
 inline bool gemm_persistent() {
   static const bool on = [] {
@@ -1454,8 +1483,9 @@ inline void launch256(int kind, dim3 grid, const GemmParams& p, hipStream_t s) {
   }
 }
 
+// Launch-independent preparation: operand sides, tile count, tile order.
 template <int MODE>
-int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
+int prepare_gemm(int kind, GemmParams& p) {
   if (kind < GK_BF16 || kind > GK_FP8_MX) {
     set_error("grouped gemm: unknown kind %d", kind);
     return 1;
@@ -1479,9 +1509,15 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
     p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256
                                     : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT) * p.splits;
   }
-  if (p.n_tiles == 0) return 0;
   p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
   p.w_fast = MODE == GM_RAGGED_M && gemm_weight_fast(p.n_i * p.K * (kind == GK_BF16 ? 2 : 1)) ? 1 : 0;
+  return 0;
+}
+
+template <int MODE>
+int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
+  if (int rc = prepare_gemm<MODE>(kind, p)) return rc;
+  if (p.n_tiles == 0) return 0;
   const dim3 grid(unsigned((p.n_tiles + 7) / 8 * 8)), block(256);
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
@@ -1576,12 +1612,17 @@ using namespace fm;
 
 extern "C" {
 
-int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
-                             int64_t m_tiles, const int32_t* tile_expert, const int32_t* offsets,
-                             int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
-                             void* out, int out_dtype, int64_t ld_out, void* stream) {
-  const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
-  kind &= ~FM_GEMM_W_KMAJOR;
+}  // extern "C"
+
+namespace {
+
+// Checks the ragged-M arguments and fills the launch parameters (`kind`
+// without flags; nn: the weights are stored [K][N]).  Returns 0 with
+// p.m_tiles == 0 when there is nothing to do.
+int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmOperand* weights, int64_t m_tiles,
+                    const int32_t* tile_expert, const int32_t* offsets, int E, int64_t N, int64_t K,
+                    const int32_t* expert_mask, int mask_want, void* out, int out_dtype, int64_t ld_out,
+                    GemmParams& p) {
   FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
   FM_REQUIRE(!nn || (kind == GK_FP8_POW2 && E <= 64 && N % 256 == 0 && K >= 256 && weights->ld >= N &&
                      weights->group_stride >= K * weights->ld),
@@ -1601,8 +1642,9 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_m: bad out dtype");
   FM_REQUIRE(kind != GK_FP8_F32 || weights->scale_row_shift == 7,
              "fm_grouped_gemm_ragged_m: fp32-scaled weights must use 128-row scale blocks");
+  p = GemmParams{};
+  p.m_tiles = m_tiles;
   if (m_tiles == 0) return 0;
-  GemmParams p{};
   p.P = make_operand(*tokens);
   p.Q = make_operand(*weights);
   p.n_i = N;
@@ -1620,6 +1662,24 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
   p.out_f32 = out_dtype == FM_DTYPE_F32;
   p.split = INT64_MAX;
   p.q_nn = nn;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
+                             int64_t m_tiles, const int32_t* tile_expert, const int32_t* offsets,
+                             int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
+                             void* out, int out_dtype, int64_t ld_out, void* stream) {
+  const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
+  kind &= ~FM_GEMM_W_KMAJOR;
+  GemmParams p;
+  if (int rc = ragged_m_params(kind, nn, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
+                               mask_want, out, out_dtype, ld_out, p))
+    return rc;
+  if (p.m_tiles == 0) return 0;
   return dispatch_gemm<GM_RAGGED_M>(kind, p, static_cast<hipStream_t>(stream));
 }
 
@@ -1679,6 +1739,39 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
     return rc;
   p.rk_jfast = a_fast;
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
+}
+
+int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
+                               int64_t m_tiles, const int32_t* tile_expert, int64_t N, int64_t K, void* out,
+                               int out_dtype, int64_t ld_out, const FmGemmOperand* a_t, const FmGemmOperand* b_t,
+                               int64_t M2, int64_t N2, void* out2, int64_t out2_gs, void* out2b, int64_t out2b_gs,
+                               int64_t split_rows, int out2_dtype, int64_t ld_out2, const int32_t* offsets, int E,
+                               const int32_t* expert_mask, int mask_want, void* stream) {
+  const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
+  const int a_fast = (kind & FM_GEMM_A_FAST) != 0;
+  kind &= ~(FM_GEMM_W_KMAJOR | FM_GEMM_A_FAST);
+  GemmParams pm, pk;
+  if (int rc = ragged_m_params(kind, nn, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
+                               mask_want, out, out_dtype, ld_out, pm))
+    return rc;
+  if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M2, N2, expert_mask, mask_want, out2, out2_gs, out2b,
+                               out2b_gs, split_rows, out2_dtype, ld_out2, pk))
+    return rc;
+  pk.rk_jfast = a_fast;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nn || pm.m_tiles == 0 || (kind != GK_BF16 && kind != GK_FP8_POW2) || !gemm_mk_one_grid()) {
+    if (pm.m_tiles > 0)
+      if (int rc = dispatch_gemm<GM_RAGGED_M>(kind, pm, s)) return rc;
+    return dispatch_gemm<GM_RAGGED_K>(kind, pk, s);
+  }
+  if (int rc = prepare_gemm<GM_RAGGED_M>(kind, pm)) return rc;
+  if (int rc = prepare_gemm<GM_RAGGED_K>(kind, pk)) return rc;
+  const int64_t nbm = (pm.n_tiles + 7) / 8 * 8, nbk = (pk.n_tiles + 7) / 8 * 8;
+  if (nbm + nbk == 0) return 0;
+  const dim3 grid(unsigned(nbm + nbk)), block(512);
+  if (kind == GK_BF16) hipLaunchKernelGGL((gemm256_mk_kernel<GK_BF16>), grid, block, 0, s, pm, pk, nbm);
+  else hipLaunchKernelGGL((gemm256_mk_kernel<GK_FP8_POW2>), grid, block, 0, s, pm, pk, nbm);
+  return check_launch("fm_grouped_gemm_ragged_m_k");
 }
 
 int64_t fm_grouped_gemm_ragged_k_split_workspace_bytes(int E, int64_t M, int64_t N, int splits) {

@@ -499,6 +499,29 @@ def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out
            2.0 * plan.num_tokens * plan.top_k * M * N, launch)
 
 
+# Kinds whose dgrad and weight-gradient launches can share one grid
+# (fm_grouped_gemm_ragged_m_k); the others run them on two streams.
+_MK_KINDS = (_lib.QUANT_BF16, _lib.QUANT_POW2)
+
+
+def _gemm_mk(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, a_t, b_t, M2, N2, out2, out2_gs,
+             mask=None, want=1, a_cold=False):
+    """_gemm_m(kind, tokens, w, plan, out) and the unsplit _gemm_k(kind, a_t,
+    b_t, plan, M2, N2, out2, out2_gs) as one grid: the weight-gradient tiles
+    fill the last round of the dgrad's."""
+    gk = (_gemm_kind(kind) | (_lib.GEMM_W_KMAJOR if w.kmajor else 0) | (_lib.GEMM_A_FAST if a_cold else 0))
+
+    def launch():
+        _lib.call("fm_grouped_gemm_ragged_m_k", gk, _token_operand(tokens, kind), w.operand(), plan.m_tiles,
+                  _lib.ptr(plan.tile_expert), w.N, w.K, _lib.ptr(out), _dt(out), out.stride(0),
+                  _col_operand(a_t, kind), _col_operand(b_t, kind), M2, N2, _lib.ptr(out2), out2_gs, None, 0, M2,
+                  _dt(out2), N2, _lib.ptr(plan.offsets), plan.num_experts, _lib.ptr(mask), want,
+                  _lib.stream_of(out))
+
+    _timed(f"grouped_gemm_ragged_m_k/{_KIND_NAME[kind]}",
+           2.0 * plan.num_tokens * plan.top_k * (w.N * w.K + M2 * N2), launch)
+
+
 def _dt(t):
     if t.dtype == torch.float32:
         return _lib.DTYPE_F32
@@ -946,17 +969,25 @@ class FP8FlowMoECompute:
         dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                       return_transpose=True, weights=None if self._dense else wts,
                                       kmajor_scales=True) for kind, _ in runs}
-        # dW2 (contraction over each expert's tokens) runs on the second stream
-        # beside dH: each alone leaves the last round of workgroups part-empty
-        # when the hidden size is not a multiple of the 256-wide tile.  There
-        # it takes no K split: the CUs it leaves idle run dH.
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            for kind, want in runs:
-                # the forward's saved SwiGLU columns are the operand not in cache
-                _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
-                        want=want, may_split=side is main, a_cold=True)
-        for kind, want in runs:
+        # dH and dW2 (contraction over each expert's tokens) both read the
+        # permuted dY: each alone leaves its last round of workgroups
+        # part-empty when the hidden size is not a multiple of the 256-wide
+        # tile.  One grid holds both (BF16, pow2); the other kinds run dW2 on
+        # the second stream beside dH, with no K split (the CUs it leaves idle
+        # run dH).  The forward's saved SwiGLU columns are dW2's operand not
+        # in cache.
+        one_grid = [(k, w) for k, w in runs if k in _MK_KINDS]
+        two_streams = [(k, w) for k, w in runs if k not in _MK_KINDS]
+        if two_streams:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                for kind, want in two_streams:
+                    _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
+                            want=want, may_split=side is main, a_cold=True)
+        for kind, want in one_grid:
+            _gemm_mk(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, ctx.saved_hcols[kind],
+                     dy[kind].rows_t, H, D, dW2, H * D, mask, want, a_cold=True)
+        for kind, want in two_streams:
             _gemm_m(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, mask, want)
         if self.capture_intermediates is not None:
             self.capture_intermediates["dh"] = dH.detach().clone()

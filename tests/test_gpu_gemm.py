@@ -204,3 +204,52 @@ def test_ragged_m_kmajor_weights_match(dev, E, T, K, zeros, D, H):
         aq = fm.quantize_to_fp8(randn_bf16((plan.rows_max, D), seed=9).to(dev), "1x128", pow2_scale=True)
         with pytest.raises(RuntimeError, match=r"\[K\]\[N\] weights need"):
             fm.fp8_grouped_gemm(aq, _kmajor(ew.w2t, E), plan)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "pow2", "mx"])
+@pytest.mark.parametrize("E,T,K,zeros,D,H,masked", [(8, 3000, 2, (2, 5), 512, 384, False),
+                                                    (6, 2500, 2, (4,), 256, 256, True),
+                                                    (80, 3000, 2, (3, 70), 256, 256, False)])
+def test_ragged_m_k_one_grid_matches_two_launches(dev, kind, E, T, K, zeros, D, H, masked):
+    """fm_grouped_gemm_ragged_m_k (dH = dY w2 and dW2 = h^T dY in one grid
+    for BF16 and pow2; MX runs the two launches) writes the bits of
+    fm_grouped_gemm_ragged_m then fm_grouped_gemm_ragged_k, zero-token experts
+    (dW2 zeros), masked experts (untouched) and more than 64 experts
+    included."""
+    from nanopysche_amd.flow_moe import _gemm_m, _gemm_mk
+    k = KINDS[kind]
+    gran = {"bf16": None, "pow2": "1x128", "mx": "1x32"}[kind]
+    dy = randn_bf16((T, D), seed=11)
+    hh = randn_bf16((T, H), seed=12)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E + 1, zero_experts=zeros)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=s, std=0.02) for s in (2, 3, 4))
+    ew = ExpertWeights(k).refresh(w1.to(dev), w2.to(dev), w3.to(dev), E)
+    pd = fm.fused_permute_pad(dy.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True, kmajor_scales=True)
+    ph = fm.fused_permute_pad(hh.to(dev), pd.plan, E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True)
+    plan = pd.plan
+    mask = None
+    if masked:
+        mask = torch.tensor([e % 2 for e in range(E)], dtype=torch.int32, device=dev)
+    R = plan.rows_max
+    outs = []
+    for one_grid in (False, True):
+        dH = torch.full((R, H), 7.0, dtype=torch.bfloat16, device=dev)
+        dW2 = torch.full((E * H, D), 7.0, dtype=torch.float32, device=dev)
+        if one_grid:
+            _gemm_mk(k, pd.rows, ew.w2, plan, dH, ph.rows_t, pd.rows_t, H, D, dW2, H * D, mask, 1, a_cold=True)
+        else:
+            _gemm_m(k, pd.rows, ew.w2, plan, dH, mask, 1)
+            _gemm_k(k, ph.rows_t, pd.rows_t, plan, H, D, dW2, H * D, mask=mask, want=1, may_split=False,
+                    a_cold=True)
+        outs.append((dH, dW2))
+    (h0, w0), (h1, w1_) = outs
+    used = int(plan.offsets[-1].item())
+    assert torch.equal(h0[:used], h1[:used]) and torch.equal(w0, w1_)
+    offs = plan.offsets.cpu().numpy()
+    for e in range(E):
+        if mask is not None and e % 2 == 0:   # left to the other precision's launch
+            assert torch.all(w1_[e * H:(e + 1) * H] == 7.0) and torch.all(h1[offs[e]:offs[e + 1]] == 7.0)
+        elif offs[e + 1] == offs[e]:
+            assert torch.all(w1_[e * H:(e + 1) * H] == 0)
