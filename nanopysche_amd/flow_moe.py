@@ -972,12 +972,15 @@ class FP8FlowMoECompute:
         # dH and dW2 (contraction over each expert's tokens) both read the
         # permuted dY: each alone leaves its last round of workgroups
         # part-empty when the hidden size is not a multiple of the 256-wide
-        # tile.  One grid holds both (BF16, pow2); the other kinds run dW2 on
-        # the second stream beside dH, with no K split (the CUs it leaves idle
-        # run dH).  The forward's saved SwiGLU columns are dW2's operand not
-        # in cache.
-        one_grid = [(k, w) for k, w in runs if k in _MK_KINDS]
-        two_streams = [(k, w) for k, w in runs if k not in _MK_KINDS]
+        # tile.  One grid holds both (BF16, pow2) when dW2's tiles fill at
+        # least a round of the GPU's CUs; otherwise (a few long tiles, as for
+        # a shared expert's one group) and for the other kinds dW2 runs on the
+        # second stream beside dH and what follows it, with no K split (the
+        # CUs it leaves idle run the main stream).  The forward's saved SwiGLU
+        # columns are dW2's operand not in cache.
+        fill = E * -(-H // 256) * -(-D // 256) >= _cus(dev)
+        one_grid = [(k, w) for k, w in runs if k in _MK_KINDS and fill]
+        two_streams = [(k, w) for k, w in runs if (k, w) not in one_grid]
         if two_streams:
             side.wait_stream(main)
             with torch.cuda.stream(side):
