@@ -389,6 +389,124 @@ __global__ __launch_bounds__(256) void sort_scatter_kernel(const I* idx, int64_t
   }
 }
 
+// sort_scan_kernel and sort_scatter_kernel as one launch for at most
+// kFusedBlocks blocks and kFusedExperts experts: each workgroup re-derives
+// what the scan would hand it from the block table -- the expert totals,
+// its own block prefix, the padded group starts -- so no workgroup waits on
+// another.  Workgroup 0 writes counts, offsets, the m-tile table and the
+// FP8 flags; the -1 of assign_of_row goes only to pad rows (after each
+// group's last assignment, and past the last group), which the scatter
+// never writes, split over the workgroups.  Same outputs as the two kernels.
+constexpr int64_t kFusedBlocks = 64;
+constexpr int kFusedExperts = 256;
+
+template <typename I>
+__global__ __launch_bounds__(256) void sort_scan_scatter_kernel(const I* idx, int64_t A, int E,
+                                                                const int32_t* block_hist, int64_t n_blocks,
+                                                                int32_t* counts, int32_t* offsets,
+                                                                int32_t* tile_expert, int64_t n_tiles_max,
+                                                                int32_t* row_of, int32_t* assign_of_row,
+                                                                int64_t rows_max, int32_t* use_fp8,
+                                                                int64_t threshold) {
+  __shared__ int32_t base[4][kFusedExperts];   // per-wave counts, then per-wave next rows
+  __shared__ int32_t start[kFusedExperts + 1];  // padded group starts; start[E] = rows used
+  __shared__ int32_t wtot[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbits = expert_bits(E);
+  for (int i = tid; i < 4 * kFusedExperts; i += 256) (&base[0][0])[i] = 0;
+  // thread e: expert e's total and this block's prefix from the block table
+  int32_t tot = 0, pre = 0;
+  if (tid < E) {
+    const int32_t* h = block_hist + int64_t(tid) * n_blocks;
+    for (int64_t b0 = 0; b0 < n_blocks; b0 += 16) {
+      int32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = b0 + u < n_blocks ? h[b0 + u] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        tot += v[u];
+        if (b0 + u < int64_t(blockIdx.x)) pre += v[u];
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t q0 = int64_t(blockIdx.x) * kSortBlock + int64_t(wave) * (kSortBlock / 4);
+  for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
+    const int64_t a = q0 + i0 + lane;
+    const int e = a < A ? load_expert(idx, a, E) : -1;
+    const uint64_t peers = expert_peers(e, nbits);
+    if (e >= 0 && (peers & lanemask_lt()) == 0) atomicAdd(&base[wave][e], __popcll(peers));
+  }
+  // group starts: exclusive scan of the padded totals over the experts
+  const int32_t pad = tid < E ? (tot + 127) / 128 * 128 : 0;
+  int32_t incl = pad;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wtot[w];
+  const int32_t st = before + incl - pad;
+  if (tid < E) start[tid] = st;
+  if (tid == 0) start[E] = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+  if (tid < E) {   // this wave-quarter's first rows: group start + block prefix + earlier quarters
+    int32_t run = st + pre;
+    for (int w = 0; w < 4; ++w) {
+      const int32_t c = base[w][tid];
+      base[w][tid] = run;
+      run += c;
+    }
+    if (blockIdx.x == 0) {
+      counts[tid] = tot;
+      if (use_fp8) use_fp8[tid] = int64_t(tot) >= threshold ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  const int32_t used = start[E];
+  if (blockIdx.x == 0) {
+    for (int e = tid; e <= E; e += 256) offsets[e] = start[e];
+    for (int64_t m = tid; m < n_tiles_max; m += 256) {
+      int32_t ex = -1;
+      if (m * 128 < used) {   // last e with start[e] <= 128 m
+        int lo = 0, hi = E - 1;
+        const int32_t r = int32_t(m * 128);
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (start[mid] <= r) lo = mid; else hi = mid - 1;
+        }
+        ex = lo;
+      }
+      tile_expert[m] = ex;
+    }
+  }
+  // pad rows: expert e's (fewer than 128) go to workgroup e % n_blocks, the
+  // rows past the last group are strided over all workgroups
+  if (tid < E && tid % n_blocks == int64_t(blockIdx.x)) {
+    for (int32_t r = st + tot; r < start[tid + 1]; ++r) assign_of_row[r] = -1;
+  }
+  for (int64_t r = used + int64_t(blockIdx.x) * 256 + tid; r < rows_max; r += n_blocks * 256) assign_of_row[r] = -1;
+  for (int i0 = 0; i0 < kSortBlock / 4; i0 += 64) {
+    const int64_t a = q0 + i0 + lane;
+    const int e = a < A ? load_expert(idx, a, E) : -1;
+    const uint64_t peers = expert_peers(e, nbits);
+    int32_t my_base = 0;
+    if (e >= 0) my_base = base[wave][e];
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) {
+      const int32_t row = my_base + __popcll(peers & lanemask_lt());
+      row_of[a] = row;
+      assign_of_row[row] = int32_t(a);
+      if ((peers & lanemask_lt()) == 0) base[wave][e] = my_base + __popcll(peers);
+    } else if (a < A) {
+      row_of[a] = -1;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // -------------------------------------------------------------- permute ----
 // Row r of the padded buffer is x[assign_of_row[r] / K] (times the router
 // weight of that assignment when WEIGHTED), zeros for pad rows.  Branch-free:
@@ -715,9 +833,20 @@ __global__ __launch_bounds__(256) void router_grad_kernel(const uint16_t* __rest
 }
 
 // ----------------------------------------------------- sort launcher ----
-// The three sort kernels on one stream.  block_hist ([E][blocks] int32) is
-// written in full by sort_hist_kernel before anything reads it, so the
-// buffer needs no clearing.
+// Small sorts take the fused scan + scatter unless FM_ROUTE_FUSED_SCAN=0
+// (read once).
+inline bool gemm_route_fused_scan() {
+  static const bool on = [] {
+    const char* e = getenv("FM_ROUTE_FUSED_SCAN");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
+// The sort kernels on one stream: histograms, then the scan and the scatter
+// (one launch for small sorts).  block_hist ([E][blocks] int32) is written in
+// full by sort_hist_kernel before anything reads it, so the buffer needs no
+// clearing.
 static int route_sort_launch(const void* indices, int indices_i64, int64_t T, int K, int E,
                              int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
                              int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
@@ -737,6 +866,17 @@ static int route_sort_launch(const void* indices, int indices_i64, int64_t T, in
       hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
                          static_cast<const int32_t*>(indices), A, E, bh, nb);
     if (int rc = check_launch(what)) return rc;
+  }
+  if (nb > 0 && nb <= kFusedBlocks && E <= kFusedExperts && gemm_route_fused_scan()) {
+    if (indices_i64)
+      hipLaunchKernelGGL(sort_scan_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int64_t*>(indices), A, E, bh, nb, counts, offsets, tile_expert,
+                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold);
+    else
+      hipLaunchKernelGGL(sort_scan_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+                         static_cast<const int32_t*>(indices), A, E, bh, nb, counts, offsets, tile_expert,
+                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold);
+    return check_launch(what);
   }
   hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
                      tile_expert, rows_max / 128, assign_of_row, rows_max, use_fp8, threshold);

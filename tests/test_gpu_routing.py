@@ -58,6 +58,11 @@ CASES = [
     (8192, 8, 2, 0.0, ()),
     (16384, 8, 2, 1.1, ()),
     (8192, 256, 8, 1.2, (0, 5, 17)),
+    # the scan folded into the scatter: at most 64 blocks of 1024 assignments
+    # and 256 experts (this case at both limits), then just past each
+    (8192, 256, 8, 1.2, (0, 5, 255)),
+    (8193, 8, 8, 0.0, ()),
+    (2000, 300, 4, 1.1, (7,)),
     (1000, 32, 8, 1.2, (1, 2)),
     (7, 8, 2, 0.0, ()),
     (1, 1, 1, 0.0, ()),
