@@ -775,7 +775,8 @@ class FP8FlowMoECompute:
         # ("gate_up") and backward the bf16 dH GEMM output ("dh"), [rows_max, *];
         # used by parity tests to feed a CPU oracle the device's own GEMM results.
         self.capture_intermediates = None
-        # Run the dW2 grouped GEMM on a second stream beside dH (False keeps
+        # Run the router's backward (and dW2 where it does not share dH's
+        # grid) on a second stream beside the main stream's work (False keeps
         # every launch on the caller's stream).
         self.overlap_streams = True
         # One group, every token in it with weight 1 (set by
@@ -798,29 +799,6 @@ class FP8FlowMoECompute:
         if ew is None:
             ew = self._cache[kind] = ExpertWeights(kind)
         return ew.refresh(*self._w, self.num_experts, need_dgrad)
-
-    def prefetch_weights(self, num_assignments: int) -> None:
-        """While a HIP graph is being captured: re-quantises the expert weights
-        (when they changed) on the second stream, a branch of the graph beside
-        what the caller issues next (the router and the routing sort); the next
-        forward waits for it before its first GEMM.  Eagerly issued steps keep
-        the re-quantisation inline: beside the router kernels on a second
-        stream it measured 0.89 against 0.82 ms per C3 step, while a replayed
-        graph gains ~1%."""
-        if (not self.overlap_streams or self._w is None
-                or not torch.cuda.is_current_stream_capturing()):
-            return
-        dev = self._w[0].device
-        main = torch.cuda.current_stream(dev)
-        side = _side_stream(dev)
-        side.wait_stream(main)
-        fp8_kind, use_bf16 = self.modes(num_assignments)
-        with torch.cuda.stream(side):
-            for kind in (fp8_kind, _lib.QUANT_BF16 if use_bf16 else None):
-                if kind is not None:
-                    self._weights(kind, self._record)
-        self._wq_event = torch.cuda.Event()
-        self._wq_event.record(side)
 
     def modes(self, num_assignments: int):
         """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
@@ -883,9 +861,6 @@ class FP8FlowMoECompute:
             ew = self._weights(kind, self._record)
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                    return_transpose=self._record, kmajor_scales=True)
-            if getattr(self, "_wq_event", None) is not None:   # weights re-quantised on the second stream
-                torch.cuda.current_stream(dev).wait_event(self._wq_event)
-                self._wq_event = None
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}

@@ -5,13 +5,13 @@ autograd, ctypes argument packing, tensor allocation) takes about as long as
 the kernels themselves at configs[2]'s shapes, so an eagerly issued step is
 bound by the host.  Captured once with ``torch.cuda.graph`` (HIP graphs on
 ROCm), the step replays all of its kernels -- expert-weight re-quantisation,
-routing, the expert block and its backward, the second stream's dW2 -- with
-no host work between them.
+routing, the expert block and its backward, the router's backward on a
+second stream -- with no host work between them.
 
 The library's kernels suit capture: no entry point allocates, synchronises,
 copies to the host or records a memset (scratch is cleared by kernels), and
-every launch goes to the caller's current stream (dW2 to a second stream
-joined by events, which the capture follows).
+every launch goes to the caller's current stream (the router's backward to a
+second stream joined by events, which the capture follows).
 """
 
 from __future__ import annotations

@@ -45,7 +45,6 @@ class _MoELayerFunction(torch.autograd.Function):
         if x2.dtype != torch.bfloat16:
             x2 = x2.to(torch.bfloat16)
         x2 = x2.contiguous()
-        layer.block.prefetch_weights(x2.shape[0] * layer.top_k)
         w, idx, aux, state = router_forward(x2, gate_weight, gate_bias, layer.score_bias, layer.top_k, layer.gating,
                                             replay, layer.normalize_expert_weights, layer.z_loss_multiplier, tracker)
         need_x, need_gw, need_gb = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
