@@ -650,8 +650,10 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t, 
     t.i0 = (first + (p.rk_jfast ? rem / NJ : rem % gsz)) * kT;
     t.j0 = (p.rk_jfast ? rem % NJ : rem / gsz) * kT;
     t.j_end = p.n_j;
-    t.k_lo = p.offsets[e];
-    t.k_hi = p.offsets[e + 1];
+    // wave-uniform by construction; said so, the DMA takes them as scalars
+    // also where the compiler cannot load them as such
+    t.k_lo = __builtin_amdgcn_readfirstlane(p.offsets[e]);
+    t.k_hi = __builtin_amdgcn_readfirstlane(p.offsets[e + 1]);
     if (p.splits > 1) {   // slice boundaries on the 128-row grid of the offsets
       const int64_t n = (t.k_hi - t.k_lo) / 128;
       t.k_hi = t.k_lo + 128 * (n * (t.slice + 1) / p.splits);
@@ -1133,6 +1135,246 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
 }
 
 // ============================================================================
+// Persistent ragged-K variant (weight gradients)
+// ============================================================================
+// gemm256p_kernel's loop over ragged-K tiles: expert e's output tiles (i: b_t
+// rows, j: a_t rows) contract over its token range [offsets[e], offsets[e+1]),
+// so each tile has its own K range, and the last two refills of a tile fetch
+// the next tile's first two K steps.  That pipeline needs at least two K steps
+// per tile: tiles of experts with fewer rows ("short": zero or one K step) are
+// skipped by the pipelined walk and done afterwards one at a time.  No expert
+// mask, no K split, at most 64 experts (checked by the launcher).  Each
+// workgroup walks a share of the tiles: one of 8 contiguous per-XCD ranges
+// when the experts are balanced (as decode_tile256), otherwise the tiles a
+// one-tile-per-block launch would give blocks b, b + G, b + 2 G, ... (G the
+// grid), so the tiles running at once are neighbours sharing operands.
+struct TileK {
+  int e, i0, j0, k_lo, nk;
+};
+
+struct RkQueue {
+  const int* off;   // LDS copy of offsets[0 .. E]
+  int NI, NJ, per_e, n_tiles, per_xcd, xcd, c0, nbx, contiguous, jfast;
+};
+
+// The c-th tile of this workgroup's share, false past its end.
+__device__ __forceinline__ bool rk_tile_at(const RkQueue& q, int c, TileK& t, int kstep) {
+  const int loc = q.c0 + c * q.nbx;
+  int L;
+  if (q.contiguous) {
+    if (loc >= q.per_xcd) return false;
+    L = q.xcd * q.per_xcd + loc;
+  } else {
+    L = q.xcd + 8 * loc;   // block index xcd + 8 loc of a one-tile-per-block launch
+  }
+  if (L >= q.n_tiles) return false;
+  const int e = L / q.per_e, Lr = L - e * q.per_e;
+  const int group = Lr / (kGroupM * q.NJ);
+  const int first = group * kGroupM;
+  const int gsz = q.NI - first < kGroupM ? q.NI - first : kGroupM;
+  const int rem = Lr - group * kGroupM * q.NJ;   // < gsz * NJ
+  t.e = e;
+  t.i0 = (first + (q.jfast ? rem / q.NJ : rem % gsz)) * kT;
+  t.j0 = (q.jfast ? rem % q.NJ : rem / gsz) * kT;
+  t.k_lo = __builtin_amdgcn_readfirstlane(q.off[e]);   // wave-uniform: it feeds the DMA's scalar offset
+  t.nk = (__builtin_amdgcn_readfirstlane(q.off[e + 1]) - t.k_lo) / kstep;
+  return true;
+}
+
+// The next tile of the share with at least two K steps, from position `c`.
+__device__ __forceinline__ bool rk_next_long(const RkQueue& q, int& c, TileK& t, int kstep) {
+  for (;;) {
+    if (!rk_tile_at(q, c, t, kstep)) return false;
+    ++c;
+    if (t.nk >= 2) return true;
+  }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
+  constexpr int kQueue = 1024;       // offsets copy
+  constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage + kSpare + kQueue + kArgs];
+  GemmParams* const pl = reinterpret_cast<GemmParams*>(smem + 2 * SM::kStage + kSpare + kQueue);
+  int* const off = reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare);
+  if (threadIdx.x == 0) *pl = p;   // read only after the first barrier
+
+  // the offsets into LDS; the expert balance for the XCD split
+  const int lane0 = threadIdx.x & 63;
+  int rows = 0, o0 = 0;
+  if (lane0 < p.E) {
+    o0 = p.offsets[lane0];
+    rows = p.offsets[lane0 + 1] - o0;
+  }
+  if (threadIdx.x < 64) {
+    if (lane0 < p.E) off[lane0] = o0;
+    if (lane0 == p.E - 1) off[p.E] = o0 + rows;
+  }
+  int sum = rows, mx = rows;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    sum += __shfl_xor(sum, d, 64);
+    mx = max(mx, __shfl_xor(mx, d, 64));
+  }
+  block_barrier();   // offsets and arguments are in LDS
+
+  WaveCoord w;
+  w.lane = threadIdx.x & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  w.wi = w.wave >> 2;
+  w.wj = w.wave & 3;
+  w.lrow = w.lane & 31;
+  w.lhalf = w.lane >> 5;
+  w.q_mx_k = false;
+  w.p_mx_k = false;
+
+  RkQueue q;
+  q.off = off;
+  q.NI = int((p.n_i + kT - 1) / kT);
+  q.NJ = int((p.n_j + kT - 1) / kT);
+  q.per_e = q.NI * q.NJ;
+  q.n_tiles = int(p.n_tiles);
+  // wave-uniform (the shuffles leave every lane the same values, which the
+  // compiler cannot see): the tile walk feeds the DMA's scalar offsets
+  q.contiguous = __builtin_amdgcn_readfirstlane(int(p.rk_xcd && int64_t(mx) * p.E * 8 <= int64_t(sum) * 9));
+  q.per_xcd = (q.n_tiles + 7) / 8;
+  q.xcd = int(blockIdx.x % 8);
+  q.c0 = int(blockIdx.x / 8);
+  q.nbx = int(gridDim.x / 8);
+  q.jfast = p.rk_jfast;
+  auto streams = [&](const TileK& t) {
+    const Operand Q = uniform_operand(&pl->Q), P = uniform_operand(&pl->P);
+    return tile_streams<KIND>(Q, P, rfl64(pl->n_i), TileP{0, t.i0, t.j0, int(rfl64(pl->n_j))}, w);
+  };
+  const uint32_t smem_lds = lds_addr(smem);
+  uint8_t* const W = smem + 2 * SM::kStage + w.wave * 2048;
+
+  // output row j (an a_t row: m of the weight gradient), contiguous column i;
+  // rows at or past `split` go to C2
+  auto epilogue = [&](const TileK& t, const v16f (&acc)[4][2]) {
+    const int64_t n_i = rfl64(pl->n_i), n_j = rfl64(pl->n_j);
+    const int64_t ib = t.i0 + w.wi * 128, jb = t.j0 + w.wj * 64;
+    if (ib >= n_i || jb >= n_j) return;
+    const int64_t split = rfl64(pl->split);
+    const bool second = jb >= split;
+    void* const Cb = second ? pl->C2 : pl->C;
+    const int64_t gs = second ? rfl64(pl->c2_gs) : rfl64(pl->c_gs);
+    const int64_t ldC = rfl64(pl->ldC);
+    const int64_t row0 = second ? jb - split : jb;
+    WaveCoord we = w;
+    we.lane = fresh_lane();
+    we.lrow = we.lane & 31;
+    we.lhalf = we.lane >> 5;
+    if (!p.out_f32) {
+      store_bf16_passes(acc, W, static_cast<uint16_t*>(Cb) + int64_t(t.e) * gs, ldC, row0, ib, we);
+    } else {
+      float* dst = static_cast<float*>(Cb) + int64_t(t.e) * gs + row0 * ldC + ib + we.lrow * ldC + 4 * we.lhalf;
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+    }
+  };
+
+  Frag<KIND> f0, f1;
+  int cursor = 0;
+  TileK cur;
+  if (rk_next_long(q, cursor, cur, KSTEP)) {
+    TileStreams S = streams(cur);
+    issue_step<KIND>(S.q, S.p, S.sc, cur.k_lo, smem_lds, w.wave);
+    issue_step<KIND>(S.q, S.p, S.sc, cur.k_lo + KSTEP, smem_lds + SM::kStage, w.wave);
+    FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
+    block_barrier();
+    read_half<KIND>(smem, 0, f0, w);
+    int cur_off = 0;
+    for (;;) {
+      TileK nxt;
+      const bool has_next = rk_next_long(q, cursor, nxt, KSTEP);
+      v16f acc[4][2];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+      // as gemm256p_kernel: steps 0 .. nk-3 refill this tile's steps t+2, the
+      // last two the next tile's steps 0 and 1 (this tile's last step again on
+      // the last tile); `k` is the absolute contraction offset of the refill
+      auto step = [&](int64_t k) {
+        const int nxt_off = SM::kStage - cur_off;
+        __builtin_amdgcn_sched_barrier(0);
+        read_half<KIND>(smem + cur_off, 1, f1, w);
+        if constexpr (KIND == GK_FP8_POW2) {
+          f1.sa[0] = f0.sa[0];
+          f1.sb[0] = f0.sb[0];
+        }
+        mma_half<KIND>(f0, acc);
+        interleave_half<KIND>();
+        __builtin_amdgcn_sched_barrier(0);
+        FM_WAIT_VMCNT(0);
+        block_barrier();
+        issue_read_half0<KIND>(S.q, S.p, S.sc, k, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
+        mma_half<KIND>(f1, acc);
+        interleave_half<KIND>();
+        __builtin_amdgcn_sched_barrier(0);
+        cur_off = nxt_off;
+      };
+      const int nk = cur.nk;   // >= 2
+#pragma unroll 1
+      for (int t = 0; t < nk - 2; ++t) step(int64_t(cur.k_lo) + int64_t(t + 2) * KSTEP);
+      const int64_t last = int64_t(cur.k_lo) + int64_t(nk - 1) * KSTEP;
+      if (has_next) S = streams(nxt);
+#pragma unroll 1
+      for (int t = 0; t < 2; ++t) step(has_next ? int64_t(nxt.k_lo) + int64_t(t) * KSTEP : last);
+      epilogue(cur, acc);
+      if (!has_next) break;
+      cur = nxt;
+    }
+    FM_WAIT_VMCNT(0);
+    block_barrier();   // the stages are free again
+  }
+
+  // short tiles of the share: zero or one K step each
+  for (int c = 0;; ++c) {
+    TileK t;
+    if (!rk_tile_at(q, c, t, KSTEP)) break;
+    if (t.nk >= 2) continue;
+    v16f acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+    if (t.nk == 1) {
+      const TileStreams S = streams(t);
+      issue_step<KIND>(S.q, S.p, S.sc, t.k_lo, smem_lds, w.wave);
+      FM_WAIT_VMCNT(0);
+      block_barrier();
+      read_half<KIND>(smem, 0, f0, w);
+      read_half<KIND>(smem, 1, f1, w);
+      if constexpr (KIND == GK_FP8_POW2) {
+        f1.sa[0] = f0.sa[0];
+        f1.sb[0] = f0.sb[0];
+      }
+      mma_half<KIND>(f0, acc);
+      mma_half<KIND>(f1, acc);
+      block_barrier();   // every wave has read the stage before the next tile's DMA
+    }
+    epilogue(t, acc);
+  }
+}
+
+// ============================================================================
 // 256 x 128 kernel: FP8_F32 (fp32 block scales, promotion per 128-deep block)
 // ============================================================================
 constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
@@ -1417,6 +1659,16 @@ inline bool gemm_mk_one_grid() {
   return on;
 }
 
+// Unmasked, unsplit BF16 and FP8 pow2 ragged-K launches with at most 64
+// experts are persistent unless FM_GEMM_PERSISTENT_K=0 (read once).
+inline bool gemm_persistent_k() {
+  static const bool on = [] {
+    const char* e = getenv("FM_GEMM_PERSISTENT_K");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  return on;
+}
+
 // Ragged-M launches are persistent unless FM_GEMM_PERSISTENT=0 (read once).
 inline bool gemm_persistent() {
   static const bool on = [] {
@@ -1463,6 +1715,16 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
       }
     }
   }
+}
+
+// Persistent ragged-K launch: one workgroup per CU (a multiple of 8), at most
+// one per tile.
+inline void launch256pk(int kind, const GemmParams& p, hipStream_t s) {
+  const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
+  const int64_t want = (p.n_tiles + 7) / 8 * 8;
+  const dim3 grid(unsigned(want < slots ? want : slots)), block(512);
+  if (kind == GK_BF16) hipLaunchKernelGGL((gemm256pk_kernel<GK_BF16>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
 }
 
 template <int MODE>
@@ -1524,6 +1786,9 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   } else if (MODE == GM_RAGGED_M && p.E <= 64 && p.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
              (gemm_persistent() || p.q_nn)) {
     launch256p(kind, p, s);
+  } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
+             (kind == GK_BF16 || kind == GK_FP8_POW2) && gemm_persistent_k()) {
+    launch256pk(kind, p, s);
   } else {
     launch256<MODE>(kind, grid, p, s);
   }

@@ -253,3 +253,42 @@ def test_ragged_m_k_one_grid_matches_two_launches(dev, kind, E, T, K, zeros, D, 
             assert torch.all(w1_[e * H:(e + 1) * H] == 7.0) and torch.all(h1[offs[e]:offs[e + 1]] == 7.0)
         elif offs[e + 1] == offs[e]:
             assert torch.all(w1_[e * H:(e + 1) * H] == 0)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "pow2"])
+def test_ragged_k_short_and_long_experts(dev, kind):
+    """Experts of 0, 100, 128, 129, 256, 300 and 1000 tokens (0, 1, 1, 2, 2, 3
+    and 8 FP8 K steps of 128 rows): the persistent weight-gradient kernel
+    pipelines the tiles of two or more K steps and does the others one at a
+    time afterwards (zeros for the empty expert); every expert against the
+    dequantised fp32 product."""
+    counts = [0, 100, 128, 129, 256, 300, 1000]
+    E, D, H = len(counts), 256, 256
+    T = sum(counts)
+    k = KINDS[kind]
+    idx = torch.cat([torch.full((n,), e, dtype=torch.int64) for e, n in enumerate(counts)])
+    idx = idx[torch.randperm(T, generator=torch.Generator().manual_seed(3))].view(T, 1)
+    x = randn_bf16((T, D), seed=21)
+    g = randn_bf16((T, 2 * H), seed=22)
+    gran = None if kind == "bf16" else "1x128"
+    px = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True)
+    pg = fm.fused_permute_pad(g.to(dev), px.plan, E, granularity=gran, pow2_scale=kind == "pow2",
+                              return_transpose=True)
+    plan = px.plan
+    dW1 = torch.full((E * H, D), float("nan"), dtype=torch.float32, device=dev)
+    dW3 = torch.full_like(dW1, float("nan"))
+    _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H, may_split=False)
+    av, bv = _deq_cols(pg.rows_t, kind), _deq_cols(px.rows_t, kind)
+    offs = plan.offsets.cpu().numpy()
+    assert [int(offs[e + 1] - offs[e]) for e in range(E)] == [0, 128, 128, 256, 256, 384, 1024]
+    d1 = dW1.cpu().numpy().reshape(E, H, D)
+    d3 = dW3.cpu().numpy().reshape(E, H, D)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 == r0:
+            assert np.all(d1[e] == 0) and np.all(d3[e] == 0)
+            continue
+        ref = av[:, r0:r1] @ bv[:, r0:r1].T
+        assert max_rel_err(d1[e], ref[:H]) < 1e-3, (kind, e)
+        assert max_rel_err(d3[e], ref[H:]) < 1e-3, (kind, e)
