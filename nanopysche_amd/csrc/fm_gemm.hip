@@ -1787,7 +1787,8 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
              (gemm_persistent() || p.q_nn)) {
     launch256p(kind, p, s);
   } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
-             (kind == GK_BF16 || kind == GK_FP8_POW2) && gemm_persistent_k()) {
+             p.n_tiles < (int64_t(1) << 28) && (kind == GK_BF16 || kind == GK_FP8_POW2) && gemm_persistent_k()) {
+    // (its tile walk counts in 32-bit integers)
     launch256pk(kind, p, s);
   } else {
     launch256<MODE>(kind, grid, p, s);
