@@ -1375,6 +1375,233 @@ __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
 }
 
 // ============================================================================
+// Persistent dgrad + weight-gradient grid (fm_grouped_gemm_ragged_m_k)
+// ============================================================================
+// gemm256_mk_kernel's pair of launches walked by one persistent pipeline:
+// each workgroup takes its share of the ragged-M tiles (the per-XCD ranges of
+// gemm256p_kernel), then its share of the ragged-K tiles (those of
+// gemm256pk_kernel, the workgroups of an XCD in reverse order, so the ones
+// with an extra ragged-M tile get one fewer ragged-K tile), and the refills
+// of a tile's last two K steps fetch the next tile's first two whichever
+// launch it belongs to.  Ragged-K tiles of fewer than two K steps come last,
+// one at a time.  No expert masks, at most 64 experts, at least two ragged-M
+// K steps (checked by the launcher).
+struct ItemMK {
+  int k_mode;   // 0: a ragged-M tile (pm), 1: a ragged-K tile (pk)
+  int e, i0, j0, j_end, k_base, nk;
+};
+
+template <int KIND>
+__global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmParams pk) {
+  using SM = Smem256<KIND>;
+  constexpr int ES = KIND == GK_BF16 ? 2 : 1;
+  constexpr int KSTEP = 128 / ES;
+  constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
+  constexpr int kQueue = 1024;       // ragged-M tile queue
+  constexpr int kOff = 512;          // ragged-K offsets copy
+  constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * SM::kStage + kSpare + kQueue + kOff + 2 * kArgs];
+  int* const qlds = reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare);
+  int* const off = reinterpret_cast<int*>(smem + 2 * SM::kStage + kSpare + kQueue);
+  GemmParams* const plm = reinterpret_cast<GemmParams*>(smem + 2 * SM::kStage + kSpare + kQueue + kOff);
+  GemmParams* const plk = reinterpret_cast<GemmParams*>(smem + 2 * SM::kStage + kSpare + kQueue + kOff + kArgs);
+  if (threadIdx.x == 0) {
+    *plm = pm;
+    *plk = pk;
+  }
+
+  WaveCoord w;
+  w.lane = threadIdx.x & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  w.wi = w.wave >> 2;
+  w.wj = w.wave & 3;
+  w.lrow = w.lane & 31;
+  w.lhalf = w.lane >> 5;
+  w.q_mx_k = false;
+  w.p_mx_k = false;
+
+  // ragged-M queue (LDS) and the ragged-K offsets (LDS); balance of the experts
+  TileQueue tq;
+  tile_queue_init(pm, tq, qlds);
+  const int lane0 = threadIdx.x & 63;
+  int rows = 0, o0 = 0;
+  if (lane0 < pk.E) {
+    o0 = pk.offsets[lane0];
+    rows = pk.offsets[lane0 + 1] - o0;
+  }
+  if (threadIdx.x < 64) {
+    if (lane0 < pk.E) off[lane0] = o0;
+    if (lane0 == pk.E - 1) off[pk.E] = o0 + rows;
+  }
+  int sum = rows, mx = rows;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    sum += __shfl_xor(sum, d, 64);
+    mx = max(mx, __shfl_xor(mx, d, 64));
+  }
+  block_barrier();   // queues and arguments are in LDS
+
+  RkQueue q;
+  q.off = off;
+  q.NI = int((pk.n_i + kT - 1) / kT);
+  q.NJ = int((pk.n_j + kT - 1) / kT);
+  q.per_e = q.NI * q.NJ;
+  q.n_tiles = int(pk.n_tiles);
+  q.contiguous = __builtin_amdgcn_readfirstlane(int(pk.rk_xcd && int64_t(mx) * pk.E * 8 <= int64_t(sum) * 9));
+  q.per_xcd = (q.n_tiles + 7) / 8;
+  q.xcd = int(blockIdx.x % 8);
+  q.nbx = int(gridDim.x / 8);
+  q.c0 = q.nbx - 1 - int(blockIdx.x / 8);
+  q.jfast = pk.rk_jfast;
+
+  const int nk_m = int(pm.K / KSTEP);   // >= 2 (launcher)
+  int cm = 0, ck = 0;                   // positions in the two shares
+  auto next_item = [&](ItemMK& it) -> bool {
+    TileP tp;
+    if (tile_queue_get(tq, cm, tp)) {
+      ++cm;
+      it = ItemMK{0, tp.e, tp.i0, tp.j0, tp.j_end, 0, nk_m};
+      return true;
+    }
+    TileK tk;
+    if (!rk_next_long(q, ck, tk, KSTEP)) return false;
+    it = ItemMK{1, tk.e, tk.i0, tk.j0, 0, tk.k_lo, tk.nk};
+    return true;
+  };
+  auto streams = [&](const ItemMK& it) {
+    if (it.k_mode) {
+      const Operand Q = uniform_operand(&plk->Q), P = uniform_operand(&plk->P);
+      return tile_streams<KIND>(Q, P, rfl64(plk->n_i), TileP{0, it.i0, it.j0, int(rfl64(plk->n_j))}, w);
+    }
+    const Operand Q = uniform_operand(&plm->Q), P = uniform_operand(&plm->P);
+    return tile_streams<KIND>(Q, P, rfl64(plm->n_i), TileP{it.e, it.i0, it.j0, it.j_end}, w);
+  };
+  const uint32_t smem_lds = lds_addr(smem);
+  uint8_t* const W = smem + 2 * SM::kStage + w.wave * 2048;
+
+  auto store = [&](void* C, int64_t ldC, int out_f32, int64_t row0, int64_t col0, const v16f (&acc)[4][2]) {
+    WaveCoord we = w;
+    we.lane = fresh_lane();
+    we.lrow = we.lane & 31;
+    we.lhalf = we.lane >> 5;
+    if (!out_f32) {
+      store_bf16_passes(acc, W, static_cast<uint16_t*>(C), ldC, row0, col0, we);
+    } else {
+      float* dst = static_cast<float*>(C) + row0 * ldC + col0 + we.lrow * ldC + 4 * we.lhalf;
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+    }
+  };
+  auto epilogue = [&](const ItemMK& it, const v16f (&acc)[4][2]) {
+    const int64_t ib = it.i0 + w.wi * 128, jb = it.j0 + w.wj * 64;
+    if (it.k_mode) {   // weight gradient: row j (m), column i; rows past `split` to C2
+      if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return;
+      const int64_t split = rfl64(plk->split);
+      const bool second = jb >= split;
+      const int64_t gs = second ? rfl64(plk->c2_gs) : rfl64(plk->c_gs);
+      uint8_t* const Cb = static_cast<uint8_t*>(second ? plk->C2 : plk->C);
+      const int f32 = __builtin_amdgcn_readfirstlane(plk->out_f32);
+      store(Cb + int64_t(it.e) * gs * (f32 ? 4 : 2), rfl64(plk->ldC), f32, second ? jb - split : jb, ib, acc);
+    } else {           // dgrad: row j (token), column i
+      const int p_rows = it.j_end - it.j0 < kT ? it.j_end - it.j0 : kT;
+      if (ib >= rfl64(plm->n_i) || jb >= it.j0 + p_rows) return;
+      store(plm->C, rfl64(plm->ldC), __builtin_amdgcn_readfirstlane(plm->out_f32), jb, ib, acc);
+    }
+  };
+
+  Frag<KIND> f0, f1;
+  ItemMK cur;
+  if (next_item(cur)) {
+    TileStreams S = streams(cur);
+    issue_step<KIND>(S.q, S.p, S.sc, cur.k_base, smem_lds, w.wave);
+    issue_step<KIND>(S.q, S.p, S.sc, cur.k_base + KSTEP, smem_lds + SM::kStage, w.wave);
+    FM_WAIT_VMCNT(KIND == GK_BF16 ? 8 : 9);
+    block_barrier();
+    read_half<KIND>(smem, 0, f0, w);
+    int cur_off = 0;
+    for (;;) {
+      ItemMK nxt;
+      const bool has_next = next_item(nxt);
+      v16f acc[4][2];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+      auto step = [&](int64_t k) {
+        const int nxt_off = SM::kStage - cur_off;
+        __builtin_amdgcn_sched_barrier(0);
+        read_half<KIND>(smem + cur_off, 1, f1, w);
+        if constexpr (KIND == GK_FP8_POW2) {
+          f1.sa[0] = f0.sa[0];
+          f1.sb[0] = f0.sb[0];
+        }
+        mma_half<KIND>(f0, acc);
+        interleave_half<KIND>();
+        __builtin_amdgcn_sched_barrier(0);
+        FM_WAIT_VMCNT(0);
+        block_barrier();
+        issue_read_half0<KIND>(S.q, S.p, S.sc, k, smem_lds + cur_off, w.wave, smem + nxt_off, f0, w);
+        mma_half<KIND>(f1, acc);
+        interleave_half<KIND>();
+        __builtin_amdgcn_sched_barrier(0);
+        cur_off = nxt_off;
+      };
+      const int nk = cur.nk;   // >= 2
+#pragma unroll 1
+      for (int t = 0; t < nk - 2; ++t) step(int64_t(cur.k_base) + int64_t(t + 2) * KSTEP);
+      const int64_t last = int64_t(cur.k_base) + int64_t(nk - 1) * KSTEP;
+      if (has_next) S = streams(nxt);
+#pragma unroll 1
+      for (int t = 0; t < 2; ++t) step(has_next ? int64_t(nxt.k_base) + int64_t(t) * KSTEP : last);
+      epilogue(cur, acc);
+      if (!has_next) break;
+      cur = nxt;
+    }
+    FM_WAIT_VMCNT(0);
+    block_barrier();   // the stages are free again
+  }
+
+  // ragged-K tiles of fewer than two K steps, one at a time
+  for (int c = 0;; ++c) {
+    TileK t;
+    if (!rk_tile_at(q, c, t, KSTEP)) break;
+    if (t.nk >= 2) continue;
+    const ItemMK it{1, t.e, t.i0, t.j0, 0, t.k_lo, t.nk};
+    v16f acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+    if (t.nk == 1) {
+      const TileStreams S = streams(it);
+      issue_step<KIND>(S.q, S.p, S.sc, t.k_lo, smem_lds, w.wave);
+      FM_WAIT_VMCNT(0);
+      block_barrier();
+      read_half<KIND>(smem, 0, f0, w);
+      read_half<KIND>(smem, 1, f1, w);
+      if constexpr (KIND == GK_FP8_POW2) {
+        f1.sa[0] = f0.sa[0];
+        f1.sb[0] = f0.sb[0];
+      }
+      mma_half<KIND>(f0, acc);
+      mma_half<KIND>(f1, acc);
+      block_barrier();   // every wave has read the stage before the next tile's DMA
+    }
+    epilogue(it, acc);
+  }
+}
+
+// ============================================================================
 // 256 x 128 kernel: FP8_F32 (fp32 block scales, promotion per 128-deep block)
 // ============================================================================
 constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
@@ -2034,6 +2261,15 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
   if (int rc = prepare_gemm<GM_RAGGED_K>(kind, pk)) return rc;
   const int64_t nbm = (pm.n_tiles + 7) / 8 * 8, nbk = (pk.n_tiles + 7) / 8 * 8;
   if (nbm + nbk == 0) return 0;
+  if (expert_mask == nullptr && E <= 64 && pm.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
+      pk.n_tiles < (int64_t(1) << 28) && gemm_persistent_k()) {
+    // persistent: one workgroup per CU (a multiple of 8), at most one per tile
+    const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
+    const dim3 pgrid(unsigned(nbm + nbk < slots ? nbm + nbk : slots)), pblock(512);
+    if (kind == GK_BF16) hipLaunchKernelGGL((gemm256pmk_kernel<GK_BF16>), pgrid, pblock, 0, s, pm, pk);
+    else hipLaunchKernelGGL((gemm256pmk_kernel<GK_FP8_POW2>), pgrid, pblock, 0, s, pm, pk);
+    return check_launch("fm_grouped_gemm_ragged_m_k");
+  }
   const dim3 grid(unsigned(nbm + nbk)), block(512);
   if (kind == GK_BF16) hipLaunchKernelGGL((gemm256_mk_kernel<GK_BF16>), grid, block, 0, s, pm, pk, nbm);
   else hipLaunchKernelGGL((gemm256_mk_kernel<GK_FP8_POW2>), grid, block, 0, s, pm, pk, nbm);
