@@ -408,7 +408,12 @@ int fm_swiglu_values(const void* g, int64_t ld_g, const void* u, int64_t ld_u, c
 /* ------------------------------------------------------- grouped GEMM ---- */
 /* One operand of the grouped GEMM: K-contiguous rows.  Scale of (row, kb) is
  * scale[g*scale_group_stride + (row >> scale_row_shift)*scale_row_stride +
- * kb*scale_kb_stride], kb counting 128-blocks (fp32 / pow2) or 32-blocks (MX). */
+ * kb*scale_kb_stride], kb counting 128-blocks (fp32 / pow2) or 32-blocks (MX).
+ * data2 (NULL: unused) splits each group's rows over two tensors of the same
+ * pitch and group stride: rows r >= split_rows are row r - split_rows of
+ * data2 -- the weights of fm_grouped_gemm_ragged_m read from w1 and w3 as
+ * they are stored, without stacking them.  BF16 weights only, split_rows a
+ * multiple of 256, at most 64 experts. */
 typedef struct FmGemmOperand {
   const void* data;
   int64_t ld;            /* row pitch, elements */
@@ -418,6 +423,8 @@ typedef struct FmGemmOperand {
   int64_t scale_kb_stride;
   int64_t scale_group_stride;
   int scale_row_shift;   /* 7 for 128x128 weight blocks, 0 otherwise */
+  const void* data2;     /* rows from split_rows on (NULL: none) */
+  int64_t split_rows;
 } FmGemmOperand;
 
 /* Replaces fp8_flow_moe.fp8_grouped_gemm (reference fp8/__init__.py:21) and

@@ -46,6 +46,8 @@ class FmGemmOperand(C.Structure):
         ("scale_kb_stride", C.c_int64),
         ("scale_group_stride", C.c_int64),
         ("scale_row_shift", C.c_int),
+        ("data2", C.c_void_p),
+        ("split_rows", C.c_int64),
     ]
 
 

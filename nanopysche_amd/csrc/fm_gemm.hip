@@ -70,6 +70,8 @@ struct Operand {
   int64_t s_kb;       //   kb counts 128-blocks (fp32 / pow2) or 32-blocks (MX)
   int64_t s_gs;
   int s_shift;
+  const uint8_t* p2;  // rows at or past `split` of each group: row - split of p2
+  int64_t split;      // INT64_MAX: one tensor
 };
 
 struct GemmParams {
@@ -949,8 +951,14 @@ __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Oper
   const int64_t q_rows = n_i - t.i0 < kT ? n_i - t.i0 : kT;
   const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
   const int lane = fresh_lane();
-  if constexpr (QNN) s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
-  else s.q = make_stream(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0) * Q.ld) * ES, Q.ld * ES, q_rows, lane, w.wave);
+  if constexpr (QNN) {
+    s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
+  } else {   // a tile lies in one of the two tensors of a split operand (split % 256 == 0)
+    const bool second = t.i0 >= Q.split;
+    const int64_t qi = second ? t.i0 - Q.split : t.i0;
+    s.q = make_stream((second ? Q.p2 : Q.p) + (int64_t(t.e) * Q.gs + qi * Q.ld) * ES, Q.ld * ES, q_rows, lane,
+                      w.wave);
+  }
   s.p = make_stream(P.p + int64_t(t.j0) * P.ld * ES, P.ld * ES, p_rows, lane, w.wave);
   s.sc = ScaleSrc{};
   if constexpr (SM::kScaled) {
@@ -979,6 +987,8 @@ __device__ __forceinline__ Operand uniform_operand(const Operand* o) {
   r.s_kb = rfl64(o->s_kb);
   r.s_gs = rfl64(o->s_gs);
   r.s_shift = __builtin_amdgcn_readfirstlane(o->s_shift);
+  r.p2 = reinterpret_cast<const uint8_t*>(rfl64(int64_t(size_t(o->p2))));
+  r.split = rfl64(o->split);
   return r;
 }
 
@@ -2011,7 +2021,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
   } else if (MODE == GM_RAGGED_M && p.E <= 64 && p.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
-             (gemm_persistent() || p.q_nn)) {
+             (gemm_persistent() || p.q_nn || p.Q.split != INT64_MAX)) {
     launch256p(kind, p, s);
   } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
              p.n_tiles < (int64_t(1) << 28) && (kind == GK_BF16 || kind == GK_FP8_POW2) && gemm_persistent_k()) {
@@ -2025,7 +2035,8 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
 
 inline Operand make_operand(const FmGemmOperand& o) {
   return Operand{static_cast<const uint8_t*>(o.data), o.ld, o.group_stride, o.scale,
-                 o.scale_row_stride, o.scale_kb_stride, o.scale_group_stride, o.scale_row_shift};
+                 o.scale_row_stride, o.scale_kb_stride, o.scale_group_stride, o.scale_row_shift,
+                 static_cast<const uint8_t*>(o.data2 ? o.data2 : o.data), o.data2 ? o.split_rows : INT64_MAX};
 }
 
 inline int check_operand(const FmGemmOperand& o, int kind, const char* name) {
@@ -2123,6 +2134,12 @@ int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmO
              "a row pitch >= N and a group stride >= K x pitch");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
+  FM_REQUIRE(tokens->data2 == nullptr, "fm_grouped_gemm_ragged_m: the token operand cannot be split");
+  FM_REQUIRE(weights->data2 == nullptr ||
+                 (kind == GK_BF16 && !nn && E <= 64 && K >= 128 && weights->split_rows > 0 &&
+                  weights->split_rows % 256 == 0 && weights->split_rows < N),
+             "fm_grouped_gemm_ragged_m: split weights need the BF16 kind, E <= 64, K >= 128 and a split that is "
+             "a multiple of 256 inside N");
   if (int rc = check_scale_span(*tokens, kind, m_tiles * 128, K, "tokens")) return rc;
   if (int rc = check_scale_span(*weights, kind, N, K, "weights")) return rc;
   FM_REQUIRE(N > 0 && N % 128 == 0, "fm_grouped_gemm_ragged_m: N must be a positive multiple of 128 (got %lld)", (long long)N);
@@ -2184,6 +2201,7 @@ int ragged_k_params(int kind, const FmGemmOperand* a_t, const FmGemmOperand* b_t
                     int64_t M, int64_t N, const int32_t* expert_mask, int mask_want, void* out, int64_t out_gs,
                     void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype, int64_t ld_out, GemmParams& p) {
   FM_REQUIRE(a_t && b_t && offsets && out, "fm_grouped_gemm_ragged_k: null pointer");
+  FM_REQUIRE(a_t->data2 == nullptr && b_t->data2 == nullptr, "fm_grouped_gemm_ragged_k: operands cannot be split");
   if (int rc = check_operand(*a_t, kind, "a_t")) return rc;
   if (int rc = check_operand(*b_t, kind, "b_t")) return rc;
   // contraction over token columns: at most the row pitch of the operands
@@ -2257,6 +2275,7 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
       if (int rc = dispatch_gemm<GM_RAGGED_M>(kind, pm, s)) return rc;
     return dispatch_gemm<GM_RAGGED_K>(kind, pk, s);
   }
+  const GemmParams pm_args = pm, pk_args = pk;   // as the single-launch entries receive them
   if (int rc = prepare_gemm<GM_RAGGED_M>(kind, pm)) return rc;
   if (int rc = prepare_gemm<GM_RAGGED_K>(kind, pk)) return rc;
   const int64_t nbm = (pm.n_tiles + 7) / 8 * 8, nbk = (pk.n_tiles + 7) / 8 * 8;
@@ -2269,6 +2288,10 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
     if (kind == GK_BF16) hipLaunchKernelGGL((gemm256pmk_kernel<GK_BF16>), pgrid, pblock, 0, s, pm, pk);
     else hipLaunchKernelGGL((gemm256pmk_kernel<GK_FP8_POW2>), pgrid, pblock, 0, s, pm, pk);
     return check_launch("fm_grouped_gemm_ragged_m_k");
+  }
+  if (pm.Q.split != INT64_MAX) {   // split weights: only the persistent ragged-M kernel reads them
+    if (int rc = dispatch_gemm<GM_RAGGED_M>(kind, pm_args, s)) return rc;
+    return dispatch_gemm<GM_RAGGED_K>(kind, pk_args, s);
   }
   const dim3 grid(unsigned(nbm + nbk)), block(512);
   if (kind == GK_BF16) hipLaunchKernelGGL((gemm256_mk_kernel<GK_BF16>), grid, block, 0, s, pm, pk, nbm);

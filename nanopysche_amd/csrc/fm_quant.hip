@@ -113,6 +113,60 @@ __device__ __forceinline__ void weight_quant_tile(const WeightQuantArgs& a, int6
   const int cc = (tid & 15) * 8;
   const int rr = tid >> 4;
   const DenseSrc<T> src{static_cast<const T*>(a.w) + g * a.gs_w, a.ld_w};
+  if (a.kind == QK_BF16) {
+    // bf16 payload: a bf16 source's words copied as they are, fp32 rounded
+    uint32_t wv[8][4];
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint4 q = *reinterpret_cast<const uint4*>(src.p + (r0 + rr + 16 * i) * src.ld + c0 + cc);
+        wv[i][0] = q.x; wv[i][1] = q.y; wv[i][2] = q.z; wv[i][3] = q.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float vi[1][8];
+        src.load8(r0 + rr + 16 * i, c0 + cc, vi);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wv[i][j] = uint32_t(f32_to_bf16(vi[0][2 * j])) | (uint32_t(f32_to_bf16(vi[0][2 * j + 1])) << 16);
+      }
+    }
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(a.q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = rr + 16 * i;
+      const uint32_t (&w)[4] = wv[i];
+      if (q16)
+        *reinterpret_cast<uint4*>(q16 + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+      if (a.qt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tile[row][(cc >> 1) + j] = w[j];
+      }
+    }
+    if (!a.qt) return;
+    __syncthreads();
+    // transposed payload: 16 lanes per transposed row (256 bytes: the tile's
+    // 128 rows of one column), lane k taking tile rows [8 k, 8 k + 8), so
+    // each store instruction writes 4 whole rows of the transpose
+    uint16_t* const base = reinterpret_cast<uint16_t*>(a.qt) + g * a.gs_qt + a.qt_col_off + r0;
+    const int k = tid & 15;
+#pragma unroll
+    for (int pass = 0; pass < 8; ++pass) {
+      const int col = pass * 16 + (tid >> 4);
+      uint32_t w4[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int row = 8 * k + 2 * m;
+        const uint32_t lo = (tile[row][col >> 1] >> (16 * (col & 1))) & 0xffffu;
+        const uint32_t hi = (tile[row + 1][col >> 1] >> (16 * (col & 1))) & 0xffffu;
+        w4[m] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(base + (c0 + col) * a.ld_qt + 8 * k) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+    return;
+  }
   float v[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) src.load8(r0 + rr + 16 * i, c0 + cc, v + i);
@@ -121,39 +175,6 @@ __device__ __forceinline__ void weight_quant_tile(const WeightQuantArgs& a, int6
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(v[i][j]));
-  const int c = tid & 127, h = tid >> 7;  // transposed-store role
-  if (a.kind == QK_BF16) {
-    uint16_t* q16 = reinterpret_cast<uint16_t*>(a.q);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = rr + 16 * i;
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        w[j] = uint32_t(f32_to_bf16(v[i][2 * j])) | (uint32_t(f32_to_bf16(v[i][2 * j + 1])) << 16);
-      if (q16)
-        *reinterpret_cast<uint4*>(q16 + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
-            make_uint4(w[0], w[1], w[2], w[3]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tile[row][(cc >> 1) + j] = w[j];
-    }
-    if (!a.qt) return;
-    __syncthreads();
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.qt) + g * a.gs_qt + (c0 + c) * a.ld_qt +
-                    a.qt_col_off + r0 + 64 * h;
-    for (int r8 = 0; r8 < 64; r8 += 8) {
-      uint32_t w4[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int row = 64 * h + r8 + 2 * k;
-        const uint32_t lo = (tile[row][c >> 1] >> (16 * (c & 1))) & 0xffffu;
-        const uint32_t hi = (tile[row + 1][c >> 1] >> (16 * (c & 1))) & 0xffffu;
-        w4[k] = lo | (hi << 16);
-      }
-      *reinterpret_cast<uint4*>(dst + r8) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    }
-    return;
-  }
   // block amax: wave maximum, then the four waves' through LDS
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));

@@ -346,9 +346,11 @@ def fused_unpermute_unpad(y: torch.Tensor, plan: RoutingPlan,
 
 
 # ================================================================ grouped GEMM ====
-def _operand(data, scale=None, *, ld=None, gs=0, s_row=0, s_kb=0, s_gs=0, shift=0):
+def _operand(data, scale=None, *, ld=None, gs=0, s_row=0, s_kb=0, s_gs=0, shift=0, data2=None, split=0):
     o = _lib.FmGemmOperand()
     o.data = data.data_ptr()
+    o.data2 = None if data2 is None else data2.data_ptr()
+    o.split_rows = split if data2 is not None else 0
     o.ld = data.stride(0) if ld is None else ld
     o.group_stride = gs
     o.scale = None if scale is None else scale.data_ptr()
@@ -377,7 +379,8 @@ def _col_operand(t, kind):
 class ExpertWeightOperand:
     """One expert-weight GEMM operand: E matrices [N, K] (K contiguous), or,
     with ``kmajor``, E matrices stored [K, N] (N contiguous) that the FP8 pow2
-    GEMM reads transposed."""
+    GEMM reads transposed.  With ``data2`` (BF16) each expert's rows from
+    ``split`` on come from ``data2``: w1 and w3 read as stored."""
 
     data: torch.Tensor
     scale: Optional[torch.Tensor]
@@ -390,10 +393,12 @@ class ExpertWeightOperand:
     N: int = 0
     K: int = 0
     kmajor: bool = False
+    data2: Optional[torch.Tensor] = None
+    split: int = 0
 
     def operand(self):
         return _operand(self.data, self.scale, ld=self.ld, gs=self.gs, s_row=self.s_row,
-                        s_kb=self.s_kb, s_gs=self.s_gs, shift=self.shift)
+                        s_kb=self.s_kb, s_gs=self.s_gs, shift=self.shift, data2=self.data2, split=self.split)
 
 
 def _gemm_kind(kind):
@@ -608,6 +613,9 @@ class ExpertWeights:
         if self.kmajor_ok(kind, E, H, D):
             self._build_kmajor(w1, w2, w3, E, H, D)
             return
+        if self.views_ok(kind, E, H, D, (w1, w2, w3)):
+            self._build_bf16_views(w1, w2, w3, E, H, D, dgrad)
+            return
         pay = torch.bfloat16 if kind == _lib.QUANT_BF16 else torch.uint8
         f32 = torch.float32
         fp8 = kind != _lib.QUANT_BF16
@@ -679,6 +687,38 @@ class ExpertWeights:
         self.w2t = ExpertWeightOperand(W2, S2, D, H * D, 1, D // 128, g2, sh, D, H, kmajor=True)
         self.w13t = ExpertWeightOperand(W13, S13, D, 2 * H * D, 1, D // 128, g13, sh, D, 2 * H, kmajor=True)
         self.has_dgrad = True
+
+    @staticmethod
+    def views_ok(kind: int, E: int, H: int, D: int, ws) -> bool:
+        """BF16 recipe on contiguous bf16 parameters, at most 64 experts, H a
+        multiple of 256: the row operands are the parameters themselves."""
+        return (ExpertWeights.KMAJOR and kind == _lib.QUANT_BF16 and E <= 64 and H % 256 == 0
+                and all(w.dtype == torch.bfloat16 and w.is_contiguous() for w in ws))
+
+    def _build_bf16_views(self, w1, w2, w3, E, H, D, dgrad):
+        """w13: w1 and w3 read as stored (a split operand), w2: the parameter
+        itself; only the transposed operands are written (w2t, and w13t for a
+        backward), in one launch."""
+        dev = w1.device
+        W2t = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
+        W13t = torch.empty(E, D, 2 * H, dtype=torch.bfloat16, device=dev) if dgrad else None
+        BF = _lib.QUANT_BF16
+
+        def job(src, dst_t, col_off, cols_out):
+            return _lib.FmWeightJob(_lib.ptr(src), _lib.DTYPE_BF16, E, H, D, D, H * D, BF,
+                                    None, 0, 0, 0, None, 0, 0,
+                                    _lib.ptr(dst_t), cols_out, D * cols_out, col_off, None, 0, 0)
+
+        jobs = [job(w2, W2t, 0, H)]
+        if dgrad:
+            jobs += [job(w1, W13t, 0, 2 * H), job(w3, W13t, H, 2 * H)]
+        arr = (_lib.FmWeightJob * len(jobs))(*jobs)
+        _lib.call("fm_quantize_weight_batch", arr, len(jobs), _lib.stream_of(w1))
+        self.w13 = ExpertWeightOperand(w1, None, D, H * D, N=2 * H, K=D, data2=w3, split=H)
+        self.w2 = ExpertWeightOperand(w2, None, D, H * D, N=H, K=D)
+        self.w2t = ExpertWeightOperand(W2t, None, H, D * H, N=D, K=H)
+        if dgrad:
+            self.w13t = ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H)
 
     def _build_mx(self, w1, w2, w3, E, H, D, dgrad):
         dev = w1.device

@@ -292,3 +292,38 @@ def test_ragged_k_short_and_long_experts(dev, kind):
         ref = av[:, r0:r1] @ bv[:, r0:r1].T
         assert max_rel_err(d1[e], ref[:H]) < 1e-3, (kind, e)
         assert max_rel_err(d3[e], ref[H:]) < 1e-3, (kind, e)
+
+
+@pytest.mark.parametrize("E,T,K,zeros,masked", [(8, 3000, 2, (2, 5), False), (6, 2500, 2, (4,), True)])
+def test_bf16_split_weights_match_stacked(dev, E, T, K, zeros, masked):
+    """BF16 gate|up with w1 and w3 read as stored (a split operand, rows from H
+    on from w3) gives the bits of the same GEMM on the stacked [E, 2H, D] copy,
+    in a single launch and as the dgrad of the dH + dW2 pair (persistent, or
+    as two launches when an expert mask is given)."""
+    from nanopysche_amd.flow_moe import ExpertWeightOperand, _gemm_m, _gemm_mk
+    D, H = 256, 512
+    x = randn_bf16((T, D), seed=1)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)
+    w1, w3 = (randn_bf16((E * H, D), seed=s, std=0.02).to(dev) for s in (2, 4))
+    pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=None, return_transpose=True)
+    plan = pt.plan
+    split = ExpertWeightOperand(w1, None, D, H * D, N=2 * H, K=D, data2=w3, split=H)
+    W13 = torch.cat([w1.view(E, H, D), w3.view(E, H, D)], 1).contiguous()
+    stacked = ExpertWeightOperand(W13, None, D, 2 * H * D, N=2 * H, K=D)
+    mask = torch.tensor([e % 2 for e in range(E)], dtype=torch.int32, device=dev) if masked else None
+    used = int(plan.offsets[-1].item())
+    outs = []
+    for w in (stacked, split):
+        out = torch.zeros(plan.rows_max, 2 * H, dtype=torch.float32, device=dev)
+        _gemm_m(_lib.QUANT_BF16, pt.rows, w, plan, out, mask, 1)
+        outs.append(out[:used])
+    assert torch.equal(outs[0], outs[1])
+    # the same operand as the dgrad of the pair (the weight gradient: x^T x)
+    pair = []
+    for w in (stacked, split):
+        o1 = torch.zeros(plan.rows_max, 2 * H, dtype=torch.float32, device=dev)
+        o2 = torch.zeros(E * D, D, dtype=torch.float32, device=dev)
+        _gemm_mk(_lib.QUANT_BF16, pt.rows, w, plan, o1, pt.rows_t, pt.rows_t, D, D, o2, D * D, mask, 1)
+        pair.append((o1[:used], o2))
+    assert torch.equal(pair[0][0], pair[1][0]) and torch.equal(pair[0][1], pair[1][1])
+    assert torch.equal(pair[1][0], outs[1])

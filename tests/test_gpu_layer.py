@@ -237,3 +237,32 @@ def test_forward_without_grad_builds_forward_operands_only(dev, kmajor, monkeypa
     assert ew.has_dgrad and ew.w13t is not None and ew.w2 is not None
     assert torch.equal(a, b.detach())
     assert p[0].grad is not None
+
+
+@pytest.mark.parametrize("param_dtype,H", [(torch.float32, 384), (torch.bfloat16, 384), (torch.bfloat16, 512)])
+def test_weight_cache_bf16_operands_are_exact_copies(dev, param_dtype, H):
+    """BF16 recipe: w13 is w1 | w3 stacked per expert, w2t each expert's w2
+    transposed, w2 and w13t (dgrad) w2 itself and [w1; w3] transposed -- the
+    parameters' values rounded to bf16, bit for bit.  bf16 parameters with H a
+    multiple of 256 are not copied: w13 reads w1 and w3 as stored (a split
+    operand) and w2 is the parameter."""
+    from nanopysche_amd import _lib
+    from nanopysche_amd.flow_moe import ExpertWeights
+
+    E, D = 3, 256
+    g = torch.Generator().manual_seed(9)
+    w1, w2, w3 = ((torch.randn(E * H, D, generator=g) * 0.02).to(param_dtype) for _ in range(3))
+    p1, p2, p3 = w1.to(dev), w2.to(dev), w3.to(dev)
+    ew = ExpertWeights(_lib.QUANT_BF16).refresh(p1, p2, p3, E)
+    b = lambda t: t.to(torch.bfloat16).view(E, H, D)
+    W13 = torch.cat([b(w1), b(w3)], 1)                      # [E, 2H, D]
+    views = param_dtype == torch.bfloat16 and H % 256 == 0
+    assert (ew.w13.data2 is not None) == views
+    if views:
+        same = lambda a, b: a.data_ptr() == b.data_ptr()
+        assert same(ew.w13.data, p1) and same(ew.w13.data2, p3) and ew.w13.split == H and same(ew.w2.data, p2)
+    else:
+        assert torch.equal(ew.w13.data.reshape(E, 2 * H, D).cpu(), W13)
+        assert torch.equal(ew.w2.data.reshape(E, H, D).cpu(), b(w2))
+    assert torch.equal(ew.w2t.data.reshape(E, D, H).cpu(), b(w2).transpose(1, 2))
+    assert torch.equal(ew.w13t.data.reshape(E, D, 2 * H).cpu(), W13.transpose(1, 2))
