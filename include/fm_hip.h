@@ -322,6 +322,20 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
                   int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
                   int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* fm_route_sort, then fm_quantize_weight_batch(jobs, n_jobs) on the same
+ * stream, with the outputs of the two calls.  No counterpart in the
+ * reference: the sort's launches occupy a few CUs for a few microseconds, so
+ * part of the weight batch's 128x128 blocks run as extra workgroups of those
+ * launches and the rest as a launch of their own after the sort (the shares
+ * change only timing, never the bytes written).  For a layer that refreshes
+ * its expert weights in the same forward that routes its tokens.  jobs as
+ * fm_quantize_weight_batch takes them (1-4, equal shapes and dtype); their
+ * outputs must not alias the sort's. */
+int fm_route_sort_weights(const void* indices, int indices_i64, int64_t T, int K, int E, int64_t threshold,
+                          int32_t* counts, int32_t* offsets, int32_t* row_of, int32_t* assign_of_row,
+                          int64_t rows_max, int32_t* tile_expert, int32_t* use_fp8, void* workspace,
+                          int64_t workspace_bytes, const FmWeightJob* jobs, int n_jobs, void* stream);
+
 /* No counterpart in the reference.  fm_route_sort without the workspace
  * argument and without any allocation, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses

@@ -113,6 +113,8 @@ SIGNATURES = {
     "fm_route_workspace_bytes": (_i64, [_i64, _i32]),
     "fm_route_sort": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp]),
+    "fm_route_sort_weights": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                                     _vp, _i64, C.POINTER(FmWeightJob), _i32, _vp]),
     "fm_route_sort_noalloc_max_workspace_bytes": (_i64, []),
     "fm_route_sort_noalloc": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
                                      _vp]),

@@ -18,7 +18,7 @@
 #include <type_traits>
 
 #include "fm_gating.h"
-#include "fm_tile.h"
+#include "fm_weight_tile.h"
 #include "../../include/fm_hip.h"
 
 namespace fm {
@@ -260,7 +260,11 @@ __device__ __forceinline__ int expert_bits(int E) {
 // experts adds the group's size (one LDS atomic per distinct expert).
 template <typename I>
 __global__ __launch_bounds__(256) void sort_hist_kernel(const I* idx, int64_t A, int E,
-                                                        int32_t* block_hist, int64_t n_blocks) {
+                                                        int32_t* block_hist, int64_t n_blocks, WeightSide side) {
+  if (int64_t(blockIdx.x) >= n_blocks) {   // workgroups past the sort's run expert-weight blocks
+    weight_side_block(side, int64_t(blockIdx.x) - n_blocks);
+    return;
+  }
   __shared__ int32_t hist[kSortMaxExperts];
   for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
   __syncthreads();
@@ -407,7 +411,11 @@ __global__ __launch_bounds__(256) void sort_scan_scatter_kernel(const I* idx, in
                                                                 int32_t* tile_expert, int64_t n_tiles_max,
                                                                 int32_t* row_of, int32_t* assign_of_row,
                                                                 int64_t rows_max, int32_t* use_fp8,
-                                                                int64_t threshold) {
+                                                                int64_t threshold, WeightSide side) {
+  if (int64_t(blockIdx.x) >= n_blocks) {   // workgroups past the sort's run expert-weight blocks
+    weight_side_block(side, int64_t(blockIdx.x) - n_blocks);
+    return;
+  }
   __shared__ int32_t base[4][kFusedExperts];   // per-wave counts, then per-wave next rows
   __shared__ int32_t start[kFusedExperts + 1];  // padded group starts; start[E] = rows used
   __shared__ int32_t wtot[4];
@@ -847,10 +855,26 @@ inline bool gemm_route_fused_scan() {
 // (one launch for small sorts).  block_hist ([E][blocks] int32) is written in
 // full by sort_hist_kernel before anything reads it, so the buffer needs no
 // clearing.
+// Shares (percent of an expert-weight batch's blocks) that the histogram and
+// the fused scan + scatter launches run beside their own workgroups
+// (FM_SORT_SIDE="hist,scan", read once); the rest runs as its own launch.
+inline void sort_side_shares(int& hist, int& scan) {
+  static const std::pair<int, int> v = [] {
+    int h = 50, c = 50;
+    if (const char* e = getenv("FM_SORT_SIDE")) sscanf(e, "%d,%d", &h, &c);
+    h = h < 0 ? 0 : h > 100 ? 100 : h;
+    c = c < 0 ? 0 : c > 100 - h ? 100 - h : c;
+    return std::make_pair(h, c);
+  }();
+  hist = v.first;
+  scan = v.second;
+}
+
 static int route_sort_launch(const void* indices, int indices_i64, int64_t T, int K, int E,
                              int64_t threshold, int32_t* counts, int32_t* offsets, int32_t* row_of,
                              int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
-                             int32_t* use_fp8, int32_t* bh, hipStream_t sm, const char* what) {
+                             int32_t* use_fp8, int32_t* bh, hipStream_t sm, const char* what,
+                             const WeightSide* side = nullptr) {
   const int64_t A = T * K;
   FM_REQUIRE(indices || A == 0, "%s: null indices", what);
   FM_REQUIRE(E >= 1 && E <= kSortMaxExperts, "%s: E must be in [1, %d]", what, kSortMaxExperts);
@@ -858,25 +882,49 @@ static int route_sort_launch(const void* indices, int indices_i64, int64_t T, in
   FM_REQUIRE(rows_max >= fm_route_rows_max(A, E) && rows_max % 128 == 0,
              "%s: rows_max must be >= fm_route_rows_max() and a multiple of 128", what);
   const int64_t nb = (A + kSortBlock - 1) / kSortBlock;
+  const bool fused = nb > 0 && nb <= kFusedBlocks && E <= kFusedExperts && gemm_route_fused_scan();
+  // weight blocks: [0, wh) beside the histograms, [wh, wh + ws) beside the
+  // fused scan + scatter, the rest on their own after the sort
+  WeightSide sh{}, sc{};
+  int64_t wh = 0, wsc = 0;
+  if (side != nullptr && nb > 0) {
+    int ph, pc;
+    sort_side_shares(ph, pc);
+    wh = side->total * ph / 100;
+    wsc = fused ? side->total * pc / 100 : 0;
+    sh = *side;
+    sh.first = 0;
+    sh.count = wh;
+    sc = *side;
+    sc.first = wh;
+    sc.count = wsc;
+    FM_REQUIRE(nb + wh < (int64_t(1) << 31) && nb + wsc < (int64_t(1) << 31), "%s: too many weight blocks", what);
+  }
   if (nb > 0) {
+    const dim3 g(unsigned(nb + wh));
     if (indices_i64)
-      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int64_t*>(indices), A, E, bh, nb);
+      hipLaunchKernelGGL(sort_hist_kernel<int64_t>, g, dim3(256), 0, sm, static_cast<const int64_t*>(indices), A, E,
+                         bh, nb, sh);
     else
-      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
-                         static_cast<const int32_t*>(indices), A, E, bh, nb);
+      hipLaunchKernelGGL(sort_hist_kernel<int32_t>, g, dim3(256), 0, sm, static_cast<const int32_t*>(indices), A, E,
+                         bh, nb, sh);
     if (int rc = check_launch(what)) return rc;
   }
-  if (nb > 0 && nb <= kFusedBlocks && E <= kFusedExperts && gemm_route_fused_scan()) {
+  auto rest = [&]() -> int {
+    return side != nullptr ? launch_weight_side(*side, wh + wsc, side->total - wh - wsc, sm) : 0;
+  };
+  if (fused) {
+    const dim3 g(unsigned(nb + wsc));
     if (indices_i64)
-      hipLaunchKernelGGL(sort_scan_scatter_kernel<int64_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+      hipLaunchKernelGGL(sort_scan_scatter_kernel<int64_t>, g, dim3(256), 0, sm,
                          static_cast<const int64_t*>(indices), A, E, bh, nb, counts, offsets, tile_expert,
-                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold);
+                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold, sc);
     else
-      hipLaunchKernelGGL(sort_scan_scatter_kernel<int32_t>, dim3(unsigned(nb)), dim3(256), 0, sm,
+      hipLaunchKernelGGL(sort_scan_scatter_kernel<int32_t>, g, dim3(256), 0, sm,
                          static_cast<const int32_t*>(indices), A, E, bh, nb, counts, offsets, tile_expert,
-                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold);
-    return check_launch(what);
+                         rows_max / 128, row_of, assign_of_row, rows_max, use_fp8, threshold, sc);
+    if (int rc = check_launch(what)) return rc;
+    return rest();
   }
   hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, sm, bh, nb, E, counts, offsets,
                      tile_expert, rows_max / 128, assign_of_row, rows_max, use_fp8, threshold);
@@ -892,7 +940,7 @@ static int route_sort_launch(const void* indices, int indices_i64, int64_t T, in
                          assign_of_row);
     if (int rc = check_launch(what)) return rc;
   }
-  return 0;
+  return rest();
 }
 
 // ------------------------------------------------ allocation-free scratch ----
@@ -987,6 +1035,19 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
   return route_sort_launch(indices, indices_i64, T, K, E, threshold, counts, offsets, row_of, assign_of_row,
                            rows_max, tile_expert, use_fp8, static_cast<int32_t*>(workspace),
                            static_cast<hipStream_t>(stream), "fm_route_sort");
+}
+
+int fm_route_sort_weights(const void* indices, int indices_i64, int64_t T, int K, int E, int64_t threshold,
+                          int32_t* counts, int32_t* offsets, int32_t* row_of, int32_t* assign_of_row,
+                          int64_t rows_max, int32_t* tile_expert, int32_t* use_fp8, void* workspace,
+                          int64_t workspace_bytes, const FmWeightJob* jobs, int n_jobs, void* stream) {
+  FM_REQUIRE(workspace, "fm_route_sort_weights: null workspace");
+  FM_REQUIRE(workspace_bytes >= fm_route_workspace_bytes(T * K, E), "fm_route_sort_weights: workspace too small");
+  WeightSide side;
+  if (int rc = make_weight_side(jobs, n_jobs, side, "fm_route_sort_weights")) return rc;
+  return route_sort_launch(indices, indices_i64, T, K, E, threshold, counts, offsets, row_of, assign_of_row,
+                           rows_max, tile_expert, use_fp8, static_cast<int32_t*>(workspace),
+                           static_cast<hipStream_t>(stream), "fm_route_sort_weights", &side);
 }
 
 int64_t fm_route_sort_noalloc_max_workspace_bytes(void) { return kRouteScratchBytes; }

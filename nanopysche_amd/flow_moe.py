@@ -591,16 +591,32 @@ class ExpertWeights:
         self.kind = kind
         self.key = None
         self.has_dgrad = False
+        self._defer = None
         self.w13 = self.w2t = self.w2 = self.w13t = None
 
-    def refresh(self, w1, w2, w3, E: int, need_dgrad: bool = True) -> "ExpertWeights":
+    def refresh(self, w1, w2, w3, E: int, need_dgrad: bool = True, defer: Optional[list] = None) -> "ExpertWeights":
+        """Rebuild the operands if a parameter changed.  With ``defer`` (a list)
+        the batched quantisation launch is not made but appended as (FmWeightJob
+        array, count, sources): the caller runs it (``route_tokens(weight_jobs=
+        (array, count))`` or ``fm_quantize_weight_batch``) before the operands are
+        read, holding ``sources`` (the tensors the jobs read) until then."""
         key = tuple((w.data_ptr(), w._version, w.dtype) for w in (w1, w2, w3))
         if key != self.key or (need_dgrad and not self.has_dgrad):
             self.w13 = self.w2t = self.w2 = self.w13t = None
             self.has_dgrad = need_dgrad
-            self._build(w1.detach(), w2.detach(), w3.detach(), E, need_dgrad)
+            self._defer = defer
+            try:
+                self._build(w1.detach(), w2.detach(), w3.detach(), E, need_dgrad)
+            finally:
+                self._defer = None
             self.key = key
         return self
+
+    def _launch(self, jobs, n: int, stream, sources) -> None:
+        if self._defer is not None:
+            self._defer.append((jobs, n, sources))
+        else:
+            _lib.call("fm_quantize_weight_batch", jobs, n, stream)
 
     def _build(self, w1, w2, w3, E, dgrad=True):
         EH, D = w1.shape
@@ -647,7 +663,7 @@ class ExpertWeights:
         jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, W13t, S13t, 0, 0, 2 * H),
                                       job(srcs[1], W13, S13, W13t, S13t, H, H, 2 * H),
                                       job(srcs[2], W2, S2, W2t, S2t, 0, 0, H))
-        _lib.call("fm_quantize_weight_batch", jobs, 3, stream)
+        self._launch(jobs, 3, stream, srcs)
         sh = 7
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, (2 * H // 128) * (D // 128), sh, 2 * H, D)
         self.w2t = ExpertWeightOperand(W2t, S2t, H, D * H, H // 128, 1, (D // 128) * (H // 128), sh, D, H)
@@ -677,7 +693,7 @@ class ExpertWeights:
 
         jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, 0, 2 * H), job(srcs[1], W13, S13, H, 2 * H),
                                       job(srcs[2], W2, S2, 0, H))
-        _lib.call("fm_quantize_weight_batch", jobs, 3, _lib.stream_of(w1))
+        self._launch(jobs, 3, _lib.stream_of(w1), srcs)
         sh = 7
         g13, g2 = (2 * H // 128) * (D // 128), (H // 128) * (D // 128)
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, g13, sh, 2 * H, D)
@@ -713,7 +729,7 @@ class ExpertWeights:
         if dgrad:
             jobs += [job(w1, W13t, 0, 2 * H), job(w3, W13t, H, 2 * H)]
         arr = (_lib.FmWeightJob * len(jobs))(*jobs)
-        _lib.call("fm_quantize_weight_batch", arr, len(jobs), _lib.stream_of(w1))
+        self._launch(arr, len(jobs), _lib.stream_of(w1), (w1, w2, w3))
         self.w13 = ExpertWeightOperand(w1, None, D, H * D, N=2 * H, K=D, data2=w3, split=H)
         self.w2 = ExpertWeightOperand(w2, None, D, H * D, N=H, K=D)
         self.w2t = ExpertWeightOperand(W2t, None, H, D * H, N=D, K=H)
@@ -834,11 +850,11 @@ class FP8FlowMoECompute:
                                  f"[{self.num_experts * self.hidden_size}, {self.d_model}], got {tuple(w.shape)}")
         self._w = (w1, w2, w3)
 
-    def _weights(self, kind: int, need_dgrad: bool = True) -> ExpertWeights:
+    def _weights(self, kind: int, need_dgrad: bool = True, defer: Optional[list] = None) -> ExpertWeights:
         ew = self._cache.get(kind)
         if ew is None:
             ew = self._cache[kind] = ExpertWeights(kind)
-        return ew.refresh(*self._w, self.num_experts, need_dgrad)
+        return ew.refresh(*self._w, self.num_experts, need_dgrad, defer)
 
     def modes(self, num_assignments: int):
         """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
@@ -883,12 +899,23 @@ class FP8FlowMoECompute:
         fp8_kind, use_bf16 = self.modes(T * K)
         dev = x.device
         thr = self.fp8_gemm_threshold if fp8_kind is not None else 1 << 62
+        # expert-weight refreshes are deferred so the first batch runs with the
+        # routing sort (its blocks fill the CUs the sort leaves idle)
+        kinds = [k for k in (fp8_kind, _lib.QUANT_BF16 if use_bf16 else None) if k is not None]
+        batches = []
+        ews = {k: self._weights(k, self._record, batches) for k in kinds}
+        side = batches.pop(0) if batches else None
         if self._dense:
             plan = self._dense_plans.get((T, dev))
             if plan is None:
-                plan = self._dense_plans[(T, dev)] = route_tokens(indices, E, thr)
+                plan = self._dense_plans[(T, dev)] = route_tokens(indices, E, thr, side and side[:2])
+                side = None
         else:
-            plan = route_tokens(indices, E, thr)
+            plan = route_tokens(indices, E, thr, side and side[:2])
+            side = None
+        for jobs, n, _sources in ([side] if side is not None else []) + batches:
+            _lib.call("fm_quantize_weight_batch", jobs, n, _lib.stream_of(x))
+        del side, batches   # the launches are enqueued: their sources may go
         wts = weights.to(torch.float32).contiguous()
         R = plan.rows_max
         GU = torch.empty(R, 2 * H, dtype=torch.bfloat16, device=dev)
@@ -898,7 +925,7 @@ class FP8FlowMoECompute:
         for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
             if kind is None:
                 continue
-            ew = self._weights(kind, self._record)
+            ew = ews[kind]
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                    return_transpose=self._record, kmajor_scales=True)
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)

@@ -54,8 +54,14 @@ def rows_max(num_assignments: int, num_experts: int) -> int:
     return int(_lib.load().fm_route_rows_max(num_assignments, num_experts))
 
 
-def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: int = 0) -> RoutingPlan:
-    """Stable counting sort of ``indices`` [T, K] (int64 or int32) by expert."""
+def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: int = 0,
+                 weight_jobs=None) -> RoutingPlan:
+    """Stable counting sort of ``indices`` [T, K] (int64 or int32) by expert.
+
+    ``weight_jobs`` = (ctypes FmWeightJob array, count): an expert-weight
+    batch run with the sort (``fm_route_sort_weights``: part of its blocks as
+    extra workgroups of the sort's launches), as if ``fm_quantize_weight_batch``
+    had been called after it on the same stream."""
     _lib.require_device(indices, "indices")
     if indices.dim() != 2:
         indices = indices.reshape(-1, indices.shape[-1])
@@ -76,10 +82,13 @@ def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: in
     use_fp8 = torch.empty(num_experts, **i32)
     ws_bytes = int(lib.fm_route_workspace_bytes(A, num_experts))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.call("fm_route_sort", _lib.ptr(indices), int(indices.dtype == torch.int64), T, K,
-              num_experts, int(fp8_gemm_threshold), _lib.ptr(counts), _lib.ptr(offsets),
-              _lib.ptr(row_of), _lib.ptr(assign_of_row), rmax, _lib.ptr(tile_expert),
-              _lib.ptr(use_fp8), _lib.ptr(ws), ws_bytes, _lib.stream_of(indices))
+    args = (_lib.ptr(indices), int(indices.dtype == torch.int64), T, K, num_experts, int(fp8_gemm_threshold),
+            _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(row_of), _lib.ptr(assign_of_row), rmax,
+            _lib.ptr(tile_expert), _lib.ptr(use_fp8), _lib.ptr(ws), ws_bytes)
+    if weight_jobs is None:
+        _lib.call("fm_route_sort", *args, _lib.stream_of(indices))
+    else:
+        _lib.call("fm_route_sort_weights", *args, weight_jobs[0], weight_jobs[1], _lib.stream_of(indices))
     return RoutingPlan(T, K, num_experts, rmax, counts, offsets, row_of[:A], assign_of_row,
                        tile_expert, use_fp8)
 

@@ -266,3 +266,33 @@ def test_weight_cache_bf16_operands_are_exact_copies(dev, param_dtype, H):
         assert torch.equal(ew.w2.data.reshape(E, H, D).cpu(), b(w2))
     assert torch.equal(ew.w2t.data.reshape(E, D, H).cpu(), b(w2).transpose(1, 2))
     assert torch.equal(ew.w13t.data.reshape(E, D, 2 * H).cpu(), W13.transpose(1, 2))
+
+
+@pytest.mark.parametrize("kind,E,H,D,T,K", [("pow2", 8, 256, 512, 3000, 2), ("pow2", 4, 384, 384, 2000, 2),
+                                             ("bf16", 4, 256, 256, 2000, 1), ("pow2", 8, 256, 256, 40000, 2)])
+def test_weight_batch_with_the_sort_matches(dev, kind, E, H, D, T, K):
+    """fm_route_sort_weights: the routing plan and every expert-weight operand
+    equal those of fm_route_sort then fm_quantize_weight_batch, bit for bit
+    (part of the weight blocks run beside the histograms and the fused scan +
+    scatter, the rest on their own; the last case's 80000 assignments take the
+    unfused scan and scatter).  Cases: pow2 rows-only, pow2 with transposed
+    copies, BF16 transposes of parameters read in place."""
+    from nanopysche_amd import _lib
+    from nanopysche_amd.flow_moe import ExpertWeights
+    from nanopysche_amd.routing import route_tokens
+    k = {"pow2": _lib.QUANT_POW2, "bf16": _lib.QUANT_BF16}[kind]
+    g = torch.Generator().manual_seed(E * H + T)
+    w1, w2, w3 = ((torch.randn(E * H, D, generator=g) * 0.02).to(torch.bfloat16).to(dev) for _ in range(3))
+    idx = torch.randint(0, E, (T, K), generator=g).to(dev)
+    ref_w = ExpertWeights(k).refresh(w1, w2, w3, E)
+    ref_p = route_tokens(idx, E, 0)
+    pending = []
+    ew = ExpertWeights(k).refresh(w1, w2, w3, E, defer=pending)
+    assert len(pending) == 1 and ew.w2t is not None
+    plan = route_tokens(idx, E, 0, pending[0][:2])
+    for f in ("counts", "offsets", "row_of", "assign_of_row", "tile_expert", "use_fp8"):
+        assert torch.equal(getattr(plan, f), getattr(ref_p, f)), f
+    for name in ("w13", "w2t", "w2", "w13t"):
+        a, b = getattr(ew, name), getattr(ref_w, name)
+        assert torch.equal(a.data, b.data), name
+        assert (a.scale is None) == (b.scale is None) and (a.scale is None or torch.equal(a.scale, b.scale)), name
