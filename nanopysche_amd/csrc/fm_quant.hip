@@ -346,6 +346,7 @@ int make_weight_side(const FmWeightJob* jobs, int n_jobs, WeightSide& ws, const 
   ws.tiles_y = jobs[0].rows / 128;
   ws.total = ws.tiles_x * ws.tiles_y * ws.b.groups * n_jobs;
   ws.src_f32 = jobs[0].w_dtype == FM_DTYPE_F32;
+  FM_REQUIRE(ws.total < (int64_t(1) << 31), "%s: %lld weight blocks (at most 2^31 - 1)", what, (long long)ws.total);
   return 0;
 }
 

@@ -857,10 +857,13 @@ inline bool gemm_route_fused_scan() {
 // clearing.
 // Shares (percent of an expert-weight batch's blocks) that the histogram and
 // the fused scan + scatter launches run beside their own workgroups
-// (FM_SORT_SIDE="hist,scan", read once); the rest runs as its own launch.
+// (FM_SORT_SIDE="hist,scan", read once; without the fused launch the
+// histogram takes both); the rest runs as its own launch.  Default: all in
+// the fused launch -- one ramp and one tail for the whole batch, and the
+// longer of the two sort launches hidden.
 inline void sort_side_shares(int& hist, int& scan) {
   static const std::pair<int, int> v = [] {
-    int h = 50, c = 50;
+    int h = 0, c = 100;
     if (const char* e = getenv("FM_SORT_SIDE")) sscanf(e, "%d,%d", &h, &c);
     h = h < 0 ? 0 : h > 100 ? 100 : h;
     c = c < 0 ? 0 : c > 100 - h ? 100 - h : c;
@@ -890,7 +893,7 @@ static int route_sort_launch(const void* indices, int indices_i64, int64_t T, in
   if (side != nullptr && nb > 0) {
     int ph, pc;
     sort_side_shares(ph, pc);
-    wh = side->total * ph / 100;
+    wh = side->total * (fused ? ph : ph + pc) / 100;
     wsc = fused ? side->total * pc / 100 : 0;
     sh = *side;
     sh.first = 0;

@@ -205,12 +205,15 @@ struct WeightSide {
 __device__ __forceinline__ void weight_side_block(const WeightSide& ws, int64_t i) {
   __shared__ float red[256];
   __shared__ uint32_t tile[128][65];
-  const int64_t blk = ws.first + i;
-  const int64_t x = blk % ws.tiles_x, yz = blk / ws.tiles_x;
-  const int64_t y = yz % ws.tiles_y, z = yz / ws.tiles_y;
-  const int j = int(z / ws.b.groups);
-  if (ws.src_f32) weight_quant_tile<float>(ws.b.job[j], z - j * ws.b.groups, y, x, red, tile);
-  else weight_quant_tile<uint16_t>(ws.b.job[j], z - j * ws.b.groups, y, x, red, tile);
+  // 32-bit decode (the host keeps total < 2^31): 64-bit divisions are long
+  // emulated sequences, as costly as a tile's own arithmetic
+  const uint32_t blk = uint32_t(ws.first + i), tx = uint32_t(ws.tiles_x), ty = uint32_t(ws.tiles_y);
+  const uint32_t gr = uint32_t(ws.b.groups);
+  const uint32_t yz = blk / tx, x = blk - yz * tx;
+  const uint32_t z = yz / ty, y = yz - z * ty;
+  const uint32_t j = z / gr, g = z - j * gr;
+  if (ws.src_f32) weight_quant_tile<float>(ws.b.job[j], g, y, x, red, tile);
+  else weight_quant_tile<uint16_t>(ws.b.job[j], g, y, x, red, tile);
 }
 
 // Host side (fm_quant.hip): validate 1-4 jobs as fm_quantize_weight_batch does
