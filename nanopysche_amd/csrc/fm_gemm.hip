@@ -97,7 +97,7 @@ struct GemmParams {
   int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
   int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
   int rk_jfast;       // ragged-K: j tiles (a_t's) vary fastest within a group of i tiles
-  int q_nn;           // ragged-M: the weights stored [K][N] (persistent FP8 pow2 kernel only)
+  int q_nn;           // ragged-M: the weights stored [K][N] (persistent BF16 / FP8 pow2 kernel only)
 };
 
 constexpr int kGroupM = 8;
@@ -250,6 +250,25 @@ __device__ __forceinline__ OpStream make_stream_nn(const uint8_t* base, int64_t 
   return s;
 }
 
+// BF16 NN weight operand (stored [K][N]: element (i, k) at k * ld + i).  A K
+// step of a 256-row tile is 64 K rows of 512 bytes in LDS, K row k's 16-byte
+// chunk c stored at chunk c ^ 4 (k % 4), so the four K rows one transposed
+// read touches fall on distinct bank slots.  The DMA moves 32 groups of 2 K
+// rows (1 KiB) per step, 4 consecutive groups per wave; lane n of a group
+// loads K row n / 32, global chunk (n % 32) ^ 4 (k % 4).
+__device__ __forceinline__ OpStream make_stream_nn16(const uint8_t* base, int64_t ld_bytes, int lane, int wave) {
+  OpStream s;
+  s.group_bytes = uint32_t(2 * ld_bytes);
+  s.k_row_bytes = uint32_t(ld_bytes);
+  s.rsrc = make_rsrc(base + int64_t(wave) * 8 * ld_bytes);
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int row = lane >> 5, kk = 2 * par + row;   // k % 4 of the lane's K row
+    s.lane_off[par] = uint32_t(row * ld_bytes + 16 * ((lane & 31) ^ (4 * kk)));
+  }
+  return s;
+}
+
 typedef int v2i __attribute__((ext_vector_type(2)));
 // ds_read_b64_tr_b8 (gfx950): in each 16-lane group, lanes 2r and 2r + 1 give
 // the addresses of bytes 0-7 and 8-15 of row r (r = 0..7), and lane m of the
@@ -278,6 +297,31 @@ __device__ __forceinline__ v8i read_frag8_nn(const uint8_t* st, int ibase, int h
   f[0] = p0[0]; f[1] = p0[1]; f[2] = p1[0]; f[3] = p1[1];
   f[4] = p2[0]; f[5] = p2[1]; f[6] = p3[0]; f[7] = p3[1];
   return f;
+}
+
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 (gfx950): in each 16-lane group, lane 4r + p gives the
+// address of elements [4p, 4p + 4) of row r (r = 0..3), and lane m of the
+// group receives element m of every row (4 elements, row order).  Established
+// with an in-bounds probe of the instruction on the device.
+__device__ __forceinline__ v4s16 lds_read_tr16(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) v4s16*>(
+          reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(lds_addr(p))));
+}
+
+// BF16 NN A fragment of rows ibase + (lane % 32) (ibase a multiple of 32), K
+// slice ks (16 deep) of the step: lane half h = lane / 32 takes K [16 ks + 8 h,
+// +8) of its row as two reads of four K rows -- the element order of
+// read_frag16.  Every K row a lane addresses has k % 4 == r = (lane % 16) / 4.
+__device__ __forceinline__ v8bf read_frag16_nn(const uint8_t* st, int ibase, int ks, int lane) {
+  const int m = lane & 15, r = m >> 2;
+  const int col = ibase + ((lane >> 4) & 1) * 16 + (m & 3) * 4;
+  const int k = 16 * ks + 8 * (lane >> 5) + r;
+  const uint8_t* b = st + k * 512 + (((col >> 3) ^ (4 * r)) << 4) + (col & 7) * 2;
+  const v4s16 lo = lds_read_tr16(b);
+  const v4s16 hi = lds_read_tr16(b + 4 * 512);
+  return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // Scales in LDS.  pow2: the DMA places the fp32 scale of tile row
@@ -385,7 +429,8 @@ __device__ __forceinline__ void read_half(const uint8_t* st, int half, Frag<KIND
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
+        if constexpr (QNN) f.a[s2][t] = read_frag16_nn(st, w.wi * 128 + t * 32, half * 2 + s2, w.lane);
+        else f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
         if (t < 2) f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, half * 2 + s2, w.lhalf);
       }
   } else {
@@ -446,11 +491,12 @@ __device__ __forceinline__ void issue_read_half0(const OpStream& qst, const OpSt
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, s2, w.lhalf);
+        if constexpr (QNN) f.a[s2][t] = read_frag16_nn(st, w.wi * 128 + t * 32, s2, w.lane);
+        else f.a[s2][t] = read_frag16(st, w.wi * 128 + t * 32 + w.lrow, s2, w.lhalf);
         if (t < 2) f.b[s2][t] = read_frag16(st + SM::kP, w.wj * 64 + t * 32 + w.lrow, s2, w.lhalf);
       }
-      issue_piece<KIND>(2 * t, qst, pst, sc, k, dst, wave);
-      issue_piece<KIND>(2 * t + 1, qst, pst, sc, k, dst, wave);
+      issue_piece<KIND, QNN>(2 * t, qst, pst, sc, k, dst, wave);
+      issue_piece<KIND, QNN>(2 * t + 1, qst, pst, sc, k, dst, wave);
     }
   } else {
     if constexpr (KIND == GK_FP8_MX) {
@@ -516,7 +562,8 @@ __device__ __forceinline__ void mma_half(const Frag<KIND>& f, v16f (&acc)[4][2])
 template <int KIND, bool QNN = false>
 __device__ __forceinline__ void interleave_half() {
   constexpr int kMfma = KIND == GK_BF16 ? 16 : 8;
-  constexpr int kReads = KIND == GK_BF16 ? 1 : QNN ? 3 : 2;   // NN: four 8-byte reads per A fragment
+  // NN: four 8-byte reads per FP8 A fragment, two per BF16 one
+  constexpr int kReads = KIND == GK_BF16 ? (QNN ? 2 : 1) : QNN ? 3 : 2;
 #pragma unroll
   for (int i = 0; i < kMfma; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
@@ -952,7 +999,10 @@ __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Oper
   const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
   const int lane = fresh_lane();
   if constexpr (QNN) {
-    s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
+    if constexpr (KIND == GK_BF16)
+      s.q = make_stream_nn16(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0)) * 2, Q.ld * 2, lane, w.wave);
+    else
+      s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
   } else {   // a tile lies in one of the two tensors of a split operand (split % 256 == 0)
     const bool second = t.i0 >= Q.split;
     const int64_t qi = second ? t.i0 - Q.split : t.i0;
@@ -1028,8 +1078,9 @@ __device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8
     }
 }
 
-// QNN (FP8 pow2 only): the weight operand Q is stored [K][N] (make_stream_nn,
-// read_frag8_nn); all N tiles are full (N % 256 == 0, checked by the launcher).
+// QNN (BF16 and FP8 pow2): the weight operand Q is stored [K][N]
+// (make_stream_nn16 / read_frag16_nn, make_stream_nn / read_frag8_nn); all N
+// tiles are full (N % 256 == 0, checked by the launcher).
 template <int KIND, int MXL = 0, bool QNN = false>
 __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
   using SM = Smem256<KIND>;
@@ -1937,7 +1988,10 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
   const int64_t want = (p.n_tiles + 7) / 8 * 8;
   const dim3 grid(unsigned(want < slots ? want : slots)), block(512);
   switch (kind) {
-    case GK_BF16: hipLaunchKernelGGL((gemm256p_kernel<GK_BF16>), grid, block, 0, s, p); break;
+    case GK_BF16:
+      if (p.q_nn) hipLaunchKernelGGL((gemm256p_kernel<GK_BF16, 0, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((gemm256p_kernel<GK_BF16>), grid, block, 0, s, p);
+      break;
     case GK_FP8_POW2:
       if (p.q_nn) hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2, 0, true>), grid, block, 0, s, p);
       else hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
@@ -2128,10 +2182,12 @@ int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmO
                     const int32_t* expert_mask, int mask_want, void* out, int out_dtype, int64_t ld_out,
                     GemmParams& p) {
   FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
-  FM_REQUIRE(!nn || (kind == GK_FP8_POW2 && E <= 64 && N % 256 == 0 && K >= 256 && weights->ld >= N &&
-                     weights->group_stride >= K * weights->ld),
-             "fm_grouped_gemm_ragged_m: [K][N] weights need the pow2 kind, E <= 64, N a multiple of 256, K >= 256, "
-             "a row pitch >= N and a group stride >= K x pitch");
+  FM_REQUIRE(!nn || (((kind == GK_FP8_POW2 && K >= 256) || (kind == GK_BF16 && K >= 128)) && E <= 64 &&
+                     N % 256 == 0 && weights->ld >= N && weights->group_stride >= K * weights->ld &&
+                     K * weights->ld * (kind == GK_BF16 ? 2 : 1) < (int64_t(1) << 32)),
+             "fm_grouped_gemm_ragged_m: [K][N] weights need the pow2 kind with K >= 256 or BF16 with K >= 128, "
+             "E <= 64, N a multiple of 256, a row pitch >= N, a group stride >= K x pitch and K x pitch bytes "
+             "below 2^32");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
   FM_REQUIRE(tokens->data2 == nullptr, "fm_grouped_gemm_ragged_m: the token operand cannot be split");

@@ -713,10 +713,13 @@ class ExpertWeights:
 
     def _build_bf16_views(self, w1, w2, w3, E, H, D, dgrad):
         """w13: w1 and w3 read as stored (a split operand), w2: the parameter
-        itself; only the transposed operands are written (w2t, and w13t for a
-        backward), in one launch."""
+        itself, and for D a multiple of 256 w2t too (the down GEMM reads w2's
+        [K = H][N = D] rows transposed in LDS); only the other transposed
+        operands are written (w2t otherwise, w13t for a backward), in one
+        launch -- none for a forward with D a multiple of 256."""
         dev = w1.device
-        W2t = torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
+        nn = D % 256 == 0
+        W2t = None if nn else torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
         W13t = torch.empty(E, D, 2 * H, dtype=torch.bfloat16, device=dev) if dgrad else None
         BF = _lib.QUANT_BF16
 
@@ -725,14 +728,18 @@ class ExpertWeights:
                                     None, 0, 0, 0, None, 0, 0,
                                     _lib.ptr(dst_t), cols_out, D * cols_out, col_off, None, 0, 0)
 
-        jobs = [job(w2, W2t, 0, H)]
+        jobs = [] if nn else [job(w2, W2t, 0, H)]
         if dgrad:
             jobs += [job(w1, W13t, 0, 2 * H), job(w3, W13t, H, 2 * H)]
-        arr = (_lib.FmWeightJob * len(jobs))(*jobs)
-        self._launch(arr, len(jobs), _lib.stream_of(w1), (w1, w2, w3))
+        if jobs:
+            arr = (_lib.FmWeightJob * len(jobs))(*jobs)
+            self._launch(arr, len(jobs), _lib.stream_of(w1), (w1, w2, w3))
         self.w13 = ExpertWeightOperand(w1, None, D, H * D, N=2 * H, K=D, data2=w3, split=H)
         self.w2 = ExpertWeightOperand(w2, None, D, H * D, N=H, K=D)
-        self.w2t = ExpertWeightOperand(W2t, None, H, D * H, N=D, K=H)
+        if nn:
+            self.w2t = ExpertWeightOperand(w2, None, D, H * D, N=D, K=H, kmajor=True)
+        else:
+            self.w2t = ExpertWeightOperand(W2t, None, H, D * H, N=D, K=H)
         if dgrad:
             self.w13t = ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H)
 

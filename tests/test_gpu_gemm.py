@@ -327,3 +327,27 @@ def test_bf16_split_weights_match_stacked(dev, E, T, K, zeros, masked):
         pair.append((o1[:used], o2))
     assert torch.equal(pair[0][0], pair[1][0]) and torch.equal(pair[0][1], pair[1][1])
     assert torch.equal(pair[1][0], outs[1])
+
+
+@pytest.mark.parametrize("E,T,K,zeros,D,H", [(8, 3000, 2, (2, 5), 512, 384), (4, 2500, 1, (1,), 256, 512),
+                                             (64, 6000, 4, (7, 63), 256, 128)])
+def test_bf16_kmajor_weights_match(dev, E, T, K, zeros, D, H):
+    """FM_GEMM_W_KMAJOR with BF16: the down GEMM reading w2 [E][K = H][N = D]
+    transposed in LDS (ds_read_b64_tr_b16) gives the bits of the same GEMM on
+    the transposed copy [E][D][H], fp32 and bf16 outputs."""
+    from nanopysche_amd.flow_moe import ExpertWeightOperand, _gemm_m
+    x = randn_bf16((T, H), seed=1)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)
+    w2 = randn_bf16((E * H, D), seed=3, std=0.02).to(dev)
+    pt = fm.fused_permute_pad(x.to(dev), idx.to(dev), E, granularity=None)
+    plan = pt.plan
+    nn = ExpertWeightOperand(w2, None, D, H * D, N=D, K=H, kmajor=True)
+    nt = ExpertWeightOperand(w2.view(E, H, D).transpose(1, 2).contiguous(), None, H, D * H, N=D, K=H)
+    used = int(plan.offsets[-1].item())
+    for dt in (torch.float32, torch.bfloat16):
+        outs = []
+        for w in (nt, nn):
+            out = torch.zeros(plan.rows_max, D, dtype=dt, device=dev)
+            _gemm_m(_lib.QUANT_BF16, pt.rows, w, plan, out)
+            outs.append(out[:used])
+        assert torch.equal(outs[0], outs[1]), dt
