@@ -61,9 +61,10 @@ extern "C" {
  * (ld >= N), e.g. an expert's w2 [H, D] rows for the down projection -- and
  * read transposed in LDS, so no [N][K] copy is needed.  FM_GEMM_FP8_POW2 with
  * 128 x 128 weight blocks (scale of rows n, K block kb at
- * s[e * scale_group_stride + (n >> 7) * scale_row_stride + kb * scale_kb_stride]),
- * E <= 64, N a multiple of 256 and K >= 256.  The results are those of the
- * [N][K] layout bit for bit. */
+ * s[e * scale_group_stride + (n >> 7) * scale_row_stride + kb * scale_kb_stride])
+ * and K >= 256, or FM_GEMM_BF16 with K >= 128; E <= 64, N a multiple of 256,
+ * K x ld bytes below 2^32.  The results are those of the [N][K] layout bit for
+ * bit. */
 #define FM_GEMM_W_KMAJOR 0x200
 
 /* gating functions (reference model/moe.py:44-46 GatingFunction) */
