@@ -427,8 +427,9 @@ int fm_swiglu_values(const void* g, int64_t ld_g, const void* u, int64_t ld_u, c
  * data2 (NULL: unused) splits each group's rows over two tensors of the same
  * pitch and group stride: rows r >= split_rows are row r - split_rows of
  * data2 -- the weights of fm_grouped_gemm_ragged_m read from w1 and w3 as
- * they are stored, without stacking them.  BF16 weights only, split_rows a
- * multiple of 256, at most 64 experts. */
+ * they are stored, without stacking them.  BF16 weights only, at most 64
+ * experts; split_rows a multiple of 256 inside N, or, with FM_GEMM_W_KMAJOR
+ * (rows are K rows), a multiple of 64 inside K. */
 typedef struct FmGemmOperand {
   const void* data;
   int64_t ld;            /* row pitch, elements */

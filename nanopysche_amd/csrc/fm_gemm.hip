@@ -201,6 +201,8 @@ struct OpStream {
   uint32_t group_bytes;   // 8 rows (NN layout: 4 K rows)
   uint32_t lane_off[2];   // even / odd group
   uint32_t k_row_bytes;   // NN layout: bytes per K row (a K step advances 128 of them)
+  v4i rsrc2;              // BF16 NN split along K: descriptor of the second tensor
+  uint32_t k_split;       //   and the K row it starts at (UINT32_MAX: no split)
 };
 
 __device__ __forceinline__ OpStream make_stream(const uint8_t* base, int64_t row_bytes, int64_t rows, int lane,
@@ -256,11 +258,15 @@ __device__ __forceinline__ OpStream make_stream_nn(const uint8_t* base, int64_t 
 // read touches fall on distinct bank slots.  The DMA moves 32 groups of 2 K
 // rows (1 KiB) per step, 4 consecutive groups per wave; lane n of a group
 // loads K row n / 32, global chunk (n % 32) ^ 4 (k % 4).
-__device__ __forceinline__ OpStream make_stream_nn16(const uint8_t* base, int64_t ld_bytes, int lane, int wave) {
+// With a split, K rows from k_split on come from base2 (row k - k_split).
+__device__ __forceinline__ OpStream make_stream_nn16(const uint8_t* base, const uint8_t* base2, int64_t k_split,
+                                                     int64_t ld_bytes, int lane, int wave) {
   OpStream s;
   s.group_bytes = uint32_t(2 * ld_bytes);
   s.k_row_bytes = uint32_t(ld_bytes);
   s.rsrc = make_rsrc(base + int64_t(wave) * 8 * ld_bytes);
+  s.rsrc2 = make_rsrc(base2 + int64_t(wave) * 8 * ld_bytes);
+  s.k_split = uint32_t(__builtin_amdgcn_readfirstlane(int(k_split < 0xffffffffll ? k_split : 0xffffffffll)));
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     const int row = lane >> 5, kk = 2 * par + row;   // k % 4 of the lane's K row
@@ -401,6 +407,21 @@ struct WaveCoord {
   bool q_mx_k, p_mx_k;
 };
 
+// The weight operand's descriptor and uniform byte offset for K step k (kb:
+// its byte offset in the NT layout): BF16 [K][N] weights split along K take
+// the rows from k_split on from the second tensor (a step never straddles it).
+template <int KIND, bool QNN>
+__device__ __forceinline__ void q_source(const OpStream& qst, int64_t k, uint32_t kb, v4i& rs, uint32_t& kq) {
+  if constexpr (QNN && KIND == GK_BF16) {
+    const bool second = uint32_t(k) >= qst.k_split;
+    rs = second ? qst.rsrc2 : qst.rsrc;
+    kq = (second ? uint32_t(k) - qst.k_split : uint32_t(k)) * qst.k_row_bytes;
+  } else {
+    rs = qst.rsrc;
+    kq = QNN ? uint32_t(k) * qst.k_row_bytes : kb;
+  }
+}
+
 // One K step of DMA for this wave: 4 row groups of each operand, then one
 // scale dword per lane (waves 0-3: Q scale slots, 4-7: P scale slots).
 template <int KIND, bool QNN = false>
@@ -410,10 +431,12 @@ __device__ __forceinline__ void issue_step(const OpStream& qst, const OpStream& 
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   const uint32_t kb = uint32_t(k * ES);
-  const uint32_t kq = QNN ? uint32_t(k) * qst.k_row_bytes : kb;
+  v4i qrs;
+  uint32_t kq;
+  q_source<KIND, QNN>(qst, k, kb, qrs, kq);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    bdma16(qst.rsrc, qst.lane_off[u & 1], u * qst.group_bytes + kq, dst + (wave * 4 + u) * 1024);
+    bdma16(qrs, qst.lane_off[u & 1], u * qst.group_bytes + kq, dst + (wave * 4 + u) * 1024);
     bdma16(pst.rsrc, pst.lane_off[u & 1], u * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + u) * 1024);
   }
   if constexpr (KIND != GK_BF16) bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
@@ -466,10 +489,12 @@ __device__ __forceinline__ void issue_piece(int u, const OpStream& qst, const Op
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
   constexpr int KSTEP = 128 / ES;
   const uint32_t kb = uint32_t(k * ES);
-  const uint32_t kq = QNN ? uint32_t(k) * qst.k_row_bytes : kb;
+  v4i qrs;
+  uint32_t kq;
+  q_source<KIND, QNN>(qst, k, kb, qrs, kq);
   if (u < 8) {
     const int g = u >> 1;
-    if ((u & 1) == 0) bdma16(qst.rsrc, qst.lane_off[g & 1], g * qst.group_bytes + kq, dst + (wave * 4 + g) * 1024);
+    if ((u & 1) == 0) bdma16(qrs, qst.lane_off[g & 1], g * qst.group_bytes + kq, dst + (wave * 4 + g) * 1024);
     else bdma16(pst.rsrc, pst.lane_off[g & 1], g * pst.group_bytes + kb, dst + SM::kP + (wave * 4 + g) * 1024);
   } else if constexpr (KIND != GK_BF16) {
     bdma4(sc.rsrc, sc.voff, uint32_t((k / KSTEP) * sc.k), dst + sc.dst);
@@ -999,10 +1024,12 @@ __device__ __forceinline__ TileStreams tile_streams(const Operand& Q, const Oper
   const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
   const int lane = fresh_lane();
   if constexpr (QNN) {
-    if constexpr (KIND == GK_BF16)
-      s.q = make_stream_nn16(Q.p + (int64_t(t.e) * Q.gs + int64_t(t.i0)) * 2, Q.ld * 2, lane, w.wave);
-    else
+    if constexpr (KIND == GK_BF16) {   // a split operand splits along K here
+      const int64_t off = (int64_t(t.e) * Q.gs + int64_t(t.i0)) * 2;
+      s.q = make_stream_nn16(Q.p + off, Q.p2 + off, Q.split, Q.ld * 2, lane, w.wave);
+    } else {
       s.q = make_stream_nn(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
+    }
   } else {   // a tile lies in one of the two tensors of a split operand (split % 256 == 0)
     const bool second = t.i0 >= Q.split;
     const int64_t qi = second ? t.i0 - Q.split : t.i0;
@@ -2182,20 +2209,26 @@ int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmO
                     const int32_t* expert_mask, int mask_want, void* out, int out_dtype, int64_t ld_out,
                     GemmParams& p) {
   FM_REQUIRE(tokens && weights && tile_expert && offsets && out, "fm_grouped_gemm_ragged_m: null pointer");
+  // K rows per tensor: a [K][N] operand split along K holds split_rows, then K - split_rows, per group
+  const int64_t nn_rows = weights->data2 == nullptr || weights->split_rows <= 0 || weights->split_rows >= K
+                              ? K
+                              : (weights->split_rows > K - weights->split_rows ? weights->split_rows
+                                                                               : K - weights->split_rows);
   FM_REQUIRE(!nn || (((kind == GK_FP8_POW2 && K >= 256) || (kind == GK_BF16 && K >= 128)) && E <= 64 &&
-                     N % 256 == 0 && weights->ld >= N && weights->group_stride >= K * weights->ld &&
-                     K * weights->ld * (kind == GK_BF16 ? 2 : 1) < (int64_t(1) << 32)),
+                     N % 256 == 0 && weights->ld >= N && weights->group_stride >= nn_rows * weights->ld &&
+                     nn_rows * weights->ld * (kind == GK_BF16 ? 2 : 1) < (int64_t(1) << 32)),
              "fm_grouped_gemm_ragged_m: [K][N] weights need the pow2 kind with K >= 256 or BF16 with K >= 128, "
              "E <= 64, N a multiple of 256, a row pitch >= N, a group stride >= K x pitch and K x pitch bytes "
-             "below 2^32");
+             "below 2^32 (split along K: the larger part's rows for K)");
   if (int rc = check_operand(*tokens, kind, "tokens")) return rc;
   if (int rc = check_operand(*weights, kind, "weights")) return rc;
   FM_REQUIRE(tokens->data2 == nullptr, "fm_grouped_gemm_ragged_m: the token operand cannot be split");
   FM_REQUIRE(weights->data2 == nullptr ||
-                 (kind == GK_BF16 && !nn && E <= 64 && K >= 128 && weights->split_rows > 0 &&
-                  weights->split_rows % 256 == 0 && weights->split_rows < N),
+                 (kind == GK_BF16 && E <= 64 && K >= 128 && weights->split_rows > 0 &&
+                  (nn ? weights->split_rows % 64 == 0 && weights->split_rows < K
+                      : weights->split_rows % 256 == 0 && weights->split_rows < N)),
              "fm_grouped_gemm_ragged_m: split weights need the BF16 kind, E <= 64, K >= 128 and a split that is "
-             "a multiple of 256 inside N");
+             "a multiple of 256 inside N ([K][N] weights: of 64 inside K)");
   if (int rc = check_scale_span(*tokens, kind, m_tiles * 128, K, "tokens")) return rc;
   if (int rc = check_scale_span(*weights, kind, N, K, "weights")) return rc;
   FM_REQUIRE(N > 0 && N % 128 == 0, "fm_grouped_gemm_ragged_m: N must be a positive multiple of 128 (got %lld)", (long long)N);

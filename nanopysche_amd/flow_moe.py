@@ -713,14 +713,14 @@ class ExpertWeights:
 
     def _build_bf16_views(self, w1, w2, w3, E, H, D, dgrad):
         """w13: w1 and w3 read as stored (a split operand), w2: the parameter
-        itself, and for D a multiple of 256 w2t too (the down GEMM reads w2's
-        [K = H][N = D] rows transposed in LDS); only the other transposed
-        operands are written (w2t otherwise, w13t for a backward), in one
-        launch -- none for a forward with D a multiple of 256."""
+        itself, and for D a multiple of 256 w2t and w13t too (the down and dX
+        GEMMs read w2's [K = H][N = D] rows, and w1's then w3's as one K = 2H
+        operand split along K, transposed in LDS): no weight is written then;
+        otherwise w2t and w13t (for a backward) are written, in one launch."""
         dev = w1.device
         nn = D % 256 == 0
         W2t = None if nn else torch.empty(E, D, H, dtype=torch.bfloat16, device=dev)
-        W13t = torch.empty(E, D, 2 * H, dtype=torch.bfloat16, device=dev) if dgrad else None
+        W13t = torch.empty(E, D, 2 * H, dtype=torch.bfloat16, device=dev) if dgrad and not nn else None
         BF = _lib.QUANT_BF16
 
         def job(src, dst_t, col_off, cols_out):
@@ -729,7 +729,7 @@ class ExpertWeights:
                                     _lib.ptr(dst_t), cols_out, D * cols_out, col_off, None, 0, 0)
 
         jobs = [] if nn else [job(w2, W2t, 0, H)]
-        if dgrad:
+        if dgrad and not nn:
             jobs += [job(w1, W13t, 0, 2 * H), job(w3, W13t, H, 2 * H)]
         if jobs:
             arr = (_lib.FmWeightJob * len(jobs))(*jobs)
@@ -741,7 +741,8 @@ class ExpertWeights:
         else:
             self.w2t = ExpertWeightOperand(W2t, None, H, D * H, N=D, K=H)
         if dgrad:
-            self.w13t = ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H)
+            self.w13t = (ExpertWeightOperand(w1, None, D, H * D, N=D, K=2 * H, kmajor=True, data2=w3, split=H)
+                         if nn else ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H))
 
     def _build_mx(self, w1, w2, w3, E, H, D, dgrad):
         dev = w1.device

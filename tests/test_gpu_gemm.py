@@ -351,3 +351,26 @@ def test_bf16_kmajor_weights_match(dev, E, T, K, zeros, D, H):
             _gemm_m(_lib.QUANT_BF16, pt.rows, w, plan, out)
             outs.append(out[:used])
         assert torch.equal(outs[0], outs[1]), dt
+
+
+@pytest.mark.parametrize("E,T,K,zeros,D,H", [(8, 3000, 2, (2, 5), 512, 384), (64, 6000, 4, (7, 63), 256, 128)])
+def test_bf16_kmajor_split_weights_match(dev, E, T, K, zeros, D, H):
+    """BF16 dX reading w1 then w3 as one [K = 2H][N = D] operand split along K
+    (rows k >= H from w3) gives the bits of the same GEMM on the stacked
+    transposed copy [E][D][2H]."""
+    from nanopysche_amd.flow_moe import ExpertWeightOperand, _gemm_m
+    g = randn_bf16((T, 2 * H), seed=1)
+    _, idx = zipf_routing(T, E, K, 1.1, seed=E, zero_experts=zeros)
+    w1, w3 = (randn_bf16((E * H, D), seed=s, std=0.02).to(dev) for s in (2, 4))
+    pt = fm.fused_permute_pad(g.to(dev), idx.to(dev), E, granularity=None)
+    plan = pt.plan
+    nn = ExpertWeightOperand(w1, None, D, H * D, N=D, K=2 * H, kmajor=True, data2=w3, split=H)
+    W13t = torch.cat([w1.view(E, H, D), w3.view(E, H, D)], 1).transpose(1, 2).contiguous()
+    nt = ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H)
+    used = int(plan.offsets[-1].item())
+    outs = []
+    for w in (nt, nn):
+        out = torch.zeros(plan.rows_max, D, dtype=torch.bfloat16, device=dev)
+        _gemm_m(_lib.QUANT_BF16, pt.rows, w, plan, out)
+        outs.append(out[:used])
+    assert torch.equal(outs[0], outs[1])
