@@ -107,10 +107,37 @@ def _q_weight(w, recipe):
     return ofp8.dequant_128x128(q, s)
 
 
+def _tf(a):
+    """float32 torch view of a numpy array (strided views stay views)."""
+    a = np.asarray(a, dtype=np.float32)
+    if any(st < 0 for st in a.strides):
+        a = np.ascontiguousarray(a)
+    return torch.from_numpy(a)
+
+
 def _mm(a, b_t):
-    """fp32 a @ b_t.T via torch CPU."""
-    return (torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
-            @ torch.from_numpy(np.ascontiguousarray(b_t, dtype=np.float32)).T).numpy()
+    """fp32 a @ b_t.T via torch CPU (either operand may be a transposed view:
+    the BLAS call takes the transpose, no copy is made)."""
+    return (_tf(a) @ _tf(b_t).T).numpy()
+
+
+def _expert_weights(W1e, W2e, W3e, recipe):
+    """One expert's four GEMM weight operands as the device reads them:
+    (w13 [2H, D], w2t [D, H], w2 [H, D], w13t [D, 2H]), dequantised (or the
+    plain values for the BF16 path).  A 128x128 block of a transpose is the
+    transpose of the block (same elements, same amax, same scale), so for the
+    128x128 recipes the transposed operands are views of the row operands'
+    values; MX blocks run along the contraction dimension of each operand,
+    so there each one is quantised on its own."""
+    W13 = np.concatenate([W1e, W3e], axis=0)
+    if recipe is None:
+        return W13, W2e.T, W2e, W13.T
+    q13 = _q_weight(W13, recipe)
+    q2 = _q_weight(W2e, recipe)
+    if recipe == "mxfp8":
+        return (q13, _q_weight(np.ascontiguousarray(W2e.T), recipe), q2,
+                _q_weight(np.ascontiguousarray(W13.T), recipe))
+    return q13, q2.T, q2, q13.T
 
 
 def _t(a):
@@ -159,13 +186,13 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
     Xv = _q_rows(Xp, recipe) if fp8 else Xp
     GU = np.zeros((Mp, 2 * H), np.float32)
     Y = np.zeros((Mp, D), np.float32)
+    ops = {}
     for e in range(E):
         r0, r1 = offs[e], offs[e + 1]
         if r1 == r0:
             continue
-        W13 = np.concatenate([W1[e], W3[e]], axis=0)
-        Bv = _q_weight(W13, recipe) if fp8 else W13
-        GU[r0:r1] = _bf16(_mm(Xv[r0:r1], Bv))
+        ops[e] = _expert_weights(W1[e], W2[e], W3[e], recipe)
+        GU[r0:r1] = _bf16(_mm(Xv[r0:r1], ops[e][0]))
     if taps is not None and "gate_up" in taps:
         GU = _bf16(np.asarray(taps["gate_up"], dtype=np.float32)[:Mp])
     g, u = np.ascontiguousarray(GU[:, :H]), np.ascontiguousarray(GU[:, H:])
@@ -176,9 +203,7 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         r0, r1 = offs[e], offs[e + 1]
         if r1 == r0:
             continue
-        W2t = np.ascontiguousarray(W2[e].T)
-        Bv = _q_weight(W2t, recipe) if fp8 else W2t
-        Y[r0:r1] = _bf16(_mm(Hv[r0:r1], Bv))
+        Y[r0:r1] = _bf16(_mm(Hv[r0:r1], ops[e][1]))
     out = orouting.unpermute_unpad(Y, rt["row_of"], wts, T, K)
     out = _bf16(out)
     if grad_out is None:
@@ -206,8 +231,7 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         r0, r1 = offs[e], offs[e + 1]
         if r1 == r0:
             continue
-        Bv = _q_weight(W2[e], recipe) if fp8 else W2[e]      # [H, D]
-        dH[r0:r1] = _bf16(_mm(dYv[r0:r1], Bv))
+        dH[r0:r1] = _bf16(_mm(dYv[r0:r1], ops[e][2]))      # w2_e [H, D]
     if taps is not None and "dh" in taps:
         dH = _bf16(np.asarray(taps["dh"], dtype=np.float32)[:Mp])
     tdH, tu, tg, tsg = _t(dH), _t(u), _t(g), _t(sg)
@@ -235,13 +259,173 @@ def moe_flow_reference(x, weights, indices, w1, w2, w3, num_experts, grad_out=No
         dW2[e] = _mm(HvT[:, r0:r1], dYvT[:, r0:r1])
         dW13 = _mm(dGUvT[:, r0:r1], XvT[:, r0:r1])
         dW1[e], dW3[e] = dW13[:H], dW13[H:]
-        W13t = np.ascontiguousarray(np.concatenate([W1[e], W3[e]], axis=0).T)  # [D, 2H]
-        Bv = _q_weight(W13t, recipe) if fp8 else W13t
-        dXp[r0:r1] = _bf16(_mm(dGUv[r0:r1], Bv))
+        dXp[r0:r1] = _bf16(_mm(dGUv[r0:r1], ops[e][3]))    # [w1_e; w3_e]^T [D, 2H]
     dx = _bf16(orouting.unpermute_unpad(dXp, rt["row_of"], None, T, K))
     grads = dict(x=dx, weights=dw, w1=dW1.reshape(E * H, D), w2=dW2.reshape(E * H, D),
                  w3=dW3.reshape(E * H, D))
     return out, grads
+
+
+def moe_flow_sampled(x, weights, indices, w1, w2, w3, num_experts, grad_out, recipe, tokens, blocks):
+    """``moe_flow_reference`` restricted to what a full-size parity test can
+    afford on the host: the output, input gradient and router-weight gradient
+    of the tokens ``tokens``, and the 128 x 128 weight-gradient blocks listed
+    in ``blocks`` as (name in {"w1", "w2", "w3"}, expert e, hidden block bi,
+    model block bj), i.e. ``grad[name][e*H + 128 bi : +128, 128 bj : +128]``.
+
+    Nothing is approximated.  Every quantiser of the dataflow is local:
+    row operands are quantised per row (blocks along the row), column
+    operands per column over 128-row (MX: 32-row) blocks of one expert's
+    padded rows (expert groups start on multiples of 128), weights per
+    expert in 128 x 128 (MX: 1 x 32) blocks.  So a token's rows need only
+    that token's inputs and its experts' weights, and a weight-gradient block
+    needs only the 128 hidden columns bi of its expert's rows (g, u, dH, h
+    there) and the 128 model columns bj (x or dY there), in padded row order.
+    The fp32 sums run in other BLAS orders than the full oracle's, which may
+    move a bf16-rounded GEMM output by one unit (tests/test_oracle_layer.py
+    pins the two against each other).
+
+    Returns (out [n, D], {"x": [n, D], "weights": [n, K], "blocks": [len(blocks), 128, 128]})."""
+    E = num_experts
+    T, D = x.shape
+    K = indices.shape[1]
+    H = w1.shape[0] // E
+    fp8 = recipe is not None
+    tokens = np.asarray(tokens, dtype=np.int64)
+    rt = orouting.sort_assignments(indices.cpu().numpy(), E, drop_out_of_range=True)
+    offs, row_of, a_of_row = rt["offsets"], rt["row_of"], rt["assign_of_row"]
+    xs = x.detach()
+    dO_all = grad_out.detach()
+    wts = _np(weights).astype(np.float32, copy=False).reshape(-1)
+
+    def rows_of(t_ids, a_ids=None):
+        """bf16 x and dO rows of the given tokens as fp32 arrays."""
+        ti = torch.from_numpy(np.asarray(t_ids, dtype=np.int64))
+        return _bf16(xs.index_select(0, ti).float().numpy()), _bf16(dO_all.index_select(0, ti).float().numpy())
+
+    def weight(name, e, r0=None, r1=None):
+        """[rows r0:r1 of] expert e's parameter rows as the GEMM's operand source."""
+        src = {"w1": w1, "w2": w2, "w3": w3}[name]
+        lo = e * H + (0 if r0 is None else r0)
+        hi = e * H + (H if r1 is None else r1)
+        a = src.detach()[lo:hi].float().numpy()
+        return a if fp8 else _bf16(a)
+
+    ops = {}
+
+    def expert_ops(e):
+        if e not in ops:
+            ops[e] = _expert_weights(weight("w1", e), weight("w2", e), weight("w3", e), recipe)
+        return ops[e]
+
+    def gate_up(Xv, e, cols=None):
+        """bf16 gate|up GEMM outputs of the row-quantised x rows ``Xv`` (all 2H
+        columns, or the 128-column hidden block ``cols`` of g and of u)."""
+        if cols is None:
+            W = expert_ops(e)[0]
+        else:
+            lo, hi = cols * 128, cols * 128 + 128
+            W13 = np.concatenate([weight("w1", e, lo, hi), weight("w3", e, lo, hi)], axis=0)
+            # 128-row slices of a 128x128-blocked (or 1x32-blocked) weight are its own blocks
+            W = _q_weight(W13, recipe) if fp8 else W13
+        GU = _bf16(_mm(Xv, W))
+        half = GU.shape[1] // 2
+        return np.ascontiguousarray(GU[:, :half]), np.ascontiguousarray(GU[:, half:])
+
+    def dgrad_h(dYv, e, cols=None):
+        """bf16 dH of the row-quantised dY rows ``dYv`` (all H columns or block ``cols``)."""
+        if cols is None:
+            W = expert_ops(e)[2]
+        else:
+            W2b = weight("w2", e, cols * 128, cols * 128 + 128)
+            W = _q_weight(W2b, recipe) if fp8 else W2b
+        return _bf16(_mm(dYv, W))
+
+    def rowq(a):
+        return _q_rows(a, recipe) if fp8 else _bf16(a)
+
+    def swiglu_grads(g, u, dH):
+        silu_g, sg = _silu_sigmoid(g)
+        h = (_t(silu_g) * _t(u)).numpy()
+        tdH, tu, tg, tsg = _t(dH), _t(u), _t(g), _t(sg)
+        dg = (tdH * tu * tsg * (1.0 + tg * (1.0 - tsg))).numpy()
+        du = (tdH * (tg * tsg)).numpy()
+        return h, dg, du
+
+    # ---- sampled tokens: their rows through the whole forward and input-gradient chain
+    n = tokens.size
+    Yrows = np.zeros((n * K, D), np.float32)
+    dXrows = np.zeros((n * K, D), np.float32)
+    sub_row_of = np.full(n * K, -1, np.int64)
+    xr, dOr = rows_of(tokens)
+    a_ids = (tokens[:, None] * K + np.arange(K)[None, :]).reshape(-1)
+    r_ids = row_of[a_ids]
+    e_of = np.searchsorted(offs, r_ids, side="right") - 1
+    for e in np.unique(e_of[r_ids >= 0]):
+        sel = np.nonzero((r_ids >= 0) & (e_of == e))[0]
+        q13, q2t, q2, q13t = expert_ops(int(e))
+        xe = xr[sel // K]
+        g, u = gate_up(_q_rows(xe, recipe) if fp8 else xe, int(e))
+        silu_g, _ = _silu_sigmoid(g)
+        h = (_t(silu_g) * _t(u)).numpy()
+        Hv = _q_rows(h, recipe) if fp8 else _bf16(h)
+        Yrows[sel] = _bf16(_mm(Hv, q2t))
+        dY = (_t(wts[a_ids[sel]])[:, None] * _t(dOr[sel // K])).numpy()
+        dH = dgrad_h(rowq(dY), int(e))
+        _, dg, du = swiglu_grads(g, u, dH)
+        dGU = np.concatenate([dg, du], axis=1)
+        dGUv = _q_rows(dGU, recipe) if fp8 else _bf16(dGU)
+        dXrows[sel] = _bf16(_mm(dGUv, q13t))
+        sub_row_of[sel] = sel
+    w_tok = wts[a_ids].reshape(n, K)
+    out = _bf16(orouting.unpermute_unpad(Yrows, sub_row_of, w_tok, n, K))
+    dx = _bf16(orouting.unpermute_unpad(dXrows, sub_row_of, None, n, K))
+    ro = torch.from_numpy(sub_row_of.reshape(n, K))
+    dO64, Y64 = _t(dOr).double(), _t(Yrows).double()
+    dw = torch.stack([(dO64 * Y64[ro[:, k].clamp(min=0)]).sum(-1) for k in range(K)], dim=1).float()
+    dw[ro < 0] = 0.0
+
+    # ---- weight-gradient blocks: one expert's padded rows, 128 hidden and 128 model columns;
+    # the expert's rows (x, dY and their row quantisation) are formed once per expert and
+    # the hidden columns once per (expert, hidden block)
+    out_blocks = [None] * len(blocks)
+    by_expert = {}
+    for i, (name, e, bi, bj) in enumerate(blocks):
+        by_expert.setdefault(int(e), []).append(i)
+    for e, items in by_expert.items():
+        r0, r1 = int(offs[e]), int(offs[e + 1])
+        if r1 == r0:
+            for i in items:
+                out_blocks[i] = np.zeros((128, 128), np.float32)
+            continue
+        ar = a_of_row[r0:r1].astype(np.int64)
+        valid = ar >= 0
+        xe, dOe = rows_of(np.where(valid, ar // K, 0))
+        xe[~valid] = 0.0
+        dY = (_t(np.where(valid, wts[np.where(valid, ar, 0)], 0.0).astype(np.float32))[:, None] * _t(dOe)).numpy()
+        dY[~valid] = 0.0
+        del dOe
+        Xv, dYv = (_q_rows(xe, recipe) if fp8 else xe), rowq(dY)
+        hidden = {}
+        for i in items:
+            name, _, bi, bj = blocks[i]
+            if bi not in hidden:
+                g, u = gate_up(Xv, e, cols=bi)
+                hidden[bi] = swiglu_grads(g, u, dgrad_h(dYv, e, cols=bi))
+            h, dg, du = hidden[bi]
+            cj = slice(bj * 128, bj * 128 + 128)
+            if name == "w2":
+                a_op, b_op = h, dY[:, cj]
+            else:
+                a_op, b_op = (dg if name == "w1" else du), xe[:, cj]
+            if fp8:
+                aT, bT = _q_cols(np.ascontiguousarray(a_op), recipe), _q_cols(np.ascontiguousarray(b_op), recipe)
+            elif name == "w2":
+                aT, bT = _bf16(a_op).T, _bf16(b_op).T
+            else:
+                aT, bT = _bf16(a_op).T, b_op.T
+            out_blocks[i] = _mm(aT, bT)
+    return out, dict(x=dx, weights=dw.numpy(), blocks=np.stack(out_blocks) if out_blocks else None)
 
 
 def max_rel_err(y, ref) -> float:

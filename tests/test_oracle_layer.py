@@ -3,6 +3,7 @@ a dense per-token formulation of ExpertMLP (model/moe.py:1181-1183) with its
 own autograd graph, and the FP8-flow oracle's structure against the loop."""
 
 import numpy as np
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -188,3 +189,55 @@ def test_flow_reference_taps_replace_gemm_outputs():
 def test_max_rel_err_metric():
     assert olayer.max_rel_err(np.array([1.0, 2.0]), np.array([1.0, 2.0])) == 0.0
     assert abs(olayer.max_rel_err(np.array([1.0, 2.1]), np.array([1.0, 2.0])) - 0.05) < 1e-12
+
+
+def _sampled_case(T, D, H, E, K, seed, zero=()):
+    x = randn_bf16((T, D), seed=seed)
+    w, idx = zipf_routing(T, E, K, 1.1, seed=seed + 1, zero_experts=zero)
+    w1, w2, w3 = (randn_bf16((E * H, D), seed=seed + s, std=0.05) for s in (2, 3, 4))
+    go = randn_bf16((T, D), seed=seed + 5, std=1e-2)
+    return x, w, idx, w1, w2, w3, go
+
+
+@pytest.mark.parametrize("recipe", [None, "blockwise", "flow_moe", "mxfp8"])
+def test_sampled_oracle_matches_full_oracle(recipe):
+    """The sampled restriction of the flow oracle (tokens' outputs and input /
+    router-weight gradients, 128 x 128 weight-gradient blocks) against the
+    full oracle's rows and blocks.  Only the BLAS summation order differs, so
+    nearly every value is identical and none moves by more than a bf16 unit
+    passed through one quantiser.  A wrong row map, block offset, expert
+    range or operand axis would be O(1) on many values."""
+    T, D, H, E, K = 400, 256, 384, 5, 2
+    x, w, idx, w1, w2, w3, go = _sampled_case(T, D, H, E, K, seed=21, zero=(4,))
+    out, grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe=recipe)
+    tokens = np.array([0, 3, 17, 111, 250, 399])
+    blocks = [("w1", 0, 0, 0), ("w3", 1, 2, 1), ("w2", 2, 1, 1), ("w2", 3, 2, 0), ("w1", 4, 0, 1)]
+    s_out, s_g = olayer.moe_flow_sampled(x, w, idx, w1, w2, w3, E, go, recipe, tokens, blocks)
+    # bf16-rounded outputs: nearly all identical
+    pairs = [(s_out, out[tokens]), (s_g["x"], grads["x"][tokens]), (s_g["weights"], grads["weights"][tokens])]
+    for got, ref in pairs:
+        got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+        assert got.shape == ref.shape
+        assert olayer.max_rel_err(got, ref) < 2e-3
+        assert np.mean(got == ref) > 0.9
+    # fp32 weight-gradient sums: the same values up to the summation order
+    for (name, e, bi, bj), blk in zip(blocks, s_g["blocks"]):
+        full = grads[name].reshape(E, H, D)[e, bi * 128:(bi + 1) * 128, bj * 128:(bj + 1) * 128]
+        assert olayer.max_rel_err(blk, full) < 2e-3, (name, e)
+    # the expert without tokens has an all-zero block
+    assert np.all(s_g["blocks"][-1] == 0)
+
+
+def test_sampled_oracle_block_index_is_checked():
+    """The block comparison tells neighbouring blocks apart: the block one
+    hidden block off (an off-by-one in the slices) fails the bound that the
+    right block meets."""
+    T, D, H, E, K = 256, 256, 256, 4, 2
+    x, w, idx, w1, w2, w3, go = _sampled_case(T, D, H, E, K, seed=31)
+    _, grads = olayer.moe_flow_reference(x, w, idx, w1, w2, w3, E, go, recipe="flow_moe")
+    blocks = [("w1", 1, 1, 0)]
+    _, s_g = olayer.moe_flow_sampled(x, w, idx, w1, w2, w3, E, go, "flow_moe", [0], [("w1", 1, 0, 0)])
+    full = grads["w1"].reshape(E, H, D)[1, 128:256, 0:128]
+    assert olayer.max_rel_err(s_g["blocks"][0], full) > 0.5
+    _, s_g = olayer.moe_flow_sampled(x, w, idx, w1, w2, w3, E, go, "flow_moe", [0], blocks)
+    assert olayer.max_rel_err(s_g["blocks"][0], full) < 2e-3
