@@ -599,9 +599,18 @@ class ExpertWeights:
         the batched quantisation launch is not made but appended as (FmWeightJob
         array, count, sources): the caller runs it (``route_tokens(weight_jobs=
         (array, count))`` or ``fm_quantize_weight_batch``) before the operands are
-        read, holding ``sources`` (the tensors the jobs read) until then."""
+        read, holding ``sources`` (the tensors the jobs read) until then, and
+        calls ``invalidate()`` if it cannot.
+
+        Inside a stream capture the operands are always rebuilt: the graph's
+        replays then re-quantise the parameters' storage as it is at each
+        replay (an optimizer step between replays changes it in place), and
+        the buffers, which every replay rewrites, are not kept as the cache of
+        later eager calls."""
         key = tuple((w.data_ptr(), w._version, w.dtype) for w in (w1, w2, w3))
-        if key != self.key or (need_dgrad and not self.has_dgrad):
+        capturing = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+        if capturing or key != self.key or (need_dgrad and not self.has_dgrad):
+            self.key = None
             self.w13 = self.w2t = self.w2 = self.w13t = None
             self.has_dgrad = need_dgrad
             self._defer = defer
@@ -609,14 +618,20 @@ class ExpertWeights:
                 self._build(w1.detach(), w2.detach(), w3.detach(), E, need_dgrad)
             finally:
                 self._defer = None
-            self.key = key
+            self.key = None if capturing else key
         return self
 
-    def _launch(self, jobs, n: int, stream, sources) -> None:
+    def invalidate(self) -> None:
+        """Forget the cache key, so the next refresh rebuilds (a deferred
+        quantisation that was never launched leaves the operands unwritten)."""
+        self.key = None
+
+    def _launch(self, jobs, n: int, like: torch.Tensor, sources) -> None:
+        """Run (or defer) a weight-quantisation batch on ``like``'s current stream."""
         if self._defer is not None:
             self._defer.append((jobs, n, sources))
         else:
-            _lib.call("fm_quantize_weight_batch", jobs, n, stream)
+            _lib.call("fm_quantize_weight_batch", jobs, n, _lib.stream_of(like))
 
     def _build(self, w1, w2, w3, E, dgrad=True):
         EH, D = w1.shape
@@ -645,7 +660,6 @@ class ExpertWeights:
             W2 = torch.empty(E, H, D, dtype=pay, device=dev)
             S13t = torch.empty(E, D // 128, 2 * H // 128, dtype=f32, device=dev) if fp8 else None
             S2 = torch.empty(E, H // 128, D // 128, dtype=f32, device=dev) if fp8 else None
-        stream = _lib.stream_of(w1)
 
         srcs = [w.contiguous() for w in (w1, w3, w2)]
         if len({w.dtype for w in srcs}) != 1:
@@ -663,7 +677,7 @@ class ExpertWeights:
         jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, W13t, S13t, 0, 0, 2 * H),
                                       job(srcs[1], W13, S13, W13t, S13t, H, H, 2 * H),
                                       job(srcs[2], W2, S2, W2t, S2t, 0, 0, H))
-        self._launch(jobs, 3, stream, srcs)
+        self._launch(jobs, 3, w1, srcs)
         sh = 7
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, (2 * H // 128) * (D // 128), sh, 2 * H, D)
         self.w2t = ExpertWeightOperand(W2t, S2t, H, D * H, H // 128, 1, (D // 128) * (H // 128), sh, D, H)
@@ -693,7 +707,7 @@ class ExpertWeights:
 
         jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, 0, 2 * H), job(srcs[1], W13, S13, H, 2 * H),
                                       job(srcs[2], W2, S2, 0, H))
-        self._launch(jobs, 3, _lib.stream_of(w1), srcs)
+        self._launch(jobs, 3, w1, srcs)
         sh = 7
         g13, g2 = (2 * H // 128) * (D // 128), (H // 128) * (D // 128)
         self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, g13, sh, 2 * H, D)
@@ -733,7 +747,7 @@ class ExpertWeights:
             jobs += [job(w1, W13t, 0, 2 * H), job(w3, W13t, H, 2 * H)]
         if jobs:
             arr = (_lib.FmWeightJob * len(jobs))(*jobs)
-            self._launch(arr, len(jobs), _lib.stream_of(w1), (w1, w2, w3))
+            self._launch(arr, len(jobs), w1, (w1, w2, w3))
         self.w13 = ExpertWeightOperand(w1, None, D, H * D, N=2 * H, K=D, data2=w3, split=H)
         self.w2 = ExpertWeightOperand(w2, None, D, H * D, N=H, K=D)
         if nn:
@@ -911,18 +925,27 @@ class FP8FlowMoECompute:
         # routing sort (its blocks fill the CUs the sort leaves idle)
         kinds = [k for k in (fp8_kind, _lib.QUANT_BF16 if use_bf16 else None) if k is not None]
         batches = []
-        ews = {k: self._weights(k, self._record, batches) for k in kinds}
-        side = batches.pop(0) if batches else None
-        if self._dense:
-            plan = self._dense_plans.get((T, dev))
-            if plan is None:
-                plan = self._dense_plans[(T, dev)] = route_tokens(indices, E, thr, side and side[:2])
+        ews = {}
+        try:
+            for k in kinds:
+                ews[k] = self._weights(k, self._record, batches)
+            side = batches.pop(0) if batches else None
+            if self._dense:
+                plan = self._dense_plans.get((T, dev))
+                if plan is None:
+                    plan = self._dense_plans[(T, dev)] = route_tokens(indices, E, thr, side and side[:2])
+                    side = None
+            else:
+                plan = route_tokens(indices, E, thr, side and side[:2])
                 side = None
-        else:
-            plan = route_tokens(indices, E, thr, side and side[:2])
-            side = None
-        for jobs, n, _sources in ([side] if side is not None else []) + batches:
-            _lib.call("fm_quantize_weight_batch", jobs, n, _lib.stream_of(x))
+            for jobs, n, _sources in ([side] if side is not None else []) + batches:
+                _lib.call("fm_quantize_weight_batch", jobs, n, _lib.stream_of(x))
+        except BaseException:
+            # a deferred weight quantisation may not have been launched: the
+            # next call must rebuild rather than read unwritten operands
+            for ew in ews.values():
+                ew.invalidate()
+            raise
         del side, batches   # the launches are enqueued: their sources may go
         wts = weights.to(torch.float32).contiguous()
         R = plan.rows_max
@@ -960,6 +983,9 @@ class FP8FlowMoECompute:
         ctx.plan = plan
         ctx.kinds = (fp8_kind, use_bf16)
         ctx.saved_cols = {k: v[0] for k, v in saved.items()}
+        # the dgrad weight operands of this forward's weights (a later forward
+        # may rebuild the cache before this backward runs)
+        ctx.dgrad_ops = {k: (ew.w2, ew.w13t) for k, ew in ews.items()} if self._record else None
         ctx.saved_hcols = h_cols
         ctx.wdtypes = (w1.dtype, w2.dtype, w3.dtype)
         # Y only feeds the router-weight gradient (the dense path's outputs are
@@ -1037,15 +1063,16 @@ class FP8FlowMoECompute:
                 for kind, want in two_streams:
                     _gemm_k(kind, ctx.saved_hcols[kind], dy[kind].rows_t, plan, H, D, dW2, H * D, mask=mask,
                             want=want, may_split=side is main, a_cold=True)
+        if ctx.dgrad_ops is None:
+            raise RuntimeError("the expert block's forward did not record a backward")
         for kind, want in one_grid:
-            _gemm_mk(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, ctx.saved_hcols[kind],
+            _gemm_mk(kind, dy[kind].rows, ctx.dgrad_ops[kind][0], plan, dH, ctx.saved_hcols[kind],
                      dy[kind].rows_t, H, D, dW2, H * D, mask, want, a_cold=True)
         for kind, want in two_streams:
-            _gemm_m(kind, dy[kind].rows, self._weights(kind).w2, plan, dH, mask, want)
+            _gemm_m(kind, dy[kind].rows, ctx.dgrad_ops[kind][0], plan, dH, mask, want)
         if self.capture_intermediates is not None:
             self.capture_intermediates["dh"] = dH.detach().clone()
         for kind, want in runs:
-            ew = self._weights(kind)
             gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev, kmajor=True)
             _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
                       _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst),
@@ -1055,7 +1082,7 @@ class FP8FlowMoECompute:
             _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,
                     mask=mask, want=want)
             # input gradient
-            _gemm_m(kind, dgu_row, ew.w13t, plan, dXp, mask, want)
+            _gemm_m(kind, dgu_row, ctx.dgrad_ops[kind][1], plan, dXp, mask, want)
         # the router's backward and dW2 (and the buffers they read, referenced
         # until here) are done before the router's dx share is summed
         main.wait_stream(side)
@@ -1067,6 +1094,7 @@ class FP8FlowMoECompute:
             dx = fused_unpermute_unpad(dXp, plan, None, addend=dx_addend, router_terms=terms)
         ctx.saved_cols = None
         ctx.saved_hcols = None
+        ctx.dgrad_ops = None
         return (dx.to(ctx.x_dtype), None if dw is None else dw.reshape(T, K), dW1, dW2, dW3, None, None)
 
 
