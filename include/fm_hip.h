@@ -210,11 +210,14 @@ int fm_router_logits(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_
  * included), the gating as fm_topk_gating (gating, flags, replay), counts[E]
  * of the T*K slots (added to tokens_per_expert / total_tokens when given, as
  * fm_expert_counts with tokens = T) and loss = E * sum_e f_e P_e (+ z-loss
- * with z_loss_multiplier != 0) as fm_aux_loss.  For E <= 8 and D = 512 n <=
- * 2048 the gate, gating, loss partials and counts run as one pass over x plus
- * one small kernel; other shapes launch the steps separately.  T > 0; the
- * workspace holds fm_router_forward_workspace_bytes(T, E) bytes. */
+ * with z_loss_multiplier != 0) as fm_aux_loss.  For E <= 8 and D a multiple
+ * of 512 with the gate [8, D] in 64 KiB (D <= 2048 for an fp32 gate, <= 4096
+ * for a bf16 one) the gate, gating, loss partials and counts run as one pass
+ * over x plus one small kernel (fm_router_forward_fused says which); other
+ * shapes launch the steps separately.  T > 0; the workspace holds
+ * fm_router_forward_workspace_bytes(T, E) bytes. */
 int64_t fm_router_forward_workspace_bytes(int64_t T, int E);
+int fm_router_forward_fused(int E, int64_t D, int w_dtype);
 int fm_router_forward(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
                       int64_t ld_w, const void* bias, const float* score_bias, int E, int K, int gating, int flags,
                       const void* replay_indices, int replay_i64, float* logits, int64_t ld_l, float* weights,
@@ -371,7 +374,9 @@ int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t*
  * -> 1, addend bf16 [T, D] pitch ld_add or NULL -> 0), fp32 sum in slot order,
  * one rounding to out_dtype.  The addend lets a MoE layer's input gradient
  * take the router's share in the same pass (the sum autograd forms for an
- * input feeding both the router and the experts, model/moe.py:1347-1375). */
+ * input feeding both the router and the experts, model/moe.py:1347-1375).
+ * y, out and addend start on 16-byte boundaries; D and the pitches are
+ * multiples of 8. */
 int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
                  int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
                  const void* addend, int64_t ld_add, void* stream);
@@ -382,7 +387,8 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
  * the experts), in the same pass: out[t] = addend[t] + sum_k weights[t*K+k]
  * y[row_of[t*K+k]] + sum_e dlogits[t*ld_dl+e] gate_w[e*ld_w + :], fp32 sums in
  * that order (the router's terms as fused multiply-adds), one rounding.
- * E <= 8; gate_w bf16 or fp32 [E, D]. */
+ * E <= 8; gate_w bf16 or fp32 [E, D]; y, out, addend and gate_w start on
+ * 16-byte boundaries (dlogits may not). */
 int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, const float* weights,
                         int64_t T, int K, int64_t D, void* out, int out_dtype, int64_t ld_out,
                         const void* addend, int64_t ld_add, const float* dlogits, int64_t ld_dl,

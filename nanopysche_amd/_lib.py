@@ -92,6 +92,7 @@ SIGNATURES = {
     "fm_aux_loss": (_i32, [_vp, _i64, _vp, _i32, _i64, _vp, C.c_float, _vp, _vp]),
     "fm_router_logits": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _i32, _vp, _i64, _vp]),
     "fm_router_forward_workspace_bytes": (_i64, [_i64, _i32]),
+    "fm_router_forward_fused": (_i32, [_i32, _i64, _i32]),
     "fm_router_forward": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _i32, _i32, _i32, _i32,
                                  _vp, _i32, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _vp, C.c_float, _vp, _vp, _i64,
                                  _vp]),

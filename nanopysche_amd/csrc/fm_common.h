@@ -206,6 +206,9 @@ inline int device_cus() {
   return n;
 }
 
+// A null pointer or one on a 16-byte boundary (the vector accesses' alignment).
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // Workgroups of `kernel` (`block` threads, no dynamic LDS) that fit on the
 // device at once: its occupancy per CU (registers, LDS) x the CUs.  A launch
 // of that many workgroups runs in one round, with no partly filled last one.

@@ -669,8 +669,8 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* _
                                                                void* __restrict__ out, int out_f32, int64_t ld_out,
                                                                const uint16_t* __restrict__ addend, int64_t ld_add,
                                                                const float* __restrict__ dl, int64_t ld_dl,
-                                                               const WT* __restrict__ W, int64_t ld_w, int E,
-                                                               int64_t tpb) {
+                                                               int dl_vec, const WT* __restrict__ W, int64_t ld_w,
+                                                               int E, int64_t tpb) {
   const int64_t c = int64_t(blockIdx.x) * 2048 + threadIdx.x * 8;
   if (c >= D) return;
   // the gate's columns of this thread for the 8 experts, kept as stored
@@ -726,7 +726,7 @@ __global__ __launch_bounds__(256) void unpermute_router_kernel(const uint16_t* _
           sw[u][k] = w ? w[t * KC + k] : 1.f;
         }
       }
-      if (E == 8 && ld_dl % 4 == 0) {   // the token's 8 dlogits as two 16-byte loads
+      if (dl_vec) {   // E == 8, 16-byte aligned rows: the token's 8 dlogits as two 16-byte loads
         const float4 p0 = *reinterpret_cast<const float4*>(dl + t * ld_dl);
         const float4 p1 = *reinterpret_cast<const float4*>(dl + t * ld_dl + 4);
         d[u][0] = p0.x; d[u][1] = p0.y; d[u][2] = p0.z; d[u][3] = p0.w;
@@ -1098,6 +1098,8 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
   FM_REQUIRE(D % 8 == 0 && ld_y % 8 == 0 && ld_out % 8 == 0 && (addend == nullptr || ld_add % 8 == 0),
              "fm_unpermute: D and pitches must be multiples of 8");
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_unpermute: bad out dtype");
+  FM_REQUIRE(aligned16(y) && aligned16(out) && aligned16(addend),
+             "fm_unpermute: y, out and addend must be 16-byte aligned (8-element vector accesses)");
   if (T == 0) return 0;
   const int64_t n = T * (D / 8);
   const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
@@ -1126,7 +1128,10 @@ int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, cons
              "fm_unpermute_router: D and pitches must be multiples of 8");
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_unpermute_router: bad out dtype");
   FM_REQUIRE(gate_dtype == FM_DTYPE_BF16 || gate_dtype == FM_DTYPE_F32, "fm_unpermute_router: bad gate dtype");
+  FM_REQUIRE(aligned16(y) && aligned16(out) && aligned16(addend) && aligned16(gate_w),
+             "fm_unpermute_router: y, out, addend and gate_w must be 16-byte aligned (8-element vector accesses)");
   if (T == 0) return 0;
+  const int dl_vec = E == 8 && ld_dl % 4 == 0 && aligned16(dlogits) ? 1 : 0;
   const int64_t nx = (D + 2047) / 2048;
   hipStream_t sm = static_cast<hipStream_t>(stream);
   auto go = [&](auto wt, auto kc) {
@@ -1140,7 +1145,7 @@ int fm_unpermute_router(const void* y, int64_t ld_y, const int32_t* row_of, cons
     hipLaunchKernelGGL((unpermute_router_kernel<WT, decltype(kc)::value>), grid, dim3(256), 0, sm,
                        static_cast<const uint16_t*>(y), ld_y, row_of, weights, T, K, D, out,
                        out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend), ld_add, dlogits,
-                       ld_dl, static_cast<const WT*>(gate_w), ld_w, E, tpb);
+                       ld_dl, dl_vec, static_cast<const WT*>(gate_w), ld_w, E, tpb);
   };
   auto go_k = [&](auto wt) {
     if (K == 1) go(wt, std::integral_constant<int, 1>{});

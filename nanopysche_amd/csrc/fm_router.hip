@@ -986,6 +986,10 @@ int64_t fm_router_forward_workspace_bytes(int64_t T, int E) {
   return fused > plain ? fused : plain;
 }
 
+int fm_router_forward_fused(int E, int64_t D, int w_dtype) {
+  return E >= 1 && D > 0 && router_small_ok(E, D, w_dtype == FM_DTYPE_BF16) ? 1 : 0;
+}
+
 int fm_router_forward(const void* x, int x_dtype, int64_t ld_x, int64_t T, int64_t D, const void* w, int w_dtype,
                       int64_t ld_w, const void* bias, const float* score_bias, int E, int K, int gating, int flags,
                       const void* replay_indices, int replay_i64, float* logits, int64_t ld_l, float* weights,

@@ -17,18 +17,23 @@ pytestmark = pytest.mark.gpu
 KINDS = {"bf16": _lib.QUANT_BF16, "block": _lib.QUANT_BLOCK, "pow2": _lib.QUANT_POW2, "mx": _lib.QUANT_MX}
 
 
-def _deq_rows(t, kind):
+def _deq_rows(t, kind, rows):
+    """The first ``rows`` rows of a row-quantised operand (the padded expert
+    groups, offsets[E]; the buffer's rows past them are never written)."""
     if kind == "bf16":
-        return t.float().cpu().numpy()
-    q, s = t.data.cpu().numpy(), t.scale.cpu().numpy()
+        return t[:rows].float().cpu().numpy()
+    q, s = t.data[:rows].cpu().numpy(), t.scale[:rows].cpu().numpy()
     return ofp8.dequant_mx_1x32(q, s) if kind == "mx" else ofp8.dequant_1x128(q, s)
 
 
-def _deq_cols(t, kind):
-    """Transposed operand [C, R] with k-major scales [R/blk, C]."""
+def _deq_cols(t, kind, rows):
+    """Transposed operand [C, R] with k-major scales [R/blk, C], its first
+    ``rows`` columns (source rows)."""
     if kind == "bf16":
-        return t.float().cpu().numpy()
-    q, s = t.data.cpu().numpy(), np.ascontiguousarray(t.scale.cpu().numpy().T)
+        return t[:, :rows].float().cpu().numpy()
+    blk = 32 if kind == "mx" else 128
+    q = t.data[:, :rows].cpu().numpy()
+    s = np.ascontiguousarray(t.scale[:rows // blk].cpu().numpy().T)
     return ofp8.dequant_mx_1x32(q, s) if kind == "mx" else ofp8.dequant_1x128(q, s)
 
 
@@ -65,7 +70,7 @@ def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros, D, H):
     plan = pt.plan
     gu = fm.fp8_grouped_gemm(pt.rows, ew.w13, plan, out_dtype=torch.float32)
     offs = plan.offsets.cpu().numpy()
-    a = _deq_rows(pt.rows, kind)
+    a = _deq_rows(pt.rows, kind, offs[-1])
     W1v = _weight_values(w1, kind).reshape(E, H, D) if kind != "mx" else None
     if kind == "mx":
         W13 = torch.cat([w1.view(E, H, D), w3.view(E, H, D)], 1).reshape(E * 2 * H, D)
@@ -80,9 +85,11 @@ def test_ragged_m_gate_up_and_down(dev, kind, E, T, K, zeros, D, H):
         ref = a[r0:r1] @ W13v[e].T
         assert max_rel_err(got[r0:r1], ref) < 1e-3, (kind, e)
     # down projection: K = H, weights = w2_e^T
+    # the rows past the padded groups hold no GEMM output: zeros keep them finite
+    gu[int(offs[-1]):] = 0
     hq = fm.quantize_to_fp8(gu[:, :H].bfloat16(), gran, pow2_scale=kind == "pow2") if gran else gu[:, :H].bfloat16()
     y = fm.fp8_grouped_gemm(hq, ew.w2t, plan, out_dtype=torch.float32)
-    hv = _deq_rows(hq, kind)
+    hv = _deq_rows(hq, kind, offs[-1])
     W2 = w2.float().numpy().reshape(E, H, D)
     got = y.cpu().numpy()
     for e in range(E):
@@ -135,9 +142,9 @@ def test_ragged_k_weight_grad(dev, kind, balanced, splits, monkeypatch):
         aw1, aw3 = torch.full_like(dW1, float("nan")), torch.full_like(dW3, float("nan"))
         _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, aw1, H * D, aw3, H * D, split=H, a_cold=True)
         assert torch.equal(aw1, dW1) and torch.equal(aw3, dW3)
-        av = _deq_cols(pg.rows_t, kind)  # [2H, R]
-        bv = _deq_cols(px.rows_t, kind)  # [D, R]
         offs = plan.offsets.cpu().numpy()
+        av = _deq_cols(pg.rows_t, kind, offs[-1])  # [2H, R]
+        bv = _deq_cols(px.rows_t, kind, offs[-1])  # [D, R]
         d1 = dW1.float().cpu().numpy().reshape(E, H, D)
         d3 = dW3.float().cpu().numpy().reshape(E, H, D)
         tol = 1e-3 if out_dtype == torch.float32 else 8e-3
@@ -279,8 +286,8 @@ def test_ragged_k_short_and_long_experts(dev, kind):
     dW1 = torch.full((E * H, D), float("nan"), dtype=torch.float32, device=dev)
     dW3 = torch.full_like(dW1, float("nan"))
     _gemm_k(k, pg.rows_t, px.rows_t, plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H, may_split=False)
-    av, bv = _deq_cols(pg.rows_t, kind), _deq_cols(px.rows_t, kind)
     offs = plan.offsets.cpu().numpy()
+    av, bv = _deq_cols(pg.rows_t, kind, offs[-1]), _deq_cols(px.rows_t, kind, offs[-1])
     assert [int(offs[e + 1] - offs[e]) for e in range(E)] == [0, 128, 128, 256, 256, 384, 1024]
     d1 = dW1.cpu().numpy().reshape(E, H, D)
     d3 = dW3.cpu().numpy().reshape(E, H, D)
