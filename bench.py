@@ -689,6 +689,9 @@ def workload_c1(args, dev):
                                     backward=False, router=(wg, bg, K, "softmax", False), graph=not args.eager)
     counts = torch.bincount(i0.reshape(-1), minlength=E).tolist()
     flops = 6.0 * T * K * D * H
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_c1(x.cpu(), wg.cpu(), bg.cpu(), w1.cpu(), w2.cpu(), w3.cpu(), E, K)
     return {
         "metric": "MoE layer fwd tokens/s on 1 MI355X (configs[0], BF16)",
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -700,8 +703,59 @@ def workload_c1(args, dev):
         "eager_ms_per_step": round(eager_ms, 4),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["bf16"], 4),
+        "roofline": gemm_roofline(summ, "bf16"),
         "gemm": gemm_report(summ, args.steps),
+        "cpu_baseline": cpu,
     }
+
+
+def gemm_roofline(summ, arith, flops_scale=1.0):
+    """`roofline` of the dominant grouped-GEMM kernel of an event summary: its
+    algorithmic FLOPs per launch / its HIP-event time against the dense peak."""
+    dom = max(summ, key=lambda k: summ[k]["ms"])
+    d = summ[dom]
+    achieved = d["flops"] * flops_scale / (d["ms"] * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[arith]
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": None, "kernel": dom}
+
+
+def _median_time(fn, runs, warmup=1):
+    import numpy as np
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def cpu_baseline_c1(x, wg, bg, w1, w2, w3, E, K, runs=2):
+    """configs[0]'s layer forward on the host cores, all tokens: the router
+    (fp32 gate, top-1 softmax; reference model/moe.py:151-255) and the
+    reference's BF16 per-expert loop (model/moe.py:1542-1596) restated in
+    torch CPU fp32 (oracle.layer.moe_bf16_loop)."""
+    import torch
+
+    from oracle import layer as olayer
+    from oracle import routing as orouting
+
+    torch.set_num_threads(os.cpu_count() or 1)
+
+    def once():
+        logits = orouting.router_logits(x.float().numpy(), wg.float().numpy(), bg.float().numpy())
+        w, idx = orouting.softmax_topk(logits, K)
+        olayer.moe_bf16_loop(x, torch.from_numpy(w), torch.from_numpy(idx), w1, w2, w3, E)
+
+    med = _median_time(once, runs)
+    T = x.shape[0]
+    return {"value": round(T / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all {T} tokens of configs[0]: router + BF16 per-expert loop forward in torch CPU fp32 "
+                      f"({torch.get_num_threads()} threads), 1 warmup + median of {runs} runs, {med:.2f} s per "
+                      f"forward; cpu: {cpu_model_name()}"}
 
 
 # ============================================================== configs[3] ====
@@ -763,14 +817,21 @@ def workload_c4(args, dev):
 
 
 # ============================================================== configs[4] ====
-def workload_c5(args, dev):
-    """One GPU's 32-expert share of a 256-expert layer, MXFP8, fwd+bwd."""
+C5_SHAPE = dict(D=7168, E_local=32, E_global=256, K=8, H=2048, A_target=65536)
+
+
+def c5_routing(dev, gen):
+    """configs[4]'s routing on the device: sigmoid top-8 over 256 experts with a
+    Zipf(1.2) per-expert bias added before the sigmoid (model/moe.py:153-162,
+    :257-265), two local experts (5 and 17) that never receive tokens; this
+    rank (experts 0-31) keeps the tokens with at least one local slot, in
+    order, until 65,536 local assignments; other slots carry the out-of-range
+    index 256.  Returns (weights [T, 8] fp32, indices [T, 8] int64, A)."""
     import torch
 
     import nanopysche_amd as fm
 
-    D, E_local, E_global, K, H, A_target = 7168, 32, 256, 8, 2048, 65536
-    gen = torch.Generator(device=dev).manual_seed(4)
+    E_local, E_global, K, A_target = (C5_SHAPE[k] for k in ("E_local", "E_global", "K", "A_target"))
     # per-expert bias from Zipf(1.2) popularity (added before the sigmoid, model/moe.py:153-162);
     # two local experts never receive tokens
     g = torch.Generator().manual_seed(4)
@@ -795,7 +856,17 @@ def workload_c5(args, dev):
     # assignments outside this rank's experts carry an out-of-range index, which routing ignores
     idx = torch.where(keep, idx, torch.full_like(idx, E_global))[:n_tok].contiguous()
     wts = wts[:n_tok].contiguous()
-    A = int(keep[:n_tok].sum())
+    return wts, idx, int(keep[:n_tok].sum())
+
+
+def workload_c5(args, dev):
+    """One GPU's 32-expert share of a 256-expert layer, MXFP8, fwd+bwd."""
+    import torch
+
+    D, E_local, K, H = (C5_SHAPE[k] for k in ("D", "E_local", "K", "H"))
+    gen = torch.Generator(device=dev).manual_seed(4)
+    wts, idx, A = c5_routing(dev, gen)
+    n_tok = idx.shape[0]
     counts = torch.bincount(idx[idx < E_local], minlength=E_local)
     x = device_normal((n_tok, D), 1.0, gen, dev, torch.bfloat16)
     go = device_normal((n_tok, D), 1e-2, gen, dev, torch.bfloat16)

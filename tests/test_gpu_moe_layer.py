@@ -32,12 +32,17 @@ def _params(T, D, H, E, seed):
     return x, gw, gb, w1, w2, w3, R
 
 
-def _reference(x, gw, gb, w1, w2, w3, R, E, K, c_aux):
+def _reference(x, gw, gb, w1, w2, w3, R, E, K, c_aux, replay=None):
     leaves = [t.double().requires_grad_(True) for t in (x, gw, gb, w1, w2, w3)]
     xd, gwd, gbd, a, b, c = leaves
     logits = F.linear(xd, gwd, gbd)                       # gate(x.float()), :151
-    vals, idx = logits.topk(K, dim=-1)                    # _softmax_gating, :249-255
-    wts = F.softmax(vals, dim=-1)
+    if replay is None:
+        vals, idx = logits.topk(K, dim=-1)                # _softmax_gating, :249-255
+        wts = F.softmax(vals, dim=-1)
+    else:                                                 # _routing_replay_gating, :195-247
+        mask = torch.zeros_like(logits).scatter_(1, replay, 1.0)
+        masked = F.softmax(logits, dim=-1) * mask
+        wts, idx = (masked / masked.sum(dim=-1, keepdim=True).clamp(min=1e-8)).topk(K, dim=-1)
     T = xd.shape[0]
     f = F.one_hot(idx, E).sum(dim=1).double().sum(dim=0) / T
     aux = E * (f * F.softmax(logits, dim=-1).mean(dim=0)).sum()   # :267-281
@@ -73,9 +78,60 @@ def test_bf16_layer_matches_reference_ops(dev):
     ((out.float() * R.to(dev)).sum() + c_aux * aux).backward()
     torch.cuda.synchronize()
     assert max_rel_err(out.detach().float().cpu().numpy(), ref_out.numpy()) < 1e-2
-    assert abs(float(aux) - float(ref_aux)) < 1e-5 * float(ref_aux)
+    assert abs(float(aux.detach()) - float(ref_aux)) < 1e-5 * float(ref_aux)
     for name, got, ref in zip(("x", "gate_w", "gate_b", "w1", "w2", "w3"), leaves, ref_grads):
         assert max_rel_err(got.grad.float().cpu().numpy(), ref.numpy()) < 1e-2, name
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("replay", [False, True])
+def test_bf16_layer_at_c3_shape_takes_the_fused_router(dev, monkeypatch, replay):
+    """configs[2]'s layer shape (T=8192, D=2048, E=8, top-2 softmax with the
+    load-balancing loss, H=1408) with BF16 experts, so the fused router
+    forward (one pass over x), the gating backward that forms the
+    router-weight dots itself and the router's dx share folded into the
+    unpermute all run -- checked against float64 autograd of the reference
+    op sequence (model/moe.py:133-184, :195-247 replay, :249-281,
+    :1542-1596) within the BF16 bar, with and without R3 replay.  The test
+    records which library entry points ran."""
+    from nanopysche_amd import _lib
+
+    T, D, H, E, K = 8192, 2048, 1408, 8, 2
+    x, gw, gb, w1, w2, w3, R = _params(T, D, H, E, seed=23)
+    c_aux = 0.5
+    t = torch.arange(T)
+    rep = torch.stack([(t * 5) % E, (t * 5 + 3) % E], 1) if replay else None
+    ref_out, ref_aux, ref_grads = _reference(x, gw, gb, w1, w2, w3, R, E, K, c_aux, replay=rep)
+    assert _lib.load().fm_router_forward_fused(E, D, _lib.DTYPE_BF16) == 1
+    called = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        called.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    leaves = [t_.to(dev).requires_grad_(True) for t_ in (x, gw, gb, w1, w2, w3)]
+    layer = _layer("none", D, H, E, K)
+    layer.set_weights(*leaves[1:])
+    out, aux = layer(leaves[0], replay_indices=None if rep is None else rep.to(dev))
+    fwd = list(called)
+    called.clear()
+    ((out.float() * R.to(dev)).sum() + c_aux * aux).backward()
+    torch.cuda.synchronize()
+    bwd = list(called)
+    assert "fm_router_forward" in fwd and fwd.count("fm_unpermute") == 1, fwd     # fused router; combine
+    for name in ("fm_router_logits", "fm_topk_gating", "fm_expert_counts", "fm_aux_loss"):
+        assert name not in fwd, (name, fwd)
+    for name in ("fm_gating_grad_dot", "fm_unpermute_router", "fm_router_backward"):
+        assert bwd.count(name) == 1, (name, bwd)
+    for name in ("fm_gating_grad", "fm_router_weight_grad", "fm_unpermute"):
+        assert name not in bwd, (name, bwd)
+    assert max_rel_err(out.detach().float().cpu().numpy(), ref_out.numpy()) < 1e-2
+    assert abs(float(aux.detach()) - float(ref_aux)) < 1e-5 * float(ref_aux)
+    for name, got, ref in zip(("x", "gate_w", "gate_b", "w1", "w2", "w3"), leaves, ref_grads):
+        err = max_rel_err(got.grad.float().cpu().numpy(), ref.numpy())
+        assert err < 1e-2, (name, err)
 
 
 @pytest.mark.parametrize("recipe", ["flow_moe", "mxfp8"])
