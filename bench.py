@@ -626,7 +626,8 @@ def workload_c2(args, dev):
     chain = [results[i] for i in (0, 5, 6, 7)]
     chain_us = sum(r["us"] for r in chain)
     chain_gbs = sum(r["bytes"] for r in chain) / (chain_us * 1e-6) / 1e9
-    dom = max(chain, key=lambda r: r["us"])
+    # the roofline reports the op furthest from the HBM peak (of all ops timed)
+    dom = min(results, key=lambda r: r["frac_of_hbm_peak"])
     cpu = None if args.no_cpu_baseline else cpu_baseline_quant(C)
     return {
         "metric": "HBM GB/s of the FP8 quantisation primitives on 1 MI355X (configs[1])",
@@ -635,9 +636,11 @@ def workload_c2(args, dev):
         "dtype": "bf16 -> e4m3", "data": "synthetic",
         "config": {"workload": "configs[1]: x [8192, 4096] bf16 N(0,1), 0.1% outliers x100; W [14336, 4096] "
                                "bf16 N(0,0.02)",
-                   "chain": [r["op"] for r in chain], "dominant_op": dom["op"]},
+                   "chain": [r["op"] for r in chain]},
         "roofline": {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["frac_of_hbm_peak"], "traffic": None},
+                     "frac": dom["frac_of_hbm_peak"], "traffic": None, "kernel": dom["op"],
+                     "note": "the slowest op by fraction of the HBM peak; every op's fraction in 'per_op'"},
+        "per_op": {r["op"]: r["frac_of_hbm_peak"] for r in results},
         "cpu_baseline": cpu,
         "ops": results,
     }
@@ -784,8 +787,9 @@ def workload_c4(args, dev):
     D, E, K, H = 4096, 8, 2, 14336
     gen = torch.Generator(device=dev).manual_seed(3)
     w1, w2, w3 = [device_normal((E * H, D), 0.02, gen, dev, torch.bfloat16) for _ in range(3)]
+    points = [int(v) for v in args.c4_points.split(",")]
     sweep = []
-    for t in (512, 1024, 2048, 4096, 8192, 16384):
+    for t in points:
         T = 4 * t
         w, idx = zipf_gumbel_topk(T, E, K, 1.1, seed=3)
         w, idx = w.to(dev), idx.to(dev)
@@ -796,24 +800,75 @@ def workload_c4(args, dev):
         row = {"tokens_per_expert": t, "tokens": T,
                "max_tokens_per_expert": int(torch.bincount(idx.reshape(-1), minlength=E).max())}
         for name, recipe in (("bf16", "none"), ("fp8", "flow_moe")):
-            ms, _, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1, gemm_timer=False,
-                               overlap=not args.no_overlap)
+            ms, summ, _ = time_layer(x, w, idx, w1, w2, w3, go, E, recipe, 0, steps, 1,
+                                     overlap=not args.no_overlap)
             row[f"{name}_ms"] = round(ms, 3)
             row[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+            row[f"{name}_gemm"] = gemm_report(summ, steps)
+            row[f"{name}_roofline"] = gemm_roofline(summ, "bf16" if recipe == "none" else "fp8")
         row["fp8_speedup"] = round(row["bf16_ms"] / row["fp8_ms"], 3)
         sweep.append(row)
         print(json.dumps({"progress": row}), file=sys.stderr, flush=True)
         del x, go
         torch.cuda.empty_cache()
     faster = [r["tokens_per_expert"] for r in sweep if r["fp8_speedup"] > 1.0]
+    # the roofline of the point the >= 60 % target is stated at (>= 4096 tokens/expert)
+    big = [r for r in sweep if r["tokens_per_expert"] >= 4096] or sweep
+    cpu = None if args.no_cpu_baseline else cpu_baseline_c4(w1, w2, w3, E, K, points)
     return {
         "metric": "FP8 vs BF16 expert block fwd+bwd crossover on 1 MI355X (configs[3])",
         "n_gpus": 1, "data": "synthetic", "dtype": "fp8-e4m3 vs bf16",
         "config": {"workload": "configs[3]: D=4096, E=8, top-2, H=14336, Zipf(1.1) Gumbel-top-2 routing",
                    "fp8_recipe": "flow_moe", "threshold": 0},
+        "roofline": dict(big[0]["fp8_roofline"], tokens_per_expert=big[0]["tokens_per_expert"]),
         "sweep": sweep,
         "fp8_faster_from_tokens_per_expert": min(faster) if faster else None,
+        "cpu_baseline": cpu,
     }
+
+
+def cpu_baseline_c4(w1, w2, w3, E, K, points, cap_s=60.0):
+    """configs[3]'s expert block fwd+bwd on the host cores: the BF16 arm as the
+    reference's per-expert loop (model/moe.py:1542-1596, torch CPU fp32
+    autograd) and the FP8 arm as the flow's dequantise-then-fp32-matmul
+    (oracle.layer.moe_flow_reference), each point timed once on all its
+    tokens, smallest first, while the CPU time spent stays under `cap_s`;
+    later points are reported as not timed (cap), never extrapolated."""
+    import torch
+
+    from oracle import layer as olayer
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    D = w1.shape[1]
+    W = [t.cpu() for t in (w1, w2, w3)]
+    g = torch.Generator().manual_seed(33)
+    spent, rows = 0.0, []
+    for t in sorted(points):
+        T = 4 * t
+        row = {"tokens_per_expert": t}
+        for name, fn in (("bf16", lambda *a: olayer.moe_bf16_loop(*a)),
+                         ("fp8", lambda *a: olayer.moe_flow_reference(*a, recipe="flow_moe"))):
+            if spent >= cap_s:
+                row[f"{name}_tokens_per_s"] = "CPU not timed (cap)"
+                continue
+            w, idx = zipf_gumbel_topk(T, E, K, 1.1, seed=3)
+            x = torch.randn(T, D, generator=g).bfloat16()
+            go = (torch.randn(T, D, generator=g) * 1e-2).bfloat16()
+            t0 = time.perf_counter()
+            fn(x, w, idx, *W, E, go)
+            dt = time.perf_counter() - t0
+            spent += dt
+            row[f"{name}_tokens_per_s"] = round(T / dt, 1)
+            row[f"{name}_s"] = round(dt, 2)
+        rows.append(row)
+    first = rows[0]
+    return {"value": first["bf16_tokens_per_s"], "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"BF16 per-expert loop fwd+bwd (torch CPU fp32) on all {4 * first['tokens_per_expert']} "
+                      f"tokens of the {first['tokens_per_expert']} tokens/expert point, one run; the per-point "
+                      f"figures (FP8 arm as dequantise-then-fp32-matmul) are in 'points', points past "
+                      f"{cap_s:.0f} s of CPU time not timed; cpu: {cpu_model_name()}",
+            "points": rows}
 
 
 # ============================================================== configs[4] ====
@@ -874,6 +929,9 @@ def workload_c5(args, dev):
     ms, summ, _ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup,
                           overlap=not args.no_overlap)
     flops = 18.0 * A * D * H
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_c5(x, wts, idx, w1, w2, w3, go, E_local)
     return {
         "metric": "MoE expert block fwd+bwd assignments/s on 1 MI355X (configs[4], MXFP8)",
         "value": round(A / (ms * 1e-3), 1), "unit": "assignments/s", "n_gpus": 1, "steps": args.steps,
@@ -885,8 +943,42 @@ def workload_c5(args, dev):
                    "max_tokens_per_expert": int(counts.max())},
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "frac_of_fp8_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["fp8"], 4),
+        "roofline": gemm_roofline(summ, "fp8", flops_scale=A / (n_tok * K)),
         "gemm": gemm_report(summ, args.steps, flops_scale=A / (n_tok * K)),
+        "cpu_baseline": cpu,
     }
+
+
+def cpu_baseline_c5(x, wts, idx, w1, w2, w3, go, E, n_experts=4, a_sample=8192):
+    """configs[4]'s MXFP8 expert block fwd+bwd on the host cores as the flow's
+    dequantise-then-fp32-matmul (oracle.layer.moe_flow_reference, recipe
+    mxfp8) on a bounded sample of the same workload: the slots of the
+    `n_experts` most loaded local experts (the others' slots treated as
+    another GPU's), on the first tokens holding `a_sample` of them, with
+    those experts' weights quantised as the GPU step quantises every
+    expert's (an eighth of the experts: weight and token work in about the
+    layer's proportion); one run."""
+    import torch
+
+    from oracle import layer as olayer
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    idx_h = idx.cpu()
+    counts = torch.bincount(idx_h[idx_h < E], minlength=E)
+    keep_e = torch.argsort(counts, descending=True, stable=True)[:n_experts]
+    keep = torch.isin(idx_h, keep_e)
+    csum = torch.cumsum(keep.sum(dim=1), 0)
+    n = min(int((csum < a_sample).sum()) + 1, idx_h.shape[0])
+    idx_s = torch.where(keep[:n], idx_h[:n], torch.full_like(idx_h[:n], 1 << 20))
+    A = int(keep[:n].sum())
+    host = [t.cpu() for t in (x[:n], wts[:n])] + [idx_s] + [t.cpu() for t in (w1, w2, w3, go[:n])]
+    t0 = time.perf_counter()
+    olayer.moe_flow_reference(*host[:6], E, host[6], recipe="mxfp8")
+    dt = time.perf_counter() - t0
+    return {"value": round(A / dt, 1), "unit": "assignments/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{A} assignments of configs[4] (the first {n} tokens' slots on the {n_experts} most loaded "
+                      f"of the 32 local experts), MXFP8 flow as dequantise-then-fp32-matmul fwd+bwd incl. those "
+                      f"experts' weight quantisation (torch CPU), one run, {dt:.1f} s; cpu: {cpu_model_name()}"}
 
 
 def main():
@@ -903,6 +995,8 @@ def main():
     ap.add_argument("--no-overlap", action="store_true",
                     help="keep every launch on one stream (the router's backward not beside the dY "
                          "permute and dH + dW2; MX: no dW2 / dH overlap)")
+    ap.add_argument("--c4-points", default="512,1024,2048,4096,8192,16384",
+                    help="configs[3] tokens/expert points (comma list)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
