@@ -807,6 +807,13 @@ def workload_c4(args, dev):
             row[f"{name}_gemm"] = gemm_report(summ, steps)
             row[f"{name}_roofline"] = gemm_roofline(summ, "bf16" if recipe == "none" else "fp8")
         row["fp8_speedup"] = round(row["bf16_ms"] / row["fp8_ms"], 3)
+        # the threshold split (model/moe.py:1215-1216): experts with at least the
+        # mean count (t assignments) take FP8, the others BF16
+        ms, summ, _ = time_layer(x, w, idx, w1, w2, w3, go, E, "flow_moe", t, steps, 1,
+                                 overlap=not args.no_overlap)
+        counts = torch.bincount(idx.reshape(-1), minlength=E)
+        row["mixed"] = {"threshold": t, "fp8_experts": int((counts >= t).sum()), "ms": round(ms, 3),
+                        "gemm": gemm_report(summ, steps)}
         sweep.append(row)
         print(json.dumps({"progress": row}), file=sys.stderr, flush=True)
         del x, go

@@ -326,6 +326,16 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
                   int32_t* assign_of_row, int64_t rows_max, int32_t* tile_expert,
                   int32_t* use_fp8, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* For the fp8_gemm_threshold switch (reference model/moe.py:1215-1216,
+ * cli.py:55-63): the routing sort's tile_expert [n_tiles] split by precision,
+ * tiles_fp8[t] = tile_expert[t] if that expert's use_fp8 flag is set, else -1,
+ * and tiles_bf16[t] the converse (-1 where tile_expert is -1).  Passed as the
+ * tile_valid list of fm_permute / fm_swiglu_quantize / fm_swiglu_backward,
+ * they make each precision's producers write only the rows of the experts
+ * whose GEMMs read them. */
+int fm_route_tile_masks(const int32_t* tile_expert, int64_t n_tiles, const int32_t* use_fp8, int32_t* tiles_fp8,
+                        int32_t* tiles_bf16, void* stream);
+
 /* fm_route_sort, then fm_quantize_weight_batch(jobs, n_jobs) on the same
  * stream, with the outputs of the two calls.  No counterpart in the
  * reference: the sort's launches occupy a few CUs for a few microseconds, so

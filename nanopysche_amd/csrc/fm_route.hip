@@ -515,6 +515,23 @@ __global__ __launch_bounds__(256) void sort_scan_scatter_kernel(const I* idx, in
   }
 }
 
+// -------------------------------------------------------- tile masks ----
+// Per-precision tile lists for the fp8_gemm_threshold split: tile t keeps
+// its expert in tiles_fp8 when that expert takes the FP8 GEMMs, in
+// tiles_bf16 otherwise, and -1 in the other list (and in both past the last
+// group), so each producer writes only the rows its own GEMMs read.
+__global__ __launch_bounds__(256) void tile_masks_kernel(const int32_t* __restrict__ tile_expert, int64_t n,
+                                                         const int32_t* __restrict__ use_fp8,
+                                                         int32_t* __restrict__ tiles_fp8,
+                                                         int32_t* __restrict__ tiles_bf16) {
+  for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < n; t += int64_t(gridDim.x) * 256) {
+    const int32_t e = tile_expert[t];
+    const bool f = e >= 0 && use_fp8[e] != 0;
+    tiles_fp8[t] = f ? e : -1;
+    tiles_bf16[t] = e >= 0 && !f ? e : -1;
+  }
+}
+
 // -------------------------------------------------------------- permute ----
 // Row r of the padded buffer is x[assign_of_row[r] / K] (times the router
 // weight of that assignment when WEIGHTED), zeros for pad rows.  Branch-free:
@@ -1071,6 +1088,18 @@ int fm_route_sort_noalloc(const void* indices, int indices_i64, int64_t T, int K
   return route_sort_launch(indices, indices_i64, T, K, E, threshold, counts, offsets, row_of, assign_of_row,
                            rows_max, tile_expert, use_fp8, bh, static_cast<hipStream_t>(stream),
                            "fm_route_sort_noalloc");
+}
+
+int fm_route_tile_masks(const int32_t* tile_expert, int64_t n_tiles, const int32_t* use_fp8, int32_t* tiles_fp8,
+                        int32_t* tiles_bf16, void* stream) {
+  FM_REQUIRE((tile_expert && use_fp8 && tiles_fp8 && tiles_bf16) || n_tiles == 0,
+             "fm_route_tile_masks: null pointer");
+  FM_REQUIRE(n_tiles >= 0, "fm_route_tile_masks: n_tiles must be >= 0");
+  if (n_tiles == 0) return 0;
+  const unsigned blocks = unsigned((n_tiles + 255) / 256 < 1024 ? (n_tiles + 255) / 256 : 1024);
+  hipLaunchKernelGGL(tile_masks_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), tile_expert,
+                     n_tiles, use_fp8, tiles_fp8, tiles_bf16);
+  return check_launch("fm_route_tile_masks");
 }
 
 int fm_permute(const void* x, int64_t T, int64_t D, int64_t ld_x, const int32_t* assign_of_row,

@@ -276,7 +276,8 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
                       granularity: Optional[BlockScalingGranularity] = G.ROW_1x128,
                       pow2_scale: bool = False, return_transpose: bool = False,
                       weights: Optional[torch.Tensor] = None,
-                      fp8_gemm_threshold: int = 0, kmajor_scales: bool = False) -> PermutedTokens:
+                      fp8_gemm_threshold: int = 0, kmajor_scales: bool = False,
+                      tile_valid: Optional[torch.Tensor] = None) -> PermutedTokens:
     """Gather the rows of ``x`` [T, D] (bf16) into expert order, each expert's
     group padded to 128 rows (zeros), and quantise them in the same pass.
     Rows past the last group (``plan.offsets[-1]`` up to ``plan.rows_max``)
@@ -286,7 +287,10 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
     earlier call.  ``weights`` [T, K] (optional) scales each gathered row by
     its router weight.  granularity None keeps bf16.  ``kmajor_scales``
     stores the row scales block-major (``rows.scale`` is then a transposed
-    view), the layout the grouped GEMM streams fastest."""
+    view), the layout the grouped GEMM streams fastest.  ``tile_valid``
+    [rows_max/128] int32 (default ``plan.tile_expert``): 128-row tiles with a
+    negative entry are not written (``RoutingPlan.precision_tiles`` gives
+    each precision's tiles under the threshold split)."""
     _lib.require_device(x, "x")
     if x.dtype != torch.bfloat16:
         raise TypeError("x must be bfloat16")
@@ -303,7 +307,7 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
         w = weights.reshape(-1).to(torch.float32).contiguous()
     _lib.call("fm_permute", _lib.ptr(x2), T, D, x2.stride(0), _lib.ptr(plan.assign_of_row),
               plan.rows_max, plan.top_k, _lib.ptr(w), *_tile_args(kind, q, s, qt, st),
-              _lib.ptr(plan.tile_expert), _lib.stream_of(x2))
+              _lib.ptr(plan.tile_expert if tile_valid is None else tile_valid), _lib.stream_of(x2))
     row, col = _wrap(q, s, qt, st, kind)
     return PermutedTokens(plan, row, col)
 
@@ -952,13 +956,19 @@ class FP8FlowMoECompute:
         GU = torch.empty(R, 2 * H, dtype=torch.bfloat16, device=dev)
         Y = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
         mask = plan.use_fp8 if (fp8_kind is not None and use_bf16) else None
+        # with the threshold splitting the experts, each precision's producers
+        # write only its own experts' tiles (the other GEMMs never read them)
+        tiles = {}
+        if mask is not None:
+            tiles[fp8_kind], tiles[_lib.QUANT_BF16] = plan.precision_tiles()
         saved = {}
         for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
             if kind is None:
                 continue
             ew = ews[kind]
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
-                                   return_transpose=self._record, kmajor_scales=True)
+                                   return_transpose=self._record, kmajor_scales=True,
+                                   tile_valid=tiles.get(kind, plan.tile_expert))
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}
@@ -966,8 +976,8 @@ class FP8FlowMoECompute:
             if kind is None:
                 continue
             # row blocks feed the down GEMM; the column blocks are kept for dW2
-            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, self._record, dev, plan.tile_expert,
-                                   kmajor=True)
+            q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, self._record, dev,
+                                   tiles.get(kind, plan.tile_expert), kmajor=True)
             hrow, hcol = _wrap(q, s, qt, st, kind)
             h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
@@ -981,6 +991,7 @@ class FP8FlowMoECompute:
             self.capture_intermediates["gate_up"] = GU.detach().clone()
         ctx.compute = self
         ctx.plan = plan
+        ctx.tiles = tiles
         ctx.kinds = (fp8_kind, use_bf16)
         ctx.saved_cols = {k: v[0] for k, v in saved.items()}
         # the dgrad weight operands of this forward's weights (a later forward
@@ -1042,9 +1053,11 @@ class FP8FlowMoECompute:
         if not (w1dt == w3dt and w1dt in (torch.float32, torch.bfloat16) and w2dt in (torch.float32, torch.bfloat16)):
             raise TypeError("expert weights must be float32 or bfloat16 (w1 and w3 alike)")
         runs = [(k, w) for k, w in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)) if k is not None]
+        tiles = ctx.tiles
         dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                       return_transpose=True, weights=None if self._dense else wts,
-                                      kmajor_scales=True) for kind, _ in runs}
+                                      kmajor_scales=True, tile_valid=tiles.get(kind, plan.tile_expert))
+              for kind, _ in runs}
         # dH and dW2 (contraction over each expert's tokens) both read the
         # permuted dY: each alone leaves its last round of workgroups
         # part-empty when the hidden size is not a multiple of the 256-wide
@@ -1076,7 +1089,7 @@ class FP8FlowMoECompute:
             gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev, kmajor=True)
             _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
                       _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst),
-                      _lib.ptr(plan.tile_expert), _lib.stream_of(GU))
+                      _lib.ptr(tiles.get(kind, plan.tile_expert)), _lib.stream_of(GU))
             dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
             # dW1 | dW3: contraction over each expert's tokens
             _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,

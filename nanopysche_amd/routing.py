@@ -48,6 +48,21 @@ class RoutingPlan:
     def m_tiles(self) -> int:
         return self.rows_max // PAD_ROWS
 
+    def precision_tiles(self):
+        """(tiles_fp8, tiles_bf16) [rows_max/128] int32: ``tile_expert`` split
+        by the experts' ``use_fp8`` flags (-1 elsewhere), the tile lists of
+        the two precisions' producers when the threshold splits the experts
+        (``fm_route_tile_masks``; made once per plan, on the device)."""
+        tm = getattr(self, "_precision_tiles", None)
+        if tm is None:
+            n = self.m_tiles
+            tf = torch.empty(n, dtype=torch.int32, device=self.tile_expert.device)
+            tb = torch.empty_like(tf)
+            _lib.call("fm_route_tile_masks", _lib.ptr(self.tile_expert), n, _lib.ptr(self.use_fp8), _lib.ptr(tf),
+                      _lib.ptr(tb), _lib.stream_of(tf))
+            tm = self._precision_tiles = (tf, tb)
+        return tm
+
 
 def rows_max(num_assignments: int, num_experts: int) -> int:
     """Upper bound of the padded buffer's rows, known without reading counts."""

@@ -3,6 +3,7 @@ FP8 recipes within 2e-2 (max|err| / max|ref|) of the dequantise-then-fp32
 flow, BF16 within 1e-2 of the reference's per-expert loop
 (model/moe.py:1542-1596)."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -117,6 +118,82 @@ def test_threshold_mixed_fp8_and_bf16(dev, splits, monkeypatch):
     assert olayer.max_rel_err(g1[0], f_grads["w1"].reshape(E, H, D)[0]) <= FP8_TOL
     assert olayer.max_rel_err(g1[1], b_grads["w1"].reshape(E, H, D)[1]) <= BF16_TOL
     assert (g1[3] == 0).all()
+
+
+@pytest.mark.parametrize("recipe", ["flow_moe", "mxfp8"])
+def test_threshold_mixed_top2_tokens_span_both_precisions(dev, recipe, monkeypatch):
+    """Top-2 with the threshold splitting the experts (the split is by each
+    expert's assignment count: 0, 1, 2, 3 hold 700, 324, 512, 512; threshold
+    500 puts 0, 2, 3 on FP8 and 1 on BF16), so the tokens of expert 1 combine
+    a BF16 and an FP8 expert row, and each precision's producers write only
+    their own experts' tiles.  Reference:
+    the FP8 oracle with the BF16 experts' slots dropped plus the BF16 oracle
+    with the FP8 experts' slots dropped (an expert's rows, and so its
+    quantisation blocks, are the same in both); weight gradients per expert
+    from its precision's oracle.  Also: exactly the producer launches of each
+    precision ran with that precision's tile list."""
+    from nanopysche_amd import _lib
+
+    T, D, H, E, K = 1024, 256, 256, 4, 2
+    x, w, _, w1, w2, w3, go = _case(T, D, H, E, K, seed=13)
+    t = torch.arange(T)
+    idx = torch.stack([(t >= 700).long(), 2 + (t % 2)], 1)
+    counts = torch.bincount(idx.reshape(-1), minlength=E)
+    assert counts.tolist() == [700, 324, 512, 512]
+    fp8 = (counts >= 500)[idx]                                   # slots on FP8 experts (expert 0, 2, 3)
+    calls = []
+    real = _lib.call
+
+    def spy(name, *args):
+        calls.append((name, args))
+        return real(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    taps = {}
+    out, grads = _run(dev, x, w, idx, w1, w2, w3, go, E, recipe, threshold=500, taps=taps)
+    monkeypatch.setattr(_lib, "call", real)
+    drop = torch.full_like(idx, 99)
+    f_idx, b_idx = torch.where(fp8, idx, drop), torch.where(fp8, drop, idx)
+    # stage-synchronised: each oracle takes the device's gate|up and dH rows of
+    # its own experts, moved from the device's padded layout to its own
+    dev_offs = orouting.sort_assignments(idx.numpy(), E)["offsets"]
+
+    def sub_taps(sub_idx):
+        offs = orouting.sort_assignments(sub_idx.numpy(), E, drop_out_of_range=True)["offsets"]
+        out_t = {}
+        for k, v in taps.items():
+            a = v.float().cpu().numpy()
+            b = np.zeros((int(offs[-1]), a.shape[1]), np.float32)
+            for e in range(E):
+                n = int(offs[e + 1] - offs[e])
+                b[offs[e]:offs[e] + n] = a[dev_offs[e]:dev_offs[e] + n]
+            out_t[k] = b
+        return out_t
+
+    f_out, f_g = olayer.moe_flow_reference(x, w, f_idx, w1, w2, w3, E, go, recipe=recipe, taps=sub_taps(f_idx))
+    b_out, b_g = olayer.moe_flow_reference(x, w, b_idx, w1, w2, w3, E, go, recipe=None, taps=sub_taps(b_idx))
+    o = out.detach().float().cpu().numpy()
+    assert olayer.max_rel_err(o, f_out + b_out) <= FP8_TOL
+    assert olayer.max_rel_err(grads["x"].float().cpu().numpy(), f_g["x"] + b_g["x"]) <= FP8_TOL
+    dw = grads["weights"].float().cpu().numpy()
+    assert olayer.max_rel_err(dw[fp8.numpy()], f_g["weights"][fp8.numpy()]) <= FP8_TOL
+    assert olayer.max_rel_err(dw[~fp8.numpy()], b_g["weights"][~fp8.numpy()]) <= BF16_TOL
+    fe = [0, 2, 3]
+    for name in ("w1", "w2", "w3"):
+        g = grads[name].float().cpu().numpy().reshape(E, H, D)
+        assert olayer.max_rel_err(g[fe], f_g[name].reshape(E, H, D)[fe]) <= FP8_TOL, name
+        assert olayer.max_rel_err(g[1], b_g[name].reshape(E, H, D)[1]) <= BF16_TOL, name
+    # the producers of the two precisions ran on the two tile lists
+    tl = {}
+    for name, args in calls:
+        if name in ("fm_permute", "fm_swiglu_quantize", "fm_swiglu_backward"):
+            kind = args[8] if name == "fm_permute" else args[6] if name == "fm_swiglu_quantize" else args[8]
+            tl.setdefault(name, set()).add((int(kind) & 0xff, args[-2].value))
+    assert "fm_route_tile_masks" in [n for n, _ in calls]
+    for name in ("fm_permute", "fm_swiglu_quantize", "fm_swiglu_backward"):
+        kinds = {k for k, _ in tl[name]}
+        lists = {v for _, v in tl[name]}
+        assert len(kinds) == 2 and len(lists) == 2, (name, tl[name])
 
 
 def test_drop_in_call_convention(dev):
