@@ -92,7 +92,7 @@ struct GemmParams {
   int64_t c2_gs, split;
   int out_f32;
   int64_t n_tiles;    // logical tiles
-  int rk_xcd;         // ragged-K, 256 x 256 kernel: allow the contiguous XCD split
+  int rk_xcd;         // ragged-K, 256 x 256 kernels: bit 0 allows the contiguous XCD split, bit 1 the chunked shares
   int splits;         // ragged-K, 256 x 256 kernel: K slices per tile (>1: fp32 partials, C = workspace)
   int64_t ws_slice;   // ragged-K split: elements between the partials of two slices
   int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
@@ -101,6 +101,7 @@ struct GemmParams {
 };
 
 constexpr int kGroupM = 8;
+constexpr bool kRkChunkedDefault = true;
 
 // 16-byte chunk `chunk` of 128-byte row `row` of an operand tile in LDS.  The
 // chunk index is XOR-swizzled with (row / 2) % 8: a ds_read_b128 serves 16
@@ -656,7 +657,7 @@ __device__ __forceinline__ bool decode_tile256(const GemmParams& p, Tile256& t, 
     if (L >= n_valid) return false;
   } else {
     L = bid;
-    if (p.rk_xcd && p.mask == nullptr && p.E <= 64) {
+    if ((p.rk_xcd & 1) && p.mask == nullptr && p.E <= 64) {
       int rows = lane < p.E ? p.offsets[lane + 1] - p.offsets[lane] : 0;
       int sum = rows, mx = rows;
 #pragma unroll
@@ -1242,16 +1243,24 @@ struct TileK {
 
 struct RkQueue {
   const int* off;   // LDS copy of offsets[0 .. E]
-  int NI, NJ, per_e, n_tiles, per_xcd, xcd, c0, nbx, contiguous, jfast;
+  int NI, NJ, per_e, n_tiles, per_xcd, xcd, c0, nbx, contiguous, chunked, jfast;
 };
 
-// The c-th tile of this workgroup's share, false past its end.
+// The c-th tile of this workgroup's share, false past its end.  Shares:
+// contiguous -- XCD x walks the x-th of 8 contiguous tile ranges;
+// chunked    -- round c of XCD x is the chunk of nbx consecutive tiles
+//               (8 c + x) nbx .. +nbx, so the tiles an XCD runs at once are
+//               neighbours sharing operand rows (L2 reuse) while every XCD
+//               still takes an equal share of every expert's tiles;
+// otherwise  -- the tiles a one-tile-per-block launch gives block xcd + 8 loc.
 __device__ __forceinline__ bool rk_tile_at(const RkQueue& q, int c, TileK& t, int kstep) {
   const int loc = q.c0 + c * q.nbx;
   int L;
   if (q.contiguous) {
     if (loc >= q.per_xcd) return false;
     L = q.xcd * q.per_xcd + loc;
+  } else if (q.chunked) {
+    L = (c * 8 + q.xcd) * q.nbx + q.c0;
   } else {
     L = q.xcd + 8 * loc;   // block index xcd + 8 loc of a one-tile-per-block launch
   }
@@ -1278,7 +1287,7 @@ __device__ __forceinline__ bool rk_next_long(const RkQueue& q, int& c, TileK& t,
   }
 }
 
-template <int KIND>
+template <int KIND, int MXL = 0>
 __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
   using SM = Smem256<KIND>;
   constexpr int ES = KIND == GK_BF16 ? 2 : 1;
@@ -1317,8 +1326,8 @@ __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
   w.wj = w.wave & 3;
   w.lrow = w.lane & 31;
   w.lhalf = w.lane >> 5;
-  w.q_mx_k = false;
-  w.p_mx_k = false;
+  w.q_mx_k = KIND == GK_FP8_MX && (MXL & 1) != 0;
+  w.p_mx_k = KIND == GK_FP8_MX && (MXL & 2) != 0;
 
   RkQueue q;
   q.off = off;
@@ -1328,7 +1337,8 @@ __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
   q.n_tiles = int(p.n_tiles);
   // wave-uniform (the shuffles leave every lane the same values, which the
   // compiler cannot see): the tile walk feeds the DMA's scalar offsets
-  q.contiguous = __builtin_amdgcn_readfirstlane(int(p.rk_xcd && int64_t(mx) * p.E * 8 <= int64_t(sum) * 9));
+  q.contiguous = __builtin_amdgcn_readfirstlane(int((p.rk_xcd & 1) && int64_t(mx) * p.E * 8 <= int64_t(sum) * 9));
+  q.chunked = !q.contiguous && (p.rk_xcd & 2) != 0;
   q.per_xcd = (q.n_tiles + 7) / 8;
   q.xcd = int(blockIdx.x % 8);
   q.c0 = int(blockIdx.x / 8);
@@ -1535,7 +1545,8 @@ __global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmPara
   q.NJ = int((pk.n_j + kT - 1) / kT);
   q.per_e = q.NI * q.NJ;
   q.n_tiles = int(pk.n_tiles);
-  q.contiguous = __builtin_amdgcn_readfirstlane(int(pk.rk_xcd && int64_t(mx) * pk.E * 8 <= int64_t(sum) * 9));
+  q.contiguous = __builtin_amdgcn_readfirstlane(int((pk.rk_xcd & 1) && int64_t(mx) * pk.E * 8 <= int64_t(sum) * 9));
+  q.chunked = !q.contiguous && (pk.rk_xcd & 2) != 0;
   q.per_xcd = (q.n_tiles + 7) / 8;
   q.xcd = int(blockIdx.x % 8);
   q.nbx = int(gridDim.x / 8);
@@ -1964,6 +1975,16 @@ inline bool gemm_rk_xcd_split() {
   return on;
 }
 
+// Persistent ragged-K launches over unbalanced experts hand each XCD chunks of
+// consecutive tiles (see rk_tile_at) unless FM_RK_CHUNKED=0 (read once).
+inline bool gemm_rk_chunked() {
+  static const bool on = [] {
+    const char* e = getenv("FM_RK_CHUNKED");
+    return e == nullptr ? kRkChunkedDefault : atoi(e) != 0;
+  }();
+  return on;
+}
+
 // fm_grouped_gemm_ragged_m_k runs its two launches as one grid unless
 // FM_GEMM_MK=0 (then back to back; read once).
 inline bool gemm_mk_one_grid() {
@@ -1974,7 +1995,7 @@ inline bool gemm_mk_one_grid() {
   return on;
 }
 
-// Unmasked, unsplit BF16 and FP8 pow2 ragged-K launches with at most 64
+// Unmasked, unsplit BF16, FP8 pow2 and MX ragged-K launches with at most 64
 // experts are persistent unless FM_GEMM_PERSISTENT_K=0 (read once).
 inline bool gemm_persistent_k() {
   static const bool on = [] {
@@ -2041,8 +2062,19 @@ inline void launch256pk(int kind, const GemmParams& p, hipStream_t s) {
   const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
   const int64_t want = (p.n_tiles + 7) / 8 * 8;
   const dim3 grid(unsigned(want < slots ? want : slots)), block(512);
-  if (kind == GK_BF16) hipLaunchKernelGGL((gemm256pk_kernel<GK_BF16>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
+  if (kind == GK_BF16) {
+    hipLaunchKernelGGL((gemm256pk_kernel<GK_BF16>), grid, block, 0, s, p);
+  } else if (kind == GK_FP8_POW2) {
+    hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
+  } else {
+    const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
+    switch (mxl) {
+      case 0: hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_MX, 0>), grid, block, 0, s, p); break;
+      case 1: hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_MX, 1>), grid, block, 0, s, p); break;
+      case 2: hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_MX, 2>), grid, block, 0, s, p); break;
+      default: hipLaunchKernelGGL((gemm256pk_kernel<GK_FP8_MX, 3>), grid, block, 0, s, p); break;
+    }
+  }
 }
 
 template <int MODE>
@@ -2089,7 +2121,7 @@ int prepare_gemm(int kind, GemmParams& p) {
     p.n_tiles = MODE == GM_RAGGED_M ? p.j_tiles * NI256
                                     : int64_t(p.E) * NI256 * ((p.n_j + kT - 1) / kT) * p.splits;
   }
-  p.rk_xcd = MODE == GM_RAGGED_K && gemm_rk_xcd_split() ? 1 : 0;
+  p.rk_xcd = MODE == GM_RAGGED_K ? (gemm_rk_xcd_split() ? 1 : 0) | (gemm_rk_chunked() ? 2 : 0) : 0;
   p.w_fast = MODE == GM_RAGGED_M && gemm_weight_fast(p.n_i * p.K * (kind == GK_BF16 ? 2 : 1)) ? 1 : 0;
   return 0;
 }
@@ -2105,7 +2137,7 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
              (gemm_persistent() || p.q_nn || p.Q.split != INT64_MAX)) {
     launch256p(kind, p, s);
   } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
-             p.n_tiles < (int64_t(1) << 28) && (kind == GK_BF16 || kind == GK_FP8_POW2) && gemm_persistent_k()) {
+             p.n_tiles < (int64_t(1) << 28) && gemm_persistent_k()) {
     // (its tile walk counts in 32-bit integers)
     launch256pk(kind, p, s);
   } else {
