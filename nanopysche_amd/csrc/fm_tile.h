@@ -529,76 +529,79 @@ __device__ __forceinline__ void block_tile(const Src& src, const TileOut& o, int
   }
 }
 
-// MX (32x1) with the transposed output, one row of each thread at a time:
-// row group rg holds rows rg + 32 it, so the it-th row of every row group
-// makes up 32-row block it.  For each it the thread computes its row, emits
-// the row blocks, and the block's column amax is reduced across the 8 row
-// groups of a wave by lane exchanges and across the 4 waves through LDS; each
-// thread then encodes its own values with their block's scale, and only the
-// e4m3 codes stay in LDS (16.5 KiB per output) until the transposed stores.
-// The same values, scales and encodes as staging the fp32 tile in LDS (66
-// KiB, two workgroups per CU), with no row's values kept past its block.
+// MX (32x1) with the transposed output.  Rows are dealt so that wave w holds
+// the tile's 32-row block w: thread (w, lane) owns rows 32 w + 4 (lane / 8) +
+// it (it = 0..3), in each the two 8-column segments of the other layouts.  A
+// block's column amax is then the maximum over the thread's own 4 rows and
+// the wave's 8 row groups (lane exchanges): the scales need no LDS and no
+// barrier.  Each row's values stay in registers until the column scales are
+// known (4 rows x 16 columns per output), each thread encodes them, and only
+// the e4m3 codes pass through LDS (16.5 KiB per output) for the transposed
+// stores -- one barrier per tile.  Values, scales and encodes are those of the
+// row blocks and of staging the fp32 tile in LDS, so the bytes are the same.
 template <class Src, bool HW>
 __device__ __forceinline__ void mx_tile(const Src& src, const TileOut& o, int64_t rows, int64_t row0,
                                         int64_t col0, bool want_row) {
   constexpr int NOUT = Src::kOut;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane8 = tid & 7;
-  __shared__ __attribute__((aligned(16))) float m_red[NOUT][kRowsPerThread][4][128];
-  __shared__ __attribute__((aligned(16))) float m_inv[NOUT][kRowsPerThread][128];
+  const int wave = tid >> 6, lane = tid & 63, lane8 = tid & 7;
   __shared__ __attribute__((aligned(16))) uint32_t m_code[NOUT][128 * 33];
+  const int rb = 32 * wave + 4 * (lane >> 3);   // the thread's first row in the tile
   typename Src::Raw raw[kRowsPerThread][2];
-  fetch_rows(src, raw, rows, row0, col0);
-  const int rg = tid >> 3;
-  RowPtr<QK_MX> p[2] = {RowPtr<QK_MX>(o, row0 + rg, col0 + o.col_off[0]),
-                        RowPtr<QK_MX>(o, row0 + rg, col0 + o.col_off[NOUT - 1])};
+  {
+    const int64_t c = col0 + 8 * lane8;   // rows % 128 == 0: every row is in range
+#pragma unroll
+    for (int it = 0; it < kRowsPerThread; ++it)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) raw[it][h] = src.fetch(row0 + rb + it, c + 64 * h);
+  }
+  float v[kRowsPerThread][NOUT][2][8];
+  float cm[NOUT][2][8];
 #pragma unroll
   for (int it = 0; it < kRowsPerThread; ++it) {
-    float v[NOUT][2][8];
-    compute_row(src, raw[it], v);
+    compute_row(src, raw[it], v[it]);
 #pragma unroll
     for (int oi = 0; oi < NOUT; ++oi) {
+      const RowPtr<QK_MX> p(o, row0 + rb + it, col0 + o.col_off[oi]);
       float sc;
-      row_quant<QK_MX, HW>(v[oi], p[oi], want_row, sc);
-      p[oi].next();
-      float cm[2][8];
+      row_quant<QK_MX, HW>(v[it][oi], p, want_row, sc);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cm[h][i] = max_across_rowgroups(fabsf(v[oi][h][i]));
-      if ((tid & 63) < 8) {
+        for (int i = 0; i < 8; ++i)
+          cm[oi][h][i] = it == 0 ? fabsf(v[it][oi][h][i]) : fmaxf(cm[oi][h][i], fabsf(v[it][oi][h][i]));
+    }
+  }
+  uint8_t* const cs = static_cast<uint8_t*>(o.col_s) + ((row0 + 32 * wave) >> 5) * o.ld_col_s + col0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float* dst = &m_red[oi][it][wave][64 * h + 8 * lane8];
-          *reinterpret_cast<float4*>(dst) = make_float4(cm[h][0], cm[h][1], cm[h][2], cm[h][3]);
-          *reinterpret_cast<float4*>(dst + 4) = make_float4(cm[h][4], cm[h][5], cm[h][6], cm[h][7]);
+  for (int oi = 0; oi < NOUT; ++oi)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t code[8];
+      float inv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        code[i] = mx_code(max_across_rowgroups(cm[oi][h][i]));
+        inv[i] = mx_inv_scale(code[i]);
+      }
+      if (lane < 8) {   // the 8 scale bytes of this lane's columns (one 8-byte store when aligned)
+        uint8_t* d = cs + o.col_off[oi] + 64 * h + 8 * lane8;
+        if ((reinterpret_cast<uintptr_t>(d) & 7) == 0) {
+          *reinterpret_cast<uint2*>(d) = make_uint2(code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                                                    code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d[i] = uint8_t(code[i]);
         }
       }
-    }
-    __syncthreads();
-    if (tid < 128 * NOUT) {   // block it's scale of each output column
-      const int oi = tid >> 7, c = tid & 127;
-      const float m = fmaxf(fmaxf(m_red[oi][it][0][c], m_red[oi][it][1][c]),
-                            fmaxf(m_red[oi][it][2][c], m_red[oi][it][3][c]));
-      const uint32_t code = mx_code(m);
-      m_inv[oi][it][c] = mx_inv_scale(code);
-      static_cast<uint8_t*>(o.col_s)[((row0 + 32 * it) >> 5) * o.ld_col_s + col0 + o.col_off[oi] + c] =
-          uint8_t(code);
-    }
-    __syncthreads();
 #pragma unroll
-    for (int oi = 0; oi < NOUT; ++oi)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int c = 64 * h + 8 * lane8;
-        const float4 i0 = *reinterpret_cast<const float4*>(&m_inv[oi][it][c]);
-        const float4 i1 = *reinterpret_cast<const float4*>(&m_inv[oi][it][c + 4]);
-        const float* x = v[oi][h];
-        const uint32_t w0 = enc_e4m3x4<HW>(x[0] * i0.x, x[1] * i0.y, x[2] * i0.z, x[3] * i0.w);
-        const uint32_t w1 = enc_e4m3x4<HW>(x[4] * i1.x, x[5] * i1.y, x[6] * i1.z, x[7] * i1.w);
-        *reinterpret_cast<uint2*>(&m_code[oi][code_word(rg + 32 * it, h)]) = make_uint2(w0, w1);
+      for (int it = 0; it < kRowsPerThread; ++it) {
+        const float* x = v[it][oi][h];
+        const uint32_t w0 = enc_e4m3x4<HW>(x[0] * inv[0], x[1] * inv[1], x[2] * inv[2], x[3] * inv[3]);
+        const uint32_t w1 = enc_e4m3x4<HW>(x[4] * inv[4], x[5] * inv[5], x[6] * inv[6], x[7] * inv[7]);
+        *reinterpret_cast<uint2*>(&m_code[oi][code_word(rb + it, h)]) = make_uint2(w0, w1);
       }
-  }
+    }
   __syncthreads();
 #pragma unroll
   for (int oi = 0; oi < NOUT; ++oi)
