@@ -43,6 +43,19 @@ extern "C" {
  * then reads the scales of 256 consecutive rows from one contiguous 1 KiB
  * span (FmGemmOperand scale_row_stride 1, scale_kb_stride ld_s). */
 #define FM_SCALES_KMAJOR 0x100
+/* OR-ed into the kind (e4m3 kinds) of fm_quantize / fm_quantize_pair /
+ * fm_permute / fm_swiglu_quantize / fm_swiglu_backward and into
+ * FmWeightJob.kind: the row-major payload q is written in the paired-row
+ * layout -- rows 2p and 2p + 1 interleaved in 64-byte pieces, byte (r, c) at
+ * q[(r >> 1) * 2 * ld_q + (c >> 6) * 128 + (r & 1) * 64 + (c & 63)] (ld_q a
+ * multiple of 64, an even number of rows) -- the operand layout of
+ * fm_grouped_gemm_ragged_m with FM_GEMM_PAIRED.  Scales and the transposed
+ * output are unchanged. */
+#define FM_ROWS_PAIRED 0x400
+/* Likewise for the transposed payload qt (its rows are the source columns,
+ * an even count): the layout of the weight-gradient operands of
+ * fm_grouped_gemm_ragged_k / _m_k with FM_GEMM_PAIRED. */
+#define FM_COLS_PAIRED 0x800
 
 /* grouped GEMM arithmetic kinds */
 #define FM_GEMM_BF16 0
@@ -66,6 +79,19 @@ extern "C" {
  * K x ld bytes below 2^32.  The results are those of the [N][K] layout bit for
  * bit. */
 #define FM_GEMM_W_KMAJOR 0x200
+/* OR-ed into the kind of fm_grouped_gemm_ragged_m (FM_GEMM_FP8_POW2, E <= 64,
+ * K >= 384, row pitches multiples of 64): the token operand, and the weights
+ * unless FM_GEMM_W_KMAJOR, are in the paired-row layout -- rows 2p and 2p + 1
+ * interleaved in 64-byte pieces, byte (r, k) at
+ * (r >> 1) * 2 * ld + (k >> 6) * 128 + (r & 1) * 64 + (k & 63) -- which the
+ * persistent kernel streams in 64-deep half steps through a four-slot ring.
+ * The results are those of the row-major operands bit for bit.  FM_ROWS_PAIRED
+ * makes the quantisers write this layout. */
+#define FM_GEMM_PAIRED 0x400
+/* With FM_GEMM_W_KMAJOR: the [K][N] weights are in the paired-row layout too
+ * (K rows 2p and 2p + 1 interleaved in 64-byte pieces of N), e.g. the paired
+ * gate|up operand read as [K = 2H][N = D] for the input gradient. */
+#define FM_GEMM_W_PAIRED 0x800
 
 /* gating functions (reference model/moe.py:44-46 GatingFunction) */
 #define FM_GATING_SOFTMAX 0

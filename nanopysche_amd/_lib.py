@@ -23,6 +23,8 @@ QUANT_BLOCK = 1
 QUANT_POW2 = 2
 QUANT_MX = 3
 SCALES_KMAJOR = 0x100   # OR-ed into a quant kind: row scales stored block-major
+ROWS_PAIRED = 0x400     # OR-ed into a quant kind: e4m3 rows in the paired-row layout
+COLS_PAIRED = 0x800     # OR-ed into a quant kind: the e4m3 transposed payload paired too
 
 GEMM_BF16 = 0
 GEMM_FP8_F32 = 1
@@ -30,6 +32,8 @@ GEMM_FP8_POW2 = 2
 GEMM_FP8_MX = 3
 GEMM_A_FAST = 0x100       # OR-ed into a ragged-K kind: a_t's tiles vary fastest (a_t not in cache)
 GEMM_W_KMAJOR = 0x200     # OR-ed into a ragged-M FP8 pow2 kind: weights stored [K][N]
+GEMM_PAIRED = 0x400       # OR-ed into a ragged-M FP8 pow2 kind: tokens (and [N][K] weights) paired rows
+GEMM_W_PAIRED = 0x800     # with GEMM_W_KMAJOR: the [K][N] weights paired too
 
 GATING_SOFTMAX = 0
 GATING_SIGMOID = 1

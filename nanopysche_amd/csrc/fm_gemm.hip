@@ -49,6 +49,7 @@
 #include <cstdlib>
 
 #include "fm_common.h"
+#include <type_traits>
 #include "../../include/fm_hip.h"
 
 namespace fm {
@@ -98,6 +99,7 @@ struct GemmParams {
   int w_fast;         // ragged-M: weight tiles vary fastest within a group of token tiles
   int rk_jfast;       // ragged-K: j tiles (a_t's) vary fastest within a group of i tiles
   int q_nn;           // ragged-M: the weights stored [K][N] (persistent BF16 / FP8 pow2 kernel only)
+  int paired;         // ragged-M FP8 pow2, ring kernel: 1 paired tokens (and [N][K] weights), 2 and paired [K][N] weights
 };
 
 constexpr int kGroupM = 8;
@@ -1701,6 +1703,472 @@ __global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmPara
 }
 
 // ============================================================================
+// Ring variant of the persistent kernels: paired-row operands
+// ============================================================================
+// In the paired-row layout (FM_GEMM_PAIRED) rows 2p and 2p + 1 of an operand
+// share "pair row" p, and each 128-byte piece of a pair row holds 64 K bytes
+// of row 2p followed by the same 64 K bytes of row 2p + 1:
+//   byte (r, k) at (r >> 1) * 2 ld + (k >> 6) * 128 + (r & 1) * 64 + (k & 63).
+// A 64-deep K slab of a tile is then whole 128-byte lines, so the K loop runs
+// over half steps (64 deep) through a ring of four LDS slots of 34 KiB (both
+// operands and, with even halves, the step's pow2 scales): the DMA of half
+// j + 4 is issued when half j's slot is released, and each half step waits
+// only for the next half while the two after it stay in flight -- the
+// two-stage loop of gemm256p_kernel drains every load at each step, which
+// bounds its operand stream (measured on gfx950 with the same tiles: 12.3
+// TB/s with one step in flight, 17 TB/s with a second one; 64-byte row pieces
+// stay at 12.5 whatever the depth).  [K][N] weights (QNN) need no pairing: a
+// 64-deep slab is 64 K rows of 256 bytes.  Each half step has its own barrier.
+// Fragments, scales and the MFMA order are those of gemm256p_kernel, so the
+// results are bit-identical.
+constexpr int kSlotOp = kT * 64;   // one operand, one 64-deep half step
+struct SmemR {
+  static constexpr int kS = kT * 4;   // pow2 scales of one operand, one step
+  static constexpr int kP = kSlotOp, kQS = 2 * kSlotOp, kPS = 2 * kSlotOp + kS;
+  static constexpr int kSlot = 2 * kSlotOp + 2 * kS;
+};
+
+// Row r of a paired slot operand: 64 bytes at r * 64, 16-byte chunk c at
+// position c ^ ((r / 4) % 4), so the 16 rows one ds_read_b128 pass touches
+// fall on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int pr_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// The NT fragment of read_frag8 (lane half h: K [16h, +16) and [32 + 16h, +16))
+__device__ __forceinline__ v8i read_frag8_pr(const uint8_t* base, int r, int lhalf) {
+  const v4i x0 = *reinterpret_cast<const v4i*>(base + pr_off(r, lhalf));
+  const v4i x1 = *reinterpret_cast<const v4i*>(base + pr_off(r, lhalf + 2));
+  return __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// DMA source of one operand for half steps.  Paired NT operand: wave w moves
+// rows [32w, 32w + 32) (pairs [16w, 16w + 16)) as two groups of 8 pair rows x
+// 128 bytes; lane n takes pair n / 8, row (n / 4) % 2 of the pair, chunk
+// (n % 4) ^ ((n / 16) % 4), which lands at LDS row 16 g + n / 4, position n % 4
+// of its group g.  [K][N] operand: wave w moves K rows [8w, 8w + 8) as two
+// groups of 4 K rows (make_stream_nn's lanes; both parities).
+struct RingStream {
+  v4i rsrc;
+  uint32_t group_bytes;
+  uint32_t lane_off[2];
+  uint32_t k_half_bytes;   // byte advance per half step
+};
+__device__ __forceinline__ RingStream make_stream_pr(const uint8_t* base, int64_t ld, int64_t rows, int lane,
+                                                     int wave) {
+  RingStream s;
+  const int last = int(rows / 32) - 1;
+  s.rsrc = make_rsrc(base + int64_t(wave < last ? wave : last) * 32 * ld);
+  s.group_bytes = uint32_t(16 * ld);
+  s.lane_off[0] = s.lane_off[1] =
+      uint32_t((lane >> 3) * 2 * ld + ((lane >> 2) & 1) * 64 + (((lane & 3) ^ ((lane >> 4) & 3)) << 4));
+  s.k_half_bytes = 128;
+  return s;
+}
+__device__ __forceinline__ RingStream make_stream_nn_half(const uint8_t* base, int64_t ld, int lane, int wave) {
+  RingStream s;
+  s.rsrc = make_rsrc(base + int64_t(wave) * 8 * ld);
+  s.group_bytes = uint32_t(4 * ld);
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int row = lane >> 4, kk = 4 * par + row;
+    s.lane_off[par] = uint32_t(row * ld + 16 * ((lane & 15) ^ (2 * kk)));
+  }
+  s.k_half_bytes = uint32_t(64 * ld);
+  return s;
+}
+
+// [K][N] operand in the paired-row layout (K rows 2p, 2p + 1 interleaved in
+// 64-byte pieces of N): the same LDS layout as make_stream_nn_half (K row k at
+// k * 256, 16-byte chunk c at position c ^ 2 (k % 8)), so lane n of group u
+// (K rows 4u .. 4u + 3 of the wave's 8) fetches K row kr = n / 16 of the
+// group, logical chunk c = (n % 16) ^ 2 (4u + kr): pair kr / 2, piece kr % 2
+// of the 128-byte line of N block c / 4.  A group's 64 lanes cover 8 whole
+// lines.  `base` points at N column 0 of the tile in K row 0.
+__device__ __forceinline__ RingStream make_stream_nn_half_paired(const uint8_t* base, int64_t ld, int lane,
+                                                                 int wave) {
+  RingStream s;
+  s.rsrc = make_rsrc(base + int64_t(wave) * 8 * ld);
+  s.group_bytes = uint32_t(4 * ld);
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int kr = lane >> 4, c = (lane & 15) ^ (2 * (4 * par + kr));
+    s.lane_off[par] = uint32_t((kr >> 1) * 2 * ld + (kr & 1) * 64 + (c >> 2) * 128 + (c & 3) * 16);
+  }
+  s.k_half_bytes = uint32_t(64 * ld);
+  return s;
+}
+
+struct RingStreams {
+  RingStream q, p;
+  ScaleSrc sc;
+};
+
+template <bool QNN, bool QP>
+__device__ __forceinline__ RingStreams ring_streams(const Operand& Q, const Operand& P, int64_t n_i, const TileP& t,
+                                                   const WaveCoord& w) {
+  RingStreams s;
+  const int64_t q_rows = n_i - t.i0 < kT ? n_i - t.i0 : kT;
+  const int64_t p_rows = t.j_end - t.j0 < kT ? t.j_end - t.j0 : kT;
+  const int lane = fresh_lane();
+  if constexpr (QNN && QP)   // tile column i0 (a multiple of 256): N block i0 / 64 of every pair row
+    s.q = make_stream_nn_half_paired(Q.p + int64_t(t.e) * Q.gs + (int64_t(t.i0) >> 6) * 128, Q.ld, lane, w.wave);
+  else if constexpr (QNN) s.q = make_stream_nn_half(Q.p + int64_t(t.e) * Q.gs + int64_t(t.i0), Q.ld, lane, w.wave);
+  else s.q = make_stream_pr(Q.p + int64_t(t.e) * Q.gs + t.i0 * Q.ld, Q.ld, q_rows, lane, w.wave);
+  s.p = make_stream_pr(P.p + int64_t(t.j0) * P.ld, P.ld, p_rows, lane, w.wave);
+  // waves 0-3 stream the weights' scales, 4-7 the tokens': the fields are
+  // selected by value (a select of the two operands' addresses would put the
+  // kernel arguments in scratch memory)
+  const int li = (w.wave & 3) * 64 + lane;
+  const bool wq = w.wave < 4;
+  Operand so;
+  so.s = wq ? Q.s : P.s;
+  so.s_row = wq ? Q.s_row : P.s_row;
+  so.s_kb = wq ? Q.s_kb : P.s_kb;
+  so.s_gs = wq ? Q.s_gs : P.s_gs;
+  so.s_shift = wq ? Q.s_shift : P.s_shift;
+  s.sc = make_scale_src<GK_FP8_POW2>(so, wq ? int64_t(t.i0) : int64_t(t.j0), wq ? q_rows : p_rows, wq ? t.e : 0,
+                                     false, li, wq ? SmemR::kQS : SmemR::kPS);
+  return s;
+}
+
+// A descriptor held in vector registers (the compiler may move the tile's
+// streams there between tiles), read back as the wave-uniform value it is.
+__device__ __forceinline__ v4i uniform_rsrc(v4i r) {
+  v4i u;
+  u[0] = __builtin_amdgcn_readfirstlane(r[0]);
+  u[1] = __builtin_amdgcn_readfirstlane(r[1]);
+  u[2] = __builtin_amdgcn_readfirstlane(r[2]);
+  u[3] = __builtin_amdgcn_readfirstlane(r[3]);
+  return u;
+}
+
+// Piece u of half j's DMA: u = 0..3 the operand groups (even: Q group u / 2,
+// odd: P group u / 2), u = 4 the step's scale dword (even halves only).
+__device__ __forceinline__ void issue_piece_r(int u, const RingStreams& S, int64_t j, uint32_t dst, int wave) {
+  const int g = u >> 1;
+  if (u == 4) {
+    bdma4(uniform_rsrc(S.sc.rsrc), S.sc.voff, __builtin_amdgcn_readfirstlane(uint32_t(j >> 1) * S.sc.k), dst + S.sc.dst);
+  } else if (u & 1) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(g * S.p.group_bytes + uint32_t(j) * S.p.k_half_bytes);
+    bdma16(uniform_rsrc(S.p.rsrc), S.p.lane_off[g], soff, dst + SmemR::kP + (wave * 2 + g) * 1024);
+  } else {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(g * S.q.group_bytes + uint32_t(j) * S.q.k_half_bytes);
+    bdma16(uniform_rsrc(S.q.rsrc), S.q.lane_off[g], soff, dst + (wave * 2 + g) * 1024);
+  }
+}
+
+// Reads the fragments of the half in slot `st` into f (with the step's
+// scales when `scales`), with half j's DMA pieces placed between the reads.
+// EVEN: half j is even (its DMA carries the step's scale dword); the parity
+// is a template argument so the loop body stays one basic block.
+template <bool QNN, bool EVEN>
+__device__ __forceinline__ void issue_read_r(const RingStreams& S, int64_t j, uint32_t dst, int wave,
+                                             const uint8_t* st, bool scales, Frag<GK_FP8_POW2>& f,
+                                             const WaveCoord& w) {
+  if (scales) {
+    f.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
+    const uint2 v = *reinterpret_cast<const uint2*>(
+        st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+    f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
+  }
+  if constexpr (EVEN) issue_piece_r(4, S, j, dst, wave);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if constexpr (QNN) f.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
+    else f.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
+    issue_piece_r(t, S, j, dst, wave);
+    if (t < 2) f.b[t] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
+  }
+}
+
+// One tile of the ring walk: a ragged-M tile (k_mode 0: expert e, weight
+// rows i0, token rows j0 .. j_end) or a ragged-K tile (k_mode 1: expert e's
+// weight-gradient tile i0, j0 over its tokens); kh0 = first 64-deep half step
+// (absolute: a token offset / 64 for ragged-K), nh = half steps.
+struct ItemR {
+  int k_mode, e, i0, j0, j_end, kh0, nh;
+};
+
+// The next tile of the share with at least `min_nk` K steps, from position `c`.
+__device__ __forceinline__ bool rk_next_min(const RkQueue& q, int& c, TileK& t, int kstep, int min_nk) {
+  for (;;) {
+    if (!rk_tile_at(q, c, t, kstep)) return false;
+    ++c;
+    if (t.nk >= min_nk) return true;
+  }
+}
+
+// Persistent ring walk over paired-row operands (FP8 pow2): HAS_M -- the
+// ragged-M tiles of pm (the per-XCD shares of gemm256p_kernel), HAS_K -- then
+// the ragged-K tiles of pk (the shares of gemm256pk_kernel; with HAS_M the
+// workgroups of an XCD take them in reverse order, as gemm256pmk_kernel).
+// QNN / QP: pm's weights stored [K][N] / paired (ragged-K operands are paired
+// [rows][tokens]).  Every tile runs the four-slot ring of half steps and the
+// last four refills of a tile fetch the next tile's first four halves;
+// ragged-K tiles of fewer than three K steps come last, one at a time.  No
+// expert masks, at most 64 experts, ragged-M K >= 384 (the launcher).
+template <bool HAS_M, bool HAS_K, bool QNN, bool QP>
+__global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams pk) {
+  static_assert(!(HAS_K && QNN), "ragged-K tiles share the NT fragment reads");
+  constexpr int KIND = GK_FP8_POW2;
+  constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
+  constexpr int kQueue = 1024;       // ragged-M tile queue
+  constexpr int kOff = 512;          // ragged-K offsets copy
+  constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
+  constexpr int kBase = 4 * SmemR::kSlot;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kBase + kSpare + kQueue + kOff + 2 * kArgs];
+  int* const qlds = reinterpret_cast<int*>(smem + kBase + kSpare);
+  int* const off = reinterpret_cast<int*>(smem + kBase + kSpare + kQueue);
+  GemmParams* const plm = reinterpret_cast<GemmParams*>(smem + kBase + kSpare + kQueue + kOff);
+  GemmParams* const plk = reinterpret_cast<GemmParams*>(smem + kBase + kSpare + kQueue + kOff + kArgs);
+  if (threadIdx.x == 0) {
+    *plm = pm;
+    *plk = pk;
+  }
+
+  WaveCoord w;
+  w.lane = threadIdx.x & 63;
+  w.wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  w.wi = w.wave >> 2;
+  w.wj = w.wave & 3;
+  w.lrow = w.lane & 31;
+  w.lhalf = w.lane >> 5;
+  w.q_mx_k = w.p_mx_k = false;
+
+  TileQueue tq;
+  if constexpr (HAS_M) tile_queue_init(pm, tq, qlds);
+  int sum = 0, mx = 0;
+  if constexpr (HAS_K) {
+    const int lane0 = threadIdx.x & 63;
+    int rows = 0, o0 = 0;
+    if (lane0 < pk.E) {
+      o0 = pk.offsets[lane0];
+      rows = pk.offsets[lane0 + 1] - o0;
+    }
+    if (threadIdx.x < 64) {
+      if (lane0 < pk.E) off[lane0] = o0;
+      if (lane0 == pk.E - 1) off[pk.E] = o0 + rows;
+    }
+    sum = rows;
+    mx = rows;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      sum += __shfl_xor(sum, d, 64);
+      mx = max(mx, __shfl_xor(mx, d, 64));
+    }
+  }
+  block_barrier();   // queues and arguments are in LDS
+
+  RkQueue q{};
+  if constexpr (HAS_K) {
+    q.off = off;
+    q.NI = int((pk.n_i + kT - 1) / kT);
+    q.NJ = int((pk.n_j + kT - 1) / kT);
+    q.per_e = q.NI * q.NJ;
+    q.n_tiles = int(pk.n_tiles);
+    q.contiguous = __builtin_amdgcn_readfirstlane(int((pk.rk_xcd & 1) && int64_t(mx) * pk.E * 8 <= int64_t(sum) * 9));
+    q.chunked = !q.contiguous && (pk.rk_xcd & 2) != 0;
+    q.per_xcd = (q.n_tiles + 7) / 8;
+    q.xcd = int(blockIdx.x % 8);
+    q.nbx = int(gridDim.x / 8);
+    q.c0 = HAS_M ? q.nbx - 1 - int(blockIdx.x / 8) : int(blockIdx.x / 8);
+    q.jfast = pk.rk_jfast;
+  }
+
+  const int nh_m = HAS_M ? int(pm.K / 64) : 0;   // >= 6 (launcher)
+  int cm = 0, ck = 0;                              // positions in the two shares
+  auto next_item = [&](ItemR& it) -> bool {
+    if constexpr (HAS_M) {
+      TileP tp;
+      if (tile_queue_get(tq, cm, tp)) {
+        ++cm;
+        it = ItemR{0, tp.e, tp.i0, tp.j0, tp.j_end, 0, nh_m};
+        return true;
+      }
+    }
+    if constexpr (HAS_K) {
+      TileK tk;
+      if (rk_next_min(q, ck, tk, 128, 3)) {
+        it = ItemR{1, tk.e, tk.i0, tk.j0, 0, tk.k_lo / 64, 2 * tk.nk};
+        return true;
+      }
+    }
+    return false;
+  };
+  auto streams = [&](const ItemR& it) -> RingStreams {
+    if (HAS_K && (!HAS_M || it.k_mode)) {
+      const Operand Q = uniform_operand(&plk->Q), P = uniform_operand(&plk->P);
+      return ring_streams<false, true>(Q, P, rfl64(plk->n_i), TileP{0, it.i0, it.j0, int(rfl64(plk->n_j))}, w);
+    }
+    const Operand Q = uniform_operand(&plm->Q), P = uniform_operand(&plm->P);
+    return ring_streams<QNN, QP>(Q, P, rfl64(plm->n_i), TileP{it.e, it.i0, it.j0, it.j_end}, w);
+  };
+  const uint32_t smem_lds = lds_addr(smem);
+  uint8_t* const W = smem + kBase + w.wave * 2048;
+
+  auto store = [&](void* C, int64_t ldC, int out_f32, int64_t row0, int64_t col0, const v16f (&acc)[4][2]) {
+    WaveCoord we = w;
+    we.lane = fresh_lane();
+    we.lrow = we.lane & 31;
+    we.lhalf = we.lane >> 5;
+    if (!out_f32) {
+      store_bf16_passes(acc, W, static_cast<uint16_t*>(C), ldC, row0, col0, we);
+    } else {
+      float* dst = static_cast<float*>(C) + row0 * ldC + col0 + we.lrow * ldC + 4 * we.lhalf;
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+    }
+  };
+  auto epilogue = [&](const ItemR& it, const v16f (&acc)[4][2]) {
+    const int64_t ib = it.i0 + w.wi * 128, jb = it.j0 + w.wj * 64;
+    if (HAS_K && (!HAS_M || it.k_mode)) {   // weight gradient: row j (m), column i; rows past `split` to C2
+      if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return;
+      const int64_t split = rfl64(plk->split);
+      const bool second = jb >= split;
+      const int64_t gs = second ? rfl64(plk->c2_gs) : rfl64(plk->c_gs);
+      uint8_t* const Cb = static_cast<uint8_t*>(second ? plk->C2 : plk->C);
+      const int f32 = __builtin_amdgcn_readfirstlane(plk->out_f32);
+      store(Cb + int64_t(it.e) * gs * (f32 ? 4 : 2), rfl64(plk->ldC), f32, second ? jb - split : jb, ib, acc);
+    } else {   // dgrad / forward: row j (token), column i
+      const int p_rows = it.j_end - it.j0 < kT ? it.j_end - it.j0 : kT;
+      if (ib >= rfl64(plm->n_i) || jb >= it.j0 + p_rows) return;
+      store(plm->C, rfl64(plm->ldC), __builtin_amdgcn_readfirstlane(plm->out_f32), jb, ib, acc);
+    }
+  };
+  auto zero = [](v16f (&acc)[4][2]) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+  };
+  auto slot = [&](int g) { return smem + (g & 3) * SmemR::kSlot; };
+  auto slot_lds = [&](int g) { return smem_lds + uint32_t(g & 3) * SmemR::kSlot; };
+
+  Frag<KIND> f0, f1;   // f0: even halves (with the step's scales), f1: odd halves
+  ItemR cur;
+  if (next_item(cur)) {
+    RingStreams S = streams(cur);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int v = 0; v < 5; ++v)
+        if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, cur.kh0 + u, slot_lds(u), w.wave);
+    }
+    FM_WAIT_VMCNT(13);   // half 0 landed (halves 1-3: 4 + 5 + 4 pieces in flight)
+    block_barrier();
+    {
+      const uint8_t* st = slot(0);
+      f0.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
+      const uint2 v = *reinterpret_cast<const uint2*>(
+          st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+      f0.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if constexpr (QNN) f0.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
+        else f0.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
+        if (t < 2) f0.b[t] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
+      }
+    }
+    int gs = 0;   // ring slot of the current even half (0 or 2)
+    for (;;) {
+      ItemR nxt;
+      const bool has_next = next_item(nxt);
+      v16f acc[4][2];
+      zero(acc);
+      // Two half steps: the even half's MFMAs (f0) while the odd half is read
+      // into f1 and absolute half jn (even) is issued into the even slot, then
+      // the odd half's MFMAs while the next even half is read into f0 and jn + 1
+      // is issued into the odd slot.  `drain`: the first pair after an
+      // epilogue, whose output stores count in vmcnt too, waits for everything.
+      auto pair = [&](int64_t jn, auto drain) {
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(drain)::value) FM_WAIT_VMCNT(0);
+        else FM_WAIT_VMCNT(9);   // the odd half landed (the two halves after it in flight)
+        block_barrier();         // every wave has read the even half: its slot is free
+        issue_read_r<QNN, true>(S, jn, slot_lds(gs), w.wave, slot(gs + 1), false, f1, w);
+        f1.sa[0] = f0.sa[0];
+        f1.sb[0] = f0.sb[0];
+        mma_half<KIND>(f0, acc);
+        interleave_half<KIND, QNN>();
+        __builtin_amdgcn_sched_barrier(0);
+        FM_WAIT_VMCNT(9);
+        block_barrier();
+        issue_read_r<QNN, false>(S, jn + 1, slot_lds(gs + 1), w.wave, slot(gs + 2), true, f0, w);
+        mma_half<KIND>(f1, acc);
+        interleave_half<KIND, QNN>();
+        __builtin_amdgcn_sched_barrier(0);
+        gs = (gs + 2) & 3;
+      };
+      const int nh = cur.nh;   // >= 6
+      const int64_t kh0 = cur.kh0;
+      pair(kh0 + 4, std::true_type{});
+#pragma unroll 1
+      for (int j = 2; j < nh - 4; j += 2) pair(kh0 + j + 4, std::false_type{});
+      if (has_next) S = streams(nxt);
+      // the last four halves: the next tile's halves 0-3 (the last tile
+      // re-issues its own last two halves, whose slots nothing reads again)
+      const int64_t kn0 = has_next ? int64_t(nxt.kh0) : kh0 + nh - 2;
+#pragma unroll 1
+      for (int j = 0; j < 4; j += 2) pair(has_next ? kn0 + j : kn0, std::false_type{});   // a loop: one block per pair
+      epilogue(cur, acc);
+      if (!has_next) break;
+      cur = nxt;
+    }
+    FM_WAIT_VMCNT(0);
+    block_barrier();   // the slots are free again
+  }
+
+  if constexpr (HAS_K) {
+    // ragged-K tiles of fewer than three K steps, one at a time
+    for (int c = 0;; ++c) {
+      TileK t;
+      if (!rk_tile_at(q, c, t, 128)) break;
+      if (t.nk >= 3) continue;
+      const ItemR it{1, t.e, t.i0, t.j0, 0, t.k_lo / 64, 2 * t.nk};
+      v16f acc[4][2];
+      zero(acc);
+      if (t.nk > 0) {
+        const RingStreams S = streams(it);
+        for (int u = 0; u < it.nh; ++u)
+#pragma unroll
+          for (int v = 0; v < 5; ++v)
+            if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, it.kh0 + u, slot_lds(u), w.wave);
+        FM_WAIT_VMCNT(0);
+        block_barrier();
+        for (int u = 0; u < it.nh; u += 2) {
+          const uint8_t* st = slot(u);
+          f0.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
+          const uint2 v = *reinterpret_cast<const uint2*>(
+              st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+          f0.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
+          f1.sa[0] = f0.sa[0];
+          f1.sb[0] = f0.sb[0];
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            f0.a[tt] = read_frag8_pr(st, w.wi * 128 + tt * 32 + w.lrow, w.lhalf);
+            f1.a[tt] = read_frag8_pr(slot(u + 1), w.wi * 128 + tt * 32 + w.lrow, w.lhalf);
+            if (tt < 2) {
+              f0.b[tt] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + tt * 32 + w.lrow, w.lhalf);
+              f1.b[tt] = read_frag8_pr(slot(u + 1) + SmemR::kP, w.wj * 64 + tt * 32 + w.lrow, w.lhalf);
+            }
+          }
+          mma_half<KIND>(f0, acc);
+          mma_half<KIND>(f1, acc);
+        }
+        block_barrier();   // every wave has read the slots before the next tile's DMA
+      }
+      epilogue(it, acc);
+    }
+  }
+}
+
+// ============================================================================
 // 256 x 128 kernel: FP8_F32 (fp32 block scales, promotion per 128-deep block)
 // ============================================================================
 constexpr int kBI = 256;   // workgroup tile along i (weight rows / M)
@@ -2041,8 +2509,15 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
       else hipLaunchKernelGGL((gemm256p_kernel<GK_BF16>), grid, block, 0, s, p);
       break;
     case GK_FP8_POW2:
-      if (p.q_nn) hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2, 0, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
+      if (p.paired) {
+        if (p.q_nn && p.paired == 2) hipLaunchKernelGGL((gemm256r_kernel<true, false, true, true>), grid, block, 0, s, p, p);
+        else if (p.q_nn) hipLaunchKernelGGL((gemm256r_kernel<true, false, true, false>), grid, block, 0, s, p, p);
+        else hipLaunchKernelGGL((gemm256r_kernel<true, false, false, true>), grid, block, 0, s, p, p);
+      } else if (p.q_nn) {
+        hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2, 0, true>), grid, block, 0, s, p);
+      } else {
+        hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2>), grid, block, 0, s, p);
+      }
       break;
     default: {
       const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
@@ -2134,8 +2609,14 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
   if (kind == GK_FP8_F32) {
     hipLaunchKernelGGL((gemm_f32_kernel<MODE>), grid, block, 0, s, p);
   } else if (MODE == GM_RAGGED_M && p.E <= 64 && p.K / (kind == GK_BF16 ? 64 : 128) >= 2 &&
-             (gemm_persistent() || p.q_nn || p.Q.split != INT64_MAX)) {
+             (gemm_persistent() || p.q_nn || p.paired || p.Q.split != INT64_MAX)) {
     launch256p(kind, p, s);
+  } else if (MODE == GM_RAGGED_K && p.paired) {
+    // paired-row operands (checked by the entry point): the ring walk
+    const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
+    const int64_t want = (p.n_tiles + 7) / 8 * 8;
+    const dim3 pgrid(unsigned(want < slots ? want : slots)), pblock(512);
+    hipLaunchKernelGGL((gemm256r_kernel<false, true, false, true>), pgrid, pblock, 0, s, p, p);
   } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
              p.n_tiles < (int64_t(1) << 28) && gemm_persistent_k()) {
     // (its tile walk counts in 32-bit integers)
@@ -2236,7 +2717,7 @@ namespace {
 // Checks the ragged-M arguments and fills the launch parameters (`kind`
 // without flags; nn: the weights are stored [K][N]).  Returns 0 with
 // p.m_tiles == 0 when there is nothing to do.
-int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmOperand* weights, int64_t m_tiles,
+int ragged_m_params(int kind, int nn, int paired, const FmGemmOperand* tokens, const FmGemmOperand* weights, int64_t m_tiles,
                     const int32_t* tile_expert, const int32_t* offsets, int E, int64_t N, int64_t K,
                     const int32_t* expert_mask, int mask_want, void* out, int out_dtype, int64_t ld_out,
                     GemmParams& p) {
@@ -2273,9 +2754,14 @@ int ragged_m_params(int kind, int nn, const FmGemmOperand* tokens, const FmGemmO
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_m: bad out dtype");
   FM_REQUIRE(kind != GK_FP8_F32 || weights->scale_row_shift == 7,
              "fm_grouped_gemm_ragged_m: fp32-scaled weights must use 128-row scale blocks");
+  FM_REQUIRE(!paired || (kind == GK_FP8_POW2 && E <= 64 && K >= 384 && tokens->ld % 64 == 0 &&
+                         weights->data2 == nullptr && (nn || weights->ld % 64 == 0)),
+             "fm_grouped_gemm_ragged_m: paired-row operands need the pow2 kind, E <= 64, K >= 384, unsplit "
+             "weights and row pitches that are multiples of 64");
   p = GemmParams{};
   p.m_tiles = m_tiles;
   if (m_tiles == 0) return 0;
+  p.paired = paired;
   p.P = make_operand(*tokens);
   p.Q = make_operand(*weights);
   p.n_i = N;
@@ -2305,9 +2791,13 @@ int fm_grouped_gemm_ragged_m(int kind, const FmGemmOperand* tokens, const FmGemm
                              int E, int64_t N, int64_t K, const int32_t* expert_mask, int mask_want,
                              void* out, int out_dtype, int64_t ld_out, void* stream) {
   const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
-  kind &= ~FM_GEMM_W_KMAJOR;
+  // paired: 1 tokens (and [N][K] weights) paired, 2 [K][N] weights paired too
+  const int paired = (kind & FM_GEMM_PAIRED) == 0 ? 0 : (nn && (kind & FM_GEMM_W_PAIRED) != 0) ? 2 : 1;
+  FM_REQUIRE((kind & FM_GEMM_W_PAIRED) == 0 || (nn && paired),
+             "fm_grouped_gemm_ragged_m: FM_GEMM_W_PAIRED needs FM_GEMM_PAIRED and FM_GEMM_W_KMAJOR");
+  kind &= ~(FM_GEMM_W_KMAJOR | FM_GEMM_PAIRED | FM_GEMM_W_PAIRED);
   GemmParams p;
-  if (int rc = ragged_m_params(kind, nn, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
+  if (int rc = ragged_m_params(kind, nn, paired, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
                                mask_want, out, out_dtype, ld_out, p))
     return rc;
   if (p.m_tiles == 0) return 0;
@@ -2364,11 +2854,19 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
                              void* out2, int64_t out2_gs, int64_t split_rows, int out_dtype,
                              int64_t ld_out, void* stream) {
   const int a_fast = (kind & FM_GEMM_A_FAST) != 0;
-  kind &= ~FM_GEMM_A_FAST;
+  const int paired = (kind & FM_GEMM_PAIRED) != 0;
+  kind &= ~(FM_GEMM_A_FAST | FM_GEMM_PAIRED);
   GemmParams p;
   if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M, N, expert_mask, mask_want, out, out_gs, out2,
                                out2_gs, split_rows, out_dtype, ld_out, p))
     return rc;
+  if (paired) {
+    FM_REQUIRE(kind == GK_FP8_POW2 && expert_mask == nullptr && E <= 64 && a_t->ld % 64 == 0 && b_t->ld % 64 == 0 &&
+                   int64_t(E) * ((M + 255) / 256) * ((N + 255) / 256) < (int64_t(1) << 28),
+               "fm_grouped_gemm_ragged_k: paired-row operands need the pow2 kind, no expert mask, E <= 64, "
+               "pitches that are multiples of 64 and fewer than 2^28 tiles");
+    p.paired = 1;
+  }
   p.rk_jfast = a_fast;
   return dispatch_gemm<GM_RAGGED_K>(kind, p, static_cast<hipStream_t>(stream));
 }
@@ -2381,9 +2879,10 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
                                const int32_t* expert_mask, int mask_want, void* stream) {
   const int nn = (kind & FM_GEMM_W_KMAJOR) != 0;
   const int a_fast = (kind & FM_GEMM_A_FAST) != 0;
-  kind &= ~(FM_GEMM_W_KMAJOR | FM_GEMM_A_FAST);
+  const int paired = (kind & FM_GEMM_PAIRED) != 0;
+  kind &= ~(FM_GEMM_W_KMAJOR | FM_GEMM_A_FAST | FM_GEMM_PAIRED);
   GemmParams pm, pk;
-  if (int rc = ragged_m_params(kind, nn, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
+  if (int rc = ragged_m_params(kind, nn, paired, tokens, weights, m_tiles, tile_expert, offsets, E, N, K, expert_mask,
                                mask_want, out, out_dtype, ld_out, pm))
     return rc;
   if (int rc = ragged_k_params(kind, a_t, b_t, offsets, E, M2, N2, expert_mask, mask_want, out2, out2_gs, out2b,
@@ -2391,6 +2890,23 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
     return rc;
   pk.rk_jfast = a_fast;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (paired) {
+    // every operand paired: one ring walk over the dgrad tiles, then the weight-gradient tiles
+    FM_REQUIRE(!nn && expert_mask == nullptr && a_t->ld % 64 == 0 && b_t->ld % 64 == 0 &&
+                   int64_t(E) * ((M2 + 255) / 256) * ((N2 + 255) / 256) < (int64_t(1) << 28),
+               "fm_grouped_gemm_ragged_m_k: paired-row operands need [N][K] weights, no expert mask, "
+               "pitches that are multiples of 64 and fewer than 2^28 weight-gradient tiles");
+    pk.paired = 1;
+    if (int rc = prepare_gemm<GM_RAGGED_M>(kind, pm)) return rc;
+    if (int rc = prepare_gemm<GM_RAGGED_K>(kind, pk)) return rc;
+    const int64_t nbm = pm.m_tiles == 0 ? 0 : (pm.n_tiles + 7) / 8 * 8, nbk = (pk.n_tiles + 7) / 8 * 8;
+    if (nbm + nbk == 0) return 0;
+    const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
+    const dim3 pgrid(unsigned(nbm + nbk < slots ? nbm + nbk : slots)), pblock(512);
+    if (nbm == 0) hipLaunchKernelGGL((gemm256r_kernel<false, true, false, true>), pgrid, pblock, 0, s, pk, pk);
+    else hipLaunchKernelGGL((gemm256r_kernel<true, true, false, true>), pgrid, pblock, 0, s, pm, pk);
+    return check_launch("fm_grouped_gemm_ragged_m_k");
+  }
   if (nn || pm.m_tiles == 0 || (kind != GK_BF16 && kind != GK_FP8_POW2) || !gemm_mk_one_grid()) {
     if (pm.m_tiles > 0)
       if (int rc = dispatch_gemm<GM_RAGGED_M>(kind, pm, s)) return rc;

@@ -336,10 +336,10 @@ int make_weight_side(const FmWeightJob* jobs, int n_jobs, WeightSide& ws, const 
     FM_REQUIRE(jb.groups == jobs[0].groups && jb.rows == jobs[0].rows && jb.cols == jobs[0].cols &&
                    jb.w_dtype == jobs[0].w_dtype,
                "%s: batched jobs must share groups, rows, cols and dtype", what);
-    ws.b.job[i] = WeightQuantArgs{jb.w, jb.w_dtype == FM_DTYPE_F32, jb.ld_w, jb.gs_w, jb.kind,
+    ws.b.job[i] = WeightQuantArgs{jb.w, jb.w_dtype == FM_DTYPE_F32, jb.ld_w, jb.gs_w, jb.kind & ~FM_ROWS_PAIRED,
                                   static_cast<uint8_t*>(jb.q), jb.ld_q, jb.gs_q, jb.q_row_off, jb.s, jb.ld_s,
                                   jb.gs_s, static_cast<uint8_t*>(jb.qt), jb.ld_qt, jb.gs_qt, jb.qt_col_off,
-                                  jb.st, jb.ld_st, jb.gs_st};
+                                  jb.st, jb.ld_st, jb.gs_st, (jb.kind & FM_ROWS_PAIRED) != 0};
   }
   ws.b.groups = jobs[0].groups;
   ws.tiles_x = jobs[0].cols / 128;
@@ -366,7 +366,8 @@ int check_weight_job(const FmWeightJob& jb) {
   const void* w = jb.w;
   const int w_dtype = jb.w_dtype;
   const int64_t groups = jb.groups, rows = jb.rows, cols = jb.cols, ld_w = jb.ld_w, gs_w = jb.gs_w;
-  const int kind = jb.kind;
+  const int kind = jb.kind & ~FM_ROWS_PAIRED;
+  const bool paired = (jb.kind & FM_ROWS_PAIRED) != 0;
   const void *q = jb.q, *qt = jb.qt;
   const float *s = jb.s, *st = jb.st;
   const int64_t ld_q = jb.ld_q, q_row_off = jb.q_row_off, ld_qt = jb.ld_qt, qt_col_off = jb.qt_col_off;
@@ -387,6 +388,9 @@ int check_weight_job(const FmWeightJob& jb) {
     FM_REQUIRE(qt == nullptr || ld_qt % 16 == 0, "fm_quantize_weight: transposed pitch must be a multiple of 16");
   }
   FM_REQUIRE(ld_w % 8 == 0 && gs_w % 8 == 0, "fm_quantize_weight: source pitch must be a multiple of 8");
+  FM_REQUIRE(!paired || (kind != QK_BF16 && ld_q % 64 == 0 && jb.gs_q % (2 * ld_q) == 0),
+             "fm_quantize_weight: paired rows need an e4m3 kind, a pitch that is a multiple of 64 and a group "
+             "stride of whole row pairs");
   return 0;
 }
 }  // namespace fm

@@ -53,6 +53,8 @@ struct TileOut {
   int64_t ld_col_s;
   int64_t col_off[2];    // output column offset of source value 0 / 1
   const int32_t* tile_valid;  // optional: skip 128-row tile t when tile_valid[t] < 0
+  int paired;            // e4m3 row output in the paired-row layout (FM_ROWS_PAIRED)
+  int col_paired;        // e4m3 transposed output in the paired-row layout (FM_COLS_PAIRED)
 };
 
 constexpr int kTileLdsPitch = 129;
@@ -165,14 +167,23 @@ constexpr int kRowsPerThread = 4;
 // Row-output addresses of one thread for one output: segment 0 of its row
 // and the scale of that row block (MX: of segment 0's 32-column block);
 // segment 1 is 64 columns (two MX blocks) further.  next() moves 32 rows down.
+// In the paired-row layout (e4m3 only) row r's 64-column piece b sits at
+// (r >> 1) * 2 ld + b * 128 + (r & 1) * 64, so segment 1 is 128 bytes on and
+// 32 rows down is still 32 ld bytes on.
 template <int KIND>
 struct RowPtr {
   uintptr_t q, s;
-  int64_t q_step, s_step, s_seg;
+  int64_t q_step, s_step, s_seg, q_seg;
   __device__ __forceinline__ RowPtr(const TileOut& o, int64_t row, int64_t ocol) {
     constexpr int64_t qb = KIND == QK_BF16 ? 2 : 1;
     const int64_t c = ocol + 8 * (threadIdx.x & 7);
-    q = uintptr_t(o.row_q) + uintptr_t((row * o.ld_row + c) * qb);
+    if (KIND != QK_BF16 && o.paired) {
+      q = uintptr_t(o.row_q) + uintptr_t((row >> 1) * 2 * o.ld_row + (c >> 6) * 128 + (row & 1) * 64 + (c & 63));
+      q_seg = 128;
+    } else {
+      q = uintptr_t(o.row_q) + uintptr_t((row * o.ld_row + c) * qb);
+      q_seg = 64 * qb;
+    }
     q_step = 32 * o.ld_row * qb;
     if (KIND == QK_MX) {
       s = uintptr_t(o.row_s) + uintptr_t(row * o.rs_row + (c >> 5) * o.rs_kb);
@@ -184,7 +195,7 @@ struct RowPtr {
       s_seg = 0;
     }
   }
-  __device__ __forceinline__ uintptr_t qseg(int h) const { return q + uintptr_t(h * 64 * (KIND == QK_BF16 ? 2 : 1)); }
+  __device__ __forceinline__ uintptr_t qseg(int h) const { return q + uintptr_t(h * q_seg); }
   __device__ __forceinline__ void next() {
     q += q_step;
     s += s_step;
@@ -316,9 +327,11 @@ __device__ __forceinline__ int code_idx(int row, int cw) { return row * 33 + (cw
 // 128-byte row of the transpose.  `tx` maps the four codes of one word (one
 // row, four columns) to their values in the transposed output; the identity
 // when the codes are already in the column scale.
+// `paired`: the transposed output in the paired-row layout (its rows -- the
+// source columns -- 2p and 2p + 1 interleaved in 64-byte pieces).
 template <class TX>
 __device__ __forceinline__ void store_transposed_codes(const uint32_t* code, uint8_t* qt8, int64_t ld_col,
-                                                       int64_t ocol, int64_t row0, TX tx) {
+                                                       int64_t ocol, int64_t row0, TX tx, bool paired = false) {
   const int tid = threadIdx.x;
   const int rg = tid & 7, cg = tid >> 3;
   uint32_t w[4][4];  // [column][4-row word]
@@ -335,9 +348,11 @@ __device__ __forceinline__ void store_transposed_codes(const uint32_t* code, uin
     for (int c4 = 0; c4 < 4; ++c4) w[c4][k] = out[c4];
   }
 #pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4)
-    *reinterpret_cast<uint4*>(qt8 + (ocol + 4 * cg + c4) * ld_col + row0 + 16 * rg) =
-        make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+  for (int c4 = 0; c4 < 4; ++c4) {
+    const int64_t f = ocol + 4 * cg + c4, t = row0 + 16 * rg;
+    const int64_t off = paired ? (f >> 1) * 2 * ld_col + (t >> 6) * 128 + (f & 1) * 64 + (t & 63) : f * ld_col + t;
+    *reinterpret_cast<uint4*>(qt8 + off) = make_uint4(w[c4][0], w[c4][1], w[c4][2], w[c4][3]);
+  }
 }
 
 // LDS word index of segment h of row r (this thread's two words) in a code tile
@@ -430,7 +445,8 @@ __device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int6
                              }
                              return enc_e4m3x4_inrange<HW>(d[0] * ratio, d[1] * ratio, d[2] * ratio,
                                                            d[3] * ratio);
-                           });
+                           },
+                           o.col_paired != 0);
     if ((tid & 7) == 0) {
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4)
@@ -525,7 +541,7 @@ __device__ __forceinline__ void block_tile(const Src& src, const TileOut& o, int
     }
     __syncthreads();
     store_transposed_codes(b_code, static_cast<uint8_t*>(o.col_q), o.ld_col, ocol, row0,
-                           [](uint32_t word, int) { return word; });
+                           [](uint32_t word, int) { return word; }, o.col_paired != 0);
   }
 }
 
@@ -606,7 +622,7 @@ __device__ __forceinline__ void mx_tile(const Src& src, const TileOut& o, int64_
 #pragma unroll
   for (int oi = 0; oi < NOUT; ++oi)
     store_transposed_codes(m_code[oi], static_cast<uint8_t*>(o.col_q), o.ld_col, col0 + o.col_off[oi], row0,
-                           [](uint32_t word, int) { return word; });
+                           [](uint32_t word, int) { return word; }, o.col_paired != 0);
 }
 
 // bf16 transposed outputs: fp32 values staged in LDS [128][129] (66 KiB),
@@ -716,8 +732,9 @@ inline TileOut make_tile_out(int kind, void* q, int64_t ld_q, void* s, int64_t l
                              int64_t ld_qt, void* st, int64_t ld_st, int64_t off0, int64_t off1,
                              const int32_t* tile_valid) {
   const bool kmajor = (kind & FM_SCALES_KMAJOR) != 0;
-  TileOut o{kind & ~FM_SCALES_KMAJOR, q, ld_q, s, kmajor ? 1 : ld_s, kmajor ? ld_s : 1,
-            qt, ld_qt, st, ld_st, {off0, off1}, tile_valid};
+  TileOut o{kind & ~(FM_SCALES_KMAJOR | FM_ROWS_PAIRED | FM_COLS_PAIRED), q, ld_q, s, kmajor ? 1 : ld_s,
+            kmajor ? ld_s : 1, qt, ld_qt, st, ld_st, {off0, off1}, tile_valid, (kind & FM_ROWS_PAIRED) != 0,
+            (kind & FM_COLS_PAIRED) != 0};
   return o;
 }
 
@@ -733,6 +750,8 @@ inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols, int nout
     FM_REQUIRE(o.ld_row >= span, "row output pitch %lld < columns %lld", (long long)o.ld_row,
                (long long)span);
     FM_REQUIRE(o.ld_row % 8 == 0, "row output pitch must be a multiple of 8");
+    FM_REQUIRE(!o.paired || (o.kind != QK_BF16 && o.ld_row % 64 == 0 && rows % 2 == 0),
+               "paired rows need an e4m3 kind, a row pitch that is a multiple of 64 and an even row count");
     if (o.kind != QK_BF16) {
       FM_REQUIRE(o.row_s != nullptr, "row scale output missing");
       const int64_t nblk = o.kind == QK_MX ? span / 32 : span / 128;
@@ -745,6 +764,8 @@ inline int check_tile_out(const TileOut& o, int64_t rows, int64_t cols, int nout
                (long long)rows);
     FM_REQUIRE(o.ld_col >= rows, "transposed output pitch too small");
     FM_REQUIRE(o.ld_col % 16 == 0, "transposed output pitch must be a multiple of 16");
+    FM_REQUIRE(!o.col_paired || (o.kind != QK_BF16 && o.ld_col % 64 == 0),
+               "paired transposed rows need an e4m3 kind and a pitch that is a multiple of 64");
     if (o.kind != QK_BF16) {
       FM_REQUIRE(o.col_s != nullptr, "transposed scale output missing");
       FM_REQUIRE(o.ld_col_s >= span, "transposed scale pitch too small");

@@ -60,6 +60,7 @@ struct WeightQuantArgs {
   int64_t ld_qt, gs_qt, qt_col_off;
   float* st;           // [G][C/128][./128]
   int64_t ld_st, gs_st;
+  int paired;          // e4m3 q in the paired-row layout (FM_ROWS_PAIRED)
 };
 
 // Tile (ty, tx) of group g; 256 threads.  Thread t loads rows rr + 16*i
@@ -154,9 +155,12 @@ __device__ __forceinline__ void weight_quant_tile(const WeightQuantArgs& a, int6
     for (int j = 0; j < 8; ++j) f[j] = pow2 ? v[i][j] * inv : div_rn(v[i][j], d);
     const uint32_t w0 = enc_e4m3x4_inrange<HW>(f[0], f[1], f[2], f[3]);
     const uint32_t w1 = enc_e4m3x4_inrange<HW>(f[4], f[5], f[6], f[7]);
-    if (a.q)
-      *reinterpret_cast<uint2*>(a.q + g * a.gs_q + (r0 + row + a.q_row_off) * a.ld_q + c0 + cc) =
-          make_uint2(w0, w1);
+    if (a.q) {
+      const int64_t r = r0 + row + a.q_row_off, c = c0 + cc;
+      const int64_t off = a.paired ? (r >> 1) * 2 * a.ld_q + (c >> 6) * 128 + (r & 1) * 64 + (c & 63)
+                                   : r * a.ld_q + c;
+      *reinterpret_cast<uint2*>(a.q + g * a.gs_q + off) = make_uint2(w0, w1);
+    }
     tile[row][(cc >> 2)] = w0;
     tile[row][(cc >> 2) + 1] = w1;
   }

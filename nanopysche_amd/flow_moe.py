@@ -48,6 +48,10 @@ class FP8Tensor:
     scale: torch.Tensor
     granularity: BlockScalingGranularity
     pow2: bool = False
+    # row blocks stored in the paired-row layout (rows 2p and 2p + 1
+    # interleaved in 64-byte pieces): a grouped-GEMM operand of the expert
+    # block, not a row-major payload
+    paired: bool = False
 
     @property
     def shape(self):
@@ -101,24 +105,30 @@ def _ld(t):
     return 0 if t is None else t.stride(0)
 
 
-def _tile_args(kind, q, s, qt, st):
+def _tile_args(kind, q, s, qt, st, paired=False, col_paired=False):
     """(kind, q, ld_q, s, ld_s, qt, ld_qt, st, ld_st) for the tile producers;
-    block-major row scales (a transposed view) add SCALES_KMAJOR to the kind."""
+    block-major row scales (a transposed view) add SCALES_KMAJOR to the kind,
+    ``paired`` / ``col_paired`` (e4m3 row / transposed output in the
+    paired-row layout) ROWS_PAIRED / COLS_PAIRED."""
     ld_s = _ld(s)
     if s is not None and s.stride(1) != 1:
         kind |= _lib.SCALES_KMAJOR
         ld_s = s.stride(1)
+    if paired:
+        kind |= _lib.ROWS_PAIRED
+    if col_paired:
+        kind |= _lib.COLS_PAIRED
     return (kind, _lib.ptr(q), _ld(q), _lib.ptr(s), ld_s, _lib.ptr(qt), _ld(qt), _lib.ptr(st), _ld(st))
 
 
-def _wrap(q, s, qt, st, kind):
+def _wrap(q, s, qt, st, kind, paired=False, col_paired=False):
     if kind == _lib.QUANT_BF16:
         return q, qt
     pow2 = kind == _lib.QUANT_POW2
     row_g = G.MX_1x32 if kind == _lib.QUANT_MX else G.ROW_1x128
     col_g = G.MX_32x1 if kind == _lib.QUANT_MX else G.COL_128x1
-    row = FP8Tensor(q, s, row_g, pow2) if q is not None else None
-    col = FP8Tensor(qt, st, col_g, pow2) if qt is not None else None
+    row = FP8Tensor(q, s, row_g, pow2, paired) if q is not None else None
+    col = FP8Tensor(qt, st, col_g, pow2, col_paired) if qt is not None else None
     return row, col
 
 
@@ -169,6 +179,8 @@ def quantize_to_fp8(x: torch.Tensor,
 
 def dequantize_from_fp8(t: FP8Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """decode(q) * scale, rounded once to ``out_dtype`` (bf16 or fp32)."""
+    if t.paired:
+        raise ValueError("a paired-row payload is a grouped-GEMM operand, not a row-major tensor")
     q, s = t.data, t.scale
     _lib.require_device(q, "data")
     R, C = q.shape
@@ -199,6 +211,8 @@ def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
     column scale is the largest of its row scales and every element is
     re-expressed as e4m3(decode(q) * s_row / s_col).  Exact for power-of-two
     scales (an exponent shift) unless the result is an e4m3 subnormal."""
+    if t.paired:
+        raise ValueError("a paired-row payload is a grouped-GEMM operand, not a row-major tensor")
     if BlockScalingGranularity(t.granularity) != G.ROW_1x128:
         raise ValueError("scaling_aware_transpose expects a ROW_1x128 tensor")
     q, s = t.data, t.scale
@@ -216,10 +230,11 @@ def scaling_aware_transpose(t: FP8Tensor) -> FP8Tensor:
 
 
 # ======================================================================= SwiGLU ====
-def _swiglu(g, u, rows, H, kind, row, col, dev, tile_valid=None, kmajor=False):
+def _swiglu(g, u, rows, H, kind, row, col, dev, tile_valid=None, kmajor=False, paired=False, col_paired=False):
     q, s, qt, st = _alloc_quant(rows, H, kind, row, col, dev, kmajor)
     _lib.call("fm_swiglu_quantize", _lib.ptr(g), g.stride(0), _lib.ptr(u), u.stride(0), rows, H,
-              *_tile_args(kind, q, s, qt, st), _lib.ptr(tile_valid), _lib.stream_of(g))
+              *_tile_args(kind, q, s, qt, st, paired, col_paired and col), _lib.ptr(tile_valid),
+              _lib.stream_of(g))
     return q, s, qt, st
 
 
@@ -277,7 +292,8 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
                       pow2_scale: bool = False, return_transpose: bool = False,
                       weights: Optional[torch.Tensor] = None,
                       fp8_gemm_threshold: int = 0, kmajor_scales: bool = False,
-                      tile_valid: Optional[torch.Tensor] = None) -> PermutedTokens:
+                      tile_valid: Optional[torch.Tensor] = None, paired_rows: bool = False,
+                      paired_cols: bool = False) -> PermutedTokens:
     """Gather the rows of ``x`` [T, D] (bf16) into expert order, each expert's
     group padded to 128 rows (zeros), and quantise them in the same pass.
     Rows past the last group (``plan.offsets[-1]`` up to ``plan.rows_max``)
@@ -290,7 +306,10 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
     view), the layout the grouped GEMM streams fastest.  ``tile_valid``
     [rows_max/128] int32 (default ``plan.tile_expert``): 128-row tiles with a
     negative entry are not written (``RoutingPlan.precision_tiles`` gives
-    each precision's tiles under the threshold split)."""
+    each precision's tiles under the threshold split).  ``paired_rows``
+    (e4m3 kinds) writes the row blocks in the paired-row layout that the
+    grouped GEMM streams in 64-deep half steps (``rows.paired``; a GEMM
+    operand only), ``paired_cols`` the transposed output likewise."""
     _lib.require_device(x, "x")
     if x.dtype != torch.bfloat16:
         raise TypeError("x must be bfloat16")
@@ -306,9 +325,10 @@ def fused_permute_pad(x: torch.Tensor, indices, num_experts: int, *,
     if weights is not None:
         w = weights.reshape(-1).to(torch.float32).contiguous()
     _lib.call("fm_permute", _lib.ptr(x2), T, D, x2.stride(0), _lib.ptr(plan.assign_of_row),
-              plan.rows_max, plan.top_k, _lib.ptr(w), *_tile_args(kind, q, s, qt, st),
+              plan.rows_max, plan.top_k, _lib.ptr(w),
+              *_tile_args(kind, q, s, qt, st, paired_rows, paired_cols and return_transpose),
               _lib.ptr(plan.tile_expert if tile_valid is None else tile_valid), _lib.stream_of(x2))
-    row, col = _wrap(q, s, qt, st, kind)
+    row, col = _wrap(q, s, qt, st, kind, paired_rows, paired_cols)
     return PermutedTokens(plan, row, col)
 
 
@@ -399,6 +419,7 @@ class ExpertWeightOperand:
     kmajor: bool = False
     data2: Optional[torch.Tensor] = None
     split: int = 0
+    paired: bool = False   # rows (K rows with kmajor) in the paired-row layout
 
     def operand(self):
         return _operand(self.data, self.scale, ld=self.ld, gs=self.gs, s_row=self.s_row,
@@ -425,8 +446,16 @@ def _timed(name, flops, fn):
 
 
 def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=None, want=1):
+    t_paired = getattr(tokens, "paired", False)
+    if (w.paired and not w.kmajor) and not t_paired:
+        raise ValueError("paired-row weights need paired-row tokens")
+
     def launch():
         gk = _gemm_kind(kind) | (_lib.GEMM_W_KMAJOR if w.kmajor else 0)
+        if t_paired:
+            gk |= _lib.GEMM_PAIRED | (_lib.GEMM_W_PAIRED if w.kmajor and w.paired else 0)
+        elif w.paired:
+            raise ValueError("paired-row weights need paired-row tokens")
         _lib.call("fm_grouped_gemm_ragged_m", gk, _token_operand(tokens, kind),
                   w.operand(), plan.m_tiles, _lib.ptr(plan.tile_expert), _lib.ptr(plan.offsets),
                   plan.num_experts, w.N, w.K,
@@ -486,6 +515,11 @@ def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out
     walked fastest (GEMM_A_FAST: fetched from memory once); by default b_t's."""
     S = _k_splits(kind, plan, M, N, out.device) if may_split else 1
     gk = _gemm_kind(kind) | (_lib.GEMM_A_FAST if a_cold else 0)
+    pa, pb = getattr(a_t, "paired", False), getattr(b_t, "paired", False)
+    if pa != pb or (pa and (S > 1 or mask is not None)):
+        raise ValueError("paired-row weight-gradient operands: both paired, unsplit and unmasked")
+    if pa:
+        gk |= _lib.GEMM_PAIRED
     ws = None
     if S > 1:
         nbytes = int(_lib.load().fm_grouped_gemm_ragged_k_split_workspace_bytes(plan.num_experts, M, N, S))
@@ -519,6 +553,11 @@ def _gemm_mk(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, a_t, 
     b_t, plan, M2, N2, out2, out2_gs) as one grid: the weight-gradient tiles
     fill the last round of the dgrad's."""
     gk = (_gemm_kind(kind) | (_lib.GEMM_W_KMAJOR if w.kmajor else 0) | (_lib.GEMM_A_FAST if a_cold else 0))
+    flags = {getattr(tokens, "paired", False), w.paired, getattr(a_t, "paired", False), getattr(b_t, "paired", False)}
+    if len(flags) != 1:
+        raise ValueError("fm_grouped_gemm_ragged_m_k: every operand paired or none")
+    if w.paired:
+        gk |= _lib.GEMM_PAIRED
 
     def launch():
         _lib.call("fm_grouped_gemm_ragged_m_k", gk, _token_operand(tokens, kind), w.operand(), plan.m_tiles,
@@ -586,13 +625,24 @@ class ExpertWeights:
     the bytes."""
 
     KMAJOR = True   # class switch: build the transposed copies instead (for comparisons)
+    PAIRED = True   # class switch: the expert block's pow2 operands in row-major layout (for comparisons)
 
     @staticmethod
     def kmajor_ok(kind: int, E: int, H: int, D: int) -> bool:
         return (ExpertWeights.KMAJOR and kind == _lib.QUANT_POW2 and E <= 64 and D % 256 == 0 and H >= 256)
 
-    def __init__(self, kind: int):
+    @staticmethod
+    def paired_ok(kind: int, E: int, H: int, D: int) -> bool:
+        """The [K][N] build with paired gate|up rows, and every ragged-M GEMM of
+        the block at least 384 deep (the paired kernel's ring of half steps)."""
+        return ExpertWeights.PAIRED and ExpertWeights.kmajor_ok(kind, E, H, D) and D >= 384 and H >= 384
+
+    def __init__(self, kind: int, paired: bool = False):
+        """``paired``: in the [K][N] (kmajor) build, w13 and w2 (and w13t,
+        w2t, the same bytes) are written in the paired-row layout; the expert
+        block pairs its token operands to match (``paired_ok``)."""
         self.kind = kind
+        self.paired = paired
         self.key = None
         self.has_dgrad = False
         self._defer = None
@@ -646,7 +696,7 @@ class ExpertWeights:
             self._build_mx(w1, w2, w3, E, H, D, dgrad)
             return
         if self.kmajor_ok(kind, E, H, D):
-            self._build_kmajor(w1, w2, w3, E, H, D)
+            self._build_kmajor(w1, w2, w3, E, H, D, self.paired and self.paired_ok(kind, E, H, D))
             return
         if self.views_ok(kind, E, H, D, (w1, w2, w3)):
             self._build_bf16_views(w1, w2, w3, E, H, D, dgrad)
@@ -690,9 +740,11 @@ class ExpertWeights:
                                             (D // 128) * (2 * H // 128), sh, D, 2 * H)
             self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, (H // 128) * (D // 128), sh, H, D)
 
-    def _build_kmajor(self, w1, w2, w3, E, H, D):
+    def _build_kmajor(self, w1, w2, w3, E, H, D, paired=False):
         """Row operands only (one launch over w1, w3, w2); the down and dX GEMMs
-        read them as [K][N] weights.  Forward and dgrad operands together."""
+        read them as [K][N] weights.  Forward and dgrad operands together.
+        ``paired``: w13 and w2 in the paired-row layout (the down and dX
+        GEMMs read them as paired [K][N] weights)."""
         dev = w1.device
         W13 = torch.empty(E, 2 * H, D, dtype=torch.uint8, device=dev)
         W2 = torch.empty(E, H, D, dtype=torch.uint8, device=dev)
@@ -703,23 +755,25 @@ class ExpertWeights:
             srcs = [w.float() for w in srcs]
         kind = self.kind
 
-        def job(src, dst, s, row_off, rows_out):
+        def job(src, dst, s, row_off, rows_out, pair=False):
             return _lib.FmWeightJob(
-                _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind,
+                _lib.ptr(src), _src_dtype(src), E, H, D, D, H * D, kind | (_lib.ROWS_PAIRED if pair else 0),
                 _lib.ptr(dst), D, rows_out * D, row_off, _lib.ptr(s), D // 128, (rows_out // 128) * (D // 128),
                 None, 0, 0, 0, None, 0, 0)
 
-        jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, 0, 2 * H), job(srcs[1], W13, S13, H, 2 * H),
-                                      job(srcs[2], W2, S2, 0, H))
+        jobs = (_lib.FmWeightJob * 3)(job(srcs[0], W13, S13, 0, 2 * H, paired),
+                                      job(srcs[1], W13, S13, H, 2 * H, paired),
+                                      job(srcs[2], W2, S2, 0, H, paired))
         self._launch(jobs, 3, w1, srcs)
         sh = 7
         g13, g2 = (2 * H // 128) * (D // 128), (H // 128) * (D // 128)
-        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, g13, sh, 2 * H, D)
-        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, g2, sh, H, D)
+        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 128, 1, g13, sh, 2 * H, D, paired=paired)
+        self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 128, 1, g2, sh, H, D, paired=paired)
         # element (n = d, k) of the [K][N] reading: rows k, column d; scale
         # block (d >> 7, k >> 7) at s[(k >> 7) * D/128 + (d >> 7)]
-        self.w2t = ExpertWeightOperand(W2, S2, D, H * D, 1, D // 128, g2, sh, D, H, kmajor=True)
-        self.w13t = ExpertWeightOperand(W13, S13, D, 2 * H * D, 1, D // 128, g13, sh, D, 2 * H, kmajor=True)
+        self.w2t = ExpertWeightOperand(W2, S2, D, H * D, 1, D // 128, g2, sh, D, H, kmajor=True, paired=paired)
+        self.w13t = ExpertWeightOperand(W13, S13, D, 2 * H * D, 1, D // 128, g13, sh, D, 2 * H, kmajor=True,
+                                        paired=paired)
         self.has_dgrad = True
 
     @staticmethod
@@ -879,8 +933,22 @@ class FP8FlowMoECompute:
     def _weights(self, kind: int, need_dgrad: bool = True, defer: Optional[list] = None) -> ExpertWeights:
         ew = self._cache.get(kind)
         if ew is None:
-            ew = self._cache[kind] = ExpertWeights(kind)
+            ew = self._cache[kind] = ExpertWeights(kind, paired=True)
         return ew.refresh(*self._w, self.num_experts, need_dgrad, defer)
+
+    def _paired(self, kind) -> bool:
+        """The block's pow2 row operands (tokens, weights) in the paired-row
+        layout: every ragged-M GEMM takes the ring kernel."""
+        return ExpertWeights.paired_ok(kind, self.num_experts, self.hidden_size, self.d_model)
+
+    def _paired_cols(self, kind, plan, mask) -> bool:
+        """The column operands of the weight gradients paired too: the ring
+        kernel's ragged-K walk takes no expert mask and no K split."""
+        if not self._paired(kind) or mask is not None:
+            return False
+        H, D = self.hidden_size, self.d_model
+        dev = plan.offsets.device
+        return _k_splits(kind, plan, 2 * H, D, dev) == 1 and _k_splits(kind, plan, H, D, dev) == 1
 
     def modes(self, num_assignments: int):
         """Which GEMM families run: (fp8_kind or None, bf16 bool), decided on
@@ -962,13 +1030,15 @@ class FP8FlowMoECompute:
         if mask is not None:
             tiles[fp8_kind], tiles[_lib.QUANT_BF16] = plan.precision_tiles()
         saved = {}
+        pcols = {k: self._paired_cols(k, plan, mask) for k in kinds}
         for kind, want in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)):
             if kind is None:
                 continue
             ew = ews[kind]
             pt = fused_permute_pad(x, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                    return_transpose=self._record, kmajor_scales=True,
-                                   tile_valid=tiles.get(kind, plan.tile_expert))
+                                   tile_valid=tiles.get(kind, plan.tile_expert), paired_rows=self._paired(kind),
+                                   paired_cols=pcols.get(kind, False))
             _gemm_m(kind, pt.rows, ew.w13, plan, GU, mask, want)
             saved[kind] = (pt.rows_t, ew)
         h_cols = {}
@@ -976,9 +1046,11 @@ class FP8FlowMoECompute:
             if kind is None:
                 continue
             # row blocks feed the down GEMM; the column blocks are kept for dW2
+            pr = self._paired(kind)
+            pc = pcols[kind]
             q, s, qt, st = _swiglu(GU[:, :H], GU[:, H:], R, H, kind, True, self._record, dev,
-                                   tiles.get(kind, plan.tile_expert), kmajor=True)
-            hrow, hcol = _wrap(q, s, qt, st, kind)
+                                   tiles.get(kind, plan.tile_expert), kmajor=True, paired=pr, col_paired=pc)
+            hrow, hcol = _wrap(q, s, qt, st, kind, pr, pc)
             h_cols[kind] = hcol
             _gemm_m(kind, hrow, saved[kind][1].w2t, plan, Y, mask, want)
         if self._dense:
@@ -992,6 +1064,7 @@ class FP8FlowMoECompute:
         ctx.compute = self
         ctx.plan = plan
         ctx.tiles = tiles
+        ctx.pcols = pcols
         ctx.kinds = (fp8_kind, use_bf16)
         ctx.saved_cols = {k: v[0] for k, v in saved.items()}
         # the dgrad weight operands of this forward's weights (a later forward
@@ -1054,9 +1127,11 @@ class FP8FlowMoECompute:
             raise TypeError("expert weights must be float32 or bfloat16 (w1 and w3 alike)")
         runs = [(k, w) for k, w in ((fp8_kind, 1), (_lib.QUANT_BF16 if use_bf16 else None, 0)) if k is not None]
         tiles = ctx.tiles
+        pcols = ctx.pcols
         dy = {kind: fused_permute_pad(dO, plan, E, granularity=_gran(kind), pow2_scale=kind == _lib.QUANT_POW2,
                                       return_transpose=True, weights=None if self._dense else wts,
-                                      kmajor_scales=True, tile_valid=tiles.get(kind, plan.tile_expert))
+                                      kmajor_scales=True, tile_valid=tiles.get(kind, plan.tile_expert),
+                                      paired_rows=self._paired(kind), paired_cols=pcols.get(kind, False))
               for kind, _ in runs}
         # dH and dW2 (contraction over each expert's tokens) both read the
         # permuted dY: each alone leaves its last round of workgroups
@@ -1068,7 +1143,9 @@ class FP8FlowMoECompute:
         # CUs it leaves idle run the main stream).  The forward's saved SwiGLU
         # columns are dW2's operand not in cache.
         fill = E * -(-H // 256) * -(-D // 256) >= _cus(dev)
-        one_grid = [(k, w) for k, w in runs if k in _MK_KINDS and fill]
+        # (paired row operands share a grid only with paired column operands)
+        one_grid = [(k, w) for k, w in runs
+                    if k in _MK_KINDS and fill and (not self._paired(k) or pcols.get(k, False))]
         two_streams = [(k, w) for k, w in runs if (k, w) not in one_grid]
         if two_streams:
             side.wait_stream(main)
@@ -1086,11 +1163,13 @@ class FP8FlowMoECompute:
         if self.capture_intermediates is not None:
             self.capture_intermediates["dh"] = dH.detach().clone()
         for kind, want in runs:
+            pr = self._paired(kind)
+            pc = pcols.get(kind, False)
             gq, gs, gqt, gst = _alloc_quant(R, 2 * H, kind, True, True, dev, kmajor=True)
             _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
-                      _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst),
+                      _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(kind, gq, gs, gqt, gst, pr, pc),
                       _lib.ptr(tiles.get(kind, plan.tile_expert)), _lib.stream_of(GU))
-            dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind)
+            dgu_row, dgu_col = _wrap(gq, gs, gqt, gst, kind, pr, pc)
             # dW1 | dW3: contraction over each expert's tokens
             _gemm_k(kind, dgu_col, ctx.saved_cols[kind], plan, 2 * H, D, dW1, H * D, dW3, H * D, split=H,
                     mask=mask, want=want)
