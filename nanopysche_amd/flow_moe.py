@@ -445,6 +445,16 @@ def _timed(name, flops, fn):
         GEMM_TIMER(name, flops, fn)
 
 
+def _assignments(plan: RoutingPlan, mask, want) -> float:
+    """Assignments a launch computes: all of them, or with an expert mask those
+    of the experts it selects (read back from the device: only when a GEMM
+    timer asks for the launch's FLOPs)."""
+    if mask is None or GEMM_TIMER is None:
+        return float(plan.num_tokens * plan.top_k)
+    sel = (mask == want).to(torch.int64)
+    return float((plan.counts.to(torch.int64) * sel).sum().item())
+
+
 def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=None, want=1):
     t_paired = getattr(tokens, "paired", False)
     if (w.paired and not w.kmajor) and not t_paired:
@@ -461,8 +471,7 @@ def _gemm_m(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, mask=N
                   plan.num_experts, w.N, w.K,
                   _lib.ptr(mask), want, _lib.ptr(out), _dt(out), out.stride(0), _lib.stream_of(out))
 
-    _timed(f"grouped_gemm_ragged_m/{_KIND_NAME[kind]}",
-           2.0 * plan.num_tokens * plan.top_k * w.N * w.K, launch)
+    _timed(f"grouped_gemm_ragged_m/{_KIND_NAME[kind]}", 2.0 * _assignments(plan, mask, want) * w.N * w.K, launch)
 
 
 # Model of a ragged-K launch for choosing its K split: ~1.3 us per 128-deep K
@@ -538,8 +547,7 @@ def _gemm_k(kind, a_t, b_t, plan: RoutingPlan, M, N, out, out_gs, out2=None, out
                       M if split is None else split, _dt(out), N, S, _lib.ptr(ws), ws.numel() * 4,
                       _lib.stream_of(out))
 
-    _timed(f"grouped_gemm_ragged_k/{_KIND_NAME[kind]}",
-           2.0 * plan.num_tokens * plan.top_k * M * N, launch)
+    _timed(f"grouped_gemm_ragged_k/{_KIND_NAME[kind]}", 2.0 * _assignments(plan, mask, want) * M * N, launch)
 
 
 # Kinds whose dgrad and weight-gradient launches can share one grid
@@ -567,7 +575,7 @@ def _gemm_mk(kind, tokens, w: ExpertWeightOperand, plan: RoutingPlan, out, a_t, 
                   _lib.stream_of(out))
 
     _timed(f"grouped_gemm_ragged_m_k/{_KIND_NAME[kind]}",
-           2.0 * plan.num_tokens * plan.top_k * (w.N * w.K + M2 * N2), launch)
+           2.0 * _assignments(plan, mask, want) * (w.N * w.K + M2 * N2), launch)
 
 
 def _dt(t):
