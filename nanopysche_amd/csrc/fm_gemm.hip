@@ -1722,10 +1722,21 @@ __global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmPara
 // Fragments, scales and the MFMA order are those of gemm256p_kernel, so the
 // results are bit-identical.
 constexpr int kSlotOp = kT * 64;   // one operand, one 64-deep half step
+// pow2: each slot holds both operands and, with an even half, the step's
+// scales (one fp32 per row and operand).  MX: the slots hold operands only;
+// a step's e8m0 scales (4 bytes per row and operand: both halves' blocks) go
+// to a ring of three 2 KiB scale slots after them, step t's in slot t % 3, so
+// an odd half still finds its step's scales after the even half's slot has
+// been refilled.
+template <int KIND>
 struct SmemR {
-  static constexpr int kS = kT * 4;   // pow2 scales of one operand, one step
-  static constexpr int kP = kSlotOp, kQS = 2 * kSlotOp, kPS = 2 * kSlotOp + kS;
-  static constexpr int kSlot = 2 * kSlotOp + 2 * kS;
+  static constexpr bool kMX = KIND == GK_FP8_MX;
+  static constexpr int kS = kT * 4;   // scales of one operand, one step
+  static constexpr int kP = kSlotOp;
+  static constexpr int kSlot = 2 * kSlotOp + (kMX ? 0 : 2 * kS);
+  static constexpr int kQS = kMX ? 0 : 2 * kSlotOp, kPS = kQS + kS;   // in the slot (pow2) / scale slot (MX)
+  static constexpr int kScaleBase = 4 * kSlot, kScaleSlot = 2 * kS;
+  static constexpr int kBytes = 4 * kSlot + (kMX ? 3 * kScaleSlot : 0);
 };
 
 // Row r of a paired slot operand: 64 bytes at r * 64, 16-byte chunk c at
@@ -1801,7 +1812,7 @@ struct RingStreams {
   ScaleSrc sc;
 };
 
-template <bool QNN, bool QP>
+template <int KIND, bool QNN, bool QP>
 __device__ __forceinline__ RingStreams ring_streams(const Operand& Q, const Operand& P, int64_t n_i, const TileP& t,
                                                    const WaveCoord& w) {
   RingStreams s;
@@ -1824,8 +1835,8 @@ __device__ __forceinline__ RingStreams ring_streams(const Operand& Q, const Oper
   so.s_kb = wq ? Q.s_kb : P.s_kb;
   so.s_gs = wq ? Q.s_gs : P.s_gs;
   so.s_shift = wq ? Q.s_shift : P.s_shift;
-  s.sc = make_scale_src<GK_FP8_POW2>(so, wq ? int64_t(t.i0) : int64_t(t.j0), wq ? q_rows : p_rows, wq ? t.e : 0,
-                                     false, li, wq ? SmemR::kQS : SmemR::kPS);
+  s.sc = make_scale_src<KIND>(so, wq ? int64_t(t.i0) : int64_t(t.j0), wq ? q_rows : p_rows, wq ? t.e : 0,
+                              wq ? w.q_mx_k : w.p_mx_k, li, wq ? SmemR<KIND>::kQS : SmemR<KIND>::kPS);
   return s;
 }
 
@@ -1841,41 +1852,55 @@ __device__ __forceinline__ v4i uniform_rsrc(v4i r) {
 }
 
 // Piece u of half j's DMA: u = 0..3 the operand groups (even: Q group u / 2,
-// odd: P group u / 2), u = 4 the step's scale dword (even halves only).
-__device__ __forceinline__ void issue_piece_r(int u, const RingStreams& S, int64_t j, uint32_t dst, int wave) {
+// odd: P group u / 2), u = 4 the step's scale dword (even halves only) into
+// `sdst` (the slot for pow2, the step's scale slot for MX).
+__device__ __forceinline__ void issue_piece_r(int u, const RingStreams& S, int64_t j, uint32_t dst, uint32_t sdst,
+                                              int wave) {
   const int g = u >> 1;
   if (u == 4) {
-    bdma4(uniform_rsrc(S.sc.rsrc), S.sc.voff, __builtin_amdgcn_readfirstlane(uint32_t(j >> 1) * S.sc.k), dst + S.sc.dst);
+    bdma4(uniform_rsrc(S.sc.rsrc), S.sc.voff, __builtin_amdgcn_readfirstlane(uint32_t(j >> 1) * S.sc.k),
+          sdst + S.sc.dst);
   } else if (u & 1) {
     const uint32_t soff = __builtin_amdgcn_readfirstlane(g * S.p.group_bytes + uint32_t(j) * S.p.k_half_bytes);
-    bdma16(uniform_rsrc(S.p.rsrc), S.p.lane_off[g], soff, dst + SmemR::kP + (wave * 2 + g) * 1024);
+    bdma16(uniform_rsrc(S.p.rsrc), S.p.lane_off[g], soff, dst + kSlotOp + (wave * 2 + g) * 1024);
   } else {
     const uint32_t soff = __builtin_amdgcn_readfirstlane(g * S.q.group_bytes + uint32_t(j) * S.q.k_half_bytes);
     bdma16(uniform_rsrc(S.q.rsrc), S.q.lane_off[g], soff, dst + (wave * 2 + g) * 1024);
   }
 }
 
-// Reads the fragments of the half in slot `st` into f (with the step's
-// scales when `scales`), with half j's DMA pieces placed between the reads.
-// EVEN: half j is even (its DMA carries the step's scale dword); the parity
-// is a template argument so the loop body stays one basic block.
-template <bool QNN, bool EVEN>
-__device__ __forceinline__ void issue_read_r(const RingStreams& S, int64_t j, uint32_t dst, int wave,
-                                             const uint8_t* st, bool scales, Frag<GK_FP8_POW2>& f,
+// Reads the fragments of the half in slot `st` into f, with half j's DMA
+// pieces placed between the reads.  EVEN: half j is even (its DMA carries the
+// step's scale dword); the parity is a template argument so the loop body
+// stays one basic block.  Scales of the half read (the other parity): pow2
+// with `scales` (an even half) from the slot; MX always, from the scale slot
+// `sst`, blocks 2 RODD + (0, 1) of the step.
+template <int KIND, bool QNN, bool EVEN>
+__device__ __forceinline__ void issue_read_r(const RingStreams& S, int64_t j, uint32_t dst, uint32_t sdst, int wave,
+                                             const uint8_t* st, const uint8_t* sst, bool scales, Frag<KIND>& f,
                                              const WaveCoord& w) {
-  if (scales) {
-    f.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
+  using SM = SmemR<KIND>;
+  if constexpr (KIND == GK_FP8_MX) {
+    constexpr int rodd = EVEN ? 1 : 0;   // the half read has the other parity
+    const int blk = 2 * rodd + w.lhalf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.sa[t] = read_mx_scale(sst, SM::kQS, w.wi * 128 + t * 32 + w.lrow, blk, w.q_mx_k);
+      if (t < 2) f.sb[t] = read_mx_scale(sst, SM::kPS, w.wj * 64 + t * 32 + w.lrow, blk, w.p_mx_k);
+    }
+  } else if (scales) {
+    f.sa[0] = read_pow2_scales(st, SM::kQS, w.wi * 128, w.lrow);
     const uint2 v = *reinterpret_cast<const uint2*>(
-        st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+        st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
     f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
   }
-  if constexpr (EVEN) issue_piece_r(4, S, j, dst, wave);
+  if constexpr (EVEN) issue_piece_r(4, S, j, dst, sdst, wave);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     if constexpr (QNN) f.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
     else f.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
-    issue_piece_r(t, S, j, dst, wave);
-    if (t < 2) f.b[t] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
+    issue_piece_r(t, S, j, dst, sdst, wave);
+    if (t < 2) f.b[t] = read_frag8_pr(st + kSlotOp, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
   }
 }
 
@@ -1905,15 +1930,17 @@ __device__ __forceinline__ bool rk_next_min(const RkQueue& q, int& c, TileK& t, 
 // last four refills of a tile fetch the next tile's first four halves;
 // ragged-K tiles of fewer than three K steps come last, one at a time.  No
 // expert masks, at most 64 experts, ragged-M K >= 384 (the launcher).
-template <bool HAS_M, bool HAS_K, bool QNN, bool QP>
+template <int KIND, int MXL, bool HAS_M, bool HAS_K, bool QNN, bool QP>
 __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams pk) {
   static_assert(!(HAS_K && QNN), "ragged-K tiles share the NT fragment reads");
-  constexpr int KIND = GK_FP8_POW2;
+  static_assert(KIND == GK_FP8_POW2 || (KIND == GK_FP8_MX && !QNN), "pow2, or MX with [N][K] weights");
+  using SM = SmemR<KIND>;
+  constexpr bool MX = KIND == GK_FP8_MX;
   constexpr int kSpare = 8 * 2048;   // epilogue staging, 2 KiB per wave
   constexpr int kQueue = 1024;       // ragged-M tile queue
   constexpr int kOff = 512;          // ragged-K offsets copy
   constexpr int kArgs = (sizeof(GemmParams) + 15) / 16 * 16;
-  constexpr int kBase = 4 * SmemR::kSlot;
+  constexpr int kBase = SM::kBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kBase + kSpare + kQueue + kOff + 2 * kArgs];
   int* const qlds = reinterpret_cast<int*>(smem + kBase + kSpare);
   int* const off = reinterpret_cast<int*>(smem + kBase + kSpare + kQueue);
@@ -1931,7 +1958,8 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
   w.wj = w.wave & 3;
   w.lrow = w.lane & 31;
   w.lhalf = w.lane >> 5;
-  w.q_mx_k = w.p_mx_k = false;
+  w.q_mx_k = MX && (MXL & 1) != 0;
+  w.p_mx_k = MX && (MXL & 2) != 0;
 
   TileQueue tq;
   if constexpr (HAS_M) tile_queue_init(pm, tq, qlds);
@@ -1996,10 +2024,10 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
   auto streams = [&](const ItemR& it) -> RingStreams {
     if (HAS_K && (!HAS_M || it.k_mode)) {
       const Operand Q = uniform_operand(&plk->Q), P = uniform_operand(&plk->P);
-      return ring_streams<false, true>(Q, P, rfl64(plk->n_i), TileP{0, it.i0, it.j0, int(rfl64(plk->n_j))}, w);
+      return ring_streams<KIND, false, true>(Q, P, rfl64(plk->n_i), TileP{0, it.i0, it.j0, int(rfl64(plk->n_j))}, w);
     }
     const Operand Q = uniform_operand(&plm->Q), P = uniform_operand(&plm->P);
-    return ring_streams<QNN, QP>(Q, P, rfl64(plm->n_i), TileP{it.e, it.i0, it.j0, it.j_end}, w);
+    return ring_streams<KIND, QNN, QP>(Q, P, rfl64(plm->n_i), TileP{it.e, it.i0, it.j0, it.j_end}, w);
   };
   const uint32_t smem_lds = lds_addr(smem);
   uint8_t* const W = smem + kBase + w.wave * 2048;
@@ -2047,8 +2075,51 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
   };
-  auto slot = [&](int g) { return smem + (g & 3) * SmemR::kSlot; };
-  auto slot_lds = [&](int g) { return smem_lds + uint32_t(g & 3) * SmemR::kSlot; };
+  auto slot = [&](int g) { return smem + (g & 3) * SM::kSlot; };
+  auto slot_lds = [&](int g) { return smem_lds + uint32_t(g & 3) * SM::kSlot; };
+  // MX: step t's scales in scale slot t % 3 (pow2: in the even half's slot)
+  auto sslot = [&](int t3) { return smem + SM::kScaleBase + t3 * SM::kScaleSlot; };
+  auto sslot_lds = [&](int t3) { return smem_lds + uint32_t(SM::kScaleBase + t3 * SM::kScaleSlot); };
+  // the scale target of half g's DMA (its step's scale slot t3 for MX)
+  auto sdst = [&](int g, int t3) { return MX ? sslot_lds(t3) : slot_lds(g); };
+  // the fragments and scales of an even half (the step's first) in slot g
+  auto read_even = [&](int g, int t3, Frag<KIND>& f) {
+    const uint8_t* st = slot(g);
+    if constexpr (MX) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        f.sa[t] = read_mx_scale(sslot(t3), SM::kQS, w.wi * 128 + t * 32 + w.lrow, w.lhalf, w.q_mx_k);
+        if (t < 2) f.sb[t] = read_mx_scale(sslot(t3), SM::kPS, w.wj * 64 + t * 32 + w.lrow, w.lhalf, w.p_mx_k);
+      }
+    } else {
+      f.sa[0] = read_pow2_scales(st, SM::kQS, w.wi * 128, w.lrow);
+      const uint2 v = *reinterpret_cast<const uint2*>(
+          st + SM::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
+      f.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if constexpr (QNN) f.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
+      else f.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
+      if (t < 2) f.b[t] = read_frag8_pr(st + kSlotOp, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
+    }
+  };
+  // the odd half (its step's second) in slot g, scales from scale slot t3 (MX)
+  auto read_odd = [&](int g, int t3, Frag<KIND>& f) {
+    const uint8_t* st = slot(g);
+    if constexpr (MX) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        f.sa[t] = read_mx_scale(sslot(t3), SM::kQS, w.wi * 128 + t * 32 + w.lrow, 2 + w.lhalf, w.q_mx_k);
+        if (t < 2) f.sb[t] = read_mx_scale(sslot(t3), SM::kPS, w.wj * 64 + t * 32 + w.lrow, 2 + w.lhalf, w.p_mx_k);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
+      if (t < 2) f.b[t] = read_frag8_pr(st + kSlotOp, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
+    }
+  };
 
   Frag<KIND> f0, f1;   // f0: even halves (with the step's scales), f1: odd halves
   ItemR cur;
@@ -2058,52 +2129,48 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int v = 0; v < 5; ++v)
-        if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, cur.kh0 + u, slot_lds(u), w.wave);
+        if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, cur.kh0 + u, slot_lds(u), sdst(u, u >> 1), w.wave);
     }
     FM_WAIT_VMCNT(13);   // half 0 landed (halves 1-3: 4 + 5 + 4 pieces in flight)
     block_barrier();
-    {
-      const uint8_t* st = slot(0);
-      f0.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
-      const uint2 v = *reinterpret_cast<const uint2*>(
-          st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
-      f0.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if constexpr (QNN) f0.a[t] = read_frag8_nn(st, w.wi * 128 + t * 32, 0, w.lane);
-        else f0.a[t] = read_frag8_pr(st, w.wi * 128 + t * 32 + w.lrow, w.lhalf);
-        if (t < 2) f0.b[t] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + t * 32 + w.lrow, w.lhalf);
-      }
-    }
+    read_even(0, 0, f0);
     int gs = 0;   // ring slot of the current even half (0 or 2)
+    int ss = 0;   // MX: scale slot of the current step (0, 1, 2)
     for (;;) {
       ItemR nxt;
       const bool has_next = next_item(nxt);
       v16f acc[4][2];
       zero(acc);
       // Two half steps: the even half's MFMAs (f0) while the odd half is read
-      // into f1 and absolute half jn (even) is issued into the even slot, then
-      // the odd half's MFMAs while the next even half is read into f0 and jn + 1
-      // is issued into the odd slot.  `drain`: the first pair after an
-      // epilogue, whose output stores count in vmcnt too, waits for everything.
+      // into f1 and absolute half jn (even; with the scales of two steps on)
+      // is issued into the even slot, then the odd half's MFMAs while the next
+      // even half is read into f0 and jn + 1 is issued into the odd slot.
+      // `drain`: the first pair after an epilogue, whose output stores count
+      // in vmcnt too, waits for everything.
       auto pair = [&](int64_t jn, auto drain) {
+        const int s2 = ss == 0 ? 2 : ss - 1, s1 = ss == 2 ? 0 : ss + 1;   // (ss + 2) % 3, (ss + 1) % 3
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (decltype(drain)::value) FM_WAIT_VMCNT(0);
         else FM_WAIT_VMCNT(9);   // the odd half landed (the two halves after it in flight)
         block_barrier();         // every wave has read the even half: its slot is free
-        issue_read_r<QNN, true>(S, jn, slot_lds(gs), w.wave, slot(gs + 1), false, f1, w);
-        f1.sa[0] = f0.sa[0];
-        f1.sb[0] = f0.sb[0];
+        issue_read_r<KIND, QNN, true>(S, jn, slot_lds(gs), sdst(gs, s2), w.wave, slot(gs + 1), sslot(ss), false,
+                                      f1, w);
+        if constexpr (!MX) {
+          f1.sa[0] = f0.sa[0];
+          f1.sb[0] = f0.sb[0];
+        }
         mma_half<KIND>(f0, acc);
         interleave_half<KIND, QNN>();
         __builtin_amdgcn_sched_barrier(0);
         FM_WAIT_VMCNT(9);
         block_barrier();
-        issue_read_r<QNN, false>(S, jn + 1, slot_lds(gs + 1), w.wave, slot(gs + 2), true, f0, w);
+        issue_read_r<KIND, QNN, false>(S, jn + 1, slot_lds(gs + 1), 0, w.wave, slot(gs + 2), sslot(s1), true,
+                                       f0, w);
         mma_half<KIND>(f1, acc);
         interleave_half<KIND, QNN>();
         __builtin_amdgcn_sched_barrier(0);
         gs = (gs + 2) & 3;
+        ss = s1;
       };
       const int nh = cur.nh;   // >= 6
       const int64_t kh0 = cur.kh0;
@@ -2138,25 +2205,15 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
         for (int u = 0; u < it.nh; ++u)
 #pragma unroll
           for (int v = 0; v < 5; ++v)
-            if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, it.kh0 + u, slot_lds(u), w.wave);
+            if (v < 4 || (u & 1) == 0) issue_piece_r(v, S, it.kh0 + u, slot_lds(u), sdst(u, u >> 1), w.wave);
         FM_WAIT_VMCNT(0);
         block_barrier();
         for (int u = 0; u < it.nh; u += 2) {
-          const uint8_t* st = slot(u);
-          f0.sa[0] = read_pow2_scales(st, SmemR::kQS, w.wi * 128, w.lrow);
-          const uint2 v = *reinterpret_cast<const uint2*>(
-              st + SmemR::kPS + ((w.wj >> 1) * 128 + w.lrow * 4 + 2 * (w.wj & 1)) * 4);
-          f0.sb[0] = pack_exp4(v.x, v.y, 0u, 0u);
-          f1.sa[0] = f0.sa[0];
-          f1.sb[0] = f0.sb[0];
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt) {
-            f0.a[tt] = read_frag8_pr(st, w.wi * 128 + tt * 32 + w.lrow, w.lhalf);
-            f1.a[tt] = read_frag8_pr(slot(u + 1), w.wi * 128 + tt * 32 + w.lrow, w.lhalf);
-            if (tt < 2) {
-              f0.b[tt] = read_frag8_pr(st + SmemR::kP, w.wj * 64 + tt * 32 + w.lrow, w.lhalf);
-              f1.b[tt] = read_frag8_pr(slot(u + 1) + SmemR::kP, w.wj * 64 + tt * 32 + w.lrow, w.lhalf);
-            }
+          read_even(u, u >> 1, f0);
+          read_odd(u + 1, u >> 1, f1);
+          if constexpr (!MX) {
+            f1.sa[0] = f0.sa[0];
+            f1.sb[0] = f0.sb[0];
           }
           mma_half<KIND>(f0, acc);
           mma_half<KIND>(f1, acc);
@@ -2510,9 +2567,11 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
       break;
     case GK_FP8_POW2:
       if (p.paired) {
-        if (p.q_nn && p.paired == 2) hipLaunchKernelGGL((gemm256r_kernel<true, false, true, true>), grid, block, 0, s, p, p);
-        else if (p.q_nn) hipLaunchKernelGGL((gemm256r_kernel<true, false, true, false>), grid, block, 0, s, p, p);
-        else hipLaunchKernelGGL((gemm256r_kernel<true, false, false, true>), grid, block, 0, s, p, p);
+        if (p.q_nn && p.paired == 2)
+          hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, true, false, true, true>), grid, block, 0, s, p, p);
+        else if (p.q_nn)
+          hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, true, false, true, false>), grid, block, 0, s, p, p);
+        else hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, true, false, false, true>), grid, block, 0, s, p, p);
       } else if (p.q_nn) {
         hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_POW2, 0, true>), grid, block, 0, s, p);
       } else {
@@ -2521,6 +2580,15 @@ inline void launch256p(int kind, const GemmParams& p, hipStream_t s) {
       break;
     default: {
       const int mxl = (p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0);
+      if (p.paired) {   // [N][K] weights and tokens paired
+        switch (mxl) {
+          case 0: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 0, true, false, false, true>), grid, block, 0, s, p, p); break;
+          case 1: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 1, true, false, false, true>), grid, block, 0, s, p, p); break;
+          case 2: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 2, true, false, false, true>), grid, block, 0, s, p, p); break;
+          default: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 3, true, false, false, true>), grid, block, 0, s, p, p); break;
+        }
+        break;
+      }
       switch (mxl) {
         case 0: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 0>), grid, block, 0, s, p); break;
         case 1: hipLaunchKernelGGL((gemm256p_kernel<GK_FP8_MX, 1>), grid, block, 0, s, p); break;
@@ -2616,7 +2684,16 @@ int dispatch_gemm(int kind, GemmParams p, hipStream_t s) {
     const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
     const int64_t want = (p.n_tiles + 7) / 8 * 8;
     const dim3 pgrid(unsigned(want < slots ? want : slots)), pblock(512);
-    hipLaunchKernelGGL((gemm256r_kernel<false, true, false, true>), pgrid, pblock, 0, s, p, p);
+    if (kind == GK_FP8_POW2) {
+      hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, false, true, false, true>), pgrid, pblock, 0, s, p, p);
+    } else {
+      switch ((p.Q.s_kb != 1 ? 1 : 0) | (p.P.s_kb != 1 ? 2 : 0)) {
+        case 0: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 0, false, true, false, true>), pgrid, pblock, 0, s, p, p); break;
+        case 1: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 1, false, true, false, true>), pgrid, pblock, 0, s, p, p); break;
+        case 2: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 2, false, true, false, true>), pgrid, pblock, 0, s, p, p); break;
+        default: hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_MX, 3, false, true, false, true>), pgrid, pblock, 0, s, p, p); break;
+      }
+    }
   } else if (MODE == GM_RAGGED_K && p.splits == 1 && p.mask == nullptr && p.E <= 64 &&
              p.n_tiles < (int64_t(1) << 28) && gemm_persistent_k()) {
     // (its tile walk counts in 32-bit integers)
@@ -2754,10 +2831,10 @@ int ragged_m_params(int kind, int nn, int paired, const FmGemmOperand* tokens, c
   FM_REQUIRE(out_dtype == FM_DTYPE_BF16 || out_dtype == FM_DTYPE_F32, "fm_grouped_gemm_ragged_m: bad out dtype");
   FM_REQUIRE(kind != GK_FP8_F32 || weights->scale_row_shift == 7,
              "fm_grouped_gemm_ragged_m: fp32-scaled weights must use 128-row scale blocks");
-  FM_REQUIRE(!paired || (kind == GK_FP8_POW2 && E <= 64 && K >= 384 && tokens->ld % 64 == 0 &&
-                         weights->data2 == nullptr && (nn || weights->ld % 64 == 0)),
-             "fm_grouped_gemm_ragged_m: paired-row operands need the pow2 kind, E <= 64, K >= 384, unsplit "
-             "weights and row pitches that are multiples of 64");
+  FM_REQUIRE(!paired || ((kind == GK_FP8_POW2 || (kind == GK_FP8_MX && !nn)) && E <= 64 && K >= 384 &&
+                         tokens->ld % 64 == 0 && weights->data2 == nullptr && (nn || weights->ld % 64 == 0)),
+             "fm_grouped_gemm_ragged_m: paired-row operands need the pow2 kind (or MX with [N][K] weights), "
+             "E <= 64, K >= 384, unsplit weights and row pitches that are multiples of 64");
   p = GemmParams{};
   p.m_tiles = m_tiles;
   if (m_tiles == 0) return 0;
@@ -2861,9 +2938,10 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
                                out2_gs, split_rows, out_dtype, ld_out, p))
     return rc;
   if (paired) {
-    FM_REQUIRE(kind == GK_FP8_POW2 && expert_mask == nullptr && E <= 64 && a_t->ld % 64 == 0 && b_t->ld % 64 == 0 &&
+    FM_REQUIRE((kind == GK_FP8_POW2 || kind == GK_FP8_MX) && expert_mask == nullptr && E <= 64 &&
+                   a_t->ld % 64 == 0 && b_t->ld % 64 == 0 &&
                    int64_t(E) * ((M + 255) / 256) * ((N + 255) / 256) < (int64_t(1) << 28),
-               "fm_grouped_gemm_ragged_k: paired-row operands need the pow2 kind, no expert mask, E <= 64, "
+               "fm_grouped_gemm_ragged_k: paired-row operands need the pow2 or MX kind, no expert mask, E <= 64, "
                "pitches that are multiples of 64 and fewer than 2^28 tiles");
     p.paired = 1;
   }
@@ -2903,8 +2981,8 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
     if (nbm + nbk == 0) return 0;
     const int64_t slots = int64_t(device_cus() / 8 > 0 ? device_cus() / 8 : 1) * 8;
     const dim3 pgrid(unsigned(nbm + nbk < slots ? nbm + nbk : slots)), pblock(512);
-    if (nbm == 0) hipLaunchKernelGGL((gemm256r_kernel<false, true, false, true>), pgrid, pblock, 0, s, pk, pk);
-    else hipLaunchKernelGGL((gemm256r_kernel<true, true, false, true>), pgrid, pblock, 0, s, pm, pk);
+    if (nbm == 0) hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, false, true, false, true>), pgrid, pblock, 0, s, pk, pk);
+    else hipLaunchKernelGGL((gemm256r_kernel<GK_FP8_POW2, 0, true, true, false, true>), pgrid, pblock, 0, s, pm, pk);
     return check_launch("fm_grouped_gemm_ragged_m_k");
   }
   if (nn || pm.m_tiles == 0 || (kind != GK_BF16 && kind != GK_FP8_POW2) || !gemm_mk_one_grid()) {

@@ -641,9 +641,15 @@ class ExpertWeights:
 
     @staticmethod
     def paired_ok(kind: int, E: int, H: int, D: int) -> bool:
-        """The [K][N] build with paired gate|up rows, and every ragged-M GEMM of
-        the block at least 384 deep (the paired kernel's ring of half steps)."""
-        return ExpertWeights.PAIRED and ExpertWeights.kmajor_ok(kind, E, H, D) and D >= 384 and H >= 384
+        """Paired-row weights and token operands: the pow2 [K][N] build or the
+        MX build (at most 64 experts, D and H multiples of 64), with every
+        ragged-M GEMM of the block at least 384 deep (the paired kernel's ring
+        of half steps)."""
+        if not ExpertWeights.PAIRED or D < 384 or H < 384:
+            return False
+        if kind == _lib.QUANT_MX:
+            return E <= 64 and D % 64 == 0 and H % 64 == 0
+        return ExpertWeights.kmajor_ok(kind, E, H, D)
 
     def __init__(self, kind: int, paired: bool = False):
         """``paired``: in the [K][N] (kmajor) build, w13 and w2 (and w13t,
@@ -701,7 +707,7 @@ class ExpertWeights:
         dev = w1.device
         kind = self.kind
         if kind == _lib.QUANT_MX:
-            self._build_mx(w1, w2, w3, E, H, D, dgrad)
+            self._build_mx(w1, w2, w3, E, H, D, dgrad, self.paired and self.paired_ok(kind, E, H, D))
             return
         if self.kmajor_ok(kind, E, H, D):
             self._build_kmajor(w1, w2, w3, E, H, D, self.paired and self.paired_ok(kind, E, H, D))
@@ -824,7 +830,11 @@ class ExpertWeights:
             self.w13t = (ExpertWeightOperand(w1, None, D, H * D, N=D, K=2 * H, kmajor=True, data2=w3, split=H)
                          if nn else ExpertWeightOperand(W13t, None, 2 * H, D * 2 * H, N=D, K=2 * H))
 
-    def _build_mx(self, w1, w2, w3, E, H, D, dgrad):
+    def _build_mx(self, w1, w2, w3, E, H, D, dgrad, paired=False):
+        """``paired``: every operand (rows and transposed outputs) in the
+        paired-row layout; a transposed operand's experts then sit 2x their
+        column offset apart in each pair row (a 64-column piece takes 128
+        bytes there)."""
         dev = w1.device
         w1, w2, w3 = (w.contiguous() for w in (w1, w2, w3))
         stream = _lib.stream_of(w1)
@@ -832,15 +842,18 @@ class ExpertWeights:
         # gate|up: w1 and w3 read in place as the [E, 2H, D] stack
         W13, S13, W13t, S13t = _alloc_quant(E * 2 * H, D, MX, True, dgrad, dev)
         _lib.call("fm_quantize_pair", _lib.ptr(w1), _lib.ptr(w3), _src_dtype(w1), E, H, D, D,
-                  *_tile_args(MX, W13, S13, W13t, S13t), stream)
+                  *_tile_args(MX, W13, S13, W13t, S13t, paired, paired and dgrad), stream)
         W2, S2, W2t, S2t = _alloc_quant(E * H, D, MX, dgrad, True, dev)
-        _lib.call("fm_quantize", _lib.ptr(w2), _src_dtype(w2), E * H, D, D, *_tile_args(MX, W2, S2, W2t, S2t),
-                  stream)
-        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 32, 1, 2 * H * D // 32, 0, 2 * H, D)
-        self.w2t = ExpertWeightOperand(W2t, S2t, E * H, H, 1, D, (H // 32) * D, 0, D, H)
+        _lib.call("fm_quantize", _lib.ptr(w2), _src_dtype(w2), E * H, D, D,
+                  *_tile_args(MX, W2, S2, W2t, S2t, paired and dgrad, paired), stream)
+        cs = 2 if paired else 1   # column-offset group strides in a paired buffer
+        self.w13 = ExpertWeightOperand(W13, S13, D, 2 * H * D, D // 32, 1, 2 * H * D // 32, 0, 2 * H, D,
+                                       paired=paired)
+        self.w2t = ExpertWeightOperand(W2t, S2t, E * H, cs * H, 1, D, (H // 32) * D, 0, D, H, paired=paired)
         if dgrad:
-            self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H)
-            self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D)
+            self.w13t = ExpertWeightOperand(W13t, S13t, E * 2 * H, cs * 2 * H, 1, D, (2 * H // 32) * D, 0, D, 2 * H,
+                                            paired=paired)
+            self.w2 = ExpertWeightOperand(W2, S2, D, H * D, D // 32, 1, H * D // 32, 0, H, D, paired=paired)
 
 
 # ================================================================= streams ====
