@@ -287,6 +287,20 @@ __device__ __forceinline__ void fetch_rows(const Src& src, typename Src::Raw (&r
   }
 }
 
+// Rows rg + 32 (it0 + k), k < N, of a full tile (no clamping): a batch of
+// a thread's rows, for sources whose raw values of all four rows would hold
+// too many registers.
+template <int N, class Src>
+__device__ __forceinline__ void fetch_row_batch(const Src& src, typename Src::Raw (&raw)[N][2], int64_t row0,
+                                                int64_t col0, int it0) {
+  const int64_t r = row0 + (threadIdx.x >> 3) + 32 * it0;
+  const int64_t c = col0 + 8 * (threadIdx.x & 7);
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) raw[k][h] = src.fetch(r + 32 * k, c + 64 * h);
+}
+
 // Values of one row: v[oi][h][i] for output oi, segment h.
 template <class Src>
 __device__ __forceinline__ void compute_row(const Src& src, const typename Src::Raw (&raw)[2],
@@ -394,15 +408,19 @@ __device__ __forceinline__ void pow2_tile(const Src& src, const TileOut& o, int6
   __shared__ float p_red[NOUT];
   __shared__ float p_rscale[NOUT][128];
   __shared__ __attribute__((aligned(16))) uint32_t p_code[NOUT][128 * 33];
-  typename Src::Raw raw[kRowsPerThread][2];
-  fetch_rows(src, raw, rows, row0, col0);  // rows % 128 == 0: every row is in range
+  // A two-output source fetches its rows in two batches of two: the raw
+  // values of four rows would keep the kernel at two waves per SIMD.
+  constexpr int kBatch = NOUT == 2 ? 2 : kRowsPerThread;
+  typename Src::Raw raw[kBatch][2];
   const int64_t rg = tid >> 3;
   RowPtr<QK_POW2> p[2] = {RowPtr<QK_POW2>(o, row0 + rg, col0 + o.col_off[0]),
                           RowPtr<QK_POW2>(o, row0 + rg, col0 + o.col_off[NOUT - 1])};
 #pragma unroll
   for (int it = 0; it < kRowsPerThread; ++it) {
+    // rows % 128 == 0: every row is in range
+    if (it % kBatch == 0) fetch_row_batch<kBatch>(src, raw, row0, col0, it);
     float v[NOUT][2][8];
-    compute_row(src, raw[it], v);
+    compute_row(src, raw[it % kBatch], v);
     const int r = int(rg) + 32 * it;
 #pragma unroll
     for (int oi = 0; oi < NOUT; ++oi) {
