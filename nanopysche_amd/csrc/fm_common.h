@@ -90,6 +90,24 @@ FM_HD float block_scale(float amax, bool pow2) {
 
 FM_HD uint8_t quant_e4m3(float x, float scale) { return f32_to_e4m3(clamp448(x / scale)); }
 
+// Stores to device buffers through global-memory pointers.  A store through
+// a pointer the compiler cannot place in global memory (one built from an
+// integer, or loaded from LDS) is a FLAT store, which counts in lgkmcnt as well
+// as vmcnt: every later wait for an LDS access then also waits for the store to
+// reach memory, and the vmcnt waits for later loads become full drains.
+// (HIP's vector types are classes whose assignment is declared for generic
+// objects only, so the stores go through clang's native vectors.)
+typedef uint32_t fm_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t fm_u32x4 __attribute__((ext_vector_type(4)));
+typedef float fm_f32x4 __attribute__((ext_vector_type(4)));
+#define FM_GLOBAL(T, p) ((__attribute__((address_space(1))) T*)(p))
+__device__ __forceinline__ void st_global(void* p, uint4 v) { *FM_GLOBAL(fm_u32x4, p) = fm_u32x4{v.x, v.y, v.z, v.w}; }
+__device__ __forceinline__ void st_global(void* p, uint2 v) { *FM_GLOBAL(fm_u32x2, p) = fm_u32x2{v.x, v.y}; }
+__device__ __forceinline__ void st_global(void* p, float4 v) { *FM_GLOBAL(fm_f32x4, p) = fm_f32x4{v.x, v.y, v.z, v.w}; }
+__device__ __forceinline__ void st_global(float* p, float v) { *FM_GLOBAL(float, p) = v; }
+__device__ __forceinline__ void st_global(uint8_t* p, uint8_t v) { *FM_GLOBAL(uint8_t, p) = v; }
+__device__ __forceinline__ void st_global(uint16_t* p, uint16_t v) { *FM_GLOBAL(uint16_t, p) = v; }
+
 // gfx950 v_cvt_pk_fp8_f32 (OCP e4m3fn, round-to-nearest-even) on four values
 // already clamped to +-448; byte i of the result encodes value i.  The GPU test
 // test_gpu_quant.py::test_hw_convert_matches_software checks it against the

@@ -172,6 +172,15 @@ __device__ __forceinline__ v4i make_rsrc(const void* base) {
 
 // A barrier the compiler moves nothing across.  It carries no memory fence,
 // which would wait for the prefetches still in flight.
+// a >= b for wave-uniform a and b, as a scalar: a select made from it is an
+// s_cmp / s_cselect pair.  64-bit comparisons have no scalar form, and a select
+// driven by the vector compare needs a VCC -> SCC copy; an exec-mask peephole
+// of the compiler has dropped that copy (the select then read a stale SCC and
+// wrote every row of a split output to its second tensor).
+__device__ __forceinline__ bool uniform_ge(int64_t a, int64_t b) {
+  return __builtin_amdgcn_readfirstlane(int(a >= b)) != 0;
+}
+
 __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
@@ -853,7 +862,7 @@ __device__ __forceinline__ void gemm256_tile(const GemmParams& p, int64_t bid, u
     C = p.C;
     row_off = jb * p.ldC + ib;
   } else {
-    const bool second = jb >= p.split;
+    const bool second = uniform_ge(jb, p.split);
     C = second ? p.C2 : p.C;
     row_off = e * (second ? p.c2_gs : p.c_gs) + (second ? jb - p.split : jb) * p.ldC + ib + tile.slice * p.ws_slice;
   }
@@ -878,17 +887,21 @@ __device__ __forceinline__ void gemm256_tile(const GemmParams& p, int64_t bid, u
         }
     const int c = lane & 15;
     uint16_t* dst = static_cast<uint16_t*>(C) + row_off + c * 8;
-    const bool vec16 = (p.ldC & 7) == 0;
+    if ((p.ldC & 7) == 0) {   // whole 16-byte stores; the split form in a loop of its own
 #pragma unroll 4
-    for (int n = 0; n < 16; ++n) {
-      const int rr = n * 4 + (lane >> 4);
-      const uint4 v = *reinterpret_cast<const uint4*>(W + rr * 256 + ((c ^ (rr & 15)) << 4));
-      uint16_t* d = dst + rr * p.ldC;
-      if (vec16) {
-        *reinterpret_cast<uint4*>(d) = v;
-      } else {
-        reinterpret_cast<uint2*>(d)[0] = make_uint2(v.x, v.y);
-        reinterpret_cast<uint2*>(d)[1] = make_uint2(v.z, v.w);
+      for (int n = 0; n < 16; ++n) {
+        const int rr = n * 4 + (lane >> 4);
+        const uint4 v = *reinterpret_cast<const uint4*>(W + rr * 256 + ((c ^ (rr & 15)) << 4));
+        st_global(dst + rr * p.ldC, v);
+      }
+    } else {
+#pragma unroll 4
+      for (int n = 0; n < 16; ++n) {
+        const int rr = n * 4 + (lane >> 4);
+        const uint4 v = *reinterpret_cast<const uint4*>(W + rr * 256 + ((c ^ (rr & 15)) << 4));
+        uint2* d = reinterpret_cast<uint2*>(dst + rr * p.ldC);
+        st_global(d, make_uint2(v.x, v.y));
+        st_global(d + 1, make_uint2(v.z, v.w));
       }
     }
     return;
@@ -901,8 +914,8 @@ __device__ __forceinline__ void gemm256_tile(const GemmParams& p, int64_t bid, u
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) =
-            make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+        st_global(dst + b * 32 * p.ldC + a * 32 + 8 * q,
+            make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]));
 }
 
 template <int KIND, int MODE, int MXL = 0>
@@ -1076,10 +1089,12 @@ __device__ __forceinline__ Operand uniform_operand(const Operand* o) {
 // of LDS `W`: 8 passes of 32 rows x 32 columns (block b of the rows, block a
 // of the columns), each written back as 64-byte row segments.  16-byte chunk
 // q of row r sits at position q ^ ((r / 4) % 4).
-__device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8_t* W, uint16_t* C, int64_t ldC,
-                                                  int64_t row0, int64_t col0, const WaveCoord& w) {
+// VEC16: whole 16-byte stores (ldC a multiple of 8), chosen once per call so
+// that the two store forms stay separate instructions.
+template <bool VEC16>
+__device__ __forceinline__ void store_bf16_passes_v(const v16f (&acc)[4][2], uint8_t* W, uint16_t* C, int64_t ldC,
+                                                    int64_t row0, int64_t col0, const WaveCoord& w) {
   const int lrow = w.lrow, lhalf = w.lhalf, lane = w.lane;
-  const bool vec16 = (ldC & 7) == 0;
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -1097,15 +1112,21 @@ __device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8
         const int r = u * 16 + (lane >> 2), c = lane & 3;
         const uint4 v = *reinterpret_cast<const uint4*>(W + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
         uint16_t* d = C + (row0 + b * 32 + r) * ldC + col0 + a * 32 + c * 8;
-        if (vec16) {
-          *reinterpret_cast<uint4*>(d) = v;
+        if constexpr (VEC16) {
+          st_global(d, v);
         } else {
-          reinterpret_cast<uint2*>(d)[0] = make_uint2(v.x, v.y);
-          reinterpret_cast<uint2*>(d)[1] = make_uint2(v.z, v.w);
+          st_global(d, make_uint2(v.x, v.y));
+          st_global(d + 4, make_uint2(v.z, v.w));
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+}
+
+__device__ __forceinline__ void store_bf16_passes(const v16f (&acc)[4][2], uint8_t* W, uint16_t* C, int64_t ldC,
+                                                  int64_t row0, int64_t col0, const WaveCoord& w) {
+  if ((ldC & 7) == 0) store_bf16_passes_v<true>(acc, W, C, ldC, row0, col0, w);
+  else store_bf16_passes_v<false>(acc, W, C, ldC, row0, col0, w);
 }
 
 // QNN (BF16 and FP8 pow2): the weight operand Q is stored [K][N]
@@ -1215,8 +1236,8 @@ __global__ __launch_bounds__(512) void gemm256p_kernel(GemmParams p) {
           for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<float4*>(dst + b * 32 * p.ldC + a * 32 + 8 * q) = make_float4(
-                  acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+              st_global(dst + b * 32 * p.ldC + a * 32 + 8 * q, make_float4(
+                  acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]));
       }
     }
     if (!has_next) break;
@@ -1360,7 +1381,7 @@ __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
     const int64_t ib = t.i0 + w.wi * 128, jb = t.j0 + w.wj * 64;
     if (ib >= n_i || jb >= n_j) return;
     const int64_t split = rfl64(pl->split);
-    const bool second = jb >= split;
+    const bool second = uniform_ge(jb, split);
     void* const Cb = second ? pl->C2 : pl->C;
     const int64_t gs = second ? rfl64(pl->c2_gs) : rfl64(pl->c_gs);
     const int64_t ldC = rfl64(pl->ldC);
@@ -1379,8 +1400,8 @@ __global__ __launch_bounds__(512) void gemm256pk_kernel(GemmParams p) {
         for (int b = 0; b < 2; ++b)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4)
-            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
-                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+            st_global(dst + b * 32 * ldC + a * 32 + 8 * r4, make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]));
     }
   };
 
@@ -1595,8 +1616,8 @@ __global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmPara
         for (int b = 0; b < 2; ++b)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4)
-            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
-                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+            st_global(dst + b * 32 * ldC + a * 32 + 8 * r4, make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]));
     }
   };
   auto epilogue = [&](const ItemMK& it, const v16f (&acc)[4][2]) {
@@ -1604,7 +1625,7 @@ __global__ __launch_bounds__(512) void gemm256pmk_kernel(GemmParams pm, GemmPara
     if (it.k_mode) {   // weight gradient: row j (m), column i; rows past `split` to C2
       if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return;
       const int64_t split = rfl64(plk->split);
-      const bool second = jb >= split;
+      const bool second = uniform_ge(jb, split);
       const int64_t gs = second ? rfl64(plk->c2_gs) : rfl64(plk->c_gs);
       uint8_t* const Cb = static_cast<uint8_t*>(second ? plk->C2 : plk->C);
       const int f32 = __builtin_amdgcn_readfirstlane(plk->out_f32);
@@ -2047,8 +2068,8 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
         for (int b = 0; b < 2; ++b)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4)
-            *reinterpret_cast<float4*>(dst + b * 32 * ldC + a * 32 + 8 * r4) = make_float4(
-                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]);
+            st_global(dst + b * 32 * ldC + a * 32 + 8 * r4, make_float4(
+                acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]));
     }
   };
   auto epilogue = [&](const ItemR& it, const v16f (&acc)[4][2]) {
@@ -2056,7 +2077,7 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
     if (HAS_K && (!HAS_M || it.k_mode)) {   // weight gradient: row j (m), column i; rows past `split` to C2
       if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return;
       const int64_t split = rfl64(plk->split);
-      const bool second = jb >= split;
+      const bool second = uniform_ge(jb, split);
       const int64_t gs = second ? rfl64(plk->c2_gs) : rfl64(plk->c_gs);
       uint8_t* const Cb = static_cast<uint8_t*>(second ? plk->C2 : plk->C);
       const int f32 = __builtin_amdgcn_readfirstlane(plk->out_f32);
@@ -2461,14 +2482,14 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
           if (i >= p.n_i) continue;
           if (p.out_f32) {
             float* dst = static_cast<float*>(p.C) + j * p.ldC + i;
-            *reinterpret_cast<float4*>(dst) =
-                make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+            st_global(dst,
+                make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]));
           } else {
             uint16_t* dst = static_cast<uint16_t*>(p.C) + j * p.ldC + i;
             uint2 v;
             v.x = hw_bf16x2(acc[a][b][4 * q], acc[a][b][4 * q + 1]);
             v.y = hw_bf16x2(acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
-            *reinterpret_cast<uint2*>(dst) = v;
+            st_global(dst, v);
           }
         }
       } else {
@@ -2480,8 +2501,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
           const int64_t row = second ? i - p.split : i;
           const int64_t off = e * (second ? p.c2_gs : p.c_gs) + row * p.ldC + j;
           void* base = second ? p.C2 : p.C;
-          if (p.out_f32) static_cast<float*>(base)[off] = acc[a][b][r];
-          else static_cast<uint16_t*>(base)[off] = f32_to_bf16(acc[a][b][r]);
+          if (p.out_f32) st_global(static_cast<float*>(base) + off, acc[a][b][r]);
+          else st_global(static_cast<uint16_t*>(base) + off, f32_to_bf16(acc[a][b][r]));
         }
       }
     }
@@ -2773,10 +2794,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(SplitReduceArgs a) {
     const bool second = r >= a.split;
     const int64_t off = e * (second ? a.out2_gs : a.out_gs) + (second ? r - a.split : r) * a.ld + c;
     if (a.out_f32) {
-      *reinterpret_cast<float4*>(static_cast<float*>(second ? a.out2 : a.out) + off) = acc;
+      st_global(static_cast<float*>(second ? a.out2 : a.out) + off, acc);
     } else {
       uint16_t* d = static_cast<uint16_t*>(second ? a.out2 : a.out) + off;
-      *reinterpret_cast<uint2*>(d) = make_uint2(hw_bf16x2(acc.x, acc.y), hw_bf16x2(acc.z, acc.w));
+      st_global(d, make_uint2(hw_bf16x2(acc.x, acc.y), hw_bf16x2(acc.z, acc.w)));
     }
   }
 }

@@ -214,9 +214,9 @@ __device__ __forceinline__ uint4 row_quant(const float (&v)[2][8], const RowPtr<
     if (store) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        *reinterpret_cast<uint4*>(p.qseg(h)) =
-            make_uint4(enc_bf16x2<HW>(v[h][0], v[h][1]), enc_bf16x2<HW>(v[h][2], v[h][3]),
-                       enc_bf16x2<HW>(v[h][4], v[h][5]), enc_bf16x2<HW>(v[h][6], v[h][7]));
+        st_global(reinterpret_cast<void*>(p.qseg(h)),
+                  make_uint4(enc_bf16x2<HW>(v[h][0], v[h][1]), enc_bf16x2<HW>(v[h][2], v[h][3]),
+                             enc_bf16x2<HW>(v[h][4], v[h][5]), enc_bf16x2<HW>(v[h][6], v[h][7])));
     }
     return make_uint4(0, 0, 0, 0);
   } else if constexpr (KIND == QK_MX) {
@@ -229,7 +229,7 @@ __device__ __forceinline__ uint4 row_quant(const float (&v)[2][8], const RowPtr<
       const float inv = mx_inv_scale(code);
       w[2 * h] = enc_e4m3x4<HW>(v[h][0] * inv, v[h][1] * inv, v[h][2] * inv, v[h][3] * inv);
       w[2 * h + 1] = enc_e4m3x4<HW>(v[h][4] * inv, v[h][5] * inv, v[h][6] * inv, v[h][7] * inv);
-      if (store && (lane8 & 3) == 0) *reinterpret_cast<uint8_t*>(p.s + h * p.s_seg) = uint8_t(code);
+      if (store && (lane8 & 3) == 0) st_global(reinterpret_cast<uint8_t*>(p.s + h * p.s_seg), uint8_t(code));
     }
   } else {
     float am = 0.f;
@@ -255,11 +255,11 @@ __device__ __forceinline__ uint4 row_quant(const float (&v)[2][8], const RowPtr<
                                               div_rn(v[h][7], d));
       }
     }
-    if (store && lane8 == 0) *reinterpret_cast<float*>(p.s) = sc;
+    if (store && lane8 == 0) st_global(reinterpret_cast<float*>(p.s), sc);
   }
   if (store) {
-    *reinterpret_cast<uint2*>(p.qseg(0)) = make_uint2(w[0], w[1]);
-    *reinterpret_cast<uint2*>(p.qseg(1)) = make_uint2(w[2], w[3]);
+    st_global(reinterpret_cast<void*>(p.qseg(0)), make_uint2(w[0], w[1]));
+    st_global(reinterpret_cast<void*>(p.qseg(1)), make_uint2(w[2], w[3]));
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
