@@ -435,6 +435,11 @@ def workload_c3(args, dev):
     traffic = recorded_traffic(dom, args.recipe)
     cpu = None if args.no_cpu_baseline else cpu_baseline(T, D, H, E, K)
     hbm = hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H) if args.recipe == "flow_moe" else None
+    probe = None
+    if hbm is not None:   # the same kernels against what a plain copy reaches on this board
+        probe = bw_probe(dev, reps=5)
+        for h in hbm:
+            h["frac_of_copy_probe"] = round(h["GB_s"] / 1e3 / probe["copy"]["TB_s"], 3)
     return {
         "metric": "MoE layer fwd+bwd tokens/s on 1 MI355X",
         "value": round(T / (ms * 1e-3), 1),
@@ -463,6 +468,7 @@ def workload_c3(args, dev):
                      "traffic_source": None if traffic is None else traffic["source"]},
         "gemm": gemm_report(summ, args.steps),
         "hbm_kernels": hbm,
+        "hbm_probe": probe,
         "cpu_baseline": cpu,
     }
 
@@ -988,6 +994,38 @@ def cpu_baseline_c5(x, wts, idx, w1, w2, w3, go, E, n_experts=4, a_sample=8192):
                       f"experts' weight quantisation (torch CPU), one run, {dt:.1f} s; cpu: {cpu_model_name()}"}
 
 
+def bw_probe(dev, gib=1, reps=10):
+    """HBM rates of plain kernels (fm_hbm_probe): a copy with one 4 KiB chunk
+    per workgroup (the tile producers' launch shape), a read-only and a
+    write-only pass, `gib` GiB each, `reps` back-to-back launches between two
+    HIP events after three warm-up launches.  The HBM-bound kernels' fractions
+    are quoted against 8 TB/s; these say what a kernel with nothing but the
+    memory traffic reaches on the same board."""
+    import torch
+
+    from nanopysche_amd import _lib
+
+    n = gib << 30
+    a = torch.ones(n, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    st = _lib.stream_of(a)
+    out = {}
+    for kind, name, moved in ((0, "copy", 2 * n), (1, "read", n), (2, "write", n)):
+        def launch():
+            _lib.call("fm_hbm_probe", kind, _lib.ptr(a), _lib.ptr(b), n, st)
+        for _ in range(3):
+            launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[name] = {"us": round(us, 1), "TB_s": round(moved / us / 1e6, 3), "frac_of_8TBps": round(moved / us / 8e6, 3)}
+    return {"probe": "HBM bandwidth (fm_hbm_probe)", "bytes_per_buffer": n, **out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1007,6 +1045,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one plain 256 MiB device copy (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
+    ap.add_argument("--bw-probe", action="store_true",
+                    help="print the HBM rates of a plain copy, read and write (fm_hbm_probe) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
@@ -1015,6 +1055,9 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    if args.bw_probe:
+        print(json.dumps(bw_probe(dev)))
+        return
     run = {"c3": workload_c3, "c1": workload_c1, "c2": workload_c2, "c4": workload_c4,
            "c5": workload_c5, "shared": workload_shared}[args.workload]
     print(json.dumps(run(args, dev)))

@@ -108,6 +108,11 @@ const char* fm_source_hash(void);
  * exported so tests can check it against other implementations. */
 void fm_host_encode_e4m3(const float* in, uint8_t* out, int64_t n);
 void fm_host_decode_e4m3(const uint8_t* in, float* out, int64_t n);
+/* HBM bandwidth probe (no counterpart in the reference: the measurement the
+ * HBM-bound kernels are compared against).  kind 0: copy `bytes` from src to
+ * dst, one 4 KiB chunk per workgroup; 1: read src (dst: a 1 KiB sink);
+ * 2: write dst.  bytes a positive multiple of 4096, 16-byte aligned buffers. */
+int fm_hbm_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);
 /* Device conversion check: x [n] fp32 (n % 4 == 0) encoded to e4m3 (after a
  * clamp to +-448) and to bf16 by the gfx950 convert instructions (*_hw) and by
  * the integer routines (*_sw).  The kernels use the hardware path; a GPU test

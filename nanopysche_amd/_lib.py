@@ -77,6 +77,7 @@ SIGNATURES = {
     "fm_source_hash": (C.c_char_p, []),
     "fm_host_encode_e4m3": (None, [_vp, _vp, _i64]),
     "fm_host_decode_e4m3": (None, [_vp, _vp, _i64]),
+    "fm_hbm_probe": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "fm_convert_check": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "fm_decode_check": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "fm_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _i64,

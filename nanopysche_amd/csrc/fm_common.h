@@ -107,6 +107,7 @@ __device__ __forceinline__ void st_global(void* p, float4 v) { *FM_GLOBAL(fm_f32
 __device__ __forceinline__ void st_global(float* p, float v) { *FM_GLOBAL(float, p) = v; }
 __device__ __forceinline__ void st_global(uint8_t* p, uint8_t v) { *FM_GLOBAL(uint8_t, p) = v; }
 __device__ __forceinline__ void st_global(uint16_t* p, uint16_t v) { *FM_GLOBAL(uint16_t, p) = v; }
+__device__ __forceinline__ void st_global(uint32_t* p, uint32_t v) { *FM_GLOBAL(uint32_t, p) = v; }
 
 // gfx950 v_cvt_pk_fp8_f32 (OCP e4m3fn, round-to-nearest-even) on four values
 // already clamped to +-448; byte i of the result encodes value i.  The GPU test

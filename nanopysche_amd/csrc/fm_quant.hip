@@ -442,3 +442,57 @@ int fm_scaling_aware_transpose(const void* q, int64_t rows, int64_t cols, int64_
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------- bandwidth probe ----
+// The HBM rates the producers are measured against: a copy with one 4 KiB
+// chunk per workgroup (the tile producers' launch shape), a read-only pass
+// and a write-only pass, both four 16-byte accesses per lane in flight over
+// a grid-stride loop.
+namespace fm {
+__global__ __launch_bounds__(256) void probe_copy_kernel(const uint4* __restrict__ a, uint4* __restrict__ b) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  st_global(b + i, a[i]);
+}
+__global__ __launch_bounds__(256) void probe_read_kernel(const uint4* __restrict__ a, size_t n,
+                                                         uint32_t* __restrict__ sink) {
+  uint32_t acc = 0;
+  for (size_t i = size_t(blockIdx.x) * 1024 + threadIdx.x; i + 768 < n; i += size_t(gridDim.x) * 1024) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = a[i + 256 * u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9e3779b9u) st_global(sink + threadIdx.x, acc);   // keeps the loads; almost never taken
+}
+__global__ __launch_bounds__(256) void probe_write_kernel(uint4* __restrict__ b, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 1024 + threadIdx.x; i + 768 < n; i += size_t(gridDim.x) * 1024) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) st_global(b + i + 256 * u, make_uint4(u, 1u, 2u, 3u));
+  }
+}
+}  // namespace fm
+
+extern "C" {
+
+int fm_hbm_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream) {
+  FM_REQUIRE(kind >= 0 && kind <= 2, "fm_hbm_probe: kind must be 0 (copy), 1 (read) or 2 (write)");
+  FM_REQUIRE(bytes > 0 && bytes % 4096 == 0 && bytes / 4096 <= INT32_MAX,
+             "fm_hbm_probe: bytes must be a positive multiple of 4096");
+  FM_REQUIRE(dst != nullptr && (kind == 2 || src != nullptr), "fm_hbm_probe: null buffer");
+  FM_REQUIRE(aligned16(src) && aligned16(dst), "fm_hbm_probe: buffers must be 16-byte aligned");
+  const size_t n = size_t(bytes) / 16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kind == 0) {
+    hipLaunchKernelGGL(probe_copy_kernel, dim3(unsigned(n / 256)), dim3(256), 0, s,
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst));
+  } else if (kind == 1) {   // dst: at least 1 KiB, written only in the untaken branch
+    hipLaunchKernelGGL(probe_read_kernel, dim3(4096), dim3(256), 0, s, static_cast<const uint4*>(src), n,
+                       static_cast<uint32_t*>(dst));
+  } else {
+    hipLaunchKernelGGL(probe_write_kernel, dim3(4096), dim3(256), 0, s, static_cast<uint4*>(dst), n);
+  }
+  return check_launch("fm_hbm_probe");
+}
+
+}  // extern "C"
