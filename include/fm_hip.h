@@ -367,6 +367,30 @@ int fm_route_sort(const void* indices, int indices_i64, int64_t T, int K, int E,
 int fm_route_tile_masks(const int32_t* tile_expert, int64_t n_tiles, const int32_t* use_fp8, int32_t* tiles_fp8,
                         int32_t* tiles_bf16, void* stream);
 
+/* Replaces the token dropping of MoEBase._apply_capacity (reference
+ * model/moe.py:1395-1448): each expert's tokens ranked in token order, a token
+ * kept when every one of its valid slots ranks below `capacity`.  Inputs: the
+ * indices [T, K] and the counts, offsets and row_of of fm_route_sort on them.
+ * Outputs: pos_of [T] (the token's position among the kept tokens, -1 if
+ * dropped), kept_index [T] (first n_kept entries: the kept tokens in order),
+ * n_kept [1], drops [E] = max(0, counts[e] - capacity) (the reference's
+ * per-expert drop counts; their sum is its `dropped`).  workspace: at least
+ * fm_capacity_workspace_bytes(T) bytes, no initial contents needed. */
+int64_t fm_capacity_workspace_bytes(int64_t T);
+int fm_capacity_select(const void* indices, int indices_i64, int64_t T, int K, int E, const int32_t* counts,
+                       const int32_t* offsets, const int32_t* row_of, int64_t capacity, int32_t* pos_of,
+                       int32_t* kept_index, int32_t* n_kept, int32_t* drops, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* Replaces the row selections around capacity dropping (reference
+ * model/moe.py:1445-1447 `x[keep_mask]`, and :1386-1391, the scatter of the
+ * kept tokens' outputs into a zero [B*S, D] buffer): dst row i (pitch ld_dst
+ * bytes) = src row index[i] (pitch ld_src bytes, n_src rows), zeros where
+ * index[i] is outside [0, n_src).  row_bytes and pitches multiples of 4,
+ * pointers 4-byte aligned. */
+int fm_gather_rows(const void* src, int64_t n_src, int64_t ld_src, const int32_t* index, int64_t n,
+                   int64_t row_bytes, void* dst, int64_t ld_dst, void* stream);
+
 /* fm_route_sort, then fm_quantize_weight_batch(jobs, n_jobs) on the same
  * stream, with the outputs of the two calls.  No counterpart in the
  * reference: the sort's launches occupy a few CUs for a few microseconds, so

@@ -124,6 +124,10 @@ SIGNATURES = {
     "fm_route_sort_noalloc_max_workspace_bytes": (_i64, []),
     "fm_route_sort_noalloc": (_i32, [_vp, _i32, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
                                      _vp]),
+    "fm_capacity_workspace_bytes": (_i64, [_i64]),
+    "fm_capacity_select": (_i32, [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64,
+                                  _vp]),
+    "fm_gather_rows": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "fm_route_tile_masks": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp]),
     "fm_permute": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _vp, _i64, _vp, _i64,
                           _vp, _i64, _vp, _i64, _vp, _vp]),

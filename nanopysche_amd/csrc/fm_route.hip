@@ -14,6 +14,10 @@
 //   fm_unpermute        -- out[t] = sum_k w[t,k] * y[row(t,k)], fp32 sum, one
 //                          rounding
 //   fm_router_weight_grad -- dw[t,k] = <dout[t], y[row(t,k)]>
+//   fm_capacity_select  -- capacity dropping: ranks from the sort's rows, keep
+//                          flags, then a block-count compaction of the kept tokens
+//   fm_gather_rows      -- row gather with zero rows for index -1 (the kept
+//                          tokens' selection and the scatter back)
 #include <mutex>
 #include <type_traits>
 
@@ -994,6 +998,107 @@ static int route_scratch_ptr(int32_t** out) {
   return 0;
 }
 
+
+// ------------------------------------------------------------- capacity ----
+// Token dropping by expert capacity.  An expert's tokens are ranked in token
+// order; a token is kept when each of its valid slots ranks below the
+// capacity.  The stable sort puts each expert's assignments in token order
+// (assignment a = t*K + k, and the K experts of a token are distinct), so a
+// slot's rank is its row less its group's start.
+constexpr int kCapBlock = 1024;   // tokens per workgroup (256 threads x 4)
+
+// pos_of[t] = 0 (kept) or -1 (dropped); block_kept[b] = kept tokens of
+// workgroup b.  Workgroup 0 also writes drops[e] = max(0, counts[e] -
+// capacity).
+template <typename I>
+__global__ __launch_bounds__(256) void capacity_keep_kernel(const I* __restrict__ idx, int64_t T, int K, int E,
+                                                            const int32_t* __restrict__ counts,
+                                                            const int32_t* __restrict__ offsets,
+                                                            const int32_t* __restrict__ row_of, int64_t capacity,
+                                                            int32_t* __restrict__ pos_of,
+                                                            int32_t* __restrict__ block_kept,
+                                                            int32_t* __restrict__ drops) {
+  int kept = 0;
+#pragma unroll 1
+  for (int i = 0; i < kCapBlock / 256; ++i) {
+    const int64_t t = int64_t(blockIdx.x) * kCapBlock + i * 256 + threadIdx.x;
+    int keep = 0;
+    if (t < T) {
+      keep = 1;
+      for (int k = 0; k < K; ++k) {
+        const int64_t a = t * K + k;
+        const int e = load_expert(idx, a, E);
+        const int32_t r = row_of[a];
+        if (e >= 0 && r >= 0 && int64_t(r - offsets[e]) >= capacity) keep = 0;
+      }
+      st_global(reinterpret_cast<uint32_t*>(pos_of + t), uint32_t(keep ? 0 : -1));
+    }
+    kept += __syncthreads_count(keep);
+  }
+  if (threadIdx.x == 0) st_global(reinterpret_cast<uint32_t*>(block_kept + blockIdx.x), uint32_t(kept));
+  if (blockIdx.x == 0)
+    for (int e = threadIdx.x; e < E; e += 256) {
+      const int64_t over = int64_t(counts[e]) - capacity;
+      st_global(reinterpret_cast<uint32_t*>(drops + e), uint32_t(over > 0 ? over : 0));
+    }
+}
+
+// Compaction: workgroup b starts at the kept tokens of the workgroups before
+// it, then ranks its own with wave ballots.  pos_of[t] becomes the token's
+// position among the kept ones (or stays -1), kept_index[pos] = t, and the
+// last workgroup writes the total to n_kept.
+__global__ __launch_bounds__(256) void capacity_compact_kernel(int64_t T, const int32_t* __restrict__ block_kept,
+                                                               int64_t n_blocks, int32_t* __restrict__ pos_of,
+                                                               int32_t* __restrict__ kept_index,
+                                                               int32_t* __restrict__ n_kept) {
+  __shared__ int32_t part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int32_t before = 0;
+  for (int64_t j = threadIdx.x; j < int64_t(blockIdx.x); j += 256) before += block_kept[j];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off);
+  if (lane == 0) part[wave] = before;
+  __syncthreads();
+  int32_t base = part[0] + part[1] + part[2] + part[3];
+  __syncthreads();
+#pragma unroll 1
+  for (int i = 0; i < kCapBlock / 256; ++i) {
+    const int64_t t = int64_t(blockIdx.x) * kCapBlock + i * 256 + threadIdx.x;
+    const bool keep = t < T && pos_of[t] >= 0;
+    const uint64_t m = __ballot(keep);
+    if (lane == 0) part[wave] = __popcll(m);
+    __syncthreads();
+    int32_t pos = base + __popcll(m & lanemask_lt());
+    for (int w = 0; w < wave; ++w) pos += part[w];
+    if (keep) {
+      st_global(reinterpret_cast<uint32_t*>(pos_of + t), uint32_t(pos));
+      st_global(reinterpret_cast<uint32_t*>(kept_index + pos), uint32_t(t));
+    }
+    base += part[0] + part[1] + part[2] + part[3];
+    __syncthreads();
+  }
+  if (int64_t(blockIdx.x) == n_blocks - 1 && threadIdx.x == 0) st_global(reinterpret_cast<uint32_t*>(n_kept),
+                                                                          uint32_t(base));
+}
+
+// dst row i = src row index[i], zeros where index[i] is outside [0, n_src).
+// VW-byte pieces (16 or 4), a piece per thread, rows walked by the grid.
+template <int VW>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restrict__ src, int64_t n_src,
+                                                          int64_t ld_src, const int32_t* __restrict__ index,
+                                                          int64_t n, int64_t pieces, uint8_t* __restrict__ dst,
+                                                          int64_t ld_dst) {
+  using V = typename std::conditional<VW == 16, uint4, uint32_t>::type;
+  const int64_t total = n * pieces;
+  for (int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x; q < total; q += int64_t(gridDim.x) * 256) {
+    const int64_t i = q / pieces, c = q - i * pieces;
+    const int64_t r = index[i];
+    V v{};
+    if (r >= 0 && r < n_src) v = *reinterpret_cast<const V*>(src + r * ld_src + c * VW);
+    st_global(reinterpret_cast<V*>(dst + i * ld_dst + c * VW), v);
+  }
+}
+
 }  // namespace fm
 
 using namespace fm;
@@ -1200,6 +1305,63 @@ int fm_router_weight_grad(const void* dout, int64_t ld_do, const void* y, int64_
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(dout), ld_do,
                      static_cast<const uint16_t*>(y), ld_y, row_of, A, K, D, dw);
   return check_launch("fm_router_weight_grad");
+}
+
+
+int64_t fm_capacity_workspace_bytes(int64_t T) {
+  const int64_t blocks = T <= 0 ? 1 : (T + kCapBlock - 1) / kCapBlock;
+  return (blocks * 4 + 255) / 256 * 256;
+}
+
+int fm_capacity_select(const void* indices, int indices_i64, int64_t T, int K, int E, const int32_t* counts,
+                       const int32_t* offsets, const int32_t* row_of, int64_t capacity, int32_t* pos_of,
+                       int32_t* kept_index, int32_t* n_kept, int32_t* drops, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  FM_REQUIRE(T >= 0 && K >= 1 && E >= 1 && E <= kSortMaxExperts, "fm_capacity_select: bad T, K or E");
+  FM_REQUIRE(T * K < (int64_t(1) << 31), "fm_capacity_select: T*K must be below 2^31");
+  FM_REQUIRE(capacity >= 0, "fm_capacity_select: capacity must be >= 0");
+  FM_REQUIRE(counts && offsets && n_kept && drops && (T == 0 || (indices && row_of && pos_of && kept_index)),
+             "fm_capacity_select: null pointer");
+  FM_REQUIRE(workspace && workspace_bytes >= fm_capacity_workspace_bytes(T),
+             "fm_capacity_select: workspace must hold fm_capacity_workspace_bytes(T) bytes");
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  // (T == 0: one workgroup of each kernel writes n_kept = 0 and the drops)
+  const int64_t blocks = T == 0 ? 1 : (T + kCapBlock - 1) / kCapBlock;
+  int32_t* bk = static_cast<int32_t*>(workspace);
+  if (indices_i64)
+    hipLaunchKernelGGL(capacity_keep_kernel<int64_t>, dim3(unsigned(blocks)), dim3(256), 0, sm,
+                       static_cast<const int64_t*>(indices), T, K, E, counts, offsets, row_of, capacity, pos_of, bk,
+                       drops);
+  else
+    hipLaunchKernelGGL(capacity_keep_kernel<int32_t>, dim3(unsigned(blocks)), dim3(256), 0, sm,
+                       static_cast<const int32_t*>(indices), T, K, E, counts, offsets, row_of, capacity, pos_of, bk,
+                       drops);
+  hipLaunchKernelGGL(capacity_compact_kernel, dim3(unsigned(blocks)), dim3(256), 0, sm, T, bk, blocks, pos_of,
+                     kept_index, n_kept);
+  return check_launch("fm_capacity_select");
+}
+
+int fm_gather_rows(const void* src, int64_t n_src, int64_t ld_src, const int32_t* index, int64_t n,
+                   int64_t row_bytes, void* dst, int64_t ld_dst, void* stream) {
+  FM_REQUIRE(n >= 0 && n_src >= 0 && row_bytes >= 0, "fm_gather_rows: sizes must be >= 0");
+  FM_REQUIRE(row_bytes % 4 == 0 && ld_src % 4 == 0 && ld_dst % 4 == 0 && ld_src >= row_bytes && ld_dst >= row_bytes,
+             "fm_gather_rows: row bytes and pitches must be multiples of 4, pitches >= row bytes");
+  FM_REQUIRE((n == 0 || row_bytes == 0) || (index && dst && (src || n_src == 0)), "fm_gather_rows: null pointer");
+  FM_REQUIRE(reinterpret_cast<uintptr_t>(src) % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 4 == 0,
+             "fm_gather_rows: src and dst must be 4-byte aligned");
+  if (n == 0 || row_bytes == 0) return 0;
+  hipStream_t sm = static_cast<hipStream_t>(stream);
+  const bool v16 = row_bytes % 16 == 0 && ld_src % 16 == 0 && ld_dst % 16 == 0 && aligned16(src) && aligned16(dst);
+  const int vw = v16 ? 16 : 4;
+  const int64_t pieces = row_bytes / vw, total = n * pieces;
+  const unsigned blocks = unsigned((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  const uint8_t* s8 = static_cast<const uint8_t*>(src);
+  uint8_t* d8 = static_cast<uint8_t*>(dst);
+  if (v16) hipLaunchKernelGGL(gather_rows_kernel<16>, dim3(blocks), dim3(256), 0, sm, s8, n_src, ld_src, index, n,
+                              pieces, d8, ld_dst);
+  else hipLaunchKernelGGL(gather_rows_kernel<4>, dim3(blocks), dim3(256), 0, sm, s8, n_src, ld_src, index, n,
+                          pieces, d8, ld_dst);
+  return check_launch("fm_gather_rows");
 }
 
 }  // extern "C"

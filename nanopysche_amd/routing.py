@@ -108,6 +108,92 @@ def route_tokens(indices: torch.Tensor, num_experts: int, fp8_gemm_threshold: in
                        tile_expert, use_fp8)
 
 
+@dataclass
+class CapacitySelection:
+    """Tokens kept by expert capacity (``fm_capacity_select``).
+
+    pos_of      [T] int32       position of each token among the kept ones, -1 if dropped
+    kept_index  [n_kept] int32  the kept tokens in token order
+    drops       list[int] [E]   tokens beyond each expert's capacity
+    dropped     int             sum of drops (a token over two experts' capacity counts twice)
+    """
+
+    capacity: int
+    n_kept: int
+    pos_of: torch.Tensor
+    kept_index: torch.Tensor
+    drops: list
+    dropped: int
+
+
+def capacity_select(indices: torch.Tensor, plan: RoutingPlan, capacity: int) -> CapacitySelection:
+    """The token dropping of ``MoEBase._apply_capacity`` (reference
+    ``model/moe.py:1395-1448``): expert e keeps the first ``capacity`` of its
+    tokens in token order; a token over the capacity of any of its experts is
+    dropped.  ``plan`` is ``route_tokens`` of the same ``indices`` [T, K].
+    Reads n_kept and the drop counts back to the host (one synchronisation,
+    as the reference's ``nonzero`` and ``dropped`` are host values)."""
+    _lib.require_device(indices, "indices")
+    indices = indices.reshape(-1, indices.shape[-1]).contiguous()
+    if indices.dtype not in (torch.int64, torch.int32):
+        raise TypeError(f"indices must be int64 or int32, got {indices.dtype}")
+    T, K = indices.shape
+    if T != plan.num_tokens or K != plan.top_k:
+        raise ValueError("indices do not match the routing plan")
+    if capacity < 0:
+        raise ValueError("capacity must be >= 0")
+    E = plan.num_experts
+    dev = indices.device
+    pos_of = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
+    kept = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
+    tally = torch.empty(1 + E, dtype=torch.int32, device=dev)      # n_kept, drops[E]
+    ws_bytes = int(_lib.load().fm_capacity_workspace_bytes(T))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("fm_capacity_select", _lib.ptr(indices), int(indices.dtype == torch.int64), T, K, E,
+              _lib.ptr(plan.counts), _lib.ptr(plan.offsets), _lib.ptr(plan.row_of), int(capacity), _lib.ptr(pos_of),
+              _lib.ptr(kept), _lib.ptr(tally), _lib.ptr(tally[1:]), _lib.ptr(ws), ws_bytes, _lib.stream_of(indices))
+    host = tally.cpu().tolist()
+    n_kept, drops = int(host[0]), [int(v) for v in host[1:]]
+    return CapacitySelection(int(capacity), n_kept, pos_of[:T], kept[:n_kept], drops, sum(drops))
+
+
+def gather_rows(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """``out[i] = src[index[i]]`` over the first dimension, zeros where
+    ``index[i]`` is outside [0, src.shape[0]) (``fm_gather_rows``; index
+    int32).  Not differentiable by itself: ``select_rows`` is."""
+    _lib.require_device(src, "src")
+    if index.dtype != torch.int32:
+        raise TypeError("index must be int32")
+    src = src.contiguous()
+    n_src = src.shape[0]
+    row = int(torch.Size(src.shape[1:]).numel()) * src.element_size()
+    out = torch.empty((index.shape[0], *src.shape[1:]), dtype=src.dtype, device=src.device)
+    if row % 4:
+        raise ValueError("fm_gather_rows moves rows of a multiple of 4 bytes")
+    _lib.call("fm_gather_rows", _lib.ptr(src), n_src, row, _lib.ptr(index.contiguous()), index.shape[0], row,
+              _lib.ptr(out), row, _lib.stream_of(src))
+    return out
+
+
+class _SelectRows(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, index, inverse):
+        ctx.save_for_backward(inverse)
+        return gather_rows(src, index)
+
+    @staticmethod
+    def backward(ctx, g):
+        (inverse,) = ctx.saved_tensors
+        return gather_rows(g, inverse), None, None
+
+
+def select_rows(src: torch.Tensor, index: torch.Tensor, inverse: torch.Tensor) -> torch.Tensor:
+    """Differentiable ``gather_rows``: ``inverse`` maps each row of ``src`` to
+    the output row that holds it, or -1 (index must be injective), so the
+    gradient is ``gather_rows(grad, inverse)``: zeros for rows not selected."""
+    return _SelectRows.apply(src, index, inverse)
+
+
 def _gating_code(gating) -> int:
     return {"softmax": _lib.GATING_SOFTMAX, "sigmoid": _lib.GATING_SIGMOID}[str(gating).lower().split(".")[-1]]
 
@@ -404,9 +490,11 @@ class _RouterFunction(torch.autograd.Function):
 
 def route(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, *, top_k: int, gating: str = "softmax",
           score_bias=None, replay_indices=None, normalize_expert_weights=None, z_loss_multiplier=None,
-          load_tracker: ExpertLoadTracker = None):
-    """MoERouter.forward on the GPU (reference model/moe.py:133-184, jitter
-    aside): fp32 gate logits x.float() @ W.T + b (+ score_bias) -> gating
+          load_tracker: ExpertLoadTracker = None, jitter_eps=None, training: bool = True):
+    """MoERouter.forward on the GPU (reference model/moe.py:133-184): with
+    ``jitter_eps`` and ``training``, x + randn_like(x) * jitter_eps first
+    (:145-148, torch's generator, so a seeded run draws the reference's
+    noise), then fp32 gate logits x.float() @ W.T + b (+ score_bias) -> gating
     (softmax over the K selected logits, sigmoid / (sum + 1e-8), or R3 replay
     of ``replay_indices``) -> optional l2 normalisation of the weights ->
     (weights [..., K] fp32, indices [..., K] int64, aux loss = E * sum_i f_i P_i
@@ -416,6 +504,8 @@ def route(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias=None, *, top_k: 
     has a score bias).  Differentiable in x, gate_weight and gate_bias through
     the weights and the loss."""
     _lib.require_device(x, "x")
+    if jitter_eps is not None and training:
+        x = x + torch.randn_like(x) * jitter_eps
     z = 0.0 if z_loss_multiplier is None else float(z_loss_multiplier)
     return _RouterFunction.apply(x, gate_weight, gate_bias, score_bias, int(top_k), gating, replay_indices,
                                  normalize_expert_weights, z, load_tracker)

@@ -9,6 +9,10 @@ Follows:
   ``model/moe.py:1565-1567`` per-expert token lists in ascending token order
                             (``nonzero``), which is the stable sort of the
                             flat (token, slot) assignments by expert.
+  ``model/moe.py:1395-1448`` capacity dropping (``_apply_capacity``): expert
+                            e keeps the first ``capacity`` of its tokens in
+                            token order; per-expert drop counts.
+  ``model/moe.py:1450-1498`` adaptive capacity factor update.
 
 Spec choices the absent ``fp8_flow_moe`` package would have fixed:
   * ties in top-k go to the lower expert index;
@@ -20,6 +24,11 @@ Pinning (tests/test_oracle_routing.py): brute-force Python loops over
 tokens/experts on small cases; invariants (counts sum to T*K, every
 assignment appears once, rows ascending within an expert, offsets multiples
 of 128); top-1 softmax weights are exactly 1.0 (``model/moe.py:253-254``).
+Capacity: a token-by-token running count per expert (a different algorithm
+from the per-expert token lists restated here), the closed cases (capacity
+>= T keeps all, capacity 0 drops every routed token), hand-worked cases and
+the invariant that no expert keeps more than ``capacity`` tokens.  Adaptive
+capacity: hand-computed EMA steps and the clamp to [1, 4].
 """
 
 from __future__ import annotations
@@ -200,3 +209,43 @@ def router_logits(x: np.ndarray, w: np.ndarray, b=None, score_bias=None) -> np.n
     if score_bias is not None:
         out = out + np.asarray(score_bias, dtype=np.float64)
     return out.astype(np.float32, copy=False)
+
+
+def capacity_keep(idx: np.ndarray, num_experts: int, capacity: int):
+    """``MoEBase._apply_capacity`` (reference model/moe.py:1421-1437): for each
+    expert, its tokens in ascending order (``(indices == e).any(-1)
+    .nonzero()``); those past the first ``capacity`` are dropped.  Returns
+    (keep [T] bool, drops [E] int64, dropped = drops.sum())."""
+    idx = np.asarray(idx)
+    T = idx.shape[0]
+    keep = np.ones(T, dtype=bool)
+    drops = np.zeros(num_experts, dtype=np.int64)
+    for e in range(num_experts):
+        tok = np.nonzero((idx == e).any(axis=-1))[0]
+        if tok.shape[0] > capacity:
+            keep[tok[capacity:]] = False
+            drops[e] = tok.shape[0] - capacity
+    return keep, drops, int(drops.sum())
+
+
+def adaptive_capacity_update(cf: float, ema: float, step: int, idx: np.ndarray, num_experts: int, target: float,
+                             ema_coef: float):
+    """``_update_adaptive_capacity`` (reference model/moe.py:1450-1498): the
+    drop rate the current factor would give, EMA-smoothed; the factor grows
+    10% above 1.5x the target, shrinks 5% below 0.5x, clamped to [1, 4].
+    Returns (cf, ema, step)."""
+    idx = np.asarray(idx)
+    T = idx.shape[0]
+    capacity = int(cf * T / num_experts)
+    est = 0.0
+    for e in range(num_experts):
+        n = float((idx == e).any(axis=-1).sum())
+        if n > capacity:
+            est += n - capacity
+    rate = est / max(1, T)
+    ema = ema_coef * rate + (1 - ema_coef) * ema
+    if ema > target * 1.5:
+        cf *= 1.1
+    elif ema < target * 0.5:
+        cf *= 0.95
+    return max(1.0, min(4.0, cf)), ema, step + 1

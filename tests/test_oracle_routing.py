@@ -239,3 +239,68 @@ def test_topk_nan_first_and_no_duplicates():
     assert idx.tolist() == [[2, 1, 3, 0, 4, 5], [0, 1, 2, 3, 4, 5], [0, 2, 5, 4, 3, 1]]
     t = torch.from_numpy(s).topk(6).indices.numpy()
     assert t[0, 0] == 2 and all(len(set(r)) == 6 for r in t)   # torch: NaN first, no repeats
+
+
+def _capacity_running_count(idx, E, capacity):
+    """Token by token: each slot takes its expert's next rank; a token is kept
+    when all its ranks are below the capacity."""
+    seen = [0] * E
+    keep = []
+    for row in np.asarray(idx).tolist():
+        ok = True
+        for e in set(row):
+            if 0 <= e < E:
+                ok &= seen[e] < capacity
+                seen[e] += 1
+        keep.append(ok)
+    drops = np.array([max(0, n - capacity) for n in seen], np.int64)
+    return np.array(keep, bool), drops
+
+
+def test_capacity_keep_hand_worked():
+    """Expert 0 holds tokens 0, 1, 2, 4; expert 1 tokens 0, 2, 3; expert 2
+    tokens 1, 3, 4.  At capacity 2 expert 0 drops 2 and 4, expert 1 drops 3
+    (ranked among all its tokens, token 2 included although expert 0 dropped
+    it) and expert 2 drops 4."""
+    idx = np.array([[0, 1], [0, 2], [1, 0], [2, 1], [0, 2]])
+    keep, drops, dropped = orouting.capacity_keep(idx, 3, 2)
+    assert keep.tolist() == [True, True, False, False, False]
+    assert drops.tolist() == [2, 1, 1] and dropped == 4
+    # a capacity of every token keeps all; capacity 0 drops every routed token
+    keep, drops, dropped = orouting.capacity_keep(idx, 3, 5)
+    assert keep.all() and dropped == 0
+    keep, drops, dropped = orouting.capacity_keep(np.array([[0, 1], [-1, 7], [2, 1]]), 3, 0)
+    assert keep.tolist() == [False, True, False] and drops.tolist() == [1, 2, 1]
+
+
+@pytest.mark.parametrize("K,E", [(1, 4), (2, 8), (4, 16)])
+def test_capacity_keep_matches_running_counts(K, E):
+    T = 3000
+    idx = zipf_routing(T, E, K, 1.1, seed=K * 10 + E)[1].numpy().copy()
+    idx[::97, 0] = -1                              # out-of-range slots constrain nothing
+    counts = np.bincount(idx[idx >= 0], minlength=E)
+    for cap in (0, 1, int(T * K / E * 0.8), int(counts.max()) - 1, int(counts.max()), T):
+        keep, drops, dropped = orouting.capacity_keep(idx, E, cap)
+        rk, rd = _capacity_running_count(idx, E, cap)
+        assert np.array_equal(keep, rk) and np.array_equal(drops, rd), cap
+        assert dropped == int(rd.sum())
+        for e in range(E):                          # no expert keeps more than its capacity
+            assert int(((idx == e).any(-1) & keep).sum()) <= cap
+
+
+def test_adaptive_capacity_hand_worked():
+    """T=8 tokens all on expert 0 of 2 (top-1): capacity int(cf * 8 / 2); at cf=1
+    the estimated drop rate is 4/8, EMA 0.3 * 0.5 = 0.15 > 1.5 * 0.01, so the
+    factor grows 10%; it is clamped at 4 on the way up and at 1 on the way
+    down (no drops: the EMA decays below 0.5 * target)."""
+    idx = np.zeros((8, 1), np.int64)
+    cf, ema, step = orouting.adaptive_capacity_update(1.0, 0.0, 0, idx, 2, 0.01, 0.3)
+    assert abs(cf - 1.1) < 1e-12 and abs(ema - 0.15) < 1e-12 and step == 1
+    # 8 experts: capacity int(3.9 * 8 / 8) = 3 < 8 tokens, so the factor grows, to the clamp
+    cf, ema, step = orouting.adaptive_capacity_update(3.9, 0.0, 0, idx, 8, 0.01, 0.3)
+    assert cf == 4.0 and abs(ema - 0.3 * 5 / 8) < 1e-12
+    even = np.array([[0], [1]] * 4)
+    cf, ema, step = orouting.adaptive_capacity_update(1.02, 0.001, 5, even, 2, 0.01, 0.3)
+    assert cf == 1.0 and abs(ema - 0.0007) < 1e-12 and step == 6
+    cf, ema, step = orouting.adaptive_capacity_update(2.0, 0.01, 0, even, 2, 0.01, 0.3)
+    assert cf == 2.0 and abs(ema - 0.007) < 1e-12               # within [0.5, 1.5] x target: unchanged
