@@ -1949,7 +1949,7 @@ __device__ __forceinline__ bool rk_next_min(const RkQueue& q, int& c, TileK& t, 
 // QNN / QP: pm's weights stored [K][N] / paired (ragged-K operands are paired
 // [rows][tokens]).  Every tile runs the four-slot ring of half steps and the
 // last four refills of a tile fetch the next tile's first four halves;
-// ragged-K tiles of fewer than three K steps come last, one at a time.  No
+// ragged-K tiles of one K step come last, one at a time.  No
 // expert masks, at most 64 experts, ragged-M K >= 384 (the launcher).
 template <int KIND, int MXL, bool HAS_M, bool HAS_K, bool QNN, bool QP>
 __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams pk) {
@@ -2035,7 +2035,7 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
     }
     if constexpr (HAS_K) {
       TileK tk;
-      if (rk_next_min(q, ck, tk, 128, 3)) {
+      if (rk_next_min(q, ck, tk, 128, 2)) {
         it = ItemR{1, tk.e, tk.i0, tk.j0, 0, tk.k_lo / 64, 2 * tk.nk};
         return true;
       }
@@ -2053,13 +2053,18 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
   const uint32_t smem_lds = lds_addr(smem);
   uint8_t* const W = smem + kBase + w.wave * 2048;
 
-  auto store = [&](void* C, int64_t ldC, int out_f32, int64_t row0, int64_t col0, const v16f (&acc)[4][2]) {
+  // returns a lower bound of the output store instructions the wave issued:
+  // 16 x 16 bytes of bf16 (the unaligned path's 8-byte pairs may be merged
+  // into 16-byte stores), 32 x 16 bytes of fp32; a count above the issued
+  // stores would let the next tile read a slot before its data landed
+  auto store = [&](void* C, int64_t ldC, int out_f32, int64_t row0, int64_t col0, const v16f (&acc)[4][2]) -> int {
     WaveCoord we = w;
     we.lane = fresh_lane();
     we.lrow = we.lane & 31;
     we.lhalf = we.lane >> 5;
     if (!out_f32) {
       store_bf16_passes(acc, W, static_cast<uint16_t*>(C), ldC, row0, col0, we);
+      return 16;
     } else {
       float* dst = static_cast<float*>(C) + row0 * ldC + col0 + we.lrow * ldC + 4 * we.lhalf;
 #pragma unroll
@@ -2070,22 +2075,25 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
           for (int r4 = 0; r4 < 4; ++r4)
             st_global(dst + b * 32 * ldC + a * 32 + 8 * r4, make_float4(
                 acc[a][b][4 * r4], acc[a][b][4 * r4 + 1], acc[a][b][4 * r4 + 2], acc[a][b][4 * r4 + 3]));
+      return 32;
     }
   };
-  auto epilogue = [&](const ItemR& it, const v16f (&acc)[4][2]) {
+  // returns the wave's output store instructions (wave-uniform)
+  auto epilogue = [&](const ItemR& it, const v16f (&acc)[4][2]) -> int {
     const int64_t ib = it.i0 + w.wi * 128, jb = it.j0 + w.wj * 64;
     if (HAS_K && (!HAS_M || it.k_mode)) {   // weight gradient: row j (m), column i; rows past `split` to C2
-      if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return;
+      if (ib >= rfl64(plk->n_i) || jb >= rfl64(plk->n_j)) return 0;
       const int64_t split = rfl64(plk->split);
       const bool second = uniform_ge(jb, split);
       const int64_t gs = second ? rfl64(plk->c2_gs) : rfl64(plk->c_gs);
       uint8_t* const Cb = static_cast<uint8_t*>(second ? plk->C2 : plk->C);
       const int f32 = __builtin_amdgcn_readfirstlane(plk->out_f32);
-      store(Cb + int64_t(it.e) * gs * (f32 ? 4 : 2), rfl64(plk->ldC), f32, second ? jb - split : jb, ib, acc);
+      return store(Cb + int64_t(it.e) * gs * (f32 ? 4 : 2), rfl64(plk->ldC), f32, second ? jb - split : jb, ib,
+                   acc);
     } else {   // dgrad / forward: row j (token), column i
       const int p_rows = it.j_end - it.j0 < kT ? it.j_end - it.j0 : kT;
-      if (ib >= rfl64(plm->n_i) || jb >= it.j0 + p_rows) return;
-      store(plm->C, rfl64(plm->ldC), __builtin_amdgcn_readfirstlane(plm->out_f32), jb, ib, acc);
+      if (ib >= rfl64(plm->n_i) || jb >= it.j0 + p_rows) return 0;
+      return store(plm->C, rfl64(plm->ldC), __builtin_amdgcn_readfirstlane(plm->out_f32), jb, ib, acc);
     }
   };
   auto zero = [](v16f (&acc)[4][2]) {
@@ -2155,8 +2163,9 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
     FM_WAIT_VMCNT(13);   // half 0 landed (halves 1-3: 4 + 5 + 4 pieces in flight)
     block_barrier();
     read_even(0, 0, f0);
-    int gs = 0;   // ring slot of the current even half (0 or 2)
-    int ss = 0;   // MX: scale slot of the current step (0, 1, 2)
+    int gs = 0;     // ring slot of the current even half (0 or 2)
+    int ss = 0;     // MX: scale slot of the current step (0, 1, 2)
+    int pend = 0;   // output stores of the last epilogue (issued after this tile's halves 1-3)
     for (;;) {
       ItemR nxt;
       const bool has_next = next_item(nxt);
@@ -2166,12 +2175,16 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
       // into f1 and absolute half jn (even; with the scales of two steps on)
       // is issued into the even slot, then the odd half's MFMAs while the next
       // even half is read into f0 and jn + 1 is issued into the odd slot.
-      // `drain`: the first pair after an epilogue, whose output stores count
-      // in vmcnt too, waits for everything.
-      auto pair = [&](int64_t jn, auto drain) {
+      // `first`: the tile's first pair, after an epilogue whose `pend` output
+      // stores count in vmcnt too: vector memory operations complete in issue
+      // order, so the odd half has landed once at most the two halves after
+      // it and those stores remain.
+      auto pair = [&](int64_t jn, bool first) {
         const int s2 = ss == 0 ? 2 : ss - 1, s1 = ss == 2 ? 0 : ss + 1;   // (ss + 2) % 3, (ss + 1) % 3
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (decltype(drain)::value) FM_WAIT_VMCNT(0);
+        const int after = first ? pend : 0;   // wave-uniform
+        if (after >= 32) FM_WAIT_VMCNT(9 + 32);
+        else if (after >= 16) FM_WAIT_VMCNT(9 + 16);
         else FM_WAIT_VMCNT(9);   // the odd half landed (the two halves after it in flight)
         block_barrier();         // every wave has read the even half: its slot is free
         issue_read_r<KIND, QNN, true>(S, jn, slot_lds(gs), sdst(gs, s2), w.wave, slot(gs + 1), sslot(ss), false,
@@ -2193,18 +2206,18 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
         gs = (gs + 2) & 3;
         ss = s1;
       };
-      const int nh = cur.nh;   // >= 6
+      const int nh = cur.nh;   // >= 4
       const int64_t kh0 = cur.kh0;
-      pair(kh0 + 4, std::true_type{});
 #pragma unroll 1
-      for (int j = 2; j < nh - 4; j += 2) pair(kh0 + j + 4, std::false_type{});
+      for (int j = 0; j < nh - 4; j += 2) pair(kh0 + j + 4, j == 0);
       if (has_next) S = streams(nxt);
       // the last four halves: the next tile's halves 0-3 (the last tile
-      // re-issues its own last two halves, whose slots nothing reads again)
+      // re-issues its own last two halves, whose slots nothing reads again);
+      // a tile of four halves has only these
       const int64_t kn0 = has_next ? int64_t(nxt.kh0) : kh0 + nh - 2;
 #pragma unroll 1
-      for (int j = 0; j < 4; j += 2) pair(has_next ? kn0 + j : kn0, std::false_type{});   // a loop: one block per pair
-      epilogue(cur, acc);
+      for (int j = 0; j < 4; j += 2) pair(has_next ? kn0 + j : kn0, nh == 4 && j == 0);   // a loop: one block per pair
+      pend = __builtin_amdgcn_readfirstlane(epilogue(cur, acc));
       if (!has_next) break;
       cur = nxt;
     }
@@ -2213,11 +2226,11 @@ __global__ __launch_bounds__(512) void gemm256r_kernel(GemmParams pm, GemmParams
   }
 
   if constexpr (HAS_K) {
-    // ragged-K tiles of fewer than three K steps, one at a time
+    // ragged-K tiles of one K step (or none), one at a time
     for (int c = 0;; ++c) {
       TileK t;
       if (!rk_tile_at(q, c, t, 128)) break;
-      if (t.nk >= 3) continue;
+      if (t.nk >= 2) continue;
       const ItemR it{1, t.e, t.i0, t.j0, 0, t.k_lo / 64, 2 * t.nk};
       v16f acc[4][2];
       zero(acc);
