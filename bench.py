@@ -345,6 +345,14 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
          + ("rows; the down and dX GEMMs read them as [K][N])" if ew.w2t.kmajor else "+ transposed)"),
          lambda: ew._build(w1, w2, w3, E), wbytes),
     ]
+    return time_hbm_ops(ops, reps)
+
+
+def time_hbm_ops(ops, reps):
+    """(name, launch, algorithmic bytes) -> one dict per op: `reps` launches
+    back to back between two events on the current stream, after 3 untimed."""
+    import torch
+
     results = []
     for name, fn, nbytes in ops:
         for _ in range(3):
@@ -361,6 +369,79 @@ def hbm_kernels_c3(x, w, idx, w1, w2, w3, go, E, H, reps=20):
         results.append({"op": name, "us": round(us, 2), "bytes": int(nbytes), "GB_s": round(gbs, 1),
                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
     return results
+
+
+def hbm_kernels_c5(x, w, idx, w1, w2, w3, go, E, H, reps=5):
+    """The HBM-bound kernels of one MXFP8 expert-block step at configs[4]'s
+    shapes, each timed alone as in hbm_kernels_c3 (C ABI, preallocated
+    outputs, paired-row operands as the block writes them).  Slots of other
+    ranks' experts (index E_global) move no bytes: the gathered rows are the
+    local assignments' rows."""
+    import torch
+
+    import nanopysche_amd as fm
+    from nanopysche_amd import _lib
+    from nanopysche_amd.flow_moe import ExpertWeights, _alloc_quant, _tile_args
+
+    dev = x.device
+    T, D = x.shape
+    K = idx.shape[1]
+    MX = _lib.QUANT_MX
+    plan = fm.route_tokens(idx, E, 0)
+    R = plan.rows_max
+    R_used = int(plan.offsets[-1].item())
+    A = int(plan.counts.sum().item())
+    gen = torch.Generator(device=dev).manual_seed(5)
+    GU = device_normal((R, 2 * H), 1.0, gen, dev, torch.bfloat16)
+    dH = device_normal((R, H), 0.01, gen, dev, torch.bfloat16)
+    Y = device_normal((R, D), 1.0, gen, dev, torch.bfloat16)
+    wts = w.reshape(-1).to(torch.float32).contiguous()
+    st = _lib.stream_of(x)
+
+    def nb(*ts):
+        return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
+    def nbq(*ts):   # padded-layout buffers: the rows of the expert groups
+        return nb(*ts) * R_used // R
+
+    row_bytes = D * 2
+    pq = _alloc_quant(R, D, MX, True, True, dev, True)
+    sq = _alloc_quant(R, H, MX, True, True, dev, True)
+    gq = _alloc_quant(R, 2 * H, MX, True, True, dev, True)
+    out = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    dw = torch.empty(T * K, dtype=torch.float32, device=dev)
+    ew = ExpertWeights(MX, paired=True)
+    ew._build(w1, w2, w3, E)
+    wouts = {o.data.data_ptr(): o for o in (ew.w13, ew.w13t, ew.w2, ew.w2t)}
+    wbytes = nb(w1, w2, w3) + sum(nb(o.data, o.scale) for o in wouts.values())
+    tiles = plan.tile_expert
+    ops = [
+        ("permute + quantise (x rows, MX row + transposed)",
+         lambda: _lib.call("fm_permute", _lib.ptr(x), T, D, x.stride(0), _lib.ptr(plan.assign_of_row), R, K, None,
+                           *_tile_args(MX, *pq, True, True), _lib.ptr(tiles), st), nb(x) + nbq(*pq)),
+        ("permute + quantise (dY rows x router weight)",
+         lambda: _lib.call("fm_permute", _lib.ptr(go), T, D, go.stride(0), _lib.ptr(plan.assign_of_row), R, K,
+                           _lib.ptr(wts), *_tile_args(MX, *pq, True, True), _lib.ptr(tiles), st),
+         nb(go, wts) + nbq(*pq)),
+        ("SwiGLU + quantise (MX row + transposed)",
+         lambda: _lib.call("fm_swiglu_quantize", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0), R, H,
+                           *_tile_args(MX, *sq, True, True), _lib.ptr(tiles), st), nbq(GU, *sq)),
+        ("SwiGLU backward + quantise (dg|du MX row + transposed)",
+         lambda: _lib.call("fm_swiglu_backward", _lib.ptr(GU), GU.stride(0), _lib.ptr(GU[:, H:]), GU.stride(0),
+                           _lib.ptr(dH), dH.stride(0), R, H, *_tile_args(MX, *gq, True, True), _lib.ptr(tiles), st),
+         nbq(GU, dH, *gq)),
+        ("unpermute (weighted sum over the local slots)",
+         lambda: _lib.call("fm_unpermute", _lib.ptr(Y), Y.stride(0), _lib.ptr(plan.row_of), _lib.ptr(wts), T, K, D,
+                           _lib.ptr(out), _lib.DTYPE_BF16, out.stride(0), None, 0, st),
+         A * row_bytes + nb(wts, out)),
+        ("router-weight gradient (dw = <dY row, expert output row>)",
+         lambda: _lib.call("fm_router_weight_grad", _lib.ptr(go), go.stride(0), _lib.ptr(Y), Y.stride(0),
+                           _lib.ptr(plan.row_of), T, K, D, _lib.ptr(dw), st),
+         nb(go, dw) + A * row_bytes),
+        ("expert weight re-quantisation (w1|w3 pair, w2; MX rows + transposed, two launches)",
+         lambda: ew._build(w1, w2, w3, E), wbytes),
+    ]
+    return time_hbm_ops(ops, reps)
 
 
 def cpu_model_name():
@@ -942,6 +1023,19 @@ def workload_c5(args, dev):
     ms, summ, _ = time_layer(x, wts, idx, w1, w2, w3, go, E_local, "mxfp8", 0, args.steps, args.warmup,
                           overlap=not args.no_overlap)
     flops = 18.0 * A * D * H
+    gemm = gemm_report(summ, args.steps, flops_scale=A / (n_tok * K))
+    # the step's HBM-bound kernels alone, against a plain copy's rate: the
+    # time outside the GEMMs and the least it could be at that rate
+    hbm = hbm_kernels_c5(x, wts, idx, w1, w2, w3, go, E_local, H)
+    probe = bw_probe(dev, reps=5)
+    copy = probe["copy"]["TB_s"] * 1e12
+    per_step = {"unpermute (weighted sum over the local slots)": 2}   # forward combine and the dx sum
+    floor_ms = 0.0
+    for h in hbm:
+        h["frac_of_copy_probe"] = round(h["GB_s"] / 1e3 / probe["copy"]["TB_s"], 3)
+        h["per_step"] = per_step.get(h["op"], 1)
+        floor_ms += h["per_step"] * h["bytes"] / copy * 1e3
+    outside = ms - gemm["gemm_ms_per_step"]
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_c5(x, wts, idx, w1, w2, w3, go, E_local)
@@ -957,7 +1051,15 @@ def workload_c5(args, dev):
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "frac_of_fp8_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["fp8"], 4),
         "roofline": gemm_roofline(summ, "fp8", flops_scale=A / (n_tok * K)),
-        "gemm": gemm_report(summ, args.steps, flops_scale=A / (n_tok * K)),
+        "gemm": gemm,
+        "outside_gemms": {"ms": round(outside, 4), "share": round(outside / ms, 4),
+                          "floor_ms_at_copy_rate": round(floor_ms, 4),
+                          "floor_share": round(floor_ms / (floor_ms + gemm["gemm_ms_per_step"]), 4),
+                          "note": "floor: the algorithmic bytes of the step's HBM-bound kernels (each op below "
+                                  "times its launches per step) at the copy probe's rate; floor_share: their "
+                                  "share of a step whose GEMMs keep their measured time"},
+        "hbm_kernels": hbm,
+        "hbm_probe": probe,
         "cpu_baseline": cpu,
     }
 
