@@ -548,8 +548,8 @@ int fm_grouped_gemm_ragged_k(int kind, const FmGemmOperand* a_t, const FmGemmOpe
  * of the two entries (M2, N2, out2 ... ld_out2: fm_grouped_gemm_ragged_k's M,
  * N, out ... ld_out); `kind` takes FM_GEMM_A_FAST for the weight gradient and
  * FM_GEMM_W_KMAJOR for the dgrad.  The outputs equal those of the two calls
- * bit for bit.  Kinds other than BF16 and FP8 pow2, and [K][N] weights, run
- * as the two launches. */
+ * bit for bit.  Kinds other than BF16 and FP8 pow2 (paired MX operands
+ * included), and [K][N] weights, run as the two launches. */
 int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGemmOperand* weights,
                                int64_t m_tiles, const int32_t* tile_expert, int64_t N, int64_t K, void* out,
                                int out_dtype, int64_t ld_out, const FmGemmOperand* a_t, const FmGemmOperand* b_t,

@@ -3009,6 +3009,11 @@ int fm_grouped_gemm_ragged_m_k(int kind, const FmGemmOperand* tokens, const FmGe
                "fm_grouped_gemm_ragged_m_k: paired-row operands need [N][K] weights, no expert mask, "
                "pitches that are multiples of 64 and fewer than 2^28 weight-gradient tiles");
     pk.paired = 1;
+    if (kind != GK_FP8_POW2) {   // MX: the two ring launches (one grid would need both MX scale layouts)
+      if (pm.m_tiles > 0)
+        if (int rc = dispatch_gemm<GM_RAGGED_M>(kind, pm, s)) return rc;
+      return dispatch_gemm<GM_RAGGED_K>(kind, pk, s);
+    }
     if (int rc = prepare_gemm<GM_RAGGED_M>(kind, pm)) return rc;
     if (int rc = prepare_gemm<GM_RAGGED_K>(kind, pk)) return rc;
     const int64_t nbm = pm.m_tiles == 0 ? 0 : (pm.n_tiles + 7) / 8 * 8, nbk = (pk.n_tiles + 7) / 8 * 8;

@@ -169,13 +169,12 @@ def test_ring_gemms_match_row_major(dev, sized, kind):
         _gemm_k(kind, a_c[0], a_c[1], plan, M, N, g0, M * N, may_split=False)
         _gemm_k(kind, b_c[0], b_c[1], plan, M, N, g1, M * N, may_split=False)
         assert torch.equal(g0, g1), ("ragged-K", M, N)
-    if kind == MX:
-        return   # MX runs dH and dW2 as two launches
+    # (MX: the entry point runs dH and dW2 as its two ring launches)
     dh0, dh1 = out(H), out(H)
     dw0 = torch.zeros(E * H, D, dtype=torch.bfloat16, device=dev)
     dw1 = torch.zeros_like(dw0)
-    _gemm_mk(POW2, d0.rows, ew0.w2, plan, dh0, hc0, d0.rows_t, H, D, dw0, H * D)
-    _gemm_mk(POW2, d1.rows, ew1.w2, plan, dh1, hc1, d1.rows_t, H, D, dw1, H * D)
+    _gemm_mk(kind, d0.rows, ew0.w2, plan, dh0, hc0, d0.rows_t, H, D, dw0, H * D)
+    _gemm_mk(kind, d1.rows, ew1.w2, plan, dh1, hc1, d1.rows_t, H, D, dw1, H * D)
     assert torch.equal(dh0[:rows], dh1[:rows]) and torch.equal(dw0, dw1), "dH + dW2 grid"
 
 
