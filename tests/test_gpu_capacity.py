@@ -14,6 +14,8 @@
 * Jitter (``:145-148``): a seeded training-mode layer draws the same noise
   as torch does for the reference; the router sees x + noise, the experts
   x; eval mode adds none.
+* FP8 recipes (flow_moe, mxfp8) with a capacity factor: bit for bit the
+  expert block run by hand on the kept tokens.
 """
 
 import numpy as np
@@ -220,3 +222,31 @@ def test_jitter_draws_torch_noise_for_the_router(dev, capacity):
     out_e, aux_e, leaves_e = _run(dev, layer, x, gw, gb, w, ws, Rm, 0.5)
     ref_out, ref_aux, ref_grads, _ = _reference(x, gw, gb, w, ws, Rm, E, K, 0.5, capacity=cap)
     _check(out_e, aux_e, leaves_e, ref_out, ref_aux, ref_grads)
+
+
+@pytest.mark.parametrize("recipe", ["flow_moe", "mxfp8"])
+def test_fp8_layer_with_capacity_is_the_block_on_kept_tokens(dev, recipe):
+    """With an FP8 recipe the capacity path is route() on every token, the
+    oracle's keep mask on the routed experts, and FP8FlowMoECompute on the
+    kept tokens' rows, weights and experts with zeros elsewhere (reference
+    model/moe.py:1351-1356, :1386-1391): the same kernels on the same inputs,
+    so the output and the expert-weight gradients match bit for bit."""
+    T, D, H, E, K = 1024, 512, 256, 8, 2
+    x, gw, gb, w, _, Rm = _params(T, D, H, E, None, seed=71)
+    cfg = fm.FP8FlowMoEConfig(enabled=True, fp8_recipe=fm.FP8RecipeConfig(True, fm.FP8RecipeType(recipe)))
+    layer = fm.FP8FlowMoELayer(cfg, D, H, E, K, fp8_gemm_threshold=0, capacity_factor=1.25)
+    out, aux, leaves = _run(dev, layer, x, gw, gb, w, [], Rm, 0.5)
+    assert layer.get_drop_stats()["last_dropped"] > 0
+
+    ref = [t.to(dev).requires_grad_(True) for t in (x, gw, gb, *w)]
+    wts, idx, aux_r = fm.route(ref[0], ref[1], ref[2], top_k=K)
+    keep = torch.from_numpy(orouting.capacity_keep(idx.cpu().numpy(), E, int(1.25 * T / E))[0]).to(dev)
+    block = fm.FP8FlowMoECompute(cfg, D, H, E, 0)
+    block.set_weights(*ref[3:6])
+    out_k = block(ref[0][keep], wts[keep], idx[keep])
+    out_r = torch.zeros(T, D, dtype=out_k.dtype, device=dev).index_put((keep.nonzero(as_tuple=True)[0],), out_k)
+    ((out_r.float() * Rm.to(dev)).sum() + 0.5 * aux_r).backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), out_r.detach()) and torch.equal(aux.detach(), aux_r.detach())
+    for name, a, b in zip(("x", "gate_w", "gate_b", "w1", "w2", "w3"), leaves, ref):
+        assert torch.allclose(a.grad.float(), b.grad.float(), rtol=1e-6, atol=0), name
