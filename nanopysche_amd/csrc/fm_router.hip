@@ -18,9 +18,11 @@
 //                        slices in order), dw and db written in the parameters' dtype
 //
 // The gate is a skinny GEMM (E <= 256 outputs per token): x is read once at
-// its size and the FMAs run on the VALU in fp32, as the reference computes it;
-// HBM, not arithmetic, bounds it at the layer's shapes.  Gate weights are
-// read as stored (fp32 or bf16).
+// its size and the products are summed in fp32, as the reference computes
+// it -- on the matrix cores for bf16 x and a bf16 gate with E <= 8, D <= 2048
+// (bf16 products are exact in fp32; the order of the sums differs), otherwise
+// as FMAs on the VALU; HBM, not arithmetic, bounds it at the layer's shapes.
+// Gate weights are read as stored (fp32 or bf16).
 #include <type_traits>
 
 #include "fm_gating.h"
@@ -251,6 +253,49 @@ struct RouterFuse {
   int32_t* block_hist;   // [E, gridDim.x]
 };
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// bf16 x and gate, D <= 2048: the workgroup's 16 x 8 logits as one 16x16
+// MFMA tile (tokens x experts, experts 8..15 zero), wave w contracting its
+// quarter of D (at most 16 steps of 32: x and gate fragments loaded straight
+// into registers, the gate from L2), then the four partial tiles summed
+// through LDS in a fixed order.  Products of bf16 values are exact in the
+// fp32 accumulator; only the summation order differs from the VALU path.
+// Returns this lane's logit of the VALU path's layout: token 4 wave + (lane
+// / 16), expert (lane / 2) % 8.
+__device__ __forceinline__ float router_logits_mfma(const RouterArgs& a, int lane, int wave,
+                                                    float (&red)[4][16][17]) {
+  const int kq = int(a.D / 4);   // a multiple of 128
+  const int nm = kq / 32;        // <= 16
+  const int64_t row = int64_t(blockIdx.x) * kRouterRows + (lane & 15);
+  const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (row < a.T ? row : a.T - 1) * a.ld_x;
+  const int en = lane & 15;
+  const bool ev = en < a.E;
+  const uint16_t* wr = static_cast<const uint16_t*>(a.w) + int64_t(ev ? en : 0) * a.ld_w;
+  const int k0 = wave * kq + 8 * (lane >> 4);
+  uint4 xa[16], wb[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    if (m < nm) {
+      xa[m] = *reinterpret_cast<const uint4*>(xr + k0 + 32 * m);
+      wb[m] = ev ? *reinterpret_cast<const uint4*>(wr + k0 + 32 * m) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  v4f c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 16; ++m)
+    if (m < nm)
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[m]), __builtin_bit_cast(v8bf, wb[m]),
+                                                  c, 0, 0, 0);
+  // lane l holds tile rows (tokens) 4 (l / 16) + i, column (expert) l % 16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][en] = c[i];
+  __syncthreads();
+  const int vi = lane >> 1, tr = 4 * wave + (vi >> 3), e = vi & 7;
+  return ((red[0][tr][e] + red[1][tr][e]) + red[2][tr][e]) + red[3][tr][e];
+}
+
 template <typename T, typename WL, bool FUSED>
 __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, RouterFuse f) {
   extern __shared__ __attribute__((aligned(16))) uint4 wl_raw[];
@@ -262,106 +307,115 @@ __global__ __launch_bounds__(256) void router_logits_small_kernel(RouterArgs a, 
   const int64_t r0 = int64_t(blockIdx.x) * kRouterRows + wave * 4;
   const int64_t D = a.D;
   const int nc = int(D / kRouterCols);   // D % 512 == 0 (launcher)
-  // rows past T re-read the last row (their sums are not stored)
-  const T* rows[4];
+  // bf16 x and gate, D <= 2048: the logits on the matrix cores; otherwise
+  // (an fp32 input or gate, or a longer row) fp32 FMAs on the VALU
+  constexpr bool kMfma = sizeof(T) == 2 && sizeof(WL) == 2;
+  float sum;
+  if (kMfma && nc <= 4) {
+    __shared__ float red[4][16][17];
+    sum = router_logits_mfma(a, lane, wave, red);
+  } else {
+    // rows past T re-read the last row (their sums are not stored)
+    const T* rows[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t row = r0 + r < a.T ? r0 + r : a.T - 1;
-    rows[r] = static_cast<const T*>(a.x) + row * a.ld_x + lane * 8;
-  }
-  // bf16 rows of at most 2048 columns: all of this wave's x loads are issued
-  // right after the gate's loads and before the gate's LDS stores, so the
-  // stores wait only for the gate (loads complete in issue order) and the two
-  // memory latencies overlap; the chunk loop then waits on none
-  constexpr bool kWhole = sizeof(T) == 2;
-  const bool whole = kWhole && nc <= 4;
-  uint4 xr[4][4];
-  auto load_x = [&]() {
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = r0 + r < a.T ? r0 + r : a.T - 1;
+      rows[r] = static_cast<const T*>(a.x) + row * a.ld_x + lane * 8;
+    }
+    // bf16 rows of at most 2048 columns: all of this wave's x loads are issued
+    // right after the gate's loads and before the gate's LDS stores, so the
+    // stores wait only for the gate (loads complete in issue order) and the two
+    // memory latencies overlap; the chunk loop then waits on none
+    constexpr bool kWhole = sizeof(T) == 2;
+    const bool whole = kWhole && nc <= 4;
+    uint4 xr[4][4];
+    auto load_x = [&]() {
+      if (whole) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (c < nc) xr[c][r] = *reinterpret_cast<const uint4*>(rows[r] + int64_t(c) * kRouterCols);
+      }
+    };
+    if constexpr (sizeof(WL) == 2) {
+      // the bf16 gate copied as stored: 8 rows of D <= 4096 over 256 threads, at
+      // most two 16-byte pieces per thread and row, all loads before the stores
+      constexpr int kPerRow = kGateLdsBytes / 8 / 16 / 256;
+      uint4 v[8][kPerRow];
+      const int Di = int(D);
+      const uint16_t* w = static_cast<const uint16_t*>(a.w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int u = 0; u < kPerRow; ++u) {
+          const int c = (int(threadIdx.x) + 256 * u) * 8;
+          v[e][u] = make_uint4(0, 0, 0, 0);
+          if (c < Di && e < a.E) v[e][u] = *reinterpret_cast<const uint4*>(w + e * a.ld_w + c);
+        }
+      load_x();
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int u = 0; u < kPerRow; ++u) {
+          const int c = (int(threadIdx.x) + 256 * u) * 8;
+          if (c < Di) *reinterpret_cast<uint4*>(&wl[e * Di + c]) = v[e][u];
+        }
+    } else {
+      // 8 gate rows of D <= 2048 floats over 256 threads: per row at most two
+      // float4 per thread (expert x column loop, no index division), all loads
+      // issued before the stores
+      constexpr int kPerRow = kGateLdsBytes / 4 / 8 / 1024;
+      float4 v[8][kPerRow];
+      const int Di = int(D);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int u = 0; u < kPerRow; ++u) {
+          const int c = (int(threadIdx.x) + 256 * u) * 4;
+          v[e][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (c < Di && e < a.E) v[e][u] = ldw4(a.w, a.w_bf16, e * a.ld_w + c);
+        }
+      load_x();
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int u = 0; u < kPerRow; ++u) {
+          const int c = (int(threadIdx.x) + 256 * u) * 4;
+          if (c < Di) *reinterpret_cast<float4*>(&wl[e * Di + c]) = v[e][u];
+        }
+    }
+    __syncthreads();
+    float acc[32];   // [row][expert]
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = 0.f;
     if (whole) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c) {
+        if (c < nc) {
+          float xv[4][8];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bf16x8_to_f32(xr[c][r], xv[r]);
+          router_fma_chunk(acc, xv, wl + int64_t(c) * kRouterCols + lane * 8, D);
+        }
+      }
+    } else {
+      float cur[4][8], nxt[4][8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load8f(rows[r], cur[r]);
+      for (int c = 0; c < nc; ++c) {
+        const int cn = c + 1 < nc ? c + 1 : c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) load8f(rows[r] + int64_t(cn) * kRouterCols, nxt[r]);
+        router_fma_chunk(acc, cur, wl + int64_t(c) * kRouterCols + lane * 8, D);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (c < nc) xr[c][r] = *reinterpret_cast<const uint4*>(rows[r] + int64_t(c) * kRouterCols);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) cur[r][j] = nxt[r][j];
+      }
     }
-  };
-  if constexpr (sizeof(WL) == 2) {
-    // the bf16 gate copied as stored: 8 rows of D <= 4096 over 256 threads, at
-    // most two 16-byte pieces per thread and row, all loads before the stores
-    constexpr int kPerRow = kGateLdsBytes / 8 / 16 / 256;
-    uint4 v[8][kPerRow];
-    const int Di = int(D);
-    const uint16_t* w = static_cast<const uint16_t*>(a.w);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int u = 0; u < kPerRow; ++u) {
-        const int c = (int(threadIdx.x) + 256 * u) * 8;
-        v[e][u] = make_uint4(0, 0, 0, 0);
-        if (c < Di && e < a.E) v[e][u] = *reinterpret_cast<const uint4*>(w + e * a.ld_w + c);
-      }
-    load_x();
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int u = 0; u < kPerRow; ++u) {
-        const int c = (int(threadIdx.x) + 256 * u) * 8;
-        if (c < Di) *reinterpret_cast<uint4*>(&wl[e * Di + c]) = v[e][u];
-      }
-  } else {
-    // 8 gate rows of D <= 2048 floats over 256 threads: per row at most two
-    // float4 per thread (expert x column loop, no index division), all loads
-    // issued before the stores
-    constexpr int kPerRow = kGateLdsBytes / 4 / 8 / 1024;
-    float4 v[8][kPerRow];
-    const int Di = int(D);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int u = 0; u < kPerRow; ++u) {
-        const int c = (int(threadIdx.x) + 256 * u) * 4;
-        v[e][u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (c < Di && e < a.E) v[e][u] = ldw4(a.w, a.w_bf16, e * a.ld_w + c);
-      }
-    load_x();
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int u = 0; u < kPerRow; ++u) {
-        const int c = (int(threadIdx.x) + 256 * u) * 4;
-        if (c < Di) *reinterpret_cast<float4*>(&wl[e * Di + c]) = v[e][u];
-      }
+    sum = wave_reduce_scatter32(acc, lane);
   }
-  __syncthreads();
-  float acc[32];   // [row][expert]
-#pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-  if (whole) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c < nc) {
-        float xv[4][8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bf16x8_to_f32(xr[c][r], xv[r]);
-        router_fma_chunk(acc, xv, wl + int64_t(c) * kRouterCols + lane * 8, D);
-      }
-    }
-  } else {
-    float cur[4][8], nxt[4][8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) load8f(rows[r], cur[r]);
-    for (int c = 0; c < nc; ++c) {
-      const int cn = c + 1 < nc ? c + 1 : c;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) load8f(rows[r] + int64_t(cn) * kRouterCols, nxt[r]);
-      router_fma_chunk(acc, cur, wl + int64_t(c) * kRouterCols + lane * 8, D);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) cur[r][j] = nxt[r][j];
-    }
-  }
-  const float sum = wave_reduce_scatter32(acc, lane);
   const int vi = lane >> 1, r = vi >> 3, e = vi & 7;
   float lv = sum;
   if (e < a.E) {
