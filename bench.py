@@ -715,6 +715,10 @@ def workload_c2(args, dev):
     chain_gbs = sum(r["bytes"] for r in chain) / (chain_us * 1e-6) / 1e9
     # the roofline reports the op furthest from the HBM peak (of all ops timed)
     dom = min(results, key=lambda r: r["frac_of_hbm_peak"])
+    # each op against what a plain copy reaches on this board
+    probe = bw_probe(dev, reps=5)
+    for r in results:
+        r["frac_of_copy_probe"] = round(r["GB_s"] / 1e3 / probe["copy"]["TB_s"], 3)
     cpu = None if args.no_cpu_baseline else cpu_baseline_quant(C)
     return {
         "metric": "HBM GB/s of the FP8 quantisation primitives on 1 MI355X (configs[1])",
@@ -730,6 +734,7 @@ def workload_c2(args, dev):
         "per_op": {r["op"]: r["frac_of_hbm_peak"] for r in results},
         "cpu_baseline": cpu,
         "ops": results,
+        "hbm_probe": probe,
     }
 
 
