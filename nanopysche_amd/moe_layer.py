@@ -95,6 +95,7 @@ class _MoELayerFunction(torch.autograd.Function):
 
 
 def _bf16_rows(x):
+    """x as contiguous bf16 rows [-1, D] (differentiable)."""
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
@@ -270,7 +271,7 @@ class FP8FlowMoELayer:
         lead, D = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, D)
         xr = x2 if noise is None else x2 + noise.reshape(-1, D)
-        w, idx, aux = route(_bf16_rows_differentiable(xr), self.gate_weight, self.gate_bias, top_k=self.top_k,
+        w, idx, aux = route(_bf16_rows(xr), self.gate_weight, self.gate_bias, top_k=self.top_k,
                             gating=self.gating, score_bias=self.score_bias, replay_indices=replay_indices,
                             normalize_expert_weights=self.normalize_expert_weights,
                             z_loss_multiplier=self.z_loss_multiplier, load_tracker=load_tracker)
@@ -283,7 +284,7 @@ class FP8FlowMoELayer:
         self._last_dropped = sel.dropped
         self._total_dropped += sel.dropped
         self._total_tokens_routed += T
-        xb = _bf16_rows_differentiable(x2)
+        xb = _bf16_rows(x2)
         if sel.dropped > 0:
             if sel.n_kept == 0:
                 return torch.zeros_like(x), aux
@@ -296,7 +297,3 @@ class FP8FlowMoELayer:
         if sel.dropped > 0:
             out = select_rows(out, sel.pos_of, sel.kept_index)
         return out.to(x.dtype).reshape(*lead, D), aux
-
-
-def _bf16_rows_differentiable(x2):
-    return (x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)).contiguous()
