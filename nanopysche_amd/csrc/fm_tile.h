@@ -722,14 +722,10 @@ __device__ __forceinline__ Src tile_source(const Src& src, int64_t) {
   return src;
 }
 
-// One workgroup per 128x128 tile.  COL: the transposed output is wanted
-// (a separate instantiation, so a row-only launch allocates no LDS).
-template <class Src, int KIND, bool COL>
-__global__ __launch_bounds__(256) void tile_producer_kernel(Src src_all, TileOut o, int64_t rows) {
-  constexpr bool HW = FM_HW_CVT != 0;
-  const int64_t col0 = int64_t(blockIdx.x) * 128;
-  const int64_t row0 = int64_t(blockIdx.y) * 128;
-  if (o.tile_valid != nullptr && o.tile_valid[blockIdx.y] < 0) return;
+// One 128x128 tile at (row0, col0).
+template <class Src, int KIND, bool HW, bool COL>
+__device__ __forceinline__ void one_tile(const Src& src_all, const TileOut& o, int64_t rows, int64_t row0,
+                                         int64_t col0) {
   const Src src = tile_source(src_all, row0);
   if constexpr (!COL) {
     rows_tile<Src, KIND, HW>(src, o, rows, row0, col0);
@@ -740,6 +736,39 @@ __global__ __launch_bounds__(256) void tile_producer_kernel(Src src_all, TileOut
     else if constexpr (KIND == QK_BLOCK) block_tile<Src, HW>(src, o, rows, row0, col0, want_row);
     else if constexpr (KIND == QK_MX) mx_tile<Src, HW>(src, o, rows, row0, col0, want_row);
     else staged_tile<Src, KIND, HW>(src, o, rows, row0, col0, want_row);
+  }
+}
+
+// COL: the transposed output is wanted (a separate instantiation, so a
+// row-only launch allocates no LDS).  One workgroup per 128x128 tile; WALK:
+// a grid capped below the row tiles (the launcher does so when tile_valid is
+// given -- the rows of a local expert share are sized for every slot, and
+// most of its tiles are then usually empty), where workgroup (x, y) takes
+// the valid tiles among row tiles y, y + gridDim.y, ...  The validity of 64 such
+// candidates comes from one load per lane and a ballot (the same in every
+// wave), so an empty tile costs neither a workgroup launch nor a round trip
+// of its own.
+template <class Src, int KIND, bool COL, bool WALK>
+__global__ __launch_bounds__(256) void tile_producer_kernel(Src src_all, TileOut o, int64_t rows) {
+  constexpr bool HW = FM_HW_CVT != 0;
+  const int64_t col0 = int64_t(blockIdx.x) * 128;
+  if constexpr (!WALK) {
+    if (o.tile_valid != nullptr && o.tile_valid[blockIdx.y] < 0) return;
+    one_tile<Src, KIND, HW, COL>(src_all, o, rows, int64_t(blockIdx.y) * 128, col0);
+  } else {
+    const int64_t ntiles = (rows + 127) / 128;
+    const int lane = threadIdx.x & 63;
+    bool busy = false;
+    for (int64_t base = blockIdx.y; base < ntiles; base += 64 * int64_t(gridDim.y)) {
+      const int64_t cand = base + int64_t(lane) * gridDim.y;
+      const bool ok = cand < ntiles && (o.tile_valid == nullptr || o.tile_valid[cand] >= 0);
+      for (uint64_t m = __ballot(ok); m != 0; m &= m - 1) {
+        if (busy) __syncthreads();   // the previous tile's LDS reads are done
+        busy = true;
+        one_tile<Src, KIND, HW, COL>(src_all, o, rows, (base + int64_t(__builtin_ctzll(m)) * gridDim.y) * 128,
+                                     col0);
+      }
+    }
   }
 }
 
@@ -797,17 +826,32 @@ int launch_tile_producer(const Src& src, const TileOut& o, int64_t rows, int64_t
                          hipStream_t stream, const char* what) {
   if (int rc = check_tile_out(o, rows, cols, Src::kOut)) return rc;
   if (rows == 0) return 0;
-  dim3 grid(unsigned(cols / 128), unsigned((rows + 127) / 128));
+  // A capped grid keeps about kTileGridCap workgroups, 128 per CU: taken
+  // when tile_valid is given and the tiles outnumber that (33,000 rows of
+  // 14,336 columns, 264 x 112 tiles, stay at one tile per workgroup), or when
+  // the row tiles exceed the grid's y limit.
+  constexpr int64_t kTileGridCap = 32768;
+  const int64_t gx = cols / 128, ntiles = (rows + 127) / 128;
+  const int64_t cap = (kTileGridCap + gx - 1) / gx;
+  const bool walk = cap < ntiles && (o.tile_valid != nullptr || ntiles > 65535);
+  const dim3 grid{unsigned(gx), unsigned(walk ? cap : ntiles), 1u};
   const bool col = o.col_q != nullptr;
-#define FM_TILE_LAUNCH(K)                                                                                    \
-  if (col) hipLaunchKernelGGL((tile_producer_kernel<Src, K, true>), grid, dim3(256), 0, stream, src, o, rows); \
-  else hipLaunchKernelGGL((tile_producer_kernel<Src, K, false>), grid, dim3(256), 0, stream, src, o, rows);
+#define FM_TILE_LAUNCH2(K, C)                                                                                 \
+  if (walk) hipLaunchKernelGGL((tile_producer_kernel<Src, K, C, true>), grid, dim3(256), 0, stream, src, o, rows); \
+  else hipLaunchKernelGGL((tile_producer_kernel<Src, K, C, false>), grid, dim3(256), 0, stream, src, o, rows);
+#define FM_TILE_LAUNCH(K)      \
+  if (col) {                   \
+    FM_TILE_LAUNCH2(K, true)   \
+  } else {                     \
+    FM_TILE_LAUNCH2(K, false)  \
+  }
   switch (o.kind) {
     case QK_BF16: FM_TILE_LAUNCH(QK_BF16) break;
     case QK_BLOCK: FM_TILE_LAUNCH(QK_BLOCK) break;
     case QK_POW2: FM_TILE_LAUNCH(QK_POW2) break;
     default: FM_TILE_LAUNCH(QK_MX) break;
   }
+#undef FM_TILE_LAUNCH2
 #undef FM_TILE_LAUNCH
   return check_launch(what);
 }
