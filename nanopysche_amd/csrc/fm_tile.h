@@ -564,8 +564,11 @@ __device__ __forceinline__ void block_tile(const Src& src, const TileOut& o, int
 }
 
 // MX (32x1) with the transposed output.  Rows are dealt so that wave w holds
-// the tile's 32-row block w: thread (w, lane) owns rows 32 w + 4 (lane / 8) +
-// it (it = 0..3), in each the two 8-column segments of the other layouts.  A
+// the tile's 32-row block w: thread (w, lane) owns rows 32 w + 8 it +
+// lane / 8 (it = 0..3), in each the two 8-column segments of the other
+// layouts, so one row-store instruction covers 8 consecutive rows (whole
+// 128-byte lines of the paired-row layout, whose rows 2p and 2p + 1 share
+// them; with 4 consecutive rows per thread each line took two stores).  A
 // block's column amax is then the maximum over the thread's own 4 rows and
 // the wave's 8 row groups (lane exchanges): the scales need no LDS and no
 // barrier.  Each row's values stay in registers until the column scales are
@@ -580,14 +583,14 @@ __device__ __forceinline__ void mx_tile(const Src& src, const TileOut& o, int64_
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, lane8 = tid & 7;
   __shared__ __attribute__((aligned(16))) uint32_t m_code[NOUT][128 * 33];
-  const int rb = 32 * wave + 4 * (lane >> 3);   // the thread's first row in the tile
+  const int rb = 32 * wave + (lane >> 3);   // the thread's row it is rb + 8 it
   typename Src::Raw raw[kRowsPerThread][2];
   {
     const int64_t c = col0 + 8 * lane8;   // rows % 128 == 0: every row is in range
 #pragma unroll
     for (int it = 0; it < kRowsPerThread; ++it)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) raw[it][h] = src.fetch(row0 + rb + it, c + 64 * h);
+      for (int h = 0; h < 2; ++h) raw[it][h] = src.fetch(row0 + rb + 8 * it, c + 64 * h);
   }
   float v[kRowsPerThread][NOUT][2][8];
   float cm[NOUT][2][8];
@@ -596,7 +599,7 @@ __device__ __forceinline__ void mx_tile(const Src& src, const TileOut& o, int64_
     compute_row(src, raw[it], v[it]);
 #pragma unroll
     for (int oi = 0; oi < NOUT; ++oi) {
-      const RowPtr<QK_MX> p(o, row0 + rb + it, col0 + o.col_off[oi]);
+      const RowPtr<QK_MX> p(o, row0 + rb + 8 * it, col0 + o.col_off[oi]);
       float sc;
       row_quant<QK_MX, HW>(v[it][oi], p, want_row, sc);
 #pragma unroll
@@ -633,7 +636,7 @@ __device__ __forceinline__ void mx_tile(const Src& src, const TileOut& o, int64_
         const float* x = v[it][oi][h];
         const uint32_t w0 = enc_e4m3x4<HW>(x[0] * inv[0], x[1] * inv[1], x[2] * inv[2], x[3] * inv[3]);
         const uint32_t w1 = enc_e4m3x4<HW>(x[4] * inv[4], x[5] * inv[5], x[6] * inv[6], x[7] * inv[7]);
-        *reinterpret_cast<uint2*>(&m_code[oi][code_word(rb + it, h)]) = make_uint2(w0, w1);
+        *reinterpret_cast<uint2*>(&m_code[oi][code_word(rb + 8 * it, h)]) = make_uint2(w0, w1);
       }
     }
   __syncthreads();
