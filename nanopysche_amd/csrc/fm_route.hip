@@ -591,7 +591,7 @@ struct ZeroSrc {
 // index-then-row round trip per slot (at top-8 with most slots outside the
 // local experts that chain was 8 dependent loads per token); the sums keep
 // the slot order.  KC == 0: any K, one slot at a time.
-template <int KC>
+template <int KC, bool VEC = false>   // VEC: row_of (and w) 16-byte aligned, KC in {4, 8}
 __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* __restrict__ y, int64_t ld_y,
                                                         const int32_t* __restrict__ row_of,
                                                         const float* __restrict__ w, int64_t T, int K,
@@ -628,10 +628,26 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const uint16_t* __restri
       int32_t r[KC];
       float sw[KC];
       uint4 pk[KC];
+      if constexpr (VEC) {   // a token's KC slots in 16-byte loads (KC = 8: sixteen 4-byte loads -> four)
+        constexpr int V = 4;
 #pragma unroll
-      for (int k = 0; k < KC; ++k) {
-        r[k] = row_of[t * KC + k];
-        sw[k] = w ? w[t * KC + k] : 1.f;
+        for (int k = 0; k < KC; k += V) {
+          const int4 a = *reinterpret_cast<const int4*>(row_of + t * KC + k);
+          r[k] = a.x; r[k + 1] = a.y; r[k + 2] = a.z; r[k + 3] = a.w;
+          if (w) {
+            const float4 b = *reinterpret_cast<const float4*>(w + t * KC + k);
+            sw[k] = b.x; sw[k + 1] = b.y; sw[k + 2] = b.z; sw[k + 3] = b.w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) sw[k + j] = 1.f;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          r[k] = row_of[t * KC + k];
+          sw[k] = w ? w[t * KC + k] : 1.f;
+        }
       }
 #pragma unroll
       for (int k = 0; k < KC; ++k)
@@ -1237,8 +1253,21 @@ int fm_unpermute(const void* y, int64_t ld_y, const int32_t* row_of, const float
   if (T == 0) return 0;
   const int64_t n = T * (D / 8);
   const unsigned blocks = unsigned(n / 256 + 1 < 16384 ? n / 256 + 1 : 16384);
+  // slot indices and weights as vectors when their rows are 16-byte aligned
+  // (K = 4, 8; K = 8 with one local slot per token at D = 7168: 399 -> 361 us)
+  const bool vec = (K == 4 || K == 8) && aligned16(row_of) && aligned16(weights);
   auto go = [&](auto kc) {
-    hipLaunchKernelGGL((unpermute_kernel<decltype(kc)::value>), dim3(blocks), dim3(256), 0,
+    constexpr int KC = decltype(kc)::value;
+    if constexpr (KC == 4 || KC == 8) {
+      if (vec) {
+        hipLaunchKernelGGL((unpermute_kernel<KC, true>), dim3(blocks), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), ld_y, row_of, weights,
+                           T, K, D, out, out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend),
+                           ld_add);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((unpermute_kernel<KC>), dim3(blocks), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), ld_y, row_of, weights,
                        T, K, D, out, out_dtype == FM_DTYPE_F32, ld_out, static_cast<const uint16_t*>(addend),
                        ld_add);
