@@ -234,3 +234,28 @@ def test_aux_loss_with_z_loss(dev):
     loss = fm.load_balancing_loss(part, counts, T, zpart, z_mult)
     ref = orouting.load_balancing_loss(logits.numpy(), _np(idx), E) + z_mult * orouting.z_loss(logits.numpy())
     assert abs(loss.item() - ref) <= 1e-5 * abs(ref)
+
+
+def test_router_weight_grad_sparse_slots(dev):
+    """A local expert share (8 of 64 experts: most slots have no row) over
+    5.6 M slots, more than one batch of 64 candidates per wave (the grid has
+    65,536 waves): every slot with a row gets its dot product (float64
+    reference on the device), every other slot exactly 0."""
+    from nanopysche_amd import _lib
+
+    T, E_local, E_global, K, D = 700_000, 8, 64, 8, 64
+    g = torch.Generator(device=dev).manual_seed(12)
+    idx = torch.randint(0, E_global, (T, K), generator=g, device=dev)
+    plan = fm.route_tokens(idx, E_local)
+    y = torch.randn(plan.rows_max, D, generator=g, device=dev).to(torch.bfloat16)
+    dout = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
+    dw = torch.full((T * K,), float("nan"), dtype=torch.float32, device=dev)
+    _lib.call("fm_router_weight_grad", _lib.ptr(dout), D, _lib.ptr(y), D, _lib.ptr(plan.row_of), T, K,
+              D, _lib.ptr(dw), _lib.stream_of(dout))
+    ro = plan.row_of.long()
+    has = ro >= 0
+    assert 0 < int(has.sum()) < T * K // 4
+    tok = torch.arange(T * K, device=dev) // K
+    ref = (dout.double()[tok[has]] * y.double()[ro[has]]).sum(dim=1)
+    assert torch.allclose(dw[has].double(), ref, rtol=1e-4, atol=1e-4)
+    assert torch.all(dw[~has] == 0)
