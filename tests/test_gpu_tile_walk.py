@@ -105,16 +105,18 @@ def test_permute_walk_matches_one_tile_per_workgroup(dev, kind):
     assert np.array_equal(_np(bufs[1])[sample], rs)
 
 
-def test_swiglu_backward_walk_matches_one_tile_per_workgroup(dev):
-    """Two outputs (dg | du) of the MX tile with its LDS codes, H = 16384
-    (the grid is capped at 256 row tiles), 629 row tiles, half of them valid."""
+@pytest.mark.parametrize("kind", ["pow2", "mx"])
+def test_swiglu_backward_walk_matches_one_tile_per_workgroup(dev, kind):
+    """Two outputs (dg | du), each with its LDS code tile (pow2: the codes of
+    the scaling-aware transpose; MX: the column-scaled codes), H = 16384 (the
+    grid is capped at 256 row tiles), 629 row tiles, half of them valid."""
     T, E, K, H = 40000, 4, 2, 16384
     _, plan, tiles = _plan(T, E, K, dev, seed=41)
     R = plan.rows_max
     g = torch.Generator(device=dev).manual_seed(42)
     GU = torch.randn(R, 2 * H, generator=g, device=dev).to(torch.bfloat16)
     dH = (torch.randn(R, H, generator=g, device=dev) * 0.01).to(torch.bfloat16)
-    qk = _lib.QUANT_MX
+    qk = KINDS[kind]
     st = _lib.stream_of(GU)
     outs = []
     for tl in (tiles, None):
@@ -127,4 +129,4 @@ def test_swiglu_backward_walk_matches_one_tile_per_workgroup(dev):
     torch.cuda.synchronize()
     rows_ok = _valid_rows(tiles)
     assert int(rows_ok.sum()) > 128 * 256
-    _compare(outs[0], outs[1], rows_ok, True)
+    _compare(outs[0], outs[1], rows_ok, kind == "mx")
